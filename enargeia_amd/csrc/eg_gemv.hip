@@ -1,0 +1,510 @@
+// Decode-shape (M=1) quantized GEMV for the projections and the tied LM head.
+//
+// Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
+// (embedding_variants.ts:135-180). Same math, same three weight streams, read verbatim:
+//   out[row + out_offset] = sum_k x[k] * (code[row,k] - zero[blk]) * scale[blk] (+ bias[row])
+//
+// MI355X design (not the reference's one-workgroup-per-row tree):
+//   * A 16-byte chunk of a row (32 int4 or 16 int8 codes) is the unit of work; a chunk never
+//     straddles a quant block because block_size is a multiple of the chunk length on this
+//     path, so each chunk needs exactly one scale and one zero-point.
+//   * A team of TEAM lanes owns one row; lane t of the team owns chunks t, t+TEAM, ... (CPL of
+//     them). The x values those chunks multiply are loaded ONCE into VGPRs and reused for every
+//     row the lane visits, so activations cost no memory traffic in the steady state. A wave
+//     holds 64/TEAM rows; consecutive lanes read consecutive 16-byte chunks of a row, so each
+//     load instruction moves TEAM*16 contiguous bytes per row (128 B at TEAM=8, 1 KiB at 64).
+//   * Dequantization is in registers: the word is split into low/high nibble bytes with one
+//     opaque AND each, and v_cvt_f32_ubyte0..3 convert each byte straight to f32 - 2.4 VALU
+//     ops per int4 weight, below the ~3 ops/byte of issue the HBM rate allows.
+//     sum (code - zero) * x * scale is evaluated as scale * (sum code*x - zero * sum x), with
+//     sum x per chunk precomputed; two's-complement codes are XORed to offset-binary first.
+//   * The row total is a butterfly over the team (fixed order: deterministic); no atomics.
+//   * The fused-argmax variant keeps a (value, index) best per lane, reduces it per workgroup
+//     and finishes in the last-arriving workgroup, so one launch yields the greedy token.
+#include "eg_internal.hpp"
+
+namespace {
+
+constexpr int kWaves = 4;  // waves per workgroup (256 threads)
+
+struct GemvArgs {
+  const float* x;
+  const uint4* w;          // code stream viewed as 16-byte chunks, row-major
+  const float* scales;
+  const uint32_t* zeros;   // offset encoding only
+  const float* bias;       // nullable
+  float* out;              // nullable in the argmax variant
+  uint32_t n;              // rows
+  uint32_t chunks;         // 16-byte chunks per row
+  uint32_t chunks_per_block;
+  uint32_t blocks_per_row;
+  uint32_t out_offset;
+  uint32_t* partials;      // argmax: (value bits, index) per workgroup
+  uint32_t* counter;       // argmax: arrival counter
+  uint32_t* result;        // argmax: [index, value bits]
+};
+
+template <int BITS>
+struct Codes;
+
+template <>
+struct Codes<4> {
+  static constexpr int kPerChunk = 32;
+  static constexpr uint32_t kSignFlip = 0x88888888u;
+  static constexpr int kZeroPerWord = 8;
+  // sum over the 32 codes of a chunk of code * x, codes as unsigned nibbles.
+  static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[32]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
+      const uint32_t hi = egd::and_opaque(d[i] >> 4, 0x0F0F0F0Fu);
+      const float* xv = x + 8 * i;
+      a0 = fmaf(egd::ub0(lo), xv[0], a0);
+      a1 = fmaf(egd::ub0(hi), xv[1], a1);
+      a0 = fmaf(egd::ub1(lo), xv[2], a0);
+      a1 = fmaf(egd::ub1(hi), xv[3], a1);
+      a0 = fmaf(egd::ub2(lo), xv[4], a0);
+      a1 = fmaf(egd::ub2(hi), xv[5], a1);
+      a0 = fmaf(egd::ub3(lo), xv[6], a0);
+      a1 = fmaf(egd::ub3(hi), xv[7], a1);
+    }
+    return a0 + a1;
+  }
+};
+
+template <>
+struct Codes<8> {
+  static constexpr int kPerChunk = 16;
+  static constexpr uint32_t kSignFlip = 0x80808080u;
+  static constexpr int kZeroPerWord = 4;
+  static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[16]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float* xv = x + 4 * i;
+      a0 = fmaf(egd::ub0(d[i]), xv[0], a0);
+      a1 = fmaf(egd::ub1(d[i]), xv[1], a1);
+      a0 = fmaf(egd::ub2(d[i]), xv[2], a0);
+      a1 = fmaf(egd::ub3(d[i]), xv[3], a1);
+    }
+    return a0 + a1;
+  }
+};
+
+template <int BITS, int ENC, int TEAM, int CPL, bool ARGMAX>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  using C = Codes<BITS>;
+  constexpr int EPC = C::kPerChunk;
+  constexpr int RPW = 64 / TEAM;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t t = lane % TEAM;
+  const uint32_t slot = lane / TEAM;
+  const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const uint32_t total_waves = gridDim.x * kWaves;
+
+  // This lane's activations, loaded once: chunk j of the lane covers x[c*EPC, c*EPC + EPC).
+  float xr[CPL][EPC];
+  float sx[CPL];
+  uint32_t blk_in_row[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; j++) {
+    const uint32_t c = t + j * TEAM;
+    sx[j] = 0.f;
+    blk_in_row[j] = 0;
+    if (c < a.chunks) {
+      const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)c * EPC);
+#pragma unroll
+      for (int e = 0; e < EPC / 4; e++) {
+        const float4 v = xs[e];
+        xr[j][4 * e + 0] = v.x;
+        xr[j][4 * e + 1] = v.y;
+        xr[j][4 * e + 2] = v.z;
+        xr[j][4 * e + 3] = v.w;
+      }
+      blk_in_row[j] = c / a.chunks_per_block;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; e++) xr[j][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
+  }
+
+  float best_v = -1.0e30f;
+  uint32_t best_i = a.out_offset;
+
+  for (uint32_t pass = wave; pass * RPW < a.n; pass += total_waves) {
+    const uint32_t row = pass * RPW + slot;
+    const bool active = row < a.n;
+    uint4 q[CPL];
+    float s[CPL], z[CPL];
+    // Issue every load of this row before any math.
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      const uint32_t c = t + j * TEAM;
+      if (active && c < a.chunks) {
+        q[j] = a.w[(size_t)row * a.chunks + c];
+        const uint32_t blk = row * a.blocks_per_row + blk_in_row[j];
+        s[j] = a.scales[blk];
+        if (ENC == EG_ENC_OFFSET_ZEROS) {
+          const uint32_t word = a.zeros[blk / C::kZeroPerWord];
+          z[j] = (float)((word >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
+        } else {
+          z[j] = (float)(1 << (BITS - 1));
+        }
+      } else {
+        q[j] = make_uint4(0, 0, 0, 0);
+        s[j] = 0.f;
+        z[j] = 0.f;
+      }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      uint4 qj = q[j];
+      if (ENC == EG_ENC_SIGNED) {
+        qj.x ^= C::kSignFlip;
+        qj.y ^= C::kSignFlip;
+        qj.z ^= C::kSignFlip;
+        qj.w ^= C::kSignFlip;
+      }
+      const float d = C::dot(qj, xr[j]);
+      acc = fmaf(s[j], d - z[j] * sx[j], acc);
+    }
+    acc = egd::team_sum<TEAM>(acc);
+    if (active && t == 0) {
+      const float v = a.bias ? acc + a.bias[row] : acc;
+      if (a.out) a.out[row + a.out_offset] = v;
+      if (ARGMAX) {
+        if (egd::better(v, row + a.out_offset, best_v, best_i)) {
+          best_v = v;
+          best_i = row + a.out_offset;
+        }
+      }
+    }
+  }
+
+  if (ARGMAX) {
+    __shared__ float wv[kWaves];
+    __shared__ uint32_t wi[kWaves];
+    egd::team_argmax<64>(best_v, best_i);
+    if (lane == 0) {
+      wv[threadIdx.x >> 6] = best_v;
+      wi[threadIdx.x >> 6] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = wv[0];
+      uint32_t bi = wi[0];
+      for (int k = 1; k < kWaves; k++)
+        if (egd::better(wv[k], wi[k], bv, bi)) {
+          bv = wv[k];
+          bi = wi[k];
+        }
+      a.partials[2 * blockIdx.x + 0] = __float_as_uint(bv);
+      a.partials[2 * blockIdx.x + 1] = bi;
+    }
+    if (egd::last_arrival(a.counter, gridDim.x)) {
+      float bv = -1.0e30f;
+      uint32_t bi = a.out_offset;
+      for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+        const float v = __uint_as_float(a.partials[2 * b]);
+        const uint32_t i = a.partials[2 * b + 1];
+        if (egd::better(v, i, bv, bi)) {
+          bv = v;
+          bi = i;
+        }
+      }
+      egd::team_argmax<64>(bv, bi);
+      if (lane == 0) {
+        wv[threadIdx.x >> 6] = bv;
+        wi[threadIdx.x >> 6] = bi;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        for (int k = 1; k < kWaves; k++)
+          if (egd::better(wv[k], wi[k], wv[0], wi[0])) {
+            wv[0] = wv[k];
+            wi[0] = wi[k];
+          }
+        a.result[0] = wi[0];
+        a.result[1] = __float_as_uint(wv[0]);
+      }
+    }
+  }
+}
+
+// Fallback for layouts the chunked kernel does not take (K or block_size not a multiple of
+// the chunk, unaligned streams, very long rows): one wave per row, the reference's exact
+// per-element indexing (matmul_q4_decode.wgsl:66-83), wave butterfly instead of the LDS tree.
+template <bool ARGMAX>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ packed, const float* __restrict__ scales,
+    const uint32_t* __restrict__ zeros, const float* __restrict__ bias, float* out, uint32_t n, uint32_t k,
+    uint32_t block_size, uint32_t blocks_per_row, uint32_t out_offset, int bits, int encoding,
+    uint32_t* partials, uint32_t* counter, uint32_t* result) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const uint32_t total_waves = gridDim.x * kWaves;
+  const uint32_t per_word = 32u / (uint32_t)bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  float best_v = -1.0e30f;
+  uint32_t best_i = out_offset;
+  for (uint32_t row = wave; row < n; row += total_waves) {
+    float acc = 0.f;
+    for (uint32_t i = lane; i < k; i += 64) {
+      const size_t flat = (size_t)row * k + i;
+      uint32_t code = (packed[flat / per_word] >> (bits * (flat % per_word))) & mask;
+      const uint32_t blk = row * blocks_per_row + i / block_size;
+      float zero;
+      if (encoding == EG_ENC_OFFSET_ZEROS) {
+        zero = (float)((zeros[blk / per_word] >> (bits * (blk % per_word))) & mask);
+      } else {
+        code ^= 1u << (bits - 1);
+        zero = (float)(1u << (bits - 1));
+      }
+      acc = fmaf(((float)code - zero) * scales[blk], x[i], acc);
+    }
+    acc = egd::team_sum<64>(acc);
+    if (lane == 0) {
+      const float v = bias ? acc + bias[row] : acc;
+      if (out) out[row + out_offset] = v;
+      if (ARGMAX && egd::better(v, row + out_offset, best_v, best_i)) {
+        best_v = v;
+        best_i = row + out_offset;
+      }
+    }
+  }
+  if (ARGMAX) {
+    __shared__ float wv[kWaves];
+    __shared__ uint32_t wi[kWaves];
+    egd::team_argmax<64>(best_v, best_i);
+    if (lane == 0) {
+      wv[threadIdx.x >> 6] = best_v;
+      wi[threadIdx.x >> 6] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = wv[0];
+      uint32_t bi = wi[0];
+      for (int q = 1; q < kWaves; q++)
+        if (egd::better(wv[q], wi[q], bv, bi)) {
+          bv = wv[q];
+          bi = wi[q];
+        }
+      partials[2 * blockIdx.x] = __float_as_uint(bv);
+      partials[2 * blockIdx.x + 1] = bi;
+    }
+    if (egd::last_arrival(counter, gridDim.x) && threadIdx.x == 0) {
+      float bv = -1.0e30f;
+      uint32_t bi = out_offset;
+      for (uint32_t b = 0; b < gridDim.x; b++) {
+        const float v = __uint_as_float(partials[2 * b]);
+        if (egd::better(v, partials[2 * b + 1], bv, bi)) {
+          bv = v;
+          bi = partials[2 * b + 1];
+        }
+      }
+      result[0] = bi;
+      result[1] = __float_as_uint(bv);
+    }
+  }
+}
+
+using KernelFn = void (*)(GemvArgs);
+
+template <int BITS, int ENC, bool ARGMAX>
+KernelFn pick(int team, int cpl) {
+#define EG_CASE(T, P) \
+  if (team == T && cpl == P) return gemv_kernel<BITS, ENC, T, P, ARGMAX>;
+#define EG_TEAM(T) EG_CASE(T, 1) EG_CASE(T, 2) EG_CASE(T, 3) EG_CASE(T, 4)
+  EG_TEAM(8) EG_TEAM(16) EG_TEAM(32) EG_TEAM(64)
+#undef EG_TEAM
+#undef EG_CASE
+  return nullptr;
+}
+
+KernelFn pick_kernel(int bits, int enc, bool argmax, int team, int cpl) {
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS)
+    return argmax ? pick<4, EG_ENC_OFFSET_ZEROS, true>(team, cpl) : pick<4, EG_ENC_OFFSET_ZEROS, false>(team, cpl);
+  if (bits == 4 && enc == EG_ENC_SIGNED)
+    return argmax ? pick<4, EG_ENC_SIGNED, true>(team, cpl) : pick<4, EG_ENC_SIGNED, false>(team, cpl);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS)
+    return argmax ? pick<8, EG_ENC_OFFSET_ZEROS, true>(team, cpl) : pick<8, EG_ENC_OFFSET_ZEROS, false>(team, cpl);
+  return argmax ? pick<8, EG_ENC_SIGNED, true>(team, cpl) : pick<8, EG_ENC_SIGNED, false>(team, cpl);
+}
+
+struct Shape {
+  int team = 0, cpl = 0;
+  uint32_t grid = 0;
+};
+
+// Team / chunks-per-lane choice. Largest CPL (fewest reductions per weight) that still leaves
+// at least ~4 waves per CU of row passes; small matrices fall back to the widest teams so more
+// waves issue loads at once.
+Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count) {
+  Shape best;
+  uint64_t best_passes = 0;
+  const uint64_t want_passes = (uint64_t)cu_count * 4;
+  for (int cpl = 4; cpl >= 1; cpl--) {
+    int team = 8;
+    while ((uint32_t)(team * cpl) < chunks && team < 64) team *= 2;
+    if ((uint32_t)(team * cpl) < chunks) continue;
+    if (cpl > 1 && (uint32_t)(team * (cpl - 1)) >= chunks) continue;  // a chunk slot always idle
+    const uint64_t rpw = 64 / team;
+    const uint64_t passes = (n + rpw - 1) / rpw;
+    if (passes >= want_passes) {  // largest CPL with enough parallelism
+      best.team = team;
+      best.cpl = cpl;
+      best_passes = passes;
+      break;
+    }
+    if (passes > best_passes) {  // otherwise the most parallel candidate
+      best.team = team;
+      best.cpl = cpl;
+      best_passes = passes;
+    }
+  }
+  if (best.team == 0) return best;
+  uint64_t blocks = (best_passes + kWaves - 1) / kWaves;
+  const uint64_t cap = (uint64_t)cu_count * 8;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  best.grid = (uint32_t)blocks;
+  return best;
+}
+
+struct QuantView {
+  const char* op;
+  const float* x;
+  const uint32_t* packed;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  float* out;
+  uint32_t n, k, block_size, blocks_per_row, out_offset;
+  int encoding, bits;
+  uint32_t* result;  // non-null for the fused argmax
+};
+
+int validate(eg_context* ctx, const QuantView& v) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", v.op);
+  if (v.bits != 4 && v.bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8, got %d", v.op, v.bits);
+  if (v.encoding != EG_ENC_OFFSET_ZEROS && v.encoding != EG_ENC_SIGNED)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", v.op, v.encoding);
+  if (!v.x || !v.packed || !v.scales) return eg::fail(ctx, EG_ERR_INVALID, "%s: x, packed and scales are required", v.op);
+  if (v.encoding == EG_ENC_OFFSET_ZEROS && !v.zeros)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: the offset encoding needs a zero-point stream", v.op);
+  if (!v.out && !v.result) return eg::fail(ctx, EG_ERR_INVALID, "%s: out is NULL", v.op);
+  if (v.block_size == 0 || v.k % v.block_size != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: reduction axis %u is not a multiple of %u", v.op, v.k, v.block_size);
+  if (v.blocks_per_row != v.k / v.block_size)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: blocksPerRow %u does not equal k / blockSize = %u", v.op,
+                    v.blocks_per_row, v.k / v.block_size);
+  const uint64_t elements = (uint64_t)v.n * v.k;
+  if (elements % (32 / v.bits) != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: %llu codes do not fill whole 32-bit words", v.op,
+                    (unsigned long long)elements);
+  if (elements >= (1ull << 32) * (32 / v.bits) || (uint64_t)v.n * v.blocks_per_row >= (1ull << 32))
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u x %u exceeds the 32-bit block index range", v.op, v.n, v.k);
+  return EG_OK;
+}
+
+int launch(eg_context* ctx, const QuantView& v) {
+  int st = validate(ctx, v);
+  if (st != EG_OK) return st;
+  if (v.n == 0) {
+    if (v.result) return eg::fail(ctx, EG_ERR_INVALID, "%s: argmax over zero rows", v.op);
+    return EG_OK;
+  }
+  const bool argmax = v.result != nullptr;
+  const uint32_t epc = 128u / v.bits;
+  const bool aligned = (reinterpret_cast<uintptr_t>(v.packed) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(v.x) & 15u) == 0;
+  const uint32_t chunks = v.k / epc;
+  Shape shape;
+  if (aligned && v.k % epc == 0 && v.block_size % epc == 0 && chunks <= 256)
+    shape = choose_shape(v.n, chunks, ctx->cu_count);
+  uint32_t* counter = eg::counters(ctx) + eg::kCounterLmHeadArgmax;
+  uint32_t* partials = reinterpret_cast<uint32_t*>(eg::partials(ctx));
+  if (shape.team != 0) {
+    GemvArgs a;
+    a.x = v.x;
+    a.w = reinterpret_cast<const uint4*>(v.packed);
+    a.scales = v.scales;
+    a.zeros = v.zeros;
+    a.bias = v.bias;
+    a.out = v.out;
+    a.n = v.n;
+    a.chunks = chunks;
+    a.chunks_per_block = v.block_size / epc;
+    a.blocks_per_row = v.blocks_per_row;
+    a.out_offset = v.out_offset;
+    a.partials = partials;
+    a.counter = counter;
+    a.result = v.result;
+    KernelFn fn = pick_kernel(v.bits, v.encoding, argmax, shape.team, shape.cpl);
+    if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel for team %d cpl %d", v.op, shape.team, shape.cpl);
+    hipLaunchKernelGGL(fn, dim3(shape.grid), dim3(256), 0, ctx->stream, a);
+  } else {
+    uint64_t blocks = (v.n + kWaves - 1) / kWaves;
+    const uint64_t cap = (uint64_t)ctx->cu_count * 8;
+    if (blocks > cap) blocks = cap;
+    if (argmax)
+      hipLaunchKernelGGL(gemv_generic_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, v.x,
+                         v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
+                         v.out_offset, v.bits, v.encoding, partials, counter, v.result);
+    else
+      hipLaunchKernelGGL(gemv_generic_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, v.x,
+                         v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
+                         v.out_offset, v.bits, v.encoding, partials, counter, v.result);
+  }
+  return eg::check_launch(ctx, v.op);
+}
+
+}  // namespace
+
+extern "C" {
+
+int eg_matmul_q4_decode(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                        const uint32_t* zeros, const float* bias, float* out, const eg_matmul_q4_dims* dims,
+                        int encoding, int bits) {
+  if (!dims) return eg::fail(ctx, EG_ERR_INVALID, "matmul_q4_decode: dims is NULL");
+  if (dims->use_bias && !bias) return eg::fail(ctx, EG_ERR_INVALID, "matmul_q4_decode: useBias set but bias is NULL");
+  QuantView v{"matmul_q4_decode", x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros,
+              dims->use_bias ? bias : nullptr, out, dims->n, dims->k, dims->block_size, dims->blocks_per_row,
+              dims->out_offset, encoding, bits, nullptr};
+  if (!out) return eg::fail(ctx, EG_ERR_INVALID, "matmul_q4_decode: out is NULL");
+  return launch(ctx, v);
+}
+
+int eg_lm_head(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales, const uint32_t* zeros,
+               float* out, const eg_embedding_dims* dims, int encoding, int bits) {
+  if (!dims) return eg::fail(ctx, EG_ERR_INVALID, "lm_head: dims is NULL");
+  if (!out) return eg::fail(ctx, EG_ERR_INVALID, "lm_head: out is NULL");
+  QuantView v{bits == 4 ? "lm_head_q4" : "lm_head_q8", x, packed, scales,
+              encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out, dims->row_count, dims->hidden,
+              dims->block_size, dims->blocks_per_row, dims->out_offset, encoding, bits, nullptr};
+  return launch(ctx, v);
+}
+
+int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                      const uint32_t* zeros, float* out, uint32_t* result, const eg_embedding_dims* dims,
+                      int encoding, int bits) {
+  if (!dims) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: dims is NULL");
+  if (!result) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: result is NULL");
+  QuantView v{"lm_head_argmax", x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
+              dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
+              bits, result};
+  if (ctx) {
+    const uint64_t max_groups = eg::kPartialsBytes / 8;
+    if ((uint64_t)ctx->cu_count * 8 > max_groups)
+      return eg::fail(ctx, EG_ERR_RANGE, "lm_head_argmax: workspace too small for the grid");
+  }
+  return launch(ctx, v);
+}
+
+}  // extern "C"

@@ -1,0 +1,248 @@
+"""Decode GEMV, LM head and argmax on the GPU against the CPU oracle, through the C ABI.
+
+Cases follow the reference's own kernel tests (test/kernels/matmul_q4.test.ts:198-231,
+forward_ops.test.ts:397-446) and the BASELINE configs 0-2.
+"""
+
+import functools
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import FP32_TOLERANCE, assert_close, gemv_tolerance
+from enargeia_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def _upload_quant(device, q):
+    bufs = [device.upload(q.packed), device.upload(q.scales)]
+    bufs.append(device.upload(q.zeros) if q.zeros is not None else None)
+    return bufs
+
+
+def run_decode(device, x, q, bias, out_len=None, out_offset=0):
+    spec = K.with_format(K.MATMUL_Q4_DECODE, q.bits, q.encoding)
+    kern = K.ComputeKernel(device, spec)
+    n_out = out_len if out_len is not None else q.rows + out_offset
+    bx = device.upload(x)
+    bp, bs, bz = _upload_quant(device, q)
+    bb = device.upload(bias if bias is not None else np.zeros(max(1, q.rows), np.float32))
+    bo = device.buffer(n_out * 4)
+    device.zero(bo, n_out * 4)
+    u = kern.uniform()
+    u.write(K.matmul_q4_dims(1, q.rows, q.cols, bias is not None, q.block_size, q.rows, out_offset))
+    kern.encode(kern.bind_group([bx, bp, bs, bz, bb, bo, u]), K.matmul_q4_decode_workgroups(q.rows))
+    y = device.read_array(bo, np.float32, n_out)
+    for b in (bx, bp, bs, bz, bb, bo):
+        if b is not None:
+            b.release()
+    return y
+
+
+@pytest.mark.parametrize("n", [896, 128, 4864])
+def test_decode_matches_reference_single_row(device, n):
+    # matmul_q4.test.ts:198-214: k=896, seeds 41/42/43, reference asymmetric block-64 format.
+    k = 896
+    x = oracle.random_floats(k, 41)
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 42), n, k)
+    bias = oracle.random_floats(n, 43)
+    got = run_decode(device, x, q, bias)
+    assert_close(got, oracle.linear_q(x, q, bias, 1), *FP32_TOLERANCE, label=f"q4 decode n={n}")
+
+
+def test_decode_matches_javascript_golden(device):
+    with open(os.path.join(os.path.dirname(__file__), "golden", "js_vectors.json")) as f:
+        case = next(c for c in json.load(f)["linear"] if c["name"] == "decode_n128_k896")
+    n, k = case["n"], case["k"]
+    x = oracle.random_floats(k, case["x_seed"])
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, case["w_seed"]), n, k)
+    got = run_decode(device, x, q, oracle.random_floats(n, case["bias_seed"]))
+    expect = np.array(case["out"], dtype=np.uint32).view(np.float32)
+    assert_close(got, expect, *FP32_TOLERANCE, label="decode vs JS")
+
+
+@functools.lru_cache(maxsize=None)
+def sym_weights(n, k, seed, group=32, bits=4):
+    w = oracle.normal_floats(n * k, seed, 0.02)
+    return oracle.quantize_sym(w, n, k, bits, group)
+
+
+# BASELINE config 0 and the config-1 projection shapes (symmetric int4, group 32).
+@pytest.mark.parametrize("n,k", [(896, 896), (128, 896), (4864, 896), (896, 4864)])
+def test_decode_baseline_projection_shapes(device, n, k):
+    x = oracle.normal_floats(k, 0x5EED ^ 1, 1.0)
+    q = sym_weights(n, k, 0x5EED ^ (n * 7 + k))
+    got = run_decode(device, x, q, None)
+    expect = oracle.linear_q(x, q, None, 1)
+    assert_close(got, expect, *gemv_tolerance(expect), label=f"sym int4 {n}x{k}")
+
+
+def test_decode_long_reduction_reference_format(device):
+    n, k = 256, 4864
+    x = oracle.random_floats(k, 5)
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 6), n, k)
+    got = run_decode(device, x, q, None)
+    assert_close(got, oracle.linear_q(x, q, None, 1), *FP32_TOLERANCE, label="q4 decode k=4864")
+
+
+def test_decode_writes_at_out_offset_and_skips_bias(device):
+    # matmul_q4.test.ts:181-195, through the decode kernel (outOffset; index 0 untouched).
+    k = 64
+    q = oracle.quantize_q4_ref(np.full(2 * k, 0.5, np.float32), 2, k)
+    got = run_decode(device, np.ones(k, np.float32), q, None, out_len=6, out_offset=4)
+    assert got[0] == 0 and got[1] == 0
+    assert abs(got[4] - 32) < 1e-3 and abs(got[5] - 32) < 1e-3
+
+
+@pytest.mark.parametrize("n,k,bs", [(5, 64, 64), (3, 40, 8), (7, 96, 32), (33, 192, 64)])
+def test_decode_ragged_and_unchunked_shapes(device, n, k, bs):
+    # Shapes the 16-byte-chunk kernel does not take go through the per-element path.
+    x = oracle.random_floats(k, 31)
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 32), n, k, bs)
+    got = run_decode(device, x, q, None)
+    assert_close(got, oracle.linear_q(x, q, None, 1), *FP32_TOLERANCE, label=f"ragged {n}x{k}/{bs}")
+
+
+def test_decode_int8_offset_format(device):
+    n, k = 512, 896
+    x = oracle.random_floats(k, 9)
+    q = oracle.quantize_blocks_n(oracle.random_floats(n * k, 10), n, k, 8)
+    got = run_decode(device, x, q, None)
+    assert_close(got, oracle.linear_q(x, q, None, 1), *FP32_TOLERANCE, label="int8 decode")
+
+
+def test_decode_is_deterministic(device):
+    # test/helpers/determinism.ts: repeated runs into separate buffers compare bitwise.
+    n, k = 4864, 896
+    x = oracle.normal_floats(k, 3, 1.0)
+    q = sym_weights(n, k, 77)
+    first = run_decode(device, x, q, None)
+    for _ in range(5):
+        assert np.array_equal(run_decode(device, x, q, None).view(np.uint32), first.view(np.uint32))
+
+
+def test_decode_rejects_bad_dims(device):
+    kern = K.ComputeKernel(device, K.MATMUL_Q4_DECODE)
+    bufs = [device.buffer(4096) for _ in range(6)]
+    u = kern.uniform()
+    u.write(K.matmul_q4_dims(1, 8, 100, False, 64))  # 100 is not a multiple of 64
+    with pytest.raises(K.EgError, match="not a multiple of 64"):
+        kern.encode(kern.bind_group([*bufs, u]), (8, 1, 1))
+    for b in bufs:
+        b.release()
+
+
+# ---- LM head --------------------------------------------------------------------------------
+
+
+@functools.lru_cache(maxsize=None)
+def lm_head_config2():
+    vocab, hidden = 151936, 896
+    table = oracle.normal_floats(vocab * hidden, 0x5EED ^ 0x100, 0.02)
+    q = oracle.quantize_sym(table, vocab, hidden, 8, hidden)
+    del table
+    h = oracle.normal_floats(hidden, 0x5EED ^ 0x101, 1.0)
+    logits = oracle.linear_q(h, q, None, 1)
+    return q, h, logits
+
+
+def _run_head(device, q, h, fused, out_offset=0):
+    bh = device.upload(h)
+    bp, bs, bz = _upload_quant(device, q)
+    n = q.rows
+    bo = device.buffer((n + out_offset) * 4)
+    device.zero(bo, (n + out_offset) * 4)
+    dims = K.embedding_dims(1, q.cols, 0, n, q.block_size, n, out_offset)
+    res = None
+    if fused:
+        br = device.buffer(8)
+        K.lm_head_argmax(device, bh, bp, bs, bz, bo, br, dims, q.bits, q.encoding)
+        res = device.read_array(br, np.uint32, 2)
+        br.release()
+    else:
+        spec = K.embedding_head_spec("q8" if q.bits == 8 else "q4", q.encoding)
+        kern = K.ComputeKernel(device, spec)
+        u = kern.uniform()
+        u.write(dims)
+        kern.encode(kern.bind_group([bh, bp, bs, bz, bo, u]), K.embedding_head_workgroups(n))
+    logits = device.read_array(bo, np.float32, n + out_offset)
+    for b in (bh, bp, bs, bz, bo):
+        if b is not None:
+            b.release()
+    return logits, res
+
+
+def test_lm_head_q8_config2_logits_and_fused_argmax(device):
+    q, h, expect = lm_head_config2()
+    logits, _ = _run_head(device, q, h, fused=False)
+    assert_close(logits, expect, *gemv_tolerance(expect), label="lm_head_q8 config 2")
+    fused_logits, res = _run_head(device, q, h, fused=True)
+    assert np.array_equal(fused_logits.view(np.uint32), logits.view(np.uint32))
+    top2 = np.sort(expect)[-2:]
+    # Bit-exact argmax index whenever the top-2 gap is beyond the GEMV tolerance.
+    assert top2[1] - top2[0] > 1e-3 * abs(top2[1])
+    assert res[0] == oracle.argmax(expect)
+    assert res[0] == oracle.argmax(logits)
+    assert res[1] == logits[res[0]].view(np.uint32)
+
+
+def test_lm_head_q8_reference_format_with_offset(device):
+    rows, hidden = 4096, 896
+    q = oracle.quantize_blocks_n(oracle.random_floats(rows * hidden, 61), rows, hidden, 8)
+    h = oracle.random_floats(hidden, 62)
+    logits, res = _run_head(device, q, h, fused=True, out_offset=1000)
+    expect = oracle.linear_q(h, q, None, 1)
+    assert np.all(logits[:1000] == 0)
+    assert_close(logits[1000:], expect, *FP32_TOLERANCE, label="lm_head_q8 reference format")
+    assert res[0] == 1000 + oracle.argmax(expect)
+
+
+def test_lm_head_q4(device):
+    rows, hidden = 3000, 896
+    q = oracle.quantize_q4_ref(oracle.random_floats(rows * hidden, 71), rows, hidden)
+    h = oracle.random_floats(hidden, 72)
+    logits, _ = _run_head(device, q, h, fused=False)
+    assert_close(logits, oracle.linear_q(h, q, None, 1), *FP32_TOLERANCE, label="lm_head_q4")
+
+
+# ---- argmax ---------------------------------------------------------------------------------
+
+
+def _run_argmax(device, logits, count, offset):
+    kern = K.ComputeKernel(device, K.ARGMAX)
+    bl = device.upload(logits)
+    bo = device.buffer(16)
+    u = kern.uniform()
+    u.write(K.argmax_dims(count, offset))
+    kern.encode(kern.bind_group([bl, bo, u]), K.ARGMAX_WORKGROUPS)
+    out = device.read_array(bo, np.uint32, 2)
+    bl.release()
+    bo.release()
+    return out
+
+
+def test_argmax_full_vocabulary(device):
+    # forward_ops.test.ts:397-421
+    logits = oracle.random_floats(151936, 101)
+    logits[123456] = 99
+    out = _run_argmax(device, logits, 151936, 0)
+    assert out[0] == oracle.argmax_wgsl(logits) == 123456
+    assert out[1] == np.float32(99).view(np.uint32)
+
+
+def test_argmax_ties_to_lowest_index(device):
+    # forward_ops.test.ts:423-446
+    logits = np.full(2048, -1, np.float32)
+    logits[100] = 5
+    logits[900] = 5
+    assert _run_argmax(device, logits, 2048, 0)[0] == 100
+
+
+def test_argmax_offset_selects_a_row(device):
+    logits = oracle.random_floats(3 * 5000, 5)
+    out = _run_argmax(device, logits, 5000, 10000)
+    assert out[0] == oracle.argmax_wgsl(logits[10000:15000])
