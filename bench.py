@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized projection hot path on one MI355X.
+
+Workload: the Qwen2.5-0.5B projection set at M=1 over 24 layers -- q
+896->896, k/v 896->128, o 896->896, gate/up 896->4864, down 4864->896 -- symmetric int4 with an
+f32 scale per 32 weights, x ~ N(0, 1), random N(0, 0.02) weights (synthetic; no checkpoint).
+One step streams every projection once. Inputs are resident in HBM before timing starts.
+
+Reported:
+  value            GB/s of the batched launch (two launches per step: the 144 K=896 matrices,
+                   then the 24 K=4864 ones), cold: 3 weight replicas rotate (672 MB > the
+                   256 MB Infinity Cache), algorithmic bytes / wall time of the timed steps;
+  sequential_*     the same step as 168 per-projection launches in one hipGraph (the
+                   reference's dispatch order), cold;
+  lm_head          config 2: the 151936 x 896 int8 tied head with the fused greedy argmax;
+  per_gemv_us      single launches of each shape, cold;
+  roofline         the dominant kernel (the K=896 batched launch), its algorithmic bytes over
+                   its own HIP-event-timed duration on the library's stream;
+  cpu_baseline     the reference's CPU loop (linearQ4, quant.ts:95-111) as restated by the
+                   oracle, on a bounded sample, host cores stated.
+
+Usage: python bench.py [--gpus 1] [--steps 30] [--warmup 5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "int4 GEMV achieved HBM GB/s (% of 8 TB/s); decode tok/s at 2048 ctx"
+HBM_PEAK_GBS = 8000.0
+HIDDEN, INTER, KV, LAYERS, VOCAB = 896, 4864, 128, 24, 151936
+GROUP = 32
+# (name, rows, K) per layer, in decode order (graph_decode.ts:276-353)
+PROJECTIONS = [("q", HIDDEN, HIDDEN), ("k", KV, HIDDEN), ("v", KV, HIDDEN), ("o", HIDDEN, HIDDEN),
+               ("gate", INTER, HIDDEN), ("up", INTER, HIDDEN), ("down", HIDDEN, INTER)]
+
+
+def gemv_bytes(rows: int, k: int, bits: int = 4, group: int = GROUP) -> int:
+    """Algorithmic bytes of one decode GEMV: codes + f32 scales + x read + y written."""
+    return rows * k * bits // 8 + rows * (k // group) * 4 + k * 4 + rows * 4
+
+
+STEP_BYTES = LAYERS * sum(gemv_bytes(r, k) for _, r, k in PROJECTIONS)
+BATCH896_BYTES = LAYERS * sum(gemv_bytes(r, k) for n, r, k in PROJECTIONS if k == HIDDEN)
+LM_HEAD_BYTES = VOCAB * HIDDEN + VOCAB * 4 + HIDDEN * 4 + VOCAB * 4
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (the library's own)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+
+    def create(self):
+        e = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.hip.hipEventRecord(e, ctypes.c_void_p(stream)) == 0
+
+    def sync(self, e):
+        assert self.hip.hipEventSynchronize(e) == 0
+
+    def ms(self, a, b) -> float:
+        out = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(out), a, b) == 0
+        return out.value
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_projection_set():
+    from enargeia_amd import quant
+
+    mats = []
+    for layer in range(LAYERS):
+        for slot, (name, rows, k) in enumerate(PROJECTIONS):
+            w = quant.normal(rows * k, 0x5EED ^ (layer * 16 + slot), 0.02)
+            mats.append((name, quant.quantize_sym(w, rows, k, 4, GROUP)))
+    return mats
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--replicas", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the path is "
+              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    from enargeia_amd import kernels as K
+    from enargeia_amd import quant
+
+    t0 = time.time()
+    mats = make_projection_set()
+    log(f"quantized {len(mats)} projection matrices in {time.time() - t0:.1f}s")
+
+    dev = K.Device(0)
+    ev = HipEvents()
+    stream = dev.stream
+    R = args.replicas
+
+    rng = np.random.default_rng(7)
+    x896 = dev.upload(rng.standard_normal(HIDDEN, dtype=np.float32))
+    x4864 = dev.upload(rng.standard_normal(INTER, dtype=np.float32))
+    rows_total = sum(q.rows for _, q in mats)
+    out = dev.buffer(rows_total * 4)
+
+    # ---- weights: R replicas, each with its own plans and per-op graph ----
+    replicas = []
+    for r in range(R):
+        bufs, seg896, seg4864, singles = [], [], [], []
+        off = 0
+        for name, q in mats:
+            bp, bs = dev.upload(q.packed), dev.upload(q.scales)
+            bufs += [bp, bs]
+            seg = (bp, bs, None, None, out, q.rows, off)
+            (seg896 if q.cols == HIDDEN else seg4864).append(seg)
+            singles.append((name, q, bp, bs, off))
+            off += q.rows
+        plans = (K.GemvPlan(dev, HIDDEN, GROUP, seg896), K.GemvPlan(dev, INTER, GROUP, seg4864))
+        replicas.append({"bufs": bufs, "plans": plans, "singles": singles})
+    log(f"uploaded {R} replicas of {STEP_BYTES / 1e6:.1f} MB")
+
+    dec = K.ComputeKernel(dev, K.with_format(K.MATMUL_Q4_DECODE, 4, K.ENC_SIGNED))
+    zero_bias = dev.buffer(INTER * 4)
+
+    def per_op(rep):
+        for name, q, bp, bs, off in rep["singles"]:
+            u = dec.uniform()
+            u.write(K.matmul_q4_dims(1, q.rows, q.cols, False, GROUP, q.rows, off))
+            xin = x896 if q.cols == HIDDEN else x4864
+            dec.encode(dec.bind_group([xin, bp, bs, None, zero_bias, out, u]), (1, 1, 1))
+
+    def batched(rep, e_mid=None):
+        rep["plans"][0].launch(x896)
+        if e_mid is not None:
+            ev.record(e_mid, stream)
+        rep["plans"][1].launch(x4864)
+
+    # ---- batched step (value) ----
+    for i in range(args.warmup):
+        batched(replicas[i % R])
+    dev.sync()
+    starts = [ev.create() for _ in range(args.steps)]
+    mids = [ev.create() for _ in range(args.steps)]
+    ends = [ev.create() for _ in range(args.steps)]
+    for i in range(args.steps):
+        ev.record(starts[i], stream)
+        batched(replicas[i % R], mids[i])
+        ev.record(ends[i], stream)
+    ev.sync(ends[-1])
+    total_ms = ev.ms(starts[0], ends[-1])
+    t896 = [ev.ms(starts[i], mids[i]) for i in range(args.steps)]
+    step_ms = total_ms / args.steps
+    value = STEP_BYTES / (step_ms * 1e-3) / 1e9
+    log(f"batched: {step_ms * 1e3:.1f} us/step, {value:.0f} GB/s cold")
+
+    # warm: the same replica every step
+    for _ in range(3):
+        batched(replicas[0])
+    ws, we = ev.create(), ev.create()
+    ev.record(ws, stream)
+    for _ in range(args.steps):
+        batched(replicas[0])
+    ev.record(we, stream)
+    ev.sync(we)
+    warm_ms = ev.ms(ws, we) / args.steps
+    warm_gbs = STEP_BYTES / (warm_ms * 1e-3) / 1e9
+    log(f"batched warm: {warm_ms * 1e3:.1f} us/step, {warm_gbs:.0f} GB/s")
+
+    # ---- per-op sequential step in a hipGraph ----
+    graphs = []
+    for rep in replicas:
+        dev.capture_begin()
+        per_op(rep)
+        graphs.append(dev.capture_end())
+    for i in range(args.warmup):
+        graphs[i % R].launch()
+    ss, se = ev.create(), ev.create()
+    ev.record(ss, stream)
+    for i in range(args.steps):
+        graphs[i % R].launch()
+    ev.record(se, stream)
+    ev.sync(se)
+    seq_ms = ev.ms(ss, se) / args.steps
+    seq_gbs = STEP_BYTES / (seq_ms * 1e-3) / 1e9
+    log(f"per-op graph: {seq_ms * 1e3:.1f} us/step, {seq_gbs:.0f} GB/s cold")
+
+    # ---- single GEMV launches per shape (cold: rotate layers and replicas) ----
+    per_gemv = {}
+    for shape_name in ("q", "k", "gate", "down"):
+        cands = [(rep, s) for rep in replicas for s in rep["singles"] if s[0] == shape_name]
+        times = []
+        for j, (rep, (name, q, bp, bs, off)) in enumerate(cands[: 3 * LAYERS]):
+            u = dec.uniform()
+            u.write(K.matmul_q4_dims(1, q.rows, q.cols, False, GROUP, q.rows, off))
+            a, b = ev.create(), ev.create()
+            xin = x896 if q.cols == HIDDEN else x4864
+            ev.record(a, stream)
+            dec.encode(dec.bind_group([xin, bp, bs, None, zero_bias, out, u]), (1, 1, 1))
+            ev.record(b, stream)
+            ev.sync(b)
+            if j >= 2:
+                times.append(ev.ms(a, b))
+        us = float(np.median(times)) * 1e3
+        nbytes = gemv_bytes(q.rows, q.cols)
+        per_gemv[f"{shape_name}_{q.rows}x{q.cols}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    log(f"per-GEMV: {per_gemv}")
+
+    for g in graphs:
+        g.destroy()
+    for rep in replicas:
+        for p in rep["plans"]:
+            p.destroy()
+        for b in rep["bufs"]:
+            b.release()
+
+    # ---- LM head (config 2), fused argmax, cold over 3 table replicas ----
+    table = quant.quantize_sym(quant.normal(VOCAB * HIDDEN, 0x5EED ^ 0x1000, 0.02), VOCAB, HIDDEN, 8, HIDDEN)
+    heads = [(dev.upload(table.packed), dev.upload(table.scales)) for _ in range(3)]
+    del table
+    h = dev.upload(rng.standard_normal(HIDDEN, dtype=np.float32))
+    logits = dev.buffer(VOCAB * 4)
+    res = dev.buffer(8)
+    dims = K.embedding_dims(1, HIDDEN, 0, VOCAB, HIDDEN, VOCAB, 0)
+    for i in range(args.warmup):
+        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
+    hs = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(hs[0], stream)
+    for i in range(args.steps):
+        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
+        ev.record(hs[i + 1], stream)
+    ev.sync(hs[-1])
+    head_times = [ev.ms(hs[i], hs[i + 1]) for i in range(args.steps)]
+    head_us = float(np.median(head_times)) * 1e3
+    head_gbs = LM_HEAD_BYTES / (head_us * 1e-6) / 1e9
+    log(f"lm_head+argmax: {head_us:.1f} us, {head_gbs:.0f} GB/s cold")
+    for a, b in heads:
+        a.release()
+        b.release()
+
+    # ---- roofline: the dominant kernel = the K=896 batched launch ----
+    t896_ms = float(np.mean(t896))
+    achieved = BATCH896_BYTES / (t896_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "kernel": "gemv_kernel<4,SIGNED,...,BATCHED> (K=896 projections, 24 layers)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": BATCH896_BYTES, "avg_launch_us": round(t896_ms * 1e3, 2)}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(mats)
+    dev.close()
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (random N(0,0.02) weights, N(0,1) inputs)",
+        "config": {"workload": "BASELINE config 1: Qwen2.5-0.5B projection set, 24 layers x 7 int4 GEMVs at M=1",
+                   "format": "int4 symmetric, f32 scale per 32 along K", "bytes_per_step": STEP_BYTES,
+                   "cache": f"cold: {R} rotating weight replicas ({R * STEP_BYTES / 1e6:.0f} MB)",
+                   "launches_per_step": 2},
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "warm_gbs": round(warm_gbs, 1),
+        "sequential_gbs": round(seq_gbs, 1), "sequential_us_per_step": round(seq_ms * 1e3, 1),
+        "sequential_launches_per_step": LAYERS * len(PROJECTIONS),
+        "lm_head": {"config": "BASELINE config 2: 151936x896 int8 per-row + fused argmax", "us": round(head_us, 2),
+                    "gbs": round(head_gbs, 1), "pct_of_peak": round(100 * head_gbs / HBM_PEAK_GBS, 2),
+                    "bytes": LM_HEAD_BYTES},
+        "per_gemv_us": per_gemv,
+        "decode_tok_s_2048": None,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(mats):
+    """The reference's CPU GEMV loop (the oracle's restatement of linearQ4, quant.ts:95-111:
+    per-element dequant, float64 accumulate) over the same config-1 step: once on one thread,
+    then 4 times on every host core. GB/s of the same algorithmic bytes."""
+    import oracle
+
+    rng = np.random.default_rng(3)
+    xs = {HIDDEN: rng.standard_normal(HIDDEN, dtype=np.float32), INTER: rng.standard_normal(INTER, dtype=np.float32)}
+    oq = [oracle.QuantizedMatrix(q.rows, q.cols, q.block_size, 4, oracle.ENC_SIGNED, q.packed, q.scales, None)
+          for _, q in mats]
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+
+    def run(threads, reps):
+        t = time.perf_counter()
+        for _ in range(reps):
+            for q in oq:
+                oracle.gemv_threads(xs[q.cols], q, None, threads)
+        return (time.perf_counter() - t) / reps
+
+    one = run(1, 1)
+    many = run(cores, 4)
+    log(f"cpu baseline: one step in {one * 1e3:.0f} ms on 1 core, {many * 1e3:.0f} ms on {cores} cores")
+    return {"value": round(STEP_BYTES / many / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"the full config-1 step ({STEP_BYTES} B, 168 GEMVs): 1 run on 1 thread, 4 runs on "
+                      f"{cores} threads; oracle restatement of the reference's linearQ4 loop",
+            "single_core_gbs": round(STEP_BYTES / one / 1e9, 4),
+            "step_ms_single_core": round(one * 1e3, 1), "step_ms_all_cores": round(many * 1e3, 1)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

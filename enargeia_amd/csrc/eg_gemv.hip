@@ -21,11 +21,27 @@
 //   * The row total is a butterfly over the team (fixed order: deterministic); no atomics.
 //   * The fused-argmax variant keeps a (value, index) best per lane, reduces it per workgroup
 //     and finishes in the last-arriving workgroup, so one launch yields the greedy token.
+#include <algorithm>
+
 #include "eg_internal.hpp"
 
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup (256 threads)
+
+// One matrix of a batched launch, as the kernel sees it: its pointers and the range of wave
+// passes (RPW rows each) it occupies in the launch's pass space.
+struct DevSegment {
+  const uint4* w;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  float* out;
+  uint32_t pass_end;  // exclusive end of this segment's passes (cumulative)
+  uint32_t rows;
+  uint32_t out_offset;
+  uint32_t pad;
+};
 
 struct GemvArgs {
   const float* x;
@@ -42,6 +58,8 @@ struct GemvArgs {
   uint32_t* partials;      // argmax: (value bits, index) per workgroup
   uint32_t* counter;       // argmax: arrival counter
   uint32_t* result;        // argmax: [index, value bits]
+  const DevSegment* segs;  // batched launches only
+  uint32_t total_passes;   // wave passes over all rows (all segments)
 };
 
 template <int BITS>
@@ -94,15 +112,16 @@ struct Codes<8> {
   }
 };
 
-template <int BITS, int ENC, int TEAM, int CPL, bool ARGMAX>
+template <int BITS, int ENC, int TEAM, int CPL, bool ARGMAX, bool BATCHED>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  static_assert(!(ARGMAX && BATCHED), "the fused argmax is a single-matrix launch");
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t t = lane % TEAM;
   const uint32_t slot = lane / TEAM;
-  const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const uint32_t total_waves = gridDim.x * kWaves;
 
   // This lane's activations, loaded once: chunk j of the lane covers x[c*EPC, c*EPC + EPC).
@@ -136,9 +155,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
-  for (uint32_t pass = wave; pass * RPW < a.n; pass += total_waves) {
-    const uint32_t row = pass * RPW + slot;
-    const bool active = row < a.n;
+  const uint4* w = a.w;
+  const float* scales = a.scales;
+  const uint32_t* zeros = a.zeros;
+  const float* bias = a.bias;
+  float* out = a.out;
+  uint32_t rows = a.n, out_offset = a.out_offset, pass_begin = 0, seg = 0;
+  uint32_t seg_end = BATCHED ? 0u : a.total_passes;  // a batched wave loads its segment first
+
+  for (uint32_t pass = wave; pass < a.total_passes; pass += total_waves) {
+    if (BATCHED && pass >= seg_end) {
+      // Segments are contiguous in pass space and a wave's passes only increase.
+      while (pass >= a.segs[seg].pass_end) seg++;
+      const DevSegment& d = a.segs[seg];
+      w = d.w;
+      scales = d.scales;
+      zeros = d.zeros;
+      bias = d.bias;
+      out = d.out;
+      rows = d.rows;
+      out_offset = d.out_offset;
+      seg_end = d.pass_end;
+      pass_begin = d.pass_end - d.rows / RPW;
+    }
+    const uint32_t row = (pass - pass_begin) * RPW + slot;
+    const bool active = row < rows;
     uint4 q[CPL];
     float s[CPL], z[CPL];
     // Issue every load of this row before any math.
@@ -146,11 +187,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int j = 0; j < CPL; j++) {
       const uint32_t c = t + j * TEAM;
       if (active && c < a.chunks) {
-        q[j] = a.w[(size_t)row * a.chunks + c];
+        q[j] = w[(size_t)row * a.chunks + c];
         const uint32_t blk = row * a.blocks_per_row + blk_in_row[j];
-        s[j] = a.scales[blk];
+        s[j] = scales[blk];
         if (ENC == EG_ENC_OFFSET_ZEROS) {
-          const uint32_t word = a.zeros[blk / C::kZeroPerWord];
+          const uint32_t word = zeros[blk / C::kZeroPerWord];
           z[j] = (float)((word >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
         } else {
           z[j] = (float)(1 << (BITS - 1));
@@ -176,12 +217,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     acc = egd::team_sum<TEAM>(acc);
     if (active && t == 0) {
-      const float v = a.bias ? acc + a.bias[row] : acc;
-      if (a.out) a.out[row + a.out_offset] = v;
+      const float v = bias ? acc + bias[row] : acc;
+      if (out) out[row + out_offset] = v;
       if (ARGMAX) {
-        if (egd::better(v, row + a.out_offset, best_v, best_i)) {
+        if (egd::better(v, row + out_offset, best_v, best_i)) {
           best_v = v;
-          best_i = row + a.out_offset;
+          best_i = row + out_offset;
         }
       }
     }
@@ -316,10 +357,10 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
 
 using KernelFn = void (*)(GemvArgs);
 
-template <int BITS, int ENC, bool ARGMAX>
+template <int BITS, int ENC, bool ARGMAX, bool BATCHED>
 KernelFn pick(int team, int cpl) {
 #define EG_CASE(T, P) \
-  if (team == T && cpl == P) return gemv_kernel<BITS, ENC, T, P, ARGMAX>;
+  if (team == T && cpl == P) return gemv_kernel<BITS, ENC, T, P, ARGMAX, BATCHED>;
 #define EG_TEAM(T) EG_CASE(T, 1) EG_CASE(T, 2) EG_CASE(T, 3) EG_CASE(T, 4)
   EG_TEAM(8) EG_TEAM(16) EG_TEAM(32) EG_TEAM(64)
 #undef EG_TEAM
@@ -327,14 +368,18 @@ KernelFn pick(int team, int cpl) {
   return nullptr;
 }
 
-KernelFn pick_kernel(int bits, int enc, bool argmax, int team, int cpl) {
-  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS)
-    return argmax ? pick<4, EG_ENC_OFFSET_ZEROS, true>(team, cpl) : pick<4, EG_ENC_OFFSET_ZEROS, false>(team, cpl);
-  if (bits == 4 && enc == EG_ENC_SIGNED)
-    return argmax ? pick<4, EG_ENC_SIGNED, true>(team, cpl) : pick<4, EG_ENC_SIGNED, false>(team, cpl);
-  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS)
-    return argmax ? pick<8, EG_ENC_OFFSET_ZEROS, true>(team, cpl) : pick<8, EG_ENC_OFFSET_ZEROS, false>(team, cpl);
-  return argmax ? pick<8, EG_ENC_SIGNED, true>(team, cpl) : pick<8, EG_ENC_SIGNED, false>(team, cpl);
+template <int BITS, int ENC>
+KernelFn pick_mode(bool argmax, bool batched, int team, int cpl) {
+  if (argmax) return pick<BITS, ENC, true, false>(team, cpl);
+  if (batched) return pick<BITS, ENC, false, true>(team, cpl);
+  return pick<BITS, ENC, false, false>(team, cpl);
+}
+
+KernelFn pick_kernel(int bits, int enc, bool argmax, bool batched, int team, int cpl) {
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(argmax, batched, team, cpl);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(argmax, batched, team, cpl);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(argmax, batched, team, cpl);
+  return pick_mode<8, EG_ENC_SIGNED>(argmax, batched, team, cpl);
 }
 
 struct Shape {
@@ -446,7 +491,9 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.partials = partials;
     a.counter = counter;
     a.result = v.result;
-    KernelFn fn = pick_kernel(v.bits, v.encoding, argmax, shape.team, shape.cpl);
+    a.segs = nullptr;
+    a.total_passes = (v.n + (64 / shape.team) - 1) / (64 / shape.team);
+    KernelFn fn = pick_kernel(v.bits, v.encoding, argmax, false, shape.team, shape.cpl);
     if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel for team %d cpl %d", v.op, shape.team, shape.cpl);
     hipLaunchKernelGGL(fn, dim3(shape.grid), dim3(256), 0, ctx->stream, a);
   } else {
@@ -505,6 +552,113 @@ int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, c
       return eg::fail(ctx, EG_ERR_RANGE, "lm_head_argmax: workspace too small for the grid");
   }
   return launch(ctx, v);
+}
+
+}  // extern "C"
+
+// ---- batched plans ------------------------------------------------------------------------
+
+struct eg_gemv_plan {
+  DevSegment* table = nullptr;  // device copy
+  uint32_t count = 0;
+  uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0;
+  int encoding = 0, bits = 0, team = 0, cpl = 0;
+};
+
+extern "C" {
+
+int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int encoding, int bits,
+                        const eg_gemv_segment* segments, uint32_t count, eg_gemv_plan** out_plan) {
+  const char* op = "gemv_plan";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!out_plan || !segments || count == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: empty segment table", op);
+  *out_plan = nullptr;
+  if (bits != 4 && bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8", op);
+  if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", op, encoding);
+  const uint32_t epc = 128u / bits;
+  if (block_size == 0 || k % block_size != 0 || block_size % epc != 0 || k % epc != 0 || k / epc > 256)
+    return eg::fail(ctx, EG_ERR_INVALID,
+                    "%s: k %u / block %u must be multiples of %u codes with at most %u codes per row", op, k,
+                    block_size, epc, 256 * epc);
+  uint64_t rows_total = 0;
+  for (uint32_t i = 0; i < count; i++) {
+    const eg_gemv_segment& g = segments[i];
+    if (!g.packed || !g.scales || !g.out || (encoding == EG_ENC_OFFSET_ZEROS && !g.zeros))
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: segment %u is missing a stream", op, i);
+    if (g.rows == 0 || g.rows % 8 != 0)
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: segment %u has %u rows, not a positive multiple of 8", op, i, g.rows);
+    if ((reinterpret_cast<uintptr_t>(g.packed) & 15u) != 0)
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: segment %u codes are not 16-byte aligned", op, i);
+    if ((uint64_t)g.rows * (k / block_size) >= (1ull << 32))
+      return eg::fail(ctx, EG_ERR_RANGE, "%s: segment %u exceeds the 32-bit block index range", op, i);
+    rows_total += g.rows;
+  }
+  const uint32_t chunks = k / epc;
+  Shape shape = choose_shape((uint32_t)std::min<uint64_t>(rows_total, 0xFFFFFFFFu), chunks, ctx->cu_count);
+  if (shape.team == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel shape for k %u", op, k);
+  const uint32_t rpw = 64u / shape.team;
+  DevSegment* host = new DevSegment[count];
+  uint32_t pass = 0;
+  for (uint32_t i = 0; i < count; i++) {
+    const eg_gemv_segment& g = segments[i];
+    pass += g.rows / rpw;
+    host[i] = DevSegment{reinterpret_cast<const uint4*>(g.packed), g.scales,
+                         encoding == EG_ENC_SIGNED ? nullptr : g.zeros, g.bias, g.out, pass, g.rows, g.out_offset, 0};
+  }
+  eg_gemv_plan* plan = new eg_gemv_plan();
+  hipError_t err = hipMalloc(&plan->table, sizeof(DevSegment) * count);
+  if (err == hipSuccess) err = hipMemcpy(plan->table, host, sizeof(DevSegment) * count, hipMemcpyHostToDevice);
+  delete[] host;
+  if (err != hipSuccess) {
+    if (plan->table) hipFree(plan->table);
+    delete plan;
+    return eg::hip_fail(ctx, err, "gemv_plan_create");
+  }
+  plan->count = count;
+  plan->k = k;
+  plan->block_size = block_size;
+  plan->chunks = chunks;
+  plan->total_passes = pass;
+  plan->encoding = encoding;
+  plan->bits = bits;
+  plan->team = shape.team;
+  plan->cpl = shape.cpl;
+  uint64_t blocks = ((uint64_t)pass + kWaves - 1) / kWaves;
+  const uint64_t cap = (uint64_t)ctx->cu_count * 8;
+  plan->grid = (uint32_t)std::max<uint64_t>(1, std::min(blocks, cap));
+  *out_plan = plan;
+  return EG_OK;
+}
+
+int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* x) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "gemv_plan_launch: ctx is NULL");
+  if (!plan || !x) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: NULL argument");
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: x is not 16-byte aligned");
+  GemvArgs a{};
+  a.x = x;
+  a.chunks = plan->chunks;
+  a.chunks_per_block = plan->block_size / (128u / plan->bits);
+  a.blocks_per_row = plan->k / plan->block_size;
+  a.segs = plan->table;
+  a.total_passes = plan->total_passes;
+  KernelFn fn = pick_kernel(plan->bits, plan->encoding, false, true, plan->team, plan->cpl);
+  hipLaunchKernelGGL(fn, dim3(plan->grid), dim3(256), 0, ctx->stream, a);
+  return eg::check_launch(ctx, "gemv_plan_launch");
+}
+
+int eg_gemv_plan_destroy(eg_context* ctx, eg_gemv_plan* plan) {
+  if (!plan) return EG_OK;
+  if (plan->table) {
+    hipError_t err = hipFree(plan->table);
+    if (err != hipSuccess) {
+      delete plan;
+      return eg::hip_fail(ctx, err, "gemv_plan_destroy");
+    }
+  }
+  delete plan;
+  return EG_OK;
 }
 
 }  // extern "C"

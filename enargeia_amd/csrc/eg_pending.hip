@@ -5,7 +5,3 @@ extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float*, const uint32_
                                     const float*, float*, const eg_matmul_q4_dims*, int, int) {
   return eg::fail(ctx, EG_ERR_STATE, "matmul_q4_prefill: not available in this build");
 }
-
-extern "C" int eg_sample(eg_context* ctx, float*, const uint32_t*, uint32_t*, const eg_sample_dims*) {
-  return eg::fail(ctx, EG_ERR_STATE, "sample: not available in this build");
-}

@@ -385,6 +385,37 @@ _DISPATCH = {
 }
 
 
+class GemvSegment(ctypes.Structure):
+    _fields_ = [("packed", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("zeros", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("out", ctypes.c_void_p), ("rows", ctypes.c_uint32),
+                ("out_offset", ctypes.c_uint32)]
+
+
+class GemvPlan:
+    """Several decode GEMVs sharing one input and K, launched together (eg_gemv_plan_*).
+    ``segments`` are (packed, scales, zeros, bias, out, rows, out_offset) tuples of buffers."""
+
+    def __init__(self, device: Device, k: int, block_size: int, segments, bits: int = 4,
+                 encoding: int = ENC_SIGNED):
+        self.device = device
+        table = (GemvSegment * len(segments))()
+        for i, (packed, scales, zeros, bias, out, rows, out_offset) in enumerate(segments):
+            table[i] = GemvSegment(_ptr(packed) or None, _ptr(scales) or None, _ptr(zeros) or None,
+                                   _ptr(bias) or None, _ptr(out) or None, rows, out_offset)
+        h = ctypes.c_void_p()
+        check(_lib.load().eg_gemv_plan_create(device.ctx, k, block_size, encoding, bits, table, len(segments),
+                                              ctypes.byref(h)), device.ctx)
+        self.handle = h
+
+    def launch(self, x) -> None:
+        check(_lib.load().eg_gemv_plan_launch(self.device.ctx, self.handle, _vp(_ptr(x))), self.device.ctx)
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(_lib.load().eg_gemv_plan_destroy(self.device.ctx, self.handle), self.device.ctx)
+            self.handle = None
+
+
 def lm_head_argmax(device: Device, x, packed, scales, zeros, out, result, dims: bytes, bits: int = 8,
                    encoding: int = ENC_OFFSET_ZEROS) -> None:
     """The fused LM head + greedy argmax (no reference op; see include/enargeia_hip.h)."""
@@ -396,7 +427,7 @@ def lm_head_argmax(device: Device, x, packed, scales, zeros, out, result, dims: 
 
 __all__ = [
     "ARGMAX", "ARGMAX_WORKGROUPS", "Binding", "Buffer", "ComputeKernel", "Device", "ENC_OFFSET_ZEROS",
-    "ENC_SIGNED", "EgError", "EgRangeError", "GREEDY", "Graph", "KernelSpec", "MATMUL_Q4_DECODE",
+    "ENC_SIGNED", "EgError", "EgRangeError", "GREEDY", "GemvPlan", "GemvSegment", "Graph", "KernelSpec", "MATMUL_Q4_DECODE",
     "MATMUL_Q4_PREFILL", "MAX_WORKGROUPS_PER_DIMENSION", "SAMPLE", "SAMPLE_WORKGROUPS", "SamplingParams",
     "argmax_dims", "coverage", "decode_grid_width", "embedding_dims", "embedding_head_spec",
     "embedding_head_workgroups", "lm_head_argmax", "matmul_q4_decode_workgroups", "matmul_q4_dims",

@@ -161,6 +161,27 @@ EG_API int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* pa
                       const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
                       const eg_embedding_dims* dims, int encoding, int bits);
 
+/* Several decode GEMVs that share one input vector and one K, in ONE launch: no counterpart
+ * op in the reference, which dispatches matmul_q4_decode once per projection
+ * (graph_decode.ts:214-236). For q|k|v of a layer (same normed input), gate|up, or one shape
+ * across layers. Each segment is a whole matrix of `rows` rows with the same semantics as
+ * eg_matmul_q4_decode: out[row + out_offset] = sum_k x[k] * W[row, k] (+ bias[row] if bias).
+ * The plan validates the table once and keeps it in device memory, so a launch is
+ * capture-safe. rows must be a multiple of 8 for every segment. */
+typedef struct eg_gemv_segment {
+  const uint32_t* packed;
+  const float* scales;
+  const uint32_t* zeros; /* NULL for EG_ENC_SIGNED */
+  const float* bias;     /* nullable */
+  float* out;
+  uint32_t rows, out_offset;
+} eg_gemv_segment;
+typedef struct eg_gemv_plan eg_gemv_plan;
+EG_API int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int encoding, int bits,
+                               const eg_gemv_segment* segments, uint32_t count, eg_gemv_plan** out_plan);
+EG_API int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* x);
+EG_API int eg_gemv_plan_destroy(eg_context* ctx, eg_gemv_plan* plan);
+
 /* argmax (argmax.wgsl:28-66): out[0] = index of the largest of logits[offset..offset+count)
  * (lowest index on ties; -1e30 sentinel as in the reference), out[1] = its f32 bits. */
 EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const eg_argmax_dims* dims);

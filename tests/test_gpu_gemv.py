@@ -246,3 +246,46 @@ def test_argmax_offset_selects_a_row(device):
     logits = oracle.random_floats(3 * 5000, 5)
     out = _run_argmax(device, logits, 5000, 10000)
     assert out[0] == oracle.argmax_wgsl(logits[10000:15000])
+
+
+# ---- batched plans --------------------------------------------------------------------------
+
+
+def test_batched_plan_matches_per_matrix(device):
+    # q | k | v of one layer plus a gate matrix: four matrices, one input, one launch.
+    k = 896
+    x = oracle.normal_floats(k, 12, 1.0)
+    mats = [sym_weights(n, k, 900 + i) for i, n in enumerate((896, 128, 128, 4864))]
+    bias = oracle.normal_floats(128, 13, 0.02)
+    bx = device.upload(x)
+    keep, segs, outs = [], [], []
+    for i, q in enumerate(mats):
+        bp, bs, _ = _upload_quant(device, q)
+        bb = device.upload(bias) if i == 1 else None
+        bo = device.buffer((q.rows + 3) * 4)
+        device.zero(bo, (q.rows + 3) * 4)
+        keep += [bp, bs, bo] + ([bb] if bb else [])
+        segs.append((bp, bs, None, bb, bo, q.rows, 3))
+        outs.append(bo)
+    plan = K.GemvPlan(device, k, 32, segs)
+    plan.launch(bx)
+    for i, q in enumerate(mats):
+        got = device.read_array(outs[i], np.float32, q.rows + 3)
+        assert np.all(got[:3] == 0)
+        expect = oracle.linear_q(x, q, bias if i == 1 else None, 1)
+        assert_close(got[3:], expect, *gemv_tolerance(expect), label=f"segment {i}")
+    plan.destroy()
+    for b in keep + [bx]:
+        b.release()
+
+
+def test_batched_plan_rejects_bad_tables(device):
+    q = sym_weights(896, 896, 5)
+    bp, bs, _ = _upload_quant(device, q)
+    bo = device.buffer(896 * 4)
+    with pytest.raises(K.EgError, match="not a positive multiple of 8"):
+        K.GemvPlan(device, 896, 32, [(bp, bs, None, None, bo, 12, 0)])
+    with pytest.raises(K.EgError, match="missing a stream"):
+        K.GemvPlan(device, 896, 32, [(bp, bs, None, None, bo, 896, 0)], encoding=K.ENC_OFFSET_ZEROS)
+    for b in (bp, bs, bo):
+        b.release()

@@ -1,0 +1,166 @@
+"""The GPU sampler (eg_sample) against the f32 oracle of sample.wgsl and a float64 statement.
+
+Token identity with the oracle is required wherever the oracle's own decisions are clear of
+their boundaries (every bisection mass at least 2e-6 from topP, the target at least 2e-6 of the
+kept mass from a cumulative boundary; the oracle's f32 running sums carry ~5e-7 relative error
+over 256 chunks, so 2e-6 is ~4 sigma): closer than that, f32 summation order alone decides,
+and the reference's WGSL has no defined order to match. The float64 statement (exact masses)
+is matched at a 1e-6 margin. Penalized logits and every greedy result are bit-exact.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from cases import VOCAB, config2_history, exact_sample, lm_head_config2, penalize
+from enargeia_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+ORACLE_EPS = 2e-6
+EXACT_EPS = 1e-6
+
+
+class Sampler:
+    def __init__(self, device, vocab):
+        self.device = device
+        self.kern = K.ComputeKernel(device, K.SAMPLE)
+        self.vocab = vocab
+        self.logits = device.buffer(vocab * 4)
+        self.history = device.buffer(8192 * 4)
+        self.out = device.buffer(16)
+
+    def __call__(self, logits, history, params, random):
+        d = self.device
+        d.write(self.logits, np.ascontiguousarray(logits, np.float32))
+        h = np.ascontiguousarray(history, np.uint32)
+        if h.size:
+            d.write(self.history, h)
+        d.sync()
+        u = self.kern.uniform()
+        u.write(K.sample_dims(self.vocab, h.size, params, random))
+        self.kern.encode(self.kern.bind_group([self.logits, self.history, self.out, u]), K.SAMPLE_WORKGROUPS)
+        return int(d.read_array(self.out, np.uint32, 1)[0])
+
+    def penalized(self):
+        return self.device.read_array(self.logits, np.float32, self.vocab)
+
+    def close(self):
+        for b in (self.logits, self.history, self.out):
+            b.release()
+
+
+@pytest.fixture(scope="module")
+def config2():
+    return lm_head_config2()[2]
+
+
+def test_greedy_is_argmax_bit_exact(device, config2):
+    s = Sampler(device, VOCAB)
+    try:
+        assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
+        hist = config2_history()
+        params = K.SamplingParams(0.0, 1.0, 1.1)
+        tok = s(config2, hist, params, 0.5)
+        ref_tok, _, ref_logits = oracle.sample(config2, hist, 0.0, 1.0, 1.1, 0.5)
+        assert tok == ref_tok
+        assert np.array_equal(s.penalized().view(np.uint32), ref_logits.view(np.uint32))
+    finally:
+        s.close()
+
+
+def test_penalty_set_semantics_in_place(device):
+    vocab = 5000
+    l = oracle.normal_floats(vocab, 3, 2.0)
+    hist = np.array([7, 7, 4999, 12, 5000, 123456, 12, 0, 7], np.uint32)  # repeats, ids >= vocab
+    s = Sampler(device, vocab)
+    try:
+        s(l, hist, K.SamplingParams(0.0, 1.0, 1.5), 0.5)
+        assert np.array_equal(s.penalized().view(np.uint32), penalize(l, hist, 1.5).view(np.uint32))
+    finally:
+        s.close()
+
+
+def _compare(device, logits, hist, params, draws, label):
+    s = Sampler(device, logits.size)
+    compared = exact_compared = 0
+    try:
+        for r in draws:
+            tok = s(logits, hist, params, r)
+            assert 0 <= tok < logits.size
+            ref, info, _ = oracle.sample(logits, hist, params.temperature, params.top_p,
+                                         params.repetition_penalty, r)
+            if info.bisect_margin > ORACLE_EPS and info.draw_margin > ORACLE_EPS:
+                assert tok == ref, f"{label}: random {r}: gpu {tok} oracle {ref}"
+                compared += 1
+            ex, bm, dm = exact_sample(logits, hist, params.temperature, params.top_p,
+                                      params.repetition_penalty, r)
+            if bm > EXACT_EPS and dm > EXACT_EPS:
+                assert tok == ex, f"{label}: random {r}: gpu {tok} float64 {ex}"
+                exact_compared += 1
+    finally:
+        s.close()
+    return compared, exact_compared
+
+
+def test_config2_temperature_top_p_penalty(device, config2):
+    # T 0.7 / top-p 0.9 / penalty 1.1 over a 512-token history.
+    rng = oracle.Mulberry32Stream(0x5EED)
+    draws = [rng() for _ in range(24)]
+    c, e = _compare(device, config2, config2_history(), K.SamplingParams(0.7, 0.9, 1.1), draws, "config 2")
+    assert e >= 18, f"only {e} of 24 draws clear of float64 boundaries"
+    assert c >= 6, f"only {c} of 24 draws clear of the oracle's f32 boundaries"
+
+
+def test_peaked_distribution_matches_oracle(device):
+    # Real-model-like logits (a few tokens hold most mass): decisions are far from boundaries.
+    logits = oracle.normal_floats(VOCAB, 11, 3.0)
+    rng = oracle.Mulberry32Stream(9)
+    draws = [rng() for _ in range(16)]
+    c, e = _compare(device, logits, np.zeros(0, np.uint32), K.SamplingParams(0.7, 0.9, 1.0), draws, "peaked")
+    assert c >= 12 and e >= 14
+
+
+@pytest.mark.parametrize("vocab", [1, 1000, 1024, 1025, 70001])
+def test_ragged_vocab_sizes(device, vocab):
+    logits = oracle.normal_floats(vocab, vocab, 2.5)
+    rng = oracle.Mulberry32Stream(vocab)
+    draws = [rng() for _ in range(6)]
+    _compare(device, logits, np.array([0, vocab - 1], np.uint32), K.SamplingParams(0.8, 0.95, 1.2), draws,
+             f"vocab {vocab}")
+
+
+def test_top_p_one_and_low_temperature(device):
+    logits = oracle.normal_floats(20000, 5, 2.0)
+    logits[int(np.argmax(logits))] += 1.0
+    s = Sampler(device, logits.size)
+    try:
+        for r in (1e-6, 0.5, 0.999):
+            assert s(logits, [], K.SamplingParams(0.01, 1.0, 1.0), r) == int(np.argmax(logits))
+    finally:
+        s.close()
+    _compare(device, logits, np.zeros(0, np.uint32), K.SamplingParams(1.0, 1.0, 1.0),
+             [0.1, 0.3, 0.6, 0.9], "top-p 1")
+
+
+def test_zero_draw_takes_first_kept_id(device):
+    logits = oracle.normal_floats(9000, 2, 1.0)
+    s = Sampler(device, logits.size)
+    try:
+        assert s(logits, [], K.SamplingParams(0.9, 1.0, 1.0), 0.0) == 0
+        ref = oracle.sample(logits, np.zeros(0, np.uint32), 0.9, 0.5, 1.0, 0.0)[0]
+        assert s(logits, [], K.SamplingParams(0.9, 0.5, 1.0), 0.0) == ref
+    finally:
+        s.close()
+
+
+def test_sampler_deterministic_and_reentrant(device, config2):
+    s = Sampler(device, VOCAB)
+    try:
+        params = K.SamplingParams(0.7, 0.9, 1.0)
+        first = [s(config2, [], params, r) for r in (0.11, 0.52, 0.93)]
+        for _ in range(3):
+            assert [s(config2, [], params, r) for r in (0.11, 0.52, 0.93)] == first
+        assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
+    finally:
+        s.close()

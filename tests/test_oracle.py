@@ -382,6 +382,24 @@ def test_sample_nucleus_and_draw_against_float64():
     assert checked >= 8
 
 
+def test_sample_agrees_with_float64_statement_on_flat_logits():
+    # BASELINE config-2-like flat logits: the f32 oracle and exact float64 masses pick the same
+    # token whenever the oracle's margins clear its own rounding (~5e-7 relative).
+    import cases
+    l = oracle.normal_floats(cases.VOCAB, 77, 0.6)
+    hist = oracle.random_ids(512, 3, cases.VOCAB)
+    rng = oracle.Mulberry32Stream(0x5EED)
+    compared = 0
+    for _ in range(8):
+        r = rng()
+        tok, info, _ = oracle.sample(l, hist, 0.7, 0.9, 1.1, r)
+        ex, bm, dm = cases.exact_sample(l, hist, 0.7, 0.9, 1.1, r)
+        if info.bisect_margin > 2e-6 and info.draw_margin > 2e-6:
+            assert tok == ex
+            compared += 1
+    assert compared >= 3
+
+
 def test_sample_seeded_reproducible_and_varies():
     l = _logits(77, 3000, 1.0)
     h = np.zeros(0, np.uint32)
