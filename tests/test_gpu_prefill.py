@@ -1,0 +1,128 @@
+"""The bf16-MFMA prefill GEMM (eg_matmul_q4_prefill) against the oracle.
+
+Two bars: against the oracle's bf16 model (bf16 x, bf16 dequantized W, exact products, float64
+sums) the MFMA's f32 accumulation must agree to 1e-4; against the fp32 reference
+(linearQ4, quant.ts:95-111) it must be within BASELINE's 2e-2 (per element |a - e| <=
+2e-2 * (|e| + rms(e))). Shapes follow test/kernels/matmul_q4.test.ts:149-196 and config 3.
+"""
+
+import functools
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close
+from enargeia_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def prefill_tol(expect):
+    rms = float(np.sqrt(np.mean(np.asarray(expect, np.float64) ** 2)))
+    return 2e-2 * rms, 2e-2
+
+
+def model_tol(expect):
+    rms = float(np.sqrt(np.mean(np.asarray(expect, np.float64) ** 2)))
+    return 1e-4 * rms, 1e-4
+
+
+def run_prefill(device, x, q, bias, m, out_len=None, out_stride=None, out_offset=0):
+    kern = K.ComputeKernel(device, K.with_format(K.MATMUL_Q4_PREFILL, q.bits, q.encoding))
+    stride = q.rows if out_stride is None else out_stride
+    n_out = out_len if out_len is not None else (m - 1) * stride + q.rows + out_offset
+    bufs = [device.upload(x), device.upload(q.packed), device.upload(q.scales),
+            device.upload(q.zeros) if q.zeros is not None else None,
+            device.upload(bias if bias is not None else np.zeros(q.rows, np.float32))]
+    bo = device.buffer(n_out * 4)
+    device.zero(bo, n_out * 4)
+    u = kern.uniform()
+    u.write(K.matmul_q4_dims(m, q.rows, q.cols, bias is not None, q.block_size, stride, out_offset))
+    kern.encode(kern.bind_group([*bufs, bo, u]), K.matmul_q4_prefill_workgroups(m, q.rows))
+    y = device.read_array(bo, np.float32, n_out)
+    for b in bufs + [bo]:
+        if b is not None:
+            b.release()
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", [(15, 896, 896), (15, 128, 896), (4, 4864, 896), (64, 32, 64)])
+def test_prefill_reference_shapes(device, m, n, k):
+    # matmul_q4.test.ts:149-160, seeds 11/12/13, reference asymmetric block-64 weights + bias.
+    x = oracle.random_floats(m * k, 11)
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 12), n, k)
+    bias = oracle.random_floats(n, 13)
+    got = run_prefill(device, x, q, bias, m)
+    model = oracle.linear_q_bf16(x, q, bias, m)
+    assert_close(got, model, *model_tol(model), label=f"bf16 model {m}x{n}x{k}")
+    fp32 = oracle.linear_q(x, q, bias, m)
+    assert_close(got, fp32, *prefill_tol(fp32), label=f"fp32 reference {m}x{n}x{k}")
+
+
+def test_prefill_ragged_tile(device):
+    # matmul_q4.test.ts:173-179: shapes that do not fill the 64x64 tile.
+    x = oracle.random_floats(3 * 64, 31)
+    q = oracle.quantize_q4_ref(oracle.random_floats(5 * 64, 32), 5, 64)
+    got = run_prefill(device, x, q, None, 3)
+    assert_close(got, oracle.linear_q_bf16(x, q, None, 3), *model_tol(oracle.linear_q(x, q, None, 3)),
+                 label="ragged 3x5x64")
+
+
+def test_prefill_out_offset_and_stride(device):
+    # matmul_q4.test.ts:181-195 (x = 1, W = 0.5 is exact in bf16: 32 at offset 4 and 5).
+    k = 64
+    q = oracle.quantize_q4_ref(np.full(2 * k, 0.5, np.float32), 2, k)
+    got = run_prefill(device, np.ones(k, np.float32), q, None, 1, out_len=6, out_stride=6, out_offset=4)
+    assert got[0] == 0 and got[1] == 0
+    assert got[4] == 32 and got[5] == 32
+
+
+def test_prefill_agrees_with_decode_at_m1(device):
+    # matmul_q4.test.ts:216-230: the two kernels are independent statements of the same math.
+    from test_gpu_gemv import run_decode
+    n, k = 256, 192
+    x = oracle.random_floats(k, 51)
+    q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 52), n, k)
+    dec = run_decode(device, x, q, None)
+    pre = run_prefill(device, x, q, None, 1)
+    assert_close(pre, dec, *prefill_tol(dec), label="prefill vs decode")
+
+
+@functools.lru_cache(maxsize=None)
+def config3(m, n, k, seed):
+    x = oracle.normal_floats(m * k, seed, 1.0)
+    q = oracle.quantize_sym(oracle.normal_floats(n * k, seed + 1, 0.02), n, k, 4, 32)
+    return x, q
+
+
+@pytest.mark.parametrize("m", [256, 128])
+@pytest.mark.parametrize("n,k", [(4864, 896), (896, 4864)])
+def test_prefill_config3(device, m, n, k):
+    # X [m x k] ~ N(0,1) through gate/up (896->4864) and down (4864->896).
+    x, q = config3(m, n, k, 0x5EED ^ (n + k))
+    got = run_prefill(device, x, q, None, m)
+    model = oracle.linear_q_bf16_fast(x, q, None, m)
+    assert_close(got, model, *model_tol(model), label=f"config 3 bf16 model {m}x{n}x{k}")
+    fp32 = oracle.linear_q_fast(x, q, None, m)
+    assert_close(got, fp32, *prefill_tol(fp32), label=f"config 3 fp32 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("bits,k,bs", [(4, 40, 8), (8, 128, 64), (4, 96, 32)])
+def test_prefill_element_staging_path(device, bits, k, bs):
+    m, n = 7, 24
+    x = oracle.random_floats(m * k, 61)
+    if bits == 4:
+        q = oracle.quantize_q4_ref(oracle.random_floats(n * k, 62), n, k, bs)
+    else:
+        q = oracle.quantize_blocks_n(oracle.random_floats(n * k, 62), n, k, 8, bs)
+    got = run_prefill(device, x, q, None, m)
+    assert_close(got, oracle.linear_q_bf16(x, q, None, m), *model_tol(oracle.linear_q(x, q, None, m)),
+                 label=f"element path bits={bits} k={k}")
+
+
+def test_prefill_deterministic(device):
+    x, q = config3(128, 4864, 896, 99)
+    a = run_prefill(device, x, q, None, 128)
+    b = run_prefill(device, x, q, None, 128)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

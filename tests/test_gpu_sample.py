@@ -5,7 +5,9 @@ their boundaries (every bisection mass at least 2e-6 from topP, the target at le
 kept mass from a cumulative boundary; the oracle's f32 running sums carry ~5e-7 relative error
 over 256 chunks, so 2e-6 is ~4 sigma): closer than that, f32 summation order alone decides,
 and the reference's WGSL has no defined order to match. The float64 statement (exact masses)
-is matched at a 1e-6 margin. Penalized logits and every greedy result are bit-exact.
+is matched at a 2e-8 margin: the kernel's fixed-point masses differ from exact float64 by
+~1e-9 of the kept mass (per-element expf differences of an ulp, averaging out). Penalized
+logits and every greedy result are bit-exact.
 """
 
 import numpy as np
@@ -18,7 +20,7 @@ from enargeia_amd import kernels as K
 pytestmark = pytest.mark.gpu
 
 ORACLE_EPS = 2e-6
-EXACT_EPS = 1e-6
+EXACT_EPS = 2e-8
 
 
 class Sampler:
@@ -108,8 +110,24 @@ def test_config2_temperature_top_p_penalty(device, config2):
     rng = oracle.Mulberry32Stream(0x5EED)
     draws = [rng() for _ in range(24)]
     c, e = _compare(device, config2, config2_history(), K.SamplingParams(0.7, 0.9, 1.1), draws, "config 2")
-    assert e >= 18, f"only {e} of 24 draws clear of float64 boundaries"
-    assert c >= 6, f"only {c} of 24 draws clear of the oracle's f32 boundaries"
+    # This realization's nucleus boundary sits 6e-7 from topP: inside the oracle's own f32
+    # rounding, so the oracle comparison is skipped and the float64 one carries the check.
+    assert e >= 22, f"only {e} of 24 draws clear of float64 boundaries"
+
+
+def test_flat_logits_match_oracle_away_from_boundaries(device):
+    # Config-2-like flat logits (sigma 0.6), T 0.7 / top-p 0.9 / penalty 1.1, six realizations.
+    compared = exact = 0
+    for seed in range(6):
+        logits = oracle.normal_floats(VOCAB, 500 + seed, 0.6)
+        hist = oracle.random_ids(512, seed, VOCAB)
+        rng = oracle.Mulberry32Stream(seed)
+        c, e = _compare(device, logits, hist, K.SamplingParams(0.7, 0.9, 1.1), [rng() for _ in range(8)],
+                        f"flat {seed}")
+        compared += c
+        exact += e
+    assert compared >= 12, f"only {compared} of 48 draws clear of the oracle's boundaries"
+    assert exact >= 44
 
 
 def test_peaked_distribution_matches_oracle(device):
