@@ -1,5 +1,7 @@
 // Context, buffers, errors and graph capture: the part of the ABI that replaces the
 // reference's gpu layer (src/gpu/device.ts, pool.ts, readback.ts) for this path.
+#include <cstdlib>
+
 #include "eg_internal.hpp"
 
 namespace {
@@ -76,6 +78,15 @@ int eg_create(int device, eg_context** out_ctx) {
     return hip_fail(nullptr, err, "eg_create: hipStreamCreateWithFlags");
   }
   ctx->stream = ctx->own_stream;
+  if (const char* shape = std::getenv("EG_GEMV_SHAPE")) {
+    int t = 0, c = 0, u = 0;
+    if (std::sscanf(shape, "%d,%d,%d", &t, &c, &u) == 3 && (t == 8 || t == 16 || t == 32 || t == 64) && c >= 1 &&
+        c <= 4 && (u == 1 || u == 2 || u == 4)) {
+      ctx->gemv_override[0] = t;
+      ctx->gemv_override[1] = c;
+      ctx->gemv_override[2] = u;
+    }
+  }
   err = hipMalloc(&ctx->workspace, eg::kWorkspaceBytes);
   if (err != hipSuccess) {
     hipStreamDestroy(ctx->own_stream);

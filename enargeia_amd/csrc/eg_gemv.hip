@@ -19,9 +19,12 @@
 //     sum (code - zero) * x * scale is evaluated as scale * (sum code*x - zero * sum x), with
 //     sum x per chunk precomputed; two's-complement codes are XORed to offset-binary first.
 //   * The row total is a butterfly over the team (fixed order: deterministic); no atomics.
-//   * The fused-argmax variant keeps a (value, index) best per lane, reduces it per workgroup
-//     and finishes in the last-arriving workgroup, so one launch yields the greedy token.
+//   * The fused-argmax variant keeps a (value, index) best per lane and reduces it per
+//     workgroup; a one-workgroup second launch reduces those partials to the greedy token, so
+//     the logits never need a second pass.
 #include <algorithm>
+#include <cstdlib>
+#include <numeric>
 
 #include "eg_internal.hpp"
 
@@ -56,8 +59,6 @@ struct GemvArgs {
   uint32_t blocks_per_row;
   uint32_t out_offset;
   uint32_t* partials;      // argmax: (value bits, index) per workgroup
-  uint32_t* counter;       // argmax: arrival counter
-  uint32_t* result;        // argmax: [index, value bits]
   const DevSegment* segs;  // batched launches only
   uint32_t total_passes;   // wave passes over all rows (all segments)
 };
@@ -112,123 +113,141 @@ struct Codes<8> {
   }
 };
 
-template <int BITS, int ENC, int TEAM, int CPL, bool ARGMAX, bool BATCHED>
+enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2 };
+
+// Where one tile of rows lives: a whole single-matrix launch, or one segment of a batched one.
+struct TileRef {
+  const uint4* w;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  float* out;
+  uint32_t rows, out_offset, row0;
+};
+
+template <int BITS, int U, int CPL>
+struct Loads {
+  uint4 q[U][CPL];
+  float s[U][CPL];
+  uint32_t zw[U][CPL];
+  float b[U];
+};
+
+// One wave computes a tile of RPW * U rows per step: RPW teams of TEAM lanes side by side,
+// each team owning U rows (spaced RPW apart so that, for every (u, j), the wave's load is RPW
+// consecutive rows x TEAM consecutive 16-byte chunks). Every load of a tile (codes, scales,
+// zero-points, bias) is issued before any of its math, so a wave has U * CPL 16-byte loads per
+// lane in flight and the other waves of the CU cover its latency. Loads are unconditional:
+// out-of-range rows read the last row and out-of-range chunk slots read chunk 0, and both are
+// masked (x is zero for a missing chunk; rows are masked at the store), so no load sits under
+// a divergent branch (whose merge would force a wait per load).
+template <int BITS, int ENC, int TEAM, int CPL, int U, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  static_assert(!(ARGMAX && BATCHED), "the fused argmax is a single-matrix launch");
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
+  constexpr int TILE = RPW * U;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t t = lane % TEAM;
   const uint32_t slot = lane / TEAM;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const uint32_t total_waves = gridDim.x * kWaves;
 
-  // This lane's activations, loaded once: chunk j of the lane covers x[c*EPC, c*EPC + EPC).
+  // This lane's activations, loaded once: chunk slot j covers x[c*EPC, c*EPC + EPC).
   float xr[CPL][EPC];
   float sx[CPL];
-  uint32_t blk_in_row[CPL];
+  uint32_t cj[CPL], bj[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; j++) {
     const uint32_t c = t + j * TEAM;
+    const bool valid = c < a.chunks;
+    cj[j] = valid ? c : 0u;
+    bj[j] = cj[j] / a.chunks_per_block;
     sx[j] = 0.f;
-    blk_in_row[j] = 0;
-    if (c < a.chunks) {
-      const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)c * EPC);
+    const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)cj[j] * EPC);
 #pragma unroll
-      for (int e = 0; e < EPC / 4; e++) {
-        const float4 v = xs[e];
-        xr[j][4 * e + 0] = v.x;
-        xr[j][4 * e + 1] = v.y;
-        xr[j][4 * e + 2] = v.z;
-        xr[j][4 * e + 3] = v.w;
-      }
-      blk_in_row[j] = c / a.chunks_per_block;
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPC; e++) xr[j][e] = 0.f;
+    for (int e = 0; e < EPC / 4; e++) {
+      const float4 v = xs[e];
+      xr[j][4 * e + 0] = valid ? v.x : 0.f;
+      xr[j][4 * e + 1] = valid ? v.y : 0.f;
+      xr[j][4 * e + 2] = valid ? v.z : 0.f;
+      xr[j][4 * e + 3] = valid ? v.w : 0.f;
     }
 #pragma unroll
     for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
   }
 
+  uint32_t seg = 0;
+  auto locate = [&](uint32_t tile) -> TileRef {
+    if (MODE == kBatched) {
+      while (tile >= a.segs[seg].pass_end) seg++;
+      const DevSegment& d = a.segs[seg];
+      return TileRef{d.w, d.scales, d.zeros, d.bias, d.out, d.rows, d.out_offset,
+                     (tile - (d.pass_end - d.rows / TILE)) * TILE};
+    }
+    return TileRef{a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, tile * TILE};
+  };
+
+  auto issue = [&](const TileRef& r, Loads<BITS, U, CPL>& L) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t row = min(r.row0 + u * RPW + slot, r.rows - 1);
+      L.b[u] = r.bias ? r.bias[row] : 0.f;
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        L.q[u][j] = r.w[(size_t)row * a.chunks + cj[j]];
+        const uint32_t blk = row * a.blocks_per_row + bj[j];
+        L.s[u][j] = r.scales[blk];
+        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = r.zeros[blk / C::kZeroPerWord];
+      }
+    }
+  };
+
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
-  const uint4* w = a.w;
-  const float* scales = a.scales;
-  const uint32_t* zeros = a.zeros;
-  const float* bias = a.bias;
-  float* out = a.out;
-  uint32_t rows = a.n, out_offset = a.out_offset, pass_begin = 0, seg = 0;
-  uint32_t seg_end = BATCHED ? 0u : a.total_passes;  // a batched wave loads its segment first
-
-  for (uint32_t pass = wave; pass < a.total_passes; pass += total_waves) {
-    if (BATCHED && pass >= seg_end) {
-      // Segments are contiguous in pass space and a wave's passes only increase.
-      while (pass >= a.segs[seg].pass_end) seg++;
-      const DevSegment& d = a.segs[seg];
-      w = d.w;
-      scales = d.scales;
-      zeros = d.zeros;
-      bias = d.bias;
-      out = d.out;
-      rows = d.rows;
-      out_offset = d.out_offset;
-      seg_end = d.pass_end;
-      pass_begin = d.pass_end - d.rows / RPW;
-    }
-    const uint32_t row = (pass - pass_begin) * RPW + slot;
-    const bool active = row < rows;
-    uint4 q[CPL];
-    float s[CPL], z[CPL];
-    // Issue every load of this row before any math.
+  auto compute = [&](const TileRef& r, const Loads<BITS, U, CPL>& L) {
 #pragma unroll
-    for (int j = 0; j < CPL; j++) {
-      const uint32_t c = t + j * TEAM;
-      if (active && c < a.chunks) {
-        q[j] = w[(size_t)row * a.chunks + c];
-        const uint32_t blk = row * a.blocks_per_row + blk_in_row[j];
-        s[j] = scales[blk];
+    for (int u = 0; u < U; u++) {
+      float acc = 0.f;
+      const uint32_t row = r.row0 + u * RPW + slot;
+      const uint32_t crow = min(row, r.rows - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        uint4 q = L.q[u][j];
+        float z;
         if (ENC == EG_ENC_OFFSET_ZEROS) {
-          const uint32_t word = zeros[blk / C::kZeroPerWord];
-          z[j] = (float)((word >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
+          const uint32_t blk = crow * a.blocks_per_row + bj[j];
+          z = (float)((L.zw[u][j] >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
         } else {
-          z[j] = (float)(1 << (BITS - 1));
+          q.x ^= C::kSignFlip;
+          q.y ^= C::kSignFlip;
+          q.z ^= C::kSignFlip;
+          q.w ^= C::kSignFlip;
+          z = (float)(1 << (BITS - 1));
         }
-      } else {
-        q[j] = make_uint4(0, 0, 0, 0);
-        s[j] = 0.f;
-        z[j] = 0.f;
+        acc = fmaf(L.s[u][j], C::dot(q, xr[j]) - z * sx[j], acc);
       }
-    }
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-      uint4 qj = q[j];
-      if (ENC == EG_ENC_SIGNED) {
-        qj.x ^= C::kSignFlip;
-        qj.y ^= C::kSignFlip;
-        qj.z ^= C::kSignFlip;
-        qj.w ^= C::kSignFlip;
-      }
-      const float d = C::dot(qj, xr[j]);
-      acc = fmaf(s[j], d - z[j] * sx[j], acc);
-    }
-    acc = egd::team_sum<TEAM>(acc);
-    if (active && t == 0) {
-      const float v = bias ? acc + bias[row] : acc;
-      if (out) out[row + out_offset] = v;
-      if (ARGMAX) {
-        if (egd::better(v, row + out_offset, best_v, best_i)) {
+      acc = egd::team_sum<TEAM>(acc);
+      if (t == TEAM - 1 && row < r.rows) {
+        const float v = acc + L.b[u];
+        if (r.out) r.out[row + r.out_offset] = v;
+        if (MODE == kArgmax && egd::better(v, row + r.out_offset, best_v, best_i)) {
           best_v = v;
-          best_i = row + out_offset;
+          best_i = row + r.out_offset;
         }
       }
     }
+  };
+
+  for (uint32_t tile = wave; tile < a.total_passes; tile += total_waves) {
+    const TileRef r = locate(tile);
+    Loads<BITS, U, CPL> L;
+    issue(r, L);
+    compute(r, L);
   }
 
-  if (ARGMAX) {
+  if (MODE == kArgmax) {
     __shared__ float wv[kWaves];
     __shared__ uint32_t wi[kWaves];
     egd::team_argmax<64>(best_v, best_i);
@@ -248,33 +267,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       a.partials[2 * blockIdx.x + 0] = __float_as_uint(bv);
       a.partials[2 * blockIdx.x + 1] = bi;
     }
-    if (egd::last_arrival(a.counter, gridDim.x)) {
-      float bv = -1.0e30f;
-      uint32_t bi = a.out_offset;
-      for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
-        const float v = __uint_as_float(a.partials[2 * b]);
-        const uint32_t i = a.partials[2 * b + 1];
-        if (egd::better(v, i, bv, bi)) {
-          bv = v;
-          bi = i;
-        }
-      }
-      egd::team_argmax<64>(bv, bi);
-      if (lane == 0) {
-        wv[threadIdx.x >> 6] = bv;
-        wi[threadIdx.x >> 6] = bi;
-      }
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        for (int k = 1; k < kWaves; k++)
-          if (egd::better(wv[k], wi[k], wv[0], wi[0])) {
-            wv[0] = wv[k];
-            wi[0] = wi[k];
-          }
-        a.result[0] = wi[0];
-        a.result[1] = __float_as_uint(wv[0]);
-      }
-    }
   }
 }
 
@@ -286,7 +278,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
     const float* __restrict__ x, const uint32_t* __restrict__ packed, const float* __restrict__ scales,
     const uint32_t* __restrict__ zeros, const float* __restrict__ bias, float* out, uint32_t n, uint32_t k,
     uint32_t block_size, uint32_t blocks_per_row, uint32_t out_offset, int bits, int encoding,
-    uint32_t* partials, uint32_t* counter, uint32_t* result) {
+    uint32_t* partials) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
   const uint32_t total_waves = gridDim.x * kWaves;
@@ -310,7 +302,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
       acc = fmaf(((float)code - zero) * scales[blk], x[i], acc);
     }
     acc = egd::team_sum<64>(acc);
-    if (lane == 0) {
+    if (lane == 63) {
       const float v = bias ? acc + bias[row] : acc;
       if (out) out[row + out_offset] = v;
       if (ARGMAX && egd::better(v, row + out_offset, best_v, best_i)) {
@@ -339,87 +331,84 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
       partials[2 * blockIdx.x] = __float_as_uint(bv);
       partials[2 * blockIdx.x + 1] = bi;
     }
-    if (egd::last_arrival(counter, gridDim.x) && threadIdx.x == 0) {
-      float bv = -1.0e30f;
-      uint32_t bi = out_offset;
-      for (uint32_t b = 0; b < gridDim.x; b++) {
-        const float v = __uint_as_float(partials[2 * b]);
-        if (egd::better(v, partials[2 * b + 1], bv, bi)) {
-          bv = v;
-          bi = partials[2 * b + 1];
-        }
-      }
-      result[0] = bi;
-      result[1] = __float_as_uint(bv);
-    }
   }
 }
 
 using KernelFn = void (*)(GemvArgs);
 
-template <int BITS, int ENC, bool ARGMAX, bool BATCHED>
-KernelFn pick(int team, int cpl) {
-#define EG_CASE(T, P) \
-  if (team == T && cpl == P) return gemv_kernel<BITS, ENC, T, P, ARGMAX, BATCHED>;
-#define EG_TEAM(T) EG_CASE(T, 1) EG_CASE(T, 2) EG_CASE(T, 3) EG_CASE(T, 4)
-  EG_TEAM(8) EG_TEAM(16) EG_TEAM(32) EG_TEAM(64)
-#undef EG_TEAM
+// Instantiated (TEAM, CPL, U) shapes: one chunk slot per lane for rows of up to 64 chunks
+// (TEAM the next power of two), a full-wave team with 2-4 slots for longer rows.
+#define EG_SHAPES(X)                                                                          \
+  X(8, 1, 1) X(8, 1, 2) X(8, 1, 4) X(16, 1, 1) X(16, 1, 2) X(16, 1, 4) X(32, 1, 1) X(32, 1, 2) \
+  X(32, 1, 4) X(64, 1, 1) X(64, 1, 2) X(64, 1, 4) X(64, 2, 1) X(64, 2, 2) X(64, 3, 1) X(64, 4, 1)
+
+template <int BITS, int ENC, int MODE>
+KernelFn pick(int team, int cpl, int u) {
+#define EG_CASE(T, P, UU) \
+  if (team == T && cpl == P && u == UU) return gemv_kernel<BITS, ENC, T, P, UU, MODE>;
+  EG_SHAPES(EG_CASE)
 #undef EG_CASE
   return nullptr;
 }
 
 template <int BITS, int ENC>
-KernelFn pick_mode(bool argmax, bool batched, int team, int cpl) {
-  if (argmax) return pick<BITS, ENC, true, false>(team, cpl);
-  if (batched) return pick<BITS, ENC, false, true>(team, cpl);
-  return pick<BITS, ENC, false, false>(team, cpl);
+KernelFn pick_mode(int mode, int team, int cpl, int u) {
+  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u);
+  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u);
+  return pick<BITS, ENC, kPlain>(team, cpl, u);
 }
 
-KernelFn pick_kernel(int bits, int enc, bool argmax, bool batched, int team, int cpl) {
-  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(argmax, batched, team, cpl);
-  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(argmax, batched, team, cpl);
-  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(argmax, batched, team, cpl);
-  return pick_mode<8, EG_ENC_SIGNED>(argmax, batched, team, cpl);
+KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u) {
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
+  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u);
 }
 
 struct Shape {
-  int team = 0, cpl = 0;
-  uint32_t grid = 0;
+  int team = 0, cpl = 0, u = 0;
+  uint32_t tiles = 0, grid = 0;
 };
 
-// Team / chunks-per-lane choice. Largest CPL (fewest reductions per weight) that still leaves
-// at least ~4 waves per CU of row passes; small matrices fall back to the widest teams so more
-// waves issue loads at once.
-Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count) {
-  Shape best;
-  uint64_t best_passes = 0;
-  const uint64_t want_passes = (uint64_t)cu_count * 4;
-  for (int cpl = 4; cpl >= 1; cpl--) {
-    int team = 8;
-    while ((uint32_t)(team * cpl) < chunks && team < 64) team *= 2;
-    if ((uint32_t)(team * cpl) < chunks) continue;
-    if (cpl > 1 && (uint32_t)(team * (cpl - 1)) >= chunks) continue;  // a chunk slot always idle
-    const uint64_t rpw = 64 / team;
-    const uint64_t passes = (n + rpw - 1) / rpw;
-    if (passes >= want_passes) {  // largest CPL with enough parallelism
-      best.team = team;
-      best.cpl = cpl;
-      best_passes = passes;
-      break;
-    }
-    if (passes > best_passes) {  // otherwise the most parallel candidate
-      best.team = team;
-      best.cpl = cpl;
-      best_passes = passes;
-    }
-  }
-  if (best.team == 0) return best;
-  uint64_t blocks = (best_passes + kWaves - 1) / kWaves;
+uint32_t grid_for(uint32_t tiles, int cu_count) {
+  // One tile per wave up to 8 workgroups of 4 waves per CU; larger matrices loop.
+  uint64_t blocks = ((uint64_t)tiles + kWaves - 1) / kWaves;
   const uint64_t cap = (uint64_t)cu_count * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  best.grid = (uint32_t)blocks;
-  return best;
+  return (uint32_t)blocks;
+}
+
+// One chunk slot per lane while rows have <= 64 chunks (x costs 32 VGPRs), four rows per lane
+// per tile; longer rows take the full wave and 2-4 slots, with fewer rows per tile to stay
+// within ~128 VGPRs. `row_multiple` (batched plans) is the row count every segment divides.
+Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count, const eg_context* ctx, uint32_t row_multiple = 0) {
+  Shape sh;
+  if (chunks == 0 || chunks > 256) return sh;
+  if (chunks <= 64) {
+    sh.team = 8;
+    while ((uint32_t)sh.team < chunks) sh.team *= 2;
+    sh.cpl = 1;
+    sh.u = 4;
+  } else {
+    sh.team = 64;
+    sh.cpl = (int)((chunks + 63) / 64);
+    sh.u = sh.cpl == 2 ? 2 : 1;
+  }
+  if (ctx && ctx->gemv_override[0]) {
+    sh.team = ctx->gemv_override[0];
+    sh.cpl = ctx->gemv_override[1];
+    sh.u = ctx->gemv_override[2];
+    if ((uint32_t)(sh.team * sh.cpl) < chunks) return Shape{};
+  }
+  const uint32_t rpw = 64u / sh.team;
+  if (row_multiple)
+    while (sh.u > 1 && row_multiple % (rpw * sh.u) != 0) sh.u /= 2;
+  if (row_multiple && row_multiple % (rpw * sh.u) != 0) return Shape{};
+  const uint32_t tile_rows = rpw * sh.u;
+  sh.tiles = (n + tile_rows - 1) / tile_rows;
+  sh.grid = grid_for(sh.tiles, cu_count);
+  return sh;
 }
 
 struct QuantView {
@@ -471,12 +460,14 @@ int launch(eg_context* ctx, const QuantView& v) {
                        (reinterpret_cast<uintptr_t>(v.x) & 15u) == 0;
   const uint32_t chunks = v.k / epc;
   Shape shape;
-  if (aligned && v.k % epc == 0 && v.block_size % epc == 0 && chunks <= 256)
-    shape = choose_shape(v.n, chunks, ctx->cu_count);
-  uint32_t* counter = eg::counters(ctx) + eg::kCounterLmHeadArgmax;
+  if (aligned && v.k % epc == 0 && v.block_size % epc == 0)
+    shape = choose_shape(v.n, chunks, ctx->cu_count, ctx);
   uint32_t* partials = reinterpret_cast<uint32_t*>(eg::partials(ctx));
-  if (shape.team != 0) {
-    GemvArgs a;
+  uint32_t grid = 0;
+  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, argmax ? kArgmax : kPlain, shape.team, shape.cpl, shape.u)
+                           : nullptr;
+  if (fn) {
+    GemvArgs a{};
     a.x = v.x;
     a.w = reinterpret_cast<const uint4*>(v.packed);
     a.scales = v.scales;
@@ -489,26 +480,25 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.blocks_per_row = v.blocks_per_row;
     a.out_offset = v.out_offset;
     a.partials = partials;
-    a.counter = counter;
-    a.result = v.result;
     a.segs = nullptr;
-    a.total_passes = (v.n + (64 / shape.team) - 1) / (64 / shape.team);
-    KernelFn fn = pick_kernel(v.bits, v.encoding, argmax, false, shape.team, shape.cpl);
-    if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel for team %d cpl %d", v.op, shape.team, shape.cpl);
+    a.total_passes = shape.tiles;
+    grid = shape.grid;
     hipLaunchKernelGGL(fn, dim3(shape.grid), dim3(256), 0, ctx->stream, a);
   } else {
     uint64_t blocks = (v.n + kWaves - 1) / kWaves;
     const uint64_t cap = (uint64_t)ctx->cu_count * 8;
     if (blocks > cap) blocks = cap;
+    grid = (uint32_t)blocks;
     if (argmax)
       hipLaunchKernelGGL(gemv_generic_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, v.x,
                          v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
-                         v.out_offset, v.bits, v.encoding, partials, counter, v.result);
+                         v.out_offset, v.bits, v.encoding, partials);
     else
       hipLaunchKernelGGL(gemv_generic_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, v.x,
                          v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
-                         v.out_offset, v.bits, v.encoding, partials, counter, v.result);
+                         v.out_offset, v.bits, v.encoding, partials);
   }
+  if (argmax) eg::launch_argmax_finalize(ctx, partials, grid, v.out_offset, v.result);
   return eg::check_launch(ctx, v.op);
 }
 
@@ -562,7 +552,7 @@ struct eg_gemv_plan {
   DevSegment* table = nullptr;  // device copy
   uint32_t count = 0;
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0;
-  int encoding = 0, bits = 0, team = 0, cpl = 0;
+  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0;
 };
 
 extern "C" {
@@ -595,14 +585,16 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
     rows_total += g.rows;
   }
   const uint32_t chunks = k / epc;
-  Shape shape = choose_shape((uint32_t)std::min<uint64_t>(rows_total, 0xFFFFFFFFu), chunks, ctx->cu_count);
-  if (shape.team == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel shape for k %u", op, k);
-  const uint32_t rpw = 64u / shape.team;
+  uint32_t row_gcd = 0;
+  for (uint32_t i = 0; i < count; i++) row_gcd = std::gcd(row_gcd, segments[i].rows);
+  Shape shape = choose_shape((uint32_t)std::min<uint64_t>(rows_total, 0xFFFFFFFFu), chunks, ctx->cu_count, ctx, row_gcd);
+  if (shape.team == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel shape for k %u and these row counts", op, k);
+  const uint32_t tile_rows = (64u / shape.team) * shape.u;
   DevSegment* host = new DevSegment[count];
   uint32_t pass = 0;
   for (uint32_t i = 0; i < count; i++) {
     const eg_gemv_segment& g = segments[i];
-    pass += g.rows / rpw;
+    pass += g.rows / tile_rows;
     host[i] = DevSegment{reinterpret_cast<const uint4*>(g.packed), g.scales,
                          encoding == EG_ENC_SIGNED ? nullptr : g.zeros, g.bias, g.out, pass, g.rows, g.out_offset, 0};
   }
@@ -624,9 +616,8 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->bits = bits;
   plan->team = shape.team;
   plan->cpl = shape.cpl;
-  uint64_t blocks = ((uint64_t)pass + kWaves - 1) / kWaves;
-  const uint64_t cap = (uint64_t)ctx->cu_count * 8;
-  plan->grid = (uint32_t)std::max<uint64_t>(1, std::min(blocks, cap));
+  plan->u = shape.u;
+  plan->grid = grid_for(pass, ctx->cu_count);
   *out_plan = plan;
   return EG_OK;
 }
@@ -643,7 +634,8 @@ int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* 
   a.blocks_per_row = plan->k / plan->block_size;
   a.segs = plan->table;
   a.total_passes = plan->total_passes;
-  KernelFn fn = pick_kernel(plan->bits, plan->encoding, false, true, plan->team, plan->cpl);
+  KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u);
+  if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   hipLaunchKernelGGL(fn, dim3(plan->grid), dim3(256), 0, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }

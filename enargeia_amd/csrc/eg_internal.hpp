@@ -16,12 +16,14 @@ struct eg_context {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;  // own_stream or a caller's stream
   int cu_count = 256;
-  // Workspace for cross-workgroup reductions (partials, histograms, arrival counters).
-  // Counters are zeroed once at creation and left at zero by every kernel that uses them,
-  // so no memset is ever recorded into a captured graph.
+  // Workspace for cross-workgroup reductions (partials, histograms, small state). Every
+  // element is written before it is read within one op, so it needs no clearing.
   uint8_t* workspace = nullptr;
   size_t workspace_bytes = 0;
   bool capturing = false;
+  // GEMV shape override (team, chunks per lane, rows per lane) from EG_GEMV_SHAPE="t,c,u",
+  // read once at creation; zeros mean the built-in choice. For tuning sweeps.
+  int gemv_override[3] = {0, 0, 0};
   char error[512] = {0};
 };
 
@@ -36,23 +38,20 @@ int fail(eg_context* ctx, int status, const char* fmt, ...) __attribute__((forma
 int hip_fail(eg_context* ctx, hipError_t err, const char* what);
 
 // Workspace layout (bytes from ctx->workspace). Fixed offsets; sizes bound the op limits.
-constexpr size_t kCountersOffset = 0;          // 64 u32 arrival counters
-constexpr size_t kStateOffset = 256;           // 4 KiB of small per-op state
+constexpr size_t kStateOffset = 256;           // small per-op state
 constexpr size_t kPartialsOffset = 8192;       // per-workgroup partials
 constexpr size_t kWorkspaceBytes = 16u << 20;  // 16 MiB
 
-enum Counter : int {
-  kCounterLmHeadArgmax = 0,
-  kCounterArgmax = 1,
-  kCounterSampleBase = 8,  // the sampler uses kCounterSampleBase .. +15
-};
-
-inline uint32_t* counters(eg_context* ctx) {
-  return reinterpret_cast<uint32_t*>(ctx->workspace + kCountersOffset);
-}
 inline uint8_t* state(eg_context* ctx) { return ctx->workspace + kStateOffset; }
 inline uint8_t* partials(eg_context* ctx) { return ctx->workspace + kPartialsOffset; }
 constexpr size_t kPartialsBytes = kWorkspaceBytes - kPartialsOffset;
+
+// Second stage of every multi-workgroup argmax: one workgroup reduces `groups` partials
+// (value bits, index) in a fixed order into result = [index, value bits]. A separate launch
+// rather than a last-arriving workgroup: the arrival protocol needs an agent-scope release
+// (an L2 writeback) in every workgroup, which costs far more than a launch.
+void launch_argmax_finalize(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t sentinel_index,
+                            uint32_t* result);
 
 // Validates a launch once the kernel is enqueued (hipGetLastError catches bad configurations
 // immediately; faults surface at the next synchronisation).
@@ -76,12 +75,25 @@ __device__ __forceinline__ float ub1(uint32_t v) { return (float)((v >> 8) & 0xf
 __device__ __forceinline__ float ub2(uint32_t v) { return (float)((v >> 16) & 0xffu); }
 __device__ __forceinline__ float ub3(uint32_t v) { return (float)(v >> 24); }
 
-// Sum across a team of TEAM consecutive lanes (power of two <= 64); every lane of the team
-// receives the total. Fixed butterfly order, so the result is deterministic.
+// One DPP step: v + (v as seen through dpp_ctrl). Lanes whose source is disabled read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, ROW_MASK == 0xF);
+  return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum across a team of TEAM consecutive lanes (TEAM a power of two <= 64, teams aligned), by
+// DPP only: quad permutes, half-row and row mirrors, then row_bcast:15 / row_bcast:31 for
+// teams spanning rows of 16 lanes. The total is valid in lane TEAM-1 of each team (in every
+// lane of the team when TEAM <= 16). Fixed order, so the result is deterministic.
 template <int TEAM>
 __device__ __forceinline__ float team_sum(float v) {
-#pragma unroll
-  for (int m = TEAM / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  if (TEAM >= 2) v = dpp_add<0xB1>(v);         // quad_perm [1,0,3,2]
+  if (TEAM >= 4) v = dpp_add<0x4E>(v);         // quad_perm [2,3,0,1]
+  if (TEAM >= 8) v = dpp_add<0x141>(v);        // row_half_mirror
+  if (TEAM >= 16) v = dpp_add<0x140>(v);       // row_mirror
+  if (TEAM >= 32) v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  if (TEAM >= 64) v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 
@@ -102,27 +114,6 @@ __device__ __forceinline__ void team_argmax(float& v, uint32_t& i) {
       i = oi;
     }
   }
-}
-
-// Arrival at a per-op counter after a workgroup published its partial results. Returns true
-// in exactly one workgroup, the last to arrive, which may then read every workgroup's
-// partials. Each thread releases its own partial writes at agent scope (written back past
-// this XCD's L2) before thread 0 counts the arrival; the last workgroup acquires at agent
-// scope (stale L2 lines invalidated) before reading. The last arrival resets the counter to
-// zero for the next launch. Call from all threads of the workgroup.
-__device__ __forceinline__ bool last_arrival(uint32_t* counter, uint32_t expected) {
-  __shared__ uint32_t is_last;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == expected - 1) ? 1u : 0u;
-    if (is_last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  const bool last = is_last != 0;
-  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return last;
 }
 
 }  // namespace egd

@@ -12,17 +12,20 @@
 //     running kept mass reaches the target (:266-321); argmax fallback (:324-331).
 //
 // MI355X design. The reference makes ~36 passes over the vocabulary inside one workgroup. Here
-// the vocabulary is split over many workgroups and the work is 2 + 4 + 1 passes:
-//   pass_max   : penalty on this workgroup's slice (LDS copy + in-place global write), then
-//                (max, argmax) of l/T; the last workgroup reduces the partials (greedy ends here).
-//   pass_sum   : sum of exp(l/T - max) in float64 per workgroup, reduced to the f32 normaliser.
-//   pass_level : one pass per 8 bisection steps. The 255 mids those 8 steps could visit are the
-//                in-order nodes of a depth-8 bisection tree below (lo, hi), computed with the
-//                same f32 expression; every p in [lo, hi) is binned against them and p >= hi
-//                goes to an 'above' bin. The last workgroup then replays the 8 steps exactly:
-//                mass(p >= mid) is 'above' plus a suffix sum of bins.
-//   pass_draw  : kept mass per workgroup; the last workgroup finds the workgroup whose prefix
-//                reaches the target, then the element, in ascending id order.
+// the vocabulary is split over G workgroups (4096 ids each) and the work is 7 short launches;
+// no launch waits on another workgroup, and each launch starts by re-reducing the previous
+// launches' few per-workgroup partials itself, in a fixed order, so every workgroup derives
+// the same global values:
+//   pass_max   : penalty on this workgroup's slice (LDS copy + in-place global write), then the
+//                slice's (max, argmax) of l/T (of l when greedy);
+//   pass_sum   : global max; the slice's sum of exp(l/T - max) in float64;
+//   pass_level : one launch per 8 bisection steps. The 255 mids those 8 steps could visit are
+//                the in-order nodes of a depth-8 bisection tree below the current (lo, hi),
+//                computed with the same f32 expression; every p in [lo, hi) is binned against
+//                them, p >= hi goes to an 'above' bin. Replaying the 8 steps from the summed
+//                bins is exact: mass(p >= mid) is 'above' plus a suffix sum of bins;
+//   pass_kept  : the threshold after 32 steps, the slice's kept mass;
+//   finalize   : one workgroup: the target, the slice whose prefix reaches it, then the id.
 // Masses are fixed-point integers (p * 2^52, exact for p >= 2^-28) summed with integer adds, so
 // every mass is independent of summation order and the result is deterministic. They differ
 // from the reference's f32 tree sums only by rounding, which can change a decision only when
@@ -32,9 +35,9 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerThread = 4;
+constexpr int kPerThread = 16;
 constexpr uint32_t kSlice = kThreads * kPerThread;  // vocabulary ids per workgroup
-constexpr uint32_t kMaxGroups = 2048;               // vocab <= 2M
+constexpr uint32_t kMaxGroups = 256;                // vocab <= 1,048,576
 constexpr int kBins = 256;
 constexpr int kLevels = 4;                          // 4 x 8 = 32 bisection steps
 constexpr double kFix = 4503599627370496.0;         // 2^52
@@ -49,19 +52,15 @@ static_assert(sizeof(SampleParams) == 32, "sample dims are 32 bytes");
 struct SampleState {
   float max_scaled;
   uint32_t argmax;
-  float total;   // f32 normaliser
-  float lo, hi;  // bisection bracket
+  float total;
   float threshold;
-  uint32_t token;
-  uint32_t pad;
 };
 
 struct Work {
   SampleState* state;
-  uint32_t* counters;     // 4 arrival counters
   uint32_t* max_part;     // 2 u32 per group
   double* sum_part;       // 1 per group
-  uint64_t* bin_part;     // (kBins + 1) per group
+  uint64_t* bin_part;     // kLevels x groups x (kBins + 1)
   uint64_t* kept_part;    // 1 per group
   uint32_t* count_part;   // 1 per group
 };
@@ -74,13 +73,10 @@ __device__ __forceinline__ float prob(float logit, const SampleParams& p, float 
   return expf(logit / p.temperature - mx) / total;
 }
 
-__device__ __forceinline__ uint64_t to_fix(float p) {
-  return (uint64_t)__double2ull_rn((double)p * kFix);
-}
+__device__ __forceinline__ uint64_t to_fix(float p) { return (uint64_t)__double2ull_rn((double)p * kFix); }
 
 template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* scratch) {
-  // Wave butterfly then the 4 wave totals in fixed order.
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
@@ -110,17 +106,110 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* sv, u
   __syncthreads();
 }
 
-// ---- pass 1: penalty + max/argmax -------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32_t* history, uint32_t* out,
-                                                     SampleParams hp, const SampleParams* dp, Work w) {
+// ---- the global values every launch re-derives from the partials ------------------------
+
+__device__ void global_max(const Work& w, uint32_t groups, float& mx, uint32_t& amax) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+  float bv = -1.0e30f;
+  uint32_t bi = 0;
+  for (uint32_t b = threadIdx.x; b < groups; b += kThreads) {
+    const float v = __uint_as_float(w.max_part[2 * b]);
+    const uint32_t i = w.max_part[2 * b + 1];
+    if (egd::better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  block_argmax(bv, bi, sv, si);
+  mx = bv;
+  amax = bi;
+}
+
+__device__ float global_total(const Work& w, uint32_t groups) {
+  __shared__ double scratch[4];
+  double t = 0.0;
+  for (uint32_t b = threadIdx.x; b < groups; b += kThreads) t += w.sum_part[b];
+  return (float)block_sum(t, scratch);
+}
+
+// In-order mid j (0..254) of the depth-8 bisection tree below [lo, hi): the f32 mid the
+// bisection reaches when its path of left/right choices spells j.
+__device__ float tree_mid(uint32_t j, float lo, float hi) {
+  const uint32_t target = j + 1;  // 1-based in-order index, root = 128
+  uint32_t cur = 128, step = 64;
+  float mid = (lo + hi) * 0.5f;
+  while (cur != target) {
+    if (target < cur) {
+      hi = mid;
+      cur -= step;
+    } else {
+      lo = mid;
+      cur += step;
+    }
+    step >>= 1;
+    mid = (lo + hi) * 0.5f;
+  }
+  return mid;
+}
+
+// Number of mids <= v (upper bound over a non-decreasing array of kBins - 1 values).
+__device__ __forceinline__ int count_le(const float* mids, float v) {
+  int a = 0, b = kBins - 1;
+  while (a < b) {
+    const int m = (a + b) >> 1;
+    if (mids[m] <= v) a = m + 1;
+    else b = m;
+  }
+  return a;
+}
+
+// Replays the 8 bisection steps of `level` from its summed bins: (lo, hi) in, (lo, hi) out.
+__device__ void replay_level(const Work& w, uint32_t groups, int level, float top_p, float& lo, float& hi,
+                             float* mids, unsigned long long* sums) {
+  if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
+  const uint64_t* part = w.bin_part + (size_t)level * kMaxGroups * (kBins + 1);
+  for (int i = threadIdx.x; i <= kBins; i += kThreads) {
+    uint64_t s = 0;
+    for (uint32_t b = 0; b < groups; b++) s += part[(size_t)b * (kBins + 1) + i];
+    sums[i] = s;
+  }
+  __syncthreads();
+  __shared__ float out_lo, out_hi;
+  if (threadIdx.x == 0) {
+    // sums[k] := mass of p >= hi plus bins k..kBins-1 (suffix sums)
+    unsigned long long run = sums[kBins];
+    for (int k = kBins - 1; k >= 0; k--) {
+      run += sums[k];
+      sums[k] = run;
+    }
+    float l = lo, h = hi;
+    const double top = (double)top_p;
+    for (int s = 0; s < 8; s++) {
+      const float mid = (l + h) * 0.5f;
+      const double mass = (double)sums[count_le(mids, mid)] / kFix;
+      if (mass < top) h = mid;
+      else l = mid;
+    }
+    out_lo = l;
+    out_hi = h;
+  }
+  __syncthreads();
+  lo = out_lo;
+  hi = out_hi;
+}
+
+// ---- launches --------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32_t* history, SampleParams hp,
+                                                     const SampleParams* dp, Work w) {
   const SampleParams p = load_params(hp, dp);
   __shared__ float slice[kSlice];
   __shared__ float sv[4];
   __shared__ uint32_t si[4];
   const uint32_t base = blockIdx.x * kSlice;
   const uint32_t end = min(base + kSlice, p.vocab);
-  for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads)
-    slice[i] = base + i < end ? logits[base + i] : 0.f;
+  for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads) slice[i] = base + i < end ? logits[base + i] : 0.f;
   __syncthreads();
   if (p.repetition_penalty != 1.0f) {
     // Each distinct id once (its first occurrence), and only ids this slice owns: no two
@@ -146,15 +235,11 @@ __global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32
   const bool greedy = p.temperature <= 0.0f;
   float bv = -1.0e30f;
   uint32_t bi = greedy ? 0u : base;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    if (i < end) {
-      const float v = greedy ? slice[i - base] : slice[i - base] / p.temperature;
-      if (egd::better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
+  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
+    const float v = greedy ? slice[i - base] : slice[i - base] / p.temperature;
+    if (egd::better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
     }
   }
   block_argmax(bv, bi, sv, si);
@@ -162,188 +247,113 @@ __global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32
     w.max_part[2 * blockIdx.x] = __float_as_uint(bv);
     w.max_part[2 * blockIdx.x + 1] = bi;
   }
-  if (egd::last_arrival(&w.counters[0], gridDim.x)) {
-    bv = -1.0e30f;
-    bi = 0;
-    for (uint32_t b = threadIdx.x; b < gridDim.x; b += kThreads) {
-      const float v = __uint_as_float(w.max_part[2 * b]);
-      const uint32_t i = w.max_part[2 * b + 1];
-      if (egd::better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    block_argmax(bv, bi, sv, si);
-    if (threadIdx.x == 0) {
-      w.state->max_scaled = bv;
-      w.state->argmax = bi;
-      w.state->lo = 0.0f;
-      w.state->hi = 1.0f;
-      if (greedy) out[0] = bi;
-    }
-  }
 }
 
-// ---- pass 2: normaliser -------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void pass_sum(const float* logits, SampleParams hp, const SampleParams* dp,
                                                      Work w) {
   const SampleParams p = load_params(hp, dp);
   if (p.temperature <= 0.0f) return;
   __shared__ double scratch[4];
-  const float mx = w.state->max_scaled;
+  float mx;
+  uint32_t amax;
+  global_max(w, gridDim.x, mx, amax);
   const uint32_t base = blockIdx.x * kSlice;
+  const uint32_t end = min(base + kSlice, p.vocab);
   double s = 0.0;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    if (i < p.vocab) s += (double)expf(logits[i] / p.temperature - mx);
-  }
+  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) s += (double)expf(logits[i] / p.temperature - mx);
   s = block_sum(s, scratch);
   if (threadIdx.x == 0) w.sum_part[blockIdx.x] = s;
-  if (egd::last_arrival(&w.counters[1], gridDim.x)) {
-    double t = 0.0;
-    for (uint32_t b = threadIdx.x; b < gridDim.x; b += kThreads) t += w.sum_part[b];
-    t = block_sum(t, scratch);
-    if (threadIdx.x == 0) w.state->total = (float)t;
-  }
 }
 
-// In-order mid j (0..254) of the depth-8 bisection tree below [lo, hi): the f32 mid the
-// bisection reaches when its path of left/right choices spells j.
-__device__ float tree_mid(uint32_t j, float lo, float hi) {
-  const uint32_t target = j + 1;  // 1-based in-order index, root = 128
-  uint32_t cur = 128, step = 64;
-  float mid = (lo + hi) * 0.5f;
-  while (cur != target) {
-    if (target < cur) {
-      hi = mid;
-      cur -= step;
-    } else {
-      lo = mid;
-      cur += step;
-    }
-    step >>= 1;
-    mid = (lo + hi) * 0.5f;
-  }
-  return mid;
-}
-
-// ---- passes 3-6: 8 bisection steps each -------------------------------------------------
-__global__ __launch_bounds__(kThreads) void pass_level(const float* logits, SampleParams hp, const SampleParams* dp,
-                                                       Work w) {
+__global__ __launch_bounds__(kThreads) void pass_level(const float* logits, int level, SampleParams hp,
+                                                       const SampleParams* dp, Work w) {
   const SampleParams p = load_params(hp, dp);
   if (p.temperature <= 0.0f || !(p.top_p < 1.0f)) return;
   __shared__ float mids[kBins - 1];
-  __shared__ unsigned long long bins[kBins + 1];  // [kBins] = p >= hi
-  const float lo = w.state->lo, hi = w.state->hi;
-  const float mx = w.state->max_scaled, total = w.state->total;
+  __shared__ unsigned long long bins[kBins + 1];
+  float mx;
+  uint32_t amax;
+  global_max(w, gridDim.x, mx, amax);
+  const float total = global_total(w, gridDim.x);
+  float lo = 0.0f, hi = 1.0f;
+  for (int l = 0; l < level; l++) replay_level(w, gridDim.x, l, p.top_p, lo, hi, mids, bins);
   if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
   for (int i = threadIdx.x; i <= kBins; i += kThreads) bins[i] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kSlice;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    if (i >= p.vocab) continue;
+  const uint32_t end = min(base + kSlice, p.vocab);
+  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
     const float pr = prob(logits[i], p, mx, total);
     if (pr < lo) continue;
-    int k;
-    if (pr >= hi) {
-      k = kBins;
-    } else {  // number of mids <= pr (upper bound over a non-decreasing array)
-      int a = 0, b = kBins - 1;
-      while (a < b) {
-        const int m = (a + b) >> 1;
-        if (mids[m] <= pr) a = m + 1;
-        else b = m;
-      }
-      k = a;
-    }
-    atomicAdd(&bins[k], (unsigned long long)to_fix(pr));
+    const int k = pr >= hi ? kBins : count_le(mids, pr);
+    atomicAdd(&bins[k], (unsigned long long)to_fix(pr));  // integer adds: order-independent
   }
   __syncthreads();
-  uint64_t* mine = w.bin_part + (size_t)blockIdx.x * (kBins + 1);
+  uint64_t* mine = w.bin_part + ((size_t)level * kMaxGroups + blockIdx.x) * (kBins + 1);
   for (int i = threadIdx.x; i <= kBins; i += kThreads) mine[i] = bins[i];
-  if (egd::last_arrival(&w.counters[2], gridDim.x)) {
-    // Column sums over the groups (integers: order-independent), then a suffix sum.
-    for (int i = threadIdx.x; i <= kBins; i += kThreads) {
-      uint64_t s = 0;
-      for (uint32_t b = 0; b < gridDim.x; b++) s += w.bin_part[(size_t)b * (kBins + 1) + i];
-      bins[i] = s;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      // suffix[k] = mass of p >= hi plus bins k..255; stored back into bins[0..255].
-      uint64_t run = bins[kBins];
-      for (int k = kBins - 1; k >= 0; k--) {
-        run += bins[k];
-        bins[k] = run;
-      }
-      float l = lo, h = hi;
-      const double top = (double)p.top_p;
-      for (int s = 0; s < 8; s++) {
-        const float mid = (l + h) * 0.5f;
-        int a = 0, b = kBins - 1;  // u = number of mids <= mid
-        while (a < b) {
-          const int m = (a + b) >> 1;
-          if (mids[m] <= mid) a = m + 1;
-          else b = m;
-        }
-        const uint64_t mass_fx = a < kBins ? bins[a] : bins[kBins];
-        const double mass = (double)mass_fx / kFix;
-        if (mass < top) h = mid;
-        else l = mid;
-      }
-      w.state->lo = l;
-      w.state->hi = h;
-    }
-  }
 }
 
-// ---- pass 7: kept mass and the draw ----------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void pass_draw(const float* logits, uint32_t* out, SampleParams hp,
-                                                      const SampleParams* dp, Work w) {
+__global__ __launch_bounds__(kThreads) void pass_kept(const float* logits, SampleParams hp, const SampleParams* dp,
+                                                      Work w) {
   const SampleParams p = load_params(hp, dp);
   if (p.temperature <= 0.0f) return;
-  __shared__ unsigned long long scratch[4];
+  __shared__ float mids[kBins - 1];
+  __shared__ unsigned long long bins[kBins + 1];
+  __shared__ unsigned long long kscratch[4];
   __shared__ uint32_t cscratch[4];
-  __shared__ uint32_t pick;
-  __shared__ uint64_t group_prefix;
-  __shared__ uint32_t group;
-  const float mx = w.state->max_scaled, total = w.state->total;
-  const float thr = (p.top_p < 1.0f) ? w.state->lo : 0.0f;
+  float mx;
+  uint32_t amax;
+  global_max(w, gridDim.x, mx, amax);
+  const float total = global_total(w, gridDim.x);
+  float lo = 0.0f, hi = 1.0f;
+  if (p.top_p < 1.0f)
+    for (int l = 0; l < kLevels; l++) replay_level(w, gridDim.x, l, p.top_p, lo, hi, mids, bins);
+  const float thr = p.top_p < 1.0f ? lo : 0.0f;
   const uint32_t base = blockIdx.x * kSlice;
+  const uint32_t end = min(base + kSlice, p.vocab);
   unsigned long long kept = 0;
   uint32_t count = 0;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    if (i < p.vocab) {
-      const float pr = prob(logits[i], p, mx, total);
-      if (pr >= thr) {
-        kept += to_fix(pr);
-        count++;
-      }
+  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
+    const float pr = prob(logits[i], p, mx, total);
+    if (pr >= thr) {
+      kept += to_fix(pr);
+      count++;
     }
   }
-  kept = block_sum(kept, scratch);
+  kept = block_sum(kept, kscratch);
   count = block_sum(count, cscratch);
   if (threadIdx.x == 0) {
     w.kept_part[blockIdx.x] = kept;
     w.count_part[blockIdx.x] = count;
+    if (blockIdx.x == 0) *w.state = SampleState{mx, amax, total, thr};
   }
-  if (!egd::last_arrival(&w.counters[3], gridDim.x)) return;
+}
 
-  // The last group: total kept mass, target, the group that holds the crossing.
+// One workgroup: greedy result, or the target and the id where the kept mass reaches it.
+__global__ __launch_bounds__(kThreads) void finalize(const float* logits, uint32_t* out, uint32_t groups,
+                                                     SampleParams hp, const SampleParams* dp, Work w) {
+  const SampleParams p = load_params(hp, dp);
+  if (p.temperature <= 0.0f) {
+    float mx;
+    uint32_t amax;
+    global_max(w, groups, mx, amax);
+    if (threadIdx.x == 0) out[0] = amax;
+    return;
+  }
+  __shared__ uint32_t group, pick;
+  __shared__ unsigned long long group_prefix;
+  __shared__ double target_fx;
+  __shared__ unsigned long long tsum[kThreads];
+  const SampleState st = *w.state;
   if (threadIdx.x == 0) {
     uint64_t all = 0;
-    for (uint32_t b = 0; b < gridDim.x; b++) all += w.kept_part[b];
+    for (uint32_t b = 0; b < groups; b++) all += w.kept_part[b];
     double kd = (double)all / kFix;
     if (kd < 1.0e-20) kd = 1.0e-20;
-    const double target_fx = (double)p.random * kd * kFix;
+    target_fx = (double)p.random * kd * kFix;
     uint64_t run = 0;
     group = 0xFFFFFFFFu;
-    for (uint32_t b = 0; b < gridDim.x; b++) {
+    for (uint32_t b = 0; b < groups; b++) {
       const uint64_t next = run + w.kept_part[b];
       if (w.count_part[b] > 0 && (double)next >= target_fx) {
         group = b;
@@ -353,27 +363,18 @@ __global__ __launch_bounds__(kThreads) void pass_draw(const float* logits, uint3
     }
     group_prefix = run;
     pick = 0xFFFFFFFFu;
-    w.state->threshold = thr;
   }
   __syncthreads();
   if (group != 0xFFFFFFFFu) {
-    // Walk the group's slice in id order: thread t owns ids [t*4, t*4+4) of the slice so that
-    // thread order is id order; an exclusive scan of the per-thread kept masses gives each
-    // thread its starting prefix.
-    __shared__ unsigned long long tsum[kThreads];
+    // Thread t owns ids [t*16, t*16+16) of the slice, so thread order is id order; an
+    // exclusive scan of the per-thread kept masses gives each thread its starting prefix.
     const uint32_t gbase = group * kSlice;
-    float pv[kPerThread];
     unsigned long long mine = 0;
-#pragma unroll
     for (int r = 0; r < kPerThread; r++) {
       const uint32_t i = gbase + threadIdx.x * kPerThread + r;
-      pv[r] = -1.0f;
       if (i < p.vocab) {
-        const float pr = prob(logits[i], p, mx, total);
-        if (pr >= thr) {
-          pv[r] = pr;
-          mine += to_fix(pr);
-        }
+        const float pr = prob(logits[i], p, st.max_scaled, st.total);
+        if (pr >= st.threshold) mine += to_fix(pr);
       }
     }
     tsum[threadIdx.x] = mine;
@@ -387,39 +388,27 @@ __global__ __launch_bounds__(kThreads) void pass_draw(const float* logits, uint3
       }
     }
     __syncthreads();
-    double kd = 0.0;
-    {
-      uint64_t all = 0;
-      for (uint32_t b = 0; b < gridDim.x; b++) all += w.kept_part[b];
-      kd = (double)all / kFix;
-      if (kd < 1.0e-20) kd = 1.0e-20;
-    }
-    const double target_fx = (double)p.random * kd * kFix;
     unsigned long long run = tsum[threadIdx.x];
-#pragma unroll
     for (int r = 0; r < kPerThread; r++) {
-      if (pv[r] >= 0.0f) {
-        run += to_fix(pv[r]);
+      const uint32_t i = gbase + threadIdx.x * kPerThread + r;
+      if (i >= p.vocab) break;
+      const float pr = prob(logits[i], p, st.max_scaled, st.total);
+      if (pr >= st.threshold) {
+        run += to_fix(pr);
         if ((double)run >= target_fx) {
-          atomicMin(&pick, gbase + threadIdx.x * kPerThread + r);
+          atomicMin(&pick, i);
           break;
         }
       }
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    const uint32_t tok = pick != 0xFFFFFFFFu ? pick : w.state->argmax;
-    out[0] = tok;
-    w.state->token = tok;
-  }
+  if (threadIdx.x == 0) out[0] = pick != 0xFFFFFFFFu ? pick : st.argmax;
 }
 
-Work workspace(eg_context* ctx, uint32_t groups) {
+Work workspace(eg_context* ctx) {
   Work w;
-  uint8_t* st = eg::state(ctx);
-  w.state = reinterpret_cast<SampleState*>(st + 512);
-  w.counters = eg::counters(ctx) + eg::kCounterSampleBase;
+  w.state = reinterpret_cast<SampleState*>(eg::state(ctx) + 512);
   uint8_t* part = eg::partials(ctx);
   size_t off = 0;
   w.max_part = reinterpret_cast<uint32_t*>(part + off);
@@ -431,24 +420,27 @@ Work workspace(eg_context* ctx, uint32_t groups) {
   w.count_part = reinterpret_cast<uint32_t*>(part + off);
   off += (size_t)kMaxGroups * 4;
   w.bin_part = reinterpret_cast<uint64_t*>(part + off);
-  (void)groups;
+  off += (size_t)kLevels * kMaxGroups * (kBins + 1) * 8;
+  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * kMaxGroups * (kBins + 1) * 8 <= eg::kPartialsBytes,
+                "sampler partials exceed the workspace");
   return w;
 }
 
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
            const SampleParams* dp, bool all_passes) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
-  Work w = workspace(ctx, groups);
+  Work w = workspace(ctx);
   const dim3 grid(groups), block(kThreads);
-  hipLaunchKernelGGL(pass_max, grid, block, 0, ctx->stream, logits, history, out, hp, dp, w);
+  hipLaunchKernelGGL(pass_max, grid, block, 0, ctx->stream, logits, history, hp, dp, w);
   const bool sampled = all_passes || hp.temperature > 0.0f;
   if (sampled) {
     hipLaunchKernelGGL(pass_sum, grid, block, 0, ctx->stream, logits, hp, dp, w);
     if (all_passes || hp.top_p < 1.0f)
       for (int l = 0; l < kLevels; l++)
-        hipLaunchKernelGGL(pass_level, grid, block, 0, ctx->stream, logits, hp, dp, w);
-    hipLaunchKernelGGL(pass_draw, grid, block, 0, ctx->stream, logits, out, hp, dp, w);
+        hipLaunchKernelGGL(pass_level, grid, block, 0, ctx->stream, logits, l, hp, dp, w);
+    hipLaunchKernelGGL(pass_kept, grid, block, 0, ctx->stream, logits, hp, dp, w);
   }
+  hipLaunchKernelGGL(finalize, dim3(1), block, 0, ctx->stream, logits, out, groups, hp, dp, w);
   return eg::check_launch(ctx, "sample");
 }
 
