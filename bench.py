@@ -255,6 +255,31 @@ def main() -> int:
     head_us = float(np.median(head_times)) * 1e3
     head_gbs = LM_HEAD_BYTES / (head_us * 1e-6) / 1e9
     log(f"lm_head+argmax: {head_us:.1f} us, {head_gbs:.0f} GB/s cold")
+
+    # sampled token (config 2: T 0.7, top-p 0.9, penalty 1.1 over 512 ids): LM head + sampler
+    smp = K.ComputeKernel(dev, K.SAMPLE)
+    hist = dev.upload(rng.integers(0, VOCAB, 512).astype(np.uint32))
+    tok = dev.buffer(16)
+    head_k = K.ComputeKernel(dev, K.embedding_head_spec("q8", K.ENC_SIGNED))
+
+    def sampled_token(i):
+        hu = head_k.uniform()
+        hu.write(dims)
+        head_k.encode(head_k.bind_group([h, heads[i % 3][0], heads[i % 3][1], None, logits, hu]), (1, 1, 1))
+        su = smp.uniform()
+        su.write(K.sample_dims(VOCAB, 512, K.SamplingParams(0.7, 0.9, 1.1), (i * 0.618) % 1.0))
+        smp.encode(smp.bind_group([logits, hist, tok, su]), (1, 1, 1))
+
+    for i in range(args.warmup):
+        sampled_token(i)
+    ss2 = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(ss2[0], stream)
+    for i in range(args.steps):
+        sampled_token(i)
+        ev.record(ss2[i + 1], stream)
+    ev.sync(ss2[-1])
+    sampled_us = float(np.median([ev.ms(ss2[i], ss2[i + 1]) for i in range(args.steps)])) * 1e3
+    log(f"lm_head+sample (T 0.7, top-p 0.9, penalty 1.1): {sampled_us:.1f} us")
     for a, b in heads:
         a.release()
         b.release()
@@ -284,7 +309,9 @@ def main() -> int:
         "sequential_launches_per_step": LAYERS * len(PROJECTIONS),
         "lm_head": {"config": "BASELINE config 2: 151936x896 int8 per-row + fused argmax", "us": round(head_us, 2),
                     "gbs": round(head_gbs, 1), "pct_of_peak": round(100 * head_gbs / HBM_PEAK_GBS, 2),
-                    "bytes": LM_HEAD_BYTES},
+                    "bytes": LM_HEAD_BYTES,
+                    "sampled_token_us": round(sampled_us, 2),
+                    "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history"},
         "per_gemv_us": per_gemv,
         "decode_tok_s_2048": None,
         "roofline": roofline,

@@ -379,9 +379,9 @@ uint32_t grid_for(uint32_t tiles, int cu_count) {
   return (uint32_t)blocks;
 }
 
-// One chunk slot per lane while rows have <= 64 chunks (x costs 32 VGPRs), four rows per lane
-// per tile; longer rows take the full wave and 2-4 slots, with fewer rows per tile to stay
-// within ~128 VGPRs. `row_multiple` (batched plans) is the row count every segment divides.
+// One chunk slot per lane while rows have <= 64 chunks (x costs 32 VGPRs), two rows per lane
+// per tile (four for full-wave teams); longer rows take the full wave and 2-4 slots, with
+// fewer rows per tile to stay within ~128 VGPRs. `row_multiple` (batched plans) is the row count every segment divides.
 Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count, const eg_context* ctx, uint32_t row_multiple = 0) {
   Shape sh;
   if (chunks == 0 || chunks > 256) return sh;
@@ -389,7 +389,7 @@ Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count, const eg_context* 
     sh.team = 8;
     while ((uint32_t)sh.team < chunks) sh.team *= 2;
     sh.cpl = 1;
-    sh.u = 4;
+    sh.u = sh.team == 64 ? 4 : 2;  // measured on MI355X: int8 rows of 56 chunks / int4 rows of 28
   } else {
     sh.team = 64;
     sh.cpl = (int)((chunks + 63) / 64);

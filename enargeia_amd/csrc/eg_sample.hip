@@ -16,14 +16,16 @@
 // no launch waits on another workgroup, and each launch starts by re-reducing the previous
 // launches' few per-workgroup partials itself, in a fixed order, so every workgroup derives
 // the same global values:
-//   pass_max   : penalty on this workgroup's slice (LDS copy + in-place global write), then the
-//                slice's (max, argmax) of l/T (of l when greedy);
+//   pass_max   : penalty on this workgroup's slice (a hit mask of the history ids it owns, LDS
+//                copy + in-place global write), then the slice's (max, argmax) of l/T (of l
+//                when greedy);
 //   pass_sum   : global max; the slice's sum of exp(l/T - max) in float64;
 //   pass_level : one launch per 8 bisection steps. The 255 mids those 8 steps could visit are
 //                the in-order nodes of a depth-8 bisection tree below the current (lo, hi),
 //                computed with the same f32 expression; every p in [lo, hi) is binned against
-//                them, p >= hi goes to an 'above' bin. Replaying the 8 steps from the summed
-//                bins is exact: mass(p >= mid) is 'above' plus a suffix sum of bins;
+//                them, p >= hi goes to an 'above' bin, and each group adds its bins into one
+//                global set with integer atomics. Replaying the 8 steps from the summed bins is
+//                exact: mass(p >= mid) is 'above' plus a suffix sum of bins;
 //   pass_kept  : the threshold after 32 steps, the slice's kept mass;
 //   finalize   : one workgroup: the target, the slice whose prefix reaches it, then the id.
 // Masses are fixed-point integers (p * 2^52, exact for p >= 2^-28) summed with integer adds, so
@@ -37,7 +39,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kPerThread = 16;
 constexpr uint32_t kSlice = kThreads * kPerThread;  // vocabulary ids per workgroup
-constexpr uint32_t kMaxGroups = 256;                // vocab <= 1,048,576
+constexpr uint32_t kMaxGroups = 256;                // vocab <= 1,048,576 (finalize: one group per thread)
 constexpr int kBins = 256;
 constexpr int kLevels = 4;                          // 4 x 8 = 32 bisection steps
 constexpr double kFix = 4503599627370496.0;         // 2^52
@@ -54,13 +56,14 @@ struct SampleState {
   uint32_t argmax;
   float total;
   float threshold;
+  float lo[kLevels + 1], hi[kLevels + 1];  // bracket each level bins against; [kLevels] = final
 };
 
 struct Work {
   SampleState* state;
   uint32_t* max_part;     // 2 u32 per group
   double* sum_part;       // 1 per group
-  uint64_t* bin_part;     // kLevels x groups x (kBins + 1)
+  unsigned long long* bins;  // kLevels x (kBins + 1), summed over groups by integer atomics
   uint64_t* kept_part;    // 1 per group
   uint32_t* count_part;   // 1 per group
 };
@@ -164,32 +167,66 @@ __device__ __forceinline__ int count_le(const float* mids, float v) {
   return a;
 }
 
-// Replays the 8 bisection steps of `level` from its summed bins: (lo, hi) in, (lo, hi) out.
-__device__ void replay_level(const Work& w, uint32_t groups, int level, float top_p, float& lo, float& hi,
-                             float* mids, unsigned long long* sums) {
-  if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
-  const uint64_t* part = w.bin_part + (size_t)level * kMaxGroups * (kBins + 1);
-  for (int i = threadIdx.x; i <= kBins; i += kThreads) {
-    uint64_t s = 0;
-    for (uint32_t b = 0; b < groups; b++) s += part[(size_t)b * (kBins + 1) + i];
-    sums[i] = s;
+// Exclusive prefix sum of one u64 per thread over the workgroup, in thread order; *total gets
+// the sum of all. Wave scan by shuffles, then the four wave totals.
+__device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigned long long* total) {
+  __shared__ unsigned long long wsum[kThreads / 64];
+  const int lane = threadIdx.x & 63;
+  unsigned long long incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned long long o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wsum[threadIdx.x >> 6] = incl;
+  __syncthreads();
+  unsigned long long before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; w++) {
+    if (w < (int)(threadIdx.x >> 6)) before += wsum[w];
+    all += wsum[w];
   }
   __syncthreads();
+  if (total) *total = all;
+  return before + incl - v;
+}
+
+// Replays the 8 bisection steps of `level` from its summed bins: (lo, hi) in, (lo, hi) out.
+// All threads: the 255 tree mids, the bin column sums, the suffix sums and the mass at every
+// tree node in parallel; then the 8-step walk reads one node mass per step.
+__device__ void replay_level(const Work& w, uint32_t groups, int level, float top_p, float& lo, float& hi,
+                             float* mids, unsigned long long* sums) {
+  __shared__ unsigned long long suffix[kBins + 1];
+  __shared__ double node_mass[kBins - 1];
   __shared__ float out_lo, out_hi;
+  if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
+  const unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
+  for (int i = threadIdx.x; i <= kBins; i += kThreads) sums[i] = summed[i];
+  __syncthreads();
+  // suffix[k] = mass of p >= hi (sums[kBins]) plus bins k..kBins-1: total minus an exclusive
+  // prefix, so one block scan instead of a serial walk.
+  static_assert(kBins == kThreads, "one bin per thread");
+  unsigned long long total = 0;
+  const unsigned long long before = block_exclusive_scan(sums[threadIdx.x], &total);
+  suffix[threadIdx.x] = sums[kBins] + (total - before);
+  if (threadIdx.x == 0) suffix[kBins] = sums[kBins];
+  __syncthreads();
+  if (threadIdx.x < kBins - 1) node_mass[threadIdx.x] = (double)suffix[count_le(mids, mids[threadIdx.x])] / kFix;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    // sums[k] := mass of p >= hi plus bins k..kBins-1 (suffix sums)
-    unsigned long long run = sums[kBins];
-    for (int k = kBins - 1; k >= 0; k--) {
-      run += sums[k];
-      sums[k] = run;
-    }
-    float l = lo, h = hi;
     const double top = (double)top_p;
+    float l = lo, h = hi;
+    uint32_t cur = 128, step = 64;
     for (int s = 0; s < 8; s++) {
-      const float mid = (l + h) * 0.5f;
-      const double mass = (double)sums[count_le(mids, mid)] / kFix;
-      if (mass < top) h = mid;
-      else l = mid;
+      const float mid = mids[cur - 1];
+      if (node_mass[cur - 1] < top) {
+        h = mid;
+        cur -= step;
+      } else {
+        l = mid;
+        cur += step;
+      }
+      step >>= 1;
     }
     out_lo = l;
     out_hi = h;
@@ -212,22 +249,23 @@ __global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32
   for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads) slice[i] = base + i < end ? logits[base + i] : 0.f;
   __syncthreads();
   if (p.repetition_penalty != 1.0f) {
-    // Each distinct id once (its first occurrence), and only ids this slice owns: no two
-    // threads ever write the same element.
+    // The penalty applies once per distinct history id (the reference applies it at an id's
+    // first occurrence only): mark the ids this slice owns, then penalize each marked element
+    // once. No two threads write the same element.
+    __shared__ uint8_t hit[kSlice];
+    for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads) hit[i] = 0;
+    __syncthreads();
     for (uint32_t h = threadIdx.x; h < p.history_length; h += kThreads) {
       const uint32_t id = history[h];
-      if (id < base || id >= end) continue;
-      bool first = true;
-      for (uint32_t e = 0; e < h; e++)
-        if (history[e] == id) {
-          first = false;
-          break;
-        }
-      if (first) {
-        const float v = slice[id - base];
+      if (id >= base && id < end) hit[id - base] = 1;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < end - base; i += kThreads) {
+      if (hit[i]) {
+        const float v = slice[i];
         const float r = v > 0.0f ? v / p.repetition_penalty : v * p.repetition_penalty;
-        slice[id - base] = r;
-        logits[id] = r;
+        slice[i] = r;
+        logits[base + i] = r;
       }
     }
     __syncthreads();
@@ -259,10 +297,22 @@ __global__ __launch_bounds__(kThreads) void pass_sum(const float* logits, Sample
   global_max(w, gridDim.x, mx, amax);
   const uint32_t base = blockIdx.x * kSlice;
   const uint32_t end = min(base + kSlice, p.vocab);
+  float lv[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const uint32_t i = base + r * kThreads + threadIdx.x;
+    lv[r] = i < end ? logits[i] : 0.f;
+  }
   double s = 0.0;
-  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) s += (double)expf(logits[i] / p.temperature - mx);
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++)
+    if (base + r * kThreads + threadIdx.x < end) s += (double)expf(lv[r] / p.temperature - mx);
   s = block_sum(s, scratch);
   if (threadIdx.x == 0) w.sum_part[blockIdx.x] = s;
+  // The level launches accumulate into these; clear them for this call (a kernel, not a
+  // memset, so a captured graph replays it).
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < kLevels * (kBins + 1); i += kThreads) w.bins[i] = 0;
 }
 
 __global__ __launch_bounds__(kThreads) void pass_level(const float* logits, int level, SampleParams hp,
@@ -271,26 +321,70 @@ __global__ __launch_bounds__(kThreads) void pass_level(const float* logits, int 
   if (p.temperature <= 0.0f || !(p.top_p < 1.0f)) return;
   __shared__ float mids[kBins - 1];
   __shared__ unsigned long long bins[kBins + 1];
+  const uint32_t base = blockIdx.x * kSlice;
+  const uint32_t end = min(base + kSlice, p.vocab);
+  float lv[kPerThread];  // issued first: independent of everything read below
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const uint32_t i = base + r * kThreads + threadIdx.x;
+    lv[r] = i < end ? logits[i] : 0.f;
+  }
   float mx;
   uint32_t amax;
   global_max(w, gridDim.x, mx, amax);
   const float total = global_total(w, gridDim.x);
+  // The bracket this level bins against: (0, 1) first, then the previous level's bracket
+  // replayed through its 8 steps. Workgroup 0 records it for the next launch.
   float lo = 0.0f, hi = 1.0f;
-  for (int l = 0; l < level; l++) replay_level(w, gridDim.x, l, p.top_p, lo, hi, mids, bins);
+  if (level > 0) {
+    lo = w.state->lo[level - 1];
+    hi = w.state->hi[level - 1];
+    replay_level(w, gridDim.x, level - 1, p.top_p, lo, hi, mids, bins);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    w.state->lo[level] = lo;
+    w.state->hi[level] = hi;
+  }
   if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
   for (int i = threadIdx.x; i <= kBins; i += kThreads) bins[i] = 0;
   __syncthreads();
-  const uint32_t base = blockIdx.x * kSlice;
-  const uint32_t end = min(base + kSlice, p.vocab);
-  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
-    const float pr = prob(logits[i], p, mx, total);
-    if (pr < lo) continue;
-    const int k = pr >= hi ? kBins : count_le(mids, pr);
-    atomicAdd(&bins[k], (unsigned long long)to_fix(pr));  // integer adds: order-independent
+  // The mids split [lo, hi) into 256 near-equal steps, so the bin is estimated arithmetically
+  // and corrected against the exact f32 mids (usually no step). Runs of equal bins are summed
+  // in registers before the LDS atomic (at the first level nearly every p shares bin 0).
+  const float scale = (float)kBins / (hi - lo);
+  int run_bin = -1;
+  unsigned long long run_mass = 0;
+  float pv[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const uint32_t i = base + r * kThreads + threadIdx.x;
+    pv[r] = i < end ? prob(lv[r], p, mx, total) : -1.0f;
   }
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const float pr = pv[r];
+    if (pr < lo) continue;
+    int k;
+    if (pr >= hi) {
+      k = kBins;
+    } else {
+      k = min(max((int)((pr - lo) * scale), 0), kBins - 1);  // estimate of #mids <= pr
+      while (k < kBins - 1 && mids[k] <= pr) k++;
+      while (k > 0 && mids[k - 1] > pr) k--;
+    }
+    if (k != run_bin) {
+      if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);  // integer adds: order-independent
+      run_bin = k;
+      run_mass = 0;
+    }
+    run_mass += to_fix(pr);
+  }
+  if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);
   __syncthreads();
-  uint64_t* mine = w.bin_part + ((size_t)level * kMaxGroups + blockIdx.x) * (kBins + 1);
-  for (int i = threadIdx.x; i <= kBins; i += kThreads) mine[i] = bins[i];
+  // Integer adds commute: the summed bins are the same whatever order the groups arrive in.
+  unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
+  for (int i = threadIdx.x; i <= kBins; i += kThreads)
+    if (bins[i]) atomicAdd(&summed[i], bins[i]);
 }
 
 __global__ __launch_bounds__(kThreads) void pass_kept(const float* logits, SampleParams hp, const SampleParams* dp,
@@ -301,20 +395,32 @@ __global__ __launch_bounds__(kThreads) void pass_kept(const float* logits, Sampl
   __shared__ unsigned long long bins[kBins + 1];
   __shared__ unsigned long long kscratch[4];
   __shared__ uint32_t cscratch[4];
+  const uint32_t base = blockIdx.x * kSlice;
+  const uint32_t end = min(base + kSlice, p.vocab);
+  float lv[kPerThread];  // issued first: independent of everything read below
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const uint32_t i = base + r * kThreads + threadIdx.x;
+    lv[r] = i < end ? logits[i] : 0.f;
+  }
   float mx;
   uint32_t amax;
   global_max(w, gridDim.x, mx, amax);
   const float total = global_total(w, gridDim.x);
   float lo = 0.0f, hi = 1.0f;
-  if (p.top_p < 1.0f)
-    for (int l = 0; l < kLevels; l++) replay_level(w, gridDim.x, l, p.top_p, lo, hi, mids, bins);
+  if (p.top_p < 1.0f) {
+    lo = w.state->lo[kLevels - 1];
+    hi = w.state->hi[kLevels - 1];
+    replay_level(w, gridDim.x, kLevels - 1, p.top_p, lo, hi, mids, bins);
+  }
   const float thr = p.top_p < 1.0f ? lo : 0.0f;
-  const uint32_t base = blockIdx.x * kSlice;
-  const uint32_t end = min(base + kSlice, p.vocab);
   unsigned long long kept = 0;
   uint32_t count = 0;
-  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
-    const float pr = prob(logits[i], p, mx, total);
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    const uint32_t i = base + r * kThreads + threadIdx.x;
+    if (i >= end) continue;
+    const float pr = prob(lv[r], p, mx, total);
     if (pr >= thr) {
       kept += to_fix(pr);
       count++;
@@ -325,7 +431,14 @@ __global__ __launch_bounds__(kThreads) void pass_kept(const float* logits, Sampl
   if (threadIdx.x == 0) {
     w.kept_part[blockIdx.x] = kept;
     w.count_part[blockIdx.x] = count;
-    if (blockIdx.x == 0) *w.state = SampleState{mx, amax, total, thr};
+    if (blockIdx.x == 0) {
+      w.state->max_scaled = mx;
+      w.state->argmax = amax;
+      w.state->total = total;
+      w.state->threshold = thr;
+      w.state->lo[kLevels] = lo;
+      w.state->hi[kLevels] = hi;
+    }
   }
 }
 
@@ -342,61 +455,49 @@ __global__ __launch_bounds__(kThreads) void finalize(const float* logits, uint32
   }
   __shared__ uint32_t group, pick;
   __shared__ unsigned long long group_prefix;
-  __shared__ double target_fx;
-  __shared__ unsigned long long tsum[kThreads];
   const SampleState st = *w.state;
+  // Kept mass per group in id order: the target, then the first group whose inclusive prefix
+  // reaches it (and that keeps something, so a zero target still lands on a kept id).
+  unsigned long long all = 0;
+  const unsigned long long gk = threadIdx.x < groups ? w.kept_part[threadIdx.x] : 0ull;
+  const uint32_t gc = threadIdx.x < groups ? w.count_part[threadIdx.x] : 0u;
+  const unsigned long long gbefore = block_exclusive_scan(gk, &all);
+  double kd = (double)all / kFix;
+  if (kd < 1.0e-20) kd = 1.0e-20;
+  const double target_fx = (double)p.random * kd * kFix;
   if (threadIdx.x == 0) {
-    uint64_t all = 0;
-    for (uint32_t b = 0; b < groups; b++) all += w.kept_part[b];
-    double kd = (double)all / kFix;
-    if (kd < 1.0e-20) kd = 1.0e-20;
-    target_fx = (double)p.random * kd * kFix;
-    uint64_t run = 0;
     group = 0xFFFFFFFFu;
-    for (uint32_t b = 0; b < groups; b++) {
-      const uint64_t next = run + w.kept_part[b];
-      if (w.count_part[b] > 0 && (double)next >= target_fx) {
-        group = b;
-        break;
-      }
-      run = next;
-    }
-    group_prefix = run;
     pick = 0xFFFFFFFFu;
   }
   __syncthreads();
+  if (threadIdx.x < groups && gc > 0 && (double)(gbefore + gk) >= target_fx) atomicMin(&group, threadIdx.x);
+  __syncthreads();
+  if (threadIdx.x == group) group_prefix = gbefore;
+  __syncthreads();
   if (group != 0xFFFFFFFFu) {
-    // Thread t owns ids [t*16, t*16+16) of the slice, so thread order is id order; an
-    // exclusive scan of the per-thread kept masses gives each thread its starting prefix.
+    // Thread t owns ids [t*16, t*16+16) of the group's slice, so thread order is id order.
     const uint32_t gbase = group * kSlice;
+    float pv[kPerThread];
     unsigned long long mine = 0;
+#pragma unroll
     for (int r = 0; r < kPerThread; r++) {
       const uint32_t i = gbase + threadIdx.x * kPerThread + r;
+      pv[r] = -1.0f;
       if (i < p.vocab) {
         const float pr = prob(logits[i], p, st.max_scaled, st.total);
-        if (pr >= st.threshold) mine += to_fix(pr);
+        if (pr >= st.threshold) {
+          pv[r] = pr;
+          mine += to_fix(pr);
+        }
       }
     }
-    tsum[threadIdx.x] = mine;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned long long run = group_prefix;
-      for (int t = 0; t < kThreads; t++) {
-        const unsigned long long v = tsum[t];
-        tsum[t] = run;
-        run += v;
-      }
-    }
-    __syncthreads();
-    unsigned long long run = tsum[threadIdx.x];
+    unsigned long long run = group_prefix + block_exclusive_scan(mine, nullptr);
+#pragma unroll
     for (int r = 0; r < kPerThread; r++) {
-      const uint32_t i = gbase + threadIdx.x * kPerThread + r;
-      if (i >= p.vocab) break;
-      const float pr = prob(logits[i], p, st.max_scaled, st.total);
-      if (pr >= st.threshold) {
-        run += to_fix(pr);
+      if (pv[r] >= 0.0f) {
+        run += to_fix(pv[r]);
         if ((double)run >= target_fx) {
-          atomicMin(&pick, i);
+          atomicMin(&pick, gbase + threadIdx.x * kPerThread + r);
           break;
         }
       }
@@ -419,9 +520,9 @@ Work workspace(eg_context* ctx) {
   off += (size_t)kMaxGroups * 8;
   w.count_part = reinterpret_cast<uint32_t*>(part + off);
   off += (size_t)kMaxGroups * 4;
-  w.bin_part = reinterpret_cast<uint64_t*>(part + off);
-  off += (size_t)kLevels * kMaxGroups * (kBins + 1) * 8;
-  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * kMaxGroups * (kBins + 1) * 8 <= eg::kPartialsBytes,
+  w.bins = reinterpret_cast<unsigned long long*>(part + off);
+  off += (size_t)kLevels * (kBins + 1) * 8;
+  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * (kBins + 1) * 8 <= eg::kPartialsBytes,
                 "sampler partials exceed the workspace");
   return w;
 }
