@@ -189,16 +189,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   };
 
   auto issue = [&](const TileRef& r, Loads<BITS, U, CPL>& L) {
+    const auto w = egd::as_global(reinterpret_cast<const egd::u32x4*>(r.w));
+    const auto scales = egd::as_global(r.scales);
+    const auto zeros = egd::as_global(r.zeros);
+    // The bias load is unconditional too (from the scale stream, which has at least one entry
+    // per row, when there is no bias): a load under even a uniform branch leaves the wait
+    // counter unknown at the merge and costs a full wait.
+    const bool has_bias = r.bias != nullptr;
+    const auto bias = egd::as_global(has_bias ? r.bias : r.scales);
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const uint32_t row = min(r.row0 + u * RPW + slot, r.rows - 1);
-      L.b[u] = r.bias ? r.bias[row] : 0.f;
+      const float b = bias[row];
+      L.b[u] = has_bias ? b : 0.f;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        L.q[u][j] = r.w[(size_t)row * a.chunks + cj[j]];
+        const egd::u32x4 q = w[(size_t)row * a.chunks + cj[j]];
+        L.q[u][j] = make_uint4(q.x, q.y, q.z, q.w);
         const uint32_t blk = row * a.blocks_per_row + bj[j];
-        L.s[u][j] = r.scales[blk];
-        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = r.zeros[blk / C::kZeroPerWord];
+        L.s[u][j] = scales[blk];
+        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = zeros[blk / C::kZeroPerWord];
       }
     }
   };
@@ -209,7 +219,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   auto compute = [&](const TileRef& r, const Loads<BITS, U, CPL>& L) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      float acc = 0.f;
+      // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too); being used
+      // by every lane keeps its load from being sunk into the store branch.
+      float acc = t == 0 ? L.b[u] : 0.f;
       const uint32_t row = r.row0 + u * RPW + slot;
       const uint32_t crow = min(row, r.rows - 1);
 #pragma unroll
@@ -230,7 +242,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
       acc = egd::team_sum<TEAM>(acc);
       if (t == TEAM - 1 && row < r.rows) {
-        const float v = acc + L.b[u];
+        const float v = acc;
         if (r.out) r.out[row + r.out_offset] = v;
         if (MODE == kArgmax && egd::better(v, row + r.out_offset, best_v, best_i)) {
           best_v = v;

@@ -63,6 +63,19 @@ int check_launch(eg_context* ctx, const char* op);
 
 namespace egd {
 
+// A pointer known to be global memory. Pointers read from device memory (tables) are generic
+// to the compiler, which then emits flat loads; flat loads count against both vmcnt and
+// lgkmcnt and force coarse waits. Casting to address space 1 restores global loads.
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+// 16 bytes as a native vector (HIP's uint4 is a class, which cannot be copied out of an
+// address-space-qualified lvalue).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global(const T* p) {
+  return (gptr<T>)p;
+}
+
 // Opaque AND: keeps the compiler from folding a nibble mask into per-element bitfield
 // extracts, so the byte converts (v_cvt_f32_ubyte0..3) consume the masked word directly.
 __device__ __forceinline__ uint32_t and_opaque(uint32_t v, uint32_t m) {
