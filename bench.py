@@ -101,6 +101,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant kernel and two calibration kernels of known size "
+                         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the path is "
@@ -110,6 +113,8 @@ def main() -> int:
     from enargeia_amd import kernels as K
     from enargeia_amd import quant
 
+    if args.traffic_probe:
+        return traffic_probe()
     t0 = time.time()
     mats = make_projection_set()
     log(f"quantized {len(mats)} projection matrices in {time.time() - t0:.1f}s")
@@ -170,10 +175,23 @@ def main() -> int:
         ev.record(ends[i], stream)
     ev.sync(ends[-1])
     total_ms = ev.ms(starts[0], ends[-1])
-    t896 = [ev.ms(starts[i], mids[i]) for i in range(args.steps)]
     step_ms = total_ms / args.steps
     value = STEP_BYTES / (step_ms * 1e-3) / 1e9
     log(f"batched: {step_ms * 1e3:.1f} us/step, {value:.0f} GB/s cold")
+
+    # the dominant kernel alone: back-to-back launches over the cold replicas, one event pair
+    # around the burst, so the per-launch average is the kernel's own duration
+    burst = 3 * args.steps
+    for i in range(R):
+        replicas[i]["plans"][0].launch(x896)
+    bs_, be_ = ev.create(), ev.create()
+    ev.record(bs_, stream)
+    for i in range(burst):
+        replicas[i % R]["plans"][0].launch(x896)
+    ev.record(be_, stream)
+    ev.sync(be_)
+    dominant_ms = ev.ms(bs_, be_) / burst
+    log(f"K=896 batched launch alone: {dominant_ms * 1e3:.1f} us ({BATCH896_BYTES / dominant_ms / 1e6:.0f} GB/s)")
 
     # warm: the same replica every step
     for _ in range(3):
@@ -285,11 +303,11 @@ def main() -> int:
         b.release()
 
     # ---- roofline: the dominant kernel = the K=896 batched launch ----
-    t896_ms = float(np.mean(t896))
+    t896_ms = dominant_ms
     achieved = BATCH896_BYTES / (t896_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "kernel": "gemv_kernel<4,SIGNED,...,BATCHED> (K=896 projections, 24 layers)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "bytes_per_launch": BATCH896_BYTES, "avg_launch_us": round(t896_ms * 1e3, 2)}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(mats)
@@ -318,6 +336,64 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+CALIBRATION_BYTES = 256 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_batched_k896_config1_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its calibration kernel)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().replace(",", ""))
+    except OSError:
+        pass
+    return None
+
+
+def traffic_probe() -> int:
+    """Dispatches, in order: argmax over CALIBRATION_BYTES of floats (reads exactly that),
+    a zero fill of CALIBRATION_BYTES (writes exactly that), then the K=896 batched projection
+    launch three times over three cold replicas. Per-dispatch FETCH_SIZE / WRITE_SIZE of the
+    calibration kernels give the counters' scale; see profiles/."""
+    from enargeia_amd import kernels as K
+    from enargeia_amd import quant
+
+    dev = K.Device(0)
+    big = dev.buffer(CALIBRATION_BYTES)
+    dev.zero(big, CALIBRATION_BYTES)
+    dev.sync()
+    out8 = dev.buffer(16)
+    am = K.ComputeKernel(dev, K.ARGMAX)
+    u = am.uniform()
+    u.write(K.argmax_dims(CALIBRATION_BYTES // 4, 0))
+    am.encode(am.bind_group([big, out8, u]), (1, 1, 1))
+    dev.sync()
+    dev.zero(big, CALIBRATION_BYTES)
+    dev.sync()
+    rows = [r for _, r, k in PROJECTIONS if k == HIDDEN]
+    mats = [quant.quantize_sym(quant.normal(r * HIDDEN, 300 + i, 0.02), r, HIDDEN, 4, GROUP) for i, r in enumerate(rows)]
+    out = dev.buffer(LAYERS * sum(rows) * 4)
+    x = dev.upload(np.random.default_rng(7).standard_normal(HIDDEN, dtype=np.float32))
+    plans = []
+    for _ in range(3):
+        segs, off = [], 0
+        for _layer in range(LAYERS):
+            for q in mats:
+                segs.append((dev.upload(q.packed), dev.upload(q.scales), None, None, out, q.rows, off))
+                off += q.rows
+        plans.append(K.GemvPlan(dev, HIDDEN, GROUP, segs))
+    for p in plans:
+        p.launch(x)
+    dev.sync()
+    print(json.dumps({"traffic_probe": True, "calibration_bytes": CALIBRATION_BYTES,
+                      "batch896_bytes": BATCH896_BYTES}), flush=True)
+    dev.close()
     return 0
 
 
