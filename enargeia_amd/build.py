@@ -2,8 +2,10 @@
 
 Every ``csrc/*.hip`` translation unit is compiled with hipcc for ``--offload-arch=gfx950``
 (packed-FP32 instructions disabled) and linked into one shared library whose exported symbols
-are exactly the ``extern "C"`` entry points of ``include/enargeia_hip.h``. Run directly
-(``python -m enargeia_amd.build``) or through ``__graft_entry__.build()``.
+are exactly the ``extern "C"`` entry points of ``include/enargeia_hip.h``. The Node N-API addon
+(``js/eg_napi.node``) is then compiled with g++ against the node headers and linked to that
+library through an ``$ORIGIN`` rpath. Run directly (``python -m enargeia_amd.build``) or
+through ``__graft_entry__.build()``.
 """
 
 from __future__ import annotations
@@ -18,6 +20,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_PATH = os.path.join(HERE, "libenargeia_hip.so")
+NAPI_SRC = os.path.join(HERE, "js", "eg_napi.cc")
+NAPI_PATH = os.path.join(HERE, "js", "eg_napi.node")
+NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -60,7 +65,28 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+    build_napi(verbose)
     return LIB_PATH
+
+
+def build_napi(verbose: bool = True) -> str | None:
+    """The N-API addon. Needs only node_api.h (Node 12 ships N-API 8); skipped with a notice
+    where the node headers are absent, since the addon is a host binding, not compute."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        print(f"node headers not found under {NODE_INCLUDE}: N-API addon not built", file=sys.stderr)
+        return None
+    tmp = NAPI_PATH + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-fvisibility=hidden",
+           "-DNAPI_VERSION=8", "-DNODE_GYP_MODULE_NAME=eg_napi",
+           "-I", NODE_INCLUDE, "-I", os.path.join(ROOT, "include"), NAPI_SRC,
+           "-L", HERE, "-lenargeia_hip", "-Wl,-rpath,$ORIGIN/..", "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"N-API addon build failed:\n{res.stderr}")
+    os.replace(tmp, NAPI_PATH)
+    if verbose:
+        print(f"built {NAPI_PATH}", file=sys.stderr)
+    return NAPI_PATH
 
 
 if __name__ == "__main__":

@@ -1,0 +1,446 @@
+// Node N-API addon over the C ABI in include/enargeia_hip.h.
+//
+// This is the thin native layer the reference's TypeScript would bind instead of WebGPU: one
+// JS function per C entry point, device pointers as JS numbers (safe integers), uniforms as the
+// same ArrayBuffer bytes the reference writes with queue.writeBuffer (matmul_q4.ts:50-64,
+// embedding_variants.ts:207-221, argmax.ts:16-18, sample.ts:35-50). A non-zero status becomes
+// a thrown RangeError (EG_ERR_RANGE, as kernel.ts:97-107 throws) or Error (everything else)
+// carrying eg_last_error's message and the status name as `code`. Nothing here allocates on
+// the device except eg_buf_alloc; nothing here launches a kernel except the op calls.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "enargeia_hip.h"
+
+namespace {
+
+const char* status_name(int st) {
+  switch (st) {
+    case EG_ERR_INVALID: return "EG_ERR_INVALID";
+    case EG_ERR_RANGE: return "EG_ERR_RANGE";
+    case EG_ERR_DEVICE: return "EG_ERR_DEVICE";
+    case EG_ERR_NOMEM: return "EG_ERR_NOMEM";
+    case EG_ERR_STATE: return "EG_ERR_STATE";
+    default: return "EG_ERR_UNKNOWN";
+  }
+}
+
+// Throws for a failed status; returns true when the caller should return early.
+bool throw_status(napi_env env, eg_context* ctx, int st) {
+  if (st == EG_OK) return false;
+  const char* msg = eg_last_error(ctx);
+  if (st == EG_ERR_RANGE)
+    napi_throw_range_error(env, status_name(st), msg);
+  else
+    napi_throw_error(env, status_name(st), msg);
+  return true;
+}
+
+void throw_type(napi_env env, const std::string& what) { napi_throw_type_error(env, "EG_ERR_INVALID", what.c_str()); }
+
+struct Args {
+  napi_env env;
+  size_t argc = 12;
+  napi_value argv[12];
+  bool ok = true;
+  const char* fn;
+
+  Args(napi_env e, napi_callback_info info, const char* name, size_t need) : env(e), fn(name) {
+    napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr);
+    if (argc < need) {
+      throw_type(env, std::string(fn) + ": expected " + std::to_string(need) + " arguments, got " +
+                          std::to_string(argc));
+      ok = false;
+    }
+  }
+
+  // A context or graph handle: an External created by this addon.
+  template <typename T>
+  T* handle(size_t i, const char* what) {
+    if (!ok) return nullptr;
+    napi_valuetype t;
+    napi_typeof(env, argv[i], &t);
+    void* p = nullptr;
+    if (t != napi_external || napi_get_value_external(env, argv[i], &p) != napi_ok) {
+      throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not a " + what);
+      ok = false;
+      return nullptr;
+    }
+    return static_cast<T*>(p);
+  }
+
+  // A device pointer: a non-negative safe integer, or null/undefined for NULL.
+  void* ptr(size_t i) {
+    if (!ok) return nullptr;
+    napi_valuetype t;
+    napi_typeof(env, argv[i], &t);
+    if (t == napi_null || t == napi_undefined) return nullptr;
+    double d = 0;
+    if (t != napi_number || napi_get_value_double(env, argv[i], &d) != napi_ok || d < 0 ||
+        d > 9007199254740991.0 || d != (double)(int64_t)d) {
+      throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not a device pointer");
+      ok = false;
+      return nullptr;
+    }
+    return reinterpret_cast<void*>(static_cast<uintptr_t>(d));
+  }
+
+  uint64_t u64(size_t i) {
+    if (!ok) return 0;
+    double d = 0;
+    napi_valuetype t;
+    napi_typeof(env, argv[i], &t);
+    if (t != napi_number || napi_get_value_double(env, argv[i], &d) != napi_ok || d < 0 ||
+        d > 9007199254740991.0 || d != (double)(int64_t)d) {
+      throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not a non-negative integer");
+      ok = false;
+      return 0;
+    }
+    return static_cast<uint64_t>(d);
+  }
+
+  int32_t i32(size_t i) {
+    if (!ok) return 0;
+    int32_t v = 0;
+    if (napi_get_value_int32(env, argv[i], &v) != napi_ok) {
+      throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not a number");
+      ok = false;
+    }
+    return v;
+  }
+
+  // Bytes of an ArrayBuffer, TypedArray or DataView.
+  bool bytes(size_t i, void** data, size_t* len) {
+    if (!ok) return false;
+    bool is = false;
+    napi_is_typedarray(env, argv[i], &is);
+    if (is) {
+      napi_typedarray_type type;
+      size_t length, offset;
+      napi_value ab;
+      void* base;
+      napi_get_typedarray_info(env, argv[i], &type, &length, &base, &ab, &offset);
+      size_t elem = 1;
+      switch (type) {
+        case napi_int16_array: case napi_uint16_array: elem = 2; break;
+        case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+        case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+        default: elem = 1;
+      }
+      *data = base;  // napi_get_typedarray_info already applies the byte offset
+      *len = length * elem;
+      return true;
+    }
+    napi_is_dataview(env, argv[i], &is);
+    if (is) {
+      napi_value ab;
+      size_t offset;
+      napi_get_dataview_info(env, argv[i], len, data, &ab, &offset);
+      return true;
+    }
+    napi_is_arraybuffer(env, argv[i], &is);
+    if (is) {
+      napi_get_arraybuffer_info(env, argv[i], data, len);
+      return true;
+    }
+    throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not an ArrayBuffer or view");
+    ok = false;
+    return false;
+  }
+
+  // A uniform: at least sizeof(T) bytes, copied into a T.
+  template <typename T>
+  bool uniform(size_t i, T* out) {
+    void* data;
+    size_t len;
+    if (!bytes(i, &data, &len)) return false;
+    if (len < sizeof(T)) {
+      throw_type(env, std::string(fn) + ": uniform of " + std::to_string(len) + " bytes, expected " +
+                          std::to_string(sizeof(T)));
+      ok = false;
+      return false;
+    }
+    std::memcpy(out, data, sizeof(T));
+    return true;
+  }
+};
+
+napi_value undefined(napi_env env) {
+  napi_value v;
+  napi_get_undefined(env, &v);
+  return v;
+}
+
+napi_value number(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+// ---- context ---------------------------------------------------------------------------------
+
+void finalize_ctx(napi_env, void*, void*) {
+  // Contexts are destroyed explicitly (destroy()); the External only carries the address, so a
+  // collected handle leaks nothing the process end does not reclaim.
+}
+
+napi_value AbiVersion(napi_env env, napi_callback_info) { return number(env, eg_abi_version()); }
+
+napi_value Create(napi_env env, napi_callback_info info) {
+  Args a(env, info, "create", 1);
+  int device = a.i32(0);
+  if (!a.ok) return nullptr;
+  eg_context* ctx = nullptr;
+  if (throw_status(env, nullptr, eg_create(device, &ctx))) return nullptr;
+  napi_value ext;
+  napi_create_external(env, ctx, finalize_ctx, nullptr, &ext);
+  return ext;
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  Args a(env, info, "destroy", 1);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  eg_destroy(ctx);
+  return undefined(env);
+}
+
+napi_value Sync(napi_env env, napi_callback_info info) {
+  Args a(env, info, "sync", 1);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_sync(ctx))) return nullptr;
+  return undefined(env);
+}
+
+napi_value GetStream(napi_env env, napi_callback_info info) {
+  Args a(env, info, "getStream", 1);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  void* s = nullptr;
+  if (throw_status(env, ctx, eg_get_stream(ctx, &s))) return nullptr;
+  return number(env, (double)reinterpret_cast<uintptr_t>(s));
+}
+
+// ---- buffers ---------------------------------------------------------------------------------
+
+napi_value BufAlloc(napi_env env, napi_callback_info info) {
+  Args a(env, info, "bufAlloc", 2);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  uint64_t bytes = a.u64(1);
+  if (!a.ok) return nullptr;
+  void* p = nullptr;
+  if (throw_status(env, ctx, eg_buf_alloc(ctx, bytes, &p))) return nullptr;
+  return number(env, (double)reinterpret_cast<uintptr_t>(p));
+}
+
+napi_value BufFree(napi_env env, napi_callback_info info) {
+  Args a(env, info, "bufFree", 2);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  void* p = a.ptr(1);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_buf_free(ctx, p))) return nullptr;
+  return undefined(env);
+}
+
+// bufWrite(ctx, ptr, offset, data): completes before returning (the JS source may be collected
+// or reused as soon as the call returns, so the copy is synchronised here).
+napi_value BufWrite(napi_env env, napi_callback_info info) {
+  Args a(env, info, "bufWrite", 4);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  void* p = a.ptr(1);
+  uint64_t offset = a.u64(2);
+  void* data = nullptr;
+  size_t len = 0;
+  a.bytes(3, &data, &len);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_buf_write(ctx, p, offset, data, len))) return nullptr;
+  if (throw_status(env, ctx, eg_sync(ctx))) return nullptr;
+  return undefined(env);
+}
+
+// bufRead(ctx, ptr, offset, bytes) -> ArrayBuffer, after all prior work on the stream.
+napi_value BufRead(napi_env env, napi_callback_info info) {
+  Args a(env, info, "bufRead", 4);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  void* p = a.ptr(1);
+  uint64_t offset = a.u64(2);
+  uint64_t bytes = a.u64(3);
+  if (!a.ok) return nullptr;
+  void* host = nullptr;
+  napi_value ab;
+  if (napi_create_arraybuffer(env, bytes, &host, &ab) != napi_ok) {
+    napi_throw_error(env, "EG_ERR_NOMEM", "bufRead: cannot allocate the host buffer");
+    return nullptr;
+  }
+  if (throw_status(env, ctx, eg_buf_read(ctx, p, offset, host, bytes))) return nullptr;
+  return ab;
+}
+
+napi_value BufZero(napi_env env, napi_callback_info info) {
+  Args a(env, info, "bufZero", 4);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  void* p = a.ptr(1);
+  uint64_t offset = a.u64(2);
+  uint64_t bytes = a.u64(3);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_buf_zero(ctx, p, offset, bytes))) return nullptr;
+  return undefined(env);
+}
+
+// ---- ops -------------------------------------------------------------------------------------
+
+// matmulQ4Decode / matmulQ4Prefill(ctx, x, packed, scales, zeros, bias, out, dims, encoding, bits)
+template <int (*FN)(eg_context*, const float*, const uint32_t*, const float*, const uint32_t*, const float*,
+                    float*, const eg_matmul_q4_dims*, int, int)>
+napi_value Matmul(napi_env env, napi_callback_info info) {
+  Args a(env, info, "matmulQ4", 10);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* x = static_cast<const float*>(a.ptr(1));
+  auto* packed = static_cast<const uint32_t*>(a.ptr(2));
+  auto* scales = static_cast<const float*>(a.ptr(3));
+  auto* zeros = static_cast<const uint32_t*>(a.ptr(4));
+  auto* bias = static_cast<const float*>(a.ptr(5));
+  auto* out = static_cast<float*>(a.ptr(6));
+  eg_matmul_q4_dims dims;
+  a.uniform(7, &dims);
+  int encoding = a.i32(8), bits = a.i32(9);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, FN(ctx, x, packed, scales, zeros, bias, out, &dims, encoding, bits))) return nullptr;
+  return undefined(env);
+}
+
+// lmHead(ctx, x, packed, scales, zeros, out, dims, encoding, bits)
+napi_value LmHead(napi_env env, napi_callback_info info) {
+  Args a(env, info, "lmHead", 9);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* x = static_cast<const float*>(a.ptr(1));
+  auto* packed = static_cast<const uint32_t*>(a.ptr(2));
+  auto* scales = static_cast<const float*>(a.ptr(3));
+  auto* zeros = static_cast<const uint32_t*>(a.ptr(4));
+  auto* out = static_cast<float*>(a.ptr(5));
+  eg_embedding_dims dims;
+  a.uniform(6, &dims);
+  int encoding = a.i32(7), bits = a.i32(8);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_lm_head(ctx, x, packed, scales, zeros, out, &dims, encoding, bits))) return nullptr;
+  return undefined(env);
+}
+
+// lmHeadArgmax(ctx, x, packed, scales, zeros, out|null, result, dims, encoding, bits)
+napi_value LmHeadArgmax(napi_env env, napi_callback_info info) {
+  Args a(env, info, "lmHeadArgmax", 10);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* x = static_cast<const float*>(a.ptr(1));
+  auto* packed = static_cast<const uint32_t*>(a.ptr(2));
+  auto* scales = static_cast<const float*>(a.ptr(3));
+  auto* zeros = static_cast<const uint32_t*>(a.ptr(4));
+  auto* out = static_cast<float*>(a.ptr(5));
+  auto* result = static_cast<uint32_t*>(a.ptr(6));
+  eg_embedding_dims dims;
+  a.uniform(7, &dims);
+  int encoding = a.i32(8), bits = a.i32(9);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_lm_head_argmax(ctx, x, packed, scales, zeros, out, result, &dims, encoding, bits)))
+    return nullptr;
+  return undefined(env);
+}
+
+// argmax(ctx, logits, out, dims)
+napi_value Argmax(napi_env env, napi_callback_info info) {
+  Args a(env, info, "argmax", 4);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* logits = static_cast<const float*>(a.ptr(1));
+  auto* out = static_cast<uint32_t*>(a.ptr(2));
+  eg_argmax_dims dims;
+  a.uniform(3, &dims);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_argmax(ctx, logits, out, &dims))) return nullptr;
+  return undefined(env);
+}
+
+// sample(ctx, logits, history, out, dims)
+napi_value Sample(napi_env env, napi_callback_info info) {
+  Args a(env, info, "sample", 5);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* logits = static_cast<float*>(a.ptr(1));
+  auto* history = static_cast<const uint32_t*>(a.ptr(2));
+  auto* out = static_cast<uint32_t*>(a.ptr(3));
+  eg_sample_dims dims;
+  a.uniform(4, &dims);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_sample(ctx, logits, history, out, &dims))) return nullptr;
+  return undefined(env);
+}
+
+// ---- graphs ----------------------------------------------------------------------------------
+
+napi_value GraphBegin(napi_env env, napi_callback_info info) {
+  Args a(env, info, "graphBegin", 1);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_graph_begin(ctx))) return nullptr;
+  return undefined(env);
+}
+
+napi_value GraphEnd(napi_env env, napi_callback_info info) {
+  Args a(env, info, "graphEnd", 1);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  eg_graph* g = nullptr;
+  if (throw_status(env, ctx, eg_graph_end(ctx, &g))) return nullptr;
+  napi_value ext;
+  napi_create_external(env, g, nullptr, nullptr, &ext);
+  return ext;
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  Args a(env, info, "graphLaunch", 2);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* g = a.handle<eg_graph>(1, "graph");
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_graph_launch(ctx, g))) return nullptr;
+  return undefined(env);
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  Args a(env, info, "graphDestroy", 1);
+  auto* g = a.handle<eg_graph>(0, "graph");
+  if (!a.ok) return nullptr;
+  eg_graph_destroy(g);
+  return undefined(env);
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const napi_property_descriptor props[] = {
+      {"abiVersion", nullptr, AbiVersion, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"create", nullptr, Create, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"destroy", nullptr, Destroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sync", nullptr, Sync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"getStream", nullptr, GetStream, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"bufAlloc", nullptr, BufAlloc, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"bufFree", nullptr, BufFree, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"bufWrite", nullptr, BufWrite, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"bufRead", nullptr, BufRead, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"bufZero", nullptr, BufZero, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"matmulQ4Decode", nullptr, Matmul<eg_matmul_q4_decode>, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"matmulQ4Prefill", nullptr, Matmul<eg_matmul_q4_prefill>, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHead", nullptr, LmHead, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadArgmax", nullptr, LmHeadArgmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphBegin", nullptr, GraphBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphEnd", nullptr, GraphEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphLaunch", nullptr, GraphLaunch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphDestroy", nullptr, GraphDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+  };
+  napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)
