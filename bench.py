@@ -156,53 +156,54 @@ def main() -> int:
             xin = x896 if q.cols == HIDDEN else x4864
             dec.encode(dec.bind_group([xin, bp, bs, None, zero_bias, out, u]), (1, 1, 1))
 
-    def batched(rep, e_mid=None):
+    def batched(rep):
         rep["plans"][0].launch(x896)
-        if e_mid is not None:
-            ev.record(e_mid, stream)
         rep["plans"][1].launch(x4864)
 
-    # ---- batched step (value) ----
+    def timed(fn, n):
+        """ms per call of fn(i) over n back-to-back calls, one event pair around all of them."""
+        a, b = ev.create(), ev.create()
+        ev.record(a, stream)
+        for i in range(n):
+            fn(i)
+        ev.record(b, stream)
+        ev.sync(b)
+        return ev.ms(a, b) / n
+
+    # ---- batched step (value): eager stream launches, and the same two launches captured in
+    # one hipGraph per replica (how a decode loop replays its step) ----
     for i in range(args.warmup):
         batched(replicas[i % R])
     dev.sync()
-    starts = [ev.create() for _ in range(args.steps)]
-    mids = [ev.create() for _ in range(args.steps)]
-    ends = [ev.create() for _ in range(args.steps)]
-    for i in range(args.steps):
-        ev.record(starts[i], stream)
-        batched(replicas[i % R], mids[i])
-        ev.record(ends[i], stream)
-    ev.sync(ends[-1])
-    total_ms = ev.ms(starts[0], ends[-1])
-    step_ms = total_ms / args.steps
+    eager_ms = timed(lambda i: batched(replicas[i % R]), args.steps)
+    step_graphs = []
+    for rep in replicas:
+        dev.capture_begin()
+        batched(rep)
+        step_graphs.append(dev.capture_end())
+    for i in range(args.warmup):
+        step_graphs[i % R].launch()
+    graph_ms = timed(lambda i: step_graphs[i % R].launch(), args.steps)
+    step_ms = min(eager_ms, graph_ms)
+    step_launch = "hipGraph" if graph_ms <= eager_ms else "stream"
     value = STEP_BYTES / (step_ms * 1e-3) / 1e9
-    log(f"batched: {step_ms * 1e3:.1f} us/step, {value:.0f} GB/s cold")
+    log(f"batched step: {eager_ms * 1e3:.1f} us eager, {graph_ms * 1e3:.1f} us as a graph -> {value:.0f} GB/s cold")
 
     # the dominant kernel alone: back-to-back launches over the cold replicas, one event pair
     # around the burst, so the per-launch average is the kernel's own duration
     burst = 3 * args.steps
     for i in range(R):
         replicas[i]["plans"][0].launch(x896)
-    bs_, be_ = ev.create(), ev.create()
-    ev.record(bs_, stream)
-    for i in range(burst):
-        replicas[i % R]["plans"][0].launch(x896)
-    ev.record(be_, stream)
-    ev.sync(be_)
-    dominant_ms = ev.ms(bs_, be_) / burst
+    dominant_ms = timed(lambda i: replicas[i % R]["plans"][0].launch(x896), burst)
     log(f"K=896 batched launch alone: {dominant_ms * 1e3:.1f} us ({BATCH896_BYTES / dominant_ms / 1e6:.0f} GB/s)")
+    down_ms = timed(lambda i: replicas[i % R]["plans"][1].launch(x4864), burst)
+    down_bytes = STEP_BYTES - BATCH896_BYTES
+    log(f"K=4864 batched launch alone: {down_ms * 1e3:.1f} us ({down_bytes / down_ms / 1e6:.0f} GB/s)")
 
     # warm: the same replica every step
     for _ in range(3):
         batched(replicas[0])
-    ws, we = ev.create(), ev.create()
-    ev.record(ws, stream)
-    for _ in range(args.steps):
-        batched(replicas[0])
-    ev.record(we, stream)
-    ev.sync(we)
-    warm_ms = ev.ms(ws, we) / args.steps
+    warm_ms = timed(lambda i: batched(replicas[0]), args.steps)
     warm_gbs = STEP_BYTES / (warm_ms * 1e-3) / 1e9
     log(f"batched warm: {warm_ms * 1e3:.1f} us/step, {warm_gbs:.0f} GB/s")
 
@@ -245,7 +246,7 @@ def main() -> int:
         per_gemv[f"{shape_name}_{q.rows}x{q.cols}"] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
     log(f"per-GEMV: {per_gemv}")
 
-    for g in graphs:
+    for g in graphs + step_graphs:
         g.destroy()
     for rep in replicas:
         for p in rep["plans"]:
@@ -320,7 +321,9 @@ def main() -> int:
         "config": {"workload": "BASELINE config 1: Qwen2.5-0.5B projection set, 24 layers x 7 int4 GEMVs at M=1",
                    "format": "int4 symmetric, f32 scale per 32 along K", "bytes_per_step": STEP_BYTES,
                    "cache": f"cold: {R} rotating weight replicas ({R * STEP_BYTES / 1e6:.0f} MB)",
-                   "launches_per_step": 2},
+                   "launches_per_step": 2, "launch": step_launch},
+        "step_us": {"eager": round(eager_ms * 1e3, 2), "graph": round(graph_ms * 1e3, 2),
+                    "k896_launch": round(dominant_ms * 1e3, 2), "k4864_launch": round(down_ms * 1e3, 2)},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "warm_gbs": round(warm_gbs, 1),
         "sequential_gbs": round(seq_gbs, 1), "sequential_us_per_step": round(seq_ms * 1e3, 1),

@@ -39,6 +39,20 @@ int hip_fail(eg_context* ctx, hipError_t err, const char* what) {
   return fail(ctx, status, "%s: %s (%s)", what, hipGetErrorString(err), hipGetErrorName(err));
 }
 
+int occupancy_of(eg_context* ctx, const void* kernel, uint32_t smem_bytes) {
+  const uint64_t key = reinterpret_cast<uint64_t>(kernel) ^ ((uint64_t)smem_bytes << 48);
+  std::lock_guard<std::mutex> guard(ctx->occupancy_lock);
+  auto it = ctx->occupancy.find(key);
+  if (it != ctx->occupancy.end()) return it->second;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, smem_bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    blocks = 0;
+  }
+  ctx->occupancy.emplace(key, blocks);
+  return blocks;
+}
+
 int check_launch(eg_context* ctx, const char* op) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(ctx, err, op);

@@ -31,6 +31,7 @@
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup (256 threads)
+constexpr uint32_t kMaxSegments = 256;  // matrices per batched plan (the table lives in LDS)
 
 // One matrix of a batched launch, as the kernel sees it: its pointers and the range of wave
 // passes (RPW rows each) it occupies in the launch's pass space.
@@ -60,7 +61,8 @@ struct GemvArgs {
   uint32_t out_offset;
   uint32_t* partials;      // argmax: (value bits, index) per workgroup
   const DevSegment* segs;  // batched launches only
-  uint32_t total_passes;   // wave passes over all rows (all segments)
+  uint32_t seg_count;
+  uint32_t total_passes;   // tiles over all rows (all segments)
 };
 
 template <int BITS>
@@ -113,21 +115,22 @@ struct Codes<8> {
   }
 };
 
-enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2 };
+// kPlain: one matrix, logits/outputs stored. kArgmax: also a per-workgroup (max, index)
+// partial. kArgmaxOnly: the partial without storing the outputs. kBatched: a segment table of
+// matrices that share x and K.
+enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3 };
 
 // Where one tile of rows lives: a whole single-matrix launch, or one segment of a batched one.
+// The streams are addressed through buffer resources (base in SGPRs, 32-bit byte offsets,
+// bounds-checked: a read past a stream returns 0 instead of faulting).
 struct TileRef {
-  const uint4* w;
-  const float* scales;
-  const uint32_t* zeros;
-  const float* bias;
-  float* out;
-  uint32_t rows, out_offset, row0;
+  __amdgpu_buffer_rsrc_t w, s, z, b, o;
+  uint32_t rows, out_offset, row0, has_bias;
 };
 
 template <int BITS, int U, int CPL>
 struct Loads {
-  uint4 q[U][CPL];
+  egd::u32x4 q[U][CPL];
   float s[U][CPL];
   uint32_t zw[U][CPL];
   float b[U];
@@ -135,25 +138,52 @@ struct Loads {
 
 // One wave computes a tile of RPW * U rows per step: RPW teams of TEAM lanes side by side,
 // each team owning U rows (spaced RPW apart so that, for every (u, j), the wave's load is RPW
-// consecutive rows x TEAM consecutive 16-byte chunks). Every load of a tile (codes, scales,
-// zero-points, bias) is issued before any of its math, so a wave has U * CPL 16-byte loads per
-// lane in flight and the other waves of the CU cover its latency. Loads are unconditional:
-// out-of-range rows read the last row and out-of-range chunk slots read chunk 0, and both are
-// masked (x is zero for a missing chunk; rows are masked at the store), so no load sits under
-// a divergent branch (whose merge would force a wait per load).
+// consecutive rows x TEAM consecutive 16-byte chunks).
+//
+// Each wave owns a contiguous range of tiles (so a batched launch looks its segment up once,
+// not per tile) and walks it two tiles at a time with two load buffers: the loads of tile i+1
+// are in flight while tile i is computed, so every wave keeps two tiles of codes outstanding.
+// The steady-state loop has no memory operation under a branch, which lets the compiler wait
+// for exactly the tile it is about to use:
+//   * loads are unconditional - out-of-range rows read the last row, out-of-range chunk slots
+//     read chunk 0 (x is zero there), and a wave whose range is odd re-reads its last tile
+//     (an L2 hit) instead of branching around the second buffer;
+//   * stores are unconditional - the team total is in every lane of the team, every lane
+//     stores it, and a clamped or repeated row stores the value that row already has.
 template <int BITS, int ENC, int TEAM, int CPL, int U, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
   constexpr int TILE = RPW * U;
+  constexpr bool kStore = MODE != kArgmaxOnly;
+  constexpr bool kBest = MODE == kArgmax || MODE == kArgmaxOnly;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t t = lane % TEAM;
   const uint32_t slot = lane / TEAM;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const uint32_t total_waves = gridDim.x * kWaves;
 
-  // This lane's activations, loaded once: chunk slot j covers x[c*EPC, c*EPC + EPC).
+  // Dynamic LDS: x (chunks * EPC floats), then (batched) the segment table. The workgroup
+  // copies x in once, so the activations cross L2 once per workgroup rather than once per
+  // wave; each lane then keeps the chunks it owns in VGPRs for every row it visits.
+  extern __shared__ __align__(16) uint8_t smem[];
+  const uint32_t x_words = a.chunks * EPC;
+  {
+    const auto src = egd::as_global(reinterpret_cast<const egd::u32x4*>(a.x));
+    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(smem);
+    for (uint32_t i = threadIdx.x; i < x_words / 4; i += blockDim.x) dst[i] = src[i];
+  }
+  DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
+  if (MODE == kBatched) {
+    const uint32_t words = a.seg_count * (uint32_t)(sizeof(DevSegment) / 4);
+    const auto src = egd::as_global(reinterpret_cast<const uint32_t*>(a.segs));
+    uint32_t* dst = reinterpret_cast<uint32_t*>(table);
+    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
+  }
+  __syncthreads();
+
+  // This lane's activations: chunk slot j covers x[c*EPC, c*EPC + EPC).
   float xr[CPL][EPC];
   float sx[CPL];
   uint32_t cj[CPL], bj[CPL];
@@ -164,51 +194,76 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     cj[j] = valid ? c : 0u;
     bj[j] = cj[j] / a.chunks_per_block;
     sx[j] = 0.f;
-    const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)cj[j] * EPC);
+    const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + (size_t)cj[j] * (EPC / 4);
 #pragma unroll
     for (int e = 0; e < EPC / 4; e++) {
-      const float4 v = xs[e];
-      xr[j][4 * e + 0] = valid ? v.x : 0.f;
-      xr[j][4 * e + 1] = valid ? v.y : 0.f;
-      xr[j][4 * e + 2] = valid ? v.z : 0.f;
-      xr[j][4 * e + 3] = valid ? v.w : 0.f;
+      const egd::u32x4 v = xs[e];
+      xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
+      xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
+      xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
+      xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
     }
 #pragma unroll
     for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
   }
 
-  uint32_t seg = 0;
-  auto locate = [&](uint32_t tile) -> TileRef {
-    if (MODE == kBatched) {
-      while (tile >= a.segs[seg].pass_end) seg++;
-      const DevSegment& d = a.segs[seg];
-      return TileRef{d.w, d.scales, d.zeros, d.bias, d.out, d.rows, d.out_offset,
-                     (tile - (d.pass_end - d.rows / TILE)) * TILE};
-    }
-    return TileRef{a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, tile * TILE};
+  // This wave's tiles: [begin, end), contiguous.
+  const uint32_t begin = (uint32_t)(((uint64_t)a.total_passes * wave) / total_waves);
+  const uint32_t end = (uint32_t)(((uint64_t)a.total_passes * (wave + 1)) / total_waves);
+
+  auto make_ref = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
+                      uint32_t rows, uint32_t out_offset) {
+    const uint32_t blocks = rows * a.blocks_per_row;
+    TileRef r;
+    r.w = egd::buffer(w, rows * a.chunks * 16u);
+    r.s = egd::buffer(scales, blocks * 4u);
+    r.z = egd::buffer(zeros, ((blocks + C::kZeroPerWord - 1) / C::kZeroPerWord) * 4u);
+    r.has_bias = bias != nullptr;
+    // Without a bias the (discarded) bias load reads the scale stream, which has >= 1 entry per row.
+    r.b = r.has_bias ? egd::buffer(bias, rows * 4u) : r.s;
+    r.o = egd::buffer(out, (out_offset + rows) * 4u);
+    r.rows = rows;
+    r.out_offset = out_offset;
+    r.row0 = 0;
+    return r;
   };
 
+  // Batched: the segment holding the current tile is read from the LDS table into scalar
+  // registers (an LDS read waits on lgkmcnt, so switching segments never waits for the tile
+  // loads in flight, as a global load of the table would).
+  TileRef cur = MODE == kBatched ? TileRef{} : make_ref(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset);
+  uint32_t seg = 0, cur_first = 0, cur_end = a.total_passes;
+  auto load_segment = [&](uint32_t s) {
+    const DevSegment& d = table[s];
+    cur = make_ref(egd::uniform(d.w), egd::uniform(d.scales), egd::uniform(d.zeros), egd::uniform(d.bias),
+                   egd::uniform(d.out), __builtin_amdgcn_readfirstlane(d.rows),
+                   __builtin_amdgcn_readfirstlane(d.out_offset));
+    cur_end = __builtin_amdgcn_readfirstlane(d.pass_end);
+    cur_first = cur_end - cur.rows / TILE;
+  };
+  if (MODE == kBatched && begin < end) {
+    uint32_t lo = 0, hi = a.seg_count - 1;  // first segment whose pass_end exceeds begin
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (__builtin_amdgcn_readfirstlane(table[mid].pass_end) > begin)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    seg = lo;
+    load_segment(seg);
+  }
   auto issue = [&](const TileRef& r, Loads<BITS, U, CPL>& L) {
-    const auto w = egd::as_global(reinterpret_cast<const egd::u32x4*>(r.w));
-    const auto scales = egd::as_global(r.scales);
-    const auto zeros = egd::as_global(r.zeros);
-    // The bias load is unconditional too (from the scale stream, which has at least one entry
-    // per row, when there is no bias): a load under even a uniform branch leaves the wait
-    // counter unknown at the merge and costs a full wait.
-    const bool has_bias = r.bias != nullptr;
-    const auto bias = egd::as_global(has_bias ? r.bias : r.scales);
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const uint32_t row = min(r.row0 + u * RPW + slot, r.rows - 1);
-      const float b = bias[row];
-      L.b[u] = has_bias ? b : 0.f;
+      L.b[u] = egd::load_f32(r.b, row * 4u);
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        const egd::u32x4 q = w[(size_t)row * a.chunks + cj[j]];
-        L.q[u][j] = make_uint4(q.x, q.y, q.z, q.w);
+        L.q[u][j] = egd::load_b128_nt(r.w, (row * a.chunks + cj[j]) * 16u);
         const uint32_t blk = row * a.blocks_per_row + bj[j];
-        L.s[u][j] = scales[blk];
-        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = zeros[blk / C::kZeroPerWord];
+        L.s[u][j] = egd::load_f32_nt(r.s, blk * 4u);
+        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = egd::load_b32(r.z, (blk / C::kZeroPerWord) * 4u);
       }
     }
   };
@@ -219,14 +274,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   auto compute = [&](const TileRef& r, const Loads<BITS, U, CPL>& L) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too); being used
-      // by every lane keeps its load from being sunk into the store branch.
-      float acc = t == 0 ? L.b[u] : 0.f;
-      const uint32_t row = r.row0 + u * RPW + slot;
-      const uint32_t crow = min(row, r.rows - 1);
+      // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too).
+      float acc = (t == 0 && r.has_bias) ? L.b[u] : 0.f;
+      const uint32_t crow = min(r.row0 + u * RPW + slot, r.rows - 1);
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        uint4 q = L.q[u][j];
+        uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
         float z;
         if (ENC == EG_ENC_OFFSET_ZEROS) {
           const uint32_t blk = crow * a.blocks_per_row + bj[j];
@@ -240,26 +293,61 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
         acc = fmaf(L.s[u][j], C::dot(q, xr[j]) - z * sx[j], acc);
       }
-      acc = egd::team_sum<TEAM>(acc);
-      if (t == TEAM - 1 && row < r.rows) {
-        const float v = acc;
-        if (r.out) r.out[row + r.out_offset] = v;
-        if (MODE == kArgmax && egd::better(v, row + r.out_offset, best_v, best_i)) {
-          best_v = v;
-          best_i = row + r.out_offset;
-        }
+      const float v = egd::team_allsum<TEAM>(acc);
+      const uint32_t idx = crow + r.out_offset;
+      if (kStore) egd::store_f32(r.o, idx * 4u, v);
+      if (kBest) {
+        const bool take = egd::better(v, idx, best_v, best_i);
+        best_v = take ? v : best_v;
+        best_i = take ? idx : best_i;
       }
     }
   };
 
-  for (uint32_t tile = wave; tile < a.total_passes; tile += total_waves) {
-    const TileRef r = locate(tile);
-    Loads<BITS, U, CPL> L;
-    issue(r, L);
-    compute(r, L);
+  // The wave's range is walked segment by segment (one segment in a plain launch). Inside a
+  // segment the loop is software-pipelined over two load buffers, two tiles per iteration,
+  // with a single exit at the bottom: an odd count computes its last tile twice (same loads,
+  // same stores) rather than breaking out mid-body. With no path leaving the loop between an
+  // issue and its consumer, the compiler's wait counts stay exact - computing a tile waits
+  // only for that tile's loads, never for the next tile's. sched_barrier(0) after each issue
+  // keeps the scheduler from sinking the next tile's loads into the current tile's math.
+  if (begin < end) {
+    Loads<BITS, U, CPL> LA, LB;
+    uint32_t tile = begin;
+    for (;;) {
+      if (MODE == kBatched)
+        while (tile >= cur_end) load_segment(++seg);
+      const uint32_t last = min(end, cur_end) - 1;  // this wave's last tile in the segment
+      const TileRef base = cur;
+      const uint32_t first = cur_first;
+      auto at = [&](uint32_t tl) {
+        TileRef r = base;
+        r.row0 = (tl - first) * TILE;
+        return r;
+      };
+      const uint32_t pairs = (last - tile) / 2 + 1;
+      issue(at(tile), LA);
+      for (uint32_t p = 0; p < pairs; p++) {
+        const uint32_t tb = min(tile + 1, last);
+        issue(at(tb), LB);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(at(tile), LA);
+        issue(at(min(tile + 2, last)), LA);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(at(tb), LB);
+        tile += 2;
+      }
+      // The last issue is a duplicate that nothing consumes. Wait it out once per segment:
+      // left pending, it would make the compiler assume those registers may still be written
+      // at the loop head, and wait for every in-flight load there on every iteration.
+      // (gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15.)
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      tile = last + 1;
+      if (tile >= end) break;
+    }
   }
 
-  if (MODE == kArgmax) {
+  if (kBest) {
     __shared__ float wv[kWaves];
     __shared__ uint32_t wi[kWaves];
     egd::team_argmax<64>(best_v, best_i);
@@ -366,6 +454,7 @@ KernelFn pick(int team, int cpl, int u) {
 template <int BITS, int ENC>
 KernelFn pick_mode(int mode, int team, int cpl, int u) {
   if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u);
+  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u);
   if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u);
   return pick<BITS, ENC, kPlain>(team, cpl, u);
 }
@@ -379,13 +468,18 @@ KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u) {
 
 struct Shape {
   int team = 0, cpl = 0, u = 0;
-  uint32_t tiles = 0, grid = 0;
+  uint32_t tiles = 0;
 };
 
-uint32_t grid_for(uint32_t tiles, int cu_count) {
-  // One tile per wave up to 8 workgroups of 4 waves per CU; larger matrices loop.
+// One tile per wave while the matrix is small; otherwise exactly the workgroups the device
+// holds at once (occupancy x CUs), each wave then walking its own contiguous range of tiles.
+// Sizing to residency matters because the ranges are equal: a second, late-starting round of
+// workgroups would double the tail.
+uint32_t grid_for(eg_context* ctx, KernelFn fn, uint32_t tiles, uint32_t smem_bytes) {
+  int occ = eg::occupancy_of(ctx, reinterpret_cast<const void*>(fn), smem_bytes);
+  if (occ <= 0) occ = 2;
   uint64_t blocks = ((uint64_t)tiles + kWaves - 1) / kWaves;
-  const uint64_t cap = (uint64_t)cu_count * 8;
+  const uint64_t cap = (uint64_t)ctx->cu_count * (uint64_t)occ;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   return (uint32_t)blocks;
@@ -394,7 +488,7 @@ uint32_t grid_for(uint32_t tiles, int cu_count) {
 // One chunk slot per lane while rows have <= 64 chunks (x costs 32 VGPRs), two rows per lane
 // per tile (four for full-wave teams); longer rows take the full wave and 2-4 slots, with
 // fewer rows per tile to stay within ~128 VGPRs. `row_multiple` (batched plans) is the row count every segment divides.
-Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count, const eg_context* ctx, uint32_t row_multiple = 0) {
+Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t row_multiple = 0) {
   Shape sh;
   if (chunks == 0 || chunks > 256) return sh;
   if (chunks <= 64) {
@@ -419,7 +513,6 @@ Shape choose_shape(uint32_t n, uint32_t chunks, int cu_count, const eg_context* 
   if (row_multiple && row_multiple % (rpw * sh.u) != 0) return Shape{};
   const uint32_t tile_rows = rpw * sh.u;
   sh.tiles = (n + tile_rows - 1) / tile_rows;
-  sh.grid = grid_for(sh.tiles, cu_count);
   return sh;
 }
 
@@ -454,8 +547,10 @@ int validate(eg_context* ctx, const QuantView& v) {
   if (elements % (32 / v.bits) != 0)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: %llu codes do not fill whole 32-bit words", v.op,
                     (unsigned long long)elements);
-  if (elements >= (1ull << 32) * (32 / v.bits) || (uint64_t)v.n * v.blocks_per_row >= (1ull << 32))
-    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u x %u exceeds the 32-bit block index range", v.op, v.n, v.k);
+  // Streams are addressed with 32-bit byte offsets.
+  if (elements * (uint64_t)v.bits / 8 >= (1ull << 32) || (uint64_t)v.n * v.blocks_per_row * 4 >= (1ull << 32) ||
+      ((uint64_t)v.out_offset + v.n) * 4 >= (1ull << 32))
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u x %u exceeds the 4 GiB stream range", v.op, v.n, v.k);
   return EG_OK;
 }
 
@@ -473,11 +568,11 @@ int launch(eg_context* ctx, const QuantView& v) {
   const uint32_t chunks = v.k / epc;
   Shape shape;
   if (aligned && v.k % epc == 0 && v.block_size % epc == 0)
-    shape = choose_shape(v.n, chunks, ctx->cu_count, ctx);
+    shape = choose_shape(v.n, chunks, ctx);
   uint32_t* partials = reinterpret_cast<uint32_t*>(eg::partials(ctx));
   uint32_t grid = 0;
-  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, argmax ? kArgmax : kPlain, shape.team, shape.cpl, shape.u)
-                           : nullptr;
+  const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
+  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u) : nullptr;
   if (fn) {
     GemvArgs a{};
     a.x = v.x;
@@ -493,9 +588,11 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.out_offset = v.out_offset;
     a.partials = partials;
     a.segs = nullptr;
+    a.seg_count = 0;
     a.total_passes = shape.tiles;
-    grid = shape.grid;
-    hipLaunchKernelGGL(fn, dim3(shape.grid), dim3(256), 0, ctx->stream, a);
+    const uint32_t smem = chunks * epc * 4u;
+    grid = grid_for(ctx, fn, shape.tiles, smem);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   } else {
     uint64_t blocks = (v.n + kWaves - 1) / kWaves;
     const uint64_t cap = (uint64_t)ctx->cu_count * 8;
@@ -563,7 +660,7 @@ int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, c
 struct eg_gemv_plan {
   DevSegment* table = nullptr;  // device copy
   uint32_t count = 0;
-  uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0;
+  uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
   int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0;
 };
 
@@ -574,6 +671,8 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   const char* op = "gemv_plan";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!out_plan || !segments || count == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: empty segment table", op);
+  if (count > kMaxSegments)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u segments, at most %u per plan", op, count, kMaxSegments);
   *out_plan = nullptr;
   if (bits != 4 && bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8", op);
   if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
@@ -592,14 +691,15 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
       return eg::fail(ctx, EG_ERR_INVALID, "%s: segment %u has %u rows, not a positive multiple of 8", op, i, g.rows);
     if ((reinterpret_cast<uintptr_t>(g.packed) & 15u) != 0)
       return eg::fail(ctx, EG_ERR_INVALID, "%s: segment %u codes are not 16-byte aligned", op, i);
-    if ((uint64_t)g.rows * (k / block_size) >= (1ull << 32))
-      return eg::fail(ctx, EG_ERR_RANGE, "%s: segment %u exceeds the 32-bit block index range", op, i);
+    if ((uint64_t)g.rows * (k / block_size) * 4 >= (1ull << 32) || (uint64_t)g.rows * k * bits / 8 >= (1ull << 32) ||
+        ((uint64_t)g.out_offset + g.rows) * 4 >= (1ull << 32))
+      return eg::fail(ctx, EG_ERR_RANGE, "%s: segment %u exceeds the 4 GiB stream range", op, i);
     rows_total += g.rows;
   }
   const uint32_t chunks = k / epc;
   uint32_t row_gcd = 0;
   for (uint32_t i = 0; i < count; i++) row_gcd = std::gcd(row_gcd, segments[i].rows);
-  Shape shape = choose_shape((uint32_t)std::min<uint64_t>(rows_total, 0xFFFFFFFFu), chunks, ctx->cu_count, ctx, row_gcd);
+  Shape shape = choose_shape((uint32_t)std::min<uint64_t>(rows_total, 0xFFFFFFFFu), chunks, ctx, row_gcd);
   if (shape.team == 0) return eg::fail(ctx, EG_ERR_INVALID, "%s: no kernel shape for k %u and these row counts", op, k);
   const uint32_t tile_rows = (64u / shape.team) * shape.u;
   DevSegment* host = new DevSegment[count];
@@ -629,7 +729,9 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->team = shape.team;
   plan->cpl = shape.cpl;
   plan->u = shape.u;
-  plan->grid = grid_for(pass, ctx->cu_count);
+  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u);
+  plan->smem = k * 4u + count * (uint32_t)sizeof(DevSegment);
+  plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
   *out_plan = plan;
   return EG_OK;
 }
@@ -645,10 +747,11 @@ int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* 
   a.chunks_per_block = plan->block_size / (128u / plan->bits);
   a.blocks_per_row = plan->k / plan->block_size;
   a.segs = plan->table;
+  a.seg_count = plan->count;
   a.total_passes = plan->total_passes;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
-  hipLaunchKernelGGL(fn, dim3(plan->grid), dim3(256), 0, ctx->stream, a);
+  hipLaunchKernelGGL(fn, dim3(plan->grid), dim3(256), plan->smem, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }
 

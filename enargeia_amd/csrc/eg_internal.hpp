@@ -8,8 +8,10 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 
-#include "../../include/enargeia_hip.h"
+#include "enargeia_hip.h"
 
 struct eg_context {
   int device = 0;
@@ -24,6 +26,11 @@ struct eg_context {
   // GEMV shape override (team, chunks per lane, rows per lane) from EG_GEMV_SHAPE="t,c,u",
   // read once at creation; zeros mean the built-in choice. For tuning sweeps.
   int gemv_override[3] = {0, 0, 0};
+  // Resident workgroups per CU of each kernel launched through this context (from
+  // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
+  // the device.
+  std::mutex occupancy_lock;
+  std::unordered_map<uint64_t, int> occupancy;  // key: kernel address ^ (LDS bytes << 48)
   char error[512] = {0};
 };
 
@@ -53,6 +60,10 @@ constexpr size_t kPartialsBytes = kWorkspaceBytes - kPartialsOffset;
 void launch_argmax_finalize(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t sentinel_index,
                             uint32_t* result);
 
+// Workgroups of `kernel` (256 threads, `smem_bytes` of dynamic LDS) resident per CU, cached
+// per context; 0 if the runtime cannot say.
+int occupancy_of(eg_context* ctx, const void* kernel, uint32_t smem_bytes = 0);
+
 // Validates a launch once the kernel is enqueued (hipGetLastError catches bad configurations
 // immediately; faults surface at the next synchronisation).
 int check_launch(eg_context* ctx, const char* op);
@@ -68,12 +79,59 @@ namespace egd {
 // lgkmcnt and force coarse waits. Casting to address space 1 restores global loads.
 template <typename T>
 using gptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+using gptr_mut = __attribute__((address_space(1))) T*;
 // 16 bytes as a native vector (HIP's uint4 is a class, which cannot be copied out of an
 // address-space-qualified lvalue).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ gptr<T> as_global(const T* p) {
   return (gptr<T>)p;
+}
+template <typename T>
+__device__ __forceinline__ gptr_mut<T> as_global_mut(T* p) {
+  return (gptr_mut<T>)p;
+}
+
+// A pointer read from memory that every lane holds: moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+// Raw buffer resources: base address in SGPRs, `bytes` records, 32-bit byte offsets per lane.
+// Reads past `bytes` return zero and writes past it are dropped (bounds-checked by hardware).
+// Word 3 = 0x00020000: raw 32-bit data for gfx950.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+// Non-temporal (streaming) loads, for data read exactly once per launch (weight codes and
+// scales): the nt cache-policy bit lets the line bypass normal retention, which measures ~10%
+// more read bandwidth on MI355X than default-policy loads.
+constexpr int kNonTemporal = 2;
+__device__ __forceinline__ u32x4 load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kNonTemporal);
+}
+__device__ __forceinline__ uint32_t load_b32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kNonTemporal);
+}
+__device__ __forceinline__ float load_f32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kNonTemporal));
+}
+__device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0);
+}
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+}
+__device__ __forceinline__ void store_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, 0, 0);
 }
 
 // Opaque AND: keeps the compiler from folding a nibble mask into per-element bitfield
@@ -107,6 +165,31 @@ __device__ __forceinline__ float team_sum(float v) {
   if (TEAM >= 16) v = dpp_add<0x140>(v);       // row_mirror
   if (TEAM >= 32) v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
   if (TEAM >= 64) v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Sum across a team of TEAM consecutive lanes with the total in EVERY lane of the team, so a
+// store or compare needs no lane-divergent branch. Within a row of 16 lanes the butterfly is
+// DPP (quad permutes, half-row and row mirrors); rows 16 apart are exchanged with a
+// ds_swizzle xor-16 (no LDS memory is touched); the two halves of a 64-lane team are joined by
+// two readlanes. Every lane adds the same operands in the same order (addition commutes), so
+// all lanes hold bit-identical totals, and the order is fixed: deterministic.
+template <int TEAM>
+__device__ __forceinline__ float team_allsum(float v) {
+  if (TEAM >= 2) v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (TEAM >= 4) v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (TEAM >= 8) v = dpp_add<0x141>(v);  // row_half_mirror
+  if (TEAM >= 16) v = dpp_add<0x140>(v); // row_mirror
+  if (TEAM >= 32) {
+    // bit mode: and_mask 0x1F, or_mask 0, xor_mask 0x10
+    const int o = __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F);
+    v = v + __builtin_bit_cast(float, o);
+  }
+  if (TEAM >= 64) {
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    v = lo + hi;
+  }
   return v;
 }
 

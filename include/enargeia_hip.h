@@ -167,7 +167,8 @@ EG_API int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* pa
  * across layers. Each segment is a whole matrix of `rows` rows with the same semantics as
  * eg_matmul_q4_decode: out[row + out_offset] = sum_k x[k] * W[row, k] (+ bias[row] if bias).
  * The plan validates the table once and keeps it in device memory, so a launch is
- * capture-safe. rows must be a multiple of 8 for every segment. */
+ * capture-safe. rows must be a multiple of 8 for every segment; at most 256 segments per plan
+ * (EG_ERR_RANGE beyond). */
 typedef struct eg_gemv_segment {
   const uint32_t* packed;
   const float* scales;
