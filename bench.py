@@ -303,6 +303,9 @@ def main() -> int:
         a.release()
         b.release()
 
+    # ---- decode tok/s at 2048 context (config 4) ----
+    decode = decode_throughput(dev, ev, stream, args)
+
     # ---- roofline: the dominant kernel = the K=896 batched launch ----
     t896_ms = dominant_ms
     achieved = BATCH896_BYTES / (t896_ms * 1e-3) / 1e9
@@ -334,12 +337,80 @@ def main() -> int:
                     "sampled_token_us": round(sampled_us, 2),
                     "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history"},
         "per_gemv_us": per_gemv,
-        "decode_tok_s_2048": None,
+        "decode_tok_s_2048": decode["tok_s"],
+        "decode": decode,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+DECODE_STEPS = 128
+
+
+def decode_throughput(dev, ev, stream, args) -> dict:
+    """the Qwen2.5-0.5B-shaped model (synthetic weights, int4 g32 projections,
+    int8 tied head, f16 KV cache), cache filled to 2048 - 128 positions (random f16 rows, the
+    reference's prime-then-decode method, decode.test.ts:97-118), then 128 greedy steps to
+    position 2047. One step = the whole token: embedding, 24 layers, LM head, argmax. tok_s
+    includes the one 4-byte readback per token (Session.decodeStep's rule); device_tok_s
+    chains the steps on the device with no readback."""
+    from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, synthetic_model
+
+    cfg = QWEN25_05B
+    t0 = time.time()
+    host = synthetic_model(cfg)
+    dm = DeviceModel(dev, host)
+    del host
+    dec = Decoder(dm)
+    log(f"decode model ready in {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(11)
+    prime = cfg.max_context - DECODE_STEPS
+    rows = cfg.layers * cfg.max_context * cfg.kv_heads * cfg.head_dim
+    for ptr in (dec.buffers.k_cache, dec.buffers.v_cache):
+        fill = rng.standard_normal(rows, dtype=np.float32).astype(np.float16).view(np.uint16)
+        dev.write(ptr, fill)
+        dev.sync()
+    first = 785  # the first greedy id of the reference's fixture prompt; any id works
+    result = {"config": "BASELINE config 4: Qwen2.5-0.5B shape, 24 layers, int4 g32 + int8 tied head, f16 KV",
+              "context": cfg.max_context, "steps": DECODE_STEPS, "launches_per_token": 5 * cfg.layers + 4}
+    for mode in ("eager", "graph"):
+        if mode == "graph":
+            dec.capture()
+        # warm-up steps end at the prime point, then the timed steps run prime .. 2047
+        dec.reset(prime - 8, first)
+        for _ in range(8):
+            dec.step(read_token=False)
+        dev.sync()
+        a, b = ev.create(), ev.create()
+        t = time.perf_counter()
+        ev.record(a, stream)
+        tokens = [dec.step(read_token=True) for _ in range(DECODE_STEPS)]
+        ev.record(b, stream)
+        ev.sync(b)
+        wall = time.perf_counter() - t
+        result[f"{mode}_tok_s"] = round(DECODE_STEPS / wall, 1)
+        result[f"{mode}_ms_per_token"] = round(wall / DECODE_STEPS * 1e3, 4)
+        # device-chained: same steps, no per-token readback
+        dec.reset(prime, first)
+        ev.record(a, stream)
+        for _ in range(DECODE_STEPS):
+            dec.step(read_token=False)
+        ev.record(b, stream)
+        ev.sync(b)
+        result[f"{mode}_device_tok_s"] = round(DECODE_STEPS / (ev.ms(a, b) * 1e-3), 1)
+        log(f"decode ({mode}): {result[f'{mode}_tok_s']} tok/s with a readback per token, "
+            f"{result[f'{mode}_device_tok_s']} tok/s device-chained; last token {tokens[-1]}")
+    best = max(("eager", "graph"), key=lambda m: result[f"{m}_tok_s"])
+    result["tok_s"] = result[f"{best}_tok_s"]
+    result["launch"] = best
+    step_bytes = (STEP_BYTES + LM_HEAD_BYTES
+                  + 2 * cfg.layers * (prime + DECODE_STEPS // 2) * cfg.kv_heads * cfg.head_dim * 2)
+    result["gbs_at_best"] = round(step_bytes * result["tok_s"] / 1e9, 1)
+    dec.close()
+    dm.release()
+    return result
 
 
 CALIBRATION_BYTES = 256 << 20

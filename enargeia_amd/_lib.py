@@ -49,6 +49,18 @@ SIGNATURES: dict[str, tuple] = {
     "eg_gemv_plan_destroy": (_i, [_vp, _vp]),
     "eg_argmax": (_i, [_vp, _vp, _vp, _vp]),
     "eg_sample": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "eg_embed_gather": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "eg_attention_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "eg_attention_combine": (_i, [_vp, _vp, _vp, _vp]),
+    "eg_gemv_plan_launch_input": (_i, [_vp, _vp, _vp]),
+    "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "eg_decode_advance": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
+    "eg_decoder_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "eg_decoder_destroy": (_i, [_vp]),
+    "eg_decoder_buffers_get": (_i, [_vp, _vp]),
+    "eg_decoder_reset": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32]),
+    "eg_decoder_step": (_i, [_vp, _vp]),
+    "eg_decoder_capture": (_i, [_vp]),
     "eg_graph_begin": (_i, [_vp]),
     "eg_graph_end": (_i, [_vp, ctypes.POINTER(_vp)]),
     "eg_graph_launch": (_i, [_vp, _vp]),

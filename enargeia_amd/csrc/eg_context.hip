@@ -101,6 +101,10 @@ int eg_create(int device, eg_context** out_ctx) {
       ctx->gemv_override[2] = u;
     }
   }
+  if (const char* tpw = std::getenv("EG_FUSED_TILES_PER_WAVE")) {
+    const int v = std::atoi(tpw);
+    if (v >= 1 && v <= 64) ctx->fused_tiles_per_wave = (uint32_t)v;
+  }
   err = hipMalloc(&ctx->workspace, eg::kWorkspaceBytes);
   if (err != hipSuccess) {
     hipStreamDestroy(ctx->own_stream);

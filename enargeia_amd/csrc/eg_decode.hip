@@ -1,0 +1,317 @@
+// The decode step's non-GEMV ops: the embedding gather, fused decode attention over the f16
+// KV cache, the attention combine, and the device-side step bookkeeping.
+//
+// Reference pieces: embed_gather (embedding_variants.ts:93-133), rope.wgsl + the f16 cache
+// pack (cache_variants.ts:147-305, graph_decode.ts:276-320), attn_scores / softmax /
+// attn_apply decode (graph_decode.ts:322-345; CPU semantics ops.ts:87-205), and the per-token
+// bookkeeping of Session.decodeStep (session.ts:347-375).
+//
+// MI355X design: the reference runs RoPE, the cache appends, the scores, the softmax and the
+// weighted sum as six dispatches with the scores and weights round-tripping through memory.
+// Here one launch does it all: each workgroup owns one kv head and one chunk of positions for
+// every query head of that kv group (GQA: the K and V rows are staged once in LDS and reused
+// by the group's query heads), and writes a flash-decoding partial (o, max, sum). The
+// partials are combined by whoever consumes the attention output (the o projection's input
+// stage), so no launch exists just to merge them.
+#include <cmath>
+
+#include "eg_internal.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// IEEE binary16 through the compiler's native _Float16 (round to nearest even on the way in).
+__device__ __forceinline__ float half_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t float_to_half(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// ---- embedding gather ------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void embed_gather_kernel(const uint32_t* token, const uint32_t* packed,
+                                                                const float* scales, const uint32_t* zeros,
+                                                                float* out, eg_embedding_dims d, int encoding,
+                                                                int bits) {
+  const uint32_t id = token[0];
+  if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
+  const uint32_t row = id - d.row_begin;
+  const uint32_t per_word = 32u / (uint32_t)bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (uint32_t i = threadIdx.x; i < d.hidden; i += blockDim.x) {
+    const uint64_t e = (uint64_t)row * d.hidden + i;
+    uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
+    const uint32_t blk = row * d.blocks_per_row + i / d.block_size;
+    float zero;
+    if (encoding == EG_ENC_OFFSET_ZEROS) {
+      zero = (float)((zeros[blk / per_word] >> (bits * (blk % per_word))) & mask);
+    } else {
+      code ^= 1u << (bits - 1);  // two's complement -> offset binary
+      zero = (float)(1u << (bits - 1));
+    }
+    out[d.out_offset + i] = ((float)code - zero) * scales[blk];
+  }
+}
+
+// ---- fused decode attention ------------------------------------------------------------------
+
+// RoPE (ops.ts:87-114): pairs (i, i + D/2) rotated by angle = position * theta^(-2i/D). The
+// angle, its cosine and sine are computed once per frequency, in double precision like the CPU
+// reference, and the rotation itself is evaluated in double too.
+template <int D>
+__device__ __forceinline__ void rope_table(double2* cs, uint32_t i, uint32_t position, float theta) {
+  const double angle = (double)position / pow((double)theta, (2.0 * i) / D);
+  cs[i] = make_double2(cos(angle), sin(angle));
+}
+template <int D>
+__device__ __forceinline__ void rope_apply(float* v, uint32_t i, const double2* cs) {
+  const double a = v[i], b = v[i + D / 2];
+  v[i] = (float)(a * cs[i].x - b * cs[i].y);
+  v[i + D / 2] = (float)(b * cs[i].x + a * cs[i].y);
+}
+
+// One workgroup: kv head kv = blockIdx.y / HSPLIT and the HSPLIT-th share of its query heads,
+// positions [j0, j0 + CHUNK) (blockIdx.x). Splitting the group's heads over HSPLIT workgroups
+// doubles the parallelism of a launch that otherwise has only chunks x kv_heads workgroups; the
+// K/V rows they share come from L2.
+template <int D, int CHUNK, int GMAX, int HSPLIT>
+__global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32_t* position, const float* q,
+                                                                    const float* k, const float* v,
+                                                                    uint16_t* k_cache, uint16_t* v_cache,
+                                                                    float* partials, eg_attention_dims d) {
+  const uint32_t pos = position[0];
+  const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
+  const uint32_t c = blockIdx.x;
+  const uint32_t chunks = gridDim.x;
+  const uint32_t group = d.heads / d.kv_heads;
+  const uint32_t share = (group + HSPLIT - 1) / HSPLIT;
+  const uint32_t gb = min(group, hs * share), ng = min(group, gb + share) - gb;  // heads [gb, gb + ng)
+  const uint32_t j0 = c * CHUNK;
+  const uint32_t tid = threadIdx.x;
+  // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
+  const uint32_t h0 = kv * group + gb;
+  float* po = partials + (size_t)h0 * D * chunks + c;
+  float* pm = partials + (size_t)d.heads * D * chunks + (size_t)h0 * chunks + c;
+  float* pl = pm + (size_t)d.heads * chunks;
+  if (ng == 0) return;
+
+  // Past the live history (or, defensively, a position beyond the cache): an empty partial.
+  // No cache row is written unless pos < max_context.
+  if (j0 > pos || pos >= d.max_context) {
+    for (uint32_t i = tid; i < ng * D; i += blockDim.x) po[(size_t)i * chunks] = 0.f;
+    if (tid < ng) {
+      pm[(size_t)tid * chunks] = -INFINITY;
+      pl[(size_t)tid * chunks] = 0.f;
+    }
+    return;
+  }
+  const uint32_t live = min((uint32_t)CHUNK, pos + 1 - j0);
+
+  __shared__ float qs[GMAX][D];          // rotated, pre-scaled queries of this workgroup's heads
+  __shared__ float knew[D], vnew[D];     // the new key (rotated) and value
+  __shared__ double2 cs[D / 2];          // RoPE cos/sin at `pos`
+  __shared__ uint16_t ks[CHUNK][D + 2];  // K rows (f16), padded against bank conflicts
+  __shared__ uint16_t vs[CHUNK][D + 2];  // V rows (f16)
+  __shared__ float p[GMAX][CHUNK];       // scores, then exp(score - max)
+  __shared__ float mstat[GMAX], lstat[GMAX];
+
+  const float scale = 1.0f / sqrtf((float)D);
+  const bool owns_new = pos < j0 + CHUNK;
+  const uint32_t cached = owns_new ? live - 1 : live;  // rows read from the cache
+  // Issue the cache reads first (16-byte loads, D/8 per row); their latency covers the RoPE.
+  for (uint32_t i = tid; i < cached * (D / 8); i += blockDim.x) {
+    const uint32_t r = i / (D / 8), w = i % (D / 8);
+    const size_t at = ((size_t)(j0 + r) * d.kv_heads + kv) * D + w * 8;
+    const uint4 kq = *reinterpret_cast<const uint4*>(k_cache + at);
+    const uint4 vq = *reinterpret_cast<const uint4*>(v_cache + at);
+    uint32_t* kd = reinterpret_cast<uint32_t*>(&ks[r][w * 8]);
+    uint32_t* vd = reinterpret_cast<uint32_t*>(&vs[r][w * 8]);
+    kd[0] = kq.x; kd[1] = kq.y; kd[2] = kq.z; kd[3] = kq.w;
+    vd[0] = vq.x; vd[1] = vq.y; vd[2] = vq.z; vd[3] = vq.w;
+  }
+  for (uint32_t i = tid; i < ng * D; i += blockDim.x) qs[i / D][i % D] = q[(size_t)h0 * D + i];
+  if (tid < D) {
+    knew[tid] = k[(size_t)kv * D + tid];
+    vnew[tid] = v[(size_t)kv * D + tid];
+  }
+  if (tid < D / 2) rope_table<D>(cs, tid, pos, d.theta);
+  __syncthreads();
+  for (uint32_t i = tid; i < ng * (D / 2); i += blockDim.x) rope_apply<D>(qs[i / (D / 2)], i % (D / 2), cs);
+  if (owns_new && tid < D / 2) rope_apply<D>(knew, tid, cs);
+  __syncthreads();
+  for (uint32_t i = tid; i < ng * D; i += blockDim.x) qs[i / D][i % D] *= scale;
+  // The row at `pos` is the new one: appended to the cache (by the first head share only) and
+  // staged from registers.
+  if (owns_new && tid < D) {
+    const uint16_t kh = float_to_half(knew[tid]), vh = float_to_half(vnew[tid]);
+    if (hs == 0) {
+      const size_t at = ((size_t)pos * d.kv_heads + kv) * D + tid;
+      k_cache[at] = kh;
+      v_cache[at] = vh;
+    }
+    ks[pos - j0][tid] = kh;
+    vs[pos - j0][tid] = vh;
+  }
+  __syncthreads();
+
+  // scores: thread -> one position, a strided subset of the group's heads
+  {
+    const uint32_t j = tid % CHUNK;
+    const uint32_t g0 = tid / CHUNK, gs = kThreads / CHUNK;
+    for (uint32_t g = g0; g < ng; g += gs) {
+      float s = -INFINITY;
+      if (j < live) {
+        float acc = 0.f;
+#pragma unroll 16
+        for (int e = 0; e < D; e++) acc = fmaf(qs[g][e], half_to_float(ks[j][e]), acc);
+        s = acc;
+      }
+      p[g][j] = s;
+    }
+  }
+  __syncthreads();
+
+  // softmax statistics: one wave per head, lanes over the chunk, fixed-order reductions
+  const uint32_t wave = tid >> 6, lane = tid & 63u;
+  for (uint32_t g = wave; g < ng; g += kThreads / 64) {
+    float m = -INFINITY;
+    for (uint32_t j = lane; j < CHUNK; j += 64) m = fmaxf(m, p[g][j]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float l = 0.f;
+    for (uint32_t j = lane; j < CHUNK; j += 64) {
+      const float e = j < live ? expf(p[g][j] - m) : 0.f;
+      p[g][j] = e;
+      l += e;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) {
+      mstat[g] = m;
+      lstat[g] = l;
+    }
+  }
+  __syncthreads();
+
+  // o[g][e] = sum_j p[g][j] * V[j][e]
+  for (uint32_t i = tid; i < ng * D; i += blockDim.x) {
+    const uint32_t g = i / D, e = i % D;
+    float acc = 0.f;
+    for (uint32_t j = 0; j < live; j++) acc = fmaf(p[g][j], half_to_float(vs[j][e]), acc);
+    po[(size_t)i * chunks] = acc;
+  }
+  if (tid < ng) {
+    pm[(size_t)tid * chunks] = mstat[tid];
+    pl[(size_t)tid * chunks] = lstat[tid];
+  }
+}
+
+// ---- combine ---------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void attention_combine_kernel(const float* partials, float* out,
+                                                                     eg_attention_dims d) {
+  const uint32_t chunks = d.max_context / d.chunk;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < d.heads * d.head_dim; i += gridDim.x * blockDim.x)
+    out[i] = egd::attention_combine_at(partials, i, d.heads, d.head_dim, chunks);
+}
+
+__global__ void advance_kernel(uint32_t* position, uint32_t* history, uint32_t* history_length,
+                               const uint32_t* token, uint32_t capacity) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    position[0] += 1;
+    if (history && history_length) {
+      const uint32_t n = history_length[0];
+      if (n < capacity) {
+        history[n] = token[0];
+        history_length[0] = n + 1;
+      }
+    }
+  }
+}
+
+int check_attention(eg_context* ctx, const char* op, const eg_attention_dims* d) {
+  if (!d) return eg::fail(ctx, EG_ERR_INVALID, "%s: dims is NULL", op);
+  if (d->head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "%s: head_dim %u (64 is supported)", op, d->head_dim);
+  if (d->kv_heads == 0 || d->heads == 0 || d->heads % d->kv_heads != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: %u heads do not group over %u kv heads", op, d->heads, d->kv_heads);
+  if (d->heads / d->kv_heads > 8)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: %u query heads per kv head (at most 8)", op, d->heads / d->kv_heads);
+  if ((uint64_t)d->kv_heads * 2 > 65535)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u kv heads exceed the grid", op, d->kv_heads);
+  if (d->chunk != 64 && d->chunk != 128)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: chunk %u (64 or 128 are supported)", op, d->chunk);
+  if (d->max_context == 0 || d->max_context % d->chunk != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: max_context %u is not a positive multiple of %u", op, d->max_context,
+                    d->chunk);
+  if ((uint64_t)d->max_context / d->chunk * d->kv_heads > 65535)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u chunks exceed the grid", op, d->max_context / d->chunk);
+  return EG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* packed, const float* scales,
+                    const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding, int bits) {
+  const char* op = "embed_gather";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!token || !packed || !scales || !out || !dims) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if (bits != 4 && bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8", op);
+  if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", op, encoding);
+  if (encoding == EG_ENC_OFFSET_ZEROS && !zeros) return eg::fail(ctx, EG_ERR_INVALID, "%s: zeros is NULL", op);
+  if (dims->seq != 1) return eg::fail(ctx, EG_ERR_INVALID, "%s: seq %u (decode gathers one token)", op, dims->seq);
+  if (dims->block_size == 0 || dims->hidden % dims->block_size != 0 ||
+      dims->blocks_per_row != dims->hidden / dims->block_size)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: hidden %u / block %u / blocksPerRow %u disagree", op, dims->hidden,
+                    dims->block_size, dims->blocks_per_row);
+  hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, token, packed, scales,
+                     encoding == EG_ENC_SIGNED ? nullptr : zeros, out, *dims, encoding, bits);
+  return eg::check_launch(ctx, op);
+}
+
+int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k, const float* v,
+                        uint16_t* k_cache, uint16_t* v_cache, float* partials, const eg_attention_dims* dims) {
+  const char* op = "attention_decode";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!position || !q || !k || !v || !k_cache || !v_cache || !partials)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15u) || (reinterpret_cast<uintptr_t>(v_cache) & 15u))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: caches must be 16-byte aligned", op);
+  int st = check_attention(ctx, op, dims);
+  if (st != EG_OK) return st;
+  constexpr int kSplit = 2;
+  const dim3 grid(dims->max_context / dims->chunk, dims->kv_heads * kSplit);
+  if (dims->chunk == 64)
+    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, kSplit>), grid, dim3(kThreads), 0, ctx->stream, position,
+                       q, k, v, k_cache, v_cache, partials, *dims);
+  else
+    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 4, kSplit>), grid, dim3(kThreads), 0, ctx->stream, position,
+                       q, k, v, k_cache, v_cache, partials, *dims);
+  return eg::check_launch(ctx, op);
+}
+
+int eg_attention_combine(eg_context* ctx, const float* partials, float* out, const eg_attention_dims* dims) {
+  const char* op = "attention_combine";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!partials || !out) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  int st = check_attention(ctx, op, dims);
+  if (st != EG_OK) return st;
+  const uint32_t n = dims->heads * dims->head_dim;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream,
+                     partials, out, *dims);
+  return eg::check_launch(ctx, op);
+}
+
+int eg_decode_advance(eg_context* ctx, uint32_t* position, uint32_t* history, uint32_t* history_length,
+                      const uint32_t* token, uint32_t history_capacity) {
+  const char* op = "decode_advance";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!position || !token) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if ((history == nullptr) != (history_length == nullptr))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: history and history_length go together", op);
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, ctx->stream, position, history, history_length, token,
+                     history_capacity);
+  return eg::check_launch(ctx, op);
+}
+
+}  // extern "C"

@@ -32,6 +32,7 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup (256 threads)
 constexpr uint32_t kMaxSegments = 256;  // matrices per batched plan (the table lives in LDS)
+constexpr uint32_t kMaxCombine = 1024;  // heads x chunks of an attention-combine input stage
 
 // One matrix of a batched launch, as the kernel sees it: its pointers and the range of wave
 // passes (RPW rows each) it occupies in the launch's pass space.
@@ -63,6 +64,11 @@ struct GemvArgs {
   const DevSegment* segs;  // batched launches only
   uint32_t seg_count;
   uint32_t total_passes;   // tiles over all rows (all segments)
+  // input stage (eg_input_kind): how each workgroup produces x in LDS
+  int in_kind;
+  const float* x2;         // norm weight / up
+  float eps;
+  uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
 };
 
 template <int BITS>
@@ -136,6 +142,104 @@ struct Loads {
   float b[U];
 };
 
+// The input stage: every workgroup writes the K-element input vector into LDS (xs), from x
+// as given or through a fused producer - RMSNorm (the reduction is per workgroup, fixed order,
+// so every workgroup computes the same bits), SiLU(gate) * up, or the attention combine.
+__device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch) {
+  // Every global read below is a 16-byte vector in a loop the compiler unrolls, so a thread has
+  // several loads in flight instead of one round trip per element (the producers read data the
+  // previous launch wrote, often from another XCD's L2: each round trip is long).
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n4 = n / 4;  // n is a multiple of 32
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* y4 = reinterpret_cast<const float4*>(a.x2);
+  float4* out4 = reinterpret_cast<float4*>(xs);
+  if (a.in_kind == EG_INPUT_RMSNORM) {
+    __shared__ float red[kWaves];
+    float ss = 0.f;
+#pragma unroll 4
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+      const float4 v = x4[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63u) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) total += red[w];
+    const float inv = 1.0f / sqrtf(total / (float)n + a.eps);
+#pragma unroll 4
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+      const float4 v = x4[i], w = y4[i];
+      out4[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+    }
+  } else if (a.in_kind == EG_INPUT_SILU_MUL) {
+#pragma unroll 4
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+      const float4 g = x4[i], u = y4[i];
+      out4[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                            g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+    }
+  } else if (a.in_kind == EG_INPUT_ATTENTION) {
+    // Three phases, none walking the chunks with dependent global loads: every (head, chunk)
+    // pair's (max, sum) is loaded once into LDS; each pair's weight e^(m_c - M) / L is formed
+    // from LDS; then every output sums its chunks' partial o values (contiguous, read as
+    // vectors) with those weights - the same operations in the same order as
+    // egd::attention_combine_at.
+    const uint32_t heads = a.att_heads, chunks = a.att_chunks, D = a.att_head_dim;
+    const uint32_t hcs = heads * chunks;
+    const float* m = a.x + (size_t)heads * D * chunks;
+    const float* l = m + hcs;
+    float* mval = scratch;
+    float* lval = scratch + hcs;
+    float* wts = scratch + 2 * hcs;
+    for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
+      mval[hc] = m[hc];
+      lval[hc] = l[hc];
+    }
+    __syncthreads();
+    for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
+      const uint32_t b = (hc / chunks) * chunks;
+      float M = -INFINITY;
+      for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, mval[b + c]);
+      float L = 0.f;
+      for (uint32_t c = 0; c < chunks; c++) L = fmaf(lval[b + c], expf(mval[b + c] - M), L);
+      wts[hc] = expf(mval[hc] - M) / L;
+    }
+    __syncthreads();
+    const uint32_t c4 = chunks / 4;
+    for (uint32_t i = tid; i < n; i += blockDim.x) {
+      const float* o = a.x + (size_t)i * chunks;
+      const float* w = wts + (i / D) * chunks;
+      float acc = 0.f;
+      if ((chunks & 3u) == 0) {
+        const float4* o4 = reinterpret_cast<const float4*>(o);
+#pragma unroll 8
+        for (uint32_t q = 0; q < c4; q++) {
+          const float4 v = o4[q];
+          acc = fmaf(v.x, w[4 * q + 0], acc);
+          acc = fmaf(v.y, w[4 * q + 1], acc);
+          acc = fmaf(v.z, w[4 * q + 2], acc);
+          acc = fmaf(v.w, w[4 * q + 3], acc);
+        }
+      } else {
+        for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], w[c], acc);
+      }
+      xs[i] = acc;
+    }
+  } else {
+    const auto src = egd::as_global(reinterpret_cast<const egd::u32x4*>(a.x));
+    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
+#pragma unroll 4
+    for (uint32_t i = tid; i < n4; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
 // One wave computes a tile of RPW * U rows per step: RPW teams of TEAM lanes side by side,
 // each team owning U rows (spaced RPW apart so that, for every (u, j), the wave's load is RPW
 // consecutive rows x TEAM consecutive 16-byte chunks).
@@ -169,12 +273,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // wave; each lane then keeps the chunks it owns in VGPRs for every row it visits.
   extern __shared__ __align__(16) uint8_t smem[];
   const uint32_t x_words = a.chunks * EPC;
-  {
-    const auto src = egd::as_global(reinterpret_cast<const egd::u32x4*>(a.x));
-    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(smem);
-    for (uint32_t i = threadIdx.x; i < x_words / 4; i += blockDim.x) dst[i] = src[i];
-  }
   DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
+  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? a.seg_count : 0u) *
+                                                                      (uint32_t)sizeof(DevSegment));
+  produce_input(a, reinterpret_cast<float*>(smem), x_words, scratch);
   if (MODE == kBatched) {
     const uint32_t words = a.seg_count * (uint32_t)(sizeof(DevSegment) / 4);
     const auto src = egd::as_global(reinterpret_cast<const uint32_t*>(a.segs));
@@ -475,10 +577,13 @@ struct Shape {
 // holds at once (occupancy x CUs), each wave then walking its own contiguous range of tiles.
 // Sizing to residency matters because the ranges are equal: a second, late-starting round of
 // workgroups would double the tail.
-uint32_t grid_for(eg_context* ctx, KernelFn fn, uint32_t tiles, uint32_t smem_bytes) {
+// A fused input stage is recomputed by every workgroup, so those launches give each wave
+// `tiles_per_wave` tiles to amortise it (fewer, longer-lived workgroups).
+uint32_t grid_for(eg_context* ctx, KernelFn fn, uint32_t tiles, uint32_t smem_bytes, uint32_t tiles_per_wave = 1) {
   int occ = eg::occupancy_of(ctx, reinterpret_cast<const void*>(fn), smem_bytes);
   if (occ <= 0) occ = 2;
-  uint64_t blocks = ((uint64_t)tiles + kWaves - 1) / kWaves;
+  const uint64_t per_block = (uint64_t)kWaves * (tiles_per_wave ? tiles_per_wave : 1);
+  uint64_t blocks = ((uint64_t)tiles + per_block - 1) / per_block;
   const uint64_t cap = (uint64_t)ctx->cu_count * (uint64_t)occ;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
@@ -527,7 +632,54 @@ struct QuantView {
   uint32_t n, k, block_size, blocks_per_row, out_offset;
   int encoding, bits;
   uint32_t* result;  // non-null for the fused argmax
+  const eg_gemv_input* input = nullptr;  // fused input stage; NULL: x as given
 };
+
+// LDS the input stage needs beyond x and the segment table.
+uint32_t input_scratch_bytes(const GemvArgs& a) {
+  return a.in_kind == EG_INPUT_ATTENTION ? 3u * a.att_heads * a.att_chunks * 4u : 0u;
+}
+
+// Validates an input stage against the GEMV's K and copies it into the kernel arguments.
+int apply_input(eg_context* ctx, const char* op, const eg_gemv_input* in, uint32_t k, GemvArgs& a) {
+  a.in_kind = EG_INPUT_VECTOR;
+  if (!in) return EG_OK;
+  a.in_kind = in->kind;
+  a.x = in->x;
+  a.x2 = in->x2;
+  a.eps = in->eps;
+  if (!in->x) return eg::fail(ctx, EG_ERR_INVALID, "%s: input x is NULL", op);
+  switch (in->kind) {
+    case EG_INPUT_VECTOR:
+      if (reinterpret_cast<uintptr_t>(in->x) & 15u)
+        return eg::fail(ctx, EG_ERR_INVALID, "%s: x is not 16-byte aligned", op);
+      return EG_OK;
+    case EG_INPUT_RMSNORM:
+    case EG_INPUT_SILU_MUL:
+      if (!in->x2) return eg::fail(ctx, EG_ERR_INVALID, "%s: the input stage needs x2", op);
+      if (in->kind == EG_INPUT_RMSNORM && !(in->eps >= 0.f))
+        return eg::fail(ctx, EG_ERR_INVALID, "%s: eps must be >= 0", op);
+      return EG_OK;
+    case EG_INPUT_ATTENTION: {
+      const eg_attention_dims& d = in->attention;
+      if (d.kv_heads == 0 || d.heads % d.kv_heads != 0 || d.chunk == 0 || d.max_context % d.chunk != 0)
+        return eg::fail(ctx, EG_ERR_INVALID, "%s: bad attention layout", op);
+      if (d.heads * d.head_dim != k)
+        return eg::fail(ctx, EG_ERR_INVALID, "%s: attention output %u x %u does not match k = %u", op, d.heads,
+                        d.head_dim, k);
+      if ((uint64_t)d.heads * (d.max_context / d.chunk) > kMaxCombine)
+        return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads x %u chunks exceed the combine stage's %u", op, d.heads,
+                        d.max_context / d.chunk, kMaxCombine);
+      a.att_heads = d.heads;
+      a.att_kv_heads = d.kv_heads;
+      a.att_head_dim = d.head_dim;
+      a.att_chunks = d.max_context / d.chunk;
+      return EG_OK;
+    }
+    default:
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown input kind %d", op, in->kind);
+  }
+}
 
 int validate(eg_context* ctx, const QuantView& v) {
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", v.op);
@@ -563,8 +715,9 @@ int launch(eg_context* ctx, const QuantView& v) {
   }
   const bool argmax = v.result != nullptr;
   const uint32_t epc = 128u / v.bits;
+  const bool fused = v.input && v.input->kind != EG_INPUT_VECTOR;
   const bool aligned = (reinterpret_cast<uintptr_t>(v.packed) & 15u) == 0 &&
-                       (reinterpret_cast<uintptr_t>(v.x) & 15u) == 0;
+                       (fused || (reinterpret_cast<uintptr_t>(v.x) & 15u) == 0);
   const uint32_t chunks = v.k / epc;
   Shape shape;
   if (aligned && v.k % epc == 0 && v.block_size % epc == 0)
@@ -573,9 +726,13 @@ int launch(eg_context* ctx, const QuantView& v) {
   uint32_t grid = 0;
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u) : nullptr;
+  if (fused && !fn)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: a fused input stage needs k and the block a multiple of %u", v.op, epc);
   if (fn) {
     GemvArgs a{};
     a.x = v.x;
+    st = apply_input(ctx, v.op, v.input, v.k, a);
+    if (st != EG_OK) return st;
     a.w = reinterpret_cast<const uint4*>(v.packed);
     a.scales = v.scales;
     a.zeros = v.zeros;
@@ -590,8 +747,8 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.segs = nullptr;
     a.seg_count = 0;
     a.total_passes = shape.tiles;
-    const uint32_t smem = chunks * epc * 4u;
-    grid = grid_for(ctx, fn, shape.tiles, smem);
+    const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
+    grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   } else {
     uint64_t blocks = (v.n + kWaves - 1) / kWaves;
@@ -650,6 +807,18 @@ int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, c
     if ((uint64_t)ctx->cu_count * 8 > max_groups)
       return eg::fail(ctx, EG_ERR_RANGE, "lm_head_argmax: workspace too small for the grid");
   }
+  return launch(ctx, v);
+}
+
+int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed,
+                            const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
+                            const eg_embedding_dims* dims, int encoding, int bits) {
+  if (!dims) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: dims is NULL");
+  if (!result) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: result is NULL");
+  if (!input) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: input is NULL");
+  QuantView v{"lm_head_argmax", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
+              dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
+              bits, result, input};
   return launch(ctx, v);
 }
 
@@ -738,11 +907,18 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
 
 int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* x) {
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "gemv_plan_launch: ctx is NULL");
-  if (!plan || !x) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: NULL argument");
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0)
-    return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: x is not 16-byte aligned");
+  eg_gemv_input in{};
+  in.kind = EG_INPUT_VECTOR;
+  in.x = x;
+  return eg_gemv_plan_launch_input(ctx, plan, &in);
+}
+
+int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const eg_gemv_input* input) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "gemv_plan_launch: ctx is NULL");
+  if (!plan || !input || !input->x) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: NULL argument");
   GemvArgs a{};
-  a.x = x;
+  int st = apply_input(ctx, "gemv_plan_launch", input, plan->k, a);
+  if (st != EG_OK) return st;
   a.chunks = plan->chunks;
   a.chunks_per_block = plan->block_size / (128u / plan->bits);
   a.blocks_per_row = plan->k / plan->block_size;
@@ -751,7 +927,11 @@ int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* 
   a.total_passes = plan->total_passes;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
-  hipLaunchKernelGGL(fn, dim3(plan->grid), dim3(256), plan->smem, ctx->stream, a);
+  const uint32_t extra = input_scratch_bytes(a);
+  const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
+                            ? grid_for(ctx, fn, plan->total_passes, plan->smem + extra, ctx->fused_tiles_per_wave)
+                            : plan->grid;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), plan->smem + extra, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }
 

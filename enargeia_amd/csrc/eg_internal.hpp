@@ -26,6 +26,8 @@ struct eg_context {
   // GEMV shape override (team, chunks per lane, rows per lane) from EG_GEMV_SHAPE="t,c,u",
   // read once at creation; zeros mean the built-in choice. For tuning sweeps.
   int gemv_override[3] = {0, 0, 0};
+  // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 2).
+  uint32_t fused_tiles_per_wave = 2;
   // Resident workgroups per CU of each kernel launched through this context (from
   // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
   // the device.
@@ -191,6 +193,25 @@ __device__ __forceinline__ float team_allsum(float v) {
     v = lo + hi;
   }
   return v;
+}
+
+// One element of the attention output from flash-decoding partials laid out chunk-fastest:
+// o[h][D][chunks], then m[h][chunks], then l[h][chunks]. out[h*D + e] =
+// sum_c o_c[e] * (e^(m_c - M) / L), M = max_c m_c, L = sum_c l_c e^(m_c - M); chunks in order, so
+// deterministic, and the same operations in the same order as the GEMV input stage's combine.
+__device__ __forceinline__ float attention_combine_at(const float* partials, uint32_t i, uint32_t heads,
+                                                      uint32_t D, uint32_t chunks) {
+  const uint32_t h = i / D;
+  const float* o = partials + (size_t)i * chunks;
+  const float* m = partials + (size_t)heads * D * chunks + (size_t)h * chunks;
+  const float* l = m + (size_t)heads * chunks;
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, m[c]);
+  float L = 0.f;
+  for (uint32_t c = 0; c < chunks; c++) L = fmaf(l[c], expf(m[c] - M), L);
+  float acc = 0.f;
+  for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], expf(m[c] - M) / L, acc);
+  return acc;
 }
 
 // (value, index) ordering used by every argmax here: larger value wins, ties go to the lower

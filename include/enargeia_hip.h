@@ -194,6 +194,133 @@ EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const 
 EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
               const eg_sample_dims* dims);
 
+/* ---- decode step: embedding, attention, fused GEMV inputs ----------------------------------- */
+
+/* embed_gather_<dtype> (embedding_variants.ts:93-133, :56-63 for q8): for the one token id read
+ * from DEVICE memory token[0] (the previous step's argmax/sample result, so a captured step
+ * needs no host round trip): if row_begin <= id < row_begin + row_count,
+ *   out[out_offset + i] = (code[id - row_begin, i] - zero) * scale[block]   for i < hidden
+ * else out is left untouched (another part of a split table owns the id). seq must be 1. */
+EG_API int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* packed, const float* scales,
+                           const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding,
+                           int bits);
+
+/* Decode attention over an f16 KV cache, fused: RoPE on q and on the new key (ops.ts:87-114,
+ * half-rotation pairing, angle in double precision), the new key and value appended to the
+ * cache at the position read from DEVICE memory position[0] (graph_decode.ts:276-320: the key
+ * is cached after rotation), then scores / softmax / weighted values (ops.ts:130-205,
+ * scale 1/sqrt(head_dim), grouped heads: query head h reads kv head h / (heads / kv_heads))
+ * over positions 0..position. The positions are split into chunks of `chunk`; each workgroup
+ * handles one kv head and one chunk for all the query heads of its group and writes a partial
+ * (o[head_dim], running max m, sum l) to `partials`, chunk index fastest so that a consumer
+ * reads each output's chunks as contiguous vectors (h = kv * group + g, chunks =
+ * max_context / chunk, chunks past the position write m = -inf, l = 0, o = 0):
+ *   o: partials[(h * head_dim + e) * chunks + c]
+ *   m: partials[heads * head_dim * chunks + h * chunks + c]
+ *   l: partials[(heads * head_dim + heads) * chunks + h * chunks + c]
+ * Caches are [max_context][kv_heads][head_dim] f16. q is [heads][head_dim], k and v are
+ * [kv_heads][head_dim] (the projection outputs, bias included). */
+typedef struct eg_attention_dims {
+  uint32_t heads, kv_heads, head_dim, max_context;
+  uint32_t chunk; /* positions per workgroup: 128 */
+  float theta;    /* RoPE base */
+  uint32_t pad0, pad1;
+} eg_attention_dims;
+EG_API int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                               const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
+                               const eg_attention_dims* dims);
+/* The attention output from the partials: out[h * head_dim + d] = sum_c o_c[d] e^(m_c - M) /
+ * sum_c l_c e^(m_c - M), M = max_c m_c (the reference's attn_out, [heads * head_dim]). The
+ * decoder does this inside the o projection's input stage instead (EG_INPUT_ATTENTION). */
+EG_API int eg_attention_combine(eg_context* ctx, const float* partials, float* out, const eg_attention_dims* dims);
+
+/* How a decode GEMV's input vector is produced: each workgroup computes it into LDS in its
+ * prologue, so the normalisation, the SwiGLU gate or the attention combine that precedes a
+ * projection costs no launch and no round trip through memory. */
+typedef enum eg_input_kind {
+  EG_INPUT_VECTOR = 0,    /* x as given                                                       */
+  EG_INPUT_RMSNORM = 1,   /* x * 1/sqrt(mean(x^2) + eps) * x2   (rmsnorm.wgsl, ops.ts:30-51)   */
+  EG_INPUT_SILU_MUL = 2,  /* silu(x) * x2, silu(g) = g / (1 + e^-g)   (ops.ts:207-216)       */
+  EG_INPUT_ATTENTION = 3, /* the combine of eg_attention_decode's partials in x (layout in dims) */
+} eg_input_kind;
+typedef struct eg_gemv_input {
+  int kind;
+  const float* x;  /* the vector / norm input / gate / attention partials */
+  const float* x2; /* norm weight / up; NULL otherwise */
+  float eps;       /* RMSNORM */
+  eg_attention_dims attention; /* ATTENTION: the producer's dims (heads * head_dim must equal k) */
+} eg_gemv_input;
+EG_API int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const eg_gemv_input* input);
+EG_API int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed,
+                                   const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
+                                   const eg_embedding_dims* dims, int encoding, int bits);
+
+/* The end of a decode step (Session.decodeStep bookkeeping, session.ts:347-375, kept on the
+ * device so a captured step replays without the host): position[0] += 1 and
+ * history[history_length[0]++] = token[0]. */
+EG_API int eg_decode_advance(eg_context* ctx, uint32_t* position, uint32_t* history, uint32_t* history_length,
+                             const uint32_t* token, uint32_t history_capacity);
+
+/* ---- the decode step driver (DecodeGraph + Session.decodeStep, graph_decode.ts:185-448,
+ *      session.ts:347-375) ----------------------------------------------------------------- */
+
+/* One quantized matrix: the three streams of the weight layout (zeros NULL when signed). */
+typedef struct eg_quant_matrix {
+  const uint32_t* packed;
+  const float* scales;
+  const uint32_t* zeros;
+} eg_quant_matrix;
+
+typedef struct eg_layer_desc {
+  eg_quant_matrix q, k, v, o, gate, up, down;  /* [out][in] row-major, as the checkpoint */
+  const float *q_bias, *k_bias, *v_bias;      /* nullable */
+  const float *input_norm, *post_attention_norm;
+} eg_layer_desc;
+
+typedef struct eg_model_desc {
+  uint32_t layers, hidden, heads, kv_heads, head_dim, intermediate, vocab, max_context;
+  float rms_eps, rope_theta;
+  int encoding, bits;          /* projections */
+  uint32_t block_size;
+  eg_quant_matrix embedding;   /* the tied table: gathered, and the LM head */
+  int embed_encoding, embed_bits;
+  uint32_t embed_block_size;
+  const float* final_norm;
+  const eg_layer_desc* layer;  /* `layers` entries */
+} eg_model_desc;
+
+typedef struct eg_decoder eg_decoder;
+
+/* Device buffers a decoder owns, for callers that fill or inspect them (the KV caches are
+ * [layers][max_context][kv_heads][head_dim] f16; logits f32[vocab]; token u32 = the next input
+ * id, written by each greedy step; position u32). */
+typedef struct eg_decoder_buffers {
+  uint16_t *k_cache, *v_cache;
+  float* logits;
+  float* hidden;
+  uint32_t* token;
+  uint32_t* position;
+} eg_decoder_buffers;
+
+/* Plans every launch of a step once: per layer one GEMV plan for q|k|v (RMSNorm input stage,
+ * biases), one fused attention launch, the o projection (attention-combine input stage, the
+ * residual as its bias), gate|up (RMSNorm input stage) and down (SiLU*up input stage, residual
+ * bias); then the LM head with the final norm fused and the greedy argmax. 5 launches per
+ * layer + 4, against the reference's ~19 dispatches per layer. Allocates the caches and
+ * scratch. The weights stay owned by the caller and must outlive the decoder. */
+EG_API int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** out_decoder);
+EG_API int eg_decoder_destroy(eg_decoder* decoder);
+EG_API int eg_decoder_buffers_get(eg_decoder* decoder, eg_decoder_buffers* out);
+/* Position and next input token (rows [0, position) of the caches are the history). */
+EG_API int eg_decoder_reset(eg_decoder* decoder, uint32_t position, uint32_t token);
+/* One greedy step at the current position on the current token: its argmax becomes the next
+ * token and the position advances, all on the device. token_out (host, nullable) receives the
+ * new token: the one 4-byte readback per step. Replays the captured graph if there is one. */
+EG_API int eg_decoder_step(eg_decoder* decoder, uint32_t* token_out);
+/* Captures one step as a hipGraph; later eg_decoder_step calls replay it (no host work per
+ * launch; every per-token value already lives in device memory). */
+EG_API int eg_decoder_capture(eg_decoder* decoder);
+
 /* ---- capture (one hipGraph replaces one encoded command buffer, graph_decode.ts:442) ---- */
 EG_API int eg_graph_begin(eg_context* ctx);
 EG_API int eg_graph_end(eg_context* ctx, eg_graph** out_graph);

@@ -1,0 +1,110 @@
+"""CPU restatement of one decode step of the reference's model (test infrastructure only).
+
+Composes the reference's CPU operators in decode order (graph_decode.ts:246-385 wires them;
+test/reference/ops.ts defines them): embed (ops.ts:222-233, int8 dequantization
+embedding_variants.ts:56-63), rmsNorm (:30-51), the quantized linears as linearQ4
+(quant.ts:95-111, float64 sums, f32 results, via eo_gemv_threads), rope (:87-114),
+attentionScores / softmaxRows / attentionApply for one query row (:130-205), siluMul
+(:207-216), add (:218-220) and argmax (:237-244). Activations are stored as f32 between
+operators, as the reference's Float32Arrays are; the KV cache holds f16-rounded rows when
+`cache="f16"` (the reference's f16 cache variant, cache_variants.ts:147-305) and exact f32 rows
+when `cache="f32"`.
+
+Pinning: every operator it composes is pinned on its own (tests/test_oracle.py); `attention`
+is pinned by closed forms in tests/test_decode_oracle.py (one position returns its value row,
+equal keys average the values, a dominant score selects its row, GQA grouping).
+The model is duck-typed: any object with the fields of enargeia_amd.model.HostModel.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+from . import gemv_threads, rmsnorm, rope
+
+
+def _threads() -> int:
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except AttributeError:
+        return max(1, min(16, os.cpu_count() or 1))
+
+
+def f16_array(a: np.ndarray) -> np.ndarray:
+    """Round f32 values to binary16 and back (round to nearest even, numpy's conversion)."""
+    with np.errstate(over="ignore"):  # beyond 65504 rounds to inf, as binary16 does
+        return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, heads: int, kv_heads: int, head_dim: int) -> np.ndarray:
+    """One decode row of ops.ts:130-205. q [heads*head_dim]; k, v [length][kv_heads][head_dim];
+    returns f32 [heads*head_dim]. Scores scaled by 1/sqrt(head_dim), softmax max-subtracted, in
+    float64."""
+    group = heads // kv_heads
+    qh = np.asarray(q, np.float64).reshape(heads, head_dim)
+    kk = np.asarray(k, np.float64)
+    vv = np.asarray(v, np.float64)
+    out = np.empty((heads, head_dim), np.float64)
+    scale = 1.0 / np.sqrt(head_dim)
+    for h in range(heads):
+        kv = h // group
+        s = kk[:, kv, :] @ qh[h] * scale
+        w = np.exp(s - s.max())
+        w /= w.sum()
+        out[h] = w @ vv[:, kv, :]
+    return out.reshape(-1).astype(np.float32)
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g64 = np.asarray(g, np.float64)
+    return (g64 / (1.0 + np.exp(-g64)) * np.asarray(u, np.float64)).astype(np.float32)
+
+
+class OracleDecoder:
+    """The model's decode step on the CPU, with its own KV cache."""
+
+    def __init__(self, model, max_context: int | None = None, cache: str = "f16", threads: int | None = None):
+        self.m = model
+        c = model.cfg
+        self.max_context = max_context or c.max_context
+        self.cache = cache
+        self.threads = threads or _threads()
+        shape = (c.layers, self.max_context, c.kv_heads, c.head_dim)
+        self.k = np.zeros(shape, np.float32)
+        self.v = np.zeros(shape, np.float32)
+
+    def embed(self, token: int) -> np.ndarray:
+        e = self.m.embedding  # int8 per row, two's-complement codes, 4 per u32
+        c = self.m.cfg
+        words = e.packed[token * c.hidden // 4:(token + 1) * c.hidden // 4]
+        codes = words.view(np.uint8).view(np.int8).astype(np.float32)
+        return (codes * e.scales[token]).astype(np.float32)
+
+    def linear(self, x: np.ndarray, q, bias=None) -> np.ndarray:
+        return gemv_threads(x, q, bias, self.threads)
+
+    def step(self, token: int, position: int) -> np.ndarray:
+        """Logits (f32 [vocab]) of the token at `position`; appends its K/V to the cache."""
+        c = self.m.cfg
+        h = self.embed(token)
+        for li, L in enumerate(self.m.layers):
+            xn = rmsnorm(h, L.input_norm, 1, c.hidden, c.rms_eps)
+            q = self.linear(xn, L.mats["q"], L.biases["q"])
+            k = self.linear(xn, L.mats["k"], L.biases["k"])
+            v = self.linear(xn, L.mats["v"], L.biases["v"])
+            q = rope(q, 1, c.heads, c.head_dim, c.rope_theta, position)
+            k = rope(k, 1, c.kv_heads, c.head_dim, c.rope_theta, position)
+            kr = k.reshape(c.kv_heads, c.head_dim)
+            vr = v.reshape(c.kv_heads, c.head_dim)
+            self.k[li, position] = f16_array(kr) if self.cache == "f16" else kr
+            self.v[li, position] = f16_array(vr) if self.cache == "f16" else vr
+            attn = attention(q, self.k[li, :position + 1], self.v[li, :position + 1], c.heads, c.kv_heads,
+                             c.head_dim)
+            h = (h + self.linear(attn, L.mats["o"])).astype(np.float32)
+            xn = rmsnorm(h, L.post_attention_norm, 1, c.hidden, c.rms_eps)
+            a = silu_mul(self.linear(xn, L.mats["gate"]), self.linear(xn, L.mats["up"]))
+            h = (h + self.linear(a, L.mats["down"])).astype(np.float32)
+        xf = rmsnorm(h, self.m.final_norm, 1, c.hidden, c.rms_eps)
+        return self.linear(xf, self.m.embedding)

@@ -1,0 +1,125 @@
+"""Pins the decode-step oracle's own pieces on the CPU: the attention row against closed forms,
+the f16 cache rounding, SiLU*mul, and one whole small step against a direct float64
+composition of the same operators."""
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle.decode import OracleDecoder, attention, f16_array, silu_mul
+
+
+def test_single_position_returns_its_value_row():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal(14 * 64).astype(np.float32)
+    k = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    out = attention(q, k, v, 14, 2, 64).reshape(14, 64)
+    for h in range(14):
+        np.testing.assert_array_equal(out[h], v[0, h // 7])
+
+
+def test_equal_keys_average_the_values():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal(4 * 64).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 1, 64)).astype(np.float32), 9, axis=0)
+    v = rng.standard_normal((9, 1, 64)).astype(np.float32)
+    out = attention(q, k, v, 4, 1, 64).reshape(4, 64)
+    np.testing.assert_allclose(out, np.broadcast_to(v[:, 0].mean(axis=0), (4, 64)), rtol=1e-6, atol=1e-7)
+
+
+def test_dominant_score_selects_its_row_and_heads_group_contiguously():
+    # query head h reads kv head h // (heads / kv_heads): heads 0..6 -> 0, 7..13 -> 1
+    head_dim, n = 64, 5
+    k = np.zeros((n, 2, head_dim), np.float32)
+    v = np.arange(n * 2 * head_dim, dtype=np.float32).reshape(n, 2, head_dim)
+    k[3, 0, 0] = 1.0  # kv head 0 matches position 3
+    k[1, 1, 1] = 1.0  # kv head 1 matches position 1
+    q = np.zeros((14, head_dim), np.float32)
+    q[:7, 0] = 1000.0
+    q[7:, 1] = 1000.0
+    out = attention(q.reshape(-1), k, v, 14, 2, head_dim).reshape(14, head_dim)
+    for h in range(7):
+        np.testing.assert_allclose(out[h], v[3, 0], rtol=1e-6)
+    for h in range(7, 14):
+        np.testing.assert_allclose(out[h], v[1, 1], rtol=1e-6)
+
+
+def test_f16_rounding_is_round_to_nearest_even():
+    # 1 + 2^-11 is halfway between 1 and 1 + 2^-10: ties to even gives 1
+    assert f16_array(np.array([1 + 2.0 ** -11], np.float32))[0] == 1.0
+    assert f16_array(np.array([1 + 3 * 2.0 ** -11], np.float32))[0] == 1 + 2.0 ** -9
+    assert f16_array(np.array([65520.0], np.float32))[0] == np.inf
+
+
+def test_silu_mul_closed_forms():
+    g = np.array([0.0, 1.0, -1.0, 20.0], np.float32)
+    u = np.array([3.0, 1.0, 2.0, 0.5], np.float32)
+    out = silu_mul(g, u)
+    assert out[0] == 0.0
+    np.testing.assert_allclose(out[1], 1.0 / (1.0 + np.exp(-1.0)), rtol=1e-7)
+    np.testing.assert_allclose(out[2], 2.0 * -1.0 / (1.0 + np.exp(1.0)), rtol=1e-7)
+    np.testing.assert_allclose(out[3], 0.5 * 20.0, rtol=1e-7)  # silu(x) -> x for large x
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    from enargeia_amd.model import ModelConfig, synthetic_model
+    cfg = ModelConfig(layers=2, hidden=128, heads=4, kv_heads=2, head_dim=32, intermediate=256, vocab=512,
+                      max_context=16)
+    return synthetic_model(cfg)
+
+
+def test_oracle_step_matches_a_direct_float64_composition(tiny_model):
+    """The step against a from-scratch float64 restatement over the dequantized weights: catches
+    a wrong operator order, a dropped residual or a mis-wired projection."""
+    m = tiny_model
+    c = m.cfg
+    dec = OracleDecoder(m, cache="f32")
+    tokens = [3, 77, 500, 3]
+
+    def deq(q):
+        return oracle.dequantize(oracle.QuantizedMatrix(q.rows, q.cols, q.block_size, q.bits, q.encoding,
+                                                        q.packed, q.scales, q.zeros)).astype(np.float64)
+
+    W = [{n: deq(q) for n, q in L.mats.items()} for L in m.layers]
+    E = deq(m.embedding)
+    ks = [[] for _ in range(c.layers)]
+    vs = [[] for _ in range(c.layers)]
+
+    def norm(x, w):
+        return x / np.sqrt(np.mean(x * x) + c.rms_eps) * w
+
+    def rot(x, heads, pos):
+        x = x.reshape(heads, c.head_dim).copy()
+        half = c.head_dim // 2
+        i = np.arange(half)
+        ang = pos / c.rope_theta ** (2 * i / c.head_dim)
+        a, b = x[:, :half].copy(), x[:, half:].copy()
+        x[:, :half] = a * np.cos(ang) - b * np.sin(ang)
+        x[:, half:] = b * np.cos(ang) + a * np.sin(ang)
+        return x
+
+    for pos, tok in enumerate(tokens):
+        got = dec.step(tok, pos)
+        h = E[tok].copy()
+        for li, L in enumerate(m.layers):
+            xn = norm(h, L.input_norm)
+            q = rot(W[li]["q"] @ xn + L.biases["q"], c.heads, pos)
+            k = rot(W[li]["k"] @ xn + L.biases["k"], c.kv_heads, pos)
+            v = (W[li]["v"] @ xn + L.biases["v"]).reshape(c.kv_heads, c.head_dim)
+            ks[li].append(k)
+            vs[li].append(v)
+            K, V = np.array(ks[li]), np.array(vs[li])
+            att = np.empty((c.heads, c.head_dim))
+            for hh in range(c.heads):
+                kv = hh // (c.heads // c.kv_heads)
+                s = K[:, kv] @ q[hh] / np.sqrt(c.head_dim)
+                w = np.exp(s - s.max())
+                att[hh] = (w / w.sum()) @ V[:, kv]
+            h = h + W[li]["o"] @ att.reshape(-1)
+            xn = norm(h, L.post_attention_norm)
+            g, u = W[li]["gate"] @ xn, W[li]["up"] @ xn
+            h = h + W[li]["down"] @ (g / (1 + np.exp(-g)) * u)
+        want = E @ norm(h, m.final_norm)
+        np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-5 * np.sqrt(np.mean(want ** 2)))

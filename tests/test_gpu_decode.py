@@ -1,0 +1,274 @@
+"""The decode step on the GPU against the CPU oracle: the fused attention (RoPE, f16 cache append,
+split-K partials, combine), the GEMV input stages (RMSNorm, SiLU*up, attention combine), and
+the whole decoder (reference-shaped model) step by step, eager and as a replayed hipGraph.
+
+Tolerances: attention output and input stages within 1e-5 x rms + 2e-5 relative (f32 vs the
+oracle's float64, one exp per score); decoder logits within 2e-3 x rms(logits) absolute (24
+layers of f32 GEMVs over the same int4 weights, f16 cache rows that may round one ulp apart),
+and greedy tokens identical wherever the oracle's top-2 gap exceeds 1e-2 x rms(logits)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import assert_close
+from enargeia_amd import _lib
+from enargeia_amd import kernels as K
+from enargeia_amd.model import (INPUT_ATTENTION, INPUT_RMSNORM, INPUT_SILU_MUL, Decoder, DeviceModel, GemvInput,
+                                ModelConfig, attention_dims, synthetic_model)
+from enargeia_amd.quant import normal, quantize_sym
+from oracle import rope as oracle_rope
+from oracle.decode import OracleDecoder, attention, f16_array
+
+pytestmark = pytest.mark.gpu
+
+ATT_TOL = (1e-5, 2e-5)  # x rms, relative
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def lib():
+    return _lib.load()
+
+
+# ---- fused attention ---------------------------------------------------------------------------
+
+
+def run_attention(device, cfg, pos, seed=0, chunk=128):
+    """q/k/v and a cache whose rows [0, pos) are random f16; returns (out, k_cache, v_cache, inputs)."""
+    rng = np.random.default_rng(seed)
+    H, KV, D, T = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.max_context
+    q = rng.standard_normal(H * D).astype(np.float32)
+    k = rng.standard_normal(KV * D).astype(np.float32)
+    v = rng.standard_normal(KV * D).astype(np.float32)
+    kc = np.zeros((T, KV, D), np.float16)
+    vc = np.zeros((T, KV, D), np.float16)
+    kc[:pos] = rng.standard_normal((pos, KV, D)).astype(np.float16)
+    vc[:pos] = rng.standard_normal((pos, KV, D)).astype(np.float16)
+    dims = attention_dims(cfg, chunk)
+    bufs = dict(q=device.upload(q), k=device.upload(k), v=device.upload(v), kc=device.upload(kc.view(np.uint16)),
+                vc=device.upload(vc.view(np.uint16)), pos=device.upload(np.array([pos], np.uint32)),
+                part=device.buffer(KV * (T // chunk) * (H // KV) * (D + 2) * 4), out=device.buffer(H * D * 4))
+    vp = ctypes.c_void_p
+    _lib.check(lib().eg_attention_decode(device.ctx, vp(bufs["pos"].ptr), vp(bufs["q"].ptr), vp(bufs["k"].ptr),
+                                         vp(bufs["v"].ptr), vp(bufs["kc"].ptr), vp(bufs["vc"].ptr),
+                                         vp(bufs["part"].ptr), ctypes.byref(dims)), device.ctx)
+    _lib.check(lib().eg_attention_combine(device.ctx, vp(bufs["part"].ptr), vp(bufs["out"].ptr), ctypes.byref(dims)),
+               device.ctx)
+    out = device.read_array(bufs["out"], np.float32, H * D)
+    kc_after = device.read_array(bufs["kc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
+    vc_after = device.read_array(bufs["vc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
+    for b in bufs.values():
+        b.release()
+    return out, kc_after, vc_after, (q, k, v, kc, vc)
+
+
+@pytest.mark.parametrize("chunk", [64, 128])
+@pytest.mark.parametrize("pos", [0, 1, 5, 63, 64, 127, 128, 129, 1000, 2047])
+def test_attention_decode_matches_oracle(device, pos, chunk):
+    cfg = ModelConfig()
+    out, kc, vc, (q, k, v, kc0, vc0) = run_attention(device, cfg, pos, seed=pos, chunk=chunk)
+    H, KV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+    qr = oracle_rope(q, 1, H, D, cfg.rope_theta, pos)
+    kr = f16_array(oracle_rope(k, 1, KV, D, cfg.rope_theta, pos)).reshape(KV, D)
+    vr = f16_array(v).reshape(KV, D)
+    # the appended rows (rotated key, value), f16; RoPE's double-precision angle may differ from
+    # the host's libm in the last bit, so allow one f16 ulp on the key
+    np.testing.assert_array_equal(vc[pos].astype(np.float32), vr)
+    np.testing.assert_allclose(kc[pos].astype(np.float32), kr, rtol=2 ** -10, atol=2 ** -24)
+    # earlier rows untouched, later rows untouched
+    np.testing.assert_array_equal(kc[:pos], kc0[:pos])
+    np.testing.assert_array_equal(vc[pos + 1:], vc0[pos + 1:])
+    K_all = np.concatenate([kc0[:pos].astype(np.float32), kr[None]], axis=0)
+    V_all = np.concatenate([vc0[:pos].astype(np.float32), vr[None]], axis=0)
+    want = attention(qr, K_all, V_all, H, KV, D)
+    assert_close(out, want, ATT_TOL[0] * rms(want), ATT_TOL[1], label=f"attention pos={pos} chunk={chunk}")
+
+
+def test_attention_rejects_unsupported_shapes(device):
+    dims = attention_dims(ModelConfig())
+    dims.head_dim = 80
+    buf = device.buffer(1 << 16)
+    vp = ctypes.c_void_p(buf.ptr)
+    st = lib().eg_attention_decode(device.ctx, vp, vp, vp, vp, vp, vp, vp, ctypes.byref(dims))
+    assert st == _lib.EG_ERR_INVALID and b"head_dim" in lib().eg_last_error(device.ctx)
+    buf.release()
+
+
+# ---- GEMV input stages ------------------------------------------------------------------------
+
+
+def plan_for(device, q, out, bias=None):
+    return K.GemvPlan(device, q.cols, q.block_size, [(device.upload(q.packed), device.upload(q.scales), None, bias,
+                                                      out, q.rows, 0)])
+
+
+def launch_input(device, plan, inp):
+    _lib.check(lib().eg_gemv_plan_launch_input(device.ctx, plan.handle, ctypes.byref(inp)), device.ctx)
+
+
+def reference_gemv(q, x):
+    import oracle
+    return oracle.gemv_threads(x, q, None, 4)
+
+
+def test_rmsnorm_input_stage(device):
+    k, n = 896, 4864
+    q = quantize_sym(normal(n * k, 41, 0.02), n, k, 4, 32)
+    x = normal(k, 42, 3.0).astype(np.float32)
+    w = (1.0 + normal(k, 43, 0.1)).astype(np.float32)
+    out = device.buffer(n * 4)
+    plan = plan_for(device, q, out)
+    xb, wb = device.upload(x), device.upload(w)
+    launch_input(device, plan, GemvInput(INPUT_RMSNORM, xb.ptr, wb.ptr, 1e-6))
+    got = device.read_array(out, np.float32, n)
+    xn = (x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w).astype(np.float32)
+    want = reference_gemv(q, xn)
+    assert_close(got, want, 1e-5 * rms(want), 1e-3, label="rmsnorm input")
+
+
+def test_silu_mul_input_stage(device):
+    k, n = 4864, 896
+    q = quantize_sym(normal(n * k, 51, 0.02), n, k, 4, 32)
+    g = normal(k, 52, 2.0).astype(np.float32)
+    u = normal(k, 53, 1.0).astype(np.float32)
+    out = device.buffer(n * 4)
+    plan = plan_for(device, q, out)
+    gb, ub = device.upload(g), device.upload(u)
+    launch_input(device, plan, GemvInput(INPUT_SILU_MUL, gb.ptr, ub.ptr, 0.0))
+    got = device.read_array(out, np.float32, n)
+    g64 = g.astype(np.float64)
+    want = reference_gemv(q, (g64 / (1 + np.exp(-g64)) * u).astype(np.float32))
+    assert_close(got, want, 1e-5 * rms(want), 1e-3, label="silu*up input")
+
+
+def test_attention_input_stage_equals_combine(device):
+    """The o projection's input stage must combine the partials exactly as eg_attention_combine."""
+    cfg = ModelConfig()
+    pos = 700
+    rng = np.random.default_rng(7)
+    H, KV, D, T = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.max_context
+    dims = attention_dims(cfg, 64)
+    kc = rng.standard_normal((T, KV, D)).astype(np.float16).view(np.uint16)
+    bufs = [device.upload(a) for a in (rng.standard_normal(H * D).astype(np.float32),
+                                        rng.standard_normal(KV * D).astype(np.float32),
+                                        rng.standard_normal(KV * D).astype(np.float32), kc, kc.copy(),
+                                        np.array([pos], np.uint32))]
+    part = device.buffer(KV * (T // 64) * (H // KV) * (D + 2) * 4)
+    comb = device.buffer(H * D * 4)
+    vp = ctypes.c_void_p
+    q, k, v, kcb, vcb, pb = bufs
+    _lib.check(lib().eg_attention_decode(device.ctx, vp(pb.ptr), vp(q.ptr), vp(k.ptr), vp(v.ptr), vp(kcb.ptr),
+                                         vp(vcb.ptr), vp(part.ptr), ctypes.byref(dims)), device.ctx)
+    _lib.check(lib().eg_attention_combine(device.ctx, vp(part.ptr), vp(comb.ptr), ctypes.byref(dims)), device.ctx)
+    wq = quantize_sym(normal(H * D * H * D, 61, 0.02), H * D, H * D, 4, 32)
+    out_a, out_b = device.buffer(H * D * 4), device.buffer(H * D * 4)
+    plan_a, plan_b = plan_for(device, wq, out_a), plan_for(device, wq, out_b)
+    launch_input(device, plan_a, GemvInput(INPUT_ATTENTION, part.ptr, None, 0.0, dims))
+    plan_b.launch(comb)
+    np.testing.assert_array_equal(device.read_array(out_a, np.float32, H * D),
+                                  device.read_array(out_b, np.float32, H * D))
+
+
+# ---- the decoder -------------------------------------------------------------------------------
+
+SMALL = ModelConfig(layers=2, max_context=256)
+
+
+@pytest.fixture(scope="module")
+def small_model():
+    return synthetic_model(SMALL)
+
+
+def prompt_ids(n, vocab, seed=0x5EED):
+    import oracle
+    return [int(t) for t in oracle.random_ids(n, seed, vocab)]
+
+
+def check_step(got_logits, want_logits, got_token, label):
+    scale = rms(want_logits)
+    err = np.abs(got_logits.astype(np.float64) - want_logits)
+    assert err.max() <= 2e-3 * scale, f"{label}: logits max error {err.max():.3e} vs rms {scale:.3e}"
+    order = np.argsort(want_logits)
+    gap = float(want_logits[order[-1]] - want_logits[order[-2]])
+    if gap > 1e-2 * scale:
+        assert got_token == int(order[-1]), f"{label}: token {got_token} vs oracle {int(order[-1])} (gap {gap:.3e})"
+    return gap
+
+
+def test_decoder_matches_oracle_prompt_then_greedy(device, small_model):
+    m = small_model
+    dm = DeviceModel(device, m)
+    dec = Decoder(dm)
+    ora = OracleDecoder(m, max_context=SMALL.max_context)
+    prompt = prompt_ids(32, SMALL.vocab)
+    checked = 0
+    try:
+        for pos, tok in enumerate(prompt):
+            dec.reset(pos, tok)
+            got_token = dec.step()
+            want = ora.step(tok, pos)
+            check_step(dec.logits(), want, got_token, f"prompt pos {pos}")
+            checked += 1
+        tok = got_token
+        for pos in range(len(prompt), len(prompt) + 16):
+            assert dec.position() == pos
+            got_token = dec.step()  # the device feeds its own argmax back
+            want = ora.step(tok, pos)  # the oracle follows the device's tokens
+            check_step(dec.logits(), want, got_token, f"greedy pos {pos}")
+            tok = got_token
+            checked += 1
+    finally:
+        dec.close()
+        dm.release()
+    assert checked == 48
+
+
+def test_decoder_graph_replay_equals_eager(device, small_model):
+    dm = DeviceModel(device, small_model)
+    eager, graph = Decoder(dm), Decoder(dm)
+    try:
+        eager.reset(0, 17)
+        graph.reset(0, 17)
+        graph.capture()
+        for step in range(8):
+            a, b = eager.step(), graph.step()
+            assert a == b, f"step {step}: eager {a} graph {b}"
+            np.testing.assert_array_equal(eager.logits(), graph.logits())
+        assert graph.position() == 8
+    finally:
+        eager.close()
+        graph.close()
+        dm.release()
+
+
+def test_decoder_full_model_first_steps(device):
+    cfg = ModelConfig(max_context=256)
+    m = synthetic_model(cfg)
+    dm = DeviceModel(device, m)
+    dec = Decoder(dm)
+    ora = OracleDecoder(m, max_context=cfg.max_context)
+    try:
+        for pos, tok in enumerate(prompt_ids(4, cfg.vocab, 0x1234)):
+            dec.reset(pos, tok)
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got_token, f"24-layer pos {pos}")
+    finally:
+        dec.close()
+        dm.release()
+
+
+def test_decoder_rejects_bad_reset(device, small_model):
+    dm = DeviceModel(device, small_model)
+    dec = Decoder(dm)
+    try:
+        with pytest.raises(_lib.EgRangeError):
+            dec.reset(SMALL.max_context, 0)
+        with pytest.raises(_lib.EgError):
+            dec.reset(0, SMALL.vocab)
+    finally:
+        dec.close()
+        dm.release()
