@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_argmax": (_i, [_vp, _vp, _vp, _vp]),
     "eg_sample": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "eg_embed_gather": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
-    "eg_attention_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "eg_attention_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "eg_attention_combine": (_i, [_vp, _vp, _vp, _vp]),
     "eg_gemv_plan_launch_input": (_i, [_vp, _vp, _vp]),
     "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),

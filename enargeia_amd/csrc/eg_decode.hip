@@ -68,41 +68,60 @@ __device__ __forceinline__ void rope_apply(float* v, uint32_t i, const double2* 
   v[i + D / 2] = (float)(b * cs[i].x + a * cs[i].y);
 }
 
-// One workgroup: kv head kv = blockIdx.y / HSPLIT and the HSPLIT-th share of its query heads,
-// positions [j0, j0 + CHUNK) (blockIdx.x). Splitting the group's heads over HSPLIT workgroups
-// doubles the parallelism of a launch that otherwise has only chunks x kv_heads workgroups; the
-// K/V rows they share come from L2.
-template <int D, int CHUNK, int GMAX, int HSPLIT>
-__global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32_t* position, const float* q,
-                                                                    const float* k, const float* v,
-                                                                    uint16_t* k_cache, uint16_t* v_cache,
-                                                                    float* partials, eg_attention_dims d) {
-  const uint32_t pos = position[0];
-  const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
-  const uint32_t c = blockIdx.x;
-  const uint32_t chunks = gridDim.x;
-  const uint32_t group = d.heads / d.kv_heads;
-  const uint32_t share = (group + HSPLIT - 1) / HSPLIT;
-  const uint32_t gb = min(group, hs * share), ng = min(group, gb + share) - gb;  // heads [gb, gb + ng)
-  const uint32_t j0 = c * CHUNK;
-  const uint32_t tid = threadIdx.x;
-  // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
-  const uint32_t h0 = kv * group + gb;
-  float* po = partials + (size_t)h0 * D * chunks + c;
-  float* pm = partials + (size_t)d.heads * D * chunks + (size_t)h0 * chunks + c;
-  float* pl = pm + (size_t)d.heads * chunks;
-  if (ng == 0) return;
+constexpr uint32_t kMaxCombine = 1024;  // heads x chunks the one-workgroup combine holds in LDS
 
-  // Past the live history (or, defensively, a position beyond the cache): an empty partial.
-  // No cache row is written unless pos < max_context.
-  if (j0 > pos || pos >= d.max_context) {
-    for (uint32_t i = tid; i < ng * D; i += blockDim.x) po[(size_t)i * chunks] = 0.f;
-    if (tid < ng) {
-      pm[(size_t)tid * chunks] = -INFINITY;
-      pl[(size_t)tid * chunks] = 0.f;
-    }
-    return;
+// The whole attention output from the chunk-fastest partials, by one workgroup: per (head,
+// chunk) statistics into LDS, each chunk's weight e^(m_c - M) / L, then every output's weighted
+// sum of its chunks' o values read as 16-byte vectors. Same operations in the same order as
+// egd::attention_combine_at (so the same bits).
+__device__ void combine_all(const float* partials, float* out, uint32_t heads, uint32_t D, uint32_t chunks) {
+  __shared__ float mval[kMaxCombine], lval[kMaxCombine], wts[kMaxCombine];
+  const uint32_t tid = threadIdx.x, hcs = heads * chunks, n = heads * D;
+  const float* m = partials + (size_t)heads * D * chunks;
+  const float* l = m + hcs;
+  for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
+    mval[hc] = m[hc];
+    lval[hc] = l[hc];
   }
+  __syncthreads();
+  for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
+    const uint32_t b = (hc / chunks) * chunks;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, mval[b + c]);
+    float L = 0.f;
+    for (uint32_t c = 0; c < chunks; c++) L = fmaf(lval[b + c], expf(mval[b + c] - M), L);
+    wts[hc] = expf(mval[hc] - M) / L;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += blockDim.x) {
+    const float* o = partials + (size_t)i * chunks;
+    const float* w = wts + (i / D) * chunks;
+    float acc = 0.f;
+    if ((chunks & 3u) == 0) {
+      const float4* o4 = reinterpret_cast<const float4*>(o);
+#pragma unroll 8
+      for (uint32_t q = 0; q < chunks / 4; q++) {
+        const float4 v = o4[q];
+        acc = fmaf(v.x, w[4 * q + 0], acc);
+        acc = fmaf(v.y, w[4 * q + 1], acc);
+        acc = fmaf(v.z, w[4 * q + 2], acc);
+        acc = fmaf(v.w, w[4 * q + 3], acc);
+      }
+    } else {
+      for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], w[c], acc);
+    }
+    out[i] = acc;
+  }
+}
+
+// The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
+// statistics and the partial o, written to po/pm/pl.
+template <int D, int CHUNK, int GMAX>
+__device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, uint32_t hs, uint32_t ng, uint32_t h0,
+                                       uint32_t chunks, const float* q, const float* k, const float* v,
+                                       uint16_t* k_cache, uint16_t* v_cache, float* po, float* pm, float* pl,
+                                       const eg_attention_dims& d) {
+  const uint32_t tid = threadIdx.x;
   const uint32_t live = min((uint32_t)CHUNK, pos + 1 - j0);
 
   __shared__ float qs[GMAX][D];          // rotated, pre-scaled queries of this workgroup's heads
@@ -204,6 +223,61 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
   }
 }
 
+// One workgroup: kv head kv = blockIdx.y / HSPLIT and the HSPLIT-th share of its query heads,
+// positions [j0, j0 + CHUNK) (blockIdx.x). Splitting the group's heads over HSPLIT workgroups
+// doubles the parallelism of a launch that otherwise has only chunks x kv_heads workgroups; the
+// K/V rows they share come from L2.
+template <int D, int CHUNK, int GMAX, int HSPLIT>
+__global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32_t* position, const float* q,
+                                                                    const float* k, const float* v,
+                                                                    uint16_t* k_cache, uint16_t* v_cache,
+                                                                    float* partials, uint32_t* counter, float* out,
+                                                                    eg_attention_dims d) {
+  const uint32_t pos = position[0];
+  const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
+  const uint32_t c = blockIdx.x;
+  const uint32_t chunks = gridDim.x;
+  const uint32_t group = d.heads / d.kv_heads;
+  const uint32_t share = (group + HSPLIT - 1) / HSPLIT;
+  const uint32_t gb = min(group, hs * share), ng = min(group, gb + share) - gb;  // heads [gb, gb + ng)
+  const uint32_t j0 = c * CHUNK;
+  const uint32_t tid = threadIdx.x;
+  // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
+  const uint32_t h0 = kv * group + gb;
+  float* po = partials + (size_t)h0 * D * chunks + c;
+  float* pm = partials + (size_t)d.heads * D * chunks + (size_t)h0 * chunks + c;
+  float* pl = pm + (size_t)d.heads * chunks;
+  // Past the live history (or, defensively, a position beyond the cache): an empty partial.
+  // No cache row is written unless pos < max_context. Every workgroup still reaches the
+  // arrival count below.
+  const bool empty = j0 > pos || pos >= d.max_context;
+  if (ng > 0 && empty) {
+    for (uint32_t i = tid; i < ng * D; i += blockDim.x) po[(size_t)i * chunks] = 0.f;
+    if (tid < ng) {
+      pm[(size_t)tid * chunks] = -INFINITY;
+      pl[(size_t)tid * chunks] = 0.f;
+    }
+  }
+  if (ng > 0 && !empty) attend<D, CHUNK, GMAX>(pos, j0, kv, hs, ng, h0, chunks, q, k, v, k_cache, v_cache, po, pm, pl, d);
+
+  // The combine, once, by the last workgroup to arrive: the fence releases this workgroup's
+  // partials device-wide before it counts itself; the last one's fence acquires everyone's.
+  if (out) {
+    __shared__ uint32_t last;
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      last = atomicAdd(counter, 1u) == gridDim.x * gridDim.y - 1;
+    }
+    __syncthreads();
+    if (last) {
+      __threadfence();
+      combine_all(partials, out, d.heads, D, chunks);
+      if (tid == 0) *counter = 0;  // ready for the next launch
+    }
+  }
+}
+
 // ---- combine ---------------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void attention_combine_kernel(const float* partials, float* out,
@@ -234,8 +308,11 @@ int check_attention(eg_context* ctx, const char* op, const eg_attention_dims* d)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: %u heads do not group over %u kv heads", op, d->heads, d->kv_heads);
   if (d->heads / d->kv_heads > 8)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: %u query heads per kv head (at most 8)", op, d->heads / d->kv_heads);
-  if ((uint64_t)d->kv_heads * 2 > 65535)
+  if ((uint64_t)d->kv_heads * 4 > 65535)
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u kv heads exceed the grid", op, d->kv_heads);
+  if ((uint64_t)d->heads * (d->max_context / d->chunk) > kMaxCombine)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads x %u chunks exceed the combine's %u", op, d->heads,
+                    d->max_context / d->chunk, kMaxCombine);
   if (d->chunk != 64 && d->chunk != 128)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: chunk %u (64 or 128 are supported)", op, d->chunk);
   if (d->max_context == 0 || d->max_context % d->chunk != 0)
@@ -270,23 +347,28 @@ int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* pack
 }
 
 int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k, const float* v,
-                        uint16_t* k_cache, uint16_t* v_cache, float* partials, const eg_attention_dims* dims) {
+                        uint16_t* k_cache, uint16_t* v_cache, float* partials, uint32_t* counter, float* out,
+                        const eg_attention_dims* dims) {
   const char* op = "attention_decode";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!position || !q || !k || !v || !k_cache || !v_cache || !partials)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if ((counter == nullptr) != (out == nullptr))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: counter and out go together", op);
   if ((reinterpret_cast<uintptr_t>(k_cache) & 15u) || (reinterpret_cast<uintptr_t>(v_cache) & 15u))
     return eg::fail(ctx, EG_ERR_INVALID, "%s: caches must be 16-byte aligned", op);
   int st = check_attention(ctx, op, dims);
   if (st != EG_OK) return st;
-  constexpr int kSplit = 2;
-  const dim3 grid(dims->max_context / dims->chunk, dims->kv_heads * kSplit);
-  if (dims->chunk == 64)
-    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, kSplit>), grid, dim3(kThreads), 0, ctx->stream, position,
-                       q, k, v, k_cache, v_cache, partials, *dims);
-  else
-    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 4, kSplit>), grid, dim3(kThreads), 0, ctx->stream, position,
-                       q, k, v, k_cache, v_cache, partials, *dims);
+  // chunk 64: two workgroups share a kv group's query heads; chunk 128: four do
+  if (dims->chunk == 64) {
+    const dim3 grid(dims->max_context / 64, dims->kv_heads * 2);
+    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
+                       v, k_cache, v_cache, partials, counter, out, *dims);
+  } else {
+    const dim3 grid(dims->max_context / 128, dims->kv_heads * 4);
+    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
+                       v, k_cache, v_cache, partials, counter, out, *dims);
+  }
   return eg::check_launch(ctx, op);
 }
 

@@ -219,7 +219,11 @@ EG_API int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_
  *   m: partials[heads * head_dim * chunks + h * chunks + c]
  *   l: partials[(heads * head_dim + heads) * chunks + h * chunks + c]
  * Caches are [max_context][kv_heads][head_dim] f16. q is [heads][head_dim], k and v are
- * [kv_heads][head_dim] (the projection outputs, bias included). */
+ * [kv_heads][head_dim] (the projection outputs, bias included).
+ * With `out` (and `counter`, a device u32 that is 0 before the first launch and that every
+ * launch leaves at 0), the last workgroup to finish also combines the partials into
+ * out[heads * head_dim], the reference's attn_out (as eg_attention_combine would, same bits).
+ * Launches that share a counter must not overlap. */
 typedef struct eg_attention_dims {
   uint32_t heads, kv_heads, head_dim, max_context;
   uint32_t chunk; /* positions per workgroup: 128 */
@@ -228,7 +232,7 @@ typedef struct eg_attention_dims {
 } eg_attention_dims;
 EG_API int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
                                const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
-                               const eg_attention_dims* dims);
+                               uint32_t* counter, float* out, const eg_attention_dims* dims);
 /* The attention output from the partials: out[h * head_dim + d] = sum_c o_c[d] e^(m_c - M) /
  * sum_c l_c e^(m_c - M), M = max_c m_c (the reference's attn_out, [heads * head_dim]). The
  * decoder does this inside the o projection's input stage instead (EG_INPUT_ATTENTION). */

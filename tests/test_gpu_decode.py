@@ -51,14 +51,20 @@ def run_attention(device, cfg, pos, seed=0, chunk=128):
     dims = attention_dims(cfg, chunk)
     bufs = dict(q=device.upload(q), k=device.upload(k), v=device.upload(v), kc=device.upload(kc.view(np.uint16)),
                 vc=device.upload(vc.view(np.uint16)), pos=device.upload(np.array([pos], np.uint32)),
-                part=device.buffer(KV * (T // chunk) * (H // KV) * (D + 2) * 4), out=device.buffer(H * D * 4))
+                part=device.buffer(KV * (T // chunk) * (H // KV) * (D + 2) * 4), out=device.buffer(H * D * 4),
+                fused=device.buffer(H * D * 4), counter=device.upload(np.zeros(1, np.uint32)))
     vp = ctypes.c_void_p
     _lib.check(lib().eg_attention_decode(device.ctx, vp(bufs["pos"].ptr), vp(bufs["q"].ptr), vp(bufs["k"].ptr),
                                          vp(bufs["v"].ptr), vp(bufs["kc"].ptr), vp(bufs["vc"].ptr),
-                                         vp(bufs["part"].ptr), ctypes.byref(dims)), device.ctx)
+                                         vp(bufs["part"].ptr), vp(bufs["counter"].ptr), vp(bufs["fused"].ptr),
+                                         ctypes.byref(dims)), device.ctx)
     _lib.check(lib().eg_attention_combine(device.ctx, vp(bufs["part"].ptr), vp(bufs["out"].ptr), ctypes.byref(dims)),
                device.ctx)
     out = device.read_array(bufs["out"], np.float32, H * D)
+    # the last workgroup's combine equals the standalone combine bit for bit, and leaves the
+    # counter at 0 for the next launch
+    np.testing.assert_array_equal(device.read_array(bufs["fused"], np.float32, H * D), out)
+    assert device.read_array(bufs["counter"], np.uint32, 1)[0] == 0
     kc_after = device.read_array(bufs["kc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
     vc_after = device.read_array(bufs["vc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
     for b in bufs.values():
@@ -93,7 +99,7 @@ def test_attention_rejects_unsupported_shapes(device):
     dims.head_dim = 80
     buf = device.buffer(1 << 16)
     vp = ctypes.c_void_p(buf.ptr)
-    st = lib().eg_attention_decode(device.ctx, vp, vp, vp, vp, vp, vp, vp, ctypes.byref(dims))
+    st = lib().eg_attention_decode(device.ctx, vp, vp, vp, vp, vp, vp, vp, None, None, ctypes.byref(dims))
     assert st == _lib.EG_ERR_INVALID and b"head_dim" in lib().eg_last_error(device.ctx)
     buf.release()
 
@@ -162,7 +168,7 @@ def test_attention_input_stage_equals_combine(device):
     vp = ctypes.c_void_p
     q, k, v, kcb, vcb, pb = bufs
     _lib.check(lib().eg_attention_decode(device.ctx, vp(pb.ptr), vp(q.ptr), vp(k.ptr), vp(v.ptr), vp(kcb.ptr),
-                                         vp(vcb.ptr), vp(part.ptr), ctypes.byref(dims)), device.ctx)
+                                         vp(vcb.ptr), vp(part.ptr), None, None, ctypes.byref(dims)), device.ctx)
     _lib.check(lib().eg_attention_combine(device.ctx, vp(part.ptr), vp(comb.ptr), ctypes.byref(dims)), device.ctx)
     wq = quantize_sym(normal(H * D * H * D, 61, 0.02), H * D, H * D, 4, 32)
     out_a, out_b = device.buffer(H * D * 4), device.buffer(H * D * 4)
