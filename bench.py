@@ -101,6 +101,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-profile", action="store_true",
+                    help="only the config-4 decode steps, launched eagerly (for rocprofv3 kernel statistics of a "
+                         "decode step; graph capture is left out of profiled runs)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel and two calibration kernels of known size "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -115,6 +118,12 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe()
+    if args.decode_profile:
+        dev = K.Device(0)
+        ev = HipEvents()
+        print(json.dumps(decode_throughput(dev, ev, dev.stream, args, modes=("eager",))), flush=True)
+        dev.close()
+        return 0
     t0 = time.time()
     mats = make_projection_set()
     log(f"quantized {len(mats)} projection matrices in {time.time() - t0:.1f}s")
@@ -349,7 +358,7 @@ def main() -> int:
 DECODE_STEPS = 128
 
 
-def decode_throughput(dev, ev, stream, args) -> dict:
+def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     """the Qwen2.5-0.5B-shaped model (synthetic weights, int4 g32 projections,
     int8 tied head, f16 KV cache), cache filled to 2048 - 128 positions (random f16 rows, the
     reference's prime-then-decode method, decode.test.ts:97-118), then 128 greedy steps to
@@ -375,7 +384,7 @@ def decode_throughput(dev, ev, stream, args) -> dict:
     first = 785  # the first greedy id of the reference's fixture prompt; any id works
     result = {"config": "BASELINE config 4: Qwen2.5-0.5B shape, 24 layers, int4 g32 + int8 tied head, f16 KV",
               "context": cfg.max_context, "steps": DECODE_STEPS, "launches_per_token": 5 * cfg.layers + 4}
-    for mode in ("eager", "graph"):
+    for mode in modes:
         if mode == "graph":
             dec.capture()
         # warm-up steps end at the prime point, then the timed steps run prime .. 2047
@@ -402,7 +411,7 @@ def decode_throughput(dev, ev, stream, args) -> dict:
         result[f"{mode}_device_tok_s"] = round(DECODE_STEPS / (ev.ms(a, b) * 1e-3), 1)
         log(f"decode ({mode}): {result[f'{mode}_tok_s']} tok/s with a readback per token, "
             f"{result[f'{mode}_device_tok_s']} tok/s device-chained; last token {tokens[-1]}")
-    best = max(("eager", "graph"), key=lambda m: result[f"{m}_tok_s"])
+    best = max(modes, key=lambda m: result[f"{m}_tok_s"])
     result["tok_s"] = result[f"{best}_tok_s"]
     result["launch"] = best
     step_bytes = (STEP_BYTES + LM_HEAD_BYTES
