@@ -12,6 +12,8 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "enargeia_hip.h"
 
@@ -41,6 +43,35 @@ bool throw_status(napi_env env, eg_context* ctx, int st) {
 
 void throw_type(napi_env env, const std::string& what) { napi_throw_type_error(env, "EG_ERR_INVALID", what.c_str()); }
 
+struct DecoderHandle;
+
+// One type tag per kind of handle.
+template <typename T>
+const napi_type_tag& tag_of();
+template <>
+const napi_type_tag& tag_of<eg_context>() {
+  static const napi_type_tag t{0x45474354584e4150ull, 0x0000000000000001ull};
+  return t;
+}
+template <>
+const napi_type_tag& tag_of<eg_graph>() {
+  static const napi_type_tag t{0x45474354584e4150ull, 0x0000000000000002ull};
+  return t;
+}
+template <>
+const napi_type_tag& tag_of<DecoderHandle>() {
+  static const napi_type_tag t{0x45474354584e4150ull, 0x0000000000000003ull};
+  return t;
+}
+
+template <typename T>
+napi_value make_handle(napi_env env, T* p, napi_finalize fin) {
+  napi_value ext;
+  napi_create_external(env, p, fin, nullptr, &ext);
+  napi_type_tag_object(env, ext, &tag_of<T>());
+  return ext;
+}
+
 struct Args {
   napi_env env;
   size_t argc = 12;
@@ -57,14 +88,17 @@ struct Args {
     }
   }
 
-  // A context or graph handle: an External created by this addon.
+  // A context, graph or decoder handle: an External this addon created and type-tagged, so a
+  // handle of one kind passed where another is expected is a TypeError, not a crash.
   template <typename T>
   T* handle(size_t i, const char* what) {
     if (!ok) return nullptr;
     napi_valuetype t;
     napi_typeof(env, argv[i], &t);
     void* p = nullptr;
-    if (t != napi_external || napi_get_value_external(env, argv[i], &p) != napi_ok) {
+    bool tagged = false;
+    if (t == napi_external) napi_check_object_type_tag(env, argv[i], &tag_of<T>(), &tagged);
+    if (t != napi_external || !tagged || napi_get_value_external(env, argv[i], &p) != napi_ok) {
       throw_type(env, std::string(fn) + ": argument " + std::to_string(i) + " is not a " + what);
       ok = false;
       return nullptr;
@@ -195,9 +229,7 @@ napi_value Create(napi_env env, napi_callback_info info) {
   if (!a.ok) return nullptr;
   eg_context* ctx = nullptr;
   if (throw_status(env, nullptr, eg_create(device, &ctx))) return nullptr;
-  napi_value ext;
-  napi_create_external(env, ctx, finalize_ctx, nullptr, &ext);
-  return ext;
+  return make_handle(env, ctx, finalize_ctx);
 }
 
 napi_value Destroy(napi_env env, napi_callback_info info) {
@@ -376,6 +408,211 @@ napi_value Sample(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- the decoder --------------------------------------------------------------------------------
+
+// What the External of a decoder carries: the decoder and its context (for error messages).
+struct DecoderHandle {
+  eg_decoder* dec;
+  eg_context* ctx;
+};
+
+bool get_prop(napi_env env, napi_value obj, const char* name, napi_value* out) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok || !has) {
+    napi_throw_type_error(env, "EG_ERR_INVALID", (std::string("decoderCreate: missing ") + name).c_str());
+    return false;
+  }
+  return napi_get_named_property(env, obj, name, out) == napi_ok;
+}
+
+bool get_u32(napi_env env, napi_value obj, const char* name, uint32_t* out) {
+  napi_value v;
+  if (!get_prop(env, obj, name, &v)) return false;
+  if (napi_get_value_uint32(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, "EG_ERR_INVALID", (std::string("decoderCreate: ") + name + " is not a number").c_str());
+    return false;
+  }
+  return true;
+}
+
+bool get_f32(napi_env env, napi_value obj, const char* name, float* out) {
+  napi_value v;
+  double d = 0;
+  if (!get_prop(env, obj, name, &v)) return false;
+  if (napi_get_value_double(env, v, &d) != napi_ok) {
+    napi_throw_type_error(env, "EG_ERR_INVALID", (std::string("decoderCreate: ") + name + " is not a number").c_str());
+    return false;
+  }
+  *out = (float)d;
+  return true;
+}
+
+// A device pointer property: a safe integer, or null/undefined (NULL).
+bool get_ptr(napi_env env, napi_value obj, const char* name, const void** out) {
+  bool has = false;
+  *out = nullptr;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok || !has) return true;
+  napi_value v;
+  napi_get_named_property(env, obj, name, &v);
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_null || t == napi_undefined) return true;
+  double d = 0;
+  if (t != napi_number || napi_get_value_double(env, v, &d) != napi_ok || d < 0 || d > 9007199254740991.0 ||
+      d != (double)(int64_t)d) {
+    napi_throw_type_error(env, "EG_ERR_INVALID", (std::string("decoderCreate: ") + name + " is not a device pointer").c_str());
+    return false;
+  }
+  *out = reinterpret_cast<const void*>(static_cast<uintptr_t>(d));
+  return true;
+}
+
+bool get_matrix(napi_env env, napi_value obj, const char* name, eg_quant_matrix* m) {
+  napi_value v;
+  if (!get_prop(env, obj, name, &v)) return false;
+  const void *p = nullptr, *s = nullptr, *z = nullptr;
+  if (!get_ptr(env, v, "packed", &p) || !get_ptr(env, v, "scales", &s) || !get_ptr(env, v, "zeros", &z)) return false;
+  m->packed = static_cast<const uint32_t*>(p);
+  m->scales = static_cast<const float*>(s);
+  m->zeros = static_cast<const uint32_t*>(z);
+  return true;
+}
+
+void finalize_decoder(napi_env, void* data, void*) { delete static_cast<DecoderHandle*>(data); }
+
+// decoderCreate(ctx, desc): desc mirrors eg_model_desc with camelCase names and `layer` an array.
+napi_value DecoderCreate(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderCreate", 2);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  if (!a.ok) return nullptr;
+  napi_value d = a.argv[1];
+  eg_model_desc m{};
+  int enc = 0, bits = 0, eenc = 0, ebits = 0;
+  uint32_t u = 0;
+  const void* final_norm = nullptr;
+  if (!get_u32(env, d, "layers", &m.layers) || !get_u32(env, d, "hidden", &m.hidden) ||
+      !get_u32(env, d, "heads", &m.heads) || !get_u32(env, d, "kvHeads", &m.kv_heads) ||
+      !get_u32(env, d, "headDim", &m.head_dim) || !get_u32(env, d, "intermediate", &m.intermediate) ||
+      !get_u32(env, d, "vocab", &m.vocab) || !get_u32(env, d, "maxContext", &m.max_context) ||
+      !get_f32(env, d, "rmsEps", &m.rms_eps) || !get_f32(env, d, "ropeTheta", &m.rope_theta) ||
+      !get_u32(env, d, "encoding", &u))
+    return nullptr;
+  enc = (int)u;
+  if (!get_u32(env, d, "bits", &u)) return nullptr;
+  bits = (int)u;
+  if (!get_u32(env, d, "blockSize", &m.block_size) || !get_matrix(env, d, "embedding", &m.embedding) ||
+      !get_u32(env, d, "embedEncoding", &u))
+    return nullptr;
+  eenc = (int)u;
+  if (!get_u32(env, d, "embedBits", &u)) return nullptr;
+  ebits = (int)u;
+  if (!get_u32(env, d, "embedBlockSize", &m.embed_block_size) || !get_ptr(env, d, "finalNorm", &final_norm))
+    return nullptr;
+  m.encoding = enc;
+  m.bits = bits;
+  m.embed_encoding = eenc;
+  m.embed_bits = ebits;
+  m.final_norm = static_cast<const float*>(final_norm);
+  napi_value arr;
+  if (!get_prop(env, d, "layer", &arr)) return nullptr;
+  uint32_t n = 0;
+  bool is_array = false;
+  napi_is_array(env, arr, &is_array);
+  if (!is_array || napi_get_array_length(env, arr, &n) != napi_ok || n != m.layers) {
+    napi_throw_type_error(env, "EG_ERR_INVALID", "decoderCreate: layer must be an array of `layers` entries");
+    return nullptr;
+  }
+  std::vector<eg_layer_desc> layers(n);
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value L;
+    napi_get_element(env, arr, i, &L);
+    eg_layer_desc& l = layers[i];
+    const void *qb = nullptr, *kb = nullptr, *vb = nullptr, *in = nullptr, *pn = nullptr;
+    if (!get_matrix(env, L, "q", &l.q) || !get_matrix(env, L, "k", &l.k) || !get_matrix(env, L, "v", &l.v) ||
+        !get_matrix(env, L, "o", &l.o) || !get_matrix(env, L, "gate", &l.gate) || !get_matrix(env, L, "up", &l.up) ||
+        !get_matrix(env, L, "down", &l.down) || !get_ptr(env, L, "qBias", &qb) || !get_ptr(env, L, "kBias", &kb) ||
+        !get_ptr(env, L, "vBias", &vb) || !get_ptr(env, L, "inputNorm", &in) ||
+        !get_ptr(env, L, "postAttentionNorm", &pn))
+      return nullptr;
+    l.q_bias = static_cast<const float*>(qb);
+    l.k_bias = static_cast<const float*>(kb);
+    l.v_bias = static_cast<const float*>(vb);
+    l.input_norm = static_cast<const float*>(in);
+    l.post_attention_norm = static_cast<const float*>(pn);
+  }
+  m.layer = layers.data();
+  eg_decoder* dec = nullptr;
+  if (throw_status(env, ctx, eg_decoder_create(ctx, &m, &dec))) return nullptr;
+  return make_handle(env, new DecoderHandle{dec, ctx}, finalize_decoder);
+}
+
+napi_value DecoderReset(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderReset", 3);
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  uint64_t position = a.u64(1), token = a.u64(2);
+  if (!a.ok) return nullptr;
+  if (!h->dec) {
+    napi_throw_error(env, "EG_ERR_STATE", "decoderReset: the decoder was destroyed");
+    return nullptr;
+  }
+  if (throw_status(env, h->ctx, eg_decoder_reset(h->dec, (uint32_t)position, (uint32_t)token))) return nullptr;
+  return undefined(env);
+}
+
+// decoderStep(dec, readToken) -> the new token id (readToken) or undefined
+napi_value DecoderStep(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderStep", 2);
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  if (!a.ok) return nullptr;
+  bool read = false;
+  napi_get_value_bool(env, a.argv[1], &read);
+  if (!h->dec) {
+    napi_throw_error(env, "EG_ERR_STATE", "decoderStep: the decoder was destroyed");
+    return nullptr;
+  }
+  uint32_t token = 0;
+  if (throw_status(env, h->ctx, eg_decoder_step(h->dec, read ? &token : nullptr))) return nullptr;
+  return read ? number(env, token) : undefined(env);
+}
+
+napi_value DecoderCapture(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderCapture", 1);
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  if (!a.ok) return nullptr;
+  if (!h->dec) {
+    napi_throw_error(env, "EG_ERR_STATE", "decoderCapture: the decoder was destroyed");
+    return nullptr;
+  }
+  if (throw_status(env, h->ctx, eg_decoder_capture(h->dec))) return nullptr;
+  return undefined(env);
+}
+
+// decoderBuffers(dec) -> {kCache, vCache, logits, hidden, token, position} device pointers
+napi_value DecoderBuffers(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderBuffers", 1);
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  if (!a.ok) return nullptr;
+  eg_decoder_buffers b{};
+  if (!h->dec || throw_status(env, h->ctx, eg_decoder_buffers_get(h->dec, &b))) return nullptr;
+  napi_value obj;
+  napi_create_object(env, &obj);
+  const std::pair<const char*, const void*> fields[] = {{"kCache", b.k_cache}, {"vCache", b.v_cache},
+                                                        {"logits", b.logits}, {"hidden", b.hidden},
+                                                        {"token", b.token}, {"position", b.position}};
+  for (const auto& f : fields)
+    napi_set_named_property(env, obj, f.first, number(env, (double)reinterpret_cast<uintptr_t>(f.second)));
+  return obj;
+}
+
+napi_value DecoderDestroy(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderDestroy", 1);
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  if (!a.ok) return nullptr;
+  if (h->dec) eg_decoder_destroy(h->dec);
+  h->dec = nullptr;
+  return undefined(env);
+}
+
 // ---- graphs ----------------------------------------------------------------------------------
 
 napi_value GraphBegin(napi_env env, napi_callback_info info) {
@@ -392,9 +629,7 @@ napi_value GraphEnd(napi_env env, napi_callback_info info) {
   if (!a.ok) return nullptr;
   eg_graph* g = nullptr;
   if (throw_status(env, ctx, eg_graph_end(ctx, &g))) return nullptr;
-  napi_value ext;
-  napi_create_external(env, g, nullptr, nullptr, &ext);
-  return ext;
+  return make_handle<eg_graph>(env, g, nullptr);
 }
 
 napi_value GraphLaunch(napi_env env, napi_callback_info info) {
@@ -432,6 +667,12 @@ napi_value Init(napi_env env, napi_value exports) {
       {"lmHeadArgmax", nullptr, LmHeadArgmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderCreate", nullptr, DecoderCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderReset", nullptr, DecoderReset, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderStep", nullptr, DecoderStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderCapture", nullptr, DecoderCapture, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderBuffers", nullptr, DecoderBuffers, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderDestroy", nullptr, DecoderDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphBegin", nullptr, GraphBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphEnd", nullptr, GraphEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphLaunch", nullptr, GraphLaunch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

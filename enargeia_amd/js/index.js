@@ -2,6 +2,7 @@
 // projection path, over HIP on MI355X through the N-API addon (eg_napi.node).
 'use strict';
 
-module.exports = Object.assign({}, require('./gpu.js'), require('./kernel.js'), require('./ops.js'), {
+module.exports = Object.assign({}, require('./gpu.js'), require('./kernel.js'), require('./ops.js'),
+  require('./decoder.js'), {
   native: require('./native.js'),
 });

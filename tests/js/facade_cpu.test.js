@@ -12,7 +12,8 @@ const eg = require(path.join(__dirname, '..', '..', 'enargeia_amd', 'js', 'index
 
 const EXPORTS = ['abiVersion', 'create', 'destroy', 'sync', 'getStream', 'bufAlloc', 'bufFree', 'bufWrite', 'bufRead',
   'bufZero', 'matmulQ4Decode', 'matmulQ4Prefill', 'lmHead', 'lmHeadArgmax', 'argmax', 'sample', 'graphBegin',
-  'graphEnd', 'graphLaunch', 'graphDestroy'];
+  'graphEnd', 'graphLaunch', 'graphDestroy', 'decoderCreate', 'decoderReset', 'decoderStep', 'decoderCapture',
+  'decoderBuffers', 'decoderDestroy'];
 
 // A device stand-in: ComputeKernel needs only the limits before it records anything.
 const FAKE_DEVICE = { limits: { maxComputeWorkgroupsPerDimension: 65535 }, ctx: null };

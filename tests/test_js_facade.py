@@ -39,3 +39,74 @@ def test_node_facade_cpu():
 @pytest.mark.gpu
 def test_node_kernels_gpu():
     _run("kernels_gpu.test.js", timeout=110)
+
+
+def _write_model(host, directory):
+    """Raw tensor bytes + a JSON manifest (offsets 256-byte aligned, as the reference's container
+    aligns its streams), for the Node decoder test to load."""
+    import json
+    import numpy as np
+
+    tensors, chunks, offset = {}, [], 0
+
+    def add(name, array):
+        nonlocal offset
+        raw = np.ascontiguousarray(array).tobytes()
+        tensors[name] = {"offset": offset, "bytes": len(raw)}
+        pad = (-len(raw)) % 256
+        chunks.append(raw + b"\0" * pad)
+        offset += len(raw) + pad
+
+    for i, L in enumerate(host.layers):
+        for name, q in L.mats.items():
+            add(f"layers.{i}.{name}.packed", q.packed)
+            add(f"layers.{i}.{name}.scales", q.scales)
+        for name, b in L.biases.items():
+            add(f"layers.{i}.{name}.bias", b)
+        add(f"layers.{i}.input_norm", L.input_norm)
+        add(f"layers.{i}.post_attention_norm", L.post_attention_norm)
+    add("embedding.packed", host.embedding.packed)
+    add("embedding.scales", host.embedding.scales)
+    add("final_norm", host.final_norm)
+    c = host.cfg
+    manifest = {"config": {k: getattr(c, k) for k in ("layers", "hidden", "heads", "kv_heads", "head_dim",
+                                                      "intermediate", "vocab", "max_context", "rms_eps",
+                                                      "rope_theta", "group", "bits")},
+                "first_token": 17, "tensors": tensors}
+    with open(os.path.join(directory, "tensors.bin"), "wb") as f:
+        for c_ in chunks:
+            f.write(c_)
+    with open(os.path.join(directory, "manifest.json"), "w") as f:
+        json.dump(manifest, f)
+    return manifest
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_decoder_matches_python_decoder(tmp_path, device):
+    """The same model driven from Node (N-API decoder binding) and from Python (ctypes) gives the
+    same greedy tokens, eagerly and as a replayed graph."""
+    import json
+
+    from enargeia_amd.model import Decoder, DeviceModel, ModelConfig, synthetic_model
+
+    cfg = ModelConfig(layers=2, vocab=4096, max_context=256)
+    host = synthetic_model(cfg)
+    manifest = _write_model(host, str(tmp_path))
+    steps = 12
+    print(f"node tests/js/decoder_gpu.test.js {tmp_path} {steps}", flush=True)
+    res = subprocess.run([NODE, os.path.join(JS_TESTS, "decoder_gpu.test.js"), str(tmp_path), str(steps)], cwd=ROOT,
+                         capture_output=True, text=True, timeout=110)
+    sys.stdout.write(res.stdout[-4000:])
+    assert res.returncode == 0, f"node exited {res.returncode}:\n{res.stdout[-3000:]}\n{res.stderr[-3000:]}"
+    node_tokens = json.loads(next(line for line in res.stdout.splitlines() if line.startswith('{"eager"')))
+    dm = DeviceModel(device, host)
+    dec = Decoder(dm)
+    try:
+        dec.reset(0, manifest["first_token"])
+        py_tokens = [dec.step() for _ in range(steps)]
+    finally:
+        dec.close()
+        dm.release()
+    assert node_tokens["eager"] == py_tokens
+    assert node_tokens["graph"] == py_tokens
