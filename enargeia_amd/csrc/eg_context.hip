@@ -93,12 +93,14 @@ int eg_create(int device, eg_context** out_ctx) {
   }
   ctx->stream = ctx->own_stream;
   if (const char* shape = std::getenv("EG_GEMV_SHAPE")) {
-    int t = 0, c = 0, u = 0;
-    if (std::sscanf(shape, "%d,%d,%d", &t, &c, &u) == 3 && (t == 8 || t == 16 || t == 32 || t == 64) && c >= 1 &&
-        c <= 4 && (u == 1 || u == 2 || u == 4)) {
+    int t = 0, c = 0, u = 0, d = 2;
+    const int got = std::sscanf(shape, "%d,%d,%d,%d", &t, &c, &u, &d);
+    if (got >= 3 && (t == 8 || t == 16 || t == 32 || t == 64) && c >= 1 && c <= 4 && (u == 1 || u == 2 || u == 4) &&
+        d >= 2 && d <= 8) {
       ctx->gemv_override[0] = t;
       ctx->gemv_override[1] = c;
       ctx->gemv_override[2] = u;
+      ctx->gemv_override[3] = d;
     }
   }
   if (const char* tpw = std::getenv("EG_FUSED_TILES_PER_WAVE")) {

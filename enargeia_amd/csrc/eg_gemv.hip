@@ -45,8 +45,11 @@ struct DevSegment {
   uint32_t pass_end;  // exclusive end of this segment's passes (cumulative)
   uint32_t rows;
   uint32_t out_offset;
-  uint32_t pad;
+  uint32_t pad[3];
 };
+// 64 bytes: the table is copied into LDS with 16-byte loads.
+static_assert(sizeof(DevSegment) == 64, "DevSegment is copied as 16-byte vectors");
+constexpr uint32_t kTableLoads = kMaxSegments * sizeof(DevSegment) / 16 / 256;  // per thread
 
 struct GemvArgs {
   const float* x;
@@ -125,14 +128,6 @@ struct Codes<8> {
 // partial. kArgmaxOnly: the partial without storing the outputs. kBatched: a segment table of
 // matrices that share x and K.
 enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3 };
-
-// Where one tile of rows lives: a whole single-matrix launch, or one segment of a batched one.
-// The streams are addressed through buffer resources (base in SGPRs, 32-bit byte offsets,
-// bounds-checked: a read past a stream returns 0 instead of faulting).
-struct TileRef {
-  __amdgpu_buffer_rsrc_t w, s, z, b, o;
-  uint32_t rows, out_offset, row0, has_bias;
-};
 
 template <int BITS, int U, int CPL>
 struct Loads {
@@ -233,10 +228,17 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       xs[i] = acc;
     }
   } else {
-    const auto src = egd::as_global(reinterpret_cast<const egd::u32x4*>(a.x));
+    // x as given: every load issued before any LDS write (8 per thread covers the longest
+    // rows, 256 chunks of 32 codes); reads past x return zeros without touching memory.
+    constexpr uint32_t kMaxLoads = 256 * 32 / 4 / 256;
+    const auto src = egd::buffer(a.x, n4 * 16u);
+    egd::u32x4 v[kMaxLoads];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxLoads; r++) v[r] = egd::load_b128(src, (tid + r * 256u) * 16u);
     egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
-#pragma unroll 4
-    for (uint32_t i = tid; i < n4; i += blockDim.x) dst[i] = src[i];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxLoads; r++)
+      if (tid + r * 256u < n4) dst[tid + r * 256u] = v[r];
   }
 }
 
@@ -245,16 +247,19 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
 // consecutive rows x TEAM consecutive 16-byte chunks).
 //
 // Each wave owns a contiguous range of tiles (so a batched launch looks its segment up once,
-// not per tile) and walks it two tiles at a time with two load buffers: the loads of tile i+1
-// are in flight while tile i is computed, so every wave keeps two tiles of codes outstanding.
+// not per tile) and walks it NB tiles at a time with NB load buffers: the loads of tiles
+// i+1 .. i+NB-1 are in flight while tile i is computed. The bytes a CU keeps in flight are
+// what bounds a streaming kernel's bandwidth (latency x rate), and they cost VGPRs: x takes
+// CPL * EPC per lane, each buffer U * (5 * CPL + 1) more, so long rows (large x) trade
+// resident waves for a deeper pipeline per wave.
 // The steady-state loop has no memory operation under a branch, which lets the compiler wait
 // for exactly the tile it is about to use:
 //   * loads are unconditional - out-of-range rows read the last row, out-of-range chunk slots
-//     read chunk 0 (x is zero there), and a wave whose range is odd re-reads its last tile
-//     (an L2 hit) instead of branching around the second buffer;
+//     read chunk 0 (x is zero there), and a wave whose count is not a multiple of NB re-reads
+//     its last tile (an L2 hit) instead of branching around the spare buffers;
 //   * stores are unconditional - the team total is in every lane of the team, every lane
 //     stores it, and a clamped or repeated row stores the value that row already has.
-template <int BITS, int ENC, int TEAM, int CPL, int U, int MODE>
+template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
@@ -276,12 +281,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
   float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? a.seg_count : 0u) *
                                                                       (uint32_t)sizeof(DevSegment));
+  // The segment table's loads are all issued up front (kTableLoads per thread at most, reads
+  // past the table return zeros), so copying it costs one L2 round trip that overlaps the
+  // input stage's, not one per element.
+  egd::u32x4 tv[MODE == kBatched ? kTableLoads : 1];
+  const uint32_t table_vecs = a.seg_count * (uint32_t)(sizeof(DevSegment) / 16);
+  if (MODE == kBatched) {
+    const auto src = egd::buffer(a.segs, table_vecs * 16u);
+#pragma unroll
+    for (uint32_t r = 0; r < kTableLoads; r++) tv[r] = egd::load_b128(src, (threadIdx.x + r * 256u) * 16u);
+  }
   produce_input(a, reinterpret_cast<float*>(smem), x_words, scratch);
   if (MODE == kBatched) {
-    const uint32_t words = a.seg_count * (uint32_t)(sizeof(DevSegment) / 4);
-    const auto src = egd::as_global(reinterpret_cast<const uint32_t*>(a.segs));
-    uint32_t* dst = reinterpret_cast<uint32_t*>(table);
-    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
+    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(table);
+#pragma unroll
+    for (uint32_t r = 0; r < kTableLoads; r++)
+      if (threadIdx.x + r * 256u < table_vecs) dst[threadIdx.x + r * 256u] = tv[r];
   }
   __syncthreads();
 
@@ -309,14 +324,40 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
   }
 
-  // This wave's tiles: [begin, end), contiguous.
-  const uint32_t begin = (uint32_t)(((uint64_t)a.total_passes * wave) / total_waves);
-  const uint32_t end = (uint32_t)(((uint64_t)a.total_passes * (wave + 1)) / total_waves);
+  // Byte offsets of this lane's loads relative to its tile's first row: constant for the whole
+  // launch. The tile's own offset is wave-uniform and rides in the buffer instruction's scalar
+  // offset, so walking tiles costs scalar adds, not per-lane address arithmetic.
+  uint32_t qoff[U][CPL], soff[U][CPL], roff[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t lrow = u * RPW + slot;
+    roff[u] = lrow * 4u;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      qoff[u][j] = (lrow * a.chunks + cj[j]) * 16u;
+      soff[u][j] = (lrow * a.blocks_per_row + bj[j]) * 4u;
+    }
+  }
 
-  auto make_ref = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
-                      uint32_t rows, uint32_t out_offset) {
+  // This wave's tiles: [begin, end), contiguous. (readfirstlane: the 64-bit divisions run on
+  // the vector unit, and the tile offsets derived from these must be known wave-uniform.)
+  const uint32_t begin =
+      __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * wave) / total_waves));
+  const uint32_t end =
+      __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * (wave + 1)) / total_waves));
+
+  // The matrix the issue side is walking (one for a plain launch; the current segment of a
+  // batched one). Rows are a multiple of TILE in a batched plan; a plain launch's last partial
+  // tile is shifted back to end at the last row (rows >= TILE), recomputing a few rows with
+  // identical results, so every access stays inside its stream.
+  struct Seg {
+    __amdgpu_buffer_rsrc_t w, s, z, b, o;
+    uint32_t rows, out_offset, first, end, has_bias;
+  };
+  auto make_seg = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
+                      uint32_t rows, uint32_t out_offset, uint32_t first, uint32_t seg_end) {
     const uint32_t blocks = rows * a.blocks_per_row;
-    TileRef r;
+    Seg r;
     r.w = egd::buffer(w, rows * a.chunks * 16u);
     r.s = egd::buffer(scales, blocks * 4u);
     r.z = egd::buffer(zeros, ((blocks + C::kZeroPerWord - 1) / C::kZeroPerWord) * 4u);
@@ -326,65 +367,89 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     r.o = egd::buffer(out, (out_offset + rows) * 4u);
     r.rows = rows;
     r.out_offset = out_offset;
-    r.row0 = 0;
+    r.first = first;
+    r.end = seg_end;
     return r;
   };
 
-  // Batched: the segment holding the current tile is read from the LDS table into scalar
-  // registers (an LDS read waits on lgkmcnt, so switching segments never waits for the tile
-  // loads in flight, as a global load of the table would).
-  TileRef cur = MODE == kBatched ? TileRef{} : make_ref(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset);
-  uint32_t seg = 0, cur_first = 0, cur_end = a.total_passes;
-  auto load_segment = [&](uint32_t s) {
-    const DevSegment& d = table[s];
-    cur = make_ref(egd::uniform(d.w), egd::uniform(d.scales), egd::uniform(d.zeros), egd::uniform(d.bias),
-                   egd::uniform(d.out), __builtin_amdgcn_readfirstlane(d.rows),
-                   __builtin_amdgcn_readfirstlane(d.out_offset));
-    cur_end = __builtin_amdgcn_readfirstlane(d.pass_end);
-    cur_first = cur_end - cur.rows / TILE;
+  // Batched: a segment is read from the LDS table into scalar registers (an LDS read waits on
+  // lgkmcnt, so switching segments never waits for the tile loads in flight, as a global load
+  // of the table would).
+  Seg cur = make_seg(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, 0, a.total_passes);
+  uint32_t seg = 0;
+  auto load_segment = [&](uint32_t sidx) {
+    const DevSegment& d = table[sidx];
+    const uint32_t rows = __builtin_amdgcn_readfirstlane(d.rows);
+    const uint32_t seg_end = __builtin_amdgcn_readfirstlane(d.pass_end);
+    cur = make_seg(egd::uniform(d.w), egd::uniform(d.scales), egd::uniform(d.zeros), egd::uniform(d.bias),
+                   egd::uniform(d.out), rows, __builtin_amdgcn_readfirstlane(d.out_offset), seg_end - rows / TILE,
+                   seg_end);
   };
   if (MODE == kBatched && begin < end) {
-    uint32_t lo = 0, hi = a.seg_count - 1;  // first segment whose pass_end exceeds begin
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (__builtin_amdgcn_readfirstlane(table[mid].pass_end) > begin)
-        hi = mid;
-      else
-        lo = mid + 1;
+    // The first segment whose pass_end exceeds `begin` = the number of segments ending at or
+    // before it (pass_end increases): 64 entries per LDS read, counted with a ballot.
+    uint32_t count = 0;
+    for (uint32_t e0 = 0; e0 < a.seg_count; e0 += 64) {
+      const uint32_t e = e0 + lane;
+      const bool done = e < a.seg_count && table[e < a.seg_count ? e : 0].pass_end <= begin;
+      count += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(done));
     }
-    seg = lo;
+    seg = __builtin_amdgcn_readfirstlane(count);
     load_segment(seg);
   }
-  auto issue = [&](const TileRef& r, Loads<BITS, U, CPL>& L) {
+
+  // What computing a tile needs once its loads are in flight: where its rows are stored.
+  struct Pending {
+    __amdgpu_buffer_rsrc_t o;
+    uint32_t row0, out_offset, has_bias;
+  };
+  const uint32_t last = end - 1;
+
+  // Issues the loads of tile `tl` (clamped to the wave's last tile; tiles are visited in
+  // increasing order, so the segment cursor only moves forward).
+  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
+    tl = min(tl, last);
+    if (MODE == kBatched)
+      while (tl >= cur.end) load_segment(++seg);
+    // (readfirstlane pins the value to a scalar register: a scalar offset left in a vector
+    // register would make the compiler wrap every load in a per-lane loop.)
+    const uint32_t row0 = __builtin_amdgcn_readfirstlane(min((tl - cur.first) * TILE, cur.rows - TILE));
+    const uint32_t sq = row0 * (a.chunks * 16u);
+    const uint32_t ss = row0 * (a.blocks_per_row * 4u);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const uint32_t row = min(r.row0 + u * RPW + slot, r.rows - 1);
-      L.b[u] = egd::load_f32(r.b, row * 4u);
+      L.b[u] = egd::load_f32(cur.b, roff[u], row0 * 4u);
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        L.q[u][j] = egd::load_b128_nt(r.w, (row * a.chunks + cj[j]) * 16u);
-        const uint32_t blk = row * a.blocks_per_row + bj[j];
-        L.s[u][j] = egd::load_f32_nt(r.s, blk * 4u);
-        if (ENC == EG_ENC_OFFSET_ZEROS) L.zw[u][j] = egd::load_b32(r.z, (blk / C::kZeroPerWord) * 4u);
+        L.q[u][j] = egd::load_b128_nt(cur.w, qoff[u][j], sq);
+        L.s[u][j] = egd::load_f32_nt(cur.s, soff[u][j], ss);
+        if (ENC == EG_ENC_OFFSET_ZEROS) {
+          const uint32_t blk = (row0 + u * RPW + slot) * a.blocks_per_row + bj[j];
+          L.zw[u][j] = egd::load_b32(cur.z, (blk / C::kZeroPerWord) * 4u);
+        }
       }
     }
+    P.o = cur.o;
+    P.row0 = row0;
+    P.out_offset = cur.out_offset;
+    P.has_bias = cur.has_bias;
   };
 
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
-  auto compute = [&](const TileRef& r, const Loads<BITS, U, CPL>& L) {
+  auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too).
-      float acc = (t == 0 && r.has_bias) ? L.b[u] : 0.f;
-      const uint32_t crow = min(r.row0 + u * RPW + slot, r.rows - 1);
+      float acc = (t == 0 && P.has_bias) ? L.b[u] : 0.f;
+      const uint32_t row = P.row0 + u * RPW + slot;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
         uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
         float z;
         if (ENC == EG_ENC_OFFSET_ZEROS) {
-          const uint32_t blk = crow * a.blocks_per_row + bj[j];
+          const uint32_t blk = row * a.blocks_per_row + bj[j];
           z = (float)((L.zw[u][j] >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
         } else {
           q.x ^= C::kSignFlip;
@@ -396,9 +461,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         acc = fmaf(L.s[u][j], C::dot(q, xr[j]) - z * sx[j], acc);
       }
       const float v = egd::team_allsum<TEAM>(acc);
-      const uint32_t idx = crow + r.out_offset;
-      if (kStore) egd::store_f32(r.o, idx * 4u, v);
+      if (kStore) egd::store_f32(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
       if (kBest) {
+        const uint32_t idx = row + P.out_offset;
         const bool take = egd::better(v, idx, best_v, best_i);
         best_v = take ? v : best_v;
         best_i = take ? idx : best_i;
@@ -406,47 +471,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
   };
 
-  // The wave's range is walked segment by segment (one segment in a plain launch). Inside a
-  // segment the loop is software-pipelined over two load buffers, two tiles per iteration,
-  // with a single exit at the bottom: an odd count computes its last tile twice (same loads,
-  // same stores) rather than breaking out mid-body. With no path leaving the loop between an
-  // issue and its consumer, the compiler's wait counts stay exact - computing a tile waits
-  // only for that tile's loads, never for the next tile's. sched_barrier(0) after each issue
-  // keeps the scheduler from sinking the next tile's loads into the current tile's math.
+  // The wave's range is one software pipeline over NB load buffers, NB tiles per iteration,
+  // with a single exit at the bottom: while tile i is computed, the loads of tiles
+  // i+1 .. i+NB-1 are in flight. Each buffer carries where its rows go, so the pipeline runs
+  // straight through segment boundaries (a boundary costs a few scalar LDS reads, not a drain
+  // of the loads in flight). A count that is not a multiple of NB computes the wave's last
+  // tile again (same loads, same stores) rather than leaving the loop mid-body. With no path
+  // leaving the loop between an issue and its consumer, the compiler's wait counts stay exact -
+  // computing a tile waits only for that tile's loads, never for a later tile's.
+  // sched_barrier(0) after each issue keeps the scheduler from sinking the next tile's loads
+  // into the current tile's math.
   if (begin < end) {
-    Loads<BITS, U, CPL> LA, LB;
+    Loads<BITS, U, CPL> L[NB];
+    Pending P[NB];
     uint32_t tile = begin;
-    for (;;) {
-      if (MODE == kBatched)
-        while (tile >= cur_end) load_segment(++seg);
-      const uint32_t last = min(end, cur_end) - 1;  // this wave's last tile in the segment
-      const TileRef base = cur;
-      const uint32_t first = cur_first;
-      auto at = [&](uint32_t tl) {
-        TileRef r = base;
-        r.row0 = (tl - first) * TILE;
-        return r;
-      };
-      const uint32_t pairs = (last - tile) / 2 + 1;
-      issue(at(tile), LA);
-      for (uint32_t p = 0; p < pairs; p++) {
-        const uint32_t tb = min(tile + 1, last);
-        issue(at(tb), LB);
+    const uint32_t groups = (end - begin + NB - 1) / NB;
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) issue(tile + b, L[b], P[b]);
+    for (uint32_t g = 0; g < groups; g++) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const int nx = (b + NB - 1) % NB;
+        issue(tile + b + NB - 1, L[nx], P[nx]);
         __builtin_amdgcn_sched_barrier(0);
-        compute(at(tile), LA);
-        issue(at(min(tile + 2, last)), LA);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(at(tb), LB);
-        tile += 2;
+        compute(L[b], P[b]);
       }
-      // The last issue is a duplicate that nothing consumes. Wait it out once per segment:
-      // left pending, it would make the compiler assume those registers may still be written
-      // at the loop head, and wait for every in-flight load there on every iteration.
-      // (gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15.)
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      tile = last + 1;
-      if (tile >= end) break;
+      tile += NB;
     }
+    // The last NB-1 issues are duplicates that nothing consumes; they complete before the
+    // wave ends.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
   }
 
   if (kBest) {
@@ -538,38 +592,43 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
 
 using KernelFn = void (*)(GemvArgs);
 
-// Instantiated (TEAM, CPL, U) shapes: one chunk slot per lane for rows of up to 64 chunks
-// (TEAM the next power of two), a full-wave team with 2-4 slots for longer rows.
-#define EG_SHAPES(X)                                                                          \
-  X(8, 1, 1) X(8, 1, 2) X(8, 1, 4) X(16, 1, 1) X(16, 1, 2) X(16, 1, 4) X(32, 1, 1) X(32, 1, 2) \
-  X(32, 1, 4) X(64, 1, 1) X(64, 1, 2) X(64, 1, 4) X(64, 2, 1) X(64, 2, 2) X(64, 3, 1) X(64, 4, 1)
+// Instantiated (TEAM, CPL, U, NB) shapes: one chunk slot per lane for rows of up to 64 chunks
+// (TEAM the next power of two), a full-wave team with 2-4 slots for longer rows. The library
+// picks NB = 2 (measured fastest on MI355X: a deeper pipeline costs resident waves and
+// duplicate tail tiles); NB 3-4 variants of the main shapes stay selectable through
+// EG_GEMV_SHAPE for tuning.
+#define EG_SHAPES(X)                                                                                      \
+  X(8, 1, 1, 2) X(8, 1, 2, 2) X(8, 1, 4, 2) X(16, 1, 1, 2) X(16, 1, 2, 2) X(16, 1, 4, 2) X(32, 1, 1, 2)    \
+  X(32, 1, 2, 2) X(32, 1, 2, 3) X(32, 1, 2, 4) X(32, 1, 4, 2) X(64, 1, 1, 2) X(64, 1, 2, 2) X(64, 1, 4, 2) \
+  X(64, 1, 4, 3) X(64, 2, 1, 2) X(64, 2, 2, 2) X(64, 3, 1, 2) X(64, 3, 1, 3) X(64, 3, 1, 4) X(64, 3, 2, 2) \
+  X(64, 4, 1, 2)
 
 template <int BITS, int ENC, int MODE>
-KernelFn pick(int team, int cpl, int u) {
-#define EG_CASE(T, P, UU) \
-  if (team == T && cpl == P && u == UU) return gemv_kernel<BITS, ENC, T, P, UU, MODE>;
+KernelFn pick(int team, int cpl, int u, int nb) {
+#define EG_CASE(T, P, UU, D) \
+  if (team == T && cpl == P && u == UU && nb == D) return gemv_kernel<BITS, ENC, T, P, UU, D, MODE>;
   EG_SHAPES(EG_CASE)
 #undef EG_CASE
   return nullptr;
 }
 
 template <int BITS, int ENC>
-KernelFn pick_mode(int mode, int team, int cpl, int u) {
-  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u);
-  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u);
-  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u);
-  return pick<BITS, ENC, kPlain>(team, cpl, u);
+KernelFn pick_mode(int mode, int team, int cpl, int u, int nb) {
+  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb);
+  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb);
+  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb);
+  return pick<BITS, ENC, kPlain>(team, cpl, u, nb);
 }
 
-KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u) {
-  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
-  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u);
-  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
-  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u);
+KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u, int nb) {
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
+  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
 }
 
 struct Shape {
-  int team = 0, cpl = 0, u = 0;
+  int team = 0, cpl = 0, u = 0, nb = 2;
   uint32_t tiles = 0;
 };
 
@@ -610,12 +669,17 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
     sh.team = ctx->gemv_override[0];
     sh.cpl = ctx->gemv_override[1];
     sh.u = ctx->gemv_override[2];
+    sh.nb = ctx->gemv_override[3];
     if ((uint32_t)(sh.team * sh.cpl) < chunks) return Shape{};
   }
   const uint32_t rpw = 64u / sh.team;
   if (row_multiple)
     while (sh.u > 1 && row_multiple % (rpw * sh.u) != 0) sh.u /= 2;
   if (row_multiple && row_multiple % (rpw * sh.u) != 0) return Shape{};
+  // A plain launch shifts its last partial tile back inside the matrix, so a tile may not
+  // have more rows than the matrix.
+  while (sh.u > 1 && rpw * sh.u > n) sh.u /= 2;
+  if (rpw * sh.u > n) return Shape{};
   const uint32_t tile_rows = rpw * sh.u;
   sh.tiles = (n + tile_rows - 1) / tile_rows;
   return sh;
@@ -725,7 +789,7 @@ int launch(eg_context* ctx, const QuantView& v) {
   uint32_t* partials = reinterpret_cast<uint32_t*>(eg::partials(ctx));
   uint32_t grid = 0;
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
-  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u) : nullptr;
+  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u, shape.nb) : nullptr;
   if (fused && !fn)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: a fused input stage needs k and the block a multiple of %u", v.op, epc);
   if (fn) {
@@ -830,7 +894,7 @@ struct eg_gemv_plan {
   DevSegment* table = nullptr;  // device copy
   uint32_t count = 0;
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
-  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0;
+  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
 };
 
 extern "C" {
@@ -877,7 +941,7 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
     const eg_gemv_segment& g = segments[i];
     pass += g.rows / tile_rows;
     host[i] = DevSegment{reinterpret_cast<const uint4*>(g.packed), g.scales,
-                         encoding == EG_ENC_SIGNED ? nullptr : g.zeros, g.bias, g.out, pass, g.rows, g.out_offset, 0};
+                         encoding == EG_ENC_SIGNED ? nullptr : g.zeros, g.bias, g.out, pass, g.rows, g.out_offset, {0, 0, 0}};
   }
   eg_gemv_plan* plan = new eg_gemv_plan();
   hipError_t err = hipMalloc(&plan->table, sizeof(DevSegment) * count);
@@ -898,7 +962,8 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->team = shape.team;
   plan->cpl = shape.cpl;
   plan->u = shape.u;
-  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u);
+  plan->nb = shape.nb;
+  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb);
   plan->smem = k * 4u + count * (uint32_t)sizeof(DevSegment);
   plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
   *out_plan = plan;
@@ -925,7 +990,7 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   a.segs = plan->table;
   a.seg_count = plan->count;
   a.total_passes = plan->total_passes;
-  KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u);
+  KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u, plan->nb);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR

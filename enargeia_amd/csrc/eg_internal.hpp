@@ -23,9 +23,10 @@ struct eg_context {
   uint8_t* workspace = nullptr;
   size_t workspace_bytes = 0;
   bool capturing = false;
-  // GEMV shape override (team, chunks per lane, rows per lane) from EG_GEMV_SHAPE="t,c,u",
-  // read once at creation; zeros mean the built-in choice. For tuning sweeps.
-  int gemv_override[3] = {0, 0, 0};
+  // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth) from
+  // EG_GEMV_SHAPE="t,c,u[,d]", read once at creation; zeros mean the built-in choice. For
+  // tuning sweeps.
+  int gemv_override[4] = {0, 0, 0, 0};
   // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 2).
   uint32_t fused_tiles_per_wave = 2;
   // Resident workgroups per CU of each kernel launched through this context (from
@@ -110,30 +111,32 @@ __device__ __forceinline__ T* uniform(T* p) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ u32x4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+// `offset` is per lane (VGPR); `soffset` is a wave-uniform byte offset added in the address
+// unit (SGPR), so a loop that walks a stream advances it with scalar adds.
+__device__ __forceinline__ u32x4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 0);
 }
 // Non-temporal (streaming) loads, for data read exactly once per launch (weight codes and
 // scales): the nt cache-policy bit lets the line bypass normal retention, which measures ~10%
 // more read bandwidth on MI355X than default-policy loads.
 constexpr int kNonTemporal = 2;
-__device__ __forceinline__ u32x4 load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kNonTemporal);
+__device__ __forceinline__ u32x4 load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, kNonTemporal);
 }
-__device__ __forceinline__ uint32_t load_b32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kNonTemporal);
+__device__ __forceinline__ uint32_t load_b32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, kNonTemporal);
 }
-__device__ __forceinline__ float load_f32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kNonTemporal));
+__device__ __forceinline__ float load_f32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, kNonTemporal));
 }
-__device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0);
+__device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, 0);
 }
-__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, 0));
 }
-__device__ __forceinline__ void store_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, 0, 0);
+__device__ __forceinline__ void store_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset, float v, uint32_t soffset = 0) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, soffset, 0);
 }
 
 // Opaque AND: keeps the compiler from folding a nibble mask into per-element bitfield

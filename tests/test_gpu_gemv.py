@@ -289,3 +289,60 @@ def test_batched_plan_rejects_bad_tables(device):
         K.GemvPlan(device, 896, 32, [(bp, bs, None, None, bo, 896, 0)], encoding=K.ENC_OFFSET_ZEROS)
     for b in (bp, bs, bo):
         b.release()
+
+
+# ---- every instantiated pipeline depth ------------------------------------------------------
+
+# (EG_GEMV_SHAPE "team,chunks per lane,rows per lane,depth", bits, K): each entry is a kernel
+# the library instantiates; the override makes a fresh context use it for every launch.
+DEPTH_CASES = [("32,1,2,3", 4, 896), ("32,1,2,4", 4, 896), ("64,1,4,3", 4, 896), ("64,3,1,3", 4, 4864),
+               ("64,3,1,4", 4, 4864), ("64,1,4,3", 8, 896), ("32,1,2,2", 4, 896), ("64,3,2,2", 4, 4864)]
+
+
+@pytest.mark.parametrize("shape,bits,k", DEPTH_CASES)
+def test_pipeline_depths_match_oracle(shape, bits, k):
+    """A batched plan over segments of unequal length (so waves start mid-segment and cross
+    segment ends with counts that are not multiples of the depth), a plain launch and the fused
+    argmax, each under one forced (team, slots, rows, depth) shape."""
+    print(f"shape {shape} bits {bits} k {k}", flush=True)
+    x = oracle.normal_floats(k, 1300 + k, 1.0)
+    rows = (1024, 136, 512, 64)
+    mats = [sym_weights(n, k, 1400 + i, 32 if bits == 4 else k, bits) for i, n in enumerate(rows)]
+    bias = oracle.normal_floats(136, 1399, 0.02)
+    old = os.environ.get("EG_GEMV_SHAPE")
+    os.environ["EG_GEMV_SHAPE"] = shape
+    try:
+        dev = K.Device(0)
+    finally:
+        if old is None:
+            os.environ.pop("EG_GEMV_SHAPE")
+        else:
+            os.environ["EG_GEMV_SHAPE"] = old
+    try:
+        bx = dev.upload(x)
+        keep, segs, outs = [bx], [], []
+        for i, q in enumerate(mats):
+            bp, bs = dev.upload(q.packed), dev.upload(q.scales)
+            bb = dev.upload(bias) if i == 1 else None
+            bo = dev.buffer(q.rows * 4)
+            dev.zero(bo, q.rows * 4)
+            keep += [bp, bs, bo] + ([bb] if bb else [])
+            segs.append((bp, bs, None, bb, bo, q.rows, 0))
+            outs.append(bo)
+        plan = K.GemvPlan(dev, k, q.block_size, segs, bits=bits)
+        plan.launch(bx)
+        for i, q in enumerate(mats):
+            got = dev.read_array(outs[i], np.float32, q.rows)
+            expect = oracle.linear_q(x, q, bias if i == 1 else None, 1)
+            assert_close(got, expect, *gemv_tolerance(expect), label=f"{shape} segment {i}")
+        plan.destroy()
+        # one matrix, plain launch and fused argmax (the LM head entry)
+        q = mats[0]
+        expect = oracle.linear_q(x, q, None, 1)
+        logits, res = _run_head(dev, q, x, fused=True)
+        assert_close(logits, expect, *gemv_tolerance(expect), label=f"{shape} single")
+        assert res[0] == oracle.argmax(logits)
+        for b in keep:
+            b.release()
+    finally:
+        dev.close()
