@@ -18,6 +18,9 @@ EG_ERR_RANGE = -2
 EG_ERR_DEVICE = -3
 EG_ERR_NOMEM = -4
 EG_ERR_STATE = -5
+EG_ERR_FORMAT = -6
+EG_ERR_IO = -7
+EG_ERR_NOT_FOUND = -8
 
 ENC_OFFSET_ZEROS = 0
 ENC_SIGNED = 1
@@ -56,6 +59,13 @@ SIGNATURES: dict[str, tuple] = {
     "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_decode_advance": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
     "eg_decoder_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "eg_container_open": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "eg_container_close": (_i, [_vp]),
+    "eg_container_header_get": (_i, [_vp, _vp]),
+    "eg_container_tensor": (_i, [_vp, ctypes.c_uint32, _vp]),
+    "eg_container_find": (_i, [_vp, ctypes.c_char_p, _vp]),
+    "eg_container_upload": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "eg_container_model_desc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
     "eg_decoder_destroy": (_i, [_vp]),
     "eg_decoder_buffers_get": (_i, [_vp, _vp]),
     "eg_decoder_reset": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32]),

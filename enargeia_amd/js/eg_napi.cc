@@ -26,24 +26,40 @@ const char* status_name(int st) {
     case EG_ERR_DEVICE: return "EG_ERR_DEVICE";
     case EG_ERR_NOMEM: return "EG_ERR_NOMEM";
     case EG_ERR_STATE: return "EG_ERR_STATE";
+    case EG_ERR_FORMAT: return "EG_ERR_FORMAT";
+    case EG_ERR_IO: return "EG_ERR_IO";
+    case EG_ERR_NOT_FOUND: return "EG_ERR_NOT_FOUND";
     default: return "EG_ERR_UNKNOWN";
   }
 }
 
-// Throws for a failed status; returns true when the caller should return early.
+// Throws for a failed status; returns true when the caller should return early. A malformed
+// container throws an Error named EnargeiaError, as the reference's parser does (enargeia.ts:84).
 bool throw_status(napi_env env, eg_context* ctx, int st) {
   if (st == EG_OK) return false;
   const char* msg = eg_last_error(ctx);
-  if (st == EG_ERR_RANGE)
+  if (st == EG_ERR_RANGE) {
     napi_throw_range_error(env, status_name(st), msg);
-  else
+  } else if (st == EG_ERR_FORMAT) {
+    napi_value code, text, err, name;
+    napi_create_string_utf8(env, status_name(st), NAPI_AUTO_LENGTH, &code);
+    napi_create_string_utf8(env, msg, NAPI_AUTO_LENGTH, &text);
+    napi_create_error(env, code, text, &err);
+    napi_create_string_utf8(env, "EnargeiaError", NAPI_AUTO_LENGTH, &name);
+    napi_set_named_property(env, err, "name", name);
+    napi_throw(env, err);
+  } else {
     napi_throw_error(env, status_name(st), msg);
+  }
   return true;
 }
 
 void throw_type(napi_env env, const std::string& what) { napi_throw_type_error(env, "EG_ERR_INVALID", what.c_str()); }
 
 struct DecoderHandle;
+struct ContainerHandle {
+  eg_container* c;
+};
 
 // One type tag per kind of handle.
 template <typename T>
@@ -61,6 +77,12 @@ const napi_type_tag& tag_of<eg_graph>() {
 template <>
 const napi_type_tag& tag_of<DecoderHandle>() {
   static const napi_type_tag t{0x45474354584e4150ull, 0x0000000000000003ull};
+  return t;
+}
+
+template <>
+const napi_type_tag& tag_of<ContainerHandle>() {
+  static const napi_type_tag t{0x45474354584e4150ull, 0x0000000000000004ull};
   return t;
 }
 
@@ -649,6 +671,199 @@ napi_value GraphDestroy(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// ---- the .enargeia container -------------------------------------------------------------------
+
+napi_value num(napi_env env, double v) {
+  napi_value r;
+  napi_create_double(env, v, &r);
+  return r;
+}
+napi_value str(napi_env env, const char* s) {
+  napi_value r;
+  napi_create_string_utf8(env, s, NAPI_AUTO_LENGTH, &r);
+  return r;
+}
+void set(napi_env env, napi_value obj, const char* name, napi_value v) { napi_set_named_property(env, obj, name, v); }
+napi_value range(napi_env env, const uint64_t r[2]) {
+  napi_value a;
+  napi_create_array_with_length(env, 2, &a);
+  napi_set_element(env, a, 0, num(env, (double)r[0]));
+  napi_set_element(env, a, 1, num(env, (double)r[1]));
+  return a;
+}
+napi_value ptr_value(napi_env env, const void* p) {
+  if (!p) {
+    napi_value n;
+    napi_get_null(env, &n);
+    return n;
+  }
+  return num(env, (double)reinterpret_cast<uintptr_t>(p));
+}
+
+void finalize_container(napi_env, void* data, void*) {
+  auto* h = static_cast<ContainerHandle*>(data);
+  if (h->c) eg_container_close(h->c);
+  delete h;
+}
+
+ContainerHandle* open_handle(Args& a, size_t index) {
+  auto* h = a.handle<ContainerHandle>(index, "container");
+  if (h && !h->c) {
+    napi_throw_error(a.env, "EG_ERR_STATE", (std::string(a.fn) + ": the container was closed").c_str());
+    return nullptr;
+  }
+  return h;
+}
+
+// containerOpen(path): parses the prefix and header; throws EnargeiaError for a malformed file.
+napi_value ContainerOpen(napi_env env, napi_callback_info info) {
+  Args a(env, info, "containerOpen", 1);
+  if (!a.ok) return nullptr;
+  size_t n = 0;
+  if (napi_get_value_string_utf8(env, a.argv[0], nullptr, 0, &n) != napi_ok) {
+    throw_type(env, "containerOpen: path is not a string");
+    return nullptr;
+  }
+  std::string path(n, '\0');
+  napi_get_value_string_utf8(env, a.argv[0], &path[0], n + 1, &n);
+  eg_container* c = nullptr;
+  if (throw_status(env, nullptr, eg_container_open(nullptr, path.c_str(), &c))) return nullptr;
+  return make_handle(env, new ContainerHandle{c}, finalize_container);
+}
+
+napi_value ContainerClose(napi_env env, napi_callback_info info) {
+  Args a(env, info, "containerClose", 1);
+  auto* h = a.handle<ContainerHandle>(0, "container");
+  if (!a.ok) return nullptr;
+  if (h->c) eg_container_close(h->c);
+  h->c = nullptr;
+  return undefined(env);
+}
+
+// containerHeader(handle): EnargeiaHeader (enargeia.ts:73-82) with `tensors` an array of
+// QuantTensorInfo / F32TensorInfo / F16TensorInfo objects in header order.
+napi_value ContainerHeader(napi_env env, napi_callback_info info) {
+  Args a(env, info, "containerHeader", 1);
+  auto* h = open_handle(a, 0);
+  if (!a.ok || !h) return nullptr;
+  eg_container_header hd;
+  if (throw_status(env, nullptr, eg_container_header_get(h->c, &hd))) return nullptr;
+  napi_value out, list;
+  napi_create_object(env, &out);
+  set(env, out, "version", num(env, hd.version));
+  set(env, out, "blockSize", num(env, hd.block_size));
+  set(env, out, "quantization", str(env, hd.quantization));
+  set(env, out, "dataOffset", num(env, (double)hd.data_offset));
+  set(env, out, "headerLength", num(env, (double)hd.header_length));
+  set(env, out, "fileSize", num(env, (double)hd.file_size));
+  napi_create_array_with_length(env, hd.tensor_count, &list);
+  static const char* kDtype[] = {"Q4", "Q8", "F32", "F16"};
+  for (uint32_t i = 0; i < hd.tensor_count; i++) {
+    eg_tensor_info t;
+    if (throw_status(env, nullptr, eg_container_tensor(h->c, i, &t))) return nullptr;
+    napi_value o, shape;
+    napi_create_object(env, &o);
+    set(env, o, "name", str(env, t.name));
+    set(env, o, "dtype", str(env, kDtype[t.dtype]));
+    napi_create_array_with_length(env, t.ndim, &shape);
+    for (uint32_t d = 0; d < t.ndim; d++) napi_set_element(env, shape, d, num(env, (double)t.shape[d]));
+    set(env, o, "shape", shape);
+    if (t.dtype == EG_DTYPE_Q4 || t.dtype == EG_DTYPE_Q8) {
+      set(env, o, "bits", num(env, t.bits));
+      set(env, o, "blockSize", num(env, t.block_size));
+      set(env, o, "packed", range(env, t.packed));
+      set(env, o, "scales", range(env, t.scales));
+      set(env, o, "zeros", range(env, t.zeros));
+      set(env, o, "blocksPerRow", num(env, t.blocks_per_row));
+      set(env, o, "totalBlocks", num(env, (double)t.total_blocks));
+    } else {
+      set(env, o, "data", range(env, t.data));
+    }
+    napi_set_element(env, list, i, o);
+  }
+  set(env, out, "tensors", list);
+  return out;
+}
+
+// containerLoad(ctx, handle, {headDim, maxContext, rmsEps, ropeTheta}): uploads the blob (one
+// device allocation; bufFree it when done) and returns {blob, desc} with desc in the shape
+// decoderCreate takes.
+napi_value ContainerLoad(napi_env env, napi_callback_info info) {
+  Args a(env, info, "containerLoad", 3);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* h = open_handle(a, 1);
+  if (!a.ok || !h) return nullptr;
+  eg_model_config cfg{};
+  napi_value c = a.argv[2];
+  if (!get_u32(env, c, "headDim", &cfg.head_dim) || !get_u32(env, c, "maxContext", &cfg.max_context) ||
+      !get_f32(env, c, "rmsEps", &cfg.rms_eps) || !get_f32(env, c, "ropeTheta", &cfg.rope_theta))
+    return nullptr;
+  eg_container_header hd;
+  eg_container_header_get(h->c, &hd);
+  void* blob = nullptr;
+  if (throw_status(env, ctx, eg_container_upload(ctx, h->c, &blob))) return nullptr;
+  std::vector<eg_layer_desc> layers(hd.tensor_count + 1);
+  eg_model_desc m{};
+  const int st = eg_container_model_desc(ctx, h->c, blob, &cfg, &m, layers.data(), (uint32_t)layers.size());
+  if (st != EG_OK) {
+    eg_buf_free(ctx, blob);
+    throw_status(env, ctx, st);
+    return nullptr;
+  }
+  auto matrix = [&](const eg_quant_matrix& q) {
+    napi_value o;
+    napi_create_object(env, &o);
+    set(env, o, "packed", ptr_value(env, q.packed));
+    set(env, o, "scales", ptr_value(env, q.scales));
+    set(env, o, "zeros", ptr_value(env, q.zeros));
+    return o;
+  };
+  napi_value d, list, out;
+  napi_create_object(env, &d);
+  set(env, d, "layers", num(env, m.layers));
+  set(env, d, "hidden", num(env, m.hidden));
+  set(env, d, "heads", num(env, m.heads));
+  set(env, d, "kvHeads", num(env, m.kv_heads));
+  set(env, d, "headDim", num(env, m.head_dim));
+  set(env, d, "intermediate", num(env, m.intermediate));
+  set(env, d, "vocab", num(env, m.vocab));
+  set(env, d, "maxContext", num(env, m.max_context));
+  set(env, d, "rmsEps", num(env, m.rms_eps));
+  set(env, d, "ropeTheta", num(env, m.rope_theta));
+  set(env, d, "encoding", num(env, m.encoding));
+  set(env, d, "bits", num(env, m.bits));
+  set(env, d, "blockSize", num(env, m.block_size));
+  set(env, d, "embedding", matrix(m.embedding));
+  set(env, d, "embedEncoding", num(env, m.embed_encoding));
+  set(env, d, "embedBits", num(env, m.embed_bits));
+  set(env, d, "embedBlockSize", num(env, m.embed_block_size));
+  set(env, d, "finalNorm", ptr_value(env, m.final_norm));
+  napi_create_array_with_length(env, m.layers, &list);
+  for (uint32_t i = 0; i < m.layers; i++) {
+    const eg_layer_desc& L = m.layer[i];
+    napi_value o;
+    napi_create_object(env, &o);
+    set(env, o, "q", matrix(L.q));
+    set(env, o, "k", matrix(L.k));
+    set(env, o, "v", matrix(L.v));
+    set(env, o, "o", matrix(L.o));
+    set(env, o, "gate", matrix(L.gate));
+    set(env, o, "up", matrix(L.up));
+    set(env, o, "down", matrix(L.down));
+    set(env, o, "qBias", ptr_value(env, L.q_bias));
+    set(env, o, "kBias", ptr_value(env, L.k_bias));
+    set(env, o, "vBias", ptr_value(env, L.v_bias));
+    set(env, o, "inputNorm", ptr_value(env, L.input_norm));
+    set(env, o, "postAttentionNorm", ptr_value(env, L.post_attention_norm));
+    napi_set_element(env, list, i, o);
+  }
+  set(env, d, "layer", list);
+  napi_create_object(env, &out);
+  set(env, out, "blob", ptr_value(env, blob));
+  set(env, out, "desc", d);
+  return out;
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   const napi_property_descriptor props[] = {
       {"abiVersion", nullptr, AbiVersion, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
@@ -677,6 +892,10 @@ napi_value Init(napi_env env, napi_value exports) {
       {"graphEnd", nullptr, GraphEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphLaunch", nullptr, GraphLaunch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphDestroy", nullptr, GraphDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"containerOpen", nullptr, ContainerOpen, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"containerClose", nullptr, ContainerClose, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"containerHeader", nullptr, ContainerHeader, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"containerLoad", nullptr, ContainerLoad, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
   return exports;

@@ -3,6 +3,6 @@
 'use strict';
 
 module.exports = Object.assign({}, require('./gpu.js'), require('./kernel.js'), require('./ops.js'),
-  require('./decoder.js'), {
+  require('./decoder.js'), require('./container.js'), {
   native: require('./native.js'),
 });

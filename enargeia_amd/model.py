@@ -18,7 +18,7 @@ import numpy as np
 from . import _lib
 from ._lib import ENC_SIGNED, check
 from .kernels import Device
-from .quant import QuantTensor, normal, quantize_sym
+from .quant import QuantTensor, normal, quantize_asym, quantize_sym
 
 
 @dataclass(frozen=True)
@@ -70,20 +70,33 @@ def seed_for(layer: int, slot: int, base: int = 0x5EED) -> int:
     return base ^ (layer * 16 + slot)
 
 
-def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED) -> HostModel:
+def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED, fmt: str = "sym") -> HostModel:
+    """Random-init weights of the model's shape. fmt "sym": the BASELINE formats (int4 with an
+    f32 scale per cfg.group weights, int8 per-row table, norms 1). fmt "reference": the
+    reference quantizer's formats (asymmetric int4 / int8 in blocks of cfg.group with zero-points,
+    quantize.py:74-103, --embed-dtype q8) and norm weights drawn around 1."""
     layers = []
+    ref = fmt == "reference"
     for layer in range(cfg.layers):
         mats = {}
         for slot, (name, rows, cols) in enumerate(projection_shapes(cfg)):
             w = normal(rows * cols, seed_for(layer, slot, base), 0.02)
-            mats[name] = quantize_sym(w, rows, cols, cfg.bits, cfg.group)
+            mats[name] = quantize_asym(w, rows, cols, cfg.bits, cfg.group) if ref else \
+                quantize_sym(w, rows, cols, cfg.bits, cfg.group)
         biases = {name: normal(rows, seed_for(layer, 8 + slot, base), 0.02).astype(np.float32)
                   for slot, (name, rows, _) in enumerate(projection_shapes(cfg)[:3])}
-        ones = np.ones(cfg.hidden, np.float32)
-        layers.append(HostLayer(mats, biases, ones, ones.copy()))
+        if ref:
+            n1 = (1.0 + normal(cfg.hidden, seed_for(layer, 12, base), 0.1)).astype(np.float32)
+            n2 = (1.0 + normal(cfg.hidden, seed_for(layer, 13, base), 0.1)).astype(np.float32)
+        else:
+            n1 = np.ones(cfg.hidden, np.float32)
+            n2 = n1.copy()
+        layers.append(HostLayer(mats, biases, n1, n2))
     table = normal(cfg.vocab * cfg.hidden, base ^ 0x1000, 0.02)
-    embedding = quantize_sym(table, cfg.vocab, cfg.hidden, 8, cfg.hidden)
-    return HostModel(cfg, layers, embedding, np.ones(cfg.hidden, np.float32))
+    embedding = quantize_asym(table, cfg.vocab, cfg.hidden, 8, cfg.group) if ref else \
+        quantize_sym(table, cfg.vocab, cfg.hidden, 8, cfg.hidden)
+    final = (1.0 + normal(cfg.hidden, base ^ 0x2000, 0.1)).astype(np.float32) if ref else np.ones(cfg.hidden, np.float32)
+    return HostModel(cfg, layers, embedding, final)
 
 
 # ---- the C structs --------------------------------------------------------------------------

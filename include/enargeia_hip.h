@@ -54,6 +54,9 @@ typedef enum eg_status {
   EG_ERR_DEVICE = -3,  /* HIP runtime failure (device lost, launch failure)             */
   EG_ERR_NOMEM = -4,   /* device allocation failed                                      */
   EG_ERR_STATE = -5,   /* call out of order (graph capture not begun, ...)              */
+  EG_ERR_FORMAT = -6,  /* a malformed .enargeia container (EnargeiaError, enargeia.ts:84) */
+  EG_ERR_IO = -7,      /* a file could not be opened or read                            */
+  EG_ERR_NOT_FOUND = -8, /* a named tensor is absent ("<name> is missing", weights.ts:397) */
 } eg_status;
 
 /* Encodings of the quantized code streams. */
@@ -324,6 +327,63 @@ EG_API int eg_decoder_step(eg_decoder* decoder, uint32_t* token_out);
 /* Captures one step as a hipGraph; later eg_decoder_step calls replay it (no host work per
  * launch; every per-token value already lives in device memory). */
 EG_API int eg_decoder_capture(eg_decoder* decoder);
+
+/* ---- the .enargeia container (enargeia.ts:1-50, 112-240; WeightStore.loadQuantized,
+ * weights.ts:299-471) ------------------------------------------------------------------------
+ * eg_container_open parses the prefix and JSON header on the host and applies the reference's
+ * checks with its messages (parseEnargeiaHeader / parseTensor, enargeia.ts:112-242), plus one of
+ * its own: the ranges must lie inside the file. It needs no device; pass ctx NULL to get the
+ * message from eg_last_error(NULL). eg_container_upload reads the blob into ONE device
+ * allocation (free it with eg_buf_free): a tensor's device address is that allocation plus its
+ * range's begin, 256-byte aligned like the file. eg_container_model_desc points a decoder
+ * description at the uploaded blob for a Qwen2 checkpoint (model.embed_tokens.weight tied,
+ * model.layers.N.{self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj}.weight, q/k/v biases,
+ * input/post_attention layernorms, model.norm.weight); layers, hidden, heads, kv_heads,
+ * intermediate and vocab come from the tensor shapes, the rest from the config. */
+
+typedef struct eg_container eg_container;
+
+typedef enum eg_dtype { EG_DTYPE_Q4 = 0, EG_DTYPE_Q8 = 1, EG_DTYPE_F32 = 2, EG_DTYPE_F16 = 3 } eg_dtype;
+
+#define EG_MAX_DIMS 8
+
+/* One header entry (QuantTensorInfo / F32TensorInfo / F16TensorInfo, enargeia.ts:37-71).
+ * Ranges are [begin, end) byte offsets within the blob; the unused ones are zero. */
+typedef struct eg_tensor_info {
+  const char* name; /* owned by the container */
+  int dtype;        /* eg_dtype */
+  int bits;         /* 4, 8, 32 or 16 */
+  uint32_t ndim;
+  uint32_t block_size, blocks_per_row; /* quantized only */
+  uint64_t shape[EG_MAX_DIMS];
+  uint64_t total_blocks;
+  uint64_t packed[2], scales[2], zeros[2]; /* quantized */
+  uint64_t data[2];                        /* F32 / F16 */
+} eg_tensor_info;
+
+/* EnargeiaHeader (enargeia.ts:73-82). */
+typedef struct eg_container_header {
+  uint32_t version, block_size, tensor_count, pad0;
+  uint64_t header_length, data_offset, blob_bytes, file_size;
+  const char* quantization; /* owned by the container; "unknown" when absent */
+} eg_container_header;
+
+/* What the container does not say about the model (ModelConfig, graph.ts:57-67). */
+typedef struct eg_model_config {
+  uint32_t head_dim, max_context;
+  float rms_eps, rope_theta;
+} eg_model_config;
+
+EG_API int eg_container_open(eg_context* ctx, const char* host_path, eg_container** out_container);
+EG_API int eg_container_close(eg_container* container);
+EG_API int eg_container_header_get(const eg_container* container, eg_container_header* out);
+EG_API int eg_container_tensor(const eg_container* container, uint32_t index, eg_tensor_info* out);
+EG_API int eg_container_find(const eg_container* container, const char* name, eg_tensor_info* out);
+EG_API int eg_container_upload(eg_context* ctx, const eg_container* container, void** out_blob);
+/* Fills `desc` and `layers[0 .. model layers)`; desc->layer points at `layers`. */
+EG_API int eg_container_model_desc(eg_context* ctx, const eg_container* container, const void* blob,
+                                   const eg_model_config* config, eg_model_desc* desc, eg_layer_desc* layers,
+                                   uint32_t layers_capacity);
 
 /* ---- capture (one hipGraph replaces one encoded command buffer, graph_decode.ts:442) ---- */
 EG_API int eg_graph_begin(eg_context* ctx);

@@ -57,6 +57,29 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, heads: int, kv_heads:
     return out.reshape(-1).astype(np.float32)
 
 
+def dequant_row(q, row: int) -> np.ndarray:
+    """One row of a quantized table as f32 (embed, ops.ts:222-233, with the gather's dequant,
+    embedding_variants.ts:56-63 / embed_gather_q4.wgsl): value = (code - zero) * scale per block
+    for the offset encoding, code * scale with two's-complement codes for the signed one. Nibble
+    n of a word is element 8w + n (byte b of a word is element 4w + b for int8)."""
+    per = 32 // q.bits
+    mask = (1 << q.bits) - 1
+    words = np.asarray(q.packed[row * q.cols // per:(row + 1) * q.cols // per], np.uint32)
+    shifts = np.arange(per, dtype=np.uint32) * q.bits
+    codes = ((words[:, None] >> shifts) & mask).reshape(-1).astype(np.int64)
+    bpr = q.cols // q.block_size
+    blocks = np.arange(row * bpr, (row + 1) * bpr)
+    scales = np.asarray(q.scales, np.float32)[blocks]
+    if q.zeros is None:  # signed: two's complement
+        codes = np.where(codes >= (1 << (q.bits - 1)), codes - (1 << q.bits), codes)
+        zero = np.zeros(bpr, np.int64)
+    else:
+        zw = np.asarray(q.zeros, np.uint32)[blocks // per]
+        zero = ((zw >> ((blocks % per) * q.bits).astype(np.uint32)) & mask).astype(np.int64)
+    vals = (codes.reshape(bpr, q.block_size) - zero[:, None]).astype(np.float32) * scales[:, None]
+    return vals.reshape(-1).astype(np.float32)
+
+
 def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     g64 = np.asarray(g, np.float64)
     return (g64 / (1.0 + np.exp(-g64)) * np.asarray(u, np.float64)).astype(np.float32)
@@ -76,11 +99,7 @@ class OracleDecoder:
         self.v = np.zeros(shape, np.float32)
 
     def embed(self, token: int) -> np.ndarray:
-        e = self.m.embedding  # int8 per row, two's-complement codes, 4 per u32
-        c = self.m.cfg
-        words = e.packed[token * c.hidden // 4:(token + 1) * c.hidden // 4]
-        codes = words.view(np.uint8).view(np.int8).astype(np.float32)
-        return (codes * e.scales[token]).astype(np.float32)
+        return dequant_row(self.m.embedding, token)
 
     def linear(self, x: np.ndarray, q, bias=None) -> np.ndarray:
         return gemv_threads(x, q, bias, self.threads)

@@ -13,7 +13,7 @@ const eg = require(path.join(__dirname, '..', '..', 'enargeia_amd', 'js', 'index
 const EXPORTS = ['abiVersion', 'create', 'destroy', 'sync', 'getStream', 'bufAlloc', 'bufFree', 'bufWrite', 'bufRead',
   'bufZero', 'matmulQ4Decode', 'matmulQ4Prefill', 'lmHead', 'lmHeadArgmax', 'argmax', 'sample', 'graphBegin',
   'graphEnd', 'graphLaunch', 'graphDestroy', 'decoderCreate', 'decoderReset', 'decoderStep', 'decoderCapture',
-  'decoderBuffers', 'decoderDestroy'];
+  'decoderBuffers', 'decoderDestroy', 'containerOpen', 'containerClose', 'containerHeader', 'containerLoad'];
 
 // A device stand-in: ComputeKernel needs only the limits before it records anything.
 const FAKE_DEVICE = { limits: { maxComputeWorkgroupsPerDimension: 65535 }, ctx: null };

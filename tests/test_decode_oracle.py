@@ -62,12 +62,31 @@ def test_silu_mul_closed_forms():
     np.testing.assert_allclose(out[3], 0.5 * 20.0, rtol=1e-7)  # silu(x) -> x for large x
 
 
-@pytest.fixture(scope="module")
-def tiny_model():
+@pytest.fixture(scope="module", params=["sym", "reference"])
+def tiny_model(request):
+    """Both weight formats: the BASELINE ones and the reference quantizer's (asymmetric codes with
+    zero-points, non-unit norm weights)."""
     from enargeia_amd.model import ModelConfig, synthetic_model
     cfg = ModelConfig(layers=2, hidden=128, heads=4, kv_heads=2, head_dim=32, intermediate=256, vocab=512,
-                      max_context=16)
-    return synthetic_model(cfg)
+                      max_context=16, group=64 if request.param == "reference" else 32)
+    return synthetic_model(cfg, fmt=request.param)
+
+
+@pytest.mark.parametrize("fmt", ["sym8_row", "sym4_g32", "asym8_g64", "asym4_g64"])
+def test_dequant_row_matches_the_c_dequantizer(fmt):
+    """oracle.decode.dequant_row (the embedding gather's row) against oracle.dequantize, the C
+    restatement of dequantElement (quant.ts:86-93), for every table format."""
+    from enargeia_amd.quant import normal, quantize_asym, quantize_sym
+    from oracle.decode import dequant_row
+    rows, cols = 24, 192
+    w = normal(rows * cols, 91, 0.02)
+    q = {"sym8_row": lambda: quantize_sym(w, rows, cols, 8, cols), "sym4_g32": lambda: quantize_sym(w, rows, cols, 4, 32),
+         "asym8_g64": lambda: quantize_asym(w, rows, cols, 8, 64),
+         "asym4_g64": lambda: quantize_asym(w, rows, cols, 4, 64)}[fmt]()
+    full = oracle.dequantize(oracle.QuantizedMatrix(q.rows, q.cols, q.block_size, q.bits, q.encoding, q.packed,
+                                                    q.scales, q.zeros))
+    for r in (0, 5, rows - 1):
+        np.testing.assert_array_equal(dequant_row(q, r), full[r].astype(np.float32))
 
 
 def test_oracle_step_matches_a_direct_float64_composition(tiny_model):

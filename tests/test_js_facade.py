@@ -110,3 +110,69 @@ def test_node_decoder_matches_python_decoder(tmp_path, device):
         dm.release()
     assert node_tokens["eager"] == py_tokens
     assert node_tokens["graph"] == py_tokens
+
+
+def _reference_checkpoint(directory, vocab=4096):
+    from enargeia_amd.container import qwen2_tensors, write_enargeia
+    from enargeia_amd.model import ModelConfig, synthetic_model
+
+    cfg = ModelConfig(layers=2, vocab=vocab, max_context=256, group=64)
+    host = synthetic_model(cfg, base=0xC0DE, fmt="reference")
+    path = os.path.join(directory, "qwen2-tiny.enargeia")
+    header = write_enargeia(path, qwen2_tensors(host))
+    return cfg, path, header
+
+
+@needs_node
+def test_node_reads_container_headers(tmp_path):
+    """readEnargeiaHeader from Node over the C++ parser: the same ranges the writer recorded, and
+    EnargeiaError for a foreign file."""
+    import json
+
+    from enargeia_amd.container import write_raw
+
+    _, path, header = _reference_checkpoint(str(tmp_path), vocab=512)
+    bad = os.path.join(str(tmp_path), "bad.enargeia")
+    write_raw(bad, b"{}", b"", magic=b"SAFETENS")
+    assert os.path.exists(ADDON), f"{ADDON} is not built (python -m enargeia_amd.build)"
+    res = subprocess.run([NODE, os.path.join(JS_TESTS, "container_cpu.test.js"), path, bad], cwd=ROOT,
+                         capture_output=True, text=True, timeout=60)
+    sys.stdout.write(res.stdout[-4000:])
+    assert res.returncode == 0, f"node exited {res.returncode}:\n{res.stdout[-3000:]}\n{res.stderr[-3000:]}"
+    got = json.loads(next(line[7:] for line in res.stdout.splitlines() if line.startswith("HEADER ")))
+    assert got["blockSize"] == 64 and got["quantization"] == header["quantization"]
+    assert set(got["tensors"]) == set(header["tensors"])
+    for name, entry in header["tensors"].items():
+        for field, rng in entry["offsets"].items():
+            assert got["tensors"][name][field] == rng, (name, field)
+        assert got["tensors"][name]["dtype"] == entry["dtype"]
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_container_decoder_matches_python(tmp_path, device):
+    """The same checkpoint loaded from Node (loadQuantized + Decoder) and from Python
+    (Container.load + Decoder) gives the same greedy tokens."""
+    import json
+
+    from enargeia_amd.container import Container
+    from enargeia_amd.model import Decoder
+
+    cfg, path, _ = _reference_checkpoint(str(tmp_path))
+    first, steps = 11, 10
+    print(f"node tests/js/container_gpu.test.js {path} {first} {steps}", flush=True)
+    res = subprocess.run([NODE, os.path.join(JS_TESTS, "container_gpu.test.js"), path, str(first), str(steps)],
+                         cwd=ROOT, capture_output=True, text=True, timeout=110)
+    sys.stdout.write(res.stdout[-4000:])
+    assert res.returncode == 0, f"node exited {res.returncode}:\n{res.stdout[-3000:]}\n{res.stderr[-3000:]}"
+    node_tokens = json.loads(next(line for line in res.stdout.splitlines() if line.startswith('{"tokens"')))
+    with Container(path) as c:
+        model = c.load(device, head_dim=64, max_context=256)
+    dec = Decoder(model)
+    try:
+        dec.reset(0, first)
+        py_tokens = [dec.step() for _ in range(steps)]
+    finally:
+        dec.close()
+        model.release()
+    assert node_tokens["tokens"] == py_tokens
