@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_decode_advance": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
     "eg_decoder_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "eg_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "eg_container_open": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "eg_container_close": (_i, [_vp]),
     "eg_container_header_get": (_i, [_vp, _vp]),

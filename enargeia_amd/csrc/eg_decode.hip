@@ -22,8 +22,10 @@ namespace {
 constexpr int kThreads = 256;
 
 // IEEE binary16 through the compiler's native _Float16 (round to nearest even on the way in).
-__device__ __forceinline__ float half_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t float_to_half(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+using egd::float_to_half;
+using egd::half_to_float;
+using egd::rope_apply;
+using egd::rope_table;
 
 // ---- embedding gather ------------------------------------------------------------------------
 
@@ -52,21 +54,6 @@ __global__ __launch_bounds__(kThreads) void embed_gather_kernel(const uint32_t* 
 }
 
 // ---- fused decode attention ------------------------------------------------------------------
-
-// RoPE (ops.ts:87-114): pairs (i, i + D/2) rotated by angle = position * theta^(-2i/D). The
-// angle, its cosine and sine are computed once per frequency, in double precision like the CPU
-// reference, and the rotation itself is evaluated in double too.
-template <int D>
-__device__ __forceinline__ void rope_table(double2* cs, uint32_t i, uint32_t position, float theta) {
-  const double angle = (double)position / pow((double)theta, (2.0 * i) / D);
-  cs[i] = make_double2(cos(angle), sin(angle));
-}
-template <int D>
-__device__ __forceinline__ void rope_apply(float* v, uint32_t i, const double2* cs) {
-  const double a = v[i], b = v[i + D / 2];
-  v[i] = (float)(a * cs[i].x - b * cs[i].y);
-  v[i + D / 2] = (float)(b * cs[i].x + a * cs[i].y);
-}
 
 constexpr uint32_t kMaxCombine = 1024;  // heads x chunks the one-workgroup combine holds in LDS
 

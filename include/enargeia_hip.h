@@ -328,6 +328,26 @@ EG_API int eg_decoder_step(eg_decoder* decoder, uint32_t* token_out);
  * launch; every per-token value already lives in device memory). */
 EG_API int eg_decoder_capture(eg_decoder* decoder);
 
+/* ---- chunked-prefill attention (cache_variants.ts:81-145 attn_scores / attn_apply with the
+ * softmax between; graph.ts:411-459 for the RoPE and cache writes before them) --------------
+ * The first six fields are the reference's 32-byte prefill Dims {queries, keys, queryBegin,
+ * heads, kvHeads, headDim} (keys = query_begin + queries, the causal extent of the chunk); the
+ * last two say what its pad words leave to other uniforms: the cache length and RoPE theta. */
+typedef struct eg_attention_prefill_dims {
+  uint32_t queries, keys, query_begin, heads, kv_heads, head_dim, max_context;
+  float theta;
+} eg_attention_prefill_dims;
+
+/* A chunk of `queries` rows at absolute positions [query_begin, query_begin + queries): q
+ * [queries][heads][64], k and v [queries][kv_heads][64] (the projections, f32, before RoPE).
+ * RoPE rotates q and k; k and v are appended to the f16 caches [max_context][kv_heads][64] at
+ * those positions; q_rope (f32, same shape as q) receives the rotated q scaled by 1/sqrt(64).
+ * Then out [queries][heads][64] = softmax(q k^T / sqrt(64), causal: key j <= query_begin + i)
+ * v over the cache. Matrix-core products in f16 with f32 accumulation; head_dim 64. */
+EG_API int eg_attention_prefill(eg_context* ctx, const float* q, const float* k, const float* v, uint16_t* k_cache,
+                                uint16_t* v_cache, float* q_rope, float* out,
+                                const eg_attention_prefill_dims* dims);
+
 /* ---- the .enargeia container (enargeia.ts:1-50, 112-240; WeightStore.loadQuantized,
  * weights.ts:299-471) ------------------------------------------------------------------------
  * eg_container_open parses the prefix and JSON header on the host and applies the reference's

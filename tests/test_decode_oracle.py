@@ -142,3 +142,28 @@ def test_oracle_step_matches_a_direct_float64_composition(tiny_model):
             h = h + W[li]["down"] @ (g / (1 + np.exp(-g)) * u)
         want = E @ norm(h, m.final_norm)
         np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-5 * np.sqrt(np.mean(want ** 2)))
+
+
+def test_prefill_attention_closed_forms_and_causality():
+    """The oracle's chunked prefill: the first query of an empty cache sees only its own key, so
+    its output is its own value row (f16-rounded) for every head of the group; perturbing a later
+    row of the chunk changes no earlier output (the causal mask); q_rope is RoPE(q) / sqrt(D)."""
+    from oracle.decode import prefill_attention
+    H, KV, D, n = 4, 2, 16, 6
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((n, H * D), dtype=np.float32)
+    k = rng.standard_normal((n, KV * D), dtype=np.float32)
+    v = rng.standard_normal((n, KV * D), dtype=np.float32)
+    kc = np.zeros((16, KV, D), np.float32)
+    vc = np.zeros((16, KV, D), np.float32)
+    qr, out = prefill_attention(q, k, v, kc, vc, 0, H, KV, D, 1e4)
+    v0 = f16_array(v[0]).reshape(KV, D)
+    for h in range(H):
+        np.testing.assert_allclose(out[0].reshape(H, D)[h], v0[h // (H // KV)], rtol=0, atol=1e-6)
+    np.testing.assert_array_equal(qr[0], (oracle.rope(q[0], 1, H, D, 1e4, 0) * np.float32(0.25)).astype(np.float32))
+    k2, v2 = k.copy(), v.copy()
+    k2[4] += 3.0
+    v2[4] -= 2.0
+    _, out2 = prefill_attention(q, k2, v2, np.zeros_like(kc), np.zeros_like(vc), 0, H, KV, D, 1e4)
+    np.testing.assert_array_equal(out2[:4], out[:4])
+    assert not np.array_equal(out2[4:], out[4:])
