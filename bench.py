@@ -16,6 +16,11 @@ Reported:
   per_gemv_us      single launches of each shape, cold;
   roofline         the dominant kernel (the K=896 batched launch), its algorithmic bytes over
                    its own HIP-event-timed duration on the library's stream;
+  prefill          config 3: the bf16-MFMA prefill GEMM at M = 256 / 128 (gate and down
+                   shapes) in TFLOP/s and % of the 2.5 PFLOP/s bf16 peak, and the chunk's
+                   f16-MFMA flash attention at the start and the end of a 2048 context;
+  decode           config 4: greedy tok/s at 2048 context (graph and eager, with and without
+                   the per-token readback);
   cpu_baseline     the reference's CPU loop (linearQ4, quant.ts:95-111) as restated by the
                    oracle, on a bounded sample, host cores stated.
 
@@ -312,6 +317,9 @@ def main() -> int:
         a.release()
         b.release()
 
+    # ---- prefill chunk (config 3) ----
+    prefill = prefill_numbers(dev, ev, stream, args)
+
     # ---- decode tok/s at 2048 context (config 4) ----
     decode = decode_throughput(dev, ev, stream, args)
 
@@ -346,6 +354,7 @@ def main() -> int:
                     "sampled_token_us": round(sampled_us, 2),
                     "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history"},
         "per_gemv_us": per_gemv,
+        "prefill": prefill,
         "decode_tok_s_2048": decode["tok_s"],
         "decode": decode,
         "roofline": roofline,
@@ -420,6 +429,85 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     dec.close()
     dm.release()
     return result
+
+
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix peak
+
+
+def prefill_numbers(dev, ev, stream, args) -> dict:
+    """the prefill chunk as a dense contraction. X [M x 896] (M = 256, 128)
+    through the int4 g32 gate (4864 x 896) and down (896 x 4864) weights on the bf16 MFMA GEMM
+    (eg_matmul_q4_prefill), and the chunk's attention on the f16 MFMA flash kernel
+    (eg_attention_prefill, 14 / 2 heads, head_dim 64) at the start of the context and at its
+    end (keys up to 2048). Median per-launch time of `steps` launches; TFLOP/s counts the
+    useful products only (2 M N K for the GEMM; 4 D per unmasked (query, key, head) for
+    attention)."""
+    import ctypes
+
+    from enargeia_amd import _lib, kernels as K, quant
+
+    rng = np.random.default_rng(17)
+    res = {"config": "BASELINE config 3: X [M x 896] through int4 g32 gate 896->4864 and down 4864->896, "
+                     "bf16 MFMA, f32 accumulate; chunk attention on f16 MFMA"}
+    gate = quant.quantize_sym(quant.normal(INTER * HIDDEN, 0x5EED ^ 0x300, 0.02), INTER, HIDDEN, 4, GROUP)
+    down = quant.quantize_sym(quant.normal(HIDDEN * INTER, 0x5EED ^ 0x301, 0.02), HIDDEN, INTER, 4, GROUP)
+    kern = K.ComputeKernel(dev, K.with_format(K.MATMUL_Q4_PREFILL, 4, K.ENC_SIGNED))
+    keep = []
+
+    def timed_each(fn, n):
+        marks = [ev.create() for _ in range(n + 1)]
+        for _ in range(3):
+            fn()
+        ev.record(marks[0], stream)
+        for i in range(n):
+            fn()
+            ev.record(marks[i + 1], stream)
+        ev.sync(marks[-1])
+        return float(np.median([ev.ms(marks[i], marks[i + 1]) for i in range(n)])) * 1e3
+
+    for m in (256, 128):
+        for name, q in (("gate", gate), ("down", down)):
+            x = dev.upload(rng.standard_normal((m, q.cols), dtype=np.float32))
+            bp, bs = dev.upload(q.packed), dev.upload(q.scales)
+            out = dev.buffer(m * q.rows * 4)
+            keep += [x, bp, bs, out]
+            u = kern.uniform()
+            u.write(K.matmul_q4_dims(m, q.rows, q.cols, False, GROUP, q.rows, 0))
+            bg = kern.bind_group([x, bp, bs, None, None, out, u])
+            us = timed_each(lambda: kern.encode(bg, (1, 1, 1)), args.steps)
+            tf = 2.0 * m * q.rows * q.cols / (us * 1e-6) / 1e12
+            res[f"gemm_{name}_m{m}"] = {"us": round(us, 2), "tflops": round(tf, 2),
+                                        "pct_of_bf16_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)}
+    log(f"prefill GEMM: {res}")
+
+    class Dims(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_uint32) for n in ("queries", "keys", "query_begin", "heads", "kv_heads",
+                                                   "head_dim", "max_context")] + [("theta", ctypes.c_float)]
+
+    H, KVH, D, CTX, M = 14, 2, 64, 2048, 256
+    q = dev.upload(rng.standard_normal((M, H * D), dtype=np.float32))
+    kvb = [dev.upload(rng.standard_normal((M, KVH * D), dtype=np.float32)) for _ in range(2)]
+    caches = [dev.upload(rng.standard_normal(CTX * KVH * D, dtype=np.float32).astype(np.float16).view(np.uint16))
+              for _ in range(2)]
+    qr, out = dev.buffer(M * H * D * 4), dev.buffer(M * H * D * 4)
+    keep += [q, qr, out] + kvb + caches
+    vp = ctypes.c_void_p
+    for begin in (0, CTX - M):
+        d = Dims(M, begin + M, begin, H, KVH, D, CTX, 1.0e6)
+
+        def call():
+            _lib.check(_lib.load().eg_attention_prefill(dev.ctx, vp(q.ptr), vp(kvb[0].ptr), vp(kvb[1].ptr),
+                                                        vp(caches[0].ptr), vp(caches[1].ptr), vp(qr.ptr),
+                                                        vp(out.ptr), ctypes.byref(d)), dev.ctx)
+
+        us = timed_each(call, args.steps)
+        pairs = H * sum(begin + i + 1 for i in range(M))
+        tf = 4.0 * D * pairs / (us * 1e-6) / 1e12
+        res[f"attention_m{M}_begin{begin}"] = {"us": round(us, 2), "tflops": round(tf, 3)}
+    log(f"prefill attention: { {k: v for k, v in res.items() if k.startswith('attention')} }")
+    for b in keep:
+        b.release()
+    return res
 
 
 CALIBRATION_BYTES = 256 << 20

@@ -2,17 +2,26 @@
 //   out[r*out_stride + col + out_offset] = sum_k x[r,k] * W[col,k] (+ bias[col])
 //
 // The prefill chunk (M = 128-256 queries) is the one dense contraction on the path. Each
-// workgroup owns a 64 x 64 output tile; its 4 waves each own 32 x 32 = 2 x 2 tiles of
-// v_mfma_f32_16x16x32_bf16. K is staged 64 at a time through LDS:
+// workgroup owns a 64 x 64 output tile and a slice of K; its 4 waves each own 32 x 32 = 2 x 2
+// tiles of v_mfma_f32_16x16x32_bf16. K is staged 64 at a time through LDS:
 //   * x (f32) is rounded to bf16 (round-to-nearest-even) on the way into LDS;
-//   * W is dequantized while staging, as the reference's prefill kernel does: one 16-byte chunk
-//     (32 int4 codes, one scale and zero-point) per thread, (code - zero) * scale in f32, then
-//     bf16 - so the codes cross HBM as int4 and each weight is unpacked once per tile, not once
-//     per MFMA that reads it.
+//   * W is dequantized while staging, as the reference's prefill kernel does: 16 int4 codes
+//     (8 bytes, one scale and zero-point) per thread, dequantized in f32, then bf16 - so the
+//     codes cross HBM as int4 and each weight is unpacked once per tile, not once per MFMA
+//     that reads it.
+// The loop is latency-bound at these sizes (a few MFMAs per staged block), so:
+//   * global loads run two blocks ahead of the LDS staging, in three register stages;
+//   * K is split over grid.z when the tile grid alone would leave the device idle (the down
+//     projection has 4 x 14 tiles at M = 256): each split writes f32 partials into the context's
+//     workspace and a second launch sums the splits in index order, plus the bias - the result
+//     does not depend on how the work was scheduled.
 // Rows are padded by 16 bytes in LDS so the 16 lanes that read one column of A (or B) hit
-// different banks. Accumulation is f32 inside the MFMA; the bias is added at the store.
-// Layouts the chunked staging cannot take (K or block size not a multiple of 32 codes,
-// int8 codes, unaligned streams) stage W element by element with the reference's indexing.
+// different banks. Accumulation is f32 inside the MFMA.
+// Layouts the chunked staging cannot take (K or block size not a multiple of 32 codes, int8
+// codes, unaligned streams, K not a multiple of 4) stage element by element with the
+// reference's indexing.
+#include <algorithm>
+
 #include "eg_internal.hpp"
 
 namespace {
@@ -24,6 +33,7 @@ constexpr int kTile = 64;   // M and N tile
 constexpr int kBK = 64;     // K staged per iteration
 constexpr int kPad = 8;     // bf16 elements of padding per LDS row
 constexpr int kLds = kBK + kPad;
+constexpr int kStages = 3;  // register stages of the chunked staging pipeline
 
 struct PrefillArgs {
   const float* x;
@@ -32,7 +42,8 @@ struct PrefillArgs {
   const uint32_t* zeros;
   const float* bias;
   float* out;
-  uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset;
+  float* partials;  // split-K: [splits][m][n] f32; NULL when grid.z == 1
+  uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset, k_per_split;
   int bits;
 };
 
@@ -43,6 +54,120 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
   return (uint16_t)(u >> 16);
 }
 
+// Two floats to a packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// One 64 x 64 block of x and of W held in registers between its global loads and its LDS
+// stores (chunked layout): x as 4 float4 per thread; W as 16 codes (8 bytes) per thread - row
+// tid / 4, codes 16 * (tid % 4) .. +16 of the block - with their block's scale and zero-point.
+struct Staged {
+  float4 x[4];
+  uint2 q;
+  float s;
+  float z;
+};
+
+// The four streams as buffer resources: an out-of-range offset reads zeros without touching
+// memory, so a block's edge needs no branch (a branch around a load makes the compiler wait
+// for it on the spot, which would serialize the stages).
+struct Streams {
+  __amdgpu_buffer_rsrc_t x, w, s, z;
+};
+constexpr uint32_t kOutside = 0x80000000u;  // an offset past every stream (streams < 2 GiB here)
+
+template <int ENC>
+__device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& r, uint32_t m0, uint32_t n0,
+                                           uint32_t k0, Staged& st) {
+  const uint32_t tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t idx = tid + i * 256u;  // 64 rows x 16 float4
+    const uint32_t row = m0 + (idx >> 4), kk = k0 + (idx & 15u) * 4u;
+    const uint32_t off = (row < a.m && kk < a.k) ? (row * a.k + kk) * 4u : kOutside;
+    const egd::u32x4 v = egd::load_b128(r.x, off);
+    st.x[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
+  const uint32_t nrow = n0 + (tid >> 2), kk = k0 + 16u * (tid & 3u);
+  const bool in = nrow < a.n && kk < a.k;
+  const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
+  const uint64_t codes = egd::load_b64(r.w, in ? (nrow * a.k + kk) / 2u : kOutside);
+  st.q = make_uint2((uint32_t)codes, (uint32_t)(codes >> 32));
+  st.s = egd::load_f32(r.s, in ? blk * 4u : kOutside);
+  if (ENC == EG_ENC_OFFSET_ZEROS) {
+    const uint32_t zw = egd::load_b32(r.z, in ? (blk / 8u) * 4u : kOutside);
+    st.z = (float)((zw >> (4 * (blk % 8))) & 0xFu);
+  } else {
+    st.z = 8.f;
+  }
+}
+
+template <int ENC>
+__device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds]) {
+  const uint32_t tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t idx = tid + i * 256u;
+    const uint32_t r = idx >> 4, c = (idx & 15u) * 4u;
+    *reinterpret_cast<uint2*>(&As[r][c]) =
+        make_uint2(pack_bf16(st.x[i].x, st.x[i].y), pack_bf16(st.x[i].z, st.x[i].w));
+  }
+  // (code - zero) * scale in f32, exactly the reference's dequantElement (the difference of two
+  // small integers is exact), then bf16.
+  const uint32_t d[2] = {st.q.x, st.q.y};
+  uint32_t packed[8];
+#pragma unroll
+  for (int w = 0; w < 2; w++) {
+    const uint32_t word = ENC == EG_ENC_SIGNED ? d[w] ^ 0x88888888u : d[w];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float c0 = (float)((word >> (4 * e)) & 0xFu), c1 = (float)((word >> (4 * e + 4)) & 0xFu);
+      packed[(w * 8 + e) / 2] = pack_bf16((c0 - st.z) * st.s, (c1 - st.z) * st.s);
+    }
+  }
+  uint4* dst = reinterpret_cast<uint4*>(&Bs[tid >> 2][16u * (tid & 3u)]);
+  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+}
+
+// Element-by-element staging for the layouts the chunked path does not take.
+template <int ENC>
+__device__ void stage_elements(const PrefillArgs& a, uint32_t m0, uint32_t n0, uint32_t k0, uint16_t (*As)[kLds],
+                               uint16_t (*Bs)[kLds]) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t per_word = 32u / (uint32_t)a.bits, mask = (1u << a.bits) - 1u;
+#pragma unroll 4
+  for (uint32_t e = tid; e < kTile * kBK; e += 256) {
+    const uint32_t r = e / kBK, c = e % kBK;
+    const uint32_t row = m0 + r, kk = k0 + c;
+    const float v = (row < a.m && kk < a.k) ? a.x[(size_t)row * a.k + kk] : 0.f;
+    As[r][c] = bf16_bits(v);
+  }
+#pragma unroll 4
+  for (uint32_t e = tid; e < kTile * kBK; e += 256) {
+    const uint32_t r = e / kBK, c = e % kBK;
+    const uint32_t nrow = n0 + r, kk = k0 + c;
+    float v = 0.f;
+    if (nrow < a.n && kk < a.k) {
+      const size_t flat = (size_t)nrow * a.k + kk;
+      uint32_t code = (a.packed[flat / per_word] >> (a.bits * (flat % per_word))) & mask;
+      const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
+      int32_t z;
+      if (ENC == EG_ENC_OFFSET_ZEROS) {
+        z = (int32_t)((a.zeros[blk / per_word] >> (a.bits * (blk % per_word))) & mask);
+      } else {
+        code ^= 1u << (a.bits - 1);
+        z = 1 << (a.bits - 1);
+      }
+      v = (float)((int32_t)code - z) * a.scales[blk];
+    }
+    Bs[r][c] = bf16_bits(v);
+  }
+}
+
 template <int ENC, bool CHUNKED>
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[kTile][kLds];
@@ -50,7 +175,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  const uint32_t per_word = 32u / (uint32_t)a.bits, mask = (1u << a.bits) - 1u;
+  const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
 
   f32x4 acc[2][2];
 #pragma unroll
@@ -58,66 +183,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (uint32_t k0 = 0; k0 < a.k; k0 += kBK) {
-    // x tile: 64 rows x 64 k, consecutive threads on consecutive k (coalesced).
-#pragma unroll 4
-    for (uint32_t e = tid; e < kTile * kBK; e += 256) {
-      const uint32_t r = e / kBK, c = e % kBK;
-      const uint32_t row = m0 + r, kk = k0 + c;
-      const float v = (row < a.m && kk < a.k) ? a.x[(size_t)row * a.k + kk] : 0.f;
-      As[r][c] = bf16_bits(v);
-    }
-    // W tile: 64 output features x 64 k, dequantized to bf16.
-    if (CHUNKED) {
-      if (tid < 128) {
-        const uint32_t r = tid >> 1, half = tid & 1u;
-        const uint32_t nrow = n0 + r, kk = k0 + half * 32;
-        uint16_t* dst = &Bs[r][half * 32];
-        if (nrow < a.n && kk < a.k) {
-          const uint4 q = *reinterpret_cast<const uint4*>(a.packed + ((size_t)nrow * a.k + kk) / 8);
-          const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
-          const float s = a.scales[blk];
-          int32_t z;
-          if (ENC == EG_ENC_OFFSET_ZEROS) z = (int32_t)((a.zeros[blk / 8] >> (4 * (blk % 8))) & 0xFu);
-          else z = 8;
-          const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-          for (int w = 0; w < 4; w++) {
-            const uint32_t word = ENC == EG_ENC_SIGNED ? d[w] ^ 0x88888888u : d[w];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-              const int32_t code = (int32_t)((word >> (4 * e)) & 0xFu);
-              dst[w * 8 + e] = bf16_bits((float)(code - z) * s);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 32; e++) dst[e] = 0;
-        }
-      }
-    } else {
-#pragma unroll 4
-      for (uint32_t e = tid; e < kTile * kBK; e += 256) {
-        const uint32_t r = e / kBK, c = e % kBK;
-        const uint32_t nrow = n0 + r, kk = k0 + c;
-        float v = 0.f;
-        if (nrow < a.n && kk < a.k) {
-          const size_t flat = (size_t)nrow * a.k + kk;
-          uint32_t code = (a.packed[flat / per_word] >> (a.bits * (flat % per_word))) & mask;
-          const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
-          int32_t z;
-          if (ENC == EG_ENC_OFFSET_ZEROS) {
-            z = (int32_t)((a.zeros[blk / per_word] >> (a.bits * (blk % per_word))) & mask);
-          } else {
-            code ^= 1u << (a.bits - 1);
-            z = 1 << (a.bits - 1);
-          }
-          v = (float)((int32_t)code - z) * a.scales[blk];
-        }
-        Bs[r][c] = bf16_bits(v);
-      }
-    }
-    __syncthreads();
+  auto mfma_block = [&]() {
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ks++) {
       const uint32_t kofs = ks * 32 + 8 * (lane >> 4);
@@ -134,7 +200,52 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    __syncthreads();
+  };
+
+  const uint32_t nblk = (kend - kbeg + kBK - 1) / kBK;
+  if (CHUNKED) {
+    // kStages register stages: block b lives in stage b % kStages and is stored to LDS while
+    // blocks b+1 .. b+kStages-1 are in flight (an iteration is ~0.3 us of staging and MFMAs;
+    // HBM latency is several of those). The steady-state loop covers whole groups of kStages
+    // blocks with no branch at all - loads unconditional, clamped to the last block - so the
+    // compiler's wait before each store counts exactly the loads issued after that stage's; the
+    // remaining blocks are already in flight and drain in a loop that issues no loads.
+    constexpr int S = kStages;
+    const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(a.packed, a.n * a.k / 2u),
+                     egd::buffer(a.scales, a.n * a.blocks_per_row * 4u),
+                     egd::buffer(a.zeros, ((a.n * a.blocks_per_row + 7u) / 8u) * 4u)};
+    Staged st[S];
+#pragma unroll
+    for (int u = 0; u + 1 < S; u++) load_block<ENC>(a, rs, m0, n0, kbeg + min((uint32_t)u, nblk - 1) * kBK, st[u]);
+    const uint32_t full = nblk / S;
+    for (uint32_t g = 0; g < full; g++) {
+#pragma unroll
+      for (int u = 0; u < S; u++) {
+        const uint32_t blk = g * S + u;
+        store_block<ENC>(st[u], As, Bs);
+        __syncthreads();
+        load_block<ENC>(a, rs, m0, n0, kbeg + min(blk + S - 1, nblk - 1) * kBK, st[(u + S - 1) % S]);
+        mfma_block();
+        __syncthreads();
+      }
+    }
+    const uint32_t rest = nblk - full * S;
+#pragma unroll
+    for (int u = 0; u + 1 < S; u++) {
+      if ((uint32_t)u < rest) {
+        store_block<ENC>(st[u], As, Bs);
+        __syncthreads();
+        mfma_block();
+        __syncthreads();
+      }
+    }
+  } else {
+    for (uint32_t k0 = kbeg; k0 < kend; k0 += kBK) {
+      stage_elements<ENC>(a, m0, n0, k0, As, Bs);
+      __syncthreads();
+      mfma_block();
+      __syncthreads();
+    }
   }
 
   // D layout of the 16x16 MFMA: lane l holds rows 4*(l/16) + e, column l % 16.
@@ -144,13 +255,31 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     for (int j = 0; j < 2; j++) {
       const uint32_t col = n0 + wn + j * 16 + (lane & 15);
       if (col >= a.n) continue;
-      const float b = a.bias ? a.bias[col] : 0.f;
+      const float b = (a.partials == nullptr && a.bias) ? a.bias[col] : 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const uint32_t row = m0 + wm + i * 16 + 4 * (lane >> 4) + e;
-        if (row < a.m) a.out[(size_t)row * a.out_stride + col + a.out_offset] = acc[i][j][e] + b;
+        if (row >= a.m) continue;
+        if (a.partials)
+          a.partials[((size_t)blockIdx.z * a.m + row) * a.n + col] = acc[i][j][e];
+        else
+          a.out[(size_t)row * a.out_stride + col + a.out_offset] = acc[i][j][e] + b;
       }
     }
+}
+
+// The split-K sum: splits added in index order, then the bias.
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __restrict__ partials,
+                                                             const float* __restrict__ bias, float* out, uint32_t m,
+                                                             uint32_t n, uint32_t splits, uint32_t out_stride,
+                                                             uint32_t out_offset) {
+  const size_t total = (size_t)m * n;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (uint32_t z = 0; z < splits; z++) acc += partials[(size_t)z * total + i];
+    const uint32_t row = (uint32_t)(i / n), col = (uint32_t)(i % n);
+    out[(size_t)row * out_stride + col + out_offset] = acc + (bias ? bias[col] : 0.f);
+  }
 }
 
 }  // namespace
@@ -180,17 +309,41 @@ extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint3
   if ((uint64_t)m * k >= (1ull << 40) || (uint64_t)n * dims->blocks_per_row >= (1ull << 32))
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u x %u x %u exceeds the index range", op, m, n, k);
   if (m == 0 || n == 0) return EG_OK;
-  const dim3 grid((n + kTile - 1) / kTile, (m + kTile - 1) / kTile);
-  if (grid.y > 65535) return eg::fail(ctx, EG_ERR_RANGE, "%s: m %u needs %u row tiles, over 65535", op, m, grid.y);
+  const uint32_t tiles_n = (n + kTile - 1) / kTile, tiles_m = (m + kTile - 1) / kTile;
+  if (tiles_m > 65535) return eg::fail(ctx, EG_ERR_RANGE, "%s: m %u needs %u row tiles, over 65535", op, m, tiles_m);
+  // Split K only where the tile grid leaves most CUs idle over a long reduction (the down
+  // projection: 4 x 14 tiles at M = 256, 76 blocks deep): the partial sums cost a second
+  // launch, so the split must save more block iterations than that launch costs. The f32
+  // partials live in the context's workspace.
+  const uint64_t tiles = (uint64_t)tiles_n * tiles_m;
+  const uint64_t blocks = (k + kBK - 1) / kBK;
+  uint64_t splits = 1;
+  if (blocks >= 32 && tiles < (uint64_t)ctx->cu_count)
+    splits = std::min<uint64_t>((ctx->cu_count + tiles - 1) / tiles, blocks / 8);
+  splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, eg::kPartialsBytes / ((uint64_t)m * n * 4)));
+  splits = std::max<uint64_t>(1, std::min<uint64_t>(splits, 65535));
+  uint32_t k_per_split = (uint32_t)((((uint64_t)k + splits - 1) / splits + kBK - 1) / kBK * kBK);
+  splits = (k + k_per_split - 1) / k_per_split;
+  const bool split = splits > 1;
   PrefillArgs a{x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
-                out, m, n, k, bs, dims->blocks_per_row, dims->out_stride, dims->out_offset, bits};
-  const bool chunked = bits == 4 && k % 32 == 0 && bs % 32 == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0;
+                out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
+                dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits};
+  const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
+  const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && k % 4 == 0 &&
+                       (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
+                       (reinterpret_cast<uintptr_t>(packed) & 7u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (encoding == EG_ENC_SIGNED) {
     if (chunked) hipLaunchKernelGGL((prefill_kernel<EG_ENC_SIGNED, true>), grid, dim3(256), 0, ctx->stream, a);
     else hipLaunchKernelGGL((prefill_kernel<EG_ENC_SIGNED, false>), grid, dim3(256), 0, ctx->stream, a);
   } else {
     if (chunked) hipLaunchKernelGGL((prefill_kernel<EG_ENC_OFFSET_ZEROS, true>), grid, dim3(256), 0, ctx->stream, a);
     else hipLaunchKernelGGL((prefill_kernel<EG_ENC_OFFSET_ZEROS, false>), grid, dim3(256), 0, ctx->stream, a);
+  }
+  if (split) {
+    const uint64_t total = (uint64_t)m * n;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);
+    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.bias, out, m, n,
+                       (uint32_t)splits, dims->out_stride, dims->out_offset);
   }
   return eg::check_launch(ctx, op);
 }

@@ -123,6 +123,11 @@ constexpr int kNonTemporal = 2;
 __device__ __forceinline__ u32x4 load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, kNonTemporal);
 }
+__device__ __forceinline__ uint64_t load_b64(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, offset, soffset, 0));
+  return (uint64_t)v.x | ((uint64_t)v.y << 32);
+}
 __device__ __forceinline__ uint32_t load_b32_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, kNonTemporal);
 }
