@@ -109,6 +109,9 @@ def main() -> int:
     ap.add_argument("--decode-profile", action="store_true",
                     help="only the config-4 decode steps, launched eagerly (for rocprofv3 kernel statistics of a "
                          "decode step; graph capture is left out of profiled runs)")
+    ap.add_argument("--prefill-profile", action="store_true",
+                    help="only the config-3 prefill GEMM and chunk-attention launches (for rocprofv3 kernel "
+                         "statistics of those kernels)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel and two calibration kernels of known size "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -123,6 +126,11 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe()
+    if args.prefill_profile:
+        dev = K.Device(0)
+        print(json.dumps(prefill_numbers(dev, HipEvents(), dev.stream, args)), flush=True)
+        dev.close()
+        return 0
     if args.decode_profile:
         dev = K.Device(0)
         ev = HipEvents()

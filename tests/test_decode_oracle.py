@@ -167,3 +167,24 @@ def test_prefill_attention_closed_forms_and_causality():
     _, out2 = prefill_attention(q, k2, v2, np.zeros_like(kc), np.zeros_like(vc), 0, H, KV, D, 1e4)
     np.testing.assert_array_equal(out2[:4], out[:4])
     assert not np.array_equal(out2[4:], out[4:])
+
+
+def test_prefill_attention_zero_queries_average_the_visible_rows():
+    """With q = 0 every score is 0, so query i of a chunk starting at `begin` returns the plain
+    mean of the value rows [0, begin + i] of its kv head (cached rows included): a mask that is
+    off by one, or a head mapped to the wrong kv head, changes the mean."""
+    from oracle.decode import prefill_attention
+    H, KV, D, n, begin = 6, 3, 8, 5, 7
+    rng = np.random.default_rng(11)
+    q = np.zeros((n, H * D), np.float32)
+    k = rng.standard_normal((n, KV * D), dtype=np.float32)
+    v = rng.standard_normal((n, KV * D), dtype=np.float32)
+    kc = f16_array(rng.standard_normal((32, KV, D), dtype=np.float32))
+    vc = f16_array(rng.standard_normal((32, KV, D), dtype=np.float32))
+    visible = vc.copy()
+    visible[begin:begin + n] = f16_array(v).reshape(n, KV, D)
+    _, out = prefill_attention(q, k, v, kc, vc, begin, H, KV, D, 1e4)
+    for i in range(n):
+        mean = visible[:begin + i + 1].astype(np.float64).mean(axis=0)
+        for h in range(H):
+            np.testing.assert_allclose(out[i].reshape(H, D)[h], mean[h // (H // KV)], rtol=1e-6, atol=1e-7)
