@@ -101,12 +101,44 @@ __device__ void combine_all(const float* partials, float* out, uint32_t heads, u
   }
 }
 
-// The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
-// statistics and the partial o, written to po/pm/pl.
+// Everything a workgroup reads from memory, loaded by its threads before anything else: the
+// chunk's K and V rows as 16-byte vectors (which rows exist does not depend on the position -
+// a chunk always lies inside the cache - so these loads need not wait for it; rows past the
+// live history are loaded too and never read), then one query element per thread and the new
+// key and value. All of it is in flight at once; the position arrives by a scalar load beside.
 template <int D, int CHUNK, int GMAX>
-__device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, uint32_t hs, uint32_t ng, uint32_t h0,
-                                       uint32_t chunks, const float* q, const float* k, const float* v,
-                                       uint16_t* k_cache, uint16_t* v_cache, float* po, float* pm, float* pl,
+struct Prefetch {
+  static constexpr uint32_t kVecs = D / 8;                      // 16-byte vectors per row
+  static constexpr uint32_t kLoads = CHUNK * kVecs / kThreads;  // per thread
+  static_assert(CHUNK * kVecs % kThreads == 0, "a chunk's rows split evenly over the threads");
+  static_assert(GMAX * D <= kThreads && D <= kThreads, "one query element per thread");
+  uint4 k[kLoads], v[kLoads];
+  float qv = 0.f, kn = 0.f, vn = 0.f;
+  __device__ __forceinline__ void load(const uint16_t* k_cache, const uint16_t* v_cache, uint32_t j0, uint32_t kv,
+                                       uint32_t kv_heads, const float* q, uint32_t h0, uint32_t ng, const float* kp,
+                                       const float* vp) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (uint32_t r = 0; r < kLoads; r++) {
+      const uint32_t i = tid + r * kThreads, row = i / kVecs, w = i % kVecs;
+      const size_t at = ((size_t)(j0 + row) * kv_heads + kv) * D + w * 8;
+      k[r] = *reinterpret_cast<const uint4*>(k_cache + at);
+      v[r] = *reinterpret_cast<const uint4*>(v_cache + at);
+    }
+    if (tid < ng * D) qv = q[(size_t)h0 * D + tid];
+    if (tid < D) {
+      kn = kp[(size_t)kv * D + tid];
+      vn = vp[(size_t)kv * D + tid];
+    }
+  }
+};
+
+// The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
+// statistics and the partial o, written to po/pm/pl, from what `pre` loaded.
+template <int D, int CHUNK, int GMAX>
+__device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, uint32_t hs, uint32_t ng,
+                                       uint32_t chunks, const Prefetch<D, CHUNK, GMAX>& pre, uint16_t* k_cache,
+                                       uint16_t* v_cache, float* po, float* pm, float* pl,
                                        const eg_attention_dims& d) {
   const uint32_t tid = threadIdx.x;
   const uint32_t live = min((uint32_t)CHUNK, pos + 1 - j0);
@@ -121,22 +153,20 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
 
   const float scale = 1.0f / sqrtf((float)D);
   const bool owns_new = pos < j0 + CHUNK;
-  const uint32_t cached = owns_new ? live - 1 : live;  // rows read from the cache
-  // Issue the cache reads first (16-byte loads, D/8 per row); their latency covers the RoPE.
-  for (uint32_t i = tid; i < cached * (D / 8); i += blockDim.x) {
-    const uint32_t r = i / (D / 8), w = i % (D / 8);
-    const size_t at = ((size_t)(j0 + r) * d.kv_heads + kv) * D + w * 8;
-    const uint4 kq = *reinterpret_cast<const uint4*>(k_cache + at);
-    const uint4 vq = *reinterpret_cast<const uint4*>(v_cache + at);
-    uint32_t* kd = reinterpret_cast<uint32_t*>(&ks[r][w * 8]);
-    uint32_t* vd = reinterpret_cast<uint32_t*>(&vs[r][w * 8]);
-    kd[0] = kq.x; kd[1] = kq.y; kd[2] = kq.z; kd[3] = kq.w;
-    vd[0] = vq.x; vd[1] = vq.y; vd[2] = vq.z; vd[3] = vq.w;
+  // The cached rows into LDS (every row of the chunk; the row at `pos`, stale in the cache, is
+  // replaced by the new one after the next barriers).
+#pragma unroll
+  for (uint32_t r = 0; r < Prefetch<D, CHUNK, GMAX>::kLoads; r++) {
+    const uint32_t i = tid + r * kThreads, row = i / (D / 8), w = i % (D / 8);
+    uint32_t* kd = reinterpret_cast<uint32_t*>(&ks[row][w * 8]);
+    uint32_t* vd = reinterpret_cast<uint32_t*>(&vs[row][w * 8]);
+    kd[0] = pre.k[r].x; kd[1] = pre.k[r].y; kd[2] = pre.k[r].z; kd[3] = pre.k[r].w;
+    vd[0] = pre.v[r].x; vd[1] = pre.v[r].y; vd[2] = pre.v[r].z; vd[3] = pre.v[r].w;
   }
-  for (uint32_t i = tid; i < ng * D; i += blockDim.x) qs[i / D][i % D] = q[(size_t)h0 * D + i];
+  if (tid < ng * D) qs[tid / D][tid % D] = pre.qv;
   if (tid < D) {
-    knew[tid] = k[(size_t)kv * D + tid];
-    vnew[tid] = v[(size_t)kv * D + tid];
+    knew[tid] = pre.kn;
+    vnew[tid] = pre.vn;
   }
   if (tid < D / 2) rope_table<D>(cs, tid, pos, d.theta);
   __syncthreads();
@@ -220,7 +250,6 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
                                                                     uint16_t* k_cache, uint16_t* v_cache,
                                                                     float* partials, uint32_t* counter, float* out,
                                                                     eg_attention_dims d) {
-  const uint32_t pos = position[0];
   const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
   const uint32_t c = blockIdx.x;
   const uint32_t chunks = gridDim.x;
@@ -229,8 +258,11 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
   const uint32_t gb = min(group, hs * share), ng = min(group, gb + share) - gb;  // heads [gb, gb + ng)
   const uint32_t j0 = c * CHUNK;
   const uint32_t tid = threadIdx.x;
-  // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
   const uint32_t h0 = kv * group + gb;
+  Prefetch<D, CHUNK, GMAX> pre;
+  pre.load(k_cache, v_cache, j0, kv, d.kv_heads, q, h0, ng, k, v);
+  const uint32_t pos = position[0];
+  // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
   float* po = partials + (size_t)h0 * D * chunks + c;
   float* pm = partials + (size_t)d.heads * D * chunks + (size_t)h0 * chunks + c;
   float* pl = pm + (size_t)d.heads * chunks;
@@ -245,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
       pl[(size_t)tid * chunks] = 0.f;
     }
   }
-  if (ng > 0 && !empty) attend<D, CHUNK, GMAX>(pos, j0, kv, hs, ng, h0, chunks, q, k, v, k_cache, v_cache, po, pm, pl, d);
+  if (ng > 0 && !empty) attend<D, CHUNK, GMAX>(pos, j0, kv, hs, ng, chunks, pre, k_cache, v_cache, po, pm, pl, d);
 
   // The combine, once, by the last workgroup to arrive: the fence releases this workgroup's
   // partials device-wide before it counts itself; the last one's fence acquires everyone's.

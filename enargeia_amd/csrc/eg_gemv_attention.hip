@@ -1,0 +1,11 @@
+// GEMV kernels with the attention-combine input stage (the o projection). The kernel template
+// is in eg_gemv_kernel.hpp; this unit only instantiates it, in parallel with the others.
+#include "eg_gemv_kernel.hpp"
+
+namespace eg_gemv {
+
+KernelFn pick_attention(int bits, int enc, int mode, int team, int cpl, int u) {
+  return pick_fused_format<EG_INPUT_ATTENTION>(bits, enc, mode, team, cpl, u);
+}
+
+}  // namespace eg_gemv

@@ -1,0 +1,714 @@
+// Decode-shape (M=1) quantized GEMV for the projections and the tied LM head.
+//
+// Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
+// (embedding_variants.ts:135-180). Same math, same three weight streams, read verbatim:
+//   out[row + out_offset] = sum_k x[k] * (code[row,k] - zero[blk]) * scale[blk] (+ bias[row])
+//
+// MI355X design (not the reference's one-workgroup-per-row tree):
+//   * A 16-byte chunk of a row (32 int4 or 16 int8 codes) is the unit of work; a chunk never
+//     straddles a quant block because block_size is a multiple of the chunk length on this
+//     path, so each chunk needs exactly one scale and one zero-point.
+//   * A team of TEAM lanes owns one row; lane t of the team owns chunks t, t+TEAM, ... (CPL of
+//     them). The x values those chunks multiply are loaded ONCE into VGPRs and reused for every
+//     row the lane visits, so activations cost no memory traffic in the steady state. A wave
+//     holds 64/TEAM rows; consecutive lanes read consecutive 16-byte chunks of a row, so each
+//     load instruction moves TEAM*16 contiguous bytes per row (128 B at TEAM=8, 1 KiB at 64).
+//   * Dequantization is in registers: the word is split into low/high nibble bytes with one
+//     opaque AND each, and v_cvt_f32_ubyte0..3 convert each byte straight to f32 - 2.4 VALU
+//     ops per int4 weight, below the ~3 ops/byte of issue the HBM rate allows.
+//     sum (code - zero) * x * scale is evaluated as scale * (sum code*x - zero * sum x), with
+//     sum x per chunk precomputed; two's-complement codes are XORed to offset-binary first.
+//   * The row total is a butterfly over the team (fixed order: deterministic); no atomics.
+//   * The fused-argmax variant keeps a (value, index) best per lane and reduces it per
+//     workgroup; a one-workgroup second launch reduces those partials to the greedy token, so
+//     the logits never need a second pass.
+//
+// This header holds the kernel template; eg_gemv.hip instantiates it for inputs given as a
+// vector (and holds the host side), eg_gemv_fused.hip for the fused input stages.
+#pragma once
+
+#include <algorithm>
+#include <cstdlib>
+#include <numeric>
+
+#include "eg_internal.hpp"
+
+namespace eg_gemv {
+
+constexpr int kWaves = 4;  // waves per workgroup (256 threads)
+constexpr uint32_t kMaxSegments = 256;  // matrices per batched plan (the table lives in LDS)
+constexpr uint32_t kMaxCombine = 1024;  // heads x chunks of an attention-combine input stage
+
+// One matrix of a batched launch, as the kernel sees it: its pointers and the range of wave
+// passes (RPW rows each) it occupies in the launch's pass space.
+struct DevSegment {
+  const uint4* w;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  float* out;
+  uint32_t pass_end;  // exclusive end of this segment's passes (cumulative)
+  uint32_t rows;
+  uint32_t out_offset;
+  uint32_t pad[3];
+};
+// 64 bytes: the table is copied into LDS with 16-byte loads.
+static_assert(sizeof(DevSegment) == 64, "DevSegment is copied as 16-byte vectors");
+constexpr uint32_t kTableLoads = kMaxSegments * sizeof(DevSegment) / 16 / 256;  // per thread
+// Plans of up to this many matrices carry their table in the kernel arguments: a wave then
+// knows its first tile before any memory round trip and can issue that tile's weight loads
+// ahead of the input stage (the decoder's q|k|v and gate|up plans are 3 and 2 matrices).
+constexpr uint32_t kInlineSegments = 4;
+
+struct GemvArgs {
+  const float* x;
+  const uint4* w;          // code stream viewed as 16-byte chunks, row-major
+  const float* scales;
+  const uint32_t* zeros;   // offset encoding only
+  const float* bias;       // nullable
+  float* out;              // nullable in the argmax variant
+  uint32_t n;              // rows
+  uint32_t chunks;         // 16-byte chunks per row
+  uint32_t chunks_per_block;
+  uint32_t blocks_per_row;
+  uint32_t out_offset;
+  uint32_t* partials;      // argmax: (value bits, index) per workgroup
+  const DevSegment* segs;  // batched launches only
+  uint32_t seg_count;
+  DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
+  uint32_t total_passes;   // tiles over all rows (all segments)
+  // input stage (eg_input_kind): how each workgroup produces x in LDS
+  int in_kind;
+  uint32_t early_tile;     // issue the first tile's loads before the input stage (when known)
+  const float* x2;         // norm weight / up
+  float eps;
+  uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
+};
+
+template <int BITS>
+struct Codes;
+
+template <>
+struct Codes<4> {
+  static constexpr int kPerChunk = 32;
+  static constexpr uint32_t kSignFlip = 0x88888888u;
+  static constexpr int kZeroPerWord = 8;
+  // sum over the 32 codes of a chunk of code * x, codes as unsigned nibbles.
+  static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[32]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
+      const uint32_t hi = egd::and_opaque(d[i] >> 4, 0x0F0F0F0Fu);
+      const float* xv = x + 8 * i;
+      a0 = fmaf(egd::ub0(lo), xv[0], a0);
+      a1 = fmaf(egd::ub0(hi), xv[1], a1);
+      a0 = fmaf(egd::ub1(lo), xv[2], a0);
+      a1 = fmaf(egd::ub1(hi), xv[3], a1);
+      a0 = fmaf(egd::ub2(lo), xv[4], a0);
+      a1 = fmaf(egd::ub2(hi), xv[5], a1);
+      a0 = fmaf(egd::ub3(lo), xv[6], a0);
+      a1 = fmaf(egd::ub3(hi), xv[7], a1);
+    }
+    return a0 + a1;
+  }
+};
+
+template <>
+struct Codes<8> {
+  static constexpr int kPerChunk = 16;
+  static constexpr uint32_t kSignFlip = 0x80808080u;
+  static constexpr int kZeroPerWord = 4;
+  static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[16]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float* xv = x + 4 * i;
+      a0 = fmaf(egd::ub0(d[i]), xv[0], a0);
+      a1 = fmaf(egd::ub1(d[i]), xv[1], a1);
+      a0 = fmaf(egd::ub2(d[i]), xv[2], a0);
+      a1 = fmaf(egd::ub3(d[i]), xv[3], a1);
+    }
+    return a0 + a1;
+  }
+};
+
+// kPlain: one matrix, logits/outputs stored. kArgmax: also a per-workgroup (max, index)
+// partial. kArgmaxOnly: the partial without storing the outputs. kBatched: a segment table of
+// matrices that share x and K.
+enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3 };
+
+template <int BITS, int U, int CPL>
+struct Loads {
+  egd::u32x4 q[U][CPL];
+  float s[U][CPL];
+  uint32_t zw[U][CPL];
+  float b[U];
+};
+
+// The input stage: every workgroup writes the K-element input vector into LDS (xs), from x
+// as given or through a fused producer - RMSNorm (the reduction is per workgroup, fixed order,
+// so every workgroup computes the same bits), SiLU(gate) * up, or the attention combine. IN
+// selects the stage at compile time, so each kernel carries only its own stage's registers.
+//
+// Each stage makes ONE round trip to memory in the common case: every global read it needs is
+// issued before any of them is used (16-byte buffer loads into registers; reads past the end
+// of a stream return zeros without touching memory), because the producers read what the
+// previous launch wrote, from L2 or beyond, and a chain of dependent round trips is what a
+// small launch's duration is made of. Inputs longer than a stage's register batch take a
+// second, looped pass for the remainder.
+template <int IN>
+__device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n4 = n / 4;  // n is a multiple of 32
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* y4 = reinterpret_cast<const float4*>(a.x2);
+  float4* out4 = reinterpret_cast<float4*>(xs);
+  auto f4 = [](const egd::u32x4& v) {
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  };
+  if (IN == EG_INPUT_RMSNORM) {
+    // x and the norm weight for up to kVec * 1024 inputs in one batch
+    constexpr uint32_t kVec = 2;
+    const auto xb = egd::buffer(a.x, n4 * 16u), wb = egd::buffer(a.x2, n4 * 16u);
+    egd::u32x4 xv[kVec], wv[kVec];
+#pragma unroll
+    for (uint32_t r = 0; r < kVec; r++) {
+      xv[r] = egd::load_b128(xb, (tid + r * 256u) * 16u);
+      wv[r] = egd::load_b128(wb, (tid + r * 256u) * 16u);
+    }
+    __shared__ float red[kWaves];
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t r = 0; r < kVec; r++) {
+      const float4 v = f4(xv[r]);
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) {
+      const float4 v = x4[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63u) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) total += red[w];
+    const float inv = 1.0f / sqrtf(total / (float)n + a.eps);
+#pragma unroll
+    for (uint32_t r = 0; r < kVec; r++) {
+      const uint32_t i = tid + r * 256u;
+      const float4 v = f4(xv[r]), w = f4(wv[r]);
+      if (i < n4) out4[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+    }
+    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) {
+      const float4 v = x4[i], w = y4[i];
+      out4[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+    }
+  } else if (IN == EG_INPUT_SILU_MUL) {
+    // gate and up for up to kVec * 1024 inputs in one batch (the intermediate width 4864 is 4.75
+    // vectors per thread)
+    constexpr uint32_t kVec = 5;
+    const auto gb = egd::buffer(a.x, n4 * 16u), ub = egd::buffer(a.x2, n4 * 16u);
+    egd::u32x4 gv[kVec], uv[kVec];
+#pragma unroll
+    for (uint32_t r = 0; r < kVec; r++) {
+      gv[r] = egd::load_b128(gb, (tid + r * 256u) * 16u);
+      uv[r] = egd::load_b128(ub, (tid + r * 256u) * 16u);
+    }
+    auto silu_mul = [](const float4& g, const float4& u) {
+      return make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                         g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+    };
+#pragma unroll
+    for (uint32_t r = 0; r < kVec; r++) {
+      const uint32_t i = tid + r * 256u;
+      if (i < n4) out4[i] = silu_mul(f4(gv[r]), f4(uv[r]));
+    }
+    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) out4[i] = silu_mul(x4[i], y4[i]);
+  } else if (IN == EG_INPUT_ATTENTION) {
+    // The combine of the attention partials (chunk-fastest: o[h][D][chunks], m[h][chunks],
+    // l[h][chunks]): every (head, chunk) pair's weight e^(m_c - M) / L is formed in LDS, then
+    // every output sums its chunks' partial o values with those weights - the same operations
+    // in the same order as egd::attention_combine_at. In the common case (<= 16 chunks of a
+    // multiple of 4, <= 1024 outputs) the (max, sum) statistics and every output's o values are
+    // all loaded at once, 4 outputs x 4 vectors per thread.
+    const uint32_t heads = a.att_heads, chunks = a.att_chunks, D = a.att_head_dim;
+    const uint32_t hcs = heads * chunks;
+    const float* m = a.x + (size_t)heads * D * chunks;
+    const float* l = m + hcs;
+    float* mval = scratch;
+    float* lval = scratch + hcs;
+    float* wts = scratch + 2 * hcs;
+    constexpr uint32_t kOut = 4, kQ = 4;  // outputs per thread, 16-byte vectors per output
+    const bool batched = (chunks & 3u) == 0 && chunks <= 4 * kQ && n <= kOut * 256u;
+    const uint32_t q4 = chunks / 4;
+    const auto ob = egd::buffer(a.x, n * chunks * 4u);
+    const auto mb = egd::buffer(m, hcs * 4u), lb = egd::buffer(l, hcs * 4u);
+    egd::u32x4 ov[kOut][kQ];
+    if (batched) {
+#pragma unroll
+      for (uint32_t r = 0; r < kOut; r++)
+#pragma unroll
+        for (uint32_t q = 0; q < kQ; q++)
+          ov[r][q] = q < q4 ? egd::load_b128(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
+    }
+    // (max, sum) statistics: kMaxCombine / 256 per thread at most
+    constexpr uint32_t kStat = kMaxCombine / 256;
+    float mv[kStat], lv[kStat];
+#pragma unroll
+    for (uint32_t r = 0; r < kStat; r++) {
+      mv[r] = __uint_as_float(egd::load_b32(mb, (tid + r * 256u) * 4u));
+      lv[r] = __uint_as_float(egd::load_b32(lb, (tid + r * 256u) * 4u));
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kStat; r++) {
+      const uint32_t hc = tid + r * 256u;
+      if (hc < hcs) {
+        mval[hc] = mv[r];
+        lval[hc] = lv[r];
+      }
+    }
+    __syncthreads();
+    for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
+      const uint32_t b = (hc / chunks) * chunks;
+      float M = -INFINITY;
+      for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, mval[b + c]);
+      float L = 0.f;
+      for (uint32_t c = 0; c < chunks; c++) L = fmaf(lval[b + c], expf(mval[b + c] - M), L);
+      wts[hc] = expf(mval[hc] - M) / L;
+    }
+    __syncthreads();
+    if (batched) {
+#pragma unroll
+      for (uint32_t r = 0; r < kOut; r++) {
+        const uint32_t i = tid + r * 256u;
+        const float* w = wts + (i / D) * chunks;
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t q = 0; q < kQ; q++) {
+          if (q < q4) {
+            const float4 v = f4(ov[r][q]);
+            acc = fmaf(v.x, w[4 * q + 0], acc);
+            acc = fmaf(v.y, w[4 * q + 1], acc);
+            acc = fmaf(v.z, w[4 * q + 2], acc);
+            acc = fmaf(v.w, w[4 * q + 3], acc);
+          }
+        }
+        if (i < n) xs[i] = acc;
+      }
+    } else {
+      for (uint32_t i = tid; i < n; i += blockDim.x) {
+        const float* o = a.x + (size_t)i * chunks;
+        const float* w = wts + (i / D) * chunks;
+        float acc = 0.f;
+        for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], w[c], acc);
+        xs[i] = acc;
+      }
+    }
+  } else {
+    // x as given: every load issued before any LDS write (8 per thread covers the longest
+    // rows, 256 chunks of 32 codes).
+    constexpr uint32_t kMaxLoads = 256 * 32 / 4 / 256;
+    const auto src = egd::buffer(a.x, n4 * 16u);
+    egd::u32x4 v[kMaxLoads];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxLoads; r++) v[r] = egd::load_b128(src, (tid + r * 256u) * 16u);
+    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxLoads; r++)
+      if (tid + r * 256u < n4) dst[tid + r * 256u] = v[r];
+  }
+}
+
+// One wave computes a tile of RPW * U rows per step: RPW teams of TEAM lanes side by side,
+// each team owning U rows (spaced RPW apart so that, for every (u, j), the wave's load is RPW
+// consecutive rows x TEAM consecutive 16-byte chunks).
+//
+// Each wave owns a contiguous range of tiles (so a batched launch looks its segment up once,
+// not per tile) and walks it NB tiles at a time with NB load buffers: the loads of tiles
+// i+1 .. i+NB-1 are in flight while tile i is computed. The bytes a CU keeps in flight are
+// what bounds a streaming kernel's bandwidth (latency x rate), and they cost VGPRs: x takes
+// CPL * EPC per lane, each buffer U * (5 * CPL + 1) more, so long rows (large x) trade
+// resident waves for a deeper pipeline per wave.
+// The steady-state loop has no memory operation under a branch, which lets the compiler wait
+// for exactly the tile it is about to use:
+//   * loads are unconditional - out-of-range rows read the last row, out-of-range chunk slots
+//     read chunk 0 (x is zero there), and a wave whose count is not a multiple of NB re-reads
+//     its last tile (an L2 hit) instead of branching around the spare buffers;
+//   * stores are unconditional - the team total is in every lane of the team, every lane
+//     stores it, and a clamped or repeated row stores the value that row already has.
+template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  using C = Codes<BITS>;
+  constexpr int EPC = C::kPerChunk;
+  constexpr int RPW = 64 / TEAM;
+  constexpr int TILE = RPW * U;
+  constexpr bool kStore = MODE != kArgmaxOnly;
+  constexpr bool kBest = MODE == kArgmax || MODE == kArgmaxOnly;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t t = lane % TEAM;
+  const uint32_t slot = lane / TEAM;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
+  const uint32_t total_waves = gridDim.x * kWaves;
+
+  // Dynamic LDS: x (chunks * EPC floats), then (batched plans of more than kInlineSegments
+  // matrices) the segment table. The workgroup copies x in once, so the activations cross L2
+  // once per workgroup rather than once per wave; each lane then keeps the chunks it owns in
+  // VGPRs for every row it visits.
+  extern __shared__ __align__(16) uint8_t smem[];
+  const uint32_t x_words = a.chunks * EPC;
+  const bool lds_table = MODE == kBatched && a.seg_count > kInlineSegments;  // wave-uniform
+  DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
+  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? a.seg_count : 0u) *
+                                                                      (uint32_t)sizeof(DevSegment));
+  // A table in LDS: its loads are all issued up front (kTableLoads per thread at most, reads
+  // past the table return zeros), so copying it costs one L2 round trip that overlaps the
+  // input stage's, not one per element.
+  egd::u32x4 tv[MODE == kBatched ? kTableLoads : 1];
+  const uint32_t table_vecs = a.seg_count * (uint32_t)(sizeof(DevSegment) / 16);
+  if (lds_table) {
+    const auto src = egd::buffer(a.segs, table_vecs * 16u);
+#pragma unroll
+    for (uint32_t r = 0; r < kTableLoads; r++) tv[r] = egd::load_b128(src, (threadIdx.x + r * 256u) * 16u);
+  }
+
+  // This lane's chunk slots: slot j covers chunk cj[j] of each row (chunk 0 past the row's end,
+  // where x is zero), in quant block bj[j].
+  uint32_t cj[CPL], bj[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; j++) {
+    const uint32_t c = t + j * TEAM;
+    cj[j] = c < a.chunks ? c : 0u;
+    bj[j] = cj[j] / a.chunks_per_block;
+  }
+
+  // Byte offsets of this lane's loads relative to its tile's first row: constant for the whole
+  // launch. The tile's own offset is wave-uniform and rides in the buffer instruction's scalar
+  // offset, so walking tiles costs scalar adds, not per-lane address arithmetic.
+  uint32_t qoff[U][CPL], soff[U][CPL], roff[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t lrow = u * RPW + slot;
+    roff[u] = lrow * 4u;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+      qoff[u][j] = (lrow * a.chunks + cj[j]) * 16u;
+      soff[u][j] = (lrow * a.blocks_per_row + bj[j]) * 4u;
+    }
+  }
+
+  // This wave's tiles: [begin, end), contiguous. (readfirstlane: the 64-bit divisions run on
+  // the vector unit, and the tile offsets derived from these must be known wave-uniform.)
+  const uint32_t begin =
+      __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * wave) / total_waves));
+  const uint32_t end =
+      __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * (wave + 1)) / total_waves));
+
+  // The matrix the issue side is walking (one for a plain launch; the current segment of a
+  // batched one). Rows are a multiple of TILE in a batched plan; a plain launch's last partial
+  // tile is shifted back to end at the last row (rows >= TILE), recomputing a few rows with
+  // identical results, so every access stays inside its stream.
+  struct Seg {
+    __amdgpu_buffer_rsrc_t w, s, z, b, o;
+    uint32_t rows, out_offset, first, end, has_bias;
+  };
+  auto make_seg = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
+                      uint32_t rows, uint32_t out_offset, uint32_t first, uint32_t seg_end) {
+    const uint32_t blocks = rows * a.blocks_per_row;
+    Seg r;
+    r.w = egd::buffer(w, rows * a.chunks * 16u);
+    r.s = egd::buffer(scales, blocks * 4u);
+    r.z = egd::buffer(zeros, ((blocks + C::kZeroPerWord - 1) / C::kZeroPerWord) * 4u);
+    r.has_bias = bias != nullptr;
+    // Without a bias the (discarded) bias load reads the scale stream, which has >= 1 entry per row.
+    r.b = r.has_bias ? egd::buffer(bias, rows * 4u) : r.s;
+    r.o = egd::buffer(out, (out_offset + rows) * 4u);
+    r.rows = rows;
+    r.out_offset = out_offset;
+    r.first = first;
+    r.end = seg_end;
+    return r;
+  };
+
+  // Batched: a segment is read into scalar registers from the kernel arguments (small plans)
+  // or from the LDS table (an LDS read waits on lgkmcnt, so switching segments never waits for
+  // the tile loads in flight, as a global load of the table would).
+  Seg cur = make_seg(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, 0, a.total_passes);
+  uint32_t seg = 0;
+  auto use_segment = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
+                         uint32_t rows, uint32_t pass_end, uint32_t out_offset) {
+    rows = __builtin_amdgcn_readfirstlane(rows);
+    const uint32_t seg_end = __builtin_amdgcn_readfirstlane(pass_end);
+    cur = make_seg(egd::uniform(w), egd::uniform(scales), egd::uniform(zeros), egd::uniform(bias), egd::uniform(out),
+                   rows, __builtin_amdgcn_readfirstlane(out_offset), seg_end - rows / TILE, seg_end);
+  };
+  auto load_segment = [&](uint32_t sidx) {
+    if (lds_table) {
+      const DevSegment& d = table[sidx];
+      use_segment(d.w, d.scales, d.zeros, d.bias, d.out, d.rows, d.pass_end, d.out_offset);
+    } else {
+      // kernel-argument table: a select per field over the few entries keeps every value scalar
+      auto sel = [&](auto DevSegment::*field) {
+        auto v = a.inline_segs[0].*field;
+#pragma unroll
+        for (uint32_t i = 1; i < kInlineSegments; i++) v = sidx == i ? a.inline_segs[i].*field : v;
+        return v;
+      };
+      use_segment(sel(&DevSegment::w), sel(&DevSegment::scales), sel(&DevSegment::zeros), sel(&DevSegment::bias),
+                  sel(&DevSegment::out), sel(&DevSegment::rows), sel(&DevSegment::pass_end),
+                  sel(&DevSegment::out_offset));
+    }
+  };
+  // The first segment whose pass_end exceeds `begin` = the number of segments ending at or
+  // before it (pass_end increases).
+  auto find_first_segment = [&]() {
+    uint32_t count = 0;
+    if (lds_table) {
+      // 64 entries per LDS read, counted with a ballot
+      for (uint32_t e0 = 0; e0 < a.seg_count; e0 += 64) {
+        const uint32_t e = e0 + lane;
+        const bool done = e < a.seg_count && table[e < a.seg_count ? e : 0].pass_end <= begin;
+        count += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(done));
+      }
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < kInlineSegments; i++) count += (i < a.seg_count && a.inline_segs[i].pass_end <= begin);
+    }
+    seg = __builtin_amdgcn_readfirstlane(count);
+    load_segment(seg);
+  };
+
+  // What computing a tile needs once its loads are in flight: where its rows are stored.
+  struct Pending {
+    __amdgpu_buffer_rsrc_t o;
+    uint32_t row0, out_offset, has_bias;
+  };
+  const uint32_t last = end - 1;
+
+  // Issues the loads of tile `tl` (clamped to the wave's last tile; tiles are visited in
+  // increasing order, so the segment cursor only moves forward).
+  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
+    tl = min(tl, last);
+    if (MODE == kBatched)
+      while (tl >= cur.end) load_segment(++seg);
+    // (readfirstlane pins the value to a scalar register: a scalar offset left in a vector
+    // register would make the compiler wrap every load in a per-lane loop.)
+    const uint32_t row0 = __builtin_amdgcn_readfirstlane(min((tl - cur.first) * TILE, cur.rows - TILE));
+    const uint32_t sq = row0 * (a.chunks * 16u);
+    const uint32_t ss = row0 * (a.blocks_per_row * 4u);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      L.b[u] = egd::load_f32(cur.b, roff[u], row0 * 4u);
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        L.q[u][j] = egd::load_b128_nt(cur.w, qoff[u][j], sq);
+        L.s[u][j] = egd::load_f32_nt(cur.s, soff[u][j], ss);
+        if (ENC == EG_ENC_OFFSET_ZEROS) {
+          const uint32_t blk = (row0 + u * RPW + slot) * a.blocks_per_row + bj[j];
+          L.zw[u][j] = egd::load_b32(cur.z, (blk / C::kZeroPerWord) * 4u);
+        }
+      }
+    }
+    P.o = cur.o;
+    P.row0 = row0;
+    P.out_offset = cur.out_offset;
+    P.has_bias = cur.has_bias;
+  };
+
+  // The weights do not depend on the input, so wherever the wave's first tile is known
+  // without the LDS table, its loads are issued before the input stage: their HBM latency
+  // then overlaps the input stage's own reads (which wait on what the previous launch wrote)
+  // instead of following them. The barriers below wait on LDS only (lgkmcnt), never on these.
+  Loads<BITS, U, CPL> L[NB];
+  Pending P[NB];
+  const bool early = !lds_table && a.early_tile;
+  if (early && begin < end) {
+    if (MODE == kBatched) find_first_segment();
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) issue(begin + b, L[b], P[b]);
+  }
+
+  produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch);
+  if (lds_table) {
+    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(table);
+#pragma unroll
+    for (uint32_t r = 0; r < kTableLoads; r++)
+      if (threadIdx.x + r * 256u < table_vecs) dst[threadIdx.x + r * 256u] = tv[r];
+  }
+  __syncthreads();
+
+  // This lane's activations: chunk slot j covers x[cj*EPC, cj*EPC + EPC), zero past the row.
+  float xr[CPL][EPC];
+  float sx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; j++) {
+    const bool valid = t + j * TEAM < a.chunks;
+    sx[j] = 0.f;
+    const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + (size_t)cj[j] * (EPC / 4);
+#pragma unroll
+    for (int e = 0; e < EPC / 4; e++) {
+      const egd::u32x4 v = xs[e];
+      xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
+      xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
+      xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
+      xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
+  }
+
+  if (!early && begin < end) {
+    if (MODE == kBatched) find_first_segment();
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) issue(begin + b, L[b], P[b]);
+  }
+
+  float best_v = -1.0e30f;
+  uint32_t best_i = a.out_offset;
+
+  auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too).
+      float acc = (t == 0 && P.has_bias) ? L.b[u] : 0.f;
+      const uint32_t row = P.row0 + u * RPW + slot;
+#pragma unroll
+      for (int j = 0; j < CPL; j++) {
+        uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
+        float z;
+        if (ENC == EG_ENC_OFFSET_ZEROS) {
+          const uint32_t blk = row * a.blocks_per_row + bj[j];
+          z = (float)((L.zw[u][j] >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
+        } else {
+          q.x ^= C::kSignFlip;
+          q.y ^= C::kSignFlip;
+          q.z ^= C::kSignFlip;
+          q.w ^= C::kSignFlip;
+          z = (float)(1 << (BITS - 1));
+        }
+        acc = fmaf(L.s[u][j], C::dot(q, xr[j]) - z * sx[j], acc);
+      }
+      const float v = egd::team_allsum<TEAM>(acc);
+      if (kStore) egd::store_f32(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
+      if (kBest) {
+        const uint32_t idx = row + P.out_offset;
+        const bool take = egd::better(v, idx, best_v, best_i);
+        best_v = take ? v : best_v;
+        best_i = take ? idx : best_i;
+      }
+    }
+  };
+
+  // The wave's range is one software pipeline over NB load buffers, NB tiles per iteration,
+  // with a single exit at the bottom: while tile i is computed, the loads of tiles
+  // i+1 .. i+NB-1 are in flight. Each buffer carries where its rows go, so the pipeline runs
+  // straight through segment boundaries (a boundary costs a few scalar reads, not a drain
+  // of the loads in flight). A count that is not a multiple of NB computes the wave's last
+  // tile again (same loads, same stores) rather than leaving the loop mid-body. With no path
+  // leaving the loop between an issue and its consumer, the compiler's wait counts stay exact -
+  // computing a tile waits only for that tile's loads, never for a later tile's.
+  // sched_barrier(0) after each issue keeps the scheduler from sinking the next tile's loads
+  // into the current tile's math.
+  if (begin < end) {
+    uint32_t tile = begin;
+    const uint32_t groups = (end - begin + NB - 1) / NB;
+    for (uint32_t g = 0; g < groups; g++) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const int nx = (b + NB - 1) % NB;
+        issue(tile + b + NB - 1, L[nx], P[nx]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(L[b], P[b]);
+      }
+      tile += NB;
+    }
+    // The last NB-1 issues are duplicates that nothing consumes; they complete before the
+    // wave ends.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
+  }
+
+  if (kBest) {
+    __shared__ float wv[kWaves];
+    __shared__ uint32_t wi[kWaves];
+    egd::team_argmax<64>(best_v, best_i);
+    if (lane == 0) {
+      wv[threadIdx.x >> 6] = best_v;
+      wi[threadIdx.x >> 6] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = wv[0];
+      uint32_t bi = wi[0];
+      for (int k = 1; k < kWaves; k++)
+        if (egd::better(wv[k], wi[k], bv, bi)) {
+          bv = wv[k];
+          bi = wi[k];
+        }
+      a.partials[2 * blockIdx.x + 0] = __float_as_uint(bv);
+      a.partials[2 * blockIdx.x + 1] = bi;
+    }
+  }
+}
+
+using KernelFn = void (*)(GemvArgs);
+
+// Fused input stages are instantiated for the shapes the library's shape choice produces (one
+// chunk slot per lane for rows of up to 64 chunks, a full-wave team with 2-4 slots for longer
+// rows; the pipeline depth is 2) and for the modes that take an input stage (batched plans and
+// the fused LM-head argmax). Each stage has its own translation unit, so they compile in
+// parallel: eg_gemv_rmsnorm.hip, eg_gemv_silu.hip, eg_gemv_attention.hip.
+#define EG_FUSED_SHAPES(X)                                                                                    \
+  X(8, 1, 1) X(8, 1, 2) X(16, 1, 1) X(16, 1, 2) X(32, 1, 1) X(32, 1, 2) X(64, 1, 1) X(64, 1, 2) X(64, 1, 4) \
+  X(64, 2, 1) X(64, 2, 2) X(64, 3, 1) X(64, 4, 1)
+
+template <int IN, int BITS, int ENC, int MODE>
+KernelFn pick_fused_shape(int team, int cpl, int u) {
+#define EG_FUSED_CASE(T, P, UU) \
+  if (team == T && cpl == P && u == UU) return gemv_kernel<BITS, ENC, T, P, UU, 2, MODE, IN>;
+  EG_FUSED_SHAPES(EG_FUSED_CASE)
+#undef EG_FUSED_CASE
+  return nullptr;
+}
+
+template <int IN, int BITS, int ENC>
+KernelFn pick_fused_mode(int mode, int team, int cpl, int u) {
+  if (mode == kBatched) return pick_fused_shape<IN, BITS, ENC, kBatched>(team, cpl, u);
+  if (mode == kArgmax) return pick_fused_shape<IN, BITS, ENC, kArgmax>(team, cpl, u);
+  if (mode == kArgmaxOnly) return pick_fused_shape<IN, BITS, ENC, kArgmaxOnly>(team, cpl, u);
+  return nullptr;
+}
+
+template <int IN>
+KernelFn pick_fused_format(int bits, int enc, int mode, int team, int cpl, int u) {
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_fused_mode<IN, 4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_fused_mode<IN, 4, EG_ENC_SIGNED>(mode, team, cpl, u);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_fused_mode<IN, 8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u);
+  return pick_fused_mode<IN, 8, EG_ENC_SIGNED>(mode, team, cpl, u);
+}
+
+// One per input-stage translation unit.
+KernelFn pick_rmsnorm(int bits, int enc, int mode, int team, int cpl, int u);
+KernelFn pick_silu_mul(int bits, int enc, int mode, int team, int cpl, int u);
+KernelFn pick_attention(int bits, int enc, int mode, int team, int cpl, int u);
+
+// The kernel for a fused input stage (in_kind RMSNORM, SILU_MUL or ATTENTION) of one
+// (format, mode, shape), or nullptr where none is instantiated.
+inline KernelFn pick_fused(int bits, int enc, int mode, int in_kind, int team, int cpl, int u, int nb) {
+  if (nb != 2) return nullptr;
+  if (in_kind == EG_INPUT_RMSNORM) return pick_rmsnorm(bits, enc, mode, team, cpl, u);
+  if (in_kind == EG_INPUT_SILU_MUL) return pick_silu_mul(bits, enc, mode, team, cpl, u);
+  if (in_kind == EG_INPUT_ATTENTION) return pick_attention(bits, enc, mode, team, cpl, u);
+  return nullptr;
+}
+
+}  // namespace eg_gemv
