@@ -107,7 +107,6 @@ int eg_create(int device, eg_context** out_ctx) {
     const int v = std::atoi(tpw);
     if (v >= 1 && v <= 64) ctx->fused_tiles_per_wave = (uint32_t)v;
   }
-  if (const char* early = std::getenv("EG_GEMV_EARLY_TILE")) ctx->gemv_early_tile = std::atoi(early) != 0;
   err = hipMalloc(&ctx->workspace, eg::kWorkspaceBytes);
   if (err != hipSuccess) {
     hipStreamDestroy(ctx->own_stream);

@@ -298,7 +298,7 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.segs = nullptr;
     a.seg_count = 0;
     a.total_passes = shape.tiles;
-    a.early_tile = ctx->gemv_early_tile;
+    a.any_bias = v.bias != nullptr;
     const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
@@ -381,6 +381,7 @@ int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, const u
 struct eg_gemv_plan {
   DevSegment* table = nullptr;  // device copy
   DevSegment inline_table[kInlineSegments] = {};  // host copy, passed in the arguments when count <= kInlineSegments
+  uint32_t any_bias = 0;                           // some segment has a bias
   uint32_t count = 0;
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
   int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
@@ -434,6 +435,7 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   }
   eg_gemv_plan* plan = new eg_gemv_plan();
   for (uint32_t i = 0; i < count && i < kInlineSegments; i++) plan->inline_table[i] = host[i];
+  for (uint32_t i = 0; i < count; i++) plan->any_bias |= segments[i].bias != nullptr;
   hipError_t err = hipMalloc(&plan->table, sizeof(DevSegment) * count);
   if (err == hipSuccess) err = hipMemcpy(plan->table, host, sizeof(DevSegment) * count, hipMemcpyHostToDevice);
   delete[] host;
@@ -482,7 +484,7 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   if (plan->count <= kInlineSegments)
     for (uint32_t i = 0; i < plan->count; i++) a.inline_segs[i] = plan->inline_table[i];
   a.total_passes = plan->total_passes;
-  a.early_tile = ctx->gemv_early_tile;
+  a.any_bias = plan->any_bias;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u, plan->nb, a.in_kind);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);

@@ -13,11 +13,13 @@
 //     row the lane visits, so activations cost no memory traffic in the steady state. A wave
 //     holds 64/TEAM rows; consecutive lanes read consecutive 16-byte chunks of a row, so each
 //     load instruction moves TEAM*16 contiguous bytes per row (128 B at TEAM=8, 1 KiB at 64).
-//   * Dequantization is in registers: the word is split into low/high nibble bytes with one
-//     opaque AND each, and v_cvt_f32_ubyte0..3 convert each byte straight to f32 - 2.4 VALU
-//     ops per int4 weight, below the ~3 ops/byte of issue the HBM rate allows.
+//   * Dequantization is in registers: the word is split into low and high nibble bytes in
+//     place (one masked flip each - a single v_bitop3 - the high nibbles left unshifted and
+//     their x values pre-divided by 16), and v_cvt_f32_ubyte0..3 convert each byte straight to
+//     f32: about 2.1 VALU ops per int4 weight. The VALU issue rate and the HBM rate are close
+//     on this path (16 lane-ops per clock per SIMD against ~3.3 bytes), so every op counts.
 //     sum (code - zero) * x * scale is evaluated as scale * (sum code*x - zero * sum x), with
-//     sum x per chunk precomputed; two's-complement codes are XORed to offset-binary first.
+//     sum x per chunk precomputed; two's-complement codes are flipped to offset binary.
 //   * The row total is a butterfly over the team (fixed order: deterministic); no atomics.
 //   * The fused-argmax variant keeps a (value, index) best per lane and reduces it per
 //     workgroup; a one-workgroup second launch reduces those partials to the greedy token, so
@@ -28,6 +30,7 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 #include <numeric>
 
@@ -79,7 +82,7 @@ struct GemvArgs {
   uint32_t total_passes;   // tiles over all rows (all segments)
   // input stage (eg_input_kind): how each workgroup produces x in LDS
   int in_kind;
-  uint32_t early_tile;     // issue the first tile's loads before the input stage (when known)
+  uint32_t any_bias;       // some matrix of the launch has a bias (else no bias loads are issued)
   const float* x2;         // norm weight / up
   float eps;
   uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
@@ -88,19 +91,33 @@ struct GemvArgs {
 template <int BITS>
 struct Codes;
 
+// Dot products of one 16-byte chunk of codes with the lane's x values, the encoding handled
+// inside: two's-complement codes are flipped to offset binary (value + 2^(BITS-1)) on the way.
 template <>
 struct Codes<4> {
   static constexpr int kPerChunk = 32;
-  static constexpr uint32_t kSignFlip = 0x88888888u;
   static constexpr int kZeroPerWord = 8;
-  // sum over the 32 codes of a chunk of code * x, codes as unsigned nibbles.
+  // x as the dot expects it: odd elements (the high nibble of each byte) divided by 16 - the
+  // high nibbles are masked in place, so their byte converts yield 16 * code, and the product
+  // 16 * code * (x / 16) equals code * x exactly (a power-of-two scale).
+  static __device__ __forceinline__ float x_scale(int e) { return (e & 1) ? 0.0625f : 1.0f; }
+  // sum over the 32 codes of (unsigned code) * x. Per word: one masked flip for the low
+  // nibbles and one for the high (v_bitop3 on gfx950: (d & mask) ^ flip), then a byte convert
+  // per code - about 2.1 VALU ops per weight.
+  template <int ENC>
   static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[32]) {
     const uint32_t d[4] = {q.x, q.y, q.z, q.w};
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
-      const uint32_t hi = egd::and_opaque(d[i] >> 4, 0x0F0F0F0Fu);
+      uint32_t lo, hi;
+      if (ENC == EG_ENC_SIGNED) {
+        lo = (d[i] & 0x0F0F0F0Fu) ^ 0x08080808u;
+        hi = (d[i] & 0xF0F0F0F0u) ^ 0x80808080u;
+      } else {
+        lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
+        hi = egd::and_opaque(d[i], 0xF0F0F0F0u);
+      }
       const float* xv = x + 8 * i;
       a0 = fmaf(egd::ub0(lo), xv[0], a0);
       a1 = fmaf(egd::ub0(hi), xv[1], a1);
@@ -118,13 +135,15 @@ struct Codes<4> {
 template <>
 struct Codes<8> {
   static constexpr int kPerChunk = 16;
-  static constexpr uint32_t kSignFlip = 0x80808080u;
   static constexpr int kZeroPerWord = 4;
+  static __device__ __forceinline__ float x_scale(int) { return 1.0f; }
+  template <int ENC>
   static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[16]) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    uint32_t d[4] = {q.x, q.y, q.z, q.w};
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+      if (ENC == EG_ENC_SIGNED) d[i] ^= 0x80808080u;
       const float* xv = x + 4 * i;
       a0 = fmaf(egd::ub0(d[i]), xv[0], a0);
       a1 = fmaf(egd::ub1(d[i]), xv[1], a1);
@@ -496,8 +515,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint32_t last = end - 1;
 
   // Issues the loads of tile `tl` (clamped to the wave's last tile; tiles are visited in
-  // increasing order, so the segment cursor only moves forward).
-  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
+  // increasing order, so the segment cursor only moves forward). WB: the launch has biases, so
+  // each row's bias is loaded with its codes (a launch without any skips those loads - a third
+  // of a tile's load instructions - in a separate copy of the loop, so no load sits under a
+  // branch).
+  auto issue = [&](auto WB, uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
     tl = min(tl, last);
     if (MODE == kBatched)
       while (tl >= cur.end) load_segment(++seg);
@@ -508,7 +530,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const uint32_t ss = row0 * (a.blocks_per_row * 4u);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      L.b[u] = egd::load_f32(cur.b, roff[u], row0 * 4u);
+      if constexpr (decltype(WB)::value) L.b[u] = egd::load_f32(cur.b, roff[u], row0 * 4u);
+      else L.b[u] = 0.f;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
         L.q[u][j] = egd::load_b128_nt(cur.w, qoff[u][j], sq);
@@ -524,19 +547,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     P.out_offset = cur.out_offset;
     P.has_bias = cur.has_bias;
   };
-
-  // The weights do not depend on the input, so wherever the wave's first tile is known
-  // without the LDS table, its loads are issued before the input stage: their HBM latency
-  // then overlaps the input stage's own reads (which wait on what the previous launch wrote)
-  // instead of following them. The barriers below wait on LDS only (lgkmcnt), never on these.
-  Loads<BITS, U, CPL> L[NB];
-  Pending P[NB];
-  const bool early = !lds_table && a.early_tile;
-  if (early && begin < end) {
-    if (MODE == kBatched) find_first_segment();
-#pragma unroll
-    for (int b = 0; b + 1 < NB; b++) issue(begin + b, L[b], P[b]);
-  }
 
   produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch);
   if (lds_table) {
@@ -565,38 +575,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
 #pragma unroll
     for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
-  }
-
-  if (!early && begin < end) {
-    if (MODE == kBatched) find_first_segment();
 #pragma unroll
-    for (int b = 0; b + 1 < NB; b++) issue(begin + b, L[b], P[b]);
+    for (int e = 0; e < EPC; e++) xr[j][e] *= C::x_scale(e);
   }
 
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
-  auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
+  auto compute = [&](auto WB, const Loads<BITS, U, CPL>& L, const Pending& P) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too).
-      float acc = (t == 0 && P.has_bias) ? L.b[u] : 0.f;
+      float acc = (decltype(WB)::value && t == 0 && P.has_bias) ? L.b[u] : 0.f;
       const uint32_t row = P.row0 + u * RPW + slot;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
+        const uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
         float z;
         if (ENC == EG_ENC_OFFSET_ZEROS) {
           const uint32_t blk = row * a.blocks_per_row + bj[j];
           z = (float)((L.zw[u][j] >> (BITS * (blk % C::kZeroPerWord))) & ((1u << BITS) - 1u));
         } else {
-          q.x ^= C::kSignFlip;
-          q.y ^= C::kSignFlip;
-          q.z ^= C::kSignFlip;
-          q.w ^= C::kSignFlip;
           z = (float)(1 << (BITS - 1));
         }
-        acc = fmaf(L.s[u][j], C::dot(q, xr[j]) - z * sx[j], acc);
+        acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j]) - z * sx[j], acc);
       }
       const float v = egd::team_allsum<TEAM>(acc);
       if (kStore) egd::store_f32(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
@@ -619,22 +621,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // computing a tile waits only for that tile's loads, never for a later tile's.
   // sched_barrier(0) after each issue keeps the scheduler from sinking the next tile's loads
   // into the current tile's math.
-  if (begin < end) {
+  auto pipeline = [&](auto WB) {
+    if (MODE == kBatched) find_first_segment();
+    Loads<BITS, U, CPL> L[NB];
+    Pending P[NB];
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) issue(WB, begin + b, L[b], P[b]);
     uint32_t tile = begin;
     const uint32_t groups = (end - begin + NB - 1) / NB;
     for (uint32_t g = 0; g < groups; g++) {
 #pragma unroll
       for (int b = 0; b < NB; b++) {
         const int nx = (b + NB - 1) % NB;
-        issue(tile + b + NB - 1, L[nx], P[nx]);
+        issue(WB, tile + b + NB - 1, L[nx], P[nx]);
         __builtin_amdgcn_sched_barrier(0);
-        compute(L[b], P[b]);
+        compute(WB, L[b], P[b]);
       }
       tile += NB;
     }
     // The last NB-1 issues are duplicates that nothing consumes; they complete before the
     // wave ends.
     __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
+  };
+  if (begin < end) {
+    if (a.any_bias)
+      pipeline(std::true_type{});
+    else
+      pipeline(std::false_type{});
   }
 
   if (kBest) {

@@ -29,10 +29,6 @@ struct eg_context {
   int gemv_override[4] = {0, 0, 0, 0};
   // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 2).
   uint32_t fused_tiles_per_wave = 2;
-  // Whether a GEMV issues its first tile's weight loads before its input stage, where the tile
-  // is known without the LDS segment table (EG_GEMV_EARLY_TILE=0/1, default 0: measured slower
-  // on MI355X for the decoder's launches).
-  uint32_t gemv_early_tile = 0;
   // Resident workgroups per CU of each kernel launched through this context (from
   // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
   // the device.
