@@ -71,13 +71,15 @@ __device__ void combine_all(const float* partials, float* out, uint32_t heads, u
     lval[hc] = l[hc];
   }
   __syncthreads();
-  for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
-    const uint32_t b = (hc / chunks) * chunks;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, mval[b + c]);
-    float L = 0.f;
-    for (uint32_t c = 0; c < chunks; c++) L = fmaf(lval[b + c], expf(mval[b + c] - M), L);
-    wts[hc] = expf(mval[hc] - M) / L;
+  // a head's statistics in a power-of-two group of lanes: M and L are butterflies across it
+  // (the order egd::combine_stats reproduces on one thread)
+  const uint32_t G = egd::combine_group(chunks);
+  for (uint32_t p0 = 0; p0 < heads * G; p0 += blockDim.x) {
+    const uint32_t p = p0 + tid, c = p % G, hc = (p / G) * chunks + c;
+    const bool valid = p < heads * G && c < chunks;
+    float M, e, L;
+    egd::group_stats(G, valid, valid ? mval[hc] : 0.f, valid ? lval[hc] : 0.f, M, e, L);
+    if (valid) wts[hc] = e / L;
   }
   __syncthreads();
   for (uint32_t i = tid; i < n; i += blockDim.x) {
@@ -332,6 +334,9 @@ int check_attention(eg_context* ctx, const char* op, const eg_attention_dims* d)
   if ((uint64_t)d->heads * (d->max_context / d->chunk) > kMaxCombine)
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads x %u chunks exceed the combine's %u", op, d->heads,
                     d->max_context / d->chunk, kMaxCombine);
+  if (d->max_context / d->chunk > egd::kMaxChunks)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %u chunks per head exceed %u", op, d->max_context / d->chunk,
+                    egd::kMaxChunks);
   if (d->chunk != 64 && d->chunk != 128)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: chunk %u (64 or 128 are supported)", op, d->chunk);
   if (d->max_context == 0 || d->max_context % d->chunk != 0)

@@ -184,7 +184,7 @@ struct QuantView {
 
 // LDS the input stage needs beyond x and the segment table.
 uint32_t input_scratch_bytes(const GemvArgs& a) {
-  return a.in_kind == EG_INPUT_ATTENTION ? 3u * a.att_heads * a.att_chunks * 4u : 0u;
+  return a.in_kind == EG_INPUT_ATTENTION ? a.att_heads * a.att_chunks * 4u : 0u;
 }
 
 // Validates an input stage against the GEMV's K and copies it into the kernel arguments.
@@ -214,9 +214,10 @@ int apply_input(eg_context* ctx, const char* op, const eg_gemv_input* in, uint32
       if (d.heads * d.head_dim != k)
         return eg::fail(ctx, EG_ERR_INVALID, "%s: attention output %u x %u does not match k = %u", op, d.heads,
                         d.head_dim, k);
-      if ((uint64_t)d.heads * (d.max_context / d.chunk) > kMaxCombine)
-        return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads x %u chunks exceed the combine stage's %u", op, d.heads,
-                        d.max_context / d.chunk, kMaxCombine);
+      if ((uint64_t)d.heads * egd::combine_group(d.max_context / d.chunk) > kMaxCombine ||
+          d.max_context / d.chunk > egd::kMaxChunks)
+        return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads x %u chunks exceed the combine stage's %u (at most %u chunks)",
+                        op, d.heads, d.max_context / d.chunk, kMaxCombine, egd::kMaxChunks);
       a.att_heads = d.heads;
       a.att_kv_heads = d.kv_heads;
       a.att_head_dim = d.head_dim;

@@ -256,18 +256,19 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) out4[i] = silu_mul(x4[i], y4[i]);
   } else if (IN == EG_INPUT_ATTENTION) {
     // The combine of the attention partials (chunk-fastest: o[h][D][chunks], m[h][chunks],
-    // l[h][chunks]): every (head, chunk) pair's weight e^(m_c - M) / L is formed in LDS, then
-    // every output sums its chunks' partial o values with those weights - the same operations
-    // in the same order as egd::attention_combine_at. In the common case (<= 16 chunks of a
-    // multiple of 4, <= 1024 outputs) the (max, sum) statistics and every output's o values are
-    // all loaded at once, 4 outputs x 4 vectors per thread.
+    // l[h][chunks]): every (head, chunk) pair's weight e^(m_c - M) / L goes into LDS, then every
+    // output sums its chunks' partial o values with those weights - the same operations as
+    // egd::attention_combine_at. A head's statistics sit in a power-of-two group of lanes
+    // (G >= chunks), so M and L are butterflies across the group (L in egd::combine_stats's
+    // pairwise tree order): one exp per lane instead of a serial loop over the chunks. In the
+    // common case (<= 16 chunks of a multiple of 4, <= 1024 outputs) the statistics and every
+    // output's o values are all loaded at once, 4 outputs x 4 vectors per thread.
     const uint32_t heads = a.att_heads, chunks = a.att_chunks, D = a.att_head_dim;
     const uint32_t hcs = heads * chunks;
+    const uint32_t G = egd::combine_group(chunks);  // <= 64 and heads * G <= kMaxCombine (host-checked)
     const float* m = a.x + (size_t)heads * D * chunks;
     const float* l = m + hcs;
-    float* mval = scratch;
-    float* lval = scratch + hcs;
-    float* wts = scratch + 2 * hcs;
+    float* wts = scratch;
     constexpr uint32_t kOut = 4, kQ = 4;  // outputs per thread, 16-byte vectors per output
     const bool batched = (chunks & 3u) == 0 && chunks <= 4 * kQ && n <= kOut * 256u;
     const uint32_t q4 = chunks / 4;
@@ -281,30 +282,28 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
         for (uint32_t q = 0; q < kQ; q++)
           ov[r][q] = q < q4 ? egd::load_b128(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
     }
-    // (max, sum) statistics: kMaxCombine / 256 per thread at most
+    // statistics: thread p = tid + 256 r holds head p / G, chunk p % G (chunks past the head's
+    // count, and groups past the last head, read nothing: m = -inf, l = 0)
     constexpr uint32_t kStat = kMaxCombine / 256;
     float mv[kStat], lv[kStat];
+    uint32_t sidx[kStat];
+    bool sval[kStat];
 #pragma unroll
     for (uint32_t r = 0; r < kStat; r++) {
-      mv[r] = __uint_as_float(egd::load_b32(mb, (tid + r * 256u) * 4u));
-      lv[r] = __uint_as_float(egd::load_b32(lb, (tid + r * 256u) * 4u));
+      const uint32_t p = tid + r * 256u, c = p % G;
+      sval[r] = p < heads * G && c < chunks;
+      sidx[r] = (p / G) * chunks + c;
+      const uint32_t off = sval[r] ? sidx[r] * 4u : 0xFFFFFFF0u;  // past the stream: reads zero
+      mv[r] = __uint_as_float(egd::load_b32(mb, off));
+      lv[r] = __uint_as_float(egd::load_b32(lb, off));
     }
 #pragma unroll
     for (uint32_t r = 0; r < kStat; r++) {
-      const uint32_t hc = tid + r * 256u;
-      if (hc < hcs) {
-        mval[hc] = mv[r];
-        lval[hc] = lv[r];
+      if (r * 256u < heads * G) {  // workgroup-uniform: only the rounds that hold a head
+        float M, e, L;
+        egd::group_stats(G, sval[r], mv[r], lv[r], M, e, L);
+        if (sval[r]) wts[sidx[r]] = e / L;
       }
-    }
-    __syncthreads();
-    for (uint32_t hc = tid; hc < hcs; hc += blockDim.x) {
-      const uint32_t b = (hc / chunks) * chunks;
-      float M = -INFINITY;
-      for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, mval[b + c]);
-      float L = 0.f;
-      for (uint32_t c = 0; c < chunks; c++) L = fmaf(lval[b + c], expf(mval[b + c] - M), L);
-      wts[hc] = expf(mval[hc] - M) / L;
     }
     __syncthreads();
     if (batched) {

@@ -203,20 +203,86 @@ __device__ __forceinline__ float team_allsum(float v) {
   return v;
 }
 
-// One element of the attention output from flash-decoding partials laid out chunk-fastest:
-// o[h][D][chunks], then m[h][chunks], then l[h][chunks]. out[h*D + e] =
-// sum_c o_c[e] * (e^(m_c - M) / L), M = max_c m_c, L = sum_c l_c e^(m_c - M); chunks in order, so
-// deterministic, and the same operations in the same order as the GEMV input stage's combine.
+// Max across a team of TEAM consecutive lanes with the result in every lane: the butterfly of
+// team_allsum (DPP within rows of 16, a swizzle across 32, readlanes across 64) with fmaxf.
+template <int TEAM>
+__device__ __forceinline__ float team_allmax(float v) {
+  auto step = [&](float o) { v = fmaxf(v, o); };
+  if (TEAM >= 2) step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));
+  if (TEAM >= 4) step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)));
+  if (TEAM >= 8) step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true)));
+  if (TEAM >= 16) step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true)));
+  if (TEAM >= 32) step(__builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+  if (TEAM >= 64) {
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    v = fmaxf(lo, hi);
+  }
+  return v;
+}
+
+// Combining flash-decoding partials (laid out chunk-fastest: o[h][D][chunks], then
+// m[h][chunks], then l[h][chunks]) needs, per head, M = max_c m_c and the normaliser
+// L = sum_c l_c e^(m_c - M). The products l_c e^(m_c - M) are summed as a balanced pairwise tree
+// in chunk order over 64 slots (chunks past the head's count add zeros, which changes no bit):
+// the tree a butterfly over a power-of-two group of lanes computes, so a wave that reduces a
+// head's chunks across its lanes and a thread that does it alone produce the same bits. At most
+// kMaxChunks chunks per head.
+constexpr uint32_t kMaxChunks = 64;
+
+// The smallest power of two >= chunks: the lanes one head's statistics span in a butterfly.
+__host__ __device__ constexpr uint32_t combine_group(uint32_t chunks) {
+  uint32_t g = 1;
+  while (g < chunks) g <<= 1;
+  return g;
+}
+
+// One thread: (M, L) of one head from its m and l rows.
+__device__ __forceinline__ void combine_stats(const float* m, const float* l, uint32_t chunks, float& M, float& L) {
+  M = -INFINITY;
+  for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, m[c]);
+  float t[kMaxChunks];
+#pragma unroll
+  for (uint32_t c = 0; c < kMaxChunks; c++) t[c] = c < chunks ? l[c] * expf(m[c] - M) : 0.f;
+#pragma unroll
+  for (uint32_t w = kMaxChunks; w > 1; w >>= 1)
+#pragma unroll
+    for (uint32_t c = 0; c < w / 2; c++) t[c] = t[2 * c] + t[2 * c + 1];
+  L = t[0];
+}
+
+// The same statistics with one head's chunks spread over a group of G lanes (G =
+// combine_group(chunks), groups aligned within a wave, every lane active): M by a max
+// butterfly, e = e^(m - M) per lane, L by the sum butterfly - the pairwise tree combine_stats
+// computes on one thread. Lanes past the head's chunks pass valid = false.
+template <int G>
+__device__ __forceinline__ void group_stats_of(bool valid, float m, float l, float& M, float& e, float& L) {
+  M = team_allmax<G>(valid ? m : -INFINITY);
+  e = expf(m - M);
+  L = team_allsum<G>(valid ? l * e : 0.f);
+}
+__device__ __forceinline__ void group_stats(uint32_t G, bool valid, float m, float l, float& M, float& e, float& L) {
+  switch (G) {
+    case 1: group_stats_of<1>(valid, m, l, M, e, L); break;
+    case 2: group_stats_of<2>(valid, m, l, M, e, L); break;
+    case 4: group_stats_of<4>(valid, m, l, M, e, L); break;
+    case 8: group_stats_of<8>(valid, m, l, M, e, L); break;
+    case 16: group_stats_of<16>(valid, m, l, M, e, L); break;
+    case 32: group_stats_of<32>(valid, m, l, M, e, L); break;
+    default: group_stats_of<64>(valid, m, l, M, e, L); break;
+  }
+}
+
+// One element of the attention output: out[h*D + e] = sum_c o_c[e] * (e^(m_c - M) / L), the
+// chunks in order - deterministic, and the same operations as the GEMV input stage's combine.
 __device__ __forceinline__ float attention_combine_at(const float* partials, uint32_t i, uint32_t heads,
                                                       uint32_t D, uint32_t chunks) {
   const uint32_t h = i / D;
   const float* o = partials + (size_t)i * chunks;
   const float* m = partials + (size_t)heads * D * chunks + (size_t)h * chunks;
   const float* l = m + (size_t)heads * chunks;
-  float M = -INFINITY;
-  for (uint32_t c = 0; c < chunks; c++) M = fmaxf(M, m[c]);
-  float L = 0.f;
-  for (uint32_t c = 0; c < chunks; c++) L = fmaf(l[c], expf(m[c] - M), L);
+  float M, L;
+  combine_stats(m, l, chunks, M, L);
   float acc = 0.f;
   for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], expf(m[c] - M) / L, acc);
   return acc;
