@@ -403,7 +403,7 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
         dev.sync()
     first = 785  # the first greedy id of the reference's fixture prompt; any id works
     result = {"config": "BASELINE config 4: Qwen2.5-0.5B shape, 24 layers, int4 g32 + int8 tied head, f16 KV",
-              "context": cfg.max_context, "steps": DECODE_STEPS, "launches_per_token": 5 * cfg.layers + 4}
+              "context": cfg.max_context, "steps": DECODE_STEPS, "launches_per_token": 5 * cfg.layers + 2}
     for mode in modes:
         if mode == "graph":
             dec.capture()

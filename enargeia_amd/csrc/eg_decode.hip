@@ -116,9 +116,10 @@ struct Prefetch {
   static_assert(GMAX * D <= kThreads && D <= kThreads, "one query element per thread");
   uint4 k[kLoads], v[kLoads];
   float qv = 0.f, kn = 0.f, vn = 0.f;
+  double2 cs = make_double2(0.0, 0.0);  // the RoPE table's entry tid, when one is given
   __device__ __forceinline__ void load(const uint16_t* k_cache, const uint16_t* v_cache, uint32_t j0, uint32_t kv,
                                        uint32_t kv_heads, const float* q, uint32_t h0, uint32_t ng, const float* kp,
-                                       const float* vp) {
+                                       const float* vp, const double2* rope) {
     const uint32_t tid = threadIdx.x;
 #pragma unroll
     for (uint32_t r = 0; r < kLoads; r++) {
@@ -132,6 +133,7 @@ struct Prefetch {
       kn = kp[(size_t)kv * D + tid];
       vn = vp[(size_t)kv * D + tid];
     }
+    if (rope && tid < D / 2) cs = rope[tid];
   }
 };
 
@@ -139,7 +141,7 @@ struct Prefetch {
 // statistics and the partial o, written to po/pm/pl, from what `pre` loaded.
 template <int D, int CHUNK, int GMAX>
 __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, uint32_t hs, uint32_t ng,
-                                       uint32_t chunks, const Prefetch<D, CHUNK, GMAX>& pre, uint16_t* k_cache,
+                                       uint32_t chunks, const Prefetch<D, CHUNK, GMAX>& pre, bool rope, uint16_t* k_cache,
                                        uint16_t* v_cache, float* po, float* pm, float* pl,
                                        const eg_attention_dims& d) {
   const uint32_t tid = threadIdx.x;
@@ -170,7 +172,10 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
     knew[tid] = pre.kn;
     vnew[tid] = pre.vn;
   }
-  if (tid < D / 2) rope_table<D>(cs, tid, pos, d.theta);
+  if (tid < D / 2) {
+    if (rope) cs[tid] = pre.cs;  // computed once per step by the step tail, same function
+    else rope_table<D>(cs, tid, pos, d.theta);
+  }
   __syncthreads();
   for (uint32_t i = tid; i < ng * (D / 2); i += blockDim.x) rope_apply<D>(qs[i / (D / 2)], i % (D / 2), cs);
   if (owns_new && tid < D / 2) rope_apply<D>(knew, tid, cs);
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
                                                                     const float* k, const float* v,
                                                                     uint16_t* k_cache, uint16_t* v_cache,
                                                                     float* partials, uint32_t* counter, float* out,
-                                                                    eg_attention_dims d) {
+                                                                    eg_attention_dims d, const double2* rope) {
   const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
   const uint32_t c = blockIdx.x;
   const uint32_t chunks = gridDim.x;
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
   const uint32_t tid = threadIdx.x;
   const uint32_t h0 = kv * group + gb;
   Prefetch<D, CHUNK, GMAX> pre;
-  pre.load(k_cache, v_cache, j0, kv, d.kv_heads, q, h0, ng, k, v);
+  pre.load(k_cache, v_cache, j0, kv, d.kv_heads, q, h0, ng, k, v, rope);
   const uint32_t pos = position[0];
   // partial layout (chunk index fastest): o[h][e][c], then m[h][c], then l[h][c]
   float* po = partials + (size_t)h0 * D * chunks + c;
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
       pl[(size_t)tid * chunks] = 0.f;
     }
   }
-  if (ng > 0 && !empty) attend<D, CHUNK, GMAX>(pos, j0, kv, hs, ng, chunks, pre, k_cache, v_cache, po, pm, pl, d);
+  if (ng > 0 && !empty) attend<D, CHUNK, GMAX>(pos, j0, kv, hs, ng, chunks, pre, rope != nullptr, k_cache, v_cache, po, pm, pl, d);
 
   // The combine, once, by the last workgroup to arrive: the fence releases this workgroup's
   // partials device-wide before it counts itself; the last one's fence acquires everyone's.
@@ -347,7 +352,123 @@ int check_attention(eg_context* ctx, const char* op, const eg_attention_dims* d)
   return EG_OK;
 }
 
+int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, const float* q, const float* k,
+                     const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials, uint32_t* counter,
+                     float* out, const eg_attention_dims* dims, const double* rope) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!position || !q || !k || !v || !k_cache || !v_cache || !partials)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if ((counter == nullptr) != (out == nullptr))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: counter and out go together", op);
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15u) || (reinterpret_cast<uintptr_t>(v_cache) & 15u))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: caches must be 16-byte aligned", op);
+  int st = check_attention(ctx, op, dims);
+  if (st != EG_OK) return st;
+  const double2* cs = reinterpret_cast<const double2*>(rope);
+  // chunk 64: two workgroups share a kv group's query heads; chunk 128: four do
+  if (dims->chunk == 64) {
+    const dim3 grid(dims->max_context / 64, dims->kv_heads * 2);
+    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
+                       v, k_cache, v_cache, partials, counter, out, *dims, cs);
+  } else {
+    const dim3 grid(dims->max_context / 128, dims->kv_heads * 4);
+    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
+                       v, k_cache, v_cache, partials, counter, out, *dims, cs);
+  }
+  return eg::check_launch(ctx, op);
+}
+
+
+// The end of a greedy decode step and the start of the next, in one launch: the LM head's
+// argmax partials reduced to the token (the same (value, index) order as the argmax finalize:
+// larger value, then lower index), the position advanced, the next step's input - the new
+// token's embedding row, dequantized - and the RoPE cos/sin of the next position, which every
+// attention launch of that step then reads instead of computing. Without partials (a reset) the
+// token and position already in device memory are used as they are.
+__global__ __launch_bounds__(kThreads) void step_tail_kernel(const uint32_t* partials, uint32_t groups,
+                                                             uint32_t* token, uint32_t* position,
+                                                             const uint32_t* packed, const float* scales,
+                                                             const uint32_t* zeros, eg_embedding_dims d, int encoding,
+                                                             int bits, float* emb, double2* rope, float theta) {
+  constexpr int D = 64;
+  __shared__ uint32_t next_token, next_pos;
+  if (partials) {
+    float bv = -1.0e30f;
+    uint32_t bi = 0;
+    for (uint32_t b = threadIdx.x; b < groups; b += kThreads) {
+      const float v = __uint_as_float(partials[2 * b]);
+      const uint32_t i = partials[2 * b + 1];
+      if (egd::better(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+    __shared__ float wv[kThreads / 64];
+    __shared__ uint32_t wi[kThreads / 64];
+    egd::team_argmax<64>(bv, bi);
+    if ((threadIdx.x & 63u) == 0) {
+      wv[threadIdx.x >> 6] = bv;
+      wi[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kThreads / 64; w++)
+        if (egd::better(wv[w], wi[w], bv, bi)) {
+          bv = wv[w];
+          bi = wi[w];
+        }
+      token[0] = bi;
+      token[1] = __float_as_uint(bv);
+      next_token = bi;
+      next_pos = position[0] + 1;
+      position[0] = next_pos;
+    }
+  } else if (threadIdx.x == 0) {
+    next_token = token[0];
+    next_pos = position[0];
+  }
+  __syncthreads();
+  const uint32_t id = next_token, pos = next_pos;
+  if (threadIdx.x < D / 2) rope_table<D>(rope, threadIdx.x, pos, theta);
+  if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
+  const uint32_t row = id - d.row_begin;
+  const uint32_t per_word = 32u / (uint32_t)bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (uint32_t i = threadIdx.x; i < d.hidden; i += blockDim.x) {
+    const uint64_t e = (uint64_t)row * d.hidden + i;
+    uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
+    const uint32_t blk = row * d.blocks_per_row + i / d.block_size;
+    float zero;
+    if (encoding == EG_ENC_OFFSET_ZEROS) {
+      zero = (float)((zeros[blk / per_word] >> (bits * (blk % per_word))) & mask);
+    } else {
+      code ^= 1u << (bits - 1);
+      zero = (float)(1u << (bits - 1));
+    }
+    emb[d.out_offset + i] = ((float)code - zero) * scales[blk];
+  }
+}
+
 }  // namespace
+
+int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                              const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
+                              const eg_attention_dims* dims, const double* rope) {
+  if (!rope) return eg::fail(ctx, EG_ERR_INVALID, "attention_decode: rope table is NULL");
+  return launch_attention(ctx, "attention_decode", position, q, k, v, k_cache, v_cache, partials, nullptr, nullptr,
+                          dims, rope);
+}
+
+int eg::launch_step_tail(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t* token,
+                         uint32_t* position, const uint32_t* packed, const float* scales, const uint32_t* zeros,
+                         const eg_embedding_dims* ed, int encoding, int bits, float* emb, double* rope,
+                         uint32_t head_dim, float theta) {
+  if (head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "step_tail: head_dim %u (64 is supported)", head_dim);
+  hipLaunchKernelGGL(step_tail_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, partials, groups, token, position,
+                     packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, *ed, encoding, bits, emb,
+                     reinterpret_cast<double2*>(rope), theta);
+  return eg::check_launch(ctx, "step_tail");
+}
 
 extern "C" {
 
@@ -373,27 +494,8 @@ int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* pack
 int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k, const float* v,
                         uint16_t* k_cache, uint16_t* v_cache, float* partials, uint32_t* counter, float* out,
                         const eg_attention_dims* dims) {
-  const char* op = "attention_decode";
-  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
-  if (!position || !q || !k || !v || !k_cache || !v_cache || !partials)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
-  if ((counter == nullptr) != (out == nullptr))
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: counter and out go together", op);
-  if ((reinterpret_cast<uintptr_t>(k_cache) & 15u) || (reinterpret_cast<uintptr_t>(v_cache) & 15u))
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: caches must be 16-byte aligned", op);
-  int st = check_attention(ctx, op, dims);
-  if (st != EG_OK) return st;
-  // chunk 64: two workgroups share a kv group's query heads; chunk 128: four do
-  if (dims->chunk == 64) {
-    const dim3 grid(dims->max_context / 64, dims->kv_heads * 2);
-    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims);
-  } else {
-    const dim3 grid(dims->max_context / 128, dims->kv_heads * 4);
-    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims);
-  }
-  return eg::check_launch(ctx, op);
+  return launch_attention(ctx, "attention_decode", position, q, k, v, k_cache, v_cache, partials, counter, out, dims,
+                          nullptr);
 }
 
 int eg_attention_combine(eg_context* ctx, const float* partials, float* out, const eg_attention_dims* dims) {

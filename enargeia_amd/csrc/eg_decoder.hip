@@ -2,15 +2,17 @@
 // order, graph_decode.ts:185-448) and Session.decodeStep (per-token bookkeeping,
 // session.ts:347-375), over the ops of this library.
 //
-// Per token: the embedding gather, then per layer
+// Per token, per layer
 //   q|k|v   one batched GEMV, RMSNorm(input_layernorm) fused into its input stage, biases
 //   attn    one fused launch: RoPE, f16 cache append, split-K attention partials
 //   o       GEMV whose input stage combines the partials; bias = the residual stream
 //   gate|up one batched GEMV, RMSNorm(post_attention_layernorm) fused into its input stage
 //   down    GEMV whose input stage is SiLU(gate) * up; bias = the residual stream
-// then the LM head with the final norm fused and the greedy argmax, and the device-side
-// advance of the position. Every per-token value (token id, position) lives in device memory,
-// so one captured hipGraph replays every step with no host work per launch.
+// then the LM head with the final norm fused and its argmax partials, and one tail launch that
+// reduces them to the token, advances the position and prepares the next step: the new token's
+// embedding row (layer 0's input) and the RoPE cos/sin of the next position (read by every
+// attention launch instead of computed there). Every per-token value (token id, position) lives
+// in device memory, so one captured hipGraph replays every step with no host work per launch.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -29,6 +31,8 @@ struct eg_decoder {
   float* gu = nullptr;               // gate then up: [2 * intermediate]
   float* partials = nullptr;         // attention partials
   float* logits = nullptr;           // [vocab]
+  float* emb = nullptr;              // [hidden]: the current token's embedding, layer 0's input
+  double* rope = nullptr;            // [head_dim / 2] (cos, sin) at the current position
   uint32_t* token = nullptr;         // [2]: next input id, its logit bits
   uint32_t* position = nullptr;      // [1]
   uint16_t* k_cache = nullptr;
@@ -59,6 +63,23 @@ bool matrix_ok(const eg_quant_matrix& m, int encoding) {
   return m.packed && m.scales && (encoding == EG_ENC_SIGNED || m.zeros);
 }
 
+// The step tail (see eg::launch_step_tail): with partials, the end of a step; without, the
+// preparation of the state a reset wrote.
+int tail(eg_decoder* d, const uint32_t* partials, uint32_t groups) {
+  const eg_model_desc& m = d->desc;
+  eg_embedding_dims ed{};
+  ed.seq = 1;
+  ed.hidden = m.hidden;
+  ed.row_begin = 0;
+  ed.row_count = m.vocab;
+  ed.block_size = m.embed_block_size;
+  ed.blocks_per_row = m.hidden / m.embed_block_size;
+  ed.grid_width = 1;
+  return eg::launch_step_tail(d->ctx, partials, groups, d->token, d->position, m.embedding.packed, m.embedding.scales,
+                              m.embedding.zeros, &ed, m.embed_encoding, m.embed_bits, d->emb, d->rope, m.head_dim,
+                              m.rope_theta);
+}
+
 int run_step(eg_decoder* d) {
   eg_context* ctx = d->ctx;
   const eg_model_desc& m = d->desc;
@@ -71,14 +92,13 @@ int run_step(eg_decoder* d) {
   ed.block_size = m.embed_block_size;
   ed.blocks_per_row = m.hidden / m.embed_block_size;
   ed.grid_width = 1;
-  int st = eg_embed_gather(ctx, d->token, e.packed, e.scales, e.zeros, d->h[0], &ed, m.embed_encoding, m.embed_bits);
-  if (st != EG_OK) return st;
+  int st = EG_OK;
   for (uint32_t l = 0; l < m.layers; l++) {
     const eg_layer_desc& L = d->layers[l];
     eg_gemv_plan* const* P = &d->plans[4 * (size_t)l];
     eg_gemv_input in{};
     in.kind = EG_INPUT_RMSNORM;
-    in.x = d->h[0];
+    in.x = l == 0 ? d->emb : d->h[0];
     in.x2 = L.input_norm;
     in.eps = m.rms_eps;
     if ((st = eg_gemv_plan_launch_input(ctx, P[0], &in)) != EG_OK) return st;
@@ -86,8 +106,8 @@ int run_step(eg_decoder* d) {
     // The combine runs in the o projection's input stage: measured faster here than the
     // attention launch's last-workgroup combine, whose device-scope fences cost more than the
     // per-workgroup recomputation.
-    if ((st = eg_attention_decode(ctx, d->position, d->q, d->kv, d->kv + kvn, d->k_cache + l * d->layer_stride,
-                                  d->v_cache + l * d->layer_stride, d->partials, nullptr, nullptr, &d->att)) != EG_OK)
+    if ((st = eg::attention_decode_rope(ctx, d->position, d->q, d->kv, d->kv + kvn, d->k_cache + l * d->layer_stride,
+                                        d->v_cache + l * d->layer_stride, d->partials, &d->att, d->rope)) != EG_OK)
       return st;
     in = eg_gemv_input{};
     in.kind = EG_INPUT_ATTENTION;
@@ -114,10 +134,11 @@ int run_step(eg_decoder* d) {
   eg_embedding_dims hd = ed;
   hd.row_count = m.vocab;
   hd.grid_width = 65535;
-  if ((st = eg_lm_head_argmax_input(ctx, &in, e.packed, e.scales, e.zeros, d->logits, d->token, &hd,
-                                    m.embed_encoding, m.embed_bits)) != EG_OK)
+  uint32_t groups = 0;
+  if ((st = eg::lm_head_argmax_partials(ctx, &in, e.packed, e.scales, e.zeros, d->logits, &hd, m.embed_encoding,
+                                        m.embed_bits, &groups)) != EG_OK)
     return st;
-  return eg_decode_advance(ctx, d->position, nullptr, nullptr, d->token, 0);
+  return tail(d, reinterpret_cast<const uint32_t*>(eg::partials(ctx)), groups);
 }
 
 }  // namespace
@@ -171,6 +192,8 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   };
   take(m.hidden * 4, &d->h[0]);
   take(m.hidden * 4, &d->h[1]);
+  take(m.hidden * 4, &d->emb);
+  take((size_t)m.head_dim / 2 * 2 * sizeof(double), &d->rope);
   take((size_t)m.heads * m.head_dim * 4, &d->q);
   take(2 * kvn * 4, &d->kv);
   take((size_t)2 * m.intermediate * 4, &d->gu);
@@ -197,7 +220,8 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     st = eg_gemv_plan_create(ctx, m.hidden, m.block_size, m.encoding, m.bits, qkv, 3, &plan);
     if (st != EG_OK) break;
     d->plans.push_back(plan);
-    eg_gemv_segment o[1] = {{L.o.packed, L.o.scales, L.o.zeros, d->h[0], d->h[1], m.hidden, 0}};
+    // the residual stream enters layer 0 as the embedding
+    eg_gemv_segment o[1] = {{L.o.packed, L.o.scales, L.o.zeros, l == 0 ? d->emb : d->h[0], d->h[1], m.hidden, 0}};
     st = eg_gemv_plan_create(ctx, m.hidden, m.block_size, m.encoding, m.bits, o, 1, &plan);
     if (st != EG_OK) break;
     d->plans.push_back(plan);
@@ -250,7 +274,8 @@ int eg_decoder_reset(eg_decoder* d, uint32_t position, uint32_t token) {
   const uint32_t tok[2] = {token, 0};
   int st = eg_buf_write(d->ctx, d->token, 0, tok, sizeof(tok));
   if (st == EG_OK) st = eg_buf_write(d->ctx, d->position, 0, &position, 4);
-  if (st == EG_OK) st = eg_sync(d->ctx);  // the host values are stack locals
+  if (st == EG_OK) st = tail(d, nullptr, 0);  // this token's embedding, this position's RoPE table
+  if (st == EG_OK) st = eg_sync(d->ctx);      // the host values are stack locals
   if (st == EG_OK) d->host_position = position;
   return st;
 }

@@ -180,6 +180,7 @@ struct QuantView {
   int encoding, bits;
   uint32_t* result;  // non-null for the fused argmax
   const eg_gemv_input* input = nullptr;  // fused input stage; NULL: x as given
+  uint32_t* groups_out = nullptr;  // fused argmax: skip the finalize, report the partials' count here
 };
 
 // LDS the input stage needs beyond x and the segment table.
@@ -317,7 +318,8 @@ int launch(eg_context* ctx, const QuantView& v) {
                          v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
                          v.out_offset, v.bits, v.encoding, partials);
   }
-  if (argmax) eg::launch_argmax_finalize(ctx, partials, grid, v.out_offset, v.result);
+  if (argmax && v.groups_out) *v.groups_out = grid;
+  else if (argmax) eg::launch_argmax_finalize(ctx, partials, grid, v.out_offset, v.result);
   return eg::check_launch(ctx, v.op);
 }
 
@@ -376,6 +378,17 @@ int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, const u
 }
 
 }  // extern "C"
+
+int eg::lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed,
+                                const float* scales, const uint32_t* zeros, float* out, const eg_embedding_dims* dims,
+                                int encoding, int bits, uint32_t* groups) {
+  if (!dims || !input || !groups) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_argmax: NULL argument");
+  uint32_t* partials = ctx ? reinterpret_cast<uint32_t*>(eg::partials(ctx)) : nullptr;
+  QuantView v{"lm_head_argmax", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
+              dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
+              bits, partials, input, groups};
+  return launch(ctx, v);
+}
 
 // ---- batched plans ------------------------------------------------------------------------
 

@@ -63,6 +63,28 @@ constexpr size_t kPartialsBytes = kWorkspaceBytes - kPartialsOffset;
 void launch_argmax_finalize(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t sentinel_index,
                             uint32_t* result);
 
+// The fused LM head + argmax without its finalize launch: the per-workgroup (value, index)
+// partials are left in the workspace (eg::partials) and their count in *groups, for a caller
+// that reduces them in a launch of its own (the decoder's step tail). Same checks and kernels as
+// eg_lm_head_argmax_input.
+int lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed,
+                            const float* scales, const uint32_t* zeros, float* out, const eg_embedding_dims* dims,
+                            int encoding, int bits, uint32_t* groups);
+
+// The decode step's tail, one single-workgroup launch: with `partials` (the LM head's argmax
+// partials, `groups` of them) the greedy token is written to token[0..1] and position[0] advances;
+// then (also without partials: a reset) the embedding row of token[0] is dequantized into `emb`
+// and the RoPE cos/sin of position[0] are written to `rope` ([head_dim / 2] pairs of doubles).
+int launch_step_tail(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t* token, uint32_t* position,
+                     const uint32_t* packed, const float* scales, const uint32_t* zeros, const eg_embedding_dims* ed,
+                     int encoding, int bits, float* emb, double* rope, uint32_t head_dim, float theta);
+
+// eg_attention_decode with the RoPE cos/sin of the current position read from `rope` ([head_dim
+// / 2] pairs of doubles, as egd::rope_table computes them) instead of computed in the launch.
+int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                          const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
+                          const eg_attention_dims* dims, const double* rope);
+
 // Workgroups of `kernel` (256 threads, `smem_bytes` of dynamic LDS) resident per CU, cached
 // per context; 0 if the runtime cannot say.
 int occupancy_of(eg_context* ctx, const void* kernel, uint32_t smem_bytes = 0);

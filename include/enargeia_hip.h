@@ -312,8 +312,9 @@ typedef struct eg_decoder_buffers {
 /* Plans every launch of a step once: per layer one GEMV plan for q|k|v (RMSNorm input stage,
  * biases), one fused attention launch, the o projection (attention-combine input stage, the
  * residual as its bias), gate|up (RMSNorm input stage) and down (SiLU*up input stage, residual
- * bias); then the LM head with the final norm fused and the greedy argmax. 5 launches per
- * layer + 4, against the reference's ~19 dispatches per layer. Allocates the caches and
+ * bias); then the LM head with the final norm fused and its argmax partials, and one tail launch
+ * (the token, the position advance, the next token's embedding row and RoPE table). 5 launches
+ * per layer + 2, against the reference's ~19 dispatches per layer. Allocates the caches and
  * scratch. The weights stay owned by the caller and must outlive the decoder. */
 EG_API int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** out_decoder);
 EG_API int eg_decoder_destroy(eg_decoder* decoder);
