@@ -4,6 +4,8 @@
 //
 // Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
 // (embedding_variants.ts:135-180).
+#include <vector>
+
 #include "eg_gemv_kernel.hpp"
 
 namespace {
@@ -396,6 +398,10 @@ struct eg_gemv_plan {
   DevSegment* table = nullptr;  // device copy
   DevSegment inline_table[kInlineSegments] = {};  // host copy, passed in the arguments when count <= kInlineSegments
   uint32_t any_bias = 0;                           // some segment has a bias
+  // Per-workgroup windows of the table for launches on `grid` (x given as a vector): workgroup b's
+  // `window` entries start at windows + b * window. NULL: every workgroup copies the whole table.
+  DevSegment* windows = nullptr;
+  uint32_t window = 0;
   uint32_t count = 0;
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
   int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
@@ -452,8 +458,8 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   for (uint32_t i = 0; i < count; i++) plan->any_bias |= segments[i].bias != nullptr;
   hipError_t err = hipMalloc(&plan->table, sizeof(DevSegment) * count);
   if (err == hipSuccess) err = hipMemcpy(plan->table, host, sizeof(DevSegment) * count, hipMemcpyHostToDevice);
-  delete[] host;
   if (err != hipSuccess) {
+    delete[] host;
     if (plan->table) (void)hipFree(plan->table);
     delete plan;
     return eg::hip_fail(ctx, err, "gemv_plan_create");
@@ -472,6 +478,45 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb);
   plan->smem = k * 4u + count * (uint32_t)sizeof(DevSegment);
   plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
+  // Windows for the vector-input grid: each workgroup's waves walk tiles [first, last) of the
+  // pass space (the kernel's own split, total * wave / waves), which touch segments
+  // seg(first) .. seg(last - 1); a window holds those, padded with copies of the last (whose
+  // pass_end lies past every tile of the workgroup, so the kernel never counts or reaches them).
+  if (count > kInlineSegments && plan->grid > 0) {
+    const uint64_t waves = (uint64_t)plan->grid * kWaves;
+    auto seg_of = [&](uint32_t tile) {  // first segment whose pass_end exceeds tile
+      uint32_t lo = 0, hi = count - 1;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (host[mid].pass_end > tile) hi = mid;
+        else lo = mid + 1;
+      }
+      return lo;
+    };
+    std::vector<uint32_t> first(plan->grid), span(plan->grid);
+    uint32_t window = 1;
+    for (uint32_t b = 0; b < plan->grid; b++) {
+      const uint32_t t0 = (uint32_t)((uint64_t)pass * (kWaves * (uint64_t)b) / waves);
+      const uint32_t t1 = (uint32_t)((uint64_t)pass * (kWaves * (uint64_t)b + kWaves) / waves);
+      first[b] = t1 > t0 ? seg_of(t0) : 0;
+      span[b] = t1 > t0 ? seg_of(t1 - 1) - first[b] + 1 : 1;
+      window = std::max(window, span[b]);
+    }
+    if (window < count / 2) {
+      std::vector<DevSegment> w((size_t)plan->grid * window);
+      for (uint32_t b = 0; b < plan->grid; b++)
+        for (uint32_t j = 0; j < window; j++) w[(size_t)b * window + j] = host[first[b] + std::min(j, span[b] - 1)];
+      err = hipMalloc(&plan->windows, w.size() * sizeof(DevSegment));
+      if (err == hipSuccess) err = hipMemcpy(plan->windows, w.data(), w.size() * sizeof(DevSegment), hipMemcpyHostToDevice);
+      if (err != hipSuccess) {
+        delete[] host;
+        eg_gemv_plan_destroy(ctx, plan);
+        return eg::hip_fail(ctx, err, "gemv_plan_create");
+      }
+      plan->window = window;
+    }
+  }
+  delete[] host;
   *out_plan = plan;
   return EG_OK;
 }
@@ -505,12 +550,19 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
                             ? grid_for(ctx, fn, plan->total_passes, plan->smem + extra, ctx->fused_tiles_per_wave)
                             : plan->grid;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), plan->smem + extra, ctx->stream, a);
+  uint32_t smem = plan->smem + extra;
+  if (a.in_kind == EG_INPUT_VECTOR && plan->windows) {  // the windows were cut for this grid
+    a.segs = plan->windows;
+    a.seg_window = plan->window;
+    smem = plan->k * 4u + plan->window * (uint32_t)sizeof(DevSegment) + extra;
+  }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }
 
 int eg_gemv_plan_destroy(eg_context* ctx, eg_gemv_plan* plan) {
   if (!plan) return EG_OK;
+  if (plan->windows) (void)hipFree(plan->windows);
   if (plan->table) {
     hipError_t err = hipFree(plan->table);
     if (err != hipSuccess) {

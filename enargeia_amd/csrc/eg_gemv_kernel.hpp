@@ -79,6 +79,7 @@ struct GemvArgs {
   const DevSegment* segs;  // batched launches only
   uint32_t seg_count;
   DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
+  uint32_t seg_window;     // > 0: segs holds seg_window entries per workgroup (its own window)
   uint32_t total_passes;   // tiles over all rows (all segments)
   // input stage (eg_input_kind): how each workgroup produces x in LDS
   int in_kind;
@@ -385,17 +386,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // VGPRs for every row it visits.
   extern __shared__ __align__(16) uint8_t smem[];
   const uint32_t x_words = a.chunks * EPC;
-  const bool lds_table = MODE == kBatched && a.seg_count > kInlineSegments;  // wave-uniform
+  const bool lds_table = MODE == kBatched && (a.seg_window || a.seg_count > kInlineSegments);  // wave-uniform
+  // The entries in LDS: the plan's whole table, or - where the plan precomputed one for this
+  // grid - this workgroup's window of it (the few segments its waves' tiles touch; 64 bytes
+  // each, against the whole table's 64 per matrix).
+  const uint32_t lds_count = a.seg_window ? a.seg_window : a.seg_count;
+  const DevSegment* lds_src = a.seg_window ? a.segs + (size_t)blockIdx.x * a.seg_window : a.segs;
   DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
-  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? a.seg_count : 0u) *
+  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? lds_count : 0u) *
                                                                       (uint32_t)sizeof(DevSegment));
   // A table in LDS: its loads are all issued up front (kTableLoads per thread at most, reads
   // past the table return zeros), so copying it costs one L2 round trip that overlaps the
   // input stage's, not one per element.
   egd::u32x4 tv[MODE == kBatched ? kTableLoads : 1];
-  const uint32_t table_vecs = a.seg_count * (uint32_t)(sizeof(DevSegment) / 16);
+  const uint32_t table_vecs = lds_count * (uint32_t)(sizeof(DevSegment) / 16);
   if (lds_table) {
-    const auto src = egd::buffer(a.segs, table_vecs * 16u);
+    const auto src = egd::buffer(lds_src, table_vecs * 16u);
 #pragma unroll
     for (uint32_t r = 0; r < kTableLoads; r++) tv[r] = egd::load_b128(src, (threadIdx.x + r * 256u) * 16u);
   }
@@ -493,9 +499,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     uint32_t count = 0;
     if (lds_table) {
       // 64 entries per LDS read, counted with a ballot
-      for (uint32_t e0 = 0; e0 < a.seg_count; e0 += 64) {
+      for (uint32_t e0 = 0; e0 < lds_count; e0 += 64) {
         const uint32_t e = e0 + lane;
-        const bool done = e < a.seg_count && table[e < a.seg_count ? e : 0].pass_end <= begin;
+        const bool done = e < lds_count && table[e < lds_count ? e : 0].pass_end <= begin;
         count += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(done));
       }
     } else {

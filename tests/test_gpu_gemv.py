@@ -279,6 +279,42 @@ def test_batched_plan_matches_per_matrix(device):
         b.release()
 
 
+@pytest.mark.parametrize("k", [896, 4864])
+def test_batched_plan_many_segments(device, k):
+    """A plan of more than four matrices keeps its table in memory, and launches with x given as a
+    vector copy only their workgroup's window of it: segments of 8 to 1024 rows, so windows span
+    one to several segments and the smallest fall inside a single workgroup; biases and outOffsets
+    on some. Every segment against the oracle."""
+    rows = (8, 16, 24, 136, 8, 512, 64, 8, 32, 1024, 16, 40) if k == 896 else (8, 16, 8, 96, 24, 8, 40, 8)
+    x = oracle.normal_floats(k, 1500 + k, 1.0)
+    mats = [sym_weights(n, k, 1510 + i) for i, n in enumerate(rows)]
+    bx = device.upload(x)
+    keep, segs, outs, biases = [bx], [], [], []
+    for i, q in enumerate(mats):
+        bp, bs, _ = _upload_quant(device, q)
+        bias = oracle.normal_floats(q.rows, 1530 + i, 0.02) if i % 3 == 1 else None
+        bb = device.upload(bias) if bias is not None else None
+        off = 5 if i % 4 == 2 else 0
+        bo = device.buffer((q.rows + off) * 4)
+        device.zero(bo, (q.rows + off) * 4)
+        keep += [bp, bs, bo] + ([bb] if bb else [])
+        segs.append((bp, bs, None, bb, bo, q.rows, off))
+        outs.append((bo, off))
+        biases.append(bias)
+    plan = K.GemvPlan(device, k, 32, segs)
+    for _ in range(2):  # twice: the windows are reused as they are
+        plan.launch(bx)
+        for i, q in enumerate(mats):
+            bo, off = outs[i]
+            got = device.read_array(bo, np.float32, q.rows + off)
+            assert np.all(got[:off] == 0)
+            expect = oracle.linear_q(x, q, biases[i], 1)
+            assert_close(got[off:], expect, *gemv_tolerance(expect), label=f"k={k} segment {i} ({q.rows} rows)")
+    plan.destroy()
+    for b in keep:
+        b.release()
+
+
 def test_batched_plan_rejects_bad_tables(device):
     q = sym_weights(896, 896, 5)
     bp, bs, _ = _upload_quant(device, q)
