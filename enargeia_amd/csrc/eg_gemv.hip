@@ -4,6 +4,7 @@
 //
 // Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
 // (embedding_variants.ts:135-180).
+#include <cstring>
 #include <vector>
 
 #include "eg_gemv_kernel.hpp"
@@ -395,13 +396,13 @@ int eg::lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, con
 // ---- batched plans ------------------------------------------------------------------------
 
 struct eg_gemv_plan {
-  DevSegment* table = nullptr;  // device copy
+  // Device copy of the table, followed (plans of more than kInlineSegments matrices) by the
+  // segment of every pass, 16 bits each: a wave finds its first segment in two scalar loads,
+  // whatever the launch's grid.
+  DevSegment* table = nullptr;
+  const uint32_t* seg_index = nullptr;
   DevSegment inline_table[kInlineSegments] = {};  // host copy, passed in the arguments when count <= kInlineSegments
   uint32_t any_bias = 0;                           // some segment has a bias
-  // Per-workgroup windows of the table for launches on `grid` (x given as a vector): workgroup b's
-  // `window` entries start at windows + b * window. NULL: every workgroup copies the whole table.
-  DevSegment* windows = nullptr;
-  uint32_t window = 0;
   uint32_t count = 0;
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
   int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
@@ -456,14 +457,27 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   eg_gemv_plan* plan = new eg_gemv_plan();
   for (uint32_t i = 0; i < count && i < kInlineSegments; i++) plan->inline_table[i] = host[i];
   for (uint32_t i = 0; i < count; i++) plan->any_bias |= segments[i].bias != nullptr;
-  hipError_t err = hipMalloc(&plan->table, sizeof(DevSegment) * count);
-  if (err == hipSuccess) err = hipMemcpy(plan->table, host, sizeof(DevSegment) * count, hipMemcpyHostToDevice);
+  // table, then the pass index (count < 2^16: kMaxSegments)
+  static_assert(kMaxSegments <= 0x10000u, "segment numbers are stored in 16 bits");
+  std::vector<uint8_t> blob(sizeof(DevSegment) * count);
+  std::memcpy(blob.data(), host, blob.size());
+  if (count > kInlineSegments) {
+    std::vector<uint16_t> index((pass + 1u) & ~1u, (uint16_t)(count - 1));
+    for (uint32_t i = 0, p = 0; i < count; i++)
+      for (; p < host[i].pass_end; p++) index[p] = (uint16_t)i;
+    const size_t at = blob.size();
+    blob.resize(at + index.size() * sizeof(uint16_t));
+    std::memcpy(blob.data() + at, index.data(), index.size() * sizeof(uint16_t));
+  }
+  hipError_t err = hipMalloc(&plan->table, blob.size());
+  if (err == hipSuccess) err = hipMemcpy(plan->table, blob.data(), blob.size(), hipMemcpyHostToDevice);
   if (err != hipSuccess) {
     delete[] host;
     if (plan->table) (void)hipFree(plan->table);
     delete plan;
     return eg::hip_fail(ctx, err, "gemv_plan_create");
   }
+  if (count > kInlineSegments) plan->seg_index = reinterpret_cast<const uint32_t*>(plan->table + count);
   plan->count = count;
   plan->k = k;
   plan->block_size = block_size;
@@ -476,46 +490,8 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->u = shape.u;
   plan->nb = shape.nb;
   KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb);
-  plan->smem = k * 4u + count * (uint32_t)sizeof(DevSegment);
+  plan->smem = k * 4u;
   plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
-  // Windows for the vector-input grid: each workgroup's waves walk tiles [first, last) of the
-  // pass space (the kernel's own split, total * wave / waves), which touch segments
-  // seg(first) .. seg(last - 1); a window holds those, padded with copies of the last (whose
-  // pass_end lies past every tile of the workgroup, so the kernel never counts or reaches them).
-  if (count > kInlineSegments && plan->grid > 0) {
-    const uint64_t waves = (uint64_t)plan->grid * kWaves;
-    auto seg_of = [&](uint32_t tile) {  // first segment whose pass_end exceeds tile
-      uint32_t lo = 0, hi = count - 1;
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) / 2;
-        if (host[mid].pass_end > tile) hi = mid;
-        else lo = mid + 1;
-      }
-      return lo;
-    };
-    std::vector<uint32_t> first(plan->grid), span(plan->grid);
-    uint32_t window = 1;
-    for (uint32_t b = 0; b < plan->grid; b++) {
-      const uint32_t t0 = (uint32_t)((uint64_t)pass * (kWaves * (uint64_t)b) / waves);
-      const uint32_t t1 = (uint32_t)((uint64_t)pass * (kWaves * (uint64_t)b + kWaves) / waves);
-      first[b] = t1 > t0 ? seg_of(t0) : 0;
-      span[b] = t1 > t0 ? seg_of(t1 - 1) - first[b] + 1 : 1;
-      window = std::max(window, span[b]);
-    }
-    if (window < count / 2) {
-      std::vector<DevSegment> w((size_t)plan->grid * window);
-      for (uint32_t b = 0; b < plan->grid; b++)
-        for (uint32_t j = 0; j < window; j++) w[(size_t)b * window + j] = host[first[b] + std::min(j, span[b] - 1)];
-      err = hipMalloc(&plan->windows, w.size() * sizeof(DevSegment));
-      if (err == hipSuccess) err = hipMemcpy(plan->windows, w.data(), w.size() * sizeof(DevSegment), hipMemcpyHostToDevice);
-      if (err != hipSuccess) {
-        delete[] host;
-        eg_gemv_plan_destroy(ctx, plan);
-        return eg::hip_fail(ctx, err, "gemv_plan_create");
-      }
-      plan->window = window;
-    }
-  }
   delete[] host;
   *out_plan = plan;
   return EG_OK;
@@ -539,6 +515,7 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   a.chunks_per_block = plan->block_size / (128u / plan->bits);
   a.blocks_per_row = plan->k / plan->block_size;
   a.segs = plan->table;
+  a.seg_index = plan->seg_index;
   a.seg_count = plan->count;
   if (plan->count <= kInlineSegments)
     for (uint32_t i = 0; i < plan->count; i++) a.inline_segs[i] = plan->inline_table[i];
@@ -550,19 +527,13 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
                             ? grid_for(ctx, fn, plan->total_passes, plan->smem + extra, ctx->fused_tiles_per_wave)
                             : plan->grid;
-  uint32_t smem = plan->smem + extra;
-  if (a.in_kind == EG_INPUT_VECTOR && plan->windows) {  // the windows were cut for this grid
-    a.segs = plan->windows;
-    a.seg_window = plan->window;
-    smem = plan->k * 4u + plan->window * (uint32_t)sizeof(DevSegment) + extra;
-  }
+  const uint32_t smem = plan->smem + extra;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }
 
 int eg_gemv_plan_destroy(eg_context* ctx, eg_gemv_plan* plan) {
   if (!plan) return EG_OK;
-  if (plan->windows) (void)hipFree(plan->windows);
   if (plan->table) {
     hipError_t err = hipFree(plan->table);
     if (err != hipSuccess) {

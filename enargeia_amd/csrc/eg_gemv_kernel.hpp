@@ -39,7 +39,7 @@
 namespace eg_gemv {
 
 constexpr int kWaves = 4;  // waves per workgroup (256 threads)
-constexpr uint32_t kMaxSegments = 256;  // matrices per batched plan (the table lives in LDS)
+constexpr uint32_t kMaxSegments = 256;  // matrices per batched plan
 constexpr uint32_t kMaxCombine = 1024;  // heads x chunks of an attention-combine input stage
 
 // One matrix of a batched launch, as the kernel sees it: its pointers and the range of wave
@@ -55,12 +55,11 @@ struct DevSegment {
   uint32_t out_offset;
   uint32_t pad[3];
 };
-// 64 bytes: the table is copied into LDS with 16-byte loads.
-static_assert(sizeof(DevSegment) == 64, "DevSegment is copied as 16-byte vectors");
-constexpr uint32_t kTableLoads = kMaxSegments * sizeof(DevSegment) / 16 / 256;  // per thread
-// Plans of up to this many matrices carry their table in the kernel arguments: a wave then
-// knows its first tile before any memory round trip and can issue that tile's weight loads
-// ahead of the input stage (the decoder's q|k|v and gate|up plans are 3 and 2 matrices).
+// 64 bytes: one entry is one 16-dword scalar load.
+static_assert(sizeof(DevSegment) == 64, "DevSegment is read as 16 dwords");
+// Plans of up to this many matrices carry their table in the kernel arguments, so a wave knows
+// its first segment with no memory round trip (the decoder's q|k|v and gate|up plans are 3 and
+// 2 matrices); larger tables stay in global memory and are read with scalar loads.
 constexpr uint32_t kInlineSegments = 4;
 
 struct GemvArgs {
@@ -79,11 +78,11 @@ struct GemvArgs {
   const DevSegment* segs;  // batched launches only
   uint32_t seg_count;
   DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
-  uint32_t seg_window;     // > 0: segs holds seg_window entries per workgroup (its own window)
+  const uint32_t* seg_index;  // seg_count > kInlineSegments: the segment of each pass, 16 bits per pass
   uint32_t total_passes;   // tiles over all rows (all segments)
   // input stage (eg_input_kind): how each workgroup produces x in LDS
   int in_kind;
-  uint32_t any_bias;       // some matrix of the launch has a bias (else no bias loads are issued)
+  uint32_t any_bias;       // some matrix of the launch has a bias (informational)
   const float* x2;         // norm weight / up
   float eps;
   uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
@@ -165,7 +164,7 @@ struct Loads {
   egd::u32x4 q[U][CPL];
   float s[U][CPL];
   uint32_t zw[U][CPL];
-  float b[U];
+  float b;  // lane t < U of a team: the bias of the team's row t
 };
 
 // The input stage: every workgroup writes the K-element input vector into LDS (xs), from x
@@ -179,8 +178,13 @@ struct Loads {
 // previous launch wrote, from L2 or beyond, and a chain of dependent round trips is what a
 // small launch's duration is made of. Inputs longer than a stage's register batch take a
 // second, looped pass for the remainder.
-template <int IN>
-__device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch) {
+// `early` runs right after the stage has issued its loads and before it uses any of them: the
+// kernel issues its first tiles' weight loads there, so the weights are in flight while the
+// stage waits for its own reads and computes. (A wave's reads complete in issue order, so the
+// stage still waits only for its own loads; a workgroup barrier does not wait for reads.)
+template <int IN, typename Early>
+__device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch,
+                                              Early&& early) {
   const uint32_t tid = threadIdx.x;
   const uint32_t n4 = n / 4;  // n is a multiple of 32
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -199,6 +203,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       xv[r] = egd::load_b128(xb, (tid + r * 256u) * 16u);
       wv[r] = egd::load_b128(wb, (tid + r * 256u) * 16u);
     }
+    early();
     __shared__ float red[kWaves];
     float ss = 0.f;
 #pragma unroll
@@ -245,6 +250,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       gv[r] = egd::load_b128(gb, (tid + r * 256u) * 16u);
       uv[r] = egd::load_b128(ub, (tid + r * 256u) * 16u);
     }
+    early();
     auto silu_mul = [](const float4& g, const float4& u) {
       return make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
                          g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
@@ -298,6 +304,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       mv[r] = __uint_as_float(egd::load_b32(mb, off));
       lv[r] = __uint_as_float(egd::load_b32(lb, off));
     }
+    early();
 #pragma unroll
     for (uint32_t r = 0; r < kStat; r++) {
       if (r * 256u < heads * G) {  // workgroup-uniform: only the rounds that hold a head
@@ -342,6 +349,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     egd::u32x4 v[kMaxLoads];
 #pragma unroll
     for (uint32_t r = 0; r < kMaxLoads; r++) v[r] = egd::load_b128(src, (tid + r * 256u) * 16u);
+    early();
     egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
 #pragma unroll
     for (uint32_t r = 0; r < kMaxLoads; r++)
@@ -380,31 +388,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const uint32_t total_waves = gridDim.x * kWaves;
 
-  // Dynamic LDS: x (chunks * EPC floats), then (batched plans of more than kInlineSegments
-  // matrices) the segment table. The workgroup copies x in once, so the activations cross L2
-  // once per workgroup rather than once per wave; each lane then keeps the chunks it owns in
-  // VGPRs for every row it visits.
+  // Dynamic LDS: x (chunks * EPC floats), then the input stage's scratch. The workgroup copies
+  // x in once, so the activations cross L2 once per workgroup rather than once per wave; each
+  // lane then keeps the chunks it owns in VGPRs for every row it visits.
   extern __shared__ __align__(16) uint8_t smem[];
   const uint32_t x_words = a.chunks * EPC;
-  const bool lds_table = MODE == kBatched && (a.seg_window || a.seg_count > kInlineSegments);  // wave-uniform
-  // The entries in LDS: the plan's whole table, or - where the plan precomputed one for this
-  // grid - this workgroup's window of it (the few segments its waves' tiles touch; 64 bytes
-  // each, against the whole table's 64 per matrix).
-  const uint32_t lds_count = a.seg_window ? a.seg_window : a.seg_count;
-  const DevSegment* lds_src = a.seg_window ? a.segs + (size_t)blockIdx.x * a.seg_window : a.segs;
-  DevSegment* table = reinterpret_cast<DevSegment*>(smem + x_words * 4u);
-  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u + (MODE == kBatched ? lds_count : 0u) *
-                                                                      (uint32_t)sizeof(DevSegment));
-  // A table in LDS: its loads are all issued up front (kTableLoads per thread at most, reads
-  // past the table return zeros), so copying it costs one L2 round trip that overlaps the
-  // input stage's, not one per element.
-  egd::u32x4 tv[MODE == kBatched ? kTableLoads : 1];
-  const uint32_t table_vecs = lds_count * (uint32_t)(sizeof(DevSegment) / 16);
-  if (lds_table) {
-    const auto src = egd::buffer(lds_src, table_vecs * 16u);
-#pragma unroll
-    for (uint32_t r = 0; r < kTableLoads; r++) tv[r] = egd::load_b128(src, (threadIdx.x + r * 256u) * 16u);
-  }
+  float* scratch = reinterpret_cast<float*>(smem + x_words * 4u);
 
   // This lane's chunk slots: slot j covers chunk cj[j] of each row (chunk 0 past the row's end,
   // where x is zero), in quant block bj[j].
@@ -437,6 +426,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * wave) / total_waves));
   const uint32_t end =
       __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)a.total_passes * (wave + 1)) / total_waves));
+  // A wave with no tiles (more waves than tiles) still issues its first loads - of a valid
+  // tile, computed by nobody - so that no load sits under a branch (see `run`).
+  const uint32_t first = begin < end ? begin : min(begin, a.total_passes - 1u);
+  const uint32_t last = begin < end ? end - 1 : first;
 
   // The matrix the issue side is walking (one for a plain launch; the current segment of a
   // batched one). Rows are a multiple of TILE in a batched plan; a plain launch's last partial
@@ -444,7 +437,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // identical results, so every access stays inside its stream.
   struct Seg {
     __amdgpu_buffer_rsrc_t w, s, z, b, o;
-    uint32_t rows, out_offset, first, end, has_bias;
+    uint32_t rows, out_offset, first, end;
   };
   auto make_seg = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
                       uint32_t rows, uint32_t out_offset, uint32_t first, uint32_t seg_end) {
@@ -453,9 +446,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     r.w = egd::buffer(w, rows * a.chunks * 16u);
     r.s = egd::buffer(scales, blocks * 4u);
     r.z = egd::buffer(zeros, ((blocks + C::kZeroPerWord - 1) / C::kZeroPerWord) * 4u);
-    r.has_bias = bias != nullptr;
-    // Without a bias the (discarded) bias load reads the scale stream, which has >= 1 entry per row.
-    r.b = r.has_bias ? egd::buffer(bias, rows * 4u) : r.s;
+    // Without a bias the stream is empty: its loads read zeros without touching memory.
+    r.b = bias != nullptr ? egd::buffer(bias, rows * 4u) : egd::buffer(scales, 0u);
     r.o = egd::buffer(out, (out_offset + rows) * 4u);
     r.rows = rows;
     r.out_offset = out_offset;
@@ -465,8 +457,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   };
 
   // Batched: a segment is read into scalar registers from the kernel arguments (small plans)
-  // or from the LDS table (an LDS read waits on lgkmcnt, so switching segments never waits for
-  // the tile loads in flight, as a global load of the table would).
+  // or with a scalar load from the table in global memory (scalar loads count on lgkmcnt, so
+  // switching segments never waits for the tile loads in flight, as a vector load would). The
+  // table is read-only for the launch, so the constant address space is accurate.
   Seg cur = make_seg(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, 0, a.total_passes);
   uint32_t seg = 0;
   auto use_segment = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
@@ -477,9 +470,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                    rows, __builtin_amdgcn_readfirstlane(out_offset), seg_end - rows / TILE, seg_end);
   };
   auto load_segment = [&](uint32_t sidx) {
-    if (lds_table) {
-      const DevSegment& d = table[sidx];
-      use_segment(d.w, d.scales, d.zeros, d.bias, d.out, d.rows, d.pass_end, d.out_offset);
+    if (a.seg_count > kInlineSegments) {
+      typedef const __attribute__((address_space(4))) DevSegment ConstSegment;
+      ConstSegment* d = (ConstSegment*)(a.segs + sidx);
+      use_segment(d->w, d->scales, d->zeros, d->bias, d->out, d->rows, d->pass_end, d->out_offset);
     } else {
       // kernel-argument table: a select per field over the few entries keeps every value scalar
       auto sel = [&](auto DevSegment::*field) {
@@ -493,20 +487,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                   sel(&DevSegment::out_offset));
     }
   };
-  // The first segment whose pass_end exceeds `begin` = the number of segments ending at or
-  // before it (pass_end increases).
+  // The segment holding the wave's first tile: looked up in the plan's pass index (two
+  // dependent scalar loads, which overlap the input stage's reads), or - small plans - the
+  // number of argument-table segments ending at or before that tile (pass_end increases).
   auto find_first_segment = [&]() {
     uint32_t count = 0;
-    if (lds_table) {
-      // 64 entries per LDS read, counted with a ballot
-      for (uint32_t e0 = 0; e0 < lds_count; e0 += 64) {
-        const uint32_t e = e0 + lane;
-        const bool done = e < lds_count && table[e < lds_count ? e : 0].pass_end <= begin;
-        count += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(done));
-      }
+    if (a.seg_count > kInlineSegments) {
+      typedef const __attribute__((address_space(4))) uint32_t ConstWord;
+      const uint32_t w = *(ConstWord*)(a.seg_index + (first >> 1));
+      count = (w >> ((first & 1u) * 16u)) & 0xFFFFu;
     } else {
 #pragma unroll
-      for (uint32_t i = 0; i < kInlineSegments; i++) count += (i < a.seg_count && a.inline_segs[i].pass_end <= begin);
+      for (uint32_t i = 0; i < kInlineSegments; i++) count += (i < a.seg_count && a.inline_segs[i].pass_end <= first);
     }
     seg = __builtin_amdgcn_readfirstlane(count);
     load_segment(seg);
@@ -515,16 +507,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // What computing a tile needs once its loads are in flight: where its rows are stored.
   struct Pending {
     __amdgpu_buffer_rsrc_t o;
-    uint32_t row0, out_offset, has_bias;
+    uint32_t row0, out_offset;
   };
-  const uint32_t last = end - 1;
 
   // Issues the loads of tile `tl` (clamped to the wave's last tile; tiles are visited in
-  // increasing order, so the segment cursor only moves forward). WB: the launch has biases, so
-  // each row's bias is loaded with its codes (a launch without any skips those loads - a third
-  // of a tile's load instructions - in a separate copy of the loop, so no load sits under a
-  // branch).
-  auto issue = [&](auto WB, uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
+  // increasing order, so the segment cursor only moves forward). The biases of a tile's rows
+  // take one load instruction: lane t < U of each team reads its row t's (lanes past U re-read
+  // row U-1's, unused).
+  const uint32_t boff = ((t < (uint32_t)U ? t : (uint32_t)(U - 1)) * RPW + slot) * 4u;
+  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
     tl = min(tl, last);
     if (MODE == kBatched)
       while (tl >= cur.end) load_segment(++seg);
@@ -533,10 +524,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const uint32_t row0 = __builtin_amdgcn_readfirstlane(min((tl - cur.first) * TILE, cur.rows - TILE));
     const uint32_t sq = row0 * (a.chunks * 16u);
     const uint32_t ss = row0 * (a.blocks_per_row * 4u);
+    L.b = egd::load_f32(cur.b, boff, row0 * 4u);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      if constexpr (decltype(WB)::value) L.b[u] = egd::load_f32(cur.b, roff[u], row0 * 4u);
-      else L.b[u] = 0.f;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
         L.q[u][j] = egd::load_b128_nt(cur.w, qoff[u][j], sq);
@@ -550,48 +540,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     P.o = cur.o;
     P.row0 = row0;
     P.out_offset = cur.out_offset;
-    P.has_bias = cur.has_bias;
   };
 
-  produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch);
-  if (lds_table) {
-    egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(table);
-#pragma unroll
-    for (uint32_t r = 0; r < kTableLoads; r++)
-      if (threadIdx.x + r * 256u < table_vecs) dst[threadIdx.x + r * 256u] = tv[r];
-  }
-  __syncthreads();
-
-  // This lane's activations: chunk slot j covers x[cj*EPC, cj*EPC + EPC), zero past the row.
+  // This lane's activations: chunk slot j covers x[cj*EPC, cj*EPC + EPC), zero past the row
+  // (filled from LDS once the input stage has written x there).
   float xr[CPL][EPC];
   float sx[CPL];
+  auto load_x = [&]() {
 #pragma unroll
-  for (int j = 0; j < CPL; j++) {
-    const bool valid = t + j * TEAM < a.chunks;
-    sx[j] = 0.f;
-    const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + (size_t)cj[j] * (EPC / 4);
+    for (int j = 0; j < CPL; j++) {
+      const bool valid = t + j * TEAM < a.chunks;
+      sx[j] = 0.f;
+      const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + (size_t)cj[j] * (EPC / 4);
 #pragma unroll
-    for (int e = 0; e < EPC / 4; e++) {
-      const egd::u32x4 v = xs[e];
-      xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
-      xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
-      xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
-      xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
+      for (int e = 0; e < EPC / 4; e++) {
+        const egd::u32x4 v = xs[e];
+        xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
+        xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
+        xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
+        xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
+#pragma unroll
+      for (int e = 0; e < EPC; e++) xr[j][e] *= C::x_scale(e);
     }
-#pragma unroll
-    for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
-#pragma unroll
-    for (int e = 0; e < EPC; e++) xr[j][e] *= C::x_scale(e);
-  }
+  };
 
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
-  auto compute = [&](auto WB, const Loads<BITS, U, CPL>& L, const Pending& P) {
+  auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      // The bias starts lane 0's partial (linearQ4 starts its sum from the bias too).
-      float acc = (decltype(WB)::value && t == 0 && P.has_bias) ? L.b[u] : 0.f;
+      // The bias starts lane u's partial (linearQ4 starts its sum from the bias too; zero
+      // where the matrix has none).
+      float acc = t == (uint32_t)u ? L.b : 0.f;
       const uint32_t row = P.row0 + u * RPW + slot;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
@@ -618,42 +602,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
   // The wave's range is one software pipeline over NB load buffers, NB tiles per iteration,
   // with a single exit at the bottom: while tile i is computed, the loads of tiles
-  // i+1 .. i+NB-1 are in flight. Each buffer carries where its rows go, so the pipeline runs
-  // straight through segment boundaries (a boundary costs a few scalar reads, not a drain
-  // of the loads in flight). A count that is not a multiple of NB computes the wave's last
-  // tile again (same loads, same stores) rather than leaving the loop mid-body. With no path
-  // leaving the loop between an issue and its consumer, the compiler's wait counts stay exact -
-  // computing a tile waits only for that tile's loads, never for a later tile's.
+  // i+1 .. i+NB-1 are in flight. The first NB-1 tiles are issued from inside the input stage,
+  // right after its own reads, so they travel while the stage waits and computes. Each buffer
+  // carries where its rows go, so the pipeline runs straight through segment boundaries (a
+  // boundary costs a few scalar reads, not a drain of the loads in flight). A count that is not
+  // a multiple of NB computes the wave's last tile again (same loads, same stores) rather than
+  // leaving the loop mid-body. No load sits under a branch - a wave without tiles issues its
+  // first ones anyway - so the compiler's wait counts stay exact: the input stage waits only
+  // for its own reads, and computing a tile waits only for that tile's loads.
   // sched_barrier(0) after each issue keeps the scheduler from sinking the next tile's loads
   // into the current tile's math.
-  auto pipeline = [&](auto WB) {
+  Loads<BITS, U, CPL> L[NB];
+  Pending P[NB];
+  auto start = [&]() {
     if (MODE == kBatched) find_first_segment();
-    Loads<BITS, U, CPL> L[NB];
-    Pending P[NB];
 #pragma unroll
-    for (int b = 0; b + 1 < NB; b++) issue(WB, begin + b, L[b], P[b]);
-    uint32_t tile = begin;
-    const uint32_t groups = (end - begin + NB - 1) / NB;
-    for (uint32_t g = 0; g < groups; g++) {
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const int nx = (b + NB - 1) % NB;
-        issue(WB, tile + b + NB - 1, L[nx], P[nx]);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(WB, L[b], P[b]);
-      }
-      tile += NB;
-    }
-    // The last NB-1 issues are duplicates that nothing consumes; they complete before the
-    // wave ends.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
+    for (int b = 0; b + 1 < NB; b++) issue(first + b, L[b], P[b]);
+    __builtin_amdgcn_sched_barrier(0);
   };
-  if (begin < end) {
-    if (a.any_bias)
-      pipeline(std::true_type{});
-    else
-      pipeline(std::false_type{});
+  produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
+  __syncthreads();
+  load_x();
+  uint32_t tile = begin;
+  const uint32_t groups = (end - begin + NB - 1) / NB;
+  for (uint32_t g = 0; g < groups; g++) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const int nx = (b + NB - 1) % NB;
+      issue(tile + b + NB - 1, L[nx], P[nx]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(L[b], P[b]);
+    }
+    tile += NB;
   }
+  // The last NB-1 issues (all of them, for a wave without tiles) are duplicates that nothing
+  // consumes; they complete before the wave ends.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
 
   if (kBest) {
     __shared__ float wv[kWaves];

@@ -281,10 +281,11 @@ def test_batched_plan_matches_per_matrix(device):
 
 @pytest.mark.parametrize("k", [896, 4864])
 def test_batched_plan_many_segments(device, k):
-    """A plan of more than four matrices keeps its table in memory, and launches with x given as a
-    vector copy only their workgroup's window of it: segments of 8 to 1024 rows, so windows span
-    one to several segments and the smallest fall inside a single workgroup; biases and outOffsets
-    on some. Every segment against the oracle."""
+    """A plan of more than four matrices keeps its table in device memory with an index of the
+    segment of every pass; each wave looks its first segment up there and walks on through the
+    table: segments of 8 to 1024 rows, so a wave's range spans one to several segments and the
+    smallest fall inside a single workgroup; biases and outOffsets on some. Every segment
+    against the oracle."""
     rows = (8, 16, 24, 136, 8, 512, 64, 8, 32, 1024, 16, 40) if k == 896 else (8, 16, 8, 96, 24, 8, 40, 8)
     x = oracle.normal_floats(k, 1500 + k, 1.0)
     mats = [sym_weights(n, k, 1510 + i) for i, n in enumerate(rows)]
@@ -302,7 +303,7 @@ def test_batched_plan_many_segments(device, k):
         outs.append((bo, off))
         biases.append(bias)
     plan = K.GemvPlan(device, k, 32, segs)
-    for _ in range(2):  # twice: the windows are reused as they are
+    for _ in range(2):  # twice: the table and index are reused as they are
         plan.launch(bx)
         for i, q in enumerate(mats):
             bo, off = outs[i]
