@@ -605,11 +605,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // i+1 .. i+NB-1 are in flight. The first NB-1 tiles are issued from inside the input stage,
   // right after its own reads, so they travel while the stage waits and computes. Each buffer
   // carries where its rows go, so the pipeline runs straight through segment boundaries (a
-  // boundary costs a few scalar reads, not a drain of the loads in flight). A count that is not
-  // a multiple of NB computes the wave's last tile again (same loads, same stores) rather than
-  // leaving the loop mid-body. No load sits under a branch - a wave without tiles issues its
-  // first ones anyway - so the compiler's wait counts stay exact: the input stage waits only
-  // for its own reads, and computing a tile waits only for that tile's loads.
+  // boundary costs a few scalar reads, not a drain of the loads in flight). The loop runs whole
+  // groups of NB tiles; the last count % NB tiles, already in flight, are computed after it. No
+  // load sits under a branch - a wave without tiles issues its first ones anyway, and issues
+  // past the last tile re-read it - so the compiler's wait counts stay exact: the input stage
+  // waits only for its own reads, and computing a tile waits only for that tile's loads.
   // sched_barrier(0) after each issue keeps the scheduler from sinking the next tile's loads
   // into the current tile's math.
   Loads<BITS, U, CPL> L[NB];
@@ -623,8 +623,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
   __syncthreads();
   load_x();
+  const uint32_t count = end - begin;
+  const uint32_t groups = count / NB;
   uint32_t tile = begin;
-  const uint32_t groups = (end - begin + NB - 1) / NB;
   for (uint32_t g = 0; g < groups; g++) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -635,8 +636,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     tile += NB;
   }
-  // The last NB-1 issues (all of them, for a wave without tiles) are duplicates that nothing
-  // consumes; they complete before the wave ends.
+  // The last count % NB tiles are already in flight in buffers 0 .. NB-2 (issued by the last
+  // group, or by the input stage when the wave has fewer than NB tiles): compute them, with no
+  // load under the branch.
+  const uint32_t rem = count - groups * NB;
+#pragma unroll
+  for (int b = 0; b + 1 < NB; b++)
+    if ((uint32_t)b < rem) compute(L[b], P[b]);
+  // Issues past the wave's last tile (clamped to it) are duplicates that nothing consumes;
+  // they complete before the wave ends.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
 
   if (kBest) {
