@@ -17,9 +17,9 @@
 //     does not depend on how the work was scheduled.
 // Rows are padded by 16 bytes in LDS so the 16 lanes that read one column of A (or B) hit
 // different banks. Accumulation is f32 inside the MFMA.
-// Layouts the chunked staging cannot take (K or block size not a multiple of 32 codes, int8
-// codes, unaligned streams, K not a multiple of 4) stage element by element with the
-// reference's indexing.
+// Layouts the chunked staging cannot take (K or block size not a multiple of 32 codes, a block
+// size that is not a power of two, int8 codes, unaligned streams, K not a multiple of 4) stage
+// element by element with the reference's indexing.
 #include <algorithm>
 
 #include "eg_internal.hpp"
@@ -45,6 +45,7 @@ struct PrefillArgs {
   float* partials;  // split-K: [splits][m][n] f32; NULL when grid.z == 1
   uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset, k_per_split;
   int bits;
+  uint32_t block_shift;  // log2(block_size) (the chunked staging takes power-of-two blocks)
 };
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) {
@@ -79,22 +80,46 @@ struct Streams {
 };
 constexpr uint32_t kOutside = 0x80000000u;  // an offset past every stream (streams < 2 GiB here)
 
-template <int ENC>
-__device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& r, uint32_t m0, uint32_t n0,
-                                           uint32_t k0, Staged& st) {
+// This thread's part of every staged block, fixed for the launch: its 4 x vectors (rows
+// m0 + tid/16 + 16i, columns 4 * (tid % 16) of the block) and its 16 codes (row n0 + tid/4,
+// columns 16 * (tid % 4) of the block). A block's loads are then these bases plus the block's
+// column, with no per-block multiplies.
+struct StageBase {
+  uint32_t x[4];    // byte offset of row r_i, column c (block 0), or kOutside when the row is outside
+  uint32_t xc;      // column of the x vectors within a block
+  uint32_t w;       // byte offset of the codes (block 0), or kOutside when the row is outside
+  uint32_t kc;      // column of the codes within a block
+  uint32_t sblk;    // the row's first quant block index
+};
+
+__device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, uint32_t m0, uint32_t n0) {
   const uint32_t tid = threadIdx.x;
+  StageBase b;
+  b.xc = (tid & 15u) * 4u;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint32_t idx = tid + i * 256u;  // 64 rows x 16 float4
-    const uint32_t row = m0 + (idx >> 4), kk = k0 + (idx & 15u) * 4u;
-    const uint32_t off = (row < a.m && kk < a.k) ? (row * a.k + kk) * 4u : kOutside;
-    const egd::u32x4 v = egd::load_b128(r.x, off);
+    const uint32_t row = m0 + (tid >> 4) + 16u * i;
+    b.x[i] = row < a.m ? (row * a.k + b.xc) * 4u : kOutside;
+  }
+  const uint32_t nrow = n0 + (tid >> 2);
+  b.kc = 16u * (tid & 3u);
+  b.w = nrow < a.n ? (nrow * a.k + b.kc) / 2u : kOutside;
+  b.sblk = nrow * a.blocks_per_row;
+  return b;
+}
+
+template <int ENC>
+__device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& r, const StageBase& b, uint32_t k0,
+                                           Staged& st) {
+  const bool xin = k0 + b.xc < a.k;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const egd::u32x4 v = egd::load_b128(r.x, xin && b.x[i] != kOutside ? b.x[i] + k0 * 4u : kOutside);
     st.x[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   }
-  const uint32_t nrow = n0 + (tid >> 2), kk = k0 + 16u * (tid & 3u);
-  const bool in = nrow < a.n && kk < a.k;
-  const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
-  const uint64_t codes = egd::load_b64(r.w, in ? (nrow * a.k + kk) / 2u : kOutside);
+  const bool in = b.w != kOutside && k0 + b.kc < a.k;
+  const uint32_t blk = b.sblk + ((k0 + b.kc) >> a.block_shift);
+  const uint64_t codes = egd::load_b64(r.w, in ? b.w + k0 / 2u : kOutside);
   st.q = make_uint2((uint32_t)codes, (uint32_t)(codes >> 32));
   st.s = egd::load_f32(r.s, in ? blk * 4u : kOutside);
   if (ENC == EG_ENC_OFFSET_ZEROS) {
@@ -115,18 +140,41 @@ __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLd
     *reinterpret_cast<uint2*>(&As[r][c]) =
         make_uint2(pack_bf16(st.x[i].x, st.x[i].y), pack_bf16(st.x[i].z, st.x[i].w));
   }
-  // (code - zero) * scale in f32, exactly the reference's dequantElement (the difference of two
-  // small integers is exact), then bf16.
+  // (code - zero) * scale in f32, exactly the reference's dequantElement, then bf16. Each word's
+  // low and high nibbles are masked in place (the high ones stay 16x, their scale is divided
+  // by 16: exact) and each byte converts straight to f32. Two's-complement codes are flipped
+  // to offset binary c = q + 8 in the same mask, and c * s - 8 * s is one fused multiply-add:
+  // the product is exact inside it and 8 * s is exact, so the single rounding is that of
+  // (c - 8) * s. Offset-binary codes keep the subtraction: (c - z) * s.
   const uint32_t d[2] = {st.q.x, st.q.y};
+  const float s16 = st.s * 0.0625f;
   uint32_t packed[8];
 #pragma unroll
   for (int w = 0; w < 2; w++) {
-    const uint32_t word = ENC == EG_ENC_SIGNED ? d[w] ^ 0x88888888u : d[w];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const float c0 = (float)((word >> (4 * e)) & 0xFu), c1 = (float)((word >> (4 * e + 4)) & 0xFu);
-      packed[(w * 8 + e) / 2] = pack_bf16((c0 - st.z) * st.s, (c1 - st.z) * st.s);
+    uint32_t lo, hi;
+    if (ENC == EG_ENC_SIGNED) {
+      lo = (d[w] & 0x0F0F0F0Fu) ^ 0x08080808u;
+      hi = (d[w] & 0xF0F0F0F0u) ^ 0x80808080u;
+    } else {
+      lo = egd::and_opaque(d[w], 0x0F0F0F0Fu);
+      hi = egd::and_opaque(d[w], 0xF0F0F0F0u);
     }
+    float v[8];
+    const float cl[4] = {egd::ub0(lo), egd::ub1(lo), egd::ub2(lo), egd::ub3(lo)};
+    const float ch[4] = {egd::ub0(hi), egd::ub1(hi), egd::ub2(hi), egd::ub3(hi)};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (ENC == EG_ENC_SIGNED) {
+        const float off = -8.f * st.s;
+        v[2 * j] = fmaf(cl[j], st.s, off);
+        v[2 * j + 1] = fmaf(ch[j], s16, off);
+      } else {
+        v[2 * j] = (cl[j] - st.z) * st.s;
+        v[2 * j + 1] = (ch[j] - 16.f * st.z) * s16;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) packed[(w * 8 + e) / 2] = pack_bf16(v[e], v[e + 1]);
   }
   uint4* dst = reinterpret_cast<uint4*>(&Bs[tid >> 2][16u * (tid & 3u)]);
   dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
@@ -214,9 +262,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(a.packed, a.n * a.k / 2u),
                      egd::buffer(a.scales, a.n * a.blocks_per_row * 4u),
                      egd::buffer(a.zeros, ((a.n * a.blocks_per_row + 7u) / 8u) * 4u)};
+    const StageBase sb = stage_base(a, m0, n0);
     Staged st[S];
 #pragma unroll
-    for (int u = 0; u + 1 < S; u++) load_block<ENC>(a, rs, m0, n0, kbeg + min((uint32_t)u, nblk - 1) * kBK, st[u]);
+    for (int u = 0; u + 1 < S; u++) load_block<ENC>(a, rs, sb, kbeg + min((uint32_t)u, nblk - 1) * kBK, st[u]);
     const uint32_t full = nblk / S;
     for (uint32_t g = 0; g < full; g++) {
 #pragma unroll
@@ -224,7 +273,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         const uint32_t blk = g * S + u;
         store_block<ENC>(st[u], As, Bs);
         __syncthreads();
-        load_block<ENC>(a, rs, m0, n0, kbeg + min(blk + S - 1, nblk - 1) * kBK, st[(u + S - 1) % S]);
+        load_block<ENC>(a, rs, sb, kbeg + min(blk + S - 1, nblk - 1) * kBK, st[(u + S - 1) % S]);
         mfma_block();
         __syncthreads();
       }
@@ -327,9 +376,10 @@ extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint3
   const bool split = splits > 1;
   PrefillArgs a{x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                 out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
-                dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits};
+                dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits,
+                (uint32_t)__builtin_ctz(bs)};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
-  const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && k % 4 == 0 &&
+  const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
                        (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
                        (reinterpret_cast<uintptr_t>(packed) & 7u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (encoding == EG_ENC_SIGNED) {
