@@ -108,7 +108,7 @@ def test_prefill_config3(device, m, n, k):
     assert_close(got, fp32, *prefill_tol(fp32), label=f"config 3 fp32 {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("bits,k,bs", [(4, 40, 8), (8, 128, 64), (4, 96, 32)])
+@pytest.mark.parametrize("bits,k,bs", [(4, 40, 8), (8, 128, 64), (4, 96, 32), (4, 96, 48)])
 def test_prefill_element_staging_path(device, bits, k, bs):
     m, n = 7, 24
     x = oracle.random_floats(m * k, 61)
@@ -119,6 +119,20 @@ def test_prefill_element_staging_path(device, bits, k, bs):
     got = run_prefill(device, x, q, None, m)
     assert_close(got, oracle.linear_q_bf16(x, q, None, m), *model_tol(oracle.linear_q(x, q, None, m)),
                  label=f"element path bits={bits} k={k}")
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_prefill_symmetric_long_blocks(device, bs):
+    # Symmetric int4 with quant blocks of 64 and 128 codes: the staged path finds a code's block
+    # by shift, and a 128-code block spans two 64-deep staging steps.
+    m, n, k = 33, 96, 640
+    x = oracle.normal_floats(m * k, 71, 1.0)
+    q = oracle.quantize_sym(oracle.normal_floats(n * k, 72, 0.02), n, k, 4, bs)
+    got = run_prefill(device, x, q, None, m)
+    model = oracle.linear_q_bf16(x, q, None, m)
+    assert_close(got, model, *model_tol(model), label=f"symmetric block {bs} bf16 model")
+    fp32 = oracle.linear_q(x, q, None, m)
+    assert_close(got, fp32, *prefill_tol(fp32), label=f"symmetric block {bs} fp32")
 
 
 def test_prefill_deterministic(device):
