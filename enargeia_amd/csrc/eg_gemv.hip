@@ -1,6 +1,7 @@
 // Decode-shape (M=1) quantized GEMV: the host side (shape choice, validation, launches, batched
 // plans) and the kernels for inputs given as a vector. The kernel template and its design notes
-// are in eg_gemv_kernel.hpp; the fused input stages are instantiated in eg_gemv_fused.hip.
+// are in eg_gemv_kernel.hpp; the fused input stages are instantiated in eg_gemv_rmsnorm.hip,
+// eg_gemv_silu.hip and eg_gemv_attention.hip.
 //
 // Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
 // (embedding_variants.ts:135-180).

@@ -26,7 +26,8 @@
 //     the logits never need a second pass.
 //
 // This header holds the kernel template; eg_gemv.hip instantiates it for inputs given as a
-// vector (and holds the host side), eg_gemv_fused.hip for the fused input stages.
+// vector (and holds the host side); eg_gemv_rmsnorm.hip, eg_gemv_silu.hip and
+// eg_gemv_attention.hip instantiate it for the fused input stages.
 #pragma once
 
 #include <algorithm>
