@@ -42,6 +42,7 @@ struct eg_decoder {
   eg_graph* graph = nullptr;
   std::vector<void*> allocations;
   uint32_t host_position = 0;  // mirrors position[0]: steps are refused once the cache is full
+  uint32_t* host_token = nullptr;  // pinned: the per-token readback lands here (no staging copy)
 };
 
 namespace {
@@ -53,6 +54,7 @@ int alloc(eg_decoder* d, size_t bytes, void** out) {
 }
 
 void release(eg_decoder* d) {
+  if (d->host_token) (void)hipHostFree(d->host_token);
   if (d->graph) eg_graph_destroy(d->graph);
   for (eg_gemv_plan* p : d->plans) eg_gemv_plan_destroy(d->ctx, p);
   for (void* p : d->allocations) eg_buf_free(d->ctx, p);
@@ -237,6 +239,13 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     if (st != EG_OK) break;
     d->plans.push_back(plan);
   }
+  if (st == EG_OK) {
+    const hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), sizeof(uint32_t), hipHostMallocDefault);
+    if (err != hipSuccess) {
+      d->host_token = nullptr;
+      st = eg::hip_fail(ctx, err, op);
+    }
+  }
   if (st != EG_OK) {
     // keep the plan error message; release() only frees
     release(d);
@@ -287,7 +296,15 @@ int eg_decoder_step(eg_decoder* d, uint32_t* token_out) {
     return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_step: context of %u positions exhausted", d->desc.max_context);
   int st = d->graph ? eg_graph_launch(d->ctx, d->graph) : run_step(d);
   if (st == EG_OK) d->host_position++;
-  if (st == EG_OK && token_out) st = eg_buf_read(d->ctx, d->token, 0, token_out, 4);
+  if (st == EG_OK && token_out) {
+    if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_step: a graph capture is in progress");
+    // the one readback per token, into pinned memory: a direct copy, no staging through a
+    // bounce buffer as a pageable destination would need
+    hipError_t err = hipMemcpyAsync(d->host_token, d->token, sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(d->ctx->stream);
+    if (err != hipSuccess) return eg::hip_fail(d->ctx, err, "decoder_step");
+    *token_out = *d->host_token;
+  }
   return st;
 }
 
