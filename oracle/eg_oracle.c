@@ -30,8 +30,8 @@
  *                                rounding checked against numpy/torch conversions.
  *   eo_argmax(_wgsl)           — forward_ops.test.ts:397-446 (seed 101, logits[123456]=99 ->
  *                                123456; tie at 100 and 900 -> 100) and numpy.argmax.
- *   eo_sample                  — the reference holds no CPU sampler and no sampled vectors
- *                                (SURVEY row c): pinned by properties only — T=0 equals argmax,
+ *   eo_sample                  — the reference holds no CPU sampler and no sampled vectors:
+ *                                pinned by properties only — T=0 equals argmax,
  *                                T=0.01/topP=1 equals greedy, kept mass >= topP, the draw is the
  *                                first ascending-id crossing, penalty set/sign rule against a
  *                                brute-force restatement, and an independent float64 nucleus
