@@ -99,6 +99,26 @@ def make_projection_set():
     return mats
 
 
+def make_replica(dev, mats, out) -> dict:
+    """One copy of the projection set on the device and the step's two batched plans: every
+    K=896 matrix (q, k, v, o, gate, up of the 24 layers: 144 segments) in one plan and every
+    K=4864 one (down: 24 segments) in the other, each matrix writing its rows at its offset in
+    `out` (the order of `mats`)."""
+    from enargeia_amd import kernels as K
+
+    bufs, seg896, seg4864, singles = [], [], [], []
+    off = 0
+    for name, q in mats:
+        bp, bs = dev.upload(q.packed), dev.upload(q.scales)
+        bufs += [bp, bs]
+        seg = (bp, bs, None, None, out, q.rows, off)
+        (seg896 if q.cols == HIDDEN else seg4864).append(seg)
+        singles.append((name, q, bp, bs, off))
+        off += q.rows
+    plans = (K.GemvPlan(dev, HIDDEN, GROUP, seg896), K.GemvPlan(dev, INTER, GROUP, seg4864))
+    return {"bufs": bufs, "plans": plans, "singles": singles}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,19 +176,7 @@ def main() -> int:
     out = dev.buffer(rows_total * 4)
 
     # ---- weights: R replicas, each with its own plans and per-op graph ----
-    replicas = []
-    for r in range(R):
-        bufs, seg896, seg4864, singles = [], [], [], []
-        off = 0
-        for name, q in mats:
-            bp, bs = dev.upload(q.packed), dev.upload(q.scales)
-            bufs += [bp, bs]
-            seg = (bp, bs, None, None, out, q.rows, off)
-            (seg896 if q.cols == HIDDEN else seg4864).append(seg)
-            singles.append((name, q, bp, bs, off))
-            off += q.rows
-        plans = (K.GemvPlan(dev, HIDDEN, GROUP, seg896), K.GemvPlan(dev, INTER, GROUP, seg4864))
-        replicas.append({"bufs": bufs, "plans": plans, "singles": singles})
+    replicas = [make_replica(dev, mats, out) for _ in range(R)]
     log(f"uploaded {R} replicas of {STEP_BYTES / 1e6:.1f} MB")
 
     dec = K.ComputeKernel(dev, K.with_format(K.MATMUL_Q4_DECODE, 4, K.ENC_SIGNED))
@@ -378,40 +386,75 @@ def main() -> int:
 DECODE_STEPS = 128
 
 
+GOLDEN_DECODE = os.path.join(ROOT, "tests", "golden", "config4_decode.npz")
+
+
+def verify_decode_tokens(tokens: list, first_step: int) -> dict:
+    """Compares the greedy tokens of the timed steps with the CPU oracle's run of the same
+    workload (tests/golden/config4_decode.npz): tokens[i] is the output of workload step
+    first_step + i. A step counts when the oracle's top-2 gap exceeds 1e-2 x rms(logits); a
+    differing token at a near-tie ends the comparison (later steps then see other inputs)."""
+    with np.load(GOLDEN_DECODE, allow_pickle=False) as g:
+        want, gaps, rms = g["tokens"], g["gaps"], g["rms"]
+    compared = mismatches = near_ties = 0
+    diverged_at = None
+    for i, tok in enumerate(tokens):
+        s = first_step + i
+        if gaps[s] > 1e-2 * rms[s]:
+            compared += 1
+            if tok != int(want[s]):
+                mismatches += 1
+                break
+        else:
+            near_ties += 1
+            if tok != int(want[s]):
+                diverged_at = s
+                break
+    return {"oracle": "tests/golden/config4_decode.npz", "compared": compared, "mismatches": mismatches,
+            "near_ties": near_ties, "diverged_at_near_tie": diverged_at,
+            "verified": mismatches == 0}
+
+
 def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     """the Qwen2.5-0.5B-shaped model (synthetic weights, int4 g32 projections,
-    int8 tied head, f16 KV cache), cache filled to 2048 - 128 positions (random f16 rows, the
-    reference's prime-then-decode method, decode.test.ts:97-118), then 128 greedy steps to
-    position 2047. One step = the whole token: embedding, 24 layers, LM head, argmax. tok_s
-    includes the one 4-byte readback per token (Session.decodeStep's rule); device_tok_s
-    chains the steps on the device with no readback."""
-    from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, synthetic_model
+    int8 tied head, f16 KV cache) on the workload of enargeia_amd.model.config4_workload: cache
+    rows [0, 1888) random f16 (the reference's prime-then-decode method, decode.test.ts:97-118),
+    a 32-token prompt at positions 1888..1919 (untimed), then 128 greedy steps at positions
+    1920..2047, timed. One step = the whole token: embedding, 24 layers, LM head, argmax. tok_s
+    includes the one 4-byte readback per token (Session.decodeStep's rule); device_tok_s chains
+    the steps on the device with no readback. The timed steps' tokens are checked against the CPU
+    oracle's run of the same workload."""
+    from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, cache_fill, config4_workload, synthetic_model
 
     cfg = QWEN25_05B
+    w = config4_workload(cfg)
+    assert w.steps == DECODE_STEPS and w.prime + len(w.prompt) + w.steps == cfg.max_context
     t0 = time.time()
     host = synthetic_model(cfg)
     dm = DeviceModel(dev, host)
     del host
     dec = Decoder(dm)
+    kf, vf = cache_fill(cfg, w.fill_seed)
+    dev.write(dec.buffers.k_cache, kf.view(np.uint16))
+    dev.write(dec.buffers.v_cache, vf.view(np.uint16))
+    dev.sync()
+    del kf, vf
     log(f"decode model ready in {time.time() - t0:.1f}s")
-    rng = np.random.default_rng(11)
-    prime = cfg.max_context - DECODE_STEPS
-    rows = cfg.layers * cfg.max_context * cfg.kv_heads * cfg.head_dim
-    for ptr in (dec.buffers.k_cache, dec.buffers.v_cache):
-        fill = rng.standard_normal(rows, dtype=np.float32).astype(np.float16).view(np.uint16)
-        dev.write(ptr, fill)
-        dev.sync()
-    first = 785  # the first greedy id of the reference's fixture prompt; any id works
+    start = w.prime + len(w.prompt)
     result = {"config": "BASELINE config 4: Qwen2.5-0.5B shape, 24 layers, int4 g32 + int8 tied head, f16 KV",
-              "context": cfg.max_context, "steps": DECODE_STEPS, "launches_per_token": 5 * cfg.layers + 2}
+              "context": cfg.max_context, "prompt": len(w.prompt), "steps": DECODE_STEPS,
+              "positions": [start, cfg.max_context - 1], "launches_per_token": 5 * cfg.layers + 2}
     for mode in modes:
         if mode == "graph":
             dec.capture()
-        # warm-up steps end at the prime point, then the timed steps run prime .. 2047
-        dec.reset(prime - 8, first)
+        # the prompt (untimed): each token at its position, the last one's argmax is the first input
+        for i, t in enumerate(w.prompt):
+            dec.reset(w.prime + i, t)
+            first = dec.step(read_token=True)
+        # warm-up: steps at positions start.. (rewritten identically by the timed steps)
         for _ in range(8):
             dec.step(read_token=False)
-        dev.sync()
+        dec.reset(start, first)
         a, b = ev.create(), ev.create()
         t = time.perf_counter()
         ev.record(a, stream)
@@ -421,8 +464,9 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
         wall = time.perf_counter() - t
         result[f"{mode}_tok_s"] = round(DECODE_STEPS / wall, 1)
         result[f"{mode}_ms_per_token"] = round(wall / DECODE_STEPS * 1e3, 4)
+        result[f"{mode}_tokens_vs_oracle"] = verify_decode_tokens([first] + tokens, len(w.prompt) - 1)
         # device-chained: same steps, no per-token readback
-        dec.reset(prime, first)
+        dec.reset(start, first)
         ev.record(a, stream)
         for _ in range(DECODE_STEPS):
             dec.step(read_token=False)
@@ -430,12 +474,14 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
         ev.sync(b)
         result[f"{mode}_device_tok_s"] = round(DECODE_STEPS / (ev.ms(a, b) * 1e-3), 1)
         log(f"decode ({mode}): {result[f'{mode}_tok_s']} tok/s with a readback per token, "
-            f"{result[f'{mode}_device_tok_s']} tok/s device-chained; last token {tokens[-1]}")
+            f"{result[f'{mode}_device_tok_s']} tok/s device-chained; tokens vs oracle "
+            f"{result[f'{mode}_tokens_vs_oracle']}")
     best = max(modes, key=lambda m: result[f"{m}_tok_s"])
     result["tok_s"] = result[f"{best}_tok_s"]
     result["launch"] = best
+    result["verified"] = all(result[f"{m}_tokens_vs_oracle"]["verified"] for m in modes)
     step_bytes = (STEP_BYTES + LM_HEAD_BYTES
-                  + 2 * cfg.layers * (prime + DECODE_STEPS // 2) * cfg.kv_heads * cfg.head_dim * 2)
+                  + 2 * cfg.layers * (start + DECODE_STEPS // 2) * cfg.kv_heads * cfg.head_dim * 2)
     result["gbs_at_best"] = round(step_bytes * result["tok_s"] / 1e9, 1)
     dec.close()
     dm.release()

@@ -58,18 +58,15 @@ def write_enargeia(path: str, tensors, block_size: int = BLOCK,
     """Writes `tensors` (name -> QuantTensor in the offset format, or a float32 / float16 array)
     in the given order: each range 256-byte aligned in the blob, the header compact JSON, then
     zeros to the next 256-byte boundary. Returns the header dict."""
-    entries, chunks, cursor = {}, [], 0
+    entries = {}
+    blob = bytearray()
 
-    def append(payload: bytes) -> list:
-        nonlocal cursor
-        pad = (-cursor) % ALIGN
-        if pad:
-            chunks.append(b"\0" * pad)
-            cursor += pad
-        begin = cursor
-        chunks.append(payload)
-        cursor += len(payload)
-        return [begin, cursor]
+    def place(payload: bytes) -> list:
+        """Appends payload at the next multiple of ALIGN (zero-filled gap): its [begin, end)."""
+        blob.extend(bytes(-len(blob) % ALIGN))
+        start = len(blob)
+        blob.extend(payload)
+        return [start, len(blob)]
 
     for name, t in tensors.items() if isinstance(tensors, dict) else tensors:
         if isinstance(t, QuantTensor):
@@ -77,17 +74,17 @@ def write_enargeia(path: str, tensors, block_size: int = BLOCK,
                 raise ValueError(f"{name}: the container stores the offset format (codes, scales, zeros)")
             entries[name] = {"dtype": "Q4" if t.bits == 4 else "Q8", "shape": [t.rows, t.cols],
                              "blockSize": t.block_size,
-                             "offsets": {"packed": append(np.ascontiguousarray(t.packed, np.uint32).tobytes()),
-                                         "scales": append(np.ascontiguousarray(t.scales, np.float32).tobytes()),
-                                         "zeros": append(np.ascontiguousarray(t.zeros, np.uint32).tobytes())}}
+                             "offsets": {"packed": place(np.ascontiguousarray(t.packed, np.uint32).tobytes()),
+                                         "scales": place(np.ascontiguousarray(t.scales, np.float32).tobytes()),
+                                         "zeros": place(np.ascontiguousarray(t.zeros, np.uint32).tobytes())}}
         else:
             a = np.asarray(t)
             dt = "F16" if a.dtype == np.float16 else "F32"
             a = np.ascontiguousarray(a, np.float16 if dt == "F16" else np.float32)
-            entries[name] = {"dtype": dt, "shape": list(a.shape), "offsets": {"data": append(a.tobytes())}}
+            entries[name] = {"dtype": dt, "shape": list(a.shape), "offsets": {"data": place(a.tobytes())}}
     header = {"generator": generator, "blockSize": block_size, "quantization": quantization, "tensors": entries}
     raw = json.dumps(header, separators=(",", ":")).encode("utf-8")
-    write_raw(path, raw, b"".join(chunks))
+    write_raw(path, raw, bytes(blob))
     return header
 
 

@@ -275,6 +275,8 @@ int eg_decoder_buffers_get(eg_decoder* d, eg_decoder_buffers* out) {
 
 int eg_decoder_reset(eg_decoder* d, uint32_t position, uint32_t token) {
   if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_reset: decoder is NULL");
+  // a reset writes and synchronises: nothing of it may land in a caller's capture
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_reset: a graph capture is in progress");
   if (position >= d->desc.max_context)
     return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_reset: position %u past the context of %u", position,
                     d->desc.max_context);
@@ -291,13 +293,15 @@ int eg_decoder_reset(eg_decoder* d, uint32_t position, uint32_t token) {
 
 int eg_decoder_step(eg_decoder* d, uint32_t* token_out) {
   if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_step: decoder is NULL");
+  // Refused before anything is enqueued: launches recorded into a caller's capture would not
+  // run now, yet the host's position would advance and no longer match the device's.
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_step: a graph capture is in progress");
   // kvcache.ts:118-127: a full context is an error, not a silent overwrite
   if (d->host_position >= d->desc.max_context)
     return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_step: context of %u positions exhausted", d->desc.max_context);
   int st = d->graph ? eg_graph_launch(d->ctx, d->graph) : run_step(d);
   if (st == EG_OK) d->host_position++;
   if (st == EG_OK && token_out) {
-    if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_step: a graph capture is in progress");
     // the one readback per token, into pinned memory: a direct copy, no staging through a
     // bounce buffer as a pageable destination would need
     hipError_t err = hipMemcpyAsync(d->host_token, d->token, sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);

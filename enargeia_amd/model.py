@@ -99,6 +99,39 @@ def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED, fmt: str 
     return HostModel(cfg, layers, embedding, final)
 
 
+# ---- BASELINE config 4's decode run ------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class DecodeWorkload:
+    """The config-4 decode run, following the reference's prime-then-decode method
+    (test/parity/decode.test.ts:97-118): cache rows [0, prime) hold random f16 keys and values,
+    the prompt enters at positions [prime, prime + len(prompt)), and `steps` greedy steps follow,
+    so the last step runs at position max_context - 1."""
+
+    prime: int
+    prompt: tuple
+    steps: int
+    fill_seed: int
+
+
+def config4_workload(cfg: ModelConfig = QWEN25_05B, prompt_len: int = 32, steps: int = 128,
+                     seed: int = 0x5EED ^ 0x4000, fill_seed: int = 11) -> DecodeWorkload:
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, prompt_len)
+    return DecodeWorkload(cfg.max_context - prompt_len - steps, tuple(int(t) for t in prompt), steps, fill_seed)
+
+
+def cache_fill(cfg: ModelConfig, seed: int):
+    """Random f16 cache contents [layers][max_context][kv_heads][head_dim] for keys, then values
+    (one generator, keys drawn first)."""
+    rng = np.random.default_rng(seed)
+    shape = (cfg.layers, cfg.max_context, cfg.kv_heads, cfg.head_dim)
+    n = int(np.prod(shape))
+    k = rng.standard_normal(n, dtype=np.float32).astype(np.float16).reshape(shape)
+    v = rng.standard_normal(n, dtype=np.float32).astype(np.float16).reshape(shape)
+    return k, v
+
+
 # ---- the C structs --------------------------------------------------------------------------
 
 

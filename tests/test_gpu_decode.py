@@ -151,19 +151,22 @@ def test_silu_mul_input_stage(device):
     assert_close(got, want, 1e-5 * rms(want), 1e-3, label="silu*up input")
 
 
-def test_attention_input_stage_equals_combine(device):
-    """The o projection's input stage must combine the partials exactly as eg_attention_combine."""
-    cfg = ModelConfig()
-    pos = 700
+@pytest.mark.parametrize("chunk,max_context,pos", [(64, 2048, 700), (128, 2048, 700), (128, 2048, 2047),
+                                                   (128, 512, 300), (128, 256, 130)])
+def test_attention_input_stage_equals_combine(device, chunk, max_context, pos):
+    """The o projection's input stage must combine the partials exactly as eg_attention_combine:
+    32 chunks (the looped statistics), 16 and 4 chunks (the batched ones, chunks % 4 == 0 and
+    <= 16), 2 chunks (looped)."""
+    cfg = ModelConfig(max_context=max_context)
     rng = np.random.default_rng(7)
     H, KV, D, T = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.max_context
-    dims = attention_dims(cfg, 64)
+    dims = attention_dims(cfg, chunk)
     kc = rng.standard_normal((T, KV, D)).astype(np.float16).view(np.uint16)
     bufs = [device.upload(a) for a in (rng.standard_normal(H * D).astype(np.float32),
                                         rng.standard_normal(KV * D).astype(np.float32),
                                         rng.standard_normal(KV * D).astype(np.float32), kc, kc.copy(),
                                         np.array([pos], np.uint32))]
-    part = device.buffer(KV * (T // 64) * (H // KV) * (D + 2) * 4)
+    part = device.buffer(KV * (T // chunk) * (H // KV) * (D + 2) * 4)
     comb = device.buffer(H * D * 4)
     vp = ctypes.c_void_p
     q, k, v, kcb, vcb, pb = bufs
@@ -233,6 +236,39 @@ def test_decoder_matches_oracle_prompt_then_greedy(device, small_model):
     assert checked == 48
 
 
+@pytest.mark.parametrize("max_context,prime", [(512, 120), (2048, 1016)])
+def test_decoder_long_context_crosses_chunks(device, max_context, prime):
+    """The decoder over a primed cache (random f16 rows [0, prime), the same on both sides),
+    stepping across a 128-position chunk boundary: 4 chunks at 512 and 16 at 2048 take the
+    o projection's batched combine statistics; logits and greedy tokens against the oracle at
+    the decoder bar, every step."""
+    cfg = ModelConfig(layers=2, max_context=max_context)
+    m = synthetic_model(cfg)
+    dm = DeviceModel(device, m)
+    dec = Decoder(dm)
+    ora = OracleDecoder(m, max_context=max_context)
+    rng = np.random.default_rng(max_context)
+    shape = (cfg.layers, max_context, cfg.kv_heads, cfg.head_dim)
+    kf = rng.standard_normal(shape, dtype=np.float32).astype(np.float16)
+    vf = rng.standard_normal(shape, dtype=np.float32).astype(np.float16)
+    ora.k[:] = kf.astype(np.float32)
+    ora.v[:] = vf.astype(np.float32)
+    try:
+        device.write(dec.buffers.k_cache, kf.view(np.uint16))
+        device.write(dec.buffers.v_cache, vf.view(np.uint16))
+        device.sync()
+        tok = prompt_ids(1, cfg.vocab, max_context)[0]
+        dec.reset(prime, tok)
+        for pos in range(prime, prime + 16):
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got_token, f"context {max_context} pos {pos}")
+            tok = got_token
+        assert dec.position() == prime + 16
+    finally:
+        dec.close()
+        dm.release()
+
+
 def test_decoder_graph_replay_equals_eager(device, small_model):
     dm = DeviceModel(device, small_model)
     eager, graph = Decoder(dm), Decoder(dm)
@@ -275,6 +311,31 @@ def test_decoder_rejects_bad_reset(device, small_model):
             dec.reset(SMALL.max_context, 0)
         with pytest.raises(_lib.EgError):
             dec.reset(0, SMALL.vocab)
+    finally:
+        dec.close()
+        dm.release()
+
+
+def test_decoder_refuses_calls_inside_a_capture(device, small_model):
+    """A step or reset while the context captures would record launches that do not run and
+    desynchronise the host's position: both are refused before anything is enqueued."""
+    dm = DeviceModel(device, small_model)
+    dec = Decoder(dm)
+    try:
+        dec.reset(3, 17)
+        device.capture_begin()
+        try:
+            with pytest.raises(_lib.EgError) as e:
+                dec.step(read_token=False)
+            assert e.value.status == _lib.EG_ERR_STATE
+            with pytest.raises(_lib.EgError) as e:
+                dec.reset(0, 1)
+            assert e.value.status == _lib.EG_ERR_STATE
+        finally:
+            device.capture_end().destroy()
+        assert dec.position() == 3
+        dec.step()
+        assert dec.position() == 4
     finally:
         dec.close()
         dm.release()
