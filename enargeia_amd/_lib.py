@@ -46,6 +46,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_matmul_q4_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_lm_head": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_lm_head_argmax": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "eg_lm_head_argmax_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_gemv_plan_create": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32, _i, _i, _vp, ctypes.c_uint32,
                                  ctypes.POINTER(_vp)]),
     "eg_gemv_plan_launch": (_i, [_vp, _vp, _vp]),

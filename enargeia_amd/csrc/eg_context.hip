@@ -123,6 +123,13 @@ int eg_create(int device, eg_context** out_ctx) {
     delete ctx;
     return hip_fail(nullptr, err, "eg_create: workspace init");
   }
+  if (eg::noalloc_scratch_init(ctx) != EG_OK) {
+    fail(nullptr, EG_ERR_DEVICE, "%s", ctx->error);
+    hipFree(ctx->workspace);
+    hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return EG_ERR_DEVICE;
+  }
   *out_ctx = ctx;
   return EG_OK;
 }

@@ -6,6 +6,8 @@
 // Reference ops: matmul_q4_decode (matmul_q4_decode.wgsl:56-101) and lm_head_q4/q8
 // (embedding_variants.ts:135-180).
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "eg_gemv_kernel.hpp"
@@ -185,6 +187,8 @@ struct QuantView {
   uint32_t* result;  // non-null for the fused argmax
   const eg_gemv_input* input = nullptr;  // fused input stage; NULL: x as given
   uint32_t* groups_out = nullptr;  // fused argmax: skip the finalize, report the partials' count here
+  uint32_t* partials = nullptr;    // fused argmax: where the partials go (NULL: the context workspace)
+  size_t partials_bytes = 0;       // its size
 };
 
 // LDS the input stage needs beyond x and the segment table.
@@ -275,7 +279,15 @@ int launch(eg_context* ctx, const QuantView& v) {
   Shape shape;
   if (aligned && v.k % epc == 0 && v.block_size % epc == 0)
     shape = choose_shape(v.n, chunks, ctx);
-  uint32_t* partials = reinterpret_cast<uint32_t*>(eg::partials(ctx));
+  uint32_t* partials = v.partials ? v.partials : reinterpret_cast<uint32_t*>(eg::partials(ctx));
+  const size_t partials_cap = v.partials ? v.partials_bytes : eg::kPartialsBytes;
+  // one (value bits, index) partial per workgroup, checked before anything is launched
+  auto partials_fit = [&](uint64_t groups) {
+    return !argmax || groups * 8 <= partials_cap ? EG_OK
+                                                 : eg::fail(ctx, EG_ERR_RANGE,
+                                                            "%s: %llu workgroups' partials exceed the %zu-byte buffer",
+                                                            v.op, (unsigned long long)groups, partials_cap);
+  };
   uint32_t grid = 0;
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   const int in_kind = v.input ? v.input->kind : EG_INPUT_VECTOR;
@@ -307,12 +319,14 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.any_bias = v.bias != nullptr;
     const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
+    if ((st = partials_fit(grid)) != EG_OK) return st;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   } else {
     uint64_t blocks = (v.n + kWaves - 1) / kWaves;
     const uint64_t cap = (uint64_t)ctx->cu_count * 8;
     if (blocks > cap) blocks = cap;
     grid = (uint32_t)blocks;
+    if ((st = partials_fit(grid)) != EG_OK) return st;
     if (argmax)
       hipLaunchKernelGGL(gemv_generic_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, v.x,
                          v.packed, v.scales, v.zeros, v.bias, v.out, v.n, v.k, v.block_size, v.blocks_per_row,
@@ -328,6 +342,37 @@ int launch(eg_context* ctx, const QuantView& v) {
 }
 
 }  // namespace
+
+// ---- the fixed scratch of eg_lm_head_argmax_noalloc ----------------------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy, at its own
+// address, until the process ends. In host code `scratch` names the symbol, not device memory,
+// so it is never passed to a kernel: eg::noalloc_scratch_init resolves this device's copy with
+// hipGetSymbolAddress once per device (at eg_create, with the device current) and the entry
+// point hands kernels that address. 64 KiB = 8192 (value bits, index) partials, four times the
+// largest grid the LM head launches (256 CUs x 8 resident workgroups).
+constexpr size_t kNoAllocScratchBytes = 64u << 10;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_lock;
+std::unordered_map<int, void*> g_scratch_address;  // device -> its copy of `scratch`
+}  // namespace
+
+int eg::noalloc_scratch_init(eg_context* ctx) {
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  auto it = g_scratch_address.find(ctx->device);
+  if (it == g_scratch_address.end()) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      ctx->noalloc_scratch = nullptr;
+      return eg::hip_fail(ctx, err != hipSuccess ? err : hipErrorInvalidSymbol, "eg_create: hipGetSymbolAddress(scratch)");
+    }
+    it = g_scratch_address.emplace(ctx->device, ptr).first;
+  }
+  ctx->noalloc_scratch = it->second;
+  return EG_OK;
+}
 
 extern "C" {
 
@@ -366,6 +411,21 @@ int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, c
     if ((uint64_t)ctx->cu_count * 8 > max_groups)
       return eg::fail(ctx, EG_ERR_RANGE, "lm_head_argmax: workspace too small for the grid");
   }
+  return launch(ctx, v);
+}
+
+int eg_lm_head_argmax_noalloc(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                              const uint32_t* zeros, float* out, uint32_t* result, const eg_embedding_dims* dims,
+                              int encoding, int bits) {
+  const char* op = "lm_head_argmax_noalloc";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!dims) return eg::fail(ctx, EG_ERR_INVALID, "%s: dims is NULL", op);
+  if (!result) return eg::fail(ctx, EG_ERR_INVALID, "%s: result is NULL", op);
+  if (!ctx->noalloc_scratch) return eg::fail(ctx, EG_ERR_STATE, "%s: the device's scratch address is unknown", op);
+  QuantView v{op, x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out, dims->row_count,
+              dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding, bits, result};
+  v.partials = static_cast<uint32_t*>(ctx->noalloc_scratch);
+  v.partials_bytes = kNoAllocScratchBytes;
   return launch(ctx, v);
 }
 

@@ -23,6 +23,9 @@ struct eg_context {
   uint8_t* workspace = nullptr;
   size_t workspace_bytes = 0;
   bool capturing = false;
+  // This device's copy of the fixed scratch array of eg_lm_head_argmax_noalloc (resolved by
+  // eg::noalloc_scratch_init at creation; shared by every context on the device).
+  void* noalloc_scratch = nullptr;
   // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth) from
   // EG_GEMV_SHAPE="t,c,u[,d]", read once at creation; zeros mean the built-in choice. For
   // tuning sweeps.
@@ -84,6 +87,10 @@ int launch_step_tail(eg_context* ctx, const uint32_t* partials, uint32_t groups,
 int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
                           const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
                           const eg_attention_dims* dims, const double* rope);
+
+// Resolves the calling thread's current device's copy of the no-alloc scratch array
+// (hipGetSymbolAddress, once per device) into ctx->noalloc_scratch.
+int noalloc_scratch_init(eg_context* ctx);
 
 // Workgroups of `kernel` (256 threads, `smem_bytes` of dynamic LDS) resident per CU, cached
 // per context; 0 if the runtime cannot say.

@@ -164,6 +164,17 @@ EG_API int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* pa
                       const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
                       const eg_embedding_dims* dims, int encoding, int bits);
 
+/* eg_lm_head_argmax for callers that cannot allocate device memory (code under graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): no counterpart in the reference. Same
+ * arguments, kernels and results; the per-workgroup argmax partials go to a fixed 64 KiB device
+ * array of the library (one per GPU, held until the process ends) instead of the context's
+ * workspace, and the call allocates and frees nothing. A launch needing more than 8192 partials
+ * fails with EG_ERR_RANGE (the largest grid it makes is 2048). Every call on one GPU shares that
+ * array: calls that overlap on one GPU (two streams, two contexts) race. */
+EG_API int eg_lm_head_argmax_noalloc(eg_context* ctx, const float* x, const uint32_t* packed,
+                                     const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
+                                     const eg_embedding_dims* dims, int encoding, int bits);
+
 /* Several decode GEMVs that share one input vector and one K, in ONE launch: no counterpart
  * op in the reference, which dispatches matmul_q4_decode once per projection
  * (graph_decode.ts:214-236). For q|k|v of a layer (same normed input), gate|up, or one shape
