@@ -379,25 +379,29 @@ int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, 
 }
 
 
-// The end of a greedy decode step and the start of the next, in one launch: the LM head's
-// argmax partials reduced to the token (the same (value, index) order as the argmax finalize:
-// larger value, then lower index), the position advanced, the next step's input - the new
-// token's embedding row, dequantized - and the RoPE cos/sin of the next position, which every
-// attention launch of that step then reads instead of computing. Without partials (a reset) the
-// token and position already in device memory are used as they are.
-__global__ __launch_bounds__(kThreads) void step_tail_kernel(const uint32_t* partials, uint32_t groups,
-                                                             uint32_t* token, uint32_t* position,
+// The end of a decode step and the start of the next, in one launch: the step's token settled
+// (a greedy step reduces the LM head's argmax partials - the same (value, index) order as the
+// argmax finalize: larger value, then lower index; a prompt-fill step takes the next prompt id;
+// a sampled step's sampler has already written it), the position advanced, the token appended
+// to the sampler's history (Session pushes every produced token, session.ts:437-445) and, for a
+// greedy step, the draw state advanced (Session draws once per decodeStep whatever the
+// temperature, session.ts:351); then the next step's input - the new token's embedding row,
+// dequantized - and the RoPE cos/sin of the next position, which every attention launch of that
+// step reads instead of computing. Without `advance` (a reset) the token and position already in
+// device memory are used as they are.
+__global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uint32_t* token, uint32_t* position,
                                                              const uint32_t* packed, const float* scales,
                                                              const uint32_t* zeros, eg_embedding_dims d, int encoding,
                                                              int bits, float* emb, double2* rope, float theta) {
   constexpr int D = 64;
   __shared__ uint32_t next_token, next_pos;
-  if (partials) {
+  uint32_t greedy_id = 0;  // thread 0: the reduced token of a greedy step
+  if (t.advance && t.partials) {
     float bv = -1.0e30f;
     uint32_t bi = 0;
-    for (uint32_t b = threadIdx.x; b < groups; b += kThreads) {
-      const float v = __uint_as_float(partials[2 * b]);
-      const uint32_t i = partials[2 * b + 1];
+    for (uint32_t b = threadIdx.x; b < t.groups; b += kThreads) {
+      const float v = __uint_as_float(t.partials[2 * b]);
+      const uint32_t i = t.partials[2 * b + 1];
       if (egd::better(v, i, bv, bi)) {
         bv = v;
         bi = i;
@@ -419,13 +423,28 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(const uint32_t* par
         }
       token[0] = bi;
       token[1] = __float_as_uint(bv);
-      next_token = bi;
+      greedy_id = bi;
+    }
+  }
+  if (threadIdx.x == 0) {
+    if (t.advance) {
+      const uint32_t id = t.partials ? greedy_id : t.token_src ? *t.token_src : token[0];
+      if (t.token_src) token[0] = id;
       next_pos = position[0] + 1;
       position[0] = next_pos;
+      if (t.history && !t.token_src) {
+        const uint32_t n = *t.history_length;
+        if (n < t.history_capacity) {
+          t.history[n] = id;
+          *t.history_length = n + 1;
+        }
+      }
+      if (t.rng) (void)egd::mulberry32_next(t.rng);
+      next_token = id;
+    } else {
+      next_token = token[0];
+      next_pos = position[0];
     }
-  } else if (threadIdx.x == 0) {
-    next_token = token[0];
-    next_pos = position[0];
   }
   __syncthreads();
   const uint32_t id = next_token, pos = next_pos;
@@ -459,13 +478,15 @@ int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const f
                           dims, rope);
 }
 
-int eg::launch_step_tail(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t* token,
-                         uint32_t* position, const uint32_t* packed, const float* scales, const uint32_t* zeros,
+int eg::launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32_t* position,
+                         const uint32_t* packed, const float* scales, const uint32_t* zeros,
                          const eg_embedding_dims* ed, int encoding, int bits, float* emb, double* rope,
                          uint32_t head_dim, float theta) {
   if (head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "step_tail: head_dim %u (64 is supported)", head_dim);
-  hipLaunchKernelGGL(step_tail_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, partials, groups, token, position,
-                     packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, *ed, encoding, bits, emb,
+  if ((t.history == nullptr) != (t.history_length == nullptr))
+    return eg::fail(ctx, EG_ERR_INVALID, "step_tail: history and history_length go together");
+  hipLaunchKernelGGL(step_tail_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, t, token, position, packed, scales,
+                     encoding == EG_ENC_SIGNED ? nullptr : zeros, *ed, encoding, bits, emb,
                      reinterpret_cast<double2*>(rope), theta);
   return eg::check_launch(ctx, "step_tail");
 }

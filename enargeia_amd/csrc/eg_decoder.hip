@@ -8,12 +8,17 @@
 //   o       GEMV whose input stage combines the partials; bias = the residual stream
 //   gate|up one batched GEMV, RMSNorm(post_attention_layernorm) fused into its input stage
 //   down    GEMV whose input stage is SiLU(gate) * up; bias = the residual stream
-// then the LM head with the final norm fused and its argmax partials, and one tail launch that
-// reduces them to the token, advances the position and prepares the next step: the new token's
-// embedding row (layer 0's input) and the RoPE cos/sin of the next position (read by every
-// attention launch instead of computed there). Every per-token value (token id, position) lives
-// in device memory, so one captured hipGraph replays every step with no host work per launch.
+// then the LM head with the final norm fused and one tail launch that settles the token, advances
+// the position and prepares the next step: the new token's embedding row (layer 0's input) and
+// the RoPE cos/sin of the next position (read by every attention launch instead of computed
+// there). Greedy steps (GREEDY, sample.ts:33) take the LM head's fused argmax partials, which the
+// tail reduces; other sampling parameters store the logits and run the sampler (penalty,
+// temperature, top-p, draw; sample.wgsl) between the head and the tail, the decoder's sample
+// step (graph_decode.ts:382-385). Every per-token value (token id, position, the sampler's
+// parameters, its history and the mulberry32 draw state) lives in device memory, so one captured
+// hipGraph replays every step with no host work per launch.
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
 #include <vector>
 
@@ -35,6 +40,15 @@ struct eg_decoder {
   double* rope = nullptr;            // [head_dim / 2] (cos, sin) at the current position
   uint32_t* token = nullptr;         // [2]: next input id, its logit bits
   uint32_t* position = nullptr;      // [1]
+  // the sample step's state (DecodeGraph.history / setPosition's uniform, graph_decode.ts:150,
+  // 398-406; Session's random source, session.ts:75-83)
+  uint32_t* history = nullptr;       // [max_context]: Session.tokens, appended by every step
+  eg_sample_dims* sp = nullptr;      // {vocab, history_length, temperature, top_p, penalty, random}
+  uint32_t* rng = nullptr;           // [1]: mulberry32 state, one draw per step
+  eg_sampling_params sampling{0.f, 1.f, 1.f};  // host copy of sp's parameters
+  eg_gemv_plan* head_plan = nullptr; // the LM head storing logits for the sampler (vocab % 8 == 0)
+  bool graph_sampled = false;        // the mode the graph was captured in
+  uint32_t* host_staging = nullptr;  // pinned [max_context]: prompt ids on their way to `history`
   uint16_t* k_cache = nullptr;
   uint16_t* v_cache = nullptr;
   size_t layer_stride = 0;  // cache elements per layer
@@ -55,7 +69,9 @@ int alloc(eg_decoder* d, size_t bytes, void** out) {
 
 void release(eg_decoder* d) {
   if (d->host_token) (void)hipHostFree(d->host_token);
+  if (d->host_staging) (void)hipHostFree(d->host_staging);
   if (d->graph) eg_graph_destroy(d->graph);
+  if (d->head_plan) eg_gemv_plan_destroy(d->ctx, d->head_plan);
   for (eg_gemv_plan* p : d->plans) eg_gemv_plan_destroy(d->ctx, p);
   for (void* p : d->allocations) eg_buf_free(d->ctx, p);
   delete d;
@@ -65,10 +81,11 @@ bool matrix_ok(const eg_quant_matrix& m, int encoding) {
   return m.packed && m.scales && (encoding == EG_ENC_SIGNED || m.zeros);
 }
 
-// The step tail (see eg::launch_step_tail): with partials, the end of a step; without, the
-// preparation of the state a reset wrote.
-int tail(eg_decoder* d, const uint32_t* partials, uint32_t groups) {
-  const eg_model_desc& m = d->desc;
+// Greedy steps fuse the argmax into the LM head; anything else (a temperature, or a penalty,
+// which the reference applies before its greedy argmax too) runs the sampler.
+bool sampled_mode(const eg_sampling_params& s) { return !(s.temperature <= 0.f && s.repetition_penalty == 1.f); }
+
+eg_embedding_dims embedding_dims_of(const eg_model_desc& m) {
   eg_embedding_dims ed{};
   ed.seq = 1;
   ed.hidden = m.hidden;
@@ -77,23 +94,31 @@ int tail(eg_decoder* d, const uint32_t* partials, uint32_t groups) {
   ed.block_size = m.embed_block_size;
   ed.blocks_per_row = m.hidden / m.embed_block_size;
   ed.grid_width = 1;
-  return eg::launch_step_tail(d->ctx, partials, groups, d->token, d->position, m.embedding.packed, m.embedding.scales,
+  return ed;
+}
+
+// The step tail (see eg::launch_step_tail).
+int tail(eg_decoder* d, const eg::StepTail& t) {
+  const eg_model_desc& m = d->desc;
+  const eg_embedding_dims ed = embedding_dims_of(m);
+  return eg::launch_step_tail(d->ctx, t, d->token, d->position, m.embedding.packed, m.embedding.scales,
                               m.embedding.zeros, &ed, m.embed_encoding, m.embed_bits, d->emb, d->rope, m.head_dim,
                               m.rope_theta);
 }
 
-int run_step(eg_decoder* d) {
+eg::StepTail advancing_tail(eg_decoder* d) {
+  eg::StepTail t;
+  t.advance = true;
+  t.history = d->history;
+  t.history_length = &d->sp->history_length;
+  t.history_capacity = d->desc.max_context;
+  return t;
+}
+
+// The 24 layers of a step on the token whose embedding is in d->emb at position[0].
+int run_layers(eg_decoder* d) {
   eg_context* ctx = d->ctx;
   const eg_model_desc& m = d->desc;
-  const eg_quant_matrix& e = m.embedding;
-  eg_embedding_dims ed{};
-  ed.seq = 1;
-  ed.hidden = m.hidden;
-  ed.row_begin = 0;
-  ed.row_count = m.vocab;
-  ed.block_size = m.embed_block_size;
-  ed.blocks_per_row = m.hidden / m.embed_block_size;
-  ed.grid_width = 1;
   int st = EG_OK;
   for (uint32_t l = 0; l < m.layers; l++) {
     const eg_layer_desc& L = d->layers[l];
@@ -128,19 +153,88 @@ int run_step(eg_decoder* d) {
     in.x2 = d->gu + m.intermediate;
     if ((st = eg_gemv_plan_launch_input(ctx, P[3], &in)) != EG_OK) return st;  // h[0] = h[1] + down(...)
   }
+  return st;
+}
+
+// A whole step: layers, the LM head, then greedy (fused argmax partials reduced in the tail,
+// which also advances the draw state) or sampled (logits stored, the sampler draws and writes
+// the token, the tail only settles it).
+int run_step(eg_decoder* d, bool sampled) {
+  eg_context* ctx = d->ctx;
+  const eg_model_desc& m = d->desc;
+  const eg_quant_matrix& e = m.embedding;
+  int st = run_layers(d);
+  if (st != EG_OK) return st;
   eg_gemv_input in{};
   in.kind = EG_INPUT_RMSNORM;
   in.x = d->h[0];
   in.x2 = m.final_norm;
   in.eps = m.rms_eps;
-  eg_embedding_dims hd = ed;
-  hd.row_count = m.vocab;
-  hd.grid_width = 65535;
-  uint32_t groups = 0;
-  if ((st = eg::lm_head_argmax_partials(ctx, &in, e.packed, e.scales, e.zeros, d->logits, &hd, m.embed_encoding,
-                                        m.embed_bits, &groups)) != EG_OK)
+  eg::StepTail t = advancing_tail(d);
+  if (!sampled) {
+    eg_embedding_dims hd = embedding_dims_of(m);
+    hd.grid_width = 65535;
+    if ((st = eg::lm_head_argmax_partials(ctx, &in, e.packed, e.scales, e.zeros, d->logits, &hd, m.embed_encoding,
+                                          m.embed_bits, &t.groups)) != EG_OK)
+      return st;
+    t.partials = reinterpret_cast<const uint32_t*>(eg::partials(ctx));
+    t.rng = d->rng;
+    return tail(d, t);
+  }
+  if (d->head_plan) {
+    st = eg_gemv_plan_launch_input(ctx, d->head_plan, &in);
+  } else {
+    eg_embedding_dims hd = embedding_dims_of(m);
+    hd.grid_width = 65535;
+    uint32_t groups = 0;  // the partials are not used
+    st = eg::lm_head_argmax_partials(ctx, &in, e.packed, e.scales, e.zeros, d->logits, &hd, m.embed_encoding,
+                                     m.embed_bits, &groups);
+  }
+  if (st != EG_OK) return st;
+  if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, d->rng)) != EG_OK)
     return st;
-  return tail(d, reinterpret_cast<const uint32_t*>(eg::partials(ctx)), groups);
+  return tail(d, t);
+}
+
+// Writes `count` u32 from host memory to device memory through the pinned staging buffer and
+// waits for the copy (the staging buffer is reused by the next call).
+int write_ids(eg_decoder* d, uint32_t* dst, const uint32_t* host, uint32_t count) {
+  if (count == 0) return EG_OK;
+  std::memcpy(d->host_staging, host, (size_t)count * 4);
+  hipError_t err = hipMemcpyAsync(dst, d->host_staging, (size_t)count * 4, hipMemcpyHostToDevice, d->ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(d->ctx->stream);
+  return err == hipSuccess ? EG_OK : eg::hip_fail(d->ctx, err, "decoder: upload");
+}
+
+// One 4-byte readback of the token the last step produced, into pinned memory (a direct copy,
+// no staging through a bounce buffer as a pageable destination would need).
+int read_token(eg_decoder* d, uint32_t* token_out) {
+  hipError_t err = hipMemcpyAsync(d->host_token, d->token, sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(d->ctx->stream);
+  if (err != hipSuccess) return eg::hip_fail(d->ctx, err, "decoder_step");
+  *token_out = *d->host_token;
+  return EG_OK;
+}
+
+int capture(eg_decoder* d) {
+  if (d->graph) {
+    eg_graph_destroy(d->graph);
+    d->graph = nullptr;
+  }
+  int st = eg_graph_begin(d->ctx);
+  if (st != EG_OK) return st;
+  const bool sampled = sampled_mode(d->sampling);
+  const int run = run_step(d, sampled);
+  eg_graph* g = nullptr;
+  st = eg_graph_end(d->ctx, &g);
+  if (run != EG_OK) {
+    if (g) eg_graph_destroy(g);
+    return run;
+  }
+  if (st != EG_OK) return st;
+  d->graph = g;
+  d->graph_sampled = sampled;
+  return EG_OK;
 }
 
 }  // namespace
@@ -203,6 +297,9 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take((size_t)m.vocab * 4, &d->logits);
   take(8, &d->token);
   take(4, &d->position);
+  take((size_t)m.max_context * 4, &d->history);
+  take(sizeof(eg_sample_dims), &d->sp);
+  take(4, &d->rng);
   take(d->layer_stride * m.layers * 2, &d->k_cache);
   take(d->layer_stride * m.layers * 2, &d->v_cache);
   if (st != EG_OK) {
@@ -239,12 +336,34 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     if (st != EG_OK) break;
     d->plans.push_back(plan);
   }
+  // the LM head storing logits for the sampler: a one-matrix plan with the final norm as its
+  // input stage (plans need rows in multiples of 8; other vocabularies use the fused-argmax head
+  // and ignore its partials)
+  if (st == EG_OK && m.vocab % 8 == 0) {
+    eg_gemv_segment head[1] = {{m.embedding.packed, m.embedding.scales, m.embedding.zeros, nullptr, d->logits, m.vocab, 0}};
+    st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
+  }
   if (st == EG_OK) {
-    const hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), sizeof(uint32_t), hipHostMallocDefault);
-    if (err != hipSuccess) {
-      d->host_token = nullptr;
-      st = eg::hip_fail(ctx, err, op);
+    hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), sizeof(uint32_t), hipHostMallocDefault);
+    if (err != hipSuccess) d->host_token = nullptr;
+    if (err == hipSuccess) {
+      err = hipHostMalloc(reinterpret_cast<void**>(&d->host_staging), (size_t)m.max_context * 4, hipHostMallocDefault);
+      if (err != hipSuccess) d->host_staging = nullptr;
     }
+    if (err != hipSuccess) st = eg::hip_fail(ctx, err, op);
+  }
+  if (st == EG_OK) {
+    // GREEDY sampling (sample.ts:33), an empty history, the session's default seed 0x5eed
+    // (session.ts:125)
+    eg_sample_dims sp{};
+    sp.vocab = m.vocab;
+    sp.temperature = d->sampling.temperature;
+    sp.top_p = d->sampling.top_p;
+    sp.repetition_penalty = d->sampling.repetition_penalty;
+    static_assert(sizeof(sp) % 4 == 0, "u32 words");
+    st = write_ids(d, reinterpret_cast<uint32_t*>(d->sp), reinterpret_cast<const uint32_t*>(&sp), sizeof(sp) / 4);
+    const uint32_t seed = 0x5eed;
+    if (st == EG_OK) st = write_ids(d, d->rng, &seed, 1);
   }
   if (st != EG_OK) {
     // keep the plan error message; release() only frees
@@ -270,6 +389,9 @@ int eg_decoder_buffers_get(eg_decoder* d, eg_decoder_buffers* out) {
   out->hidden = d->h[0];
   out->token = d->token;
   out->position = d->position;
+  out->history = d->history;
+  out->sample_params = d->sp;
+  out->rng = d->rng;
   return EG_OK;
 }
 
@@ -285,7 +407,7 @@ int eg_decoder_reset(eg_decoder* d, uint32_t position, uint32_t token) {
   const uint32_t tok[2] = {token, 0};
   int st = eg_buf_write(d->ctx, d->token, 0, tok, sizeof(tok));
   if (st == EG_OK) st = eg_buf_write(d->ctx, d->position, 0, &position, 4);
-  if (st == EG_OK) st = tail(d, nullptr, 0);  // this token's embedding, this position's RoPE table
+  if (st == EG_OK) st = tail(d, eg::StepTail{});  // this token's embedding, this position's RoPE table
   if (st == EG_OK) st = eg_sync(d->ctx);      // the host values are stack locals
   if (st == EG_OK) d->host_position = position;
   return st;
@@ -299,37 +421,83 @@ int eg_decoder_step(eg_decoder* d, uint32_t* token_out) {
   // kvcache.ts:118-127: a full context is an error, not a silent overwrite
   if (d->host_position >= d->desc.max_context)
     return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_step: context of %u positions exhausted", d->desc.max_context);
-  int st = d->graph ? eg_graph_launch(d->ctx, d->graph) : run_step(d);
+  int st = d->graph ? eg_graph_launch(d->ctx, d->graph) : run_step(d, sampled_mode(d->sampling));
   if (st == EG_OK) d->host_position++;
-  if (st == EG_OK && token_out) {
-    // the one readback per token, into pinned memory: a direct copy, no staging through a
-    // bounce buffer as a pageable destination would need
-    hipError_t err = hipMemcpyAsync(d->host_token, d->token, sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);
-    if (err == hipSuccess) err = hipStreamSynchronize(d->ctx->stream);
-    if (err != hipSuccess) return eg::hip_fail(d->ctx, err, "decoder_step");
-    *token_out = *d->host_token;
-  }
+  if (st == EG_OK && token_out) st = read_token(d, token_out);
   return st;
 }
 
 int eg_decoder_capture(eg_decoder* d) {
   if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_capture: decoder is NULL");
-  if (d->graph) {
-    eg_graph_destroy(d->graph);
-    d->graph = nullptr;
-  }
-  int st = eg_graph_begin(d->ctx);
+  return capture(d);
+}
+
+int eg_decoder_set_sampling(eg_decoder* d, const eg_sampling_params* params) {
+  const char* op = "decoder_set_sampling";
+  if (!d || !params) return eg::fail(d ? d->ctx : nullptr, EG_ERR_INVALID, "%s: NULL argument", op);
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "%s: a graph capture is in progress", op);
+  const eg_sampling_params& p = *params;
+  if (!(p.temperature == p.temperature) || !(p.top_p > 0.f && p.top_p <= 1.f) || !(p.repetition_penalty > 0.f))
+    return eg::fail(d->ctx, EG_ERR_INVALID, "%s: temperature %g, topP %g (0, 1], repetitionPenalty %g (> 0)", op,
+                    (double)p.temperature, (double)p.top_p, (double)p.repetition_penalty);
+  const float vals[3] = {p.temperature, p.top_p, p.repetition_penalty};
+  uint32_t words[3];
+  std::memcpy(words, vals, sizeof(words));
+  int st = write_ids(d, reinterpret_cast<uint32_t*>(&d->sp->temperature), words, 3);
   if (st != EG_OK) return st;
-  const int run = run_step(d);
-  eg_graph* g = nullptr;
-  st = eg_graph_end(d->ctx, &g);
-  if (run != EG_OK) {
-    if (g) eg_graph_destroy(g);
-    return run;
+  d->sampling = p;
+  // a graph captured in the other mode (greedy fused argmax / sampler) is captured again
+  if (d->graph && d->graph_sampled != sampled_mode(p)) st = capture(d);
+  return st;
+}
+
+int eg_decoder_seed(eg_decoder* d, uint32_t seed) {
+  if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_seed: decoder is NULL");
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_seed: a graph capture is in progress");
+  return write_ids(d, d->rng, &seed, 1);
+}
+
+int eg_decoder_set_history(eg_decoder* d, const uint32_t* host_ids, uint32_t count) {
+  const char* op = "decoder_set_history";
+  if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "%s: decoder is NULL", op);
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "%s: a graph capture is in progress", op);
+  if (count > 0 && !host_ids) return eg::fail(d->ctx, EG_ERR_INVALID, "%s: %u ids from NULL", op, count);
+  if (count > d->desc.max_context)
+    return eg::fail(d->ctx, EG_ERR_RANGE, "%s: %u ids exceed the history of %u", op, count, d->desc.max_context);
+  int st = write_ids(d, d->history, host_ids, count);
+  if (st == EG_OK) st = write_ids(d, &d->sp->history_length, &count, 1);
+  return st;
+}
+
+int eg_decoder_prefill(eg_decoder* d, uint32_t position, const uint32_t* host_ids, uint32_t count,
+                       uint32_t* token_out) {
+  const char* op = "decoder_prefill";
+  if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "%s: decoder is NULL", op);
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "%s: a graph capture is in progress", op);
+  if (count == 0 || !host_ids) return eg::fail(d->ctx, EG_ERR_INVALID, "%s: an empty prompt", op);
+  // session.ts:326-330: a prompt longer than the remaining context is a RangeError
+  if ((uint64_t)position + count > d->desc.max_context)
+    return eg::fail(d->ctx, EG_ERR_RANGE, "%s: prompt of %u exceeds the remaining context of %u", op, count,
+                    position < d->desc.max_context ? d->desc.max_context - position : 0u);
+  for (uint32_t i = 0; i < count; i++)
+    if (host_ids[i] >= d->desc.vocab)
+      return eg::fail(d->ctx, EG_ERR_INVALID, "%s: token %u at %u outside the vocabulary", op, host_ids[i], i);
+  // the history is the prompt (Session.runPrefill: this.tokens = [...prompt]); the prompt ids
+  // stay there for the fill steps to read
+  int st = eg_decoder_set_history(d, host_ids, count);
+  if (st == EG_OK) st = eg_decoder_reset(d, position, host_ids[0]);
+  // every prompt position but the last: the layers only (the cache rows), then the next id
+  for (uint32_t i = 0; st == EG_OK && i + 1 < count; i++) {
+    st = run_layers(d);
+    eg::StepTail t;
+    t.advance = true;
+    t.token_src = d->history + i + 1;
+    if (st == EG_OK) st = tail(d, t);
   }
   if (st != EG_OK) return st;
-  d->graph = g;
-  return EG_OK;
+  d->host_position = position + count - 1;
+  // the last position samples the first token (sampleFromPrefill, session.ts:472-495)
+  return eg_decoder_step(d, token_out);
 }
 
 }  // extern "C"

@@ -74,13 +74,36 @@ int lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, const u
                             const float* scales, const uint32_t* zeros, float* out, const eg_embedding_dims* dims,
                             int encoding, int bits, uint32_t* groups);
 
-// The decode step's tail, one single-workgroup launch: with `partials` (the LM head's argmax
-// partials, `groups` of them) the greedy token is written to token[0..1] and position[0] advances;
-// then (also without partials: a reset) the embedding row of token[0] is dequantized into `emb`
-// and the RoPE cos/sin of position[0] are written to `rope` ([head_dim / 2] pairs of doubles).
-int launch_step_tail(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t* token, uint32_t* position,
-                     const uint32_t* packed, const float* scales, const uint32_t* zeros, const eg_embedding_dims* ed,
-                     int encoding, int bits, float* emb, double* rope, uint32_t head_dim, float theta);
+// What a decode step's tail does before it prepares the next step (see launch_step_tail).
+struct StepTail {
+  bool advance = false;                 // false: a reset (token[0] and position[0] as written)
+  const uint32_t* partials = nullptr;   // greedy step: the LM head's argmax partials, `groups` of them
+  uint32_t groups = 0;
+  const uint32_t* token_src = nullptr;  // prompt-fill step: the next input id is *token_src
+  // (neither: a sampled step, whose sampler already wrote token[0])
+  uint32_t* history = nullptr;          // the new token is appended (not by fill steps) ...
+  uint32_t* history_length = nullptr;   // ... at history[*history_length]++, up to the capacity
+  uint32_t history_capacity = 0;
+  uint32_t* rng = nullptr;              // mulberry32 state: advanced once (a greedy step's draw)
+};
+
+// The decode step's tail, one single-workgroup launch. With `advance` the step's token is
+// settled (greedy: reduced from the argmax partials into token[0..1]; fill: copied from
+// token_src; sampled: already in token[0]), position[0] advances, the token is appended to the
+// history and the draw state advances as asked. Then (also for a reset) the embedding row of
+// token[0] is dequantized into `emb` and the RoPE cos/sin of position[0] are written to `rope`
+// ([head_dim / 2] pairs of doubles).
+int launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32_t* position, const uint32_t* packed,
+                     const float* scales, const uint32_t* zeros, const eg_embedding_dims* ed, int encoding, int bits,
+                     float* emb, double* rope, uint32_t head_dim, float theta);
+
+// eg_sample's launches with every parameter read from DEVICE memory `params` (the 32-byte
+// sample dims: vocab, history_length, temperature, top_p, repetition_penalty, random), all
+// passes launched whatever the values, so a captured graph replays with new values. With `rng`
+// the launch first draws params->random from the mulberry32 state there (advancing it).
+// `vocab` sizes the grid and must equal params->vocab.
+int launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
+                         eg_sample_dims* params, uint32_t* rng);
 
 // eg_attention_decode with the RoPE cos/sin of the current position read from `rope` ([head_dim
 // / 2] pairs of doubles, as egd::rope_table computes them) instead of computed in the launch.
@@ -334,6 +357,17 @@ __device__ __forceinline__ void team_argmax(float& v, uint32_t& i) {
       i = oi;
     }
   }
+}
+
+// mulberry32 (session.ts:75-83): advances the state and returns the next draw as the f32 the
+// reference's uniform carries (u / 2^32 rounded to f32; rounding u to 24 bits then scaling by
+// the power of two 2^-32 rounds identically).
+__device__ __forceinline__ float mulberry32_next(uint32_t* state) {
+  const uint32_t s = *state + 0x6D2B79F5u;
+  *state = s;
+  uint32_t t = (s ^ (s >> 15)) * (1u | s);
+  t = (t + (t ^ (t >> 7)) * (61u | t)) ^ t;
+  return (float)(t ^ (t >> 14)) * 0x1p-32f;
 }
 
 // binary16 <-> f32 (round to nearest even), the KV cache's element type.

@@ -239,7 +239,11 @@ __device__ void replay_level(const Work& w, uint32_t groups, int level, float to
 // ---- launches --------------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32_t* history, SampleParams hp,
-                                                     const SampleParams* dp, Work w) {
+                                                     const SampleParams* dp, Work w, uint32_t* rng) {
+  // This call's draw (one per sampled step, Session.decodeStep session.ts:351), consumed by
+  // finalize; no workgroup of this launch reads `random`.
+  if (rng && blockIdx.x == 0 && threadIdx.x == 0)
+    const_cast<SampleParams*>(dp)->random = egd::mulberry32_next(rng);
   const SampleParams p = load_params(hp, dp);
   __shared__ float slice[kSlice];
   __shared__ float sv[4];
@@ -528,11 +532,11 @@ Work workspace(eg_context* ctx) {
 }
 
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
-           const SampleParams* dp, bool all_passes) {
+           const SampleParams* dp, bool all_passes, uint32_t* rng = nullptr) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
   Work w = workspace(ctx);
   const dim3 grid(groups), block(kThreads);
-  hipLaunchKernelGGL(pass_max, grid, block, 0, ctx->stream, logits, history, hp, dp, w);
+  hipLaunchKernelGGL(pass_max, grid, block, 0, ctx->stream, logits, history, hp, dp, w, rng);
   const bool sampled = all_passes || hp.temperature > 0.0f;
   if (sampled) {
     hipLaunchKernelGGL(pass_sum, grid, block, 0, ctx->stream, logits, hp, dp, w);
@@ -546,6 +550,18 @@ int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* ou
 }
 
 }  // namespace
+
+int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
+                             eg_sample_dims* params, uint32_t* rng) {
+  static_assert(sizeof(eg_sample_dims) == sizeof(SampleParams), "the device block is the 32-byte sample dims");
+  if (!logits || !out || !params) return eg::fail(ctx, EG_ERR_INVALID, "sample: NULL argument");
+  if (vocab == 0 || (vocab + kSlice - 1) / kSlice > kMaxGroups)
+    return eg::fail(ctx, EG_ERR_RANGE, "sample: vocab %u outside the sampler's range (1..%u)", vocab,
+                    kMaxGroups * kSlice);
+  SampleParams hp{};
+  hp.vocab = vocab;
+  return launch(ctx, logits, history, out, hp, reinterpret_cast<const SampleParams*>(params), true, rng);
+}
 
 extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
                          const eg_sample_dims* dims) {

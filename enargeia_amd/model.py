@@ -164,7 +164,13 @@ class GemvInput(ctypes.Structure):
 
 
 class DecoderBuffers(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in ("k_cache", "v_cache", "logits", "hidden", "token", "position")]
+    _fields_ = [(n, ctypes.c_void_p) for n in ("k_cache", "v_cache", "logits", "hidden", "token", "position",
+                                               "history", "sample_params", "rng")]
+
+
+class SamplingParamsC(ctypes.Structure):
+    """eg_sampling_params = SamplingParams (sample.ts:24-31)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float)]
 
 
 INPUT_VECTOR, INPUT_RMSNORM, INPUT_SILU_MUL, INPUT_ATTENTION = 0, 1, 2, 3
@@ -211,7 +217,8 @@ class DeviceModel:
 
 
 class Decoder:
-    """eg_decoder: greedy decode steps with the token and the position on the device."""
+    """eg_decoder: decode steps with the token, the position, the sampler's parameters, its
+    history and the draw state on the device (greedy until set_sampling says otherwise)."""
 
     def __init__(self, model: DeviceModel):
         self.model = model
@@ -234,6 +241,40 @@ class Decoder:
 
     def capture(self) -> None:
         check(_lib.load().eg_decoder_capture(self.handle), self.device.ctx)
+
+    def set_sampling(self, temperature: float, top_p: float = 1.0, repetition_penalty: float = 1.0) -> None:
+        p = SamplingParamsC(temperature, top_p, repetition_penalty)
+        check(_lib.load().eg_decoder_set_sampling(self.handle, ctypes.byref(p)), self.device.ctx)
+
+    def seed(self, seed: int) -> None:
+        check(_lib.load().eg_decoder_seed(self.handle, ctypes.c_uint32(seed)), self.device.ctx)
+
+    def set_history(self, ids) -> None:
+        a = np.ascontiguousarray(ids, np.uint32)
+        check(_lib.load().eg_decoder_set_history(self.handle, a.ctypes.data_as(ctypes.c_void_p), a.size),
+              self.device.ctx)
+
+    def prefill(self, position: int, prompt, read_token: bool = True) -> int | None:
+        """The prompt at [position, position + len) and its first token (runPrefill +
+        sampleFromPrefill)."""
+        a = np.ascontiguousarray(prompt, np.uint32)
+        out = ctypes.c_uint32()
+        check(_lib.load().eg_decoder_prefill(self.handle, position, a.ctypes.data_as(ctypes.c_void_p), a.size,
+                                             ctypes.byref(out) if read_token else None), self.device.ctx)
+        return out.value if read_token else None
+
+    def history(self) -> np.ndarray:
+        n = int(self.sample_params()["history_length"])
+        return self.device.read_array(self.buffers.history, np.uint32, n) if n else np.zeros(0, np.uint32)
+
+    def sample_params(self) -> dict:
+        raw = self.device.read_array(self.buffers.sample_params, np.uint32, 8)
+        f = raw.view(np.float32)
+        return {"vocab": int(raw[0]), "history_length": int(raw[1]), "temperature": float(f[2]),
+                "top_p": float(f[3]), "repetition_penalty": float(f[4]), "random": f[5]}
+
+    def rng_state(self) -> int:
+        return int(self.device.read_array(self.buffers.rng, np.uint32, 1)[0])
 
     def logits(self) -> np.ndarray:
         return self.device.read_array(self.buffers.logits, np.float32, self.model.cfg.vocab)

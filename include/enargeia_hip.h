@@ -310,15 +310,28 @@ typedef struct eg_model_desc {
 typedef struct eg_decoder eg_decoder;
 
 /* Device buffers a decoder owns, for callers that fill or inspect them (the KV caches are
- * [layers][max_context][kv_heads][head_dim] f16; logits f32[vocab]; token u32 = the next input
- * id, written by each greedy step; position u32). */
+ * [layers][max_context][kv_heads][head_dim] f16; logits f32[vocab] (penalized in place by a
+ * sampled step, as the reference's sample kernel does); token u32 = the next input id, written
+ * by each step; position u32; history u32[max_context] = the sampler's history (DecodeGraph's
+ * `history` buffer); sample_params = the sample step's 32-byte uniform, live on the device:
+ * history_length is advanced by every step and `random` holds the last step's draw; rng = the
+ * mulberry32 state). */
 typedef struct eg_decoder_buffers {
   uint16_t *k_cache, *v_cache;
   float* logits;
   float* hidden;
   uint32_t* token;
   uint32_t* position;
+  uint32_t* history;
+  eg_sample_dims* sample_params;
+  uint32_t* rng;
 } eg_decoder_buffers;
+
+/* SamplingParams (sample.ts:24-31): temperature <= 0 is greedy (GREEDY = {0, 1, 1}, sample.ts:33),
+ * top_p in (0, 1], repetition_penalty > 0 (1 disables it). */
+typedef struct eg_sampling_params {
+  float temperature, top_p, repetition_penalty;
+} eg_sampling_params;
 
 /* Plans every launch of a step once: per layer one GEMV plan for q|k|v (RMSNorm input stage,
  * biases), one fused attention launch, the o projection (attention-combine input stage, the
@@ -332,13 +345,35 @@ EG_API int eg_decoder_destroy(eg_decoder* decoder);
 EG_API int eg_decoder_buffers_get(eg_decoder* decoder, eg_decoder_buffers* out);
 /* Position and next input token (rows [0, position) of the caches are the history). */
 EG_API int eg_decoder_reset(eg_decoder* decoder, uint32_t position, uint32_t token);
-/* One greedy step at the current position on the current token: its argmax becomes the next
- * token and the position advances, all on the device. token_out (host, nullable) receives the
- * new token: the one 4-byte readback per step. Replays the captured graph if there is one. */
+/* One step at the current position on the current token (Session.decodeStep, session.ts:347-375):
+ * with GREEDY parameters the LM head's fused argmax gives the next token; with any other the
+ * logits go through the sample step (repetition penalty over the history, temperature, top-p,
+ * the draw; sample.wgsl:143-332) with one mulberry32 draw taken on the device. Either way the
+ * token is appended to the history, the draw state advances once (Session draws once per step
+ * whatever the parameters) and the position advances, all on the device. token_out (host,
+ * nullable) receives the new token: the one 4-byte readback per step. Replays the captured
+ * graph if there is one. */
 EG_API int eg_decoder_step(eg_decoder* decoder, uint32_t* token_out);
 /* Captures one step as a hipGraph; later eg_decoder_step calls replay it (no host work per
- * launch; every per-token value already lives in device memory). */
+ * launch; every per-token value already lives in device memory). A change of sampling
+ * parameters between greedy and sampled captures it again. */
 EG_API int eg_decoder_capture(eg_decoder* decoder);
+/* The sampling parameters of the following steps (DecodeGraph.setSampling, graph_decode.ts:387;
+ * a new decoder is GREEDY). */
+EG_API int eg_decoder_set_sampling(eg_decoder* decoder, const eg_sampling_params* params);
+/* Restarts the draw source: mulberry32(seed) (session.ts:75-83; a new decoder has the session's
+ * default seed 0x5eed, :125). */
+EG_API int eg_decoder_seed(eg_decoder* decoder, uint32_t seed);
+/* The repetition-penalty history (Session.tokens, written before each step, session.ts:349-350):
+ * every step then appends the token it produces. count <= max_context. */
+EG_API int eg_decoder_set_history(eg_decoder* decoder, const uint32_t* host_ids, uint32_t count);
+/* The prompt and its first token (Session.runPrefill + sampleFromPrefill, session.ts:326-344,
+ * 472-495): the history becomes the prompt, positions [position, position + count) receive the
+ * prompt's cache rows, and the last one's logits are sampled (one draw) into the next token,
+ * which is appended to the history. A prompt past the context is EG_ERR_RANGE
+ * ("prompt of N exceeds the remaining context of M"). token_out as for eg_decoder_step. */
+EG_API int eg_decoder_prefill(eg_decoder* decoder, uint32_t position, const uint32_t* host_ids, uint32_t count,
+                              uint32_t* token_out);
 
 /* ---- chunked-prefill attention (cache_variants.ts:81-145 attn_scores / attn_apply with the
  * softmax between; graph.ts:411-459 for the RoPE and cache writes before them) --------------
