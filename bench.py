@@ -480,12 +480,58 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     result["tok_s"] = result[f"{best}_tok_s"]
     result["launch"] = best
     result["verified"] = all(result[f"{m}_tokens_vs_oracle"]["verified"] for m in modes)
+    if "graph" in modes:
+        # the reference's live default (ui/engine.ts:261): T 0.7 / top-p 0.9 / penalty 1.1 over the
+        # session's history (the prompt and every token), one device-side draw per step; the same
+        # positions, captured, one readback per token
+        dec.set_sampling(0.7, 0.9, 1.1)  # recaptures the step with the sampler
+        dec.seed(0x5EED)
+        dec.set_history(list(w.prompt) + [first])
+        dec.reset(start, first)
+        for _ in range(8):
+            dec.step(read_token=False)
+        dec.set_history(list(w.prompt) + [first])
+        dec.reset(start, first)
+        t = time.perf_counter()
+        sampled = [dec.step(read_token=True) for _ in range(DECODE_STEPS)]
+        wall = time.perf_counter() - t
+        result["sampled_tok_s"] = round(DECODE_STEPS / wall, 1)
+        result["sampled_ms_per_token"] = round(wall / DECODE_STEPS * 1e3, 4)
+        result["sampled_config"] = "T 0.7 / top-p 0.9 / penalty 1.1, history = prompt + tokens, graph"
+        log(f"decode (graph, sampled): {result['sampled_tok_s']} tok/s with a readback per token; "
+            f"{len(set(sampled))} distinct tokens")
+        dec.set_sampling(0.0, 1.0, 1.0)
+    result["prompt"] = prompt_throughput(dev, dec, cfg)
     step_bytes = (STEP_BYTES + LM_HEAD_BYTES
                   + 2 * cfg.layers * (start + DECODE_STEPS // 2) * cfg.kv_heads * cfg.head_dim * 2)
     result["gbs_at_best"] = round(step_bytes * result["tok_s"] / 1e9, 1)
     dec.close()
     dm.release()
     return result
+
+
+def prompt_throughput(dev, dec, cfg) -> dict:
+    """The prompt path (eg_decoder_prefill: chunks of 256 rows through the bf16-MFMA projections
+    and the chunk attention, then the first token from the last row): the reference's prefill
+    figures (README.md:41-44: 1105 tok/s at 128 tokens, 708 tok/s at 2048 chunked at 256, 219 ms
+    to the first token of a 32-token prompt, on an M2). Wall time per call, host to first token
+    id, median of 5 after a warm-up call; GREEDY."""
+    out = {"config": "Qwen2.5-0.5B shape, 24 layers, prompt at position 0, chunks of 256, wall time to the first "
+                     "token id (one readback)",
+           "reference_m2": {"prefill_128_tok_s": 1105, "prefill_2048_tok_s": 708, "ttft_32_ms": 219}}
+    for n in (32, 128, 2048):
+        prompt = [int(t) for t in np.random.default_rng(0x5EED + n).integers(0, cfg.vocab, n)]
+        dec.prefill(0, prompt)
+        times = []
+        for _ in range(5):
+            t = time.perf_counter()
+            dec.prefill(0, prompt)
+            times.append(time.perf_counter() - t)
+        ms = float(np.median(times)) * 1e3
+        out[f"prefill_{n}"] = {"ms": round(ms, 3), "tok_s": round(n / ms * 1e3, 1)}
+    out["ttft_32_ms"] = out["prefill_32"]["ms"]
+    log(f"prompt: {out}")
+    return out
 
 
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix peak

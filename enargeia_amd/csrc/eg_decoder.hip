@@ -49,6 +49,15 @@ struct eg_decoder {
   eg_gemv_plan* head_plan = nullptr; // the LM head storing logits for the sampler (vocab % 8 == 0)
   bool graph_sampled = false;        // the mode the graph was captured in
   uint32_t* host_staging = nullptr;  // pinned [max_context]: prompt ids on their way to `history`
+  // the prompt chain (ForwardGraph, graph.ts:380-567) over chunks of up to `chunk` rows
+  uint32_t chunk = 256;              // DEFAULT_PREFILL_CHUNK (session.ts:30)
+  float *ph[2] = {nullptr, nullptr}; // [chunk][hidden] residual stream, ping-pong
+  float* pxn = nullptr;              // [chunk][hidden] normed rows
+  float *pq = nullptr, *pk = nullptr, *pv = nullptr;  // projections [chunk][hidden | kv | kv]
+  float* pqr = nullptr;              // [chunk][hidden] rotated, scaled q
+  float* patt = nullptr;             // [chunk][hidden] attention output
+  float* pgu = nullptr;              // [chunk][2 * intermediate] gate | up
+  float* pa = nullptr;               // [chunk][intermediate] silu(gate) * up
   uint16_t* k_cache = nullptr;
   uint16_t* v_cache = nullptr;
   size_t layer_stride = 0;  // cache elements per layer
@@ -156,18 +165,17 @@ int run_layers(eg_decoder* d) {
   return st;
 }
 
-// A whole step: layers, the LM head, then greedy (fused argmax partials reduced in the tail,
-// which also advances the draw state) or sampled (logits stored, the sampler draws and writes
-// the token, the tail only settles it).
-int run_step(eg_decoder* d, bool sampled) {
+// The LM head on `hidden` (the last layer's output row) with the final norm fused, then greedy
+// (fused argmax partials reduced in the tail, which also advances the draw state) or sampled
+// (logits stored, the sampler draws and writes the token, the tail only settles it).
+int run_head(eg_decoder* d, bool sampled, const float* hidden) {
   eg_context* ctx = d->ctx;
   const eg_model_desc& m = d->desc;
   const eg_quant_matrix& e = m.embedding;
-  int st = run_layers(d);
-  if (st != EG_OK) return st;
+  int st = EG_OK;
   eg_gemv_input in{};
   in.kind = EG_INPUT_RMSNORM;
-  in.x = d->h[0];
+  in.x = hidden;
   in.x2 = m.final_norm;
   in.eps = m.rms_eps;
   eg::StepTail t = advancing_tail(d);
@@ -194,6 +202,59 @@ int run_step(eg_decoder* d, bool sampled) {
   if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, d->rng)) != EG_OK)
     return st;
   return tail(d, t);
+}
+
+// A whole decode step: the layers on the current token, then the head.
+int run_step(eg_decoder* d, bool sampled) {
+  const int st = run_layers(d);
+  return st != EG_OK ? st : run_head(d, sampled, d->h[0]);
+}
+
+// One chunk of the prompt (ForwardGraph.encode over `count` rows at positions begin..,
+// graph.ts:380-500, without its tail): the rows' embeddings, then per layer RMSNorm, the q / k / v
+// projections with their biases on the matrix cores, RoPE + cache append + causal attention
+// (eg_attention_prefill), the o projection with the residual added in its epilogue, RMSNorm,
+// gate and up, SiLU(gate) * up, and the down projection with the residual. The chunk's last
+// hidden row ends in ph[0].
+int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32_t count) {
+  eg_context* ctx = d->ctx;
+  const eg_model_desc& m = d->desc;
+  const uint32_t H = m.hidden, I = m.intermediate, kvn = m.kv_heads * m.head_dim;
+  int st = eg::embed_rows(ctx, ids, count, m.embedding.packed, m.embedding.scales, m.embedding.zeros, H,
+                          m.embed_block_size, m.embed_encoding, m.embed_bits, d->ph[0]);
+  auto gemm = [&](const float* x, const eg_quant_matrix& w, const float* bias, const float* residual, float* out,
+                  uint32_t n, uint32_t k, uint32_t out_stride, uint32_t out_offset) {
+    if (st != EG_OK) return;
+    eg_matmul_q4_dims dm{};
+    dm.m = count;
+    dm.n = n;
+    dm.k = k;
+    dm.use_bias = bias != nullptr;
+    dm.block_size = m.block_size;
+    dm.blocks_per_row = k / m.block_size;
+    dm.out_stride = out_stride;
+    dm.out_offset = out_offset;
+    st = eg::prefill_gemm(ctx, x, w.packed, w.scales, w.zeros, bias, residual, out, &dm, m.encoding, m.bits);
+  };
+  for (uint32_t l = 0; l < m.layers && st == EG_OK; l++) {
+    const eg_layer_desc& L = d->layers[l];
+    st = eg::rmsnorm_rows(ctx, d->ph[0], L.input_norm, count, H, m.rms_eps, d->pxn);
+    gemm(d->pxn, L.q, L.q_bias, nullptr, d->pq, H, H, H, 0);
+    gemm(d->pxn, L.k, L.k_bias, nullptr, d->pk, kvn, H, kvn, 0);
+    gemm(d->pxn, L.v, L.v_bias, nullptr, d->pv, kvn, H, kvn, 0);
+    if (st != EG_OK) break;
+    eg_attention_prefill_dims ad{count, begin + count, begin, m.heads, m.kv_heads, m.head_dim, m.max_context,
+                                 m.rope_theta};
+    st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, d->k_cache + l * d->layer_stride,
+                              d->v_cache + l * d->layer_stride, d->pqr, d->patt, &ad);
+    gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
+    if (st == EG_OK) st = eg::rmsnorm_rows(ctx, d->ph[1], L.post_attention_norm, count, H, m.rms_eps, d->pxn);
+    gemm(d->pxn, L.gate, nullptr, nullptr, d->pgu, I, H, 2 * I, 0);
+    gemm(d->pxn, L.up, nullptr, nullptr, d->pgu, I, H, 2 * I, I);
+    if (st == EG_OK) st = eg::silu_mul_rows(ctx, d->pgu, count, I, d->pa);
+    gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0);  // ph0 = ph1 + down(...)
+  }
+  return st;
 }
 
 // Writes `count` u32 from host memory to device memory through the pinned staging buffer and
@@ -298,6 +359,18 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take(8, &d->token);
   take(4, &d->position);
   take((size_t)m.max_context * 4, &d->history);
+  d->chunk = std::min<uint32_t>(256u, m.max_context);
+  const size_t rows = d->chunk;
+  take(rows * m.hidden * 4, &d->ph[0]);
+  take(rows * m.hidden * 4, &d->ph[1]);
+  take(rows * m.hidden * 4, &d->pxn);
+  take(rows * m.hidden * 4, &d->pq);
+  take(rows * kvn * 4, &d->pk);
+  take(rows * kvn * 4, &d->pv);
+  take(rows * m.hidden * 4, &d->pqr);
+  take(rows * m.hidden * 4, &d->patt);
+  take(rows * 2 * m.intermediate * 4, &d->pgu);
+  take(rows * m.intermediate * 4, &d->pa);
   take(sizeof(eg_sample_dims), &d->sp);
   take(4, &d->rng);
   take(d->layer_stride * m.layers * 2, &d->k_cache);
@@ -482,22 +555,23 @@ int eg_decoder_prefill(eg_decoder* d, uint32_t position, const uint32_t* host_id
   for (uint32_t i = 0; i < count; i++)
     if (host_ids[i] >= d->desc.vocab)
       return eg::fail(d->ctx, EG_ERR_INVALID, "%s: token %u at %u outside the vocabulary", op, host_ids[i], i);
-  // the history is the prompt (Session.runPrefill: this.tokens = [...prompt]); the prompt ids
-  // stay there for the fill steps to read
+  // the history is the prompt (Session.runPrefill: this.tokens = [...prompt]); the chunks read
+  // their ids from there
   int st = eg_decoder_set_history(d, host_ids, count);
-  if (st == EG_OK) st = eg_decoder_reset(d, position, host_ids[0]);
-  // every prompt position but the last: the layers only (the cache rows), then the next id
-  for (uint32_t i = 0; st == EG_OK && i + 1 < count; i++) {
-    st = run_layers(d);
-    eg::StepTail t;
-    t.advance = true;
-    t.token_src = d->history + i + 1;
-    if (st == EG_OK) st = tail(d, t);
+  // the prompt in chunks (ForwardGraph.encodeChunks, graph.ts:610-621)
+  uint32_t last_rows = 0;
+  for (uint32_t c0 = 0; st == EG_OK && c0 < count; c0 += d->chunk) {
+    last_rows = std::min(d->chunk, count - c0);
+    st = run_prefill_chunk(d, d->history + c0, position + c0, last_rows);
   }
+  // the last position's token: the head on the last row, then the tail advances the position
+  // past the prompt (sampleFromPrefill, session.ts:472-495: the decode graph's sample step)
+  const uint32_t last = position + count - 1;
+  if (st == EG_OK) st = write_ids(d, d->position, &last, 1);
+  if (st == EG_OK) st = run_head(d, sampled_mode(d->sampling), d->ph[0] + (size_t)(last_rows - 1) * d->desc.hidden);
   if (st != EG_OK) return st;
-  d->host_position = position + count - 1;
-  // the last position samples the first token (sampleFromPrefill, session.ts:472-495)
-  return eg_decoder_step(d, token_out);
+  d->host_position = position + count;
+  return token_out ? read_token(d, token_out) : EG_OK;
 }
 
 }  // extern "C"

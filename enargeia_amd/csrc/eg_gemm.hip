@@ -41,6 +41,7 @@ struct PrefillArgs {
   const float* scales;
   const uint32_t* zeros;
   const float* bias;
+  const float* residual;  // nullable: out = acc + bias + residual[r * out_stride + col + out_offset]
   float* out;
   float* partials;  // split-K: [splits][m][n] f32; NULL when grid.z == 1
   uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset, k_per_split;
@@ -309,17 +310,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       for (int e = 0; e < 4; e++) {
         const uint32_t row = m0 + wm + i * 16 + 4 * (lane >> 4) + e;
         if (row >= a.m) continue;
-        if (a.partials)
+        if (a.partials) {
           a.partials[((size_t)blockIdx.z * a.m + row) * a.n + col] = acc[i][j][e];
-        else
-          a.out[(size_t)row * a.out_stride + col + a.out_offset] = acc[i][j][e] + b;
+        } else {
+          const size_t o = (size_t)row * a.out_stride + col + a.out_offset;
+          a.out[o] = acc[i][j][e] + b + (a.residual ? a.residual[o] : 0.f);
+        }
       }
     }
 }
 
 // The split-K sum: splits added in index order, then the bias.
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __restrict__ partials,
-                                                             const float* __restrict__ bias, float* out, uint32_t m,
+                                                             const float* __restrict__ bias,
+                                                             const float* __restrict__ residual, float* out, uint32_t m,
                                                              uint32_t n, uint32_t splits, uint32_t out_stride,
                                                              uint32_t out_offset) {
   const size_t total = (size_t)m * n;
@@ -327,15 +331,16 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
     float acc = 0.f;
     for (uint32_t z = 0; z < splits; z++) acc += partials[(size_t)z * total + i];
     const uint32_t row = (uint32_t)(i / n), col = (uint32_t)(i % n);
-    out[(size_t)row * out_stride + col + out_offset] = acc + (bias ? bias[col] : 0.f);
+    const size_t o = (size_t)row * out_stride + col + out_offset;
+    out[o] = acc + (bias ? bias[col] : 0.f) + (residual ? residual[o] : 0.f);
   }
 }
 
 }  // namespace
 
-extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
-                                    const uint32_t* zeros, const float* bias, float* out,
-                                    const eg_matmul_q4_dims* dims, int encoding, int bits) {
+int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                     const uint32_t* zeros, const float* bias, const float* residual, float* out,
+                     const eg_matmul_q4_dims* dims, int encoding, int bits) {
   const char* op = "matmul_q4_prefill";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!dims || !x || !packed || !scales || !out) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
@@ -375,7 +380,7 @@ extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint3
   splits = (k + k_per_split - 1) / k_per_split;
   const bool split = splits > 1;
   PrefillArgs a{x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
-                out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
+                residual, out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
                 dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits,
                 (uint32_t)__builtin_ctz(bs)};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
@@ -392,8 +397,14 @@ extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint3
   if (split) {
     const uint64_t total = (uint64_t)m * n;
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);
-    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.bias, out, m, n,
-                       (uint32_t)splits, dims->out_stride, dims->out_offset);
+    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.bias, residual,
+                       out, m, n, (uint32_t)splits, dims->out_stride, dims->out_offset);
   }
   return eg::check_launch(ctx, op);
+}
+
+extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                                    const uint32_t* zeros, const float* bias, float* out,
+                                    const eg_matmul_q4_dims* dims, int encoding, int bits) {
+  return eg::prefill_gemm(ctx, x, packed, scales, zeros, bias, nullptr, out, dims, encoding, bits);
 }

@@ -111,6 +111,23 @@ int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float
                           const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
                           const eg_attention_dims* dims, const double* rope);
 
+// eg_matmul_q4_prefill with a residual added in the epilogue: out[r * out_stride + col +
+// out_offset] = sum_k x[r, k] W[col, k] + bias[col] + residual[same index] (residual nullable;
+// it may not alias out).
+int prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales, const uint32_t* zeros,
+                 const float* bias, const float* residual, float* out, const eg_matmul_q4_dims* dims, int encoding,
+                 int bits);
+
+// Row-wise kernels of the prefill chain (one workgroup per row):
+//   embed_rows: out[r] = the dequantized table row of ids[r] (ops.ts:222-233), r < rows;
+//   rmsnorm_rows: out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w (ops.ts:30-51);
+//   silu_mul_rows: out[r][j] = silu(x[r][j]) * x[r][n + j] for j < n (gate then up in one row of
+//   2n, ops.ts:207-216).
+int embed_rows(eg_context* ctx, const uint32_t* ids, uint32_t rows, const uint32_t* packed, const float* scales,
+               const uint32_t* zeros, uint32_t hidden, uint32_t block_size, int encoding, int bits, float* out);
+int rmsnorm_rows(eg_context* ctx, const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* out);
+int silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out);
+
 // Resolves the calling thread's current device's copy of the no-alloc scratch array
 // (hipGetSymbolAddress, once per device) into ctx->noalloc_scratch.
 int noalloc_scratch_init(eg_context* ctx);
