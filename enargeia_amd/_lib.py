@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_decoder_seed": (_i, [_vp, ctypes.c_uint32]),
     "eg_decoder_set_history": (_i, [_vp, _vp, ctypes.c_uint32]),
     "eg_decoder_prefill": (_i, [_vp, ctypes.c_uint32, _vp, ctypes.c_uint32, _vp]),
+    "eg_decoder_set_prefill_chunk": (_i, [_vp, ctypes.c_uint32]),
     "eg_graph_begin": (_i, [_vp]),
     "eg_graph_end": (_i, [_vp, ctypes.POINTER(_vp)]),
     "eg_graph_launch": (_i, [_vp, _vp]),

@@ -107,6 +107,10 @@ int eg_create(int device, eg_context** out_ctx) {
     const int v = std::atoi(tpw);
     if (v >= 1 && v <= 64) ctx->fused_tiles_per_wave = (uint32_t)v;
   }
+  if (const char* g = std::getenv("EG_PREFILL_GROUPS")) {
+    const int v = std::atoi(g);
+    if (v == 1 || v == 2 || v == 4) ctx->prefill_groups = v;
+  }
   err = hipMalloc(&ctx->workspace, eg::kWorkspaceBytes);
   if (err != hipSuccess) {
     hipStreamDestroy(ctx->own_stream);

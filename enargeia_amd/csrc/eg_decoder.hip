@@ -50,7 +50,12 @@ struct eg_decoder {
   bool graph_sampled = false;        // the mode the graph was captured in
   uint32_t* host_staging = nullptr;  // pinned [max_context]: prompt ids on their way to `history`
   // the prompt chain (ForwardGraph, graph.ts:380-567) over chunks of up to `chunk` rows
-  uint32_t chunk = 256;              // DEFAULT_PREFILL_CHUNK (session.ts:30)
+  // Rows per prompt chunk. The reference runs 256 (DEFAULT_PREFILL_CHUNK, session.ts:30; a
+  // browser's buffer limits); here the buffers hold up to kMaxChunk rows (79 KB of activations a
+  // row at the Qwen2.5-0.5B shape) and a whole prompt of that length is one chunk, so the
+  // projections run as GEMMs of up to 2048 rows, which fill the device, instead of 256.
+  uint32_t chunk = 0;
+  uint32_t chunk_capacity = 0;
   float *ph[2] = {nullptr, nullptr}; // [chunk][hidden] residual stream, ping-pong
   float* pxn = nullptr;              // [chunk][hidden] normed rows
   float *pq = nullptr, *pk = nullptr, *pv = nullptr;  // projections [chunk][hidden | kv | kv]
@@ -69,6 +74,8 @@ struct eg_decoder {
 };
 
 namespace {
+
+constexpr uint32_t kMaxChunk = 2048;
 
 int alloc(eg_decoder* d, size_t bytes, void** out) {
   int st = eg_buf_alloc(d->ctx, bytes, out);
@@ -359,7 +366,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take(8, &d->token);
   take(4, &d->position);
   take((size_t)m.max_context * 4, &d->history);
-  d->chunk = std::min<uint32_t>(256u, m.max_context);
+  d->chunk_capacity = d->chunk = std::min<uint32_t>(kMaxChunk, m.max_context);
   const size_t rows = d->chunk;
   take(rows * m.hidden * 4, &d->ph[0]);
   take(rows * m.hidden * 4, &d->ph[1]);
@@ -540,6 +547,14 @@ int eg_decoder_set_history(eg_decoder* d, const uint32_t* host_ids, uint32_t cou
   int st = write_ids(d, d->history, host_ids, count);
   if (st == EG_OK) st = write_ids(d, &d->sp->history_length, &count, 1);
   return st;
+}
+
+int eg_decoder_set_prefill_chunk(eg_decoder* d, uint32_t rows) {
+  if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_set_prefill_chunk: decoder is NULL");
+  if (rows == 0 || rows > d->chunk_capacity)
+    return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_set_prefill_chunk: %u rows (1..%u)", rows, d->chunk_capacity);
+  d->chunk = rows;
+  return EG_OK;
 }
 
 int eg_decoder_prefill(eg_decoder* d, uint32_t position, const uint32_t* host_ids, uint32_t count,

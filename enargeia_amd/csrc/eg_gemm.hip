@@ -94,7 +94,7 @@ struct StageBase {
 };
 
 __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, uint32_t m0, uint32_t n0) {
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x & 255u;  // the thread within its group of 4 waves
   StageBase b;
   b.xc = (tid & 15u) * 4u;
 #pragma unroll
@@ -133,7 +133,7 @@ __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& 
 
 template <int ENC>
 __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds]) {
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x & 255u;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t idx = tid + i * 256u;
@@ -186,7 +186,7 @@ __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLd
 template <int ENC>
 __device__ void stage_elements(const PrefillArgs& a, uint32_t m0, uint32_t n0, uint32_t k0, uint16_t (*As)[kLds],
                                uint16_t (*Bs)[kLds]) {
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x & 255u;
   const uint32_t per_word = 32u / (uint32_t)a.bits, mask = (1u << a.bits) - 1u;
 #pragma unroll 4
   for (uint32_t e = tid; e < kTile * kBK; e += 256) {
@@ -217,12 +217,23 @@ __device__ void stage_elements(const PrefillArgs& a, uint32_t m0, uint32_t n0, u
   }
 }
 
-template <int ENC, bool CHUNKED>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[kTile][kLds];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kTile][kLds];
+// KG groups of 4 waves share a workgroup and a tile: group g stages and multiplies the 64-deep
+// blocks g, g + KG, ... of the workgroup's K range into its own accumulators (its own LDS
+// buffers; one barrier pair per KG blocks), and the groups' sums are added in group order at the
+// end. With one workgroup per CU (the tile grids here hold ~1 per CU) a single group leaves
+// every SIMD one wave, so each block's staging, LDS round trip, barriers and MFMAs run back to
+// back; KG groups put KG waves on each SIMD and cut the serial chain by KG.
+template <int ENC, bool CHUNKED, int KG>
+__global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
+  // staging buffers of every group; after the K loop they hold the groups' f32 sums
+  constexpr uint32_t kStageBytes = 2u * kTile * kLds * 2u;  // As + Bs of one group
+  static_assert(kStageBytes >= kTile * kTile * 4u, "a group's buffers hold its 64 x 64 f32 sums");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[KG * kStageBytes];
+  const uint32_t group = threadIdx.x >> 8;
+  uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
+  uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
   const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+  const uint32_t tid = threadIdx.x & 255u, wave = tid >> 6, lane = tid & 63u;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
 
@@ -252,6 +263,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   };
 
   const uint32_t nblk = (kend - kbeg + kBK - 1) / kBK;
+  // this group's blocks: group + KG * i for i < iters (the last ones past nblk are skipped; the
+  // groups run the same number of iterations so the barriers match)
+  const uint32_t iters = (nblk + KG - 1) / KG;
+  auto block_of = [&](uint32_t i) { return group + KG * i; };
   if (CHUNKED) {
     // kStages register stages: block b lives in stage b % kStages and is stored to LDS while
     // blocks b+1 .. b+kStages-1 are in flight (an iteration is ~0.3 us of staging and MFMAs;
@@ -259,43 +274,73 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     // blocks with no branch at all - loads unconditional, clamped to the last block - so the
     // compiler's wait before each store counts exactly the loads issued after that stage's; the
     // remaining blocks are already in flight and drain in a loop that issues no loads.
-    constexpr int S = kStages;
+    // four groups fit four waves per SIMD only within 128 VGPRs: they keep one block in flight
+    constexpr int S = KG >= 4 ? 2 : kStages;
     const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(a.packed, a.n * a.k / 2u),
                      egd::buffer(a.scales, a.n * a.blocks_per_row * 4u),
                      egd::buffer(a.zeros, ((a.n * a.blocks_per_row + 7u) / 8u) * 4u)};
     const StageBase sb = stage_base(a, m0, n0);
     Staged st[S];
 #pragma unroll
-    for (int u = 0; u + 1 < S; u++) load_block<ENC>(a, rs, sb, kbeg + min((uint32_t)u, nblk - 1) * kBK, st[u]);
-    const uint32_t full = nblk / S;
+    for (int u = 0; u + 1 < S; u++)
+      load_block<ENC>(a, rs, sb, kbeg + min(block_of((uint32_t)u), nblk - 1) * kBK, st[u]);
+    const uint32_t full = iters / S;
     for (uint32_t g = 0; g < full; g++) {
 #pragma unroll
       for (int u = 0; u < S; u++) {
-        const uint32_t blk = g * S + u;
+        const uint32_t it = g * S + u;
         store_block<ENC>(st[u], As, Bs);
         __syncthreads();
-        load_block<ENC>(a, rs, sb, kbeg + min(blk + S - 1, nblk - 1) * kBK, st[(u + S - 1) % S]);
-        mfma_block();
+        load_block<ENC>(a, rs, sb, kbeg + min(block_of(it + S - 1), nblk - 1) * kBK, st[(u + S - 1) % S]);
+        if (block_of(it) < nblk) mfma_block();
         __syncthreads();
       }
     }
-    const uint32_t rest = nblk - full * S;
+    const uint32_t rest = iters - full * S;
 #pragma unroll
     for (int u = 0; u + 1 < S; u++) {
       if ((uint32_t)u < rest) {
         store_block<ENC>(st[u], As, Bs);
         __syncthreads();
-        mfma_block();
+        if (block_of(full * S + u) < nblk) mfma_block();
         __syncthreads();
       }
     }
   } else {
-    for (uint32_t k0 = kbeg; k0 < kend; k0 += kBK) {
-      stage_elements<ENC>(a, m0, n0, k0, As, Bs);
+    for (uint32_t it = 0; it < iters; it++) {
+      const uint32_t blk = min(block_of(it), nblk - 1);
+      stage_elements<ENC>(a, m0, n0, kbeg + blk * kBK, As, Bs);
       __syncthreads();
-      mfma_block();
+      if (block_of(it) < nblk) mfma_block();
       __syncthreads();
     }
+  }
+  if (KG > 1) {
+    // every group's sums into its own buffers (the last barrier above ended the staging), then
+    // the groups added in order by the thread that stores the element
+    float* sums = reinterpret_cast<float*>(lds + group * kStageBytes);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          sums[(wm + i * 16 + 4 * (lane >> 4) + e) * kTile + wn + j * 16 + (lane & 15)] = acc[i][j][e];
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < kTile * kTile; idx += 256u * KG) {
+      const uint32_t r = idx / kTile, c = idx % kTile, row = m0 + r, col = n0 + c;
+      if (row >= a.m || col >= a.n) continue;
+      float v = reinterpret_cast<const float*>(lds)[idx];
+#pragma unroll
+      for (int g = 1; g < KG; g++) v += reinterpret_cast<const float*>(lds + g * kStageBytes)[idx];
+      if (a.partials) {
+        a.partials[((size_t)blockIdx.z * a.m + row) * a.n + col] = v;
+      } else {
+        const size_t o = (size_t)row * a.out_stride + col + a.out_offset;
+        a.out[o] = v + (a.bias ? a.bias[col] : 0.f) + (a.residual ? a.residual[o] : 0.f);
+      }
+    }
+    return;
   }
 
   // D layout of the 16x16 MFMA: lane l holds rows 4*(l/16) + e, column l % 16.
@@ -365,15 +410,23 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   if (m == 0 || n == 0) return EG_OK;
   const uint32_t tiles_n = (n + kTile - 1) / kTile, tiles_m = (m + kTile - 1) / kTile;
   if (tiles_m > 65535) return eg::fail(ctx, EG_ERR_RANGE, "%s: m %u needs %u row tiles, over 65535", op, m, tiles_m);
-  // Split K only where the tile grid leaves most CUs idle over a long reduction (the down
-  // projection: 4 x 14 tiles at M = 256, 76 blocks deep): the partial sums cost a second
-  // launch, so the split must save more block iterations than that launch costs. The f32
-  // partials live in the context's workspace.
+  // Groups per workgroup: a grid of at least one tile per CU runs one-group workgroups (three
+  // fit on a CU, so a second round of tiles overlaps the first); a smaller grid runs four groups
+  // per workgroup (one per CU), whose 16 waves work through the tile's K blocks four at a time
+  // (measured at M = 128: gate 11.4 -> 8.3 us; at M = 256 the 304 gate tiles would need a
+  // second round of 1024-thread workgroups: 14.6 -> 16.3 us).
   const uint64_t tiles = (uint64_t)tiles_n * tiles_m;
   const uint64_t blocks = (k + kBK - 1) / kBK;
+  const int kg = ctx->prefill_groups ? ctx->prefill_groups : (tiles >= (uint64_t)ctx->cu_count ? 1 : 4);
+  // Split K only where the tile grid leaves most CUs idle over a long reduction (the down
+  // projection: 4 x 14 tiles at M = 256, 76 blocks deep): the partial sums cost a second
+  // launch, so the split must save more block iterations than that launch costs. Four-group
+  // workgroups keep the split grid within one workgroup per CU and at least two blocks per
+  // group. The f32 partials live in the context's workspace.
   uint64_t splits = 1;
   if (blocks >= 32 && tiles < (uint64_t)ctx->cu_count)
-    splits = std::min<uint64_t>((ctx->cu_count + tiles - 1) / tiles, blocks / 8);
+    splits = kg == 1 ? std::min<uint64_t>((ctx->cu_count + tiles - 1) / tiles, blocks / 8)
+                     : std::min<uint64_t>(ctx->cu_count / tiles, blocks / (2 * (uint64_t)kg));
   splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, eg::kPartialsBytes / ((uint64_t)m * n * 4)));
   splits = std::max<uint64_t>(1, std::min<uint64_t>(splits, 65535));
   uint32_t k_per_split = (uint32_t)((((uint64_t)k + splits - 1) / splits + kBK - 1) / kBK * kBK);
@@ -387,13 +440,21 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
                        (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
                        (reinterpret_cast<uintptr_t>(packed) & 7u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  const dim3 block(256 * kg);
+#define EG_PREFILL_LAUNCH(ENC, CH)                                                                        \
+  do {                                                                                                    \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 4>), grid, block, 0, ctx->stream, a);        \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 2>), grid, block, 0, ctx->stream, a);   \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1>), grid, block, 0, ctx->stream, a);                \
+  } while (0)
   if (encoding == EG_ENC_SIGNED) {
-    if (chunked) hipLaunchKernelGGL((prefill_kernel<EG_ENC_SIGNED, true>), grid, dim3(256), 0, ctx->stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<EG_ENC_SIGNED, false>), grid, dim3(256), 0, ctx->stream, a);
+    if (chunked) EG_PREFILL_LAUNCH(EG_ENC_SIGNED, true);
+    else EG_PREFILL_LAUNCH(EG_ENC_SIGNED, false);
   } else {
-    if (chunked) hipLaunchKernelGGL((prefill_kernel<EG_ENC_OFFSET_ZEROS, true>), grid, dim3(256), 0, ctx->stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<EG_ENC_OFFSET_ZEROS, false>), grid, dim3(256), 0, ctx->stream, a);
+    if (chunked) EG_PREFILL_LAUNCH(EG_ENC_OFFSET_ZEROS, true);
+    else EG_PREFILL_LAUNCH(EG_ENC_OFFSET_ZEROS, false);
   }
+#undef EG_PREFILL_LAUNCH
   if (split) {
     const uint64_t total = (uint64_t)m * n;
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);

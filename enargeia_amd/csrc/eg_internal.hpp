@@ -32,6 +32,9 @@ struct eg_context {
   int gemv_override[4] = {0, 0, 0, 0};
   // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 2).
   uint32_t fused_tiles_per_wave = 2;
+  // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
+  // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
+  int prefill_groups = 0;
   // Resident workgroups per CU of each kernel launched through this context (from
   // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
   // the device.

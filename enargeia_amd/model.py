@@ -263,6 +263,9 @@ class Decoder:
                                              ctypes.byref(out) if read_token else None), self.device.ctx)
         return out.value if read_token else None
 
+    def set_prefill_chunk(self, rows: int) -> None:
+        check(_lib.load().eg_decoder_set_prefill_chunk(self.handle, rows), self.device.ctx)
+
     def history(self) -> np.ndarray:
         n = int(self.sample_params()["history_length"])
         return self.device.read_array(self.buffers.history, np.uint32, n) if n else np.zeros(0, np.uint32)

@@ -374,6 +374,10 @@ EG_API int eg_decoder_set_history(eg_decoder* decoder, const uint32_t* host_ids,
  * ("prompt of N exceeds the remaining context of M"). token_out as for eg_decoder_step. */
 EG_API int eg_decoder_prefill(eg_decoder* decoder, uint32_t position, const uint32_t* host_ids, uint32_t count,
                               uint32_t* token_out);
+/* Rows per prompt chunk (Session's prefillChunk, session.ts:146): a longer prompt runs as several
+ * chunks, each attending to the cache rows before it. The decoder holds buffers for
+ * min(2048, max_context) rows, its default; the reference's default is 256. */
+EG_API int eg_decoder_set_prefill_chunk(eg_decoder* decoder, uint32_t rows);
 
 /* ---- chunked-prefill attention (cache_variants.ts:81-145 attn_scores / attn_apply with the
  * softmax between; graph.ts:411-459 for the RoPE and cache writes before them) --------------

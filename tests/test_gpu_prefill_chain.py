@@ -32,13 +32,17 @@ def gap_of(logits):
     return float(logits[order[-1]] - logits[order[-2]]), int(order[-1])
 
 
-@pytest.mark.parametrize("n,begin", [(40, 0), (300, 0), (129, 100), (1, 7)])
-def test_prefill_chain_matches_oracle(device, n, begin):
-    """One chunk, two chunks (256 + 44), a chunk starting mid-context after cached rows, one row."""
+@pytest.mark.parametrize("n,begin,chunk", [(40, 0, None), (300, 0, 256), (300, 0, None), (129, 100, None),
+                                           (1, 7, None), (200, 50, 64)])
+def test_prefill_chain_matches_oracle(device, n, begin, chunk):
+    """One chunk; two chunks of the reference's 256 (256 + 44); the same prompt as one chunk; a
+    chunk starting mid-context after cached rows; one row; four chunks of 64 after cached rows."""
     cfg = ModelConfig(layers=2, max_context=512)
     m = synthetic_model(cfg)
     dm = DeviceModel(device, m)
     dec = Decoder(dm)
+    if chunk:
+        dec.set_prefill_chunk(chunk)
     ora = OracleDecoder(m, max_context=cfg.max_context)
     try:
         rng = np.random.default_rng(n)
