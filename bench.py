@@ -348,6 +348,9 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": "gemv_kernel<4,SIGNED,...,BATCHED> (K=896 projections, 24 layers)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "traffic_source": "not measured in this run: the committed rocprofv3 --pmc summary "
+                                  "profiles/gemv_batched_k896_config1_traffic.md (FETCH_SIZE + WRITE_SIZE per "
+                                  "dispatch, each scaled by a calibration kernel of known size)",
                 "bytes_per_launch": BATCH896_BYTES, "avg_launch_us": round(t896_ms * 1e3, 2)}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(mats)

@@ -47,7 +47,12 @@ struct eg_decoder {
   uint32_t* rng = nullptr;           // [1]: mulberry32 state, one draw per step
   eg_sampling_params sampling{0.f, 1.f, 1.f};  // host copy of sp's parameters
   eg_gemv_plan* head_plan = nullptr; // the LM head storing logits for the sampler (vocab % 8 == 0)
-  bool graph_sampled = false;        // the mode the graph was captured in
+  // Host-driven steps (DecodeGraph.setPosition, graph_decode.ts:398-406): the host writes the
+  // position, the history length and the draw before each step, and each step starts from the
+  // token in `token` (its embedding and RoPE table prepared first), as the reference's Session
+  // drives its DecodeGraph. Otherwise steps chain on the device and the draw is taken there.
+  bool host_driven = false;
+  bool graph_sampled = false, graph_host_driven = false;  // the mode the graph was captured in
   uint32_t* host_staging = nullptr;  // pinned [max_context]: prompt ids on their way to `history`
   // the prompt chain (ForwardGraph, graph.ts:380-567) over chunks of up to `chunk` rows
   // Rows per prompt chunk. The reference runs 256 (DEFAULT_PREFILL_CHUNK, session.ts:30; a
@@ -176,6 +181,7 @@ int run_layers(eg_decoder* d) {
 // (fused argmax partials reduced in the tail, which also advances the draw state) or sampled
 // (logits stored, the sampler draws and writes the token, the tail only settles it).
 int run_head(eg_decoder* d, bool sampled, const float* hidden) {
+  uint32_t* const rng = d->host_driven ? nullptr : d->rng;  // host-driven: the host's draw is in sp
   eg_context* ctx = d->ctx;
   const eg_model_desc& m = d->desc;
   const eg_quant_matrix& e = m.embedding;
@@ -193,7 +199,7 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
                                           m.embed_bits, &t.groups)) != EG_OK)
       return st;
     t.partials = reinterpret_cast<const uint32_t*>(eg::partials(ctx));
-    t.rng = d->rng;
+    t.rng = rng;
     return tail(d, t);
   }
   if (d->head_plan) {
@@ -206,14 +212,16 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
                                      m.embed_bits, &groups);
   }
   if (st != EG_OK) return st;
-  if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, d->rng)) != EG_OK)
+  if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, rng)) != EG_OK)
     return st;
   return tail(d, t);
 }
 
 // A whole decode step: the layers on the current token, then the head.
 int run_step(eg_decoder* d, bool sampled) {
-  const int st = run_layers(d);
+  // host-driven: the input is whatever token[0] and position[0] the host wrote
+  int st = d->host_driven ? tail(d, eg::StepTail{}) : EG_OK;
+  if (st == EG_OK) st = run_layers(d);
   return st != EG_OK ? st : run_head(d, sampled, d->h[0]);
 }
 
@@ -284,6 +292,16 @@ int read_token(eg_decoder* d, uint32_t* token_out) {
   return EG_OK;
 }
 
+int capture(eg_decoder* d);
+
+// Switches between host-driven and device-chained steps; a graph captured in the other mode is
+// captured again.
+int set_host_driven(eg_decoder* d, bool host) {
+  if (d->host_driven == host) return EG_OK;
+  d->host_driven = host;
+  return d->graph ? capture(d) : EG_OK;
+}
+
 int capture(eg_decoder* d) {
   if (d->graph) {
     eg_graph_destroy(d->graph);
@@ -302,6 +320,7 @@ int capture(eg_decoder* d) {
   if (st != EG_OK) return st;
   d->graph = g;
   d->graph_sampled = sampled;
+  d->graph_host_driven = d->host_driven;
   return EG_OK;
 }
 
@@ -527,14 +546,34 @@ int eg_decoder_set_sampling(eg_decoder* d, const eg_sampling_params* params) {
   if (st != EG_OK) return st;
   d->sampling = p;
   // a graph captured in the other mode (greedy fused argmax / sampler) is captured again
-  if (d->graph && d->graph_sampled != sampled_mode(p)) st = capture(d);
+  if (d->graph && (d->graph_sampled != sampled_mode(p) || d->graph_host_driven != d->host_driven)) st = capture(d);
   return st;
 }
 
 int eg_decoder_seed(eg_decoder* d, uint32_t seed) {
   if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "decoder_seed: decoder is NULL");
   if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "decoder_seed: a graph capture is in progress");
-  return write_ids(d, d->rng, &seed, 1);
+  int st = write_ids(d, d->rng, &seed, 1);
+  if (st == EG_OK) st = set_host_driven(d, false);
+  return st;
+}
+
+int eg_decoder_set_position(eg_decoder* d, uint32_t position, uint32_t history_length, float random) {
+  const char* op = "decoder_set_position";
+  if (!d) return eg::fail(nullptr, EG_ERR_INVALID, "%s: decoder is NULL", op);
+  if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "%s: a graph capture is in progress", op);
+  if (position >= d->desc.max_context)  // kvcache.ts:118-127
+    return eg::fail(d->ctx, EG_ERR_RANGE, "%s: position %u past the context of %u", op, position, d->desc.max_context);
+  if (history_length > d->desc.max_context)
+    return eg::fail(d->ctx, EG_ERR_RANGE, "%s: history of %u exceeds %u", op, history_length, d->desc.max_context);
+  uint32_t rbits;
+  std::memcpy(&rbits, &random, 4);
+  int st = write_ids(d, d->position, &position, 1);
+  if (st == EG_OK) st = write_ids(d, &d->sp->history_length, &history_length, 1);
+  if (st == EG_OK) st = write_ids(d, reinterpret_cast<uint32_t*>(&d->sp->random), &rbits, 1);
+  if (st == EG_OK) st = set_host_driven(d, true);
+  if (st == EG_OK) d->host_position = position;
+  return st;
 }
 
 int eg_decoder_set_history(eg_decoder* d, const uint32_t* host_ids, uint32_t count) {
@@ -571,8 +610,9 @@ int eg_decoder_prefill(eg_decoder* d, uint32_t position, const uint32_t* host_id
     if (host_ids[i] >= d->desc.vocab)
       return eg::fail(d->ctx, EG_ERR_INVALID, "%s: token %u at %u outside the vocabulary", op, host_ids[i], i);
   // the history is the prompt (Session.runPrefill: this.tokens = [...prompt]); the chunks read
-  // their ids from there
-  int st = eg_decoder_set_history(d, host_ids, count);
+  // their ids from there. The steps that follow chain on the device.
+  int st = set_host_driven(d, false);
+  if (st == EG_OK) st = eg_decoder_set_history(d, host_ids, count);
   // the prompt in chunks (ForwardGraph.encodeChunks, graph.ts:610-621)
   uint32_t last_rows = 0;
   for (uint32_t c0 = 0; st == EG_OK && c0 < count; c0 += d->chunk) {

@@ -4,6 +4,7 @@
 'use strict';
 
 const native = require('./native.js');
+const { HipBuffer, BufferUsage } = require('./gpu.js');
 
 class Decoder {
   /** device: a HipDevice; desc: {layers, hidden, heads, kvHeads, headDim, intermediate, vocab,
@@ -42,4 +43,81 @@ class Decoder {
   }
 }
 
-module.exports = { Decoder };
+/** A buffer the decoder owns, seen through the facade's buffer type so queue.writeBuffer,
+ * readBuffer and bindings reach it; destroy() leaves it to the decoder. */
+function borrowed(device, ptr, size, label) {
+  const buffer = Object.create(HipBuffer.prototype);
+  Object.assign(buffer, {
+    device, size, usage: BufferUsage.STORAGE | BufferUsage.COPY_SRC | BufferUsage.COPY_DST, label, uniform: false,
+    host: null, ptr,
+  });
+  buffer.destroy = () => {};
+  // the shape of a BufferPool entry (pool.ts:83-120), which the reference's graph fields are
+  return { buffer, size, capacity: size, binding: { buffer, offset: 0, size } };
+}
+
+/**
+ * DecodeGraph (src/model/graph_decode.ts:85-460) over eg_decoder, for a host that drives it the
+ * way the reference's Session.decodeStep does (session.ts:347-375): write the token into
+ * `tokenId` and the history into `history`, `setPosition(position, historyLength, random)`,
+ * `encode` into a command encoder, submit, read `result`. The buffers are the decoder's own
+ * device buffers. encode records one whole decode step (every layer, the LM head and the sample
+ * step: one launch sequence, or one graph replay after capture()).
+ */
+class DecodeGraph {
+  constructor(device, desc) {
+    this.device = device;
+    this.config = { layers: desc.layers, vocab: desc.vocab, maxContext: desc.maxContext };
+    this.handle = native.decoderCreate(device.ctx, desc);
+    const b = native.decoderBuffers(this.handle);
+    this.tokenId = borrowed(device, b.token, 4, 'decode/token_id');
+    this.result = borrowed(device, b.token, 4, 'decode/result');
+    this.history = borrowed(device, b.history, desc.maxContext * 4, 'decode/history');
+    this.logits = borrowed(device, b.logits, desc.vocab * 4, 'decode/logits');
+    this.params = { temperature: 0, topP: 1, repetitionPenalty: 1 };
+  }
+
+  /** graph_decode.ts:387 */
+  setSampling(params) {
+    native.decoderSetSampling(this.handle, params);
+    this.params = params;
+  }
+
+  /** graph_decode.ts:398-406: the per-token values of the next step (the one host write). */
+  setPosition(position, historyLength, random) {
+    native.decoderSetPosition(this.handle, position, historyLength, random);
+  }
+
+  /** graph_decode.ts:442-448: one decode step, run at submit. */
+  encode(encoder, position) {
+    const handle = this.handle;
+    encoder.record(() => native.decoderStep(handle, false));
+  }
+
+  /** Captures the step as a hipGraph; later encodes replay it. */
+  capture() {
+    native.decoderCapture(this.handle);
+  }
+
+  /** The prompt and its first token (ForwardGraph + sampleFromPrefill in one call); the draw is
+   * the decoder's own mulberry32 stream, restarted by seed(). */
+  prefill(position, prompt) {
+    return native.decoderPrefill(this.handle, position, new Uint32Array(prompt));
+  }
+
+  seed(seed) {
+    native.decoderSeed(this.handle, seed);
+  }
+
+  /** launches per step (5 per layer, the LM head, the sampler's 8, the tail) */
+  get dispatchCount() {
+    return 5 * this.config.layers + 2 + (this.params.temperature > 0 || this.params.repetitionPenalty !== 1 ? 8 : 0);
+  }
+
+  destroy() {
+    if (this.handle) native.decoderDestroy(this.handle);
+    this.handle = null;
+  }
+}
+
+module.exports = { Decoder, DecodeGraph };

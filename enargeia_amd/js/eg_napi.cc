@@ -609,7 +609,103 @@ napi_value DecoderCapture(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
-// decoderBuffers(dec) -> {kCache, vCache, logits, hidden, token, position} device pointers
+// A number argument as f32 (sampling parameters, the draw).
+bool f32_arg(Args& a, size_t i, float* out) {
+  if (!a.ok) return false;
+  double d = 0;
+  napi_valuetype t;
+  napi_typeof(a.env, a.argv[i], &t);
+  if (t != napi_number || napi_get_value_double(a.env, a.argv[i], &d) != napi_ok) {
+    throw_type(a.env, std::string(a.fn) + ": argument " + std::to_string(i) + " is not a number");
+    a.ok = false;
+    return false;
+  }
+  *out = (float)d;
+  return true;
+}
+
+DecoderHandle* live_decoder(napi_env env, Args& a, const char* fn) {
+  auto* h = a.handle<DecoderHandle>(0, "decoder");
+  if (!a.ok) return nullptr;
+  if (!h->dec) {
+    napi_throw_error(env, "EG_ERR_STATE", (std::string(fn) + ": the decoder was destroyed").c_str());
+    return nullptr;
+  }
+  return h;
+}
+
+// decoderSetSampling(dec, {temperature, topP, repetitionPenalty}) (DecodeGraph.setSampling)
+napi_value DecoderSetSampling(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderSetSampling", 2);
+  auto* h = live_decoder(env, a, "decoderSetSampling");
+  if (!h) return nullptr;
+  eg_sampling_params p{};
+  const char* names[3] = {"temperature", "topP", "repetitionPenalty"};
+  float* fields[3] = {&p.temperature, &p.top_p, &p.repetition_penalty};
+  for (int i = 0; i < 3; i++) {
+    napi_value v;
+    double d = 0;
+    if (napi_get_named_property(env, a.argv[1], names[i], &v) != napi_ok || napi_get_value_double(env, v, &d) != napi_ok) {
+      throw_type(env, std::string("decoderSetSampling: params.") + names[i] + " is not a number");
+      return nullptr;
+    }
+    *fields[i] = (float)d;
+  }
+  if (throw_status(env, h->ctx, eg_decoder_set_sampling(h->dec, &p))) return nullptr;
+  return undefined(env);
+}
+
+// decoderSeed(dec, seed)
+napi_value DecoderSeed(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderSeed", 2);
+  auto* h = live_decoder(env, a, "decoderSeed");
+  uint64_t seed = a.u64(1);
+  if (!h || !a.ok) return nullptr;
+  if (throw_status(env, h->ctx, eg_decoder_seed(h->dec, (uint32_t)seed))) return nullptr;
+  return undefined(env);
+}
+
+// decoderSetPosition(dec, position, historyLength, random) (DecodeGraph.setPosition)
+napi_value DecoderSetPosition(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderSetPosition", 4);
+  auto* h = live_decoder(env, a, "decoderSetPosition");
+  uint64_t position = a.u64(1), length = a.u64(2);
+  float random = 0.f;
+  if (!h || !f32_arg(a, 3, &random)) return nullptr;
+  if (throw_status(env, h->ctx, eg_decoder_set_position(h->dec, (uint32_t)position, (uint32_t)length, random)))
+    return nullptr;
+  return undefined(env);
+}
+
+// decoderSetHistory(dec, Uint32Array)
+napi_value DecoderSetHistory(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderSetHistory", 2);
+  auto* h = live_decoder(env, a, "decoderSetHistory");
+  void* data = nullptr;
+  size_t len = 0;
+  if (!h || !a.bytes(1, &data, &len)) return nullptr;
+  if (throw_status(env, h->ctx, eg_decoder_set_history(h->dec, static_cast<const uint32_t*>(data), (uint32_t)(len / 4))))
+    return nullptr;
+  return undefined(env);
+}
+
+// decoderPrefill(dec, position, Uint32Array prompt) -> the first token id
+napi_value DecoderPrefill(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderPrefill", 3);
+  auto* h = live_decoder(env, a, "decoderPrefill");
+  uint64_t position = a.u64(1);
+  void* data = nullptr;
+  size_t len = 0;
+  if (!h || !a.bytes(2, &data, &len)) return nullptr;
+  uint32_t token = 0;
+  if (throw_status(env, h->ctx, eg_decoder_prefill(h->dec, (uint32_t)position, static_cast<const uint32_t*>(data),
+                                                   (uint32_t)(len / 4), &token)))
+    return nullptr;
+  return number(env, token);
+}
+
+// decoderBuffers(dec) -> {kCache, vCache, logits, hidden, token, position, history, sampleParams,
+// rng} device pointers
 napi_value DecoderBuffers(napi_env env, napi_callback_info info) {
   Args a(env, info, "decoderBuffers", 1);
   auto* h = a.handle<DecoderHandle>(0, "decoder");
@@ -620,7 +716,9 @@ napi_value DecoderBuffers(napi_env env, napi_callback_info info) {
   napi_create_object(env, &obj);
   const std::pair<const char*, const void*> fields[] = {{"kCache", b.k_cache}, {"vCache", b.v_cache},
                                                         {"logits", b.logits}, {"hidden", b.hidden},
-                                                        {"token", b.token}, {"position", b.position}};
+                                                        {"token", b.token}, {"position", b.position},
+                                                        {"history", b.history}, {"sampleParams", b.sample_params},
+                                                        {"rng", b.rng}};
   for (const auto& f : fields)
     napi_set_named_property(env, obj, f.first, number(env, (double)reinterpret_cast<uintptr_t>(f.second)));
   return obj;
@@ -887,6 +985,11 @@ napi_value Init(napi_env env, napi_value exports) {
       {"decoderStep", nullptr, DecoderStep, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderCapture", nullptr, DecoderCapture, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderBuffers", nullptr, DecoderBuffers, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderSetSampling", nullptr, DecoderSetSampling, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderSeed", nullptr, DecoderSeed, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderSetPosition", nullptr, DecoderSetPosition, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderSetHistory", nullptr, DecoderSetHistory, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderPrefill", nullptr, DecoderPrefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderDestroy", nullptr, DecoderDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphBegin", nullptr, GraphBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"graphEnd", nullptr, GraphEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

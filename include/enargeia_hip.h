@@ -362,8 +362,15 @@ EG_API int eg_decoder_capture(eg_decoder* decoder);
  * a new decoder is GREEDY). */
 EG_API int eg_decoder_set_sampling(eg_decoder* decoder, const eg_sampling_params* params);
 /* Restarts the draw source: mulberry32(seed) (session.ts:75-83; a new decoder has the session's
- * default seed 0x5eed, :125). */
+ * default seed 0x5eed, :125), and returns the decoder to device-chained steps. */
 EG_API int eg_decoder_seed(eg_decoder* decoder, uint32_t seed);
+/* DecodeGraph.setPosition(position, historyLength, random) (graph_decode.ts:398-406), for a host
+ * that drives the decoder as the reference's Session.decodeStep does (session.ts:347-375): it
+ * writes the input token into the `token` buffer and the history into `history`, calls this,
+ * then steps. The decoder is then host-driven: each step first prepares the input from token[0]
+ * and the given position, and the sample step uses `random` as given instead of drawing on the
+ * device. eg_decoder_seed or eg_decoder_prefill return it to device-chained steps. */
+EG_API int eg_decoder_set_position(eg_decoder* decoder, uint32_t position, uint32_t history_length, float random);
 /* The repetition-penalty history (Session.tokens, written before each step, session.ts:349-350):
  * every step then appends the token it produces. count <= max_context. */
 EG_API int eg_decoder_set_history(eg_decoder* decoder, const uint32_t* host_ids, uint32_t count);

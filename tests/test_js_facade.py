@@ -11,6 +11,7 @@ import shutil
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -110,6 +111,42 @@ def test_node_decoder_matches_python_decoder(tmp_path, device):
         dm.release()
     assert node_tokens["eager"] == py_tokens
     assert node_tokens["graph"] == py_tokens
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_session_over_decode_graph_matches_python(tmp_path, device):
+    """The reference's Session.generate / decodeStep restated in JS over the DecodeGraph-shaped
+    binding (host-driven steps: tokenId, history, setPosition with the host's mulberry32 draw,
+    encode, submit, readBuffer) yields the same sampled tokens as the Python Session, whose
+    decoder chains the steps and draws on the device; eager and as a replayed graph."""
+    import json
+
+    from enargeia_amd.kernels import SamplingParams
+    from enargeia_amd.model import Decoder, DeviceModel, ModelConfig, synthetic_model
+    from enargeia_amd.session import Session
+
+    cfg = ModelConfig(layers=2, vocab=4096, max_context=256)
+    host = synthetic_model(cfg)
+    _write_model(host, str(tmp_path))
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, cfg.vocab, 12)]
+    steps = 24
+    arg = ",".join(map(str, prompt))
+    print(f"node tests/js/decode_graph_gpu.test.js {tmp_path} {arg} {steps}", flush=True)
+    res = subprocess.run([NODE, os.path.join(JS_TESTS, "decode_graph_gpu.test.js"), str(tmp_path), arg, str(steps)],
+                         cwd=ROOT, capture_output=True, text=True, timeout=110)
+    sys.stdout.write(res.stdout[-4000:])
+    assert res.returncode == 0, f"node exited {res.returncode}:\n{res.stdout[-3000:]}\n{res.stderr[-3000:]}"
+    node = json.loads(next(line for line in res.stdout.splitlines() if line.startswith('{"tokens"')))
+    dm = DeviceModel(device, host)
+    dec = Decoder(dm)
+    try:
+        py = Session(dec, SamplingParams(0.7, 0.9, 1.1), seed=0x5EED, capture=False).generate(prompt, steps).tokens
+    finally:
+        dec.close()
+        dm.release()
+    assert node["tokens"] == py
+    assert node["graph"] == py
 
 
 def _reference_checkpoint(directory, vocab=4096):
