@@ -132,6 +132,9 @@ def main() -> int:
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only the config-3 prefill GEMM and chunk-attention launches (for rocprofv3 kernel "
                          "statistics of those kernels)")
+    ap.add_argument("--prompt-profile", action="store_true",
+                    help="only the prompt path (eg_decoder_prefill of a 2048-token prompt as one chunk and in chunks "
+                         "of 256) on the config-4 model, for rocprofv3 kernel statistics of the prompt chain")
     ap.add_argument("--skip-decode", action="store_true",
                     help="leave out the config-4 decode measurement (rocprofv3 kernel tracing does not survive the "
                          "decoder's captured graph; --decode-profile covers the decode step eagerly)")
@@ -152,6 +155,16 @@ def main() -> int:
     if args.prefill_profile:
         dev = K.Device(0)
         print(json.dumps(prefill_numbers(dev, HipEvents(), dev.stream, args)), flush=True)
+        dev.close()
+        return 0
+    if args.prompt_profile:
+        from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, synthetic_model
+        dev = K.Device(0)
+        dm = DeviceModel(dev, synthetic_model(QWEN25_05B))
+        dec = Decoder(dm)
+        print(json.dumps(prompt_throughput(dev, dec, QWEN25_05B)), flush=True)
+        dec.close()
+        dm.release()
         dev.close()
         return 0
     if args.decode_profile:
