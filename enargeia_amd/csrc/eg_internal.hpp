@@ -191,7 +191,10 @@ __device__ __forceinline__ u32x4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t of
 // Non-temporal (streaming) loads, for data read exactly once per launch (weight codes and
 // scales): the nt cache-policy bit lets the line bypass normal retention, which measures ~10%
 // more read bandwidth on MI355X than default-policy loads.
-constexpr int kNonTemporal = 2;
+#ifndef EG_WEIGHT_CACHE_POLICY
+#define EG_WEIGHT_CACHE_POLICY 2  // the nt bit; 0 (default policy) builds a variant for measurement
+#endif
+constexpr int kNonTemporal = EG_WEIGHT_CACHE_POLICY;
 __device__ __forceinline__ u32x4 load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, kNonTemporal);
 }
