@@ -57,6 +57,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_attention_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "eg_attention_combine": (_i, [_vp, _vp, _vp, _vp]),
     "eg_gemv_plan_launch_input": (_i, [_vp, _vp, _vp]),
+    "eg_gemv_swiglu_plan_create": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32, _i, _i, _vp, ctypes.POINTER(_vp)]),
     "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_decode_advance": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
     "eg_decoder_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),

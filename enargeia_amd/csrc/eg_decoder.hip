@@ -6,8 +6,9 @@
 //   q|k|v   one batched GEMV, RMSNorm(input_layernorm) fused into its input stage, biases
 //   attn    one fused launch: RoPE, f16 cache append, split-K attention partials
 //   o       GEMV whose input stage combines the partials; bias = the residual stream
-//   gate|up one batched GEMV, RMSNorm(post_attention_layernorm) fused into its input stage
-//   down    GEMV whose input stage is SiLU(gate) * up; bias = the residual stream
+//   gate|up one GEMV launch over both matrices, RMSNorm(post_attention_layernorm) fused into its
+//           input stage, each row pair stored as SiLU(gate) * up
+//   down    GEMV on that vector; bias = the residual stream
 // then the LM head with the final norm fused and one tail launch that settles the token, advances
 // the position and prepares the next step: the new token's embedding row (layer 0's input) and
 // the RoPE cos/sin of the next position (read by every attention launch instead of computed
@@ -71,7 +72,8 @@ struct eg_decoder {
   uint16_t* k_cache = nullptr;
   uint16_t* v_cache = nullptr;
   size_t layer_stride = 0;  // cache elements per layer
-  std::vector<eg_gemv_plan*> plans;  // per layer: qkv, o, gateup, down
+  std::vector<eg_gemv_plan*> plans;  // per layer: qkv, o, gate|up (a SwiGLU pair if swiglu), down
+  bool swiglu = false;               // gate|up stores silu(gate) * up in gu[0, intermediate)
   eg_graph* graph = nullptr;
   std::vector<void*> allocations;
   uint32_t host_position = 0;  // mirrors position[0]: steps are refused once the cache is full
@@ -169,9 +171,9 @@ int run_layers(eg_decoder* d) {
     in.eps = m.rms_eps;
     if ((st = eg_gemv_plan_launch_input(ctx, P[2], &in)) != EG_OK) return st;
     in = eg_gemv_input{};
-    in.kind = EG_INPUT_SILU_MUL;
+    in.kind = d->swiglu ? EG_INPUT_VECTOR : EG_INPUT_SILU_MUL;
     in.x = d->gu;
-    in.x2 = d->gu + m.intermediate;
+    in.x2 = d->swiglu ? nullptr : d->gu + m.intermediate;
     if ((st = eg_gemv_plan_launch_input(ctx, P[3], &in)) != EG_OK) return st;  // h[0] = h[1] + down(...)
   }
   return st;
@@ -427,7 +429,15 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
         {L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, d->gu, m.intermediate, 0},
         {L.up.packed, L.up.scales, L.up.zeros, nullptr, d->gu, m.intermediate, m.intermediate},
     };
-    st = eg_gemv_plan_create(ctx, m.hidden, m.block_size, m.encoding, m.bits, gu, 2, &plan);
+    // int4 projections: one launch stores silu(gate) * up (the pair), so the down projection
+    // reads a plain vector; otherwise gate and up are stored and down's input stage applies
+    // SiLU * up. The choice is the same for every layer (same shapes).
+    if (l == 0) d->swiglu = m.bits == 4;
+    if (d->swiglu) {
+      st = eg_gemv_swiglu_plan_create(ctx, m.hidden, m.block_size, m.encoding, m.bits, gu, &plan);
+      if (st != EG_OK && l == 0) d->swiglu = false;  // no pair kernel for this shape
+    }
+    if (!d->swiglu) st = eg_gemv_plan_create(ctx, m.hidden, m.block_size, m.encoding, m.bits, gu, 2, &plan);
     if (st != EG_OK) break;
     d->plans.push_back(plan);
     eg_gemv_segment dn[1] = {{L.down.packed, L.down.scales, L.down.zeros, d->h[1], d->h[0], m.hidden, 0}};

@@ -465,6 +465,7 @@ struct eg_gemv_plan {
   DevSegment inline_table[kInlineSegments] = {};  // host copy, passed in the arguments when count <= kInlineSegments
   uint32_t any_bias = 0;                           // some segment has a bias
   uint32_t count = 0;
+  uint32_t swiglu_rows = 0;  // a SwiGLU pair (eg_gemv_swiglu_plan_create): the rows of each matrix
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
   int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
 };
@@ -558,6 +559,40 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   return EG_OK;
 }
 
+int eg_gemv_swiglu_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int encoding, int bits,
+                               const eg_gemv_segment* pair, eg_gemv_plan** out_plan) {
+  const char* op = "gemv_swiglu_plan";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!out_plan || !pair) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  *out_plan = nullptr;
+  if (bits != 4) return eg::fail(ctx, EG_ERR_INVALID, "%s: int4 weights only, got %d bits", op, bits);
+  const eg_gemv_segment &g = pair[0], &u = pair[1];
+  if (g.rows != u.rows) return eg::fail(ctx, EG_ERR_INVALID, "%s: gate has %u rows, up %u", op, g.rows, u.rows);
+  if (g.bias || u.bias) return eg::fail(ctx, EG_ERR_INVALID, "%s: the pair takes no biases", op);
+  // the streams, alignment and ranges of each matrix, as a two-matrix plan checks them (the
+  // pair stores through the gate's output only)
+  eg_gemv_segment both[2] = {g, u};
+  both[1].out = g.out;
+  both[1].out_offset = g.out_offset;
+  eg_gemv_plan* plan = nullptr;
+  int st = eg_gemv_plan_create(ctx, k, block_size, encoding, bits, both, 2, &plan);
+  if (st != EG_OK) return st;
+  // one team per row of each matrix: two rows (gate r, up r) per lane pair of slots
+  int u2 = 2;
+  const uint32_t rpw = 64u / plan->team;
+  if (plan->cpl > 2 || g.rows % rpw != 0) u2 = 0;
+  if (!u2 || !pick_kernel(bits, encoding, kSwiGLU, plan->team, plan->cpl, u2, plan->nb, EG_INPUT_RMSNORM)) {
+    eg_gemv_plan_destroy(ctx, plan);
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: no SwiGLU kernel for k %u and %u rows", op, k, g.rows);
+  }
+  plan->u = u2;
+  plan->swiglu_rows = g.rows;
+  plan->total_passes = g.rows / rpw;
+  plan->grid = 0;  // a pair always has its input stage: the grid is sized at launch
+  *out_plan = plan;
+  return EG_OK;
+}
+
 int eg_gemv_plan_launch(eg_context* ctx, const eg_gemv_plan* plan, const float* x) {
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "gemv_plan_launch: ctx is NULL");
   eg_gemv_input in{};
@@ -582,7 +617,12 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
     for (uint32_t i = 0; i < plan->count; i++) a.inline_segs[i] = plan->inline_table[i];
   a.total_passes = plan->total_passes;
   a.any_bias = plan->any_bias;
-  KernelFn fn = pick_kernel(plan->bits, plan->encoding, kBatched, plan->team, plan->cpl, plan->u, plan->nb, a.in_kind);
+  const bool pair = plan->swiglu_rows != 0;
+  if (pair && a.in_kind != EG_INPUT_RMSNORM)
+    return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: a SwiGLU pair takes the RMSNORM input stage");
+  a.n = plan->swiglu_rows;
+  KernelFn fn = pick_kernel(plan->bits, plan->encoding, pair ? kSwiGLU : kBatched, plan->team, plan->cpl, plan->u,
+                            plan->nb, a.in_kind);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR

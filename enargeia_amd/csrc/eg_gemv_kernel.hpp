@@ -157,8 +157,11 @@ struct Codes<8> {
 
 // kPlain: one matrix, logits/outputs stored. kArgmax: also a per-workgroup (max, index)
 // partial. kArgmaxOnly: the partial without storing the outputs. kBatched: a segment table of
-// matrices that share x and K.
-enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3 };
+// matrices that share x and K. kSwiGLU: two matrices of equal shape (gate, up; the argument
+// table's first two entries) whose row r is computed by the same team, which stores
+// silu(gate_r) * up_r (ops.ts:207-216) - so the SiLU is evaluated once per row, in the
+// producer, instead of by every workgroup of the down projection's input stage.
+enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3, kSwiGLU = 4 };
 
 template <int BITS, int U, int CPL>
 struct Loads {
@@ -380,7 +383,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
-  constexpr int TILE = RPW * U;
+  // kSwiGLU: slot u = 0 of a tile reads the gate matrix and u = 1 the up matrix at the same rows,
+  // so a tile produces RPW outputs; otherwise RPW * U rows of one matrix.
+  constexpr bool kPair = MODE == kSwiGLU;
+  static_assert(!kPair || U == 2, "a SwiGLU tile pairs one gate row with one up row");
+  constexpr int TILE = kPair ? RPW : RPW * U;
   constexpr bool kStore = MODE != kArgmaxOnly;
   constexpr bool kBest = MODE == kArgmax || MODE == kArgmaxOnly;
   const uint32_t lane = threadIdx.x & 63u;
@@ -412,7 +419,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   uint32_t qoff[U][CPL], soff[U][CPL], roff[U];
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    const uint32_t lrow = u * RPW + slot;
+    const uint32_t lrow = (kPair ? 0u : (uint32_t)u * RPW) + slot;
     roff[u] = lrow * 4u;
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
@@ -461,7 +468,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   // or with a scalar load from the table in global memory (scalar loads count on lgkmcnt, so
   // switching segments never waits for the tile loads in flight, as a vector load would). The
   // table is read-only for the launch, so the constant address space is accurate.
-  Seg cur = make_seg(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, 0, a.total_passes);
+  Seg cur = kPair ? make_seg(a.inline_segs[0].w, a.inline_segs[0].scales, a.inline_segs[0].zeros, nullptr,
+                             a.inline_segs[0].out, a.n, a.inline_segs[0].out_offset, 0, a.total_passes)
+                  : make_seg(a.w, a.scales, a.zeros, a.bias, a.out, a.n, a.out_offset, 0, a.total_passes);
+  // kSwiGLU: the up matrix (its output pointer unused: the pair stores through cur)
+  const Seg up = kPair ? make_seg(a.inline_segs[1].w, a.inline_segs[1].scales, a.inline_segs[1].zeros, nullptr,
+                                  a.inline_segs[0].out, a.n, 0, 0, a.total_passes)
+                       : cur;
   uint32_t seg = 0;
   auto use_segment = [&](const uint4* w, const float* scales, const uint32_t* zeros, const float* bias, float* out,
                          uint32_t rows, uint32_t pass_end, uint32_t out_offset) {
@@ -530,11 +543,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int u = 0; u < U; u++) {
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
-        L.q[u][j] = egd::load_b128_nt(cur.w, qoff[u][j], sq);
-        L.s[u][j] = egd::load_f32_nt(cur.s, soff[u][j], ss);
+        const Seg& m = kPair && u == 1 ? up : cur;
+        L.q[u][j] = egd::load_b128_nt(m.w, qoff[u][j], sq);
+        L.s[u][j] = egd::load_f32_nt(m.s, soff[u][j], ss);
         if (ENC == EG_ENC_OFFSET_ZEROS) {
-          const uint32_t blk = (row0 + u * RPW + slot) * a.blocks_per_row + bj[j];
-          L.zw[u][j] = egd::load_b32(cur.z, (blk / C::kZeroPerWord) * 4u);
+          const uint32_t blk = (row0 + (kPair ? 0u : (uint32_t)u * RPW) + slot) * a.blocks_per_row + bj[j];
+          L.zw[u][j] = egd::load_b32(m.z, (blk / C::kZeroPerWord) * 4u);
         }
       }
     }
@@ -572,12 +586,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   uint32_t best_i = a.out_offset;
 
   auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
+    float pair[2];  // kSwiGLU: the gate and up totals of the team's row
 #pragma unroll
     for (int u = 0; u < U; u++) {
       // The bias starts lane u's partial (linearQ4 starts its sum from the bias too; zero
       // where the matrix has none).
       float acc = t == (uint32_t)u ? L.b : 0.f;
-      const uint32_t row = P.row0 + u * RPW + slot;
+      const uint32_t row = P.row0 + (kPair ? 0u : (uint32_t)u * RPW) + slot;
 #pragma unroll
       for (int j = 0; j < CPL; j++) {
         const uint4 q = make_uint4(L.q[u][j].x, L.q[u][j].y, L.q[u][j].z, L.q[u][j].w);
@@ -591,6 +606,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j]) - z * sx[j], acc);
       }
       const float v = egd::team_allsum<TEAM>(acc);
+      if (kPair) {
+        pair[u & 1] = v;
+        continue;
+      }
       if (kStore) egd::store_f32(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
       if (kBest) {
         const uint32_t idx = row + P.out_offset;
@@ -598,6 +617,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         best_v = take ? v : best_v;
         best_i = take ? idx : best_i;
       }
+    }
+    if (kPair) {
+      const float g = pair[0];
+      egd::store_f32(P.o, roff[0], g / (1.0f + expf(-g)) * pair[1], (P.row0 + P.out_offset) * 4u);
     }
   };
 
@@ -682,12 +705,22 @@ using KernelFn = void (*)(GemvArgs);
   X(8, 1, 1) X(8, 1, 2) X(16, 1, 1) X(16, 1, 2) X(32, 1, 1) X(32, 1, 2) X(64, 1, 1) X(64, 1, 2) X(64, 1, 4) \
   X(64, 2, 1) X(64, 2, 2) X(64, 3, 1) X(64, 4, 1)
 
+// The shapes a SwiGLU pair takes (two rows per tile slot pair: U = 2).
+#define EG_SWIGLU_SHAPES(X) X(8, 1, 2) X(16, 1, 2) X(32, 1, 2) X(64, 1, 2) X(64, 2, 2)
+
 template <int IN, int BITS, int ENC, int MODE>
 KernelFn pick_fused_shape(int team, int cpl, int u) {
+  if constexpr (MODE == kSwiGLU) {
+#define EG_SWIGLU_CASE(T, P, UU) \
+  if (team == T && cpl == P && u == UU) return gemv_kernel<BITS, ENC, T, P, UU, 2, kSwiGLU, IN>;
+    EG_SWIGLU_SHAPES(EG_SWIGLU_CASE)
+#undef EG_SWIGLU_CASE
+  } else {
 #define EG_FUSED_CASE(T, P, UU) \
   if (team == T && cpl == P && u == UU) return gemv_kernel<BITS, ENC, T, P, UU, 2, MODE, IN>;
-  EG_FUSED_SHAPES(EG_FUSED_CASE)
+    EG_FUSED_SHAPES(EG_FUSED_CASE)
 #undef EG_FUSED_CASE
+  }
   return nullptr;
 }
 
@@ -696,6 +729,8 @@ KernelFn pick_fused_mode(int mode, int team, int cpl, int u) {
   if (mode == kBatched) return pick_fused_shape<IN, BITS, ENC, kBatched>(team, cpl, u);
   if (mode == kArgmax) return pick_fused_shape<IN, BITS, ENC, kArgmax>(team, cpl, u);
   if (mode == kArgmaxOnly) return pick_fused_shape<IN, BITS, ENC, kArgmaxOnly>(team, cpl, u);
+  if constexpr (IN == EG_INPUT_RMSNORM && BITS == 4)  // the int4 gate|up pair after the post-attention norm
+    if (mode == kSwiGLU) return pick_fused_shape<IN, BITS, ENC, kSwiGLU>(team, cpl, u);
   return nullptr;
 }
 

@@ -273,6 +273,16 @@ EG_API int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, 
                                    const float* scales, const uint32_t* zeros, float* out, uint32_t* result,
                                    const eg_embedding_dims* dims, int encoding, int bits);
 
+/* A gate|up pair in ONE launch that stores the SwiGLU product instead of both projections: no
+ * counterpart op in the reference, which dispatches gate, up and silu_mul separately
+ * (graph_decode.ts:330-345, ops.ts:207-216). pair[0] is the gate matrix, pair[1] the up matrix
+ * (same rows, no biases; int4 only); out = pair[0].out: out[r + pair[0].out_offset] =
+ * silu(g_r) * u_r with g_r, u_r the two GEMV rows on the launch's input and silu(g) =
+ * g / (1 + e^-g). Launched with eg_gemv_plan_launch_input and EG_INPUT_RMSNORM (the
+ * post-attention norm), so the down projection reads a plain vector (EG_INPUT_VECTOR). */
+EG_API int eg_gemv_swiglu_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int encoding, int bits,
+                                      const eg_gemv_segment* pair, eg_gemv_plan** out_plan);
+
 /* The end of a decode step (Session.decodeStep bookkeeping, session.ts:347-375, kept on the
  * device so a captured step replays without the host): position[0] += 1 and
  * history[history_length[0]++] = token[0]. */

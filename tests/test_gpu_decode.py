@@ -15,9 +15,9 @@ import pytest
 from conftest import assert_close
 from enargeia_amd import _lib
 from enargeia_amd import kernels as K
-from enargeia_amd.model import (INPUT_ATTENTION, INPUT_RMSNORM, INPUT_SILU_MUL, Decoder, DeviceModel, GemvInput,
-                                ModelConfig, attention_dims, synthetic_model)
-from enargeia_amd.quant import normal, quantize_sym
+from enargeia_amd.model import (INPUT_ATTENTION, INPUT_RMSNORM, INPUT_SILU_MUL, INPUT_VECTOR, Decoder, DeviceModel,
+                                GemvInput, ModelConfig, attention_dims, synthetic_model)
+from enargeia_amd.quant import normal, quantize_asym, quantize_sym
 from oracle import rope as oracle_rope
 from oracle.decode import OracleDecoder, attention, f16_array
 
@@ -339,3 +339,71 @@ def test_decoder_refuses_calls_inside_a_capture(device, small_model):
     finally:
         dec.close()
         dm.release()
+
+
+def swiglu_plan(device, gate, up, out):
+    """eg_gemv_swiglu_plan_create over (gate, up), writing silu(gate . x) * (up . x) to out."""
+    table = (K.GemvSegment * 2)()
+    keep = []
+    for i, q in enumerate((gate, up)):
+        bp, bs = device.upload(q.packed), device.upload(q.scales)
+        bz = device.upload(q.zeros) if q.zeros is not None else None
+        keep += [b for b in (bp, bs, bz) if b is not None]
+        table[i] = K.GemvSegment(bp.ptr, bs.ptr, bz.ptr if bz else None, None, out.ptr if i == 0 else None,
+                                 q.rows, 0)
+    h = ctypes.c_void_p()
+    _lib.check(lib().eg_gemv_swiglu_plan_create(device.ctx, gate.cols, gate.block_size, gate.encoding, gate.bits,
+                                                table, ctypes.byref(h)), device.ctx)
+    return h, keep
+
+
+@pytest.mark.parametrize("k,n,fmt", [(896, 4864, "sym"), (2048, 512, "sym"), (896, 1024, "offset")])
+def test_swiglu_pair_matches_gate_up_plan(device, k, n, fmt):
+    """The gate|up pair stores silu(g) * u per row: g and u are the bits a two-matrix plan
+    produces (same lane layout and sums), the product the expression of the SiLU input stage;
+    checked against the plan's own g and u to a few ulps and against the oracle at the GEMV bar.
+    K = 896 takes 32-lane teams, K = 2048 full-wave teams; the reference's offset format too."""
+    if fmt == "sym":
+        gate = quantize_sym(normal(n * k, 61 + k, 0.02), n, k, 4, 32)
+        up = quantize_sym(normal(n * k, 62 + k, 0.02), n, k, 4, 32)
+    else:
+        gate = quantize_asym(normal(n * k, 63, 0.02), n, k, 4, 64)
+        up = quantize_asym(normal(n * k, 64, 0.02), n, k, 4, 64)
+    x = normal(k, 65, 2.0).astype(np.float32)
+    w = (1.0 + normal(k, 66, 0.1)).astype(np.float32)
+    xb, wb = device.upload(x), device.upload(w)
+    pair_out, both = device.buffer(n * 4), device.buffer(2 * n * 4)
+    h, keep = swiglu_plan(device, gate, up, pair_out)
+    inp = GemvInput(INPUT_RMSNORM, xb.ptr, wb.ptr, 1e-6)
+    _lib.check(lib().eg_gemv_plan_launch_input(device.ctx, h, ctypes.byref(inp)), device.ctx)
+    got = device.read_array(pair_out, np.float32, n)
+    segs = []
+    for i, q in enumerate((gate, up)):
+        bz = device.upload(q.zeros) if q.zeros is not None else None
+        segs.append((device.upload(q.packed), device.upload(q.scales), bz, None, both, n, i * n))
+    plan = K.GemvPlan(device, k, gate.block_size, segs, encoding=gate.encoding)
+    launch_input(device, plan, inp)
+    gu = device.read_array(both, np.float32, 2 * n)
+    g, u = gu[:n].astype(np.float64), gu[n:].astype(np.float64)
+    assert_close(got, g / (1 + np.exp(-g)) * u, 0.0, 4e-7, label="pair vs plan g, u")
+    xn = (x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w).astype(np.float32)
+    g_ref, u_ref = reference_gemv(gate, xn).astype(np.float64), reference_gemv(up, xn).astype(np.float64)
+    want = g_ref / (1 + np.exp(-g_ref)) * u_ref
+    assert_close(got, want, 1e-5 * rms(want), 2e-3, label="pair vs oracle")
+    _lib.check(lib().eg_gemv_plan_destroy(device.ctx, h), device.ctx)
+    plan.destroy()
+
+
+def test_swiglu_pair_rejects_bad_pairs(device):
+    k = 896
+    gate = quantize_sym(normal(512 * k, 71, 0.02), 512, k, 4, 32)
+    up = quantize_sym(normal(256 * k, 72, 0.02), 256, k, 4, 32)
+    out = device.buffer(512 * 4)
+    with pytest.raises(K.EgError, match="gate has 512 rows, up 256"):
+        swiglu_plan(device, gate, up, out)
+    h, _ = swiglu_plan(device, gate, gate, out)
+    x = device.upload(normal(k, 73, 1.0).astype(np.float32))
+    inp = GemvInput(INPUT_VECTOR, x.ptr, None, 0.0)
+    st = lib().eg_gemv_plan_launch_input(device.ctx, h, ctypes.byref(inp))
+    assert st == _lib.EG_ERR_INVALID and b"RMSNORM" in lib().eg_last_error(device.ctx)
+    _lib.check(lib().eg_gemv_plan_destroy(device.ctx, h), device.ctx)
