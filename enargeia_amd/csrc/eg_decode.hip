@@ -389,20 +389,41 @@ int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, 
 // dequantized - and the RoPE cos/sin of the next position, which every attention launch of that
 // step reads instead of computing. Without `advance` (a reset) the token and position already in
 // device memory are used as they are.
+//
+// The launch is a chain of two memory round trips, each issued all at once: (1) every partial
+// (up to kTailPartials per thread), the position and the small state; (2) once the token is known,
+// its embedding row (one 32-bit word of codes and its scale per thread) and the next position's
+// row of the precomputed RoPE table.
+constexpr uint32_t kTailPartials = 8;  // per thread: 2048 partials, the LM head's largest grid
+
 __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uint32_t* token, uint32_t* position,
                                                              const uint32_t* packed, const float* scales,
                                                              const uint32_t* zeros, eg_embedding_dims d, int encoding,
                                                              int bits, float* emb, double2* rope, float theta) {
   constexpr int D = 64;
+  const uint32_t tid = threadIdx.x;
   __shared__ uint32_t next_token, next_pos;
+  // (1) everything the token and the position depend on, at once
+  const bool greedy = t.advance && t.partials;
+  uint64_t pv[kTailPartials];
+  if (greedy) {
+    const auto pb = egd::buffer(t.partials, t.groups * 8u);  // past the partials: zeros, masked below
+#pragma unroll
+    for (uint32_t r = 0; r < kTailPartials; r++) pv[r] = egd::load_b64(pb, (tid + r * kThreads) * 8u);
+  }
+  const uint32_t pos0 = position[0];
+  const uint32_t tok0 = token[0];
+  const uint32_t src = t.token_src ? *t.token_src : 0u;
+  const uint32_t hlen = t.history_length ? *t.history_length : 0u;
   uint32_t greedy_id = 0;  // thread 0: the reduced token of a greedy step
-  if (t.advance && t.partials) {
+  if (greedy) {
     float bv = -1.0e30f;
     uint32_t bi = 0;
-    for (uint32_t b = threadIdx.x; b < t.groups; b += kThreads) {
-      const float v = __uint_as_float(t.partials[2 * b]);
-      const uint32_t i = t.partials[2 * b + 1];
-      if (egd::better(v, i, bv, bi)) {
+#pragma unroll
+    for (uint32_t r = 0; r < kTailPartials; r++) {
+      const float v = __uint_as_float((uint32_t)pv[r]);
+      const uint32_t i = (uint32_t)(pv[r] >> 32);
+      if (tid + r * kThreads < t.groups && egd::better(v, i, bv, bi)) {
         bv = v;
         bi = i;
       }
@@ -410,12 +431,12 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
     __shared__ float wv[kThreads / 64];
     __shared__ uint32_t wi[kThreads / 64];
     egd::team_argmax<64>(bv, bi);
-    if ((threadIdx.x & 63u) == 0) {
-      wv[threadIdx.x >> 6] = bv;
-      wi[threadIdx.x >> 6] = bi;
+    if ((tid & 63u) == 0) {
+      wv[tid >> 6] = bv;
+      wi[tid >> 6] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
       for (int w = 1; w < kThreads / 64; w++)
         if (egd::better(wv[w], wi[w], bv, bi)) {
           bv = wv[w];
@@ -426,34 +447,53 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
       greedy_id = bi;
     }
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     if (t.advance) {
-      const uint32_t id = t.partials ? greedy_id : t.token_src ? *t.token_src : token[0];
+      const uint32_t id = t.partials ? greedy_id : t.token_src ? src : tok0;
       if (t.token_src) token[0] = id;
-      next_pos = position[0] + 1;
+      next_pos = pos0 + 1;
       position[0] = next_pos;
-      if (t.history && !t.token_src) {
-        const uint32_t n = *t.history_length;
-        if (n < t.history_capacity) {
-          t.history[n] = id;
-          *t.history_length = n + 1;
-        }
+      if (t.history && !t.token_src && hlen < t.history_capacity) {
+        t.history[hlen] = id;
+        *t.history_length = hlen + 1;
       }
       if (t.rng) (void)egd::mulberry32_next(t.rng);
       next_token = id;
     } else {
-      next_token = token[0];
-      next_pos = position[0];
+      next_token = tok0;
+      next_pos = pos0;
     }
   }
   __syncthreads();
+  // (2) the next step's RoPE row and the token's embedding row
   const uint32_t id = next_token, pos = next_pos;
-  if (threadIdx.x < D / 2) rope_table<D>(rope, threadIdx.x, pos, theta);
+  if (tid < D / 2) {
+    if (t.rope_table && pos < t.rope_positions) rope[tid] = t.rope_table[(size_t)pos * (D / 2) + tid];
+    else rope_table<D>(rope, tid, pos, theta);
+  }
   if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
   const uint32_t row = id - d.row_begin;
   const uint32_t per_word = 32u / (uint32_t)bits;
   const uint32_t mask = (1u << bits) - 1u;
-  for (uint32_t i = threadIdx.x; i < d.hidden; i += blockDim.x) {
+  if (d.block_size % per_word == 0 && (uint64_t)d.hidden * bits % 32 == 0) {
+    // one word of codes per thread; its per_word elements share a quant block (and zero-point)
+    const uint32_t words = d.hidden / per_word;
+    for (uint32_t wd = tid; wd < words; wd += blockDim.x) {
+      const uint64_t e0 = (uint64_t)row * d.hidden + (uint64_t)wd * per_word;
+      const uint32_t code_word = packed[e0 / per_word];
+      const uint32_t blk = row * d.blocks_per_row + wd * per_word / d.block_size;
+      const float sc = scales[blk];
+      float zero = (float)(1u << (bits - 1));
+      uint32_t flip = 0;
+      if (encoding == EG_ENC_OFFSET_ZEROS) zero = (float)((zeros[blk / per_word] >> (bits * (blk % per_word))) & mask);
+      else flip = 1u << (bits - 1);
+      float* out = emb + d.out_offset + wd * per_word;
+      for (uint32_t k = 0; k < per_word; k++)
+        out[k] = ((float)(((code_word >> (bits * k)) & mask) ^ flip) - zero) * sc;
+    }
+    return;
+  }
+  for (uint32_t i = tid; i < d.hidden; i += blockDim.x) {
     const uint64_t e = (uint64_t)row * d.hidden + i;
     uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
     const uint32_t blk = row * d.blocks_per_row + i / d.block_size;
@@ -468,6 +508,15 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
   }
 }
 
+// The RoPE cos/sin table of positions [0, positions): row p = what rope_table computes at p
+// (the same function, so a step reads exactly the values it would compute).
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(double2* table, uint32_t positions, float theta) {
+  constexpr int D = 64;
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t pos = i / (D / 2);
+  if (pos < positions) rope_table<D>(table + (size_t)pos * (D / 2), i % (D / 2), pos, theta);
+}
+
 }  // namespace
 
 int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
@@ -478,6 +527,15 @@ int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const f
                           dims, rope);
 }
 
+int eg::launch_rope_table(eg_context* ctx, double* table, uint32_t positions, uint32_t head_dim, float theta) {
+  if (head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "rope_table: head_dim %u (64 is supported)", head_dim);
+  if (positions == 0) return EG_OK;
+  const uint64_t n = (uint64_t)positions * (head_dim / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     ctx->stream, reinterpret_cast<double2*>(table), positions, theta);
+  return eg::check_launch(ctx, "rope_table");
+}
+
 int eg::launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32_t* position,
                          const uint32_t* packed, const float* scales, const uint32_t* zeros,
                          const eg_embedding_dims* ed, int encoding, int bits, float* emb, double* rope,
@@ -485,6 +543,8 @@ int eg::launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, ui
   if (head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "step_tail: head_dim %u (64 is supported)", head_dim);
   if ((t.history == nullptr) != (t.history_length == nullptr))
     return eg::fail(ctx, EG_ERR_INVALID, "step_tail: history and history_length go together");
+  if (t.partials && t.groups > kTailPartials * kThreads)
+    return eg::fail(ctx, EG_ERR_RANGE, "step_tail: %u argmax partials, at most %u", t.groups, kTailPartials * kThreads);
   hipLaunchKernelGGL(step_tail_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, t, token, position, packed, scales,
                      encoding == EG_ENC_SIGNED ? nullptr : zeros, *ed, encoding, bits, emb,
                      reinterpret_cast<double2*>(rope), theta);

@@ -39,6 +39,7 @@ struct eg_decoder {
   float* logits = nullptr;           // [vocab]
   float* emb = nullptr;              // [hidden]: the current token's embedding, layer 0's input
   double* rope = nullptr;            // [head_dim / 2] (cos, sin) at the current position
+  double* rope_table = nullptr;      // [max_context][head_dim / 2] (cos, sin), computed once
   uint32_t* token = nullptr;         // [2]: next input id, its logit bits
   uint32_t* position = nullptr;      // [1]
   // the sample step's state (DecodeGraph.history / setPosition's uniform, graph_decode.ts:150,
@@ -121,9 +122,11 @@ eg_embedding_dims embedding_dims_of(const eg_model_desc& m) {
 }
 
 // The step tail (see eg::launch_step_tail).
-int tail(eg_decoder* d, const eg::StepTail& t) {
+int tail(eg_decoder* d, eg::StepTail t) {
   const eg_model_desc& m = d->desc;
   const eg_embedding_dims ed = embedding_dims_of(m);
+  t.rope_table = reinterpret_cast<const double2*>(d->rope_table);
+  t.rope_positions = m.max_context;
   return eg::launch_step_tail(d->ctx, t, d->token, d->position, m.embedding.packed, m.embedding.scales,
                               m.embedding.zeros, &ed, m.embed_encoding, m.embed_bits, d->emb, d->rope, m.head_dim,
                               m.rope_theta);
@@ -379,6 +382,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take(m.hidden * 4, &d->h[1]);
   take(m.hidden * 4, &d->emb);
   take((size_t)m.head_dim / 2 * 2 * sizeof(double), &d->rope);
+  take((size_t)m.max_context * (m.head_dim / 2) * 2 * sizeof(double), &d->rope_table);
   take((size_t)m.heads * m.head_dim * 4, &d->q);
   take(2 * kvn * 4, &d->kv);
   take((size_t)2 * m.intermediate * 4, &d->gu);
@@ -403,6 +407,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take(4, &d->rng);
   take(d->layer_stride * m.layers * 2, &d->k_cache);
   take(d->layer_stride * m.layers * 2, &d->v_cache);
+  if (st == EG_OK) st = eg::launch_rope_table(ctx, d->rope_table, m.max_context, m.head_dim, m.rope_theta);
   if (st != EG_OK) {
     release(d);
     return st;

@@ -125,8 +125,9 @@ struct Shape {
 // holds at once (occupancy x CUs), each wave then walking its own contiguous range of tiles.
 // Sizing to residency matters because the ranges are equal: a second, late-starting round of
 // workgroups would double the tail.
-// A fused input stage is recomputed by every workgroup, so those launches give each wave
-// `tiles_per_wave` tiles to amortise it (fewer, longer-lived workgroups).
+// A fused input stage is recomputed by every workgroup; those launches give each wave
+// `tiles_per_wave` tiles (the context's setting, 1 by default: measured, the decoder's launches
+// finish sooner with more workgroups than with fewer that amortise the stage).
 uint32_t grid_for(eg_context* ctx, KernelFn fn, uint32_t tiles, uint32_t smem_bytes, uint32_t tiles_per_wave = 1) {
   int occ = eg::occupancy_of(ctx, reinterpret_cast<const void*>(fn), smem_bytes);
   if (occ <= 0) occ = 2;
@@ -148,7 +149,13 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
     sh.team = 8;
     while ((uint32_t)sh.team < chunks) sh.team *= 2;
     sh.cpl = 1;
-    sh.u = sh.team == 64 ? 4 : 2;  // measured on MI355X: int8 rows of 56 chunks / int4 rows of 28
+    // measured on MI355X: int8 rows of 56 chunks / int4 rows of 28 stream best with 4 / 2 rows
+    // per lane; a matrix whose one-row-per-lane tiles all fit in about one resident wave of the
+    // device (the decoder's per-layer projections) is faster with one - each wave's chain of
+    // dependent steps is then a single tile
+    const uint32_t rpw = 64u / sh.team;
+    const uint32_t cus = ctx ? (uint32_t)ctx->cu_count : 256u;
+    sh.u = sh.team == 64 ? 4 : (n + rpw - 1) / rpw <= 16u * cus ? 1 : 2;
   } else {
     sh.team = 64;
     sh.cpl = (int)((chunks + 63) / 64);

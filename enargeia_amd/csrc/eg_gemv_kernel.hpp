@@ -285,16 +285,10 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     const uint32_t q4 = chunks / 4;
     const auto ob = egd::buffer(a.x, n * chunks * 4u);
     const auto mb = egd::buffer(m, hcs * 4u), lb = egd::buffer(l, hcs * 4u);
-    egd::u32x4 ov[kOut][kQ];
-    if (batched) {
-#pragma unroll
-      for (uint32_t r = 0; r < kOut; r++)
-#pragma unroll
-        for (uint32_t q = 0; q < kQ; q++)
-          ov[r][q] = q < q4 ? egd::load_b128(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
-    }
     // statistics: thread p = tid + 256 r holds head p / G, chunk p % G (chunks past the head's
-    // count, and groups past the last head, read nothing: m = -inf, l = 0)
+    // count, and groups past the last head, read nothing: m = -inf, l = 0). Issued before the o
+    // values, so the weights are computed while those are still arriving (a wave's reads
+    // complete in issue order).
     constexpr uint32_t kStat = kMaxCombine / 256;
     float mv[kStat], lv[kStat];
     uint32_t sidx[kStat];
@@ -307,6 +301,14 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       const uint32_t off = sval[r] ? sidx[r] * 4u : 0xFFFFFFF0u;  // past the stream: reads zero
       mv[r] = __uint_as_float(egd::load_b32(mb, off));
       lv[r] = __uint_as_float(egd::load_b32(lb, off));
+    }
+    egd::u32x4 ov[kOut][kQ];
+    if (batched) {
+#pragma unroll
+      for (uint32_t r = 0; r < kOut; r++)
+#pragma unroll
+        for (uint32_t q = 0; q < kQ; q++)
+          ov[r][q] = q < q4 ? egd::load_b128(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
     }
     early();
 #pragma unroll
@@ -322,16 +324,18 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
 #pragma unroll
       for (uint32_t r = 0; r < kOut; r++) {
         const uint32_t i = tid + r * 256u;
-        const float* w = wts + (i / D) * chunks;
+        // the head's weights: one 16-byte LDS read per 4 chunks, the same address in every lane
+        // of the wave (a head is 64 consecutive outputs), so a broadcast
+        const float4* w = reinterpret_cast<const float4*>(wts + (i / D) * chunks);
         float acc = 0.f;
 #pragma unroll
         for (uint32_t q = 0; q < kQ; q++) {
           if (q < q4) {
-            const float4 v = f4(ov[r][q]);
-            acc = fmaf(v.x, w[4 * q + 0], acc);
-            acc = fmaf(v.y, w[4 * q + 1], acc);
-            acc = fmaf(v.z, w[4 * q + 2], acc);
-            acc = fmaf(v.w, w[4 * q + 3], acc);
+            const float4 v = f4(ov[r][q]), wq = w[q];
+            acc = fmaf(v.x, wq.x, acc);
+            acc = fmaf(v.y, wq.y, acc);
+            acc = fmaf(v.z, wq.z, acc);
+            acc = fmaf(v.w, wq.w, acc);
           }
         }
         if (i < n) xs[i] = acc;

@@ -30,8 +30,10 @@ struct eg_context {
   // EG_GEMV_SHAPE="t,c,u[,d]", read once at creation; zeros mean the built-in choice. For
   // tuning sweeps.
   int gemv_override[4] = {0, 0, 0, 0};
-  // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 2).
-  uint32_t fused_tiles_per_wave = 2;
+  // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 1: every
+  // workgroup recomputes the stage, but the decoder's launches measured faster with more,
+  // shorter-lived workgroups than with two tiles per wave).
+  uint32_t fused_tiles_per_wave = 1;
   // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
   // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
   int prefill_groups = 0;
@@ -88,7 +90,16 @@ struct StepTail {
   uint32_t* history_length = nullptr;   // ... at history[*history_length]++, up to the capacity
   uint32_t history_capacity = 0;
   uint32_t* rng = nullptr;              // mulberry32 state: advanced once (a greedy step's draw)
+  // the RoPE cos/sin of positions [0, rope_positions) (launch_rope_table); the next position's
+  // row is copied from here (computed in the launch where it is NULL or the position is past it)
+  const double2* rope_table = nullptr;
+  uint32_t rope_positions = 0;
 };
+
+// Fills table[p * head_dim / 2 + i] with the RoPE (cos, sin) of position p and frequency i for
+// p < positions: the values launch_step_tail and the attention launch compute, by the same
+// function. head_dim 64.
+int launch_rope_table(eg_context* ctx, double* table, uint32_t positions, uint32_t head_dim, float theta);
 
 // The decode step's tail, one single-workgroup launch. With `advance` the step's token is
 // settled (greedy: reduced from the argmax partials into token[0..1]; fill: copied from
