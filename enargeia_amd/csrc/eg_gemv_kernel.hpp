@@ -171,6 +171,16 @@ struct Loads {
   float b;  // lane t < U of a team: the bias of the team's row t
 };
 
+// Where float4 i of x (P float4 per 16-byte chunk of codes: 8 for int4, 4 for int8) sits in LDS:
+// chunk-transposed, piece e of every chunk side by side (x_slot = e * chunks + chunk). A lane
+// reads its chunk's pieces in order, so at each read the lanes of a team touch consecutive 16-byte
+// slots - no bank conflicts - where a row-major x would put every lane 128 (int4) or 64 (int8)
+// bytes apart, on the same banks.
+template <int P>
+__device__ __forceinline__ uint32_t x_slot(uint32_t i, uint32_t chunks) {
+  return (i % P) * chunks + i / P;
+}
+
 // The input stage: every workgroup writes the K-element input vector into LDS (xs), from x
 // as given or through a fused producer - RMSNorm (the reduction is per workgroup, fixed order,
 // so every workgroup computes the same bits), SiLU(gate) * up, or the attention combine. IN
@@ -186,14 +196,17 @@ struct Loads {
 // kernel issues its first tiles' weight loads there, so the weights are in flight while the
 // stage waits for its own reads and computes. (A wave's reads complete in issue order, so the
 // stage still waits only for its own loads; a workgroup barrier does not wait for reads.)
-template <int IN, typename Early>
+template <int IN, int P, typename Early>
 __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch,
                                               Early&& early) {
   const uint32_t tid = threadIdx.x;
   const uint32_t n4 = n / 4;  // n is a multiple of 32
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
   const float4* y4 = reinterpret_cast<const float4*>(a.x2);
-  float4* out4 = reinterpret_cast<float4*>(xs);
+  // x goes into LDS chunk-transposed (see x_slot): float4 i of x at x_slot(i)
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  const uint32_t xchunks = n4 / P;  // 16-byte chunks of codes per row
+  auto put4 = [&](uint32_t i, const float4& v) { xs4[x_slot<P>(i, xchunks)] = v; };
   auto f4 = [](const egd::u32x4& v) {
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   };
@@ -237,11 +250,11 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     for (uint32_t r = 0; r < kVec; r++) {
       const uint32_t i = tid + r * 256u;
       const float4 v = f4(xv[r]), w = f4(wv[r]);
-      if (i < n4) out4[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+      if (i < n4) put4(i, make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w));
     }
     for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) {
       const float4 v = x4[i], w = y4[i];
-      out4[i] = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+      put4(i, make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w));
     }
   } else if (IN == EG_INPUT_SILU_MUL) {
     // gate and up for up to kVec * 1024 inputs in one batch (the intermediate width 4864 is 4.75
@@ -262,9 +275,9 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
 #pragma unroll
     for (uint32_t r = 0; r < kVec; r++) {
       const uint32_t i = tid + r * 256u;
-      if (i < n4) out4[i] = silu_mul(f4(gv[r]), f4(uv[r]));
+      if (i < n4) put4(i, silu_mul(f4(gv[r]), f4(uv[r])));
     }
-    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) out4[i] = silu_mul(x4[i], y4[i]);
+    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) put4(i, silu_mul(x4[i], y4[i]));
   } else if (IN == EG_INPUT_ATTENTION) {
     // The combine of the attention partials (chunk-fastest: o[h][D][chunks], m[h][chunks],
     // l[h][chunks]): every (head, chunk) pair's weight e^(m_c - M) / L goes into LDS, then every
@@ -338,7 +351,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
             acc = fmaf(v.w, wq.w, acc);
           }
         }
-        if (i < n) xs[i] = acc;
+        if (i < n) xs[x_slot<P>(i / 4, xchunks) * 4 + i % 4] = acc;
       }
     } else {
       for (uint32_t i = tid; i < n; i += blockDim.x) {
@@ -346,7 +359,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
         const float* w = wts + (i / D) * chunks;
         float acc = 0.f;
         for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], w[c], acc);
-        xs[i] = acc;
+        xs[x_slot<P>(i / 4, xchunks) * 4 + i % 4] = acc;
       }
     }
   } else {
@@ -361,7 +374,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
 #pragma unroll
     for (uint32_t r = 0; r < kMaxLoads; r++)
-      if (tid + r * 256u < n4) dst[tid + r * 256u] = v[r];
+      if (tid + r * 256u < n4) dst[x_slot<P>(tid + r * 256u, xchunks)] = v[r];
   }
 }
 
@@ -570,10 +583,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int j = 0; j < CPL; j++) {
       const bool valid = t + j * TEAM < a.chunks;
       sx[j] = 0.f;
-      const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + (size_t)cj[j] * (EPC / 4);
+      const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + cj[j];  // piece e at e * chunks
 #pragma unroll
       for (int e = 0; e < EPC / 4; e++) {
-        const egd::u32x4 v = xs[e];
+        const egd::u32x4 v = xs[(size_t)e * a.chunks];
         xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
         xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
         xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
@@ -648,7 +661,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int b = 0; b + 1 < NB; b++) issue(first + b, L[b], P[b]);
     __builtin_amdgcn_sched_barrier(0);
   };
-  produce_input<IN>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
+  produce_input<IN, EPC / 4>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
   __syncthreads();
   load_x();
   const uint32_t count = end - begin;
