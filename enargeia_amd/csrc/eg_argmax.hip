@@ -57,11 +57,28 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
   }
 }
 
+// Up to kFinalPerThread partials per thread are loaded at once (one round trip for the largest
+// grids, 2048 partials); more take a loop.
+constexpr uint32_t kFinalPerThread = 8;
+
 __global__ __launch_bounds__(kThreads) void finalize_kernel(const uint32_t* partials, uint32_t groups,
                                                             uint32_t sentinel_index, uint32_t* result) {
   float bv = -1.0e30f;
   uint32_t bi = sentinel_index;
-  for (uint32_t b = threadIdx.x; b < groups; b += kThreads) {
+  const auto pb = egd::buffer(partials, groups * 8u);  // past the partials: zeros, masked below
+  uint64_t pv[kFinalPerThread];
+#pragma unroll
+  for (uint32_t r = 0; r < kFinalPerThread; r++) pv[r] = egd::load_b64(pb, (threadIdx.x + r * kThreads) * 8u);
+#pragma unroll
+  for (uint32_t r = 0; r < kFinalPerThread; r++) {
+    const float v = __uint_as_float((uint32_t)pv[r]);
+    const uint32_t i = (uint32_t)(pv[r] >> 32);
+    if (threadIdx.x + r * kThreads < groups && egd::better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  for (uint32_t b = threadIdx.x + kFinalPerThread * kThreads; b < groups; b += kThreads) {
     const float v = __uint_as_float(partials[2 * b]);
     const uint32_t i = partials[2 * b + 1];
     if (egd::better(v, i, bv, bi)) {
