@@ -12,26 +12,29 @@
 //     running kept mass reaches the target (:266-321); argmax fallback (:324-331).
 //
 // MI355X design. The reference makes ~36 passes over the vocabulary inside one workgroup. Here
-// the vocabulary is split over G workgroups (4096 ids each) and the work is 7 short launches;
-// no launch waits on another workgroup, and each launch starts by re-reducing the previous
-// launches' few per-workgroup partials itself, in a fixed order, so every workgroup derives
-// the same global values:
-//   pass_max   : penalty on this workgroup's slice (a hit mask of the history ids it owns, LDS
-//                copy + in-place global write), then the slice's (max, argmax) of l/T (of l
-//                when greedy);
-//   pass_sum   : global max; the slice's sum of exp(l/T - max) in float64;
-//   pass_level : one launch per 8 bisection steps. The 255 mids those 8 steps could visit are
-//                the in-order nodes of a depth-8 bisection tree below the current (lo, hi),
-//                computed with the same f32 expression; every p in [lo, hi) is binned against
-//                them, p >= hi goes to an 'above' bin, and each group adds its bins into one
-//                global set with integer atomics. Replaying the 8 steps from the summed bins is
-//                exact: mass(p >= mid) is 'above' plus a suffix sum of bins;
-//   pass_kept  : the threshold after 32 steps, the slice's kept mass;
-//   finalize   : one workgroup: the target, the slice whose prefix reaches it, then the id.
+// the vocabulary is split over G workgroups (4096 ids each, G = 38 at 151,936 ids) that are all
+// resident at once, and the whole sample is ONE launch whose phases are separated by grid
+// barriers (a central counter with a generation word, agent-scope release/acquire; every wait
+// bounded): each workgroup loads its slice's logits once and keeps them - and later their
+// probabilities - in registers through every phase:
+//   penalty on the slice (a hit mask of the history ids it owns) and the slice's (max, argmax)
+//     of l/T (of l when greedy)                                                   | barrier
+//   global max (greedy: the token, done); the slice's sum of exp(l/T - max) in float64 | barrier
+//   4 levels of 8 bisection steps: the 255 mids those 8 steps could visit are the in-order nodes
+//     of a depth-8 bisection tree below the current (lo, hi), computed with the same f32
+//     expression; every p in [lo, hi) is binned against them, p >= hi goes to an 'above' bin,
+//     and each workgroup adds its bins into one global set with integer atomics; after the
+//     barrier every workgroup replays the 8 steps from the summed bins (exact: mass(p >= mid)
+//     is 'above' plus a suffix sum of bins)                                       | barrier x 4
+//   the threshold after 32 steps; the slice's kept mass                           | barrier
+//   the target and the first slice whose kept prefix reaches it; that slice's workgroup finds
+//     the id in ascending order.
 // Masses are fixed-point integers (p * 2^52, exact for p >= 2^-28) summed with integer adds, so
 // every mass is independent of summation order and the result is deterministic. They differ
 // from the reference's f32 tree sums only by rounding, which can change a decision only when
 // a mass is within ~1e-7 of topP or the target within ~1e-7 of a cumulative boundary.
+// A barrier that times out (a workgroup that never became resident) raises an abort flag that
+// every wait also reads; every workgroup then leaves and the result is 0xFFFFFFFF.
 #include "eg_internal.hpp"
 
 namespace {
@@ -51,30 +54,13 @@ struct SampleParams {
 };
 static_assert(sizeof(SampleParams) == 32, "sample dims are 32 bytes");
 
-struct SampleState {
-  float max_scaled;
-  uint32_t argmax;
-  float total;
-  float threshold;
-  float lo[kLevels + 1], hi[kLevels + 1];  // bracket each level bins against; [kLevels] = final
-};
-
 struct Work {
-  SampleState* state;
   uint32_t* max_part;     // 2 u32 per group
   double* sum_part;       // 1 per group
   unsigned long long* bins;  // kLevels x (kBins + 1), summed over groups by integer atomics
   uint64_t* kept_part;    // 1 per group
   uint32_t* count_part;   // 1 per group
 };
-
-__device__ __forceinline__ SampleParams load_params(const SampleParams& p, const SampleParams* dev) {
-  return dev ? *dev : p;
-}
-
-__device__ __forceinline__ float prob(float logit, const SampleParams& p, float mx, float total) {
-  return expf(logit / p.temperature - mx) / total;
-}
 
 __device__ __forceinline__ uint64_t to_fix(float p) { return (uint64_t)__double2ull_rn((double)p * kFix); }
 
@@ -107,33 +93,6 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* sv, u
       i = si[w];
     }
   __syncthreads();
-}
-
-// ---- the global values every launch re-derives from the partials ------------------------
-
-__device__ void global_max(const Work& w, uint32_t groups, float& mx, uint32_t& amax) {
-  __shared__ float sv[4];
-  __shared__ uint32_t si[4];
-  float bv = -1.0e30f;
-  uint32_t bi = 0;
-  for (uint32_t b = threadIdx.x; b < groups; b += kThreads) {
-    const float v = __uint_as_float(w.max_part[2 * b]);
-    const uint32_t i = w.max_part[2 * b + 1];
-    if (egd::better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  block_argmax(bv, bi, sv, si);
-  mx = bv;
-  amax = bi;
-}
-
-__device__ float global_total(const Work& w, uint32_t groups) {
-  __shared__ double scratch[4];
-  double t = 0.0;
-  for (uint32_t b = threadIdx.x; b < groups; b += kThreads) t += w.sum_part[b];
-  return (float)block_sum(t, scratch);
 }
 
 // In-order mid j (0..254) of the depth-8 bisection tree below [lo, hi): the f32 mid the
@@ -191,16 +150,68 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
   return before + incl - v;
 }
 
-// Replays the 8 bisection steps of `level` from its summed bins: (lo, hi) in, (lo, hi) out.
-// All threads: the 255 tree mids, the bin column sums, the suffix sums and the mass at every
-// tree node in parallel; then the 8-step walk reads one node mass per step.
-__device__ void replay_level(const Work& w, uint32_t groups, int level, float top_p, float& lo, float& hi,
-                             float* mids, unsigned long long* sums) {
+// ---- grid barrier --------------------------------------------------------------------------
+
+// Central barrier over the launch's workgroups: thread 0 of each releases the workgroup's writes
+// at agent scope and counts itself; the last to arrive resets the count and advances the
+// generation, which the others poll (acquire). Polls are bounded: past kSpin, or when another
+// workgroup has given up, the abort flag is raised and false is returned to every thread.
+constexpr uint32_t kSpin = 1u << 20;  // polls of ~1 us: a barrier gives up after about a second
+
+struct GridSync {
+  uint32_t* count;  // arrivals at the current barrier (0 between barriers)
+  uint32_t* gen;    // advanced once per completed barrier
+  uint32_t* abort;  // set by a timed-out wait
+};
+
+__device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
+  __shared__ uint32_t ok;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    bool good = true;
+    const uint32_t gen0 = __hip_atomic_load(g.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t arrived = __hip_atomic_fetch_add(g.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (arrived == groups - 1) {
+      __hip_atomic_store(g.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(g.gen, gen0 + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      uint32_t n = 0;
+      while (__hip_atomic_load(g.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen0) {
+        if (__hip_atomic_load(g.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u || ++n > kSpin) {
+          good = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!good) __hip_atomic_store(g.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ok = good ? 1u : 0u;
+  }
+  __syncthreads();
+  return ok != 0u;
+}
+
+// Sets the barrier's words for the next launch (a kernel, not a memset, so a captured graph
+// replays it): a sample launch never starts from a count left by an aborted one.
+__global__ void sync_reset_kernel(GridSync g) {
+  if (threadIdx.x == 0) {
+    *g.count = 0u;
+    *g.abort = 0u;
+  }
+}
+
+// The depth-8 tree's 255 mids below [lo, hi) and the replay of its 8 bisection steps from the
+// globally summed bins of one level: (lo, hi) in, (lo, hi) out. All threads: the mids, the bins'
+// suffix sums and the mass at every tree node in parallel; then the 8-step walk reads one node
+// mass per step.
+__device__ void replay_level(const unsigned long long* summed, float top_p, float& lo, float& hi, float* mids) {
+  __shared__ unsigned long long sums[kBins + 1];
   __shared__ unsigned long long suffix[kBins + 1];
   __shared__ double node_mass[kBins - 1];
   __shared__ float out_lo, out_hi;
   if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
-  const unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
   for (int i = threadIdx.x; i <= kBins; i += kThreads) sums[i] = summed[i];
   __syncthreads();
   // suffix[k] = mass of p >= hi (sums[kBins]) plus bins k..kBins-1: total minus an exclusive
@@ -236,284 +247,246 @@ __device__ void replay_level(const Work& w, uint32_t groups, int level, float to
   hi = out_hi;
 }
 
-// ---- launches --------------------------------------------------------------------------------
+// ---- the launch --------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void pass_max(float* logits, const uint32_t* history, SampleParams hp,
-                                                     const SampleParams* dp, Work w, uint32_t* rng) {
-  // This call's draw (one per sampled step, Session.decodeStep session.ts:351), consumed by
-  // finalize; no workgroup of this launch reads `random`.
-  if (rng && blockIdx.x == 0 && threadIdx.x == 0)
-    const_cast<SampleParams*>(dp)->random = egd::mulberry32_next(rng);
-  const SampleParams p = load_params(hp, dp);
-  __shared__ float slice[kSlice];
-  __shared__ float sv[4];
-  __shared__ uint32_t si[4];
-  const uint32_t base = blockIdx.x * kSlice;
+// Thread t of workgroup g owns ids g * kSlice + t * kPerThread + [0, kPerThread): thread order is
+// id order, which the final scan relies on.
+__global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const uint32_t* history, uint32_t* out,
+                                                          SampleParams hp, SampleParams* dp, Work w, GridSync gs,
+                                                          uint32_t* rng) {
+  const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
+  // This call's draw (one per sampled step, Session.decodeStep session.ts:351): taken by
+  // workgroup 0 before the first barrier, read by everyone after it.
+  if (rng && dp && g == 0 && tid == 0) dp->random = egd::mulberry32_next(rng);
+  SampleParams p = dp ? *dp : hp;  // `random` is read again after the first barrier (below)
+  const uint32_t base = g * kSlice, first = base + tid * kPerThread;
   const uint32_t end = min(base + kSlice, p.vocab);
-  for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads) slice[i] = base + i < end ? logits[base + i] : 0.f;
-  __syncthreads();
+  float v[kPerThread];
+#pragma unroll
+  for (int r = 0; r < kPerThread; r += 4) {
+    if (first + r + 4 <= p.vocab) {
+      const float4 q = *reinterpret_cast<const float4*>(logits + first + r);
+      v[r] = q.x;
+      v[r + 1] = q.y;
+      v[r + 2] = q.z;
+      v[r + 3] = q.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[r + e] = first + r + e < p.vocab ? logits[first + r + e] : 0.f;
+    }
+  }
   if (p.repetition_penalty != 1.0f) {
     // The penalty applies once per distinct history id (the reference applies it at an id's
     // first occurrence only): mark the ids this slice owns, then penalize each marked element
-    // once. No two threads write the same element.
+    // once, in registers and in place in memory.
     __shared__ uint8_t hit[kSlice];
-    for (uint32_t i = threadIdx.x; i < kSlice; i += kThreads) hit[i] = 0;
+    for (uint32_t i = tid; i < kSlice; i += kThreads) hit[i] = 0;
     __syncthreads();
-    for (uint32_t h = threadIdx.x; h < p.history_length; h += kThreads) {
+    for (uint32_t h = tid; h < p.history_length; h += kThreads) {
       const uint32_t id = history[h];
       if (id >= base && id < end) hit[id - base] = 1;
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < end - base; i += kThreads) {
-      if (hit[i]) {
-        const float v = slice[i];
-        const float r = v > 0.0f ? v / p.repetition_penalty : v * p.repetition_penalty;
-        slice[i] = r;
-        logits[base + i] = r;
+#pragma unroll
+    for (int r = 0; r < kPerThread; r++) {
+      const uint32_t i = first + r;
+      if (i < end && hit[i - base]) {
+        v[r] = v[r] > 0.0f ? v[r] / p.repetition_penalty : v[r] * p.repetition_penalty;
+        logits[i] = v[r];
       }
     }
-    __syncthreads();
   }
   const bool greedy = p.temperature <= 0.0f;
-  float bv = -1.0e30f;
-  uint32_t bi = greedy ? 0u : base;
-  for (uint32_t i = base + threadIdx.x; i < end; i += kThreads) {
-    const float v = greedy ? slice[i - base] : slice[i - base] / p.temperature;
-    if (egd::better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
+  {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    float bv = -1.0e30f;
+    uint32_t bi = greedy ? 0u : base;
+#pragma unroll
+    for (int r = 0; r < kPerThread; r++) {
+      const uint32_t i = first + r;
+      const float x = greedy ? v[r] : v[r] / p.temperature;
+      if (i < end && egd::better(x, i, bv, bi)) {
+        bv = x;
+        bi = i;
+      }
+    }
+    block_argmax(bv, bi, sv, si);
+    if (tid == 0) {
+      w.max_part[2 * g] = __float_as_uint(bv);
+      w.max_part[2 * g + 1] = bi;
     }
   }
-  block_argmax(bv, bi, sv, si);
-  if (threadIdx.x == 0) {
-    w.max_part[2 * blockIdx.x] = __float_as_uint(bv);
-    w.max_part[2 * blockIdx.x + 1] = bi;
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void pass_sum(const float* logits, SampleParams hp, const SampleParams* dp,
-                                                     Work w) {
-  const SampleParams p = load_params(hp, dp);
-  if (p.temperature <= 0.0f) return;
-  __shared__ double scratch[4];
-  float mx;
-  uint32_t amax;
-  global_max(w, gridDim.x, mx, amax);
-  const uint32_t base = blockIdx.x * kSlice;
-  const uint32_t end = min(base + kSlice, p.vocab);
-  float lv[kPerThread];
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    lv[r] = i < end ? logits[i] : 0.f;
-  }
-  double s = 0.0;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++)
-    if (base + r * kThreads + threadIdx.x < end) s += (double)expf(lv[r] / p.temperature - mx);
-  s = block_sum(s, scratch);
-  if (threadIdx.x == 0) w.sum_part[blockIdx.x] = s;
-  // The level launches accumulate into these; clear them for this call (a kernel, not a
-  // memset, so a captured graph replays it).
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < kLevels * (kBins + 1); i += kThreads) w.bins[i] = 0;
-}
-
-__global__ __launch_bounds__(kThreads) void pass_level(const float* logits, int level, SampleParams hp,
-                                                       const SampleParams* dp, Work w) {
-  const SampleParams p = load_params(hp, dp);
-  if (p.temperature <= 0.0f || !(p.top_p < 1.0f)) return;
-  __shared__ float mids[kBins - 1];
-  __shared__ unsigned long long bins[kBins + 1];
-  const uint32_t base = blockIdx.x * kSlice;
-  const uint32_t end = min(base + kSlice, p.vocab);
-  float lv[kPerThread];  // issued first: independent of everything read below
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    lv[r] = i < end ? logits[i] : 0.f;
-  }
-  float mx;
-  uint32_t amax;
-  global_max(w, gridDim.x, mx, amax);
-  const float total = global_total(w, gridDim.x);
-  // The bracket this level bins against: (0, 1) first, then the previous level's bracket
-  // replayed through its 8 steps. Workgroup 0 records it for the next launch.
-  float lo = 0.0f, hi = 1.0f;
-  if (level > 0) {
-    lo = w.state->lo[level - 1];
-    hi = w.state->hi[level - 1];
-    replay_level(w, gridDim.x, level - 1, p.top_p, lo, hi, mids, bins);
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    w.state->lo[level] = lo;
-    w.state->hi[level] = hi;
-  }
-  if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
-  for (int i = threadIdx.x; i <= kBins; i += kThreads) bins[i] = 0;
-  __syncthreads();
-  // The mids split [lo, hi) into 256 near-equal steps, so the bin is estimated arithmetically
-  // and corrected against the exact f32 mids (usually no step). Runs of equal bins are summed
-  // in registers before the LDS atomic (at the first level nearly every p shares bin 0).
-  const float scale = (float)kBins / (hi - lo);
-  int run_bin = -1;
-  unsigned long long run_mass = 0;
-  float pv[kPerThread];
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    pv[r] = i < end ? prob(lv[r], p, mx, total) : -1.0f;
-  }
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const float pr = pv[r];
-    if (pr < lo) continue;
-    int k;
-    if (pr >= hi) {
-      k = kBins;
-    } else {
-      k = min(max((int)((pr - lo) * scale), 0), kBins - 1);  // estimate of #mids <= pr
-      while (k < kBins - 1 && mids[k] <= pr) k++;
-      while (k > 0 && mids[k - 1] > pr) k--;
-    }
-    if (k != run_bin) {
-      if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);  // integer adds: order-independent
-      run_bin = k;
-      run_mass = 0;
-    }
-    run_mass += to_fix(pr);
-  }
-  if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);
-  __syncthreads();
-  // Integer adds commute: the summed bins are the same whatever order the groups arrive in.
-  unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
-  for (int i = threadIdx.x; i <= kBins; i += kThreads)
-    if (bins[i]) atomicAdd(&summed[i], bins[i]);
-}
-
-__global__ __launch_bounds__(kThreads) void pass_kept(const float* logits, SampleParams hp, const SampleParams* dp,
-                                                      Work w) {
-  const SampleParams p = load_params(hp, dp);
-  if (p.temperature <= 0.0f) return;
-  __shared__ float mids[kBins - 1];
-  __shared__ unsigned long long bins[kBins + 1];
-  __shared__ unsigned long long kscratch[4];
-  __shared__ uint32_t cscratch[4];
-  const uint32_t base = blockIdx.x * kSlice;
-  const uint32_t end = min(base + kSlice, p.vocab);
-  float lv[kPerThread];  // issued first: independent of everything read below
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    lv[r] = i < end ? logits[i] : 0.f;
-  }
-  float mx;
-  uint32_t amax;
-  global_max(w, gridDim.x, mx, amax);
-  const float total = global_total(w, gridDim.x);
-  float lo = 0.0f, hi = 1.0f;
-  if (p.top_p < 1.0f) {
-    lo = w.state->lo[kLevels - 1];
-    hi = w.state->hi[kLevels - 1];
-    replay_level(w, gridDim.x, kLevels - 1, p.top_p, lo, hi, mids, bins);
-  }
-  const float thr = p.top_p < 1.0f ? lo : 0.0f;
-  unsigned long long kept = 0;
-  uint32_t count = 0;
-#pragma unroll
-  for (int r = 0; r < kPerThread; r++) {
-    const uint32_t i = base + r * kThreads + threadIdx.x;
-    if (i >= end) continue;
-    const float pr = prob(lv[r], p, mx, total);
-    if (pr >= thr) {
-      kept += to_fix(pr);
-      count++;
-    }
-  }
-  kept = block_sum(kept, kscratch);
-  count = block_sum(count, cscratch);
-  if (threadIdx.x == 0) {
-    w.kept_part[blockIdx.x] = kept;
-    w.count_part[blockIdx.x] = count;
-    if (blockIdx.x == 0) {
-      w.state->max_scaled = mx;
-      w.state->argmax = amax;
-      w.state->total = total;
-      w.state->threshold = thr;
-      w.state->lo[kLevels] = lo;
-      w.state->hi[kLevels] = hi;
-    }
-  }
-}
-
-// One workgroup: greedy result, or the target and the id where the kept mass reaches it.
-__global__ __launch_bounds__(kThreads) void finalize(const float* logits, uint32_t* out, uint32_t groups,
-                                                     SampleParams hp, const SampleParams* dp, Work w) {
-  const SampleParams p = load_params(hp, dp);
-  if (p.temperature <= 0.0f) {
-    float mx;
-    uint32_t amax;
-    global_max(w, groups, mx, amax);
-    if (threadIdx.x == 0) out[0] = amax;
+  // the level bins are summed with atomics: cleared here, before the barrier that orders them
+  // before any level adds to them
+  if (g == 0)
+    for (int i = tid; i < kLevels * (kBins + 1); i += kThreads) w.bins[i] = 0;
+  if (!grid_barrier(gs, G)) {
+    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
     return;
   }
-  __shared__ uint32_t group, pick;
+  if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
+  float mx;
+  uint32_t amax;
+  {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    float bv = -1.0e30f;
+    uint32_t bi = 0;
+    if (tid < G) {
+      bv = __uint_as_float(w.max_part[2 * tid]);
+      bi = w.max_part[2 * tid + 1];
+    }
+    block_argmax(bv, bi, sv, si);
+    mx = bv;
+    amax = bi;
+  }
+  if (greedy) {
+    if (g == 0 && tid == 0) out[0] = amax;
+    return;
+  }
+  // e = exp(l/T - max), kept in registers; the slice's sum in float64
+  {
+    __shared__ double scratch[4];
+    double s = 0.0;
+#pragma unroll
+    for (int r = 0; r < kPerThread; r++) {
+      v[r] = first + r < end ? expf(v[r] / p.temperature - mx) : 0.f;
+      s += (double)v[r];
+    }
+    s = block_sum(s, scratch);
+    if (tid == 0) w.sum_part[g] = s;
+  }
+  if (!grid_barrier(gs, G)) {
+    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
+    return;
+  }
+  float total;
+  {
+    __shared__ double scratch[4];
+    total = (float)block_sum(tid < G ? w.sum_part[tid] : 0.0, scratch);
+  }
+  // p in registers; ids past the vocabulary get -1 (never kept)
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) v[r] = first + r < end ? v[r] / total : -1.0f;
+  float thr = 0.0f;
+  if (p.top_p < 1.0f) {
+    __shared__ float mids[kBins - 1];
+    __shared__ unsigned long long bins[kBins + 1];
+    float lo = 0.0f, hi = 1.0f;
+    for (int level = 0; level < kLevels; level++) {
+      if (tid < kBins - 1) mids[tid] = tree_mid(tid, lo, hi);
+      for (int i = tid; i <= kBins; i += kThreads) bins[i] = 0;
+      __syncthreads();
+      // The mids split [lo, hi) into 256 near-equal steps, so the bin is estimated
+      // arithmetically and corrected against the exact f32 mids (usually no step). Runs of
+      // equal bins are summed in registers before the LDS atomic.
+      const float scale = (float)kBins / (hi - lo);
+      int run_bin = -1;
+      unsigned long long run_mass = 0;
+#pragma unroll
+      for (int r = 0; r < kPerThread; r++) {
+        const float pr = v[r];
+        if (pr < lo) continue;
+        int k;
+        if (pr >= hi) {
+          k = kBins;
+        } else {
+          k = min(max((int)((pr - lo) * scale), 0), kBins - 1);  // estimate of #mids <= pr
+          while (k < kBins - 1 && mids[k] <= pr) k++;
+          while (k > 0 && mids[k - 1] > pr) k--;
+        }
+        if (k != run_bin) {
+          if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);  // integer adds: order-independent
+          run_bin = k;
+          run_mass = 0;
+        }
+        run_mass += to_fix(pr);
+      }
+      if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);
+      __syncthreads();
+      unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
+      for (int i = tid; i <= kBins; i += kThreads)
+        if (bins[i]) __hip_atomic_fetch_add(&summed[i], bins[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!grid_barrier(gs, G)) {
+        if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
+        return;
+      }
+      replay_level(summed, p.top_p, lo, hi, mids);
+    }
+    thr = lo;
+  }
+  // the slice's kept mass and count
+  unsigned long long mine = 0;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++)
+    if (v[r] >= thr) {
+      mine += to_fix(v[r]);
+      cnt++;
+    }
+  {
+    __shared__ unsigned long long ks[4];
+    __shared__ uint32_t cs[4];
+    const unsigned long long kept = block_sum(mine, ks);
+    const uint32_t count = block_sum(cnt, cs);
+    if (tid == 0) {
+      w.kept_part[g] = kept;
+      w.count_part[g] = count;
+    }
+  }
+  if (!grid_barrier(gs, G)) {
+    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
+    return;
+  }
+  // Kept mass per slice in id order: the target, then the first slice whose inclusive prefix
+  // reaches it (and that keeps something, so a zero target still lands on a kept id). Every
+  // workgroup derives the same slice; only that slice's workgroup (or, with none, workgroup 0)
+  // goes on.
+  __shared__ uint32_t pick_group, pick;
   __shared__ unsigned long long group_prefix;
-  const SampleState st = *w.state;
-  // Kept mass per group in id order: the target, then the first group whose inclusive prefix
-  // reaches it (and that keeps something, so a zero target still lands on a kept id).
   unsigned long long all = 0;
-  const unsigned long long gk = threadIdx.x < groups ? w.kept_part[threadIdx.x] : 0ull;
-  const uint32_t gc = threadIdx.x < groups ? w.count_part[threadIdx.x] : 0u;
+  const unsigned long long gk = tid < G ? w.kept_part[tid] : 0ull;
+  const uint32_t gc = tid < G ? w.count_part[tid] : 0u;
   const unsigned long long gbefore = block_exclusive_scan(gk, &all);
   double kd = (double)all / kFix;
   if (kd < 1.0e-20) kd = 1.0e-20;
   const double target_fx = (double)p.random * kd * kFix;
-  if (threadIdx.x == 0) {
-    group = 0xFFFFFFFFu;
+  if (tid == 0) {
+    pick_group = 0xFFFFFFFFu;
     pick = 0xFFFFFFFFu;
   }
   __syncthreads();
-  if (threadIdx.x < groups && gc > 0 && (double)(gbefore + gk) >= target_fx) atomicMin(&group, threadIdx.x);
+  if (tid < G && gc > 0 && (double)(gbefore + gk) >= target_fx) atomicMin(&pick_group, tid);
   __syncthreads();
-  if (threadIdx.x == group) group_prefix = gbefore;
+  if (tid == pick_group) group_prefix = gbefore;
   __syncthreads();
-  if (group != 0xFFFFFFFFu) {
-    // Thread t owns ids [t*16, t*16+16) of the group's slice, so thread order is id order.
-    const uint32_t gbase = group * kSlice;
-    float pv[kPerThread];
-    unsigned long long mine = 0;
-#pragma unroll
-    for (int r = 0; r < kPerThread; r++) {
-      const uint32_t i = gbase + threadIdx.x * kPerThread + r;
-      pv[r] = -1.0f;
-      if (i < p.vocab) {
-        const float pr = prob(logits[i], p, st.max_scaled, st.total);
-        if (pr >= st.threshold) {
-          pv[r] = pr;
-          mine += to_fix(pr);
-        }
-      }
-    }
-    unsigned long long run = group_prefix + block_exclusive_scan(mine, nullptr);
-#pragma unroll
-    for (int r = 0; r < kPerThread; r++) {
-      if (pv[r] >= 0.0f) {
-        run += to_fix(pv[r]);
-        if ((double)run >= target_fx) {
-          atomicMin(&pick, gbase + threadIdx.x * kPerThread + r);
-          break;
-        }
-      }
-    }
-    __syncthreads();
+  if (pick_group == 0xFFFFFFFFu) {
+    if (g == 0 && tid == 0) out[0] = amax;
+    return;
   }
-  if (threadIdx.x == 0) out[0] = pick != 0xFFFFFFFFu ? pick : st.argmax;
+  if (g != pick_group) return;
+  unsigned long long run = group_prefix + block_exclusive_scan(mine, nullptr);
+#pragma unroll
+  for (int r = 0; r < kPerThread; r++) {
+    if (v[r] >= thr) {
+      run += to_fix(v[r]);
+      if ((double)run >= target_fx) {
+        atomicMin(&pick, first + r);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) out[0] = pick != 0xFFFFFFFFu ? pick : amax;
 }
 
-Work workspace(eg_context* ctx) {
+Work workspace(eg_context* ctx, GridSync* gs) {
   Work w;
-  w.state = reinterpret_cast<SampleState*>(eg::state(ctx) + 512);
+  uint32_t* sync = reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048);  // three words, 128 bytes apart
+  gs->count = sync;
+  gs->gen = sync + 32;
+  gs->abort = sync + 64;
   uint8_t* part = eg::partials(ctx);
   size_t off = 0;
   w.max_part = reinterpret_cast<uint32_t*>(part + off);
@@ -531,21 +504,16 @@ Work workspace(eg_context* ctx) {
   return w;
 }
 
+// The barrier reset, then the sample launch (all its workgroups must be resident at once:
+// G <= kMaxGroups = 256 workgroups of 256 threads and ~12 KB of LDS each fit the device).
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
-           const SampleParams* dp, bool all_passes, uint32_t* rng = nullptr) {
+           SampleParams* dp, uint32_t* rng = nullptr) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
-  Work w = workspace(ctx);
-  const dim3 grid(groups), block(kThreads);
-  hipLaunchKernelGGL(pass_max, grid, block, 0, ctx->stream, logits, history, hp, dp, w, rng);
-  const bool sampled = all_passes || hp.temperature > 0.0f;
-  if (sampled) {
-    hipLaunchKernelGGL(pass_sum, grid, block, 0, ctx->stream, logits, hp, dp, w);
-    if (all_passes || hp.top_p < 1.0f)
-      for (int l = 0; l < kLevels; l++)
-        hipLaunchKernelGGL(pass_level, grid, block, 0, ctx->stream, logits, l, hp, dp, w);
-    hipLaunchKernelGGL(pass_kept, grid, block, 0, ctx->stream, logits, hp, dp, w);
-  }
-  hipLaunchKernelGGL(finalize, dim3(1), block, 0, ctx->stream, logits, out, groups, hp, dp, w);
+  GridSync gs;
+  Work w = workspace(ctx, &gs);
+  hipLaunchKernelGGL(sync_reset_kernel, dim3(1), dim3(64), 0, ctx->stream, gs);
+  hipLaunchKernelGGL(sample_kernel, dim3(groups), dim3(kThreads), 0, ctx->stream, logits, history, out, hp, dp, w, gs,
+                     rng);
   return eg::check_launch(ctx, "sample");
 }
 
@@ -560,7 +528,7 @@ int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* his
                     kMaxGroups * kSlice);
   SampleParams hp{};
   hp.vocab = vocab;
-  return launch(ctx, logits, history, out, hp, reinterpret_cast<const SampleParams*>(params), true, rng);
+  return launch(ctx, logits, history, out, hp, reinterpret_cast<SampleParams*>(params), rng);
 }
 
 extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
@@ -575,5 +543,5 @@ extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history
                     kMaxGroups * kSlice);
   SampleParams hp;
   std::memcpy(&hp, dims, sizeof(hp));
-  return launch(ctx, logits, history, out, hp, nullptr, false);
+  return launch(ctx, logits, history, out, hp, nullptr);
 }
