@@ -19,14 +19,17 @@
 // probabilities - in registers through every phase:
 //   penalty on the slice (a hit mask of the history ids it owns) and the slice's (max, argmax)
 //     of l/T (of l when greedy)                                                   | barrier
-//   global max (greedy: the token, done); the slice's sum of exp(l/T - max) in float64 | barrier
-//   4 levels of 8 bisection steps: the 255 mids those 8 steps could visit are the in-order nodes
-//     of a depth-8 bisection tree below the current (lo, hi), computed with the same f32
-//     expression; every p in [lo, hi) is binned against them, p >= hi goes to an 'above' bin,
-//     and each workgroup adds its bins into one global set with integer atomics; after the
-//     barrier every workgroup replays the 8 steps from the summed bins (exact: mass(p >= mid)
-//     is 'above' plus a suffix sum of bins)                                       | barrier x 4
-//   the threshold after 32 steps; the slice's kept mass                           | barrier
+//   (the same pass) the slice's sum of exp(l/T - its own max) in float64           | barrier
+//   global max (greedy: the token, done); the normaliser sum_g s_g e^(m_g - max)
+//   the threshold: the 32 bisection steps compare mass(p >= mid) with topP, and mass(p >= m) is
+//     a non-increasing step function of m, so mass(p >= mid) < topP exactly when mid lies above
+//     p* = the largest probability whose mass(p >= p*) reaches topP: the steps' path, and the
+//     threshold lo it ends on, follow from p* alone. p* is found by radix selection on the bits
+//     of p (a p in [0, 1] has 30 significant bits): 3 levels of 10 bits, each a histogram of
+//     the masses of the candidates by their next 10 bits, summed over the workgroups with
+//     integer atomics; after the barrier every workgroup takes the highest bin whose
+//     cumulative mass from the top reaches topP                                  | barrier x 3
+//   the slice's kept mass (p >= the threshold)                                    | barrier
 //   the target and the first slice whose kept prefix reaches it; that slice's workgroup finds
 //     the id in ascending order.
 // Masses are fixed-point integers (p * 2^52, exact for p >= 2^-28) summed with integer adds, so
@@ -43,8 +46,9 @@ constexpr int kThreads = 256;
 constexpr int kPerThread = 16;
 constexpr uint32_t kSlice = kThreads * kPerThread;  // vocabulary ids per workgroup
 constexpr uint32_t kMaxGroups = 256;                // vocab <= 1,048,576 (finalize: one group per thread)
-constexpr int kBins = 256;
-constexpr int kLevels = 4;                          // 4 x 8 = 32 bisection steps
+constexpr int kRadixBits = 10;                      // bits of p selected per level
+constexpr int kBins = 1 << kRadixBits;
+constexpr int kLevels = 3;                          // 3 x 10 bits: every bit of a p in [0, 1]
 constexpr double kFix = 4503599627370496.0;         // 2^52
 
 struct SampleParams {
@@ -57,7 +61,7 @@ static_assert(sizeof(SampleParams) == 32, "sample dims are 32 bytes");
 struct Work {
   uint32_t* max_part;     // 2 u32 per group
   double* sum_part;       // 1 per group
-  unsigned long long* bins;  // kLevels x (kBins + 1), summed over groups by integer atomics
+  unsigned long long* bins;  // kLevels x kBins, summed over groups by integer atomics
   uint64_t* kept_part;    // 1 per group
   uint32_t* count_part;   // 1 per group
 };
@@ -93,37 +97,6 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* sv, u
       i = si[w];
     }
   __syncthreads();
-}
-
-// In-order mid j (0..254) of the depth-8 bisection tree below [lo, hi): the f32 mid the
-// bisection reaches when its path of left/right choices spells j.
-__device__ float tree_mid(uint32_t j, float lo, float hi) {
-  const uint32_t target = j + 1;  // 1-based in-order index, root = 128
-  uint32_t cur = 128, step = 64;
-  float mid = (lo + hi) * 0.5f;
-  while (cur != target) {
-    if (target < cur) {
-      hi = mid;
-      cur -= step;
-    } else {
-      lo = mid;
-      cur += step;
-    }
-    step >>= 1;
-    mid = (lo + hi) * 0.5f;
-  }
-  return mid;
-}
-
-// Number of mids <= v (upper bound over a non-decreasing array of kBins - 1 values).
-__device__ __forceinline__ int count_le(const float* mids, float v) {
-  int a = 0, b = kBins - 1;
-  while (a < b) {
-    const int m = (a + b) >> 1;
-    if (mids[m] <= v) a = m + 1;
-    else b = m;
-  }
-  return a;
 }
 
 // Exclusive prefix sum of one u64 per thread over the workgroup, in thread order; *total gets
@@ -202,51 +175,6 @@ __global__ void sync_reset_kernel(GridSync g) {
   }
 }
 
-// The depth-8 tree's 255 mids below [lo, hi) and the replay of its 8 bisection steps from the
-// globally summed bins of one level: (lo, hi) in, (lo, hi) out. All threads: the mids, the bins'
-// suffix sums and the mass at every tree node in parallel; then the 8-step walk reads one node
-// mass per step.
-__device__ void replay_level(const unsigned long long* summed, float top_p, float& lo, float& hi, float* mids) {
-  __shared__ unsigned long long sums[kBins + 1];
-  __shared__ unsigned long long suffix[kBins + 1];
-  __shared__ double node_mass[kBins - 1];
-  __shared__ float out_lo, out_hi;
-  if (threadIdx.x < kBins - 1) mids[threadIdx.x] = tree_mid(threadIdx.x, lo, hi);
-  for (int i = threadIdx.x; i <= kBins; i += kThreads) sums[i] = summed[i];
-  __syncthreads();
-  // suffix[k] = mass of p >= hi (sums[kBins]) plus bins k..kBins-1: total minus an exclusive
-  // prefix, so one block scan instead of a serial walk.
-  static_assert(kBins == kThreads, "one bin per thread");
-  unsigned long long total = 0;
-  const unsigned long long before = block_exclusive_scan(sums[threadIdx.x], &total);
-  suffix[threadIdx.x] = sums[kBins] + (total - before);
-  if (threadIdx.x == 0) suffix[kBins] = sums[kBins];
-  __syncthreads();
-  if (threadIdx.x < kBins - 1) node_mass[threadIdx.x] = (double)suffix[count_le(mids, mids[threadIdx.x])] / kFix;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const double top = (double)top_p;
-    float l = lo, h = hi;
-    uint32_t cur = 128, step = 64;
-    for (int s = 0; s < 8; s++) {
-      const float mid = mids[cur - 1];
-      if (node_mass[cur - 1] < top) {
-        h = mid;
-        cur -= step;
-      } else {
-        l = mid;
-        cur += step;
-      }
-      step >>= 1;
-    }
-    out_lo = l;
-    out_hi = h;
-  }
-  __syncthreads();
-  lo = out_lo;
-  hi = out_hi;
-}
-
 // ---- the launch --------------------------------------------------------------------------------
 
 // Thread t of workgroup g owns ids g * kSlice + t * kPerThread + [0, kPerThread): thread order is
@@ -298,8 +226,10 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   }
   const bool greedy = p.temperature <= 0.0f;
   {
+    // the slice's (max, argmax) of l/T (of l when greedy) and its sum of exp(l/T - that max)
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
+    __shared__ double scratch[4];
     float bv = -1.0e30f;
     uint32_t bi = greedy ? 0u : base;
 #pragma unroll
@@ -312,15 +242,23 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
       }
     }
     block_argmax(bv, bi, sv, si);
+    double s = 0.0;
+    if (!greedy) {
+#pragma unroll
+      for (int r = 0; r < kPerThread; r++)
+        if (first + r < end) s += (double)expf(v[r] / p.temperature - bv);
+      s = block_sum(s, scratch);
+    }
     if (tid == 0) {
       w.max_part[2 * g] = __float_as_uint(bv);
       w.max_part[2 * g + 1] = bi;
+      w.sum_part[g] = s;
     }
   }
   // the level bins are summed with atomics: cleared here, before the barrier that orders them
   // before any level adds to them
   if (g == 0)
-    for (int i = tid; i < kLevels * (kBins + 1); i += kThreads) w.bins[i] = 0;
+    for (int i = tid; i < kLevels * kBins; i += kThreads) w.bins[i] = 0;
   if (!grid_barrier(gs, G)) {
     if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
     return;
@@ -328,93 +266,117 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
   float mx;
   uint32_t amax;
+  float total;
   {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
-    float bv = -1.0e30f;
+    __shared__ double scratch[4];
+    float bv = -1.0e30f, mg = -1.0e30f;
     uint32_t bi = 0;
+    double sg = 0.0;
     if (tid < G) {
-      bv = __uint_as_float(w.max_part[2 * tid]);
+      bv = mg = __uint_as_float(w.max_part[2 * tid]);
       bi = w.max_part[2 * tid + 1];
+      sg = w.sum_part[tid];
     }
     block_argmax(bv, bi, sv, si);
     mx = bv;
     amax = bi;
-  }
-  if (greedy) {
-    if (g == 0 && tid == 0) out[0] = amax;
-    return;
-  }
-  // e = exp(l/T - max), kept in registers; the slice's sum in float64
-  {
-    __shared__ double scratch[4];
-    double s = 0.0;
-#pragma unroll
-    for (int r = 0; r < kPerThread; r++) {
-      v[r] = first + r < end ? expf(v[r] / p.temperature - mx) : 0.f;
-      s += (double)v[r];
+    if (greedy) {
+      if (g == 0 && tid == 0) out[0] = amax;
+      return;
     }
-    s = block_sum(s, scratch);
-    if (tid == 0) w.sum_part[g] = s;
+    // the normaliser: every slice's sum rescaled from its own max to the global one
+    total = (float)block_sum(tid < G ? sg * exp((double)mg - (double)mx) : 0.0, scratch);
   }
-  if (!grid_barrier(gs, G)) {
-    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
-    return;
-  }
-  float total;
-  {
-    __shared__ double scratch[4];
-    total = (float)block_sum(tid < G ? w.sum_part[tid] : 0.0, scratch);
-  }
-  // p in registers; ids past the vocabulary get -1 (never kept)
+  // p = exp(l/T - max) / total in registers; ids past the vocabulary get -1 (never kept)
 #pragma unroll
-  for (int r = 0; r < kPerThread; r++) v[r] = first + r < end ? v[r] / total : -1.0f;
+  for (int r = 0; r < kPerThread; r++) v[r] = first + r < end ? expf(v[r] / p.temperature - mx) / total : -1.0f;
   float thr = 0.0f;
   if (p.top_p < 1.0f) {
-    __shared__ float mids[kBins - 1];
-    __shared__ unsigned long long bins[kBins + 1];
-    float lo = 0.0f, hi = 1.0f;
-    for (int level = 0; level < kLevels; level++) {
-      if (tid < kBins - 1) mids[tid] = tree_mid(tid, lo, hi);
-      for (int i = tid; i <= kBins; i += kThreads) bins[i] = 0;
+    // p*: radix selection over the 30 significant bits of p, 10 per level. `prefix` holds the
+    // selected bits so far, `above` the mass of every p above the candidates (integer masses).
+    __shared__ unsigned long long bins[kBins];
+    __shared__ uint32_t sel;
+    __shared__ unsigned long long sel_above;
+    const double need = (double)p.top_p * kFix;
+    uint32_t prefix = 0;
+    unsigned long long above = 0;
+    // topP <= 0: every mass reaches it, so every step moves lo up (p* above everything)
+    bool found = need > 0.0;
+    if (!found) prefix = 0x7F800000u;  // +inf
+    for (int level = 0; level < kLevels && need > 0.0 && found; level++) {
+      const int shift = kRadixBits * (kLevels - 1 - level);
+      for (int i = tid; i < kBins; i += kThreads) bins[i] = 0;
+      if (tid == 0) sel = 0xFFFFFFFFu;
       __syncthreads();
-      // The mids split [lo, hi) into 256 near-equal steps, so the bin is estimated
-      // arithmetically and corrected against the exact f32 mids (usually no step). Runs of
-      // equal bins are summed in registers before the LDS atomic.
-      const float scale = (float)kBins / (hi - lo);
+      // runs of equal bins summed in registers before the LDS atomic
       int run_bin = -1;
       unsigned long long run_mass = 0;
 #pragma unroll
       for (int r = 0; r < kPerThread; r++) {
-        const float pr = v[r];
-        if (pr < lo) continue;
-        int k;
-        if (pr >= hi) {
-          k = kBins;
-        } else {
-          k = min(max((int)((pr - lo) * scale), 0), kBins - 1);  // estimate of #mids <= pr
-          while (k < kBins - 1 && mids[k] <= pr) k++;
-          while (k > 0 && mids[k - 1] > pr) k--;
-        }
+        if (!(v[r] >= 0.0f)) continue;
+        const uint32_t bits = __float_as_uint(v[r]);
+        if ((bits >> (shift + kRadixBits)) != prefix) continue;
+        const int k = (int)((bits >> shift) & (kBins - 1));
         if (k != run_bin) {
           if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);  // integer adds: order-independent
           run_bin = k;
           run_mass = 0;
         }
-        run_mass += to_fix(pr);
+        run_mass += to_fix(v[r]);
       }
       if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);
       __syncthreads();
-      unsigned long long* summed = w.bins + (size_t)level * (kBins + 1);
-      for (int i = tid; i <= kBins; i += kThreads)
+      unsigned long long* summed = w.bins + (size_t)level * kBins;
+      for (int i = tid; i < kBins; i += kThreads)
         if (bins[i]) __hip_atomic_fetch_add(&summed[i], bins[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (!grid_barrier(gs, G)) {
         if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
         return;
       }
-      replay_level(summed, p.top_p, lo, hi, mids);
+      // cum(k) = above + mass of bins >= k; the selected bin is the highest k with cum(k) >=
+      // topP (cum grows as k falls). Thread t holds bins kBins - 4 (t + 1) .. kBins - 4 t - 1,
+      // so thread order runs from the top bin down and an exclusive scan gives each thread the
+      // mass above its bins.
+      constexpr int kPer = kBins / kThreads;
+      static_assert(kBins % kThreads == 0, "whole bins per thread");
+      unsigned long long m[kPer], part = 0;
+#pragma unroll
+      for (int j = 0; j < kPer; j++) {
+        m[j] = summed[kBins - 1 - (tid * kPer + j)];  // descending bin order
+        part += m[j];
+      }
+      unsigned long long cum = above + block_exclusive_scan(part, nullptr);
+#pragma unroll
+      for (int j = 0; j < kPer; j++) {
+        const unsigned long long prev = cum;
+        cum += m[j];
+        if ((double)prev < need && (double)cum >= need) {
+          sel = (uint32_t)(kBins - 1 - (tid * kPer + j));
+          sel_above = prev;  // the mass above the selected bin
+        }
+      }
+      __syncthreads();
+      if (sel == 0xFFFFFFFFu) {
+        found = false;  // the whole mass falls short of topP (rounding): no p*, threshold 0
+      } else {
+        above = sel_above;
+        prefix = (prefix << kRadixBits) | sel;
+      }
+      __syncthreads();
     }
-    thr = lo;
+    // the 32 bisection steps: mass(p >= mid) < topP exactly when mid > p*
+    if (found || need <= 0.0) {
+      const float pstar = __uint_as_float(prefix);
+      float lo = 0.0f, hi = 1.0f;
+      for (int step = 0; step < 32; step++) {
+        const float mid = (lo + hi) * 0.5f;
+        if (mid > pstar) hi = mid;
+        else lo = mid;
+      }
+      thr = lo;
+    }
   }
   // the slice's kept mass and count
   unsigned long long mine = 0;
@@ -498,8 +460,8 @@ Work workspace(eg_context* ctx, GridSync* gs) {
   w.count_part = reinterpret_cast<uint32_t*>(part + off);
   off += (size_t)kMaxGroups * 4;
   w.bins = reinterpret_cast<unsigned long long*>(part + off);
-  off += (size_t)kLevels * (kBins + 1) * 8;
-  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * (kBins + 1) * 8 <= eg::kPartialsBytes,
+  off += (size_t)kLevels * kBins * 8;
+  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * kBins * 8 <= eg::kPartialsBytes,
                 "sampler partials exceed the workspace");
   return w;
 }
