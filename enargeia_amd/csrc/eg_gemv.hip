@@ -178,6 +178,11 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
   if (rpw * sh.u > n) return Shape{};
   const uint32_t tile_rows = rpw * sh.u;
   sh.tiles = (n + tile_rows - 1) / tile_rows;
+  // Three-slot rows (K = 4864 int4: 152 chunks) over many tiles per wave stream best with three
+  // load buffers (measured, interleaved: the 24-matrix K = 4864 launch 14.1-14.3 against
+  // 14.8-15.0 us with two); launches with a fused input stage always take two.
+  if (!(ctx && ctx->gemv_override[0]) && sh.cpl == 3 && sh.u == 1 && sh.tiles > 16u * (ctx ? (uint32_t)ctx->cu_count : 256u))
+    sh.nb = 3;
   return sh;
 }
 
@@ -298,8 +303,9 @@ int launch(eg_context* ctx, const QuantView& v) {
   uint32_t grid = 0;
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   const int in_kind = v.input ? v.input->kind : EG_INPUT_VECTOR;
-  KernelFn fn =
-      shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u, shape.nb, in_kind) : nullptr;
+  KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u,
+                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind)
+                           : nullptr;
   if (fused && !fn)
     return eg::fail(ctx, EG_ERR_INVALID,
                     "%s: no kernel for this shape with a fused input stage (k and the block must be multiples of %u)",
@@ -588,7 +594,7 @@ int eg_gemv_swiglu_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size,
   int u2 = 2;
   const uint32_t rpw = 64u / plan->team;
   if (plan->cpl > 2 || g.rows % rpw != 0) u2 = 0;
-  if (!u2 || !pick_kernel(bits, encoding, kSwiGLU, plan->team, plan->cpl, u2, plan->nb, EG_INPUT_RMSNORM)) {
+  if (!u2 || !pick_kernel(bits, encoding, kSwiGLU, plan->team, plan->cpl, u2, 2, EG_INPUT_RMSNORM)) {
     eg_gemv_plan_destroy(ctx, plan);
     return eg::fail(ctx, EG_ERR_INVALID, "%s: no SwiGLU kernel for k %u and %u rows", op, k, g.rows);
   }
@@ -629,7 +635,7 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
     return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: a SwiGLU pair takes the RMSNORM input stage");
   a.n = plan->swiglu_rows;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, pair ? kSwiGLU : kBatched, plan->team, plan->cpl, plan->u,
-                            plan->nb, a.in_kind);
+                            a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb, a.in_kind);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
