@@ -15,6 +15,12 @@
 //      the softmax weights are rounded to f16 - with f32 accumulation), the softmax is the
 //      online (running max / sum) form in f32, masked scores are the reference's NEG_LARGE.
 //      Only key tiles up to the workgroup's last query's causal limit are visited.
+//      When those workgroups would leave most CUs idle over a long key range (a late chunk of a
+//      long prompt: 4 x 14 workgroups walking up to 32 tiles at 2048 keys), the keys are split
+//      over grid.z: each split writes its rows' unnormalised o and (max, sum) to the context's
+//      workspace and 3. a combine launch merges the splits in split order.
+#include <algorithm>
+
 #include "eg_internal.hpp"
 
 namespace {
@@ -65,10 +71,17 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const float* __restric
     v_cache[(size_t)pos * d.kv_heads * kD + p] = float_to_half(v[(size_t)i * d.kv_heads * kD + p]);
 }
 
+// Split partials: o [split][query][head][kD] (unnormalised), then m and l [split][query][head].
+struct Splits {
+  float* o;          // NULL: no split, out written directly
+  uint32_t keys;     // keys per split (a multiple of kK)
+  uint32_t count;    // splits (grid.z)
+};
+
 __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q_rope,
                                                         const uint16_t* __restrict__ k_cache,
                                                         const uint16_t* __restrict__ v_cache, float* __restrict__ out,
-                                                        eg_attention_prefill_dims d) {
+                                                        eg_attention_prefill_dims d, Splits sp) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kK][kRow];     // [key][d]
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kRow];     // [d][key]
   __shared__ __attribute__((aligned(16))) uint16_t Ps[4][16][kRow];  // per wave: [query][key]
@@ -101,9 +114,14 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   }
 
   const uint32_t last_query = min(q0 + (uint32_t)kQ, d.queries) - 1;
-  const uint32_t key_end = d.query_begin + last_query + 1;  // the keys any row of this group sees
+  uint32_t key_end = d.query_begin + last_query + 1;  // the keys any row of this group sees
+  uint32_t key_begin = 0;
+  if (sp.o) {  // this split's keys
+    key_begin = blockIdx.z * sp.keys;
+    key_end = min(key_end, key_begin + sp.keys);
+  }
   const size_t pitch = (size_t)d.kv_heads * kD;             // f16 elements between cache rows
-  for (uint32_t j0 = 0; j0 < key_end; j0 += kK) {
+  for (uint32_t j0 = key_begin; j0 < key_end; j0 += kK) {
     __syncthreads();  // the previous tile's K, V and P are consumed
     {
       const uint32_t r = tid >> 2, c = (tid & 3u) * 16u;  // 64 keys x 4 pieces of 16 elements
@@ -155,10 +173,12 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
       for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
       const float mnew = fmaxf(m[e], mx);
       const float alpha = expf(m[e] - mnew);
+      // a row with no visible key yet (a split wholly past its causal limit) keeps nothing
+      const bool none = mnew == kMasked;
       float sum = 0.f;
 #pragma unroll
       for (int n = 0; n < 4; n++) {
-        const float p = expf(s[n][e] - mnew);
+        const float p = none ? 0.f : expf(s[n][e] - mnew);
         s[n][e] = p;
         sum += p;
       }
@@ -192,9 +212,41 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   for (int e = 0; e < 4; e++) {
     const uint32_t i = row0 + 4 * lg + e;
     if (i >= d.queries) continue;
+    if (sp.o) {
+      const size_t row = ((size_t)blockIdx.z * d.queries + i) * d.heads + h;
+#pragma unroll
+      for (int n = 0; n < 4; n++) sp.o[row * kD + 16 * n + lr] = o[n][e];
+      if (lr == 0) {
+        float* ml = sp.o + (size_t)sp.count * d.queries * d.heads * kD;
+        ml[row] = m[e];
+        ml[(size_t)sp.count * d.queries * d.heads + row] = l[e];
+      }
+      continue;
+    }
     const float inv = 1.0f / l[e];
 #pragma unroll
     for (int n = 0; n < 4; n++) out[((size_t)i * d.heads + h) * kD + 16 * n + lr] = o[n][e] * inv;
+  }
+}
+
+// The splits merged: out = sum_z o_z e^(m_z - M) / sum_z l_z e^(m_z - M), M = max_z m_z, splits
+// in order (an empty split has m = NEG_LARGE and l = 0, weight 0).
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                      uint32_t rows, uint32_t splits) {
+  const size_t total = (size_t)rows * kD;
+  const float* m = part + (size_t)splits * total;
+  const float* l = m + (size_t)splits * rows;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = idx / kD;
+    float M = kMasked;
+    for (uint32_t z = 0; z < splits; z++) M = fmaxf(M, m[(size_t)z * rows + row]);
+    float L = 0.f, acc = 0.f;
+    for (uint32_t z = 0; z < splits; z++) {
+      const float w = l[(size_t)z * rows + row] > 0.f ? expf(m[(size_t)z * rows + row] - M) : 0.f;
+      L = fmaf(l[(size_t)z * rows + row], w, L);
+      acc = fmaf(part[(size_t)z * total + idx], w, acc);
+    }
+    out[idx] = acc / L;
   }
 }
 
@@ -225,7 +277,28 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads over the grid limit", op, d.heads);
   hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
                      v_cache, d);
-  hipLaunchKernelGGL(attention_kernel, dim3((d.queries + kQ - 1) / kQ, d.heads), dim3(256), 0, ctx->stream, q_rope,
-                     k_cache, v_cache, out, d);
+  // Keys split where the (query block, head) grid leaves most CUs idle over a long key range:
+  // splits of at least 4 key tiles, about one workgroup per CU in all, within the workspace.
+  const uint32_t blocks = (d.queries + kQ - 1) / kQ;
+  const uint64_t grid = (uint64_t)blocks * d.heads;
+  const uint32_t tiles = (d.keys + kK - 1) / kK;
+  uint32_t splits = 1;
+  if (grid < (uint64_t)ctx->cu_count && tiles >= 8)
+    splits = (uint32_t)std::min<uint64_t>((ctx->cu_count + grid - 1) / grid, tiles / 4);
+  const uint64_t rows = (uint64_t)d.queries * d.heads;
+  while (splits > 1 && (uint64_t)splits * rows * (kD + 2) * 4 > eg::kPartialsBytes) splits--;
+  Splits sp{nullptr, 0, 1};
+  if (splits > 1) {
+    sp.keys = ((tiles + splits - 1) / splits) * kK;
+    sp.count = (d.keys + sp.keys - 1) / sp.keys;
+    sp.o = reinterpret_cast<float*>(eg::partials(ctx));
+  }
+  hipLaunchKernelGGL(attention_kernel, dim3(blocks, d.heads, sp.count), dim3(256), 0, ctx->stream, q_rope, k_cache,
+                     v_cache, out, d, sp);
+  if (sp.o) {
+    const uint64_t total = rows * kD;
+    const uint32_t cblocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);
+    hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count);
+  }
   return eg::check_launch(ctx, op);
 }

@@ -47,7 +47,11 @@ def run(device, q, k, v, kc16, vc16, begin, dims=None):
             b.release()
 
 
-@pytest.mark.parametrize("begin,n", [(0, 256), (0, 128), (300, 77), (1900, 148), (5, 1), (63, 64)])
+# (1000, 256) and (1792, 256) split their keys over grid.z (the (query block, head) grid alone
+# would leave most CUs idle): 5 and 8 splits of 256 keys, rows whose causal limit ends before a
+# split's first key (an empty split for that row) included; (1900, 148) splits into 7.
+@pytest.mark.parametrize("begin,n", [(0, 256), (0, 128), (300, 77), (1900, 148), (5, 1), (63, 64), (1000, 256),
+                                     (1792, 256)])
 def test_prefill_attention_matches_oracle(device, begin, n):
     print(f"prefill attention begin {begin} queries {n}", flush=True)
     rng = np.random.default_rng(1000 + begin + n)
