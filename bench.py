@@ -135,6 +135,9 @@ def main() -> int:
     ap.add_argument("--prompt-profile", action="store_true",
                     help="only the prompt path (eg_decoder_prefill of a 2048-token prompt as one chunk and in chunks "
                          "of 256) on the config-4 model, for rocprofv3 kernel statistics of the prompt chain")
+    ap.add_argument("--head-profile", action="store_true",
+                    help="only the config-2 LM head (fused argmax) and sampled-token calls, for rocprofv3 kernel "
+                         "statistics of the head and the sampler")
     ap.add_argument("--skip-decode", action="store_true",
                     help="leave out the config-4 decode measurement (rocprofv3 kernel tracing does not survive the "
                          "decoder's captured graph; --decode-profile covers the decode step eagerly)")
@@ -165,6 +168,11 @@ def main() -> int:
         print(json.dumps(prompt_throughput(dev, dec, QWEN25_05B)), flush=True)
         dec.close()
         dm.release()
+        dev.close()
+        return 0
+    if args.head_profile:
+        dev = K.Device(0)
+        print(json.dumps(head_numbers(dev, HipEvents(), dev.stream, args, np.random.default_rng(7))), flush=True)
         dev.close()
         return 0
     if args.decode_profile:
@@ -308,54 +316,8 @@ def main() -> int:
         for b in rep["bufs"]:
             b.release()
 
-    # ---- LM head (config 2), fused argmax, cold over 3 table replicas ----
-    table = quant.quantize_sym(quant.normal(VOCAB * HIDDEN, 0x5EED ^ 0x1000, 0.02), VOCAB, HIDDEN, 8, HIDDEN)
-    heads = [(dev.upload(table.packed), dev.upload(table.scales)) for _ in range(3)]
-    del table
-    h = dev.upload(rng.standard_normal(HIDDEN, dtype=np.float32))
-    logits = dev.buffer(VOCAB * 4)
-    res = dev.buffer(8)
-    dims = K.embedding_dims(1, HIDDEN, 0, VOCAB, HIDDEN, VOCAB, 0)
-    for i in range(args.warmup):
-        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
-    hs = [ev.create() for _ in range(args.steps + 1)]
-    ev.record(hs[0], stream)
-    for i in range(args.steps):
-        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
-        ev.record(hs[i + 1], stream)
-    ev.sync(hs[-1])
-    head_times = [ev.ms(hs[i], hs[i + 1]) for i in range(args.steps)]
-    head_us = float(np.median(head_times)) * 1e3
-    head_gbs = LM_HEAD_BYTES / (head_us * 1e-6) / 1e9
-    log(f"lm_head+argmax: {head_us:.1f} us, {head_gbs:.0f} GB/s cold")
-
-    # sampled token (config 2: T 0.7, top-p 0.9, penalty 1.1 over 512 ids): LM head + sampler
-    smp = K.ComputeKernel(dev, K.SAMPLE)
-    hist = dev.upload(rng.integers(0, VOCAB, 512).astype(np.uint32))
-    tok = dev.buffer(16)
-    head_k = K.ComputeKernel(dev, K.embedding_head_spec("q8", K.ENC_SIGNED))
-
-    def sampled_token(i):
-        hu = head_k.uniform()
-        hu.write(dims)
-        head_k.encode(head_k.bind_group([h, heads[i % 3][0], heads[i % 3][1], None, logits, hu]), (1, 1, 1))
-        su = smp.uniform()
-        su.write(K.sample_dims(VOCAB, 512, K.SamplingParams(0.7, 0.9, 1.1), (i * 0.618) % 1.0))
-        smp.encode(smp.bind_group([logits, hist, tok, su]), (1, 1, 1))
-
-    for i in range(args.warmup):
-        sampled_token(i)
-    ss2 = [ev.create() for _ in range(args.steps + 1)]
-    ev.record(ss2[0], stream)
-    for i in range(args.steps):
-        sampled_token(i)
-        ev.record(ss2[i + 1], stream)
-    ev.sync(ss2[-1])
-    sampled_us = float(np.median([ev.ms(ss2[i], ss2[i + 1]) for i in range(args.steps)])) * 1e3
-    log(f"lm_head+sample (T 0.7, top-p 0.9, penalty 1.1): {sampled_us:.1f} us")
-    for a, b in heads:
-        a.release()
-        b.release()
+    hn = head_numbers(dev, ev, stream, args, rng)
+    head_us, head_gbs, sampled_us = hn["us"], hn["gbs"], hn["sampled_us"]
 
     # ---- prefill chunk (config 3) ----
     prefill = prefill_numbers(dev, ev, stream, args)
@@ -437,6 +399,65 @@ def verify_decode_tokens(tokens: list, first_step: int) -> dict:
     return {"oracle": "tests/golden/config4_decode.npz", "compared": compared, "mismatches": mismatches,
             "near_ties": near_ties, "diverged_at_near_tie": diverged_at,
             "verified": mismatches == 0}
+
+
+def head_numbers(dev, ev, stream, args, rng) -> dict:
+    """the 151,936 x 896 int8 tied head with the fused greedy argmax (its
+    finalize launch included), cold over 3 table replicas, and the sampled token (the head storing
+    logits, then the sampler at T 0.7 / top-p 0.9 / penalty 1.1 over a 512-id history): the median
+    time between events recorded after each of back-to-back calls."""
+    from enargeia_amd import kernels as K
+    from enargeia_amd import quant
+
+    # ---- LM head (config 2), fused argmax, cold over 3 table replicas ----
+    table = quant.quantize_sym(quant.normal(VOCAB * HIDDEN, 0x5EED ^ 0x1000, 0.02), VOCAB, HIDDEN, 8, HIDDEN)
+    heads = [(dev.upload(table.packed), dev.upload(table.scales)) for _ in range(3)]
+    del table
+    h = dev.upload(rng.standard_normal(HIDDEN, dtype=np.float32))
+    logits = dev.buffer(VOCAB * 4)
+    res = dev.buffer(8)
+    dims = K.embedding_dims(1, HIDDEN, 0, VOCAB, HIDDEN, VOCAB, 0)
+    for i in range(args.warmup):
+        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
+    hs = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(hs[0], stream)
+    for i in range(args.steps):
+        K.lm_head_argmax(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, res, dims, 8, K.ENC_SIGNED)
+        ev.record(hs[i + 1], stream)
+    ev.sync(hs[-1])
+    head_times = [ev.ms(hs[i], hs[i + 1]) for i in range(args.steps)]
+    head_us = float(np.median(head_times)) * 1e3
+    head_gbs = LM_HEAD_BYTES / (head_us * 1e-6) / 1e9
+    log(f"lm_head+argmax: {head_us:.1f} us, {head_gbs:.0f} GB/s cold")
+
+    # sampled token (config 2: T 0.7, top-p 0.9, penalty 1.1 over 512 ids): LM head + sampler
+    smp = K.ComputeKernel(dev, K.SAMPLE)
+    hist = dev.upload(rng.integers(0, VOCAB, 512).astype(np.uint32))
+    tok = dev.buffer(16)
+    head_k = K.ComputeKernel(dev, K.embedding_head_spec("q8", K.ENC_SIGNED))
+
+    def sampled_token(i):
+        hu = head_k.uniform()
+        hu.write(dims)
+        head_k.encode(head_k.bind_group([h, heads[i % 3][0], heads[i % 3][1], None, logits, hu]), (1, 1, 1))
+        su = smp.uniform()
+        su.write(K.sample_dims(VOCAB, 512, K.SamplingParams(0.7, 0.9, 1.1), (i * 0.618) % 1.0))
+        smp.encode(smp.bind_group([logits, hist, tok, su]), (1, 1, 1))
+
+    for i in range(args.warmup):
+        sampled_token(i)
+    ss2 = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(ss2[0], stream)
+    for i in range(args.steps):
+        sampled_token(i)
+        ev.record(ss2[i + 1], stream)
+    ev.sync(ss2[-1])
+    sampled_us = float(np.median([ev.ms(ss2[i], ss2[i + 1]) for i in range(args.steps)])) * 1e3
+    log(f"lm_head+sample (T 0.7, top-p 0.9, penalty 1.1): {sampled_us:.1f} us")
+    for a, b in heads:
+        a.release()
+        b.release()
+    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us}
 
 
 def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:

@@ -12,14 +12,13 @@
 //     running kept mass reaches the target (:266-321); argmax fallback (:324-331).
 //
 // MI355X design. The reference makes ~36 passes over the vocabulary inside one workgroup. Here
-// the vocabulary is split over G workgroups (4096 ids each, G = 38 at 151,936 ids) that are all
+// the vocabulary is split over G workgroups (2048 ids each, G = 75 at 151,936 ids) that are all
 // resident at once, and the whole sample is ONE launch whose phases are separated by grid
 // barriers (a central counter with a generation word, agent-scope release/acquire; every wait
 // bounded): each workgroup loads its slice's logits once and keeps them - and later their
 // probabilities - in registers through every phase:
-//   penalty on the slice (a hit mask of the history ids it owns) and the slice's (max, argmax)
-//     of l/T (of l when greedy)                                                   | barrier
-//   (the same pass) the slice's sum of exp(l/T - its own max) in float64           | barrier
+//   penalty on the slice (a hit mask of the history ids it owns), the slice's (max, argmax)
+//     of l/T (of l when greedy) and its sum of exp(l/T - its own max) in float64   | barrier
 //   global max (greedy: the token, done); the normaliser sum_g s_g e^(m_g - max)
 //   the threshold: the 32 bisection steps compare mass(p >= mid) with topP, and mass(p >= m) is
 //     a non-increasing step function of m, so mass(p >= mid) < topP exactly when mid lies above
@@ -29,7 +28,11 @@
 //     the masses of the candidates by their next 10 bits, summed over the workgroups with
 //     integer atomics; after the barrier every workgroup takes the highest bin whose
 //     cumulative mass from the top reaches topP                                  | barrier x 3
-//   the slice's kept mass (p >= the threshold)                                    | barrier
+//   the slices' kept masses (p >= the threshold): the last level also publishes each slice's
+//     mass above its candidate range and lists the candidates themselves (up to 32 per slice),
+//     so when the threshold shares the candidates' prefix every workgroup derives them with no
+//     further barrier; otherwise (top-p 1, ties filling the list) each slice sums its own
+//                                                                                  | barrier
 //   the target and the first slice whose kept prefix reaches it; that slice's workgroup finds
 //     the id in ascending order.
 // Masses are fixed-point integers (p * 2^52, exact for p >= 2^-28) summed with integer adds, so
@@ -43,9 +46,10 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerThread = 16;
+constexpr int kPerThread = 8;
+constexpr int kWaves = kThreads / 64;
 constexpr uint32_t kSlice = kThreads * kPerThread;  // vocabulary ids per workgroup
-constexpr uint32_t kMaxGroups = 256;                // vocab <= 1,048,576 (finalize: one group per thread)
+constexpr uint32_t kMaxGroups = 256;                // vocab <= 524,288 (one group per thread in the final scan)
 constexpr int kRadixBits = 10;                      // bits of p selected per level
 constexpr int kBins = 1 << kRadixBits;
 constexpr int kLevels = 3;                          // 3 x 10 bits: every bit of a p in [0, 1]
@@ -58,12 +62,18 @@ struct SampleParams {
 };
 static_assert(sizeof(SampleParams) == 32, "sample dims are 32 bytes");
 
+constexpr uint32_t kCand = 32;  // candidates of the last radix level kept per group
+
 struct Work {
   uint32_t* max_part;     // 2 u32 per group
   double* sum_part;       // 1 per group
   unsigned long long* bins;  // kLevels x kBins, summed over groups by integer atomics
   uint64_t* kept_part;    // 1 per group
   uint32_t* count_part;   // 1 per group
+  uint64_t* above_part;   // 1 per group: mass above the last level's candidate range
+  uint32_t* above_count;  // 1 per group: ids above it
+  uint32_t* cand_count;   // 1 per group: ids inside it (only the first kCand are stored)
+  uint2* cand;            // kCand per group: (id, bits of p)
 };
 
 __device__ __forceinline__ uint64_t to_fix(float p) { return (uint64_t)__double2ull_rn((double)p * kFix); }
@@ -76,7 +86,7 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
   __syncthreads();
   T r = scratch[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / 64; w++) r += scratch[w];
+  for (int w = 1; w < kWaves; w++) r += scratch[w];
   __syncthreads();
   return r;
 }
@@ -91,7 +101,7 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* sv, u
   v = sv[0];
   i = si[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / 64; w++)
+  for (int w = 1; w < kWaves; w++)
     if (egd::better(sv[w], si[w], v, i)) {
       v = sv[w];
       i = si[w];
@@ -100,9 +110,9 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i, float* sv, u
 }
 
 // Exclusive prefix sum of one u64 per thread over the workgroup, in thread order; *total gets
-// the sum of all. Wave scan by shuffles, then the four wave totals.
+// the sum of all. Wave scan by shuffles, then the wave totals.
 __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigned long long* total) {
-  __shared__ unsigned long long wsum[kThreads / 64];
+  __shared__ unsigned long long wsum[kWaves];
   const int lane = threadIdx.x & 63;
   unsigned long long incl = v;
 #pragma unroll
@@ -114,7 +124,7 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
   __syncthreads();
   unsigned long long before = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < kThreads / 64; w++) {
+  for (int w = 0; w < kWaves; w++) {
     if (w < (int)(threadIdx.x >> 6)) before += wsum[w];
     all += wsum[w];
   }
@@ -135,6 +145,7 @@ struct GridSync {
   uint32_t* count;  // arrivals at the current barrier (0 between barriers)
   uint32_t* gen;    // advanced once per completed barrier
   uint32_t* abort;  // set by a timed-out wait
+  uint32_t* exits;  // workgroups done with every barrier of the current launch
 };
 
 __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
@@ -159,19 +170,31 @@ __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (!good) __hip_atomic_store(g.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!good) {
+      __hip_atomic_store(g.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // ordered before this workgroup's exit count
+    }
     ok = good ? 1u : 0u;
   }
   __syncthreads();
   return ok != 0u;
 }
 
-// Sets the barrier's words for the next launch (a kernel, not a memset, so a captured graph
-// replays it): a sample launch never starts from a count left by an aborted one.
-__global__ void sync_reset_kernel(GridSync g) {
+// Called by every workgroup once it has passed its last barrier or given up: the last to leave
+// returns the words to their starting state, so the next launch needs no reset launch before it
+// and never starts from a count or an abort flag left by an aborted one (the context's state
+// starts zeroed). The exit count is relaxed: a workgroup that raised the abort flag released it
+// first, and only the last workgroup acquires, so the common path adds one atomic and no L2
+// writeback.
+__device__ void leave(const GridSync& g, uint32_t groups) {
   if (threadIdx.x == 0) {
-    *g.count = 0u;
-    *g.abort = 0u;
+    const uint32_t left = __hip_atomic_fetch_add(g.exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (left == groups - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(g.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(g.abort, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(g.exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -179,9 +202,9 @@ __global__ void sync_reset_kernel(GridSync g) {
 
 // Thread t of workgroup g owns ids g * kSlice + t * kPerThread + [0, kPerThread): thread order is
 // id order, which the final scan relies on.
-__global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const uint32_t* history, uint32_t* out,
-                                                          SampleParams hp, SampleParams* dp, Work w, GridSync gs,
-                                                          uint32_t* rng) {
+// Every return is taken by a whole workgroup at once.
+__device__ __forceinline__ void sample_phases(float* logits, const uint32_t* history, uint32_t* out, SampleParams hp,
+                                              SampleParams* dp, const Work& w, const GridSync& gs, uint32_t* rng) {
   const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
   // This call's draw (one per sampled step, Session.decodeStep session.ts:351): taken by
   // workgroup 0 before the first barrier, read by everyone after it.
@@ -227,9 +250,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   const bool greedy = p.temperature <= 0.0f;
   {
     // the slice's (max, argmax) of l/T (of l when greedy) and its sum of exp(l/T - that max)
-    __shared__ float sv[4];
-    __shared__ uint32_t si[4];
-    __shared__ double scratch[4];
+    __shared__ float sv[kWaves];
+    __shared__ uint32_t si[kWaves];
+    __shared__ double scratch[kWaves];
     float bv = -1.0e30f;
     uint32_t bi = greedy ? 0u : base;
 #pragma unroll
@@ -268,9 +291,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   uint32_t amax;
   float total;
   {
-    __shared__ float sv[4];
-    __shared__ uint32_t si[4];
-    __shared__ double scratch[4];
+    __shared__ float sv[kWaves];
+    __shared__ uint32_t si[kWaves];
+    __shared__ double scratch[kWaves];
     float bv = -1.0e30f, mg = -1.0e30f;
     uint32_t bi = 0;
     double sg = 0.0;
@@ -293,6 +316,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
 #pragma unroll
   for (int r = 0; r < kPerThread; r++) v[r] = first + r < end ? expf(v[r] / p.temperature - mx) / total : -1.0f;
   float thr = 0.0f;
+  // thread t < G: group t's mass and count above the last level's candidate range, and the
+  // number of its candidates
+  unsigned long long g_above = 0;
+  uint32_t g_above_n = 0, g_cand_n = 0;
+  bool listed = false;  // the kept set is the ids above the candidate range + listed candidates
   if (p.top_p < 1.0f) {
     // p*: radix selection over the 30 significant bits of p, 10 per level. `prefix` holds the
     // selected bits so far, `above` the mass of every p above the candidates (integer masses).
@@ -300,24 +328,46 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
     __shared__ uint32_t sel;
     __shared__ unsigned long long sel_above;
     const double need = (double)p.top_p * kFix;
-    uint32_t prefix = 0;
+    uint32_t prefix = 0, cand_prefix = 0;
     unsigned long long above = 0;
+    bool last_done = false;  // the last level ran: its candidates and masses above were published
     // topP <= 0: every mass reaches it, so every step moves lo up (p* above everything)
     bool found = need > 0.0;
     if (!found) prefix = 0x7F800000u;  // +inf
     for (int level = 0; level < kLevels && need > 0.0 && found; level++) {
       const int shift = kRadixBits * (kLevels - 1 - level);
+      const bool last = level == kLevels - 1;
+      __shared__ unsigned long long above_g;
+      __shared__ uint32_t above_n, cand_n;
       for (int i = tid; i < kBins; i += kThreads) bins[i] = 0;
-      if (tid == 0) sel = 0xFFFFFFFFu;
+      if (tid == 0) {
+        sel = 0xFFFFFFFFu;
+        above_g = 0;
+        above_n = 0;
+        cand_n = 0;
+      }
       __syncthreads();
       // runs of equal bins summed in registers before the LDS atomic
       int run_bin = -1;
-      unsigned long long run_mass = 0;
+      unsigned long long run_mass = 0, up_mass = 0;
+      uint32_t up_n = 0;
 #pragma unroll
       for (int r = 0; r < kPerThread; r++) {
         if (!(v[r] >= 0.0f)) continue;
         const uint32_t bits = __float_as_uint(v[r]);
-        if ((bits >> (shift + kRadixBits)) != prefix) continue;
+        if ((bits >> (shift + kRadixBits)) != prefix) {
+          // the last level also counts what lies above its range and lists its candidates, so
+          // the slices' kept masses follow from the selection without another barrier
+          if (last && (bits >> (shift + kRadixBits)) > prefix) {
+            up_mass += to_fix(v[r]);
+            up_n++;
+          }
+          continue;
+        }
+        if (last) {
+          const uint32_t slot = atomicAdd(&cand_n, 1u);
+          if (slot < kCand) w.cand[(size_t)g * kCand + slot] = make_uint2(first + r, bits);
+        }
         const int k = (int)((bits >> shift) & (kBins - 1));
         if (k != run_bin) {
           if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);  // integer adds: order-independent
@@ -327,13 +377,39 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
         run_mass += to_fix(v[r]);
       }
       if (run_bin >= 0) atomicAdd(&bins[run_bin], run_mass);
+      if (last) {
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) {
+          up_mass += __shfl_xor(up_mass, m, 64);
+          up_n += __shfl_xor(up_n, m, 64);
+        }
+        if ((tid & 63) == 0 && up_n) {
+          atomicAdd(&above_g, up_mass);
+          atomicAdd(&above_n, up_n);
+        }
+      }
       __syncthreads();
       unsigned long long* summed = w.bins + (size_t)level * kBins;
       for (int i = tid; i < kBins; i += kThreads)
         if (bins[i]) __hip_atomic_fetch_add(&summed[i], bins[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last && tid == 0) {
+        w.above_part[g] = above_g;
+        w.above_count[g] = above_n;
+        w.cand_count[g] = cand_n;
+      }
       if (!grid_barrier(gs, G)) {
         if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
         return;
+      }
+      if (last) {
+        // every group's figures for the kept masses below (loaded here, beside the bins)
+        last_done = true;
+        cand_prefix = prefix;
+        if (tid < G) {
+          g_above = w.above_part[tid];
+          g_above_n = w.above_count[tid];
+          g_cand_n = w.cand_count[tid];
+        }
       }
       // cum(k) = above + mass of bins >= k; the selected bin is the highest k with cum(k) >=
       // topP (cum grows as k falls). Thread t holds bins kBins - 4 (t + 1) .. kBins - 4 t - 1,
@@ -377,6 +453,12 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
       }
       thr = lo;
     }
+    // When thr has the candidates' prefix, every id above their range is kept, every id below
+    // it is not, and the candidates are decided one by one: the slices' kept masses come from
+    // the published figures. Otherwise (thr from a failed selection, or a group with more
+    // candidates than it stored) they are summed and exchanged through one more barrier.
+    listed = last_done && found && (__float_as_uint(thr) >> kRadixBits) >= cand_prefix;
+    listed = !__syncthreads_or(!listed || (tid < G && g_cand_n > kCand));
   }
   // the slice's kept mass and count
   unsigned long long mine = 0;
@@ -387,19 +469,37 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
       mine += to_fix(v[r]);
       cnt++;
     }
-  {
-    __shared__ unsigned long long ks[4];
-    __shared__ uint32_t cs[4];
+  unsigned long long gk = 0;
+  uint32_t gc = 0;
+  if (listed) {
+    if (tid < G) {
+      gk = g_above;
+      gc = g_above_n;
+      for (uint32_t c = 0; c < g_cand_n; c++) {
+        const float pc = __uint_as_float(w.cand[(size_t)tid * kCand + c].y);
+        if (pc >= thr) {
+          gk += to_fix(pc);
+          gc++;
+        }
+      }
+    }
+  } else {
+    __shared__ unsigned long long ks[kWaves];
+    __shared__ uint32_t cs[kWaves];
     const unsigned long long kept = block_sum(mine, ks);
     const uint32_t count = block_sum(cnt, cs);
     if (tid == 0) {
       w.kept_part[g] = kept;
       w.count_part[g] = count;
     }
-  }
-  if (!grid_barrier(gs, G)) {
-    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
-    return;
+    if (!grid_barrier(gs, G)) {
+      if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
+      return;
+    }
+    if (tid < G) {
+      gk = w.kept_part[tid];
+      gc = w.count_part[tid];
+    }
   }
   // Kept mass per slice in id order: the target, then the first slice whose inclusive prefix
   // reaches it (and that keeps something, so a zero target still lands on a kept id). Every
@@ -408,8 +508,6 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   __shared__ uint32_t pick_group, pick;
   __shared__ unsigned long long group_prefix;
   unsigned long long all = 0;
-  const unsigned long long gk = tid < G ? w.kept_part[tid] : 0ull;
-  const uint32_t gc = tid < G ? w.count_part[tid] : 0u;
   const unsigned long long gbefore = block_exclusive_scan(gk, &all);
   double kd = (double)all / kFix;
   if (kd < 1.0e-20) kd = 1.0e-20;
@@ -443,12 +541,20 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
   if (tid == 0) out[0] = pick != 0xFFFFFFFFu ? pick : amax;
 }
 
+__global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const uint32_t* history, uint32_t* out,
+                                                          SampleParams hp, SampleParams* dp, Work w, GridSync gs,
+                                                          uint32_t* rng) {
+  sample_phases(logits, history, out, hp, dp, w, gs, rng);
+  leave(gs, gridDim.x);
+}
+
 Work workspace(eg_context* ctx, GridSync* gs) {
   Work w;
-  uint32_t* sync = reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048);  // three words, 128 bytes apart
+  uint32_t* sync = reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048);  // four words, 128 bytes apart
   gs->count = sync;
   gs->gen = sync + 32;
   gs->abort = sync + 64;
+  gs->exits = sync + 96;
   uint8_t* part = eg::partials(ctx);
   size_t off = 0;
   w.max_part = reinterpret_cast<uint32_t*>(part + off);
@@ -461,19 +567,26 @@ Work workspace(eg_context* ctx, GridSync* gs) {
   off += (size_t)kMaxGroups * 4;
   w.bins = reinterpret_cast<unsigned long long*>(part + off);
   off += (size_t)kLevels * kBins * 8;
-  static_assert((size_t)kMaxGroups * 28 + (size_t)kLevels * kBins * 8 <= eg::kPartialsBytes,
+  w.above_part = reinterpret_cast<uint64_t*>(part + off);
+  off += (size_t)kMaxGroups * 8;
+  w.above_count = reinterpret_cast<uint32_t*>(part + off);
+  off += (size_t)kMaxGroups * 4;
+  w.cand_count = reinterpret_cast<uint32_t*>(part + off);
+  off += (size_t)kMaxGroups * 4;
+  w.cand = reinterpret_cast<uint2*>(part + off);
+  off += (size_t)kMaxGroups * kCand * 8;
+  static_assert((size_t)kMaxGroups * (44 + kCand * 8) + (size_t)kLevels * kBins * 8 <= eg::kPartialsBytes,
                 "sampler partials exceed the workspace");
   return w;
 }
 
-// The barrier reset, then the sample launch (all its workgroups must be resident at once:
-// G <= kMaxGroups = 256 workgroups of 256 threads and ~12 KB of LDS each fit the device).
+// One launch (all its workgroups must be resident at once: G <= kMaxGroups = 256 workgroups of
+// 256 threads and ~12 KB of LDS each fit the device).
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
            SampleParams* dp, uint32_t* rng = nullptr) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
   GridSync gs;
   Work w = workspace(ctx, &gs);
-  hipLaunchKernelGGL(sync_reset_kernel, dim3(1), dim3(64), 0, ctx->stream, gs);
   hipLaunchKernelGGL(sample_kernel, dim3(groups), dim3(kThreads), 0, ctx->stream, logits, history, out, hp, dp, w, gs,
                      rng);
   return eg::check_launch(ctx, "sample");

@@ -205,7 +205,7 @@ EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const 
  * occurrence of each id in history[0..history_length), then greedy argmax (temperature <= 0)
  * or temperature / top-p (threshold bisection, 32 steps) / draw at `random` in ascending id
  * order, with the argmax fallback. out[0] = the token id. One launch whose workgroups (one per
- * 4096 ids) must all be resident at once; should one never start (the device shared with other
+ * 2048 ids, vocab <= 524,288) must all be resident at once; should one never start (the device shared with other
  * work), the launch's bounded waits give up and out[0] = 0xFFFFFFFF. Calls that overlap on one
  * context race (they share its workspace). */
 EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,

@@ -139,6 +139,17 @@ def test_peaked_distribution_matches_oracle(device):
     assert c >= 12 and e >= 14
 
 
+def test_tied_logits_match_oracle(device):
+    # Logits on four levels: the nucleus boundary falls on a class of ~38,000 equal p, so every
+    # slice holds far more ids with p* than the last radix level lists one by one, and the kept
+    # masses take the summed path (the peaked and flat cases take the listed one).
+    rng = np.random.default_rng(21)
+    logits = (rng.integers(0, 4, VOCAB) * 0.75).astype(np.float32)
+    draws = [float(x) for x in rng.random(8)]
+    c, e = _compare(device, logits, np.zeros(0, np.uint32), K.SamplingParams(0.7, 0.6, 1.0), draws, "tied")
+    assert e >= 7
+
+
 @pytest.mark.parametrize("vocab", [1, 1000, 1024, 1025, 70001])
 def test_ragged_vocab_sizes(device, vocab):
     logits = oracle.normal_floats(vocab, vocab, 2.5)
