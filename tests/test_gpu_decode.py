@@ -407,3 +407,28 @@ def test_swiglu_pair_rejects_bad_pairs(device):
     st = lib().eg_gemv_plan_launch_input(device.ctx, h, ctypes.byref(inp))
     assert st == _lib.EG_ERR_INVALID and b"RMSNORM" in lib().eg_last_error(device.ctx)
     _lib.check(lib().eg_gemv_plan_destroy(device.ctx, h), device.ctx)
+
+
+def test_decode_advance_appends_history_until_capacity(device):
+    # eg_decode_advance (Session.decodeStep's bookkeeping, session.ts:347-375): the position
+    # moves on every call; the token joins the history while it has room, then the history
+    # stays as it is; without a history only the position moves.
+    vp = ctypes.c_void_p
+    pos = device.upload(np.array([5], np.uint32))
+    hist = device.upload(np.array([1, 2, 3, 0], np.uint32))
+    hlen = device.upload(np.array([3], np.uint32))
+    tok = device.upload(np.array([42], np.uint32))
+    try:
+        for _ in range(2):
+            _lib.check(lib().eg_decode_advance(device.ctx, vp(pos.ptr), vp(hist.ptr), vp(hlen.ptr), vp(tok.ptr), 4),
+                       device.ctx)
+        assert device.read_array(pos, np.uint32, 1).tolist() == [7]
+        assert device.read_array(hist, np.uint32, 4).tolist() == [1, 2, 3, 42]
+        assert device.read_array(hlen, np.uint32, 1).tolist() == [4]
+        _lib.check(lib().eg_decode_advance(device.ctx, vp(pos.ptr), None, None, vp(tok.ptr), 0), device.ctx)
+        assert device.read_array(pos, np.uint32, 1).tolist() == [8]
+        st = lib().eg_decode_advance(device.ctx, vp(pos.ptr), vp(hist.ptr), None, vp(tok.ptr), 4)
+        assert st == _lib.EG_ERR_INVALID and b"go together" in lib().eg_last_error(device.ctx)
+    finally:
+        for b in (pos, hist, hlen, tok):
+            b.release()
