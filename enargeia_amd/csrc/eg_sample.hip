@@ -14,9 +14,10 @@
 // MI355X design. The reference makes ~36 passes over the vocabulary inside one workgroup. Here
 // the vocabulary is split over G workgroups (2048 ids each, G = 75 at 151,936 ids) that are all
 // resident at once, and the whole sample is ONE launch whose phases are separated by grid
-// barriers (a central counter with a generation word, agent-scope release/acquire; every wait
-// bounded): each workgroup loads its slice's logits once and keeps them - and later their
-// probabilities - in registers through every phase:
+// barriers (a central counter with a generation word; every wait bounded; what workgroups hand
+// each other moves through device-coherent accesses, so a barrier only drains stores and needs
+// no cache write-back or invalidate): each workgroup loads its slice's logits once and keeps
+// them - and later their probabilities - in registers through every phase:
 //   penalty on the slice (a hit mask of the history ids it owns), the slice's (max, argmax)
 //     of l/T (of l when greedy) and its sum of exp(l/T - its own max) in float64   | barrier
 //   global max (greedy: the token, done); the normaliser sum_g s_g e^(m_g - max)
@@ -73,7 +74,7 @@ struct Work {
   uint64_t* above_part;   // 1 per group: mass above the last level's candidate range
   uint32_t* above_count;  // 1 per group: ids above it
   uint32_t* cand_count;   // 1 per group: ids inside it (only the first kCand are stored)
-  uint2* cand;            // kCand per group: (id, bits of p)
+  unsigned long long* cand;  // kCand per group: bits of p << 32 | id
 };
 
 __device__ __forceinline__ uint64_t to_fix(float p) { return (uint64_t)__double2ull_rn((double)p * kFix); }
@@ -133,12 +134,43 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
   return before + incl - v;
 }
 
-// ---- grid barrier --------------------------------------------------------------------------
+// ---- cross-workgroup data and the grid barrier -----------------------------------------------
 
-// Central barrier over the launch's workgroups: thread 0 of each releases the workgroup's writes
-// at agent scope and counts itself; the last to arrive resets the count and advances the
-// generation, which the others poll (acquire). Polls are bounded: past kSpin, or when another
-// workgroup has given up, the abort flag is raised and false is returned to every thread.
+// Everything one workgroup hands another inside the launch moves through device-coherent
+// accesses: agent-scope atomic stores and loads (the sc1 bit on gfx950), which write through and
+// read past the XCD-private caching of ordinary accesses - the same instructions the agent-scope
+// atomics of the memory model use. The only thing a barrier then has to order is that every such
+// store of a workgroup has completed before the workgroup is counted: each wave drains its
+// stores (vmcnt 0) before the workgroup's s_barrier, and thread 0 counts it after. No L2
+// write-back or invalidate is needed (the release/acquire fences that do them cost ~2.5 us per
+// barrier here), and no ordinary load ever reads data another workgroup wrote in this launch.
+template <typename T>
+__device__ __forceinline__ void put(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T get(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_f64(double* p, double v) {
+  put(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v));
+}
+__device__ __forceinline__ double get_f64(const double* p) {
+  return __builtin_bit_cast(double, get(reinterpret_cast<const unsigned long long*>(p)));
+}
+// This wave's memory operations issued so far complete before any issued after (the compiler
+// keeps them on their side of it: a signal fence on each side of the wait).
+__device__ __forceinline__ void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0 (loads and stores), expcnt 7, lgkmcnt 15
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Central barrier over the launch's workgroups: thread 0 of each counts the workgroup once its
+// waves have drained their stores; the last to arrive resets the count and, once that store
+// has completed, advances the generation, which the others poll. Polls are bounded: past kSpin,
+// or when another workgroup has given up, the abort flag is raised and false is returned to
+// every thread.
 constexpr uint32_t kSpin = 1u << 20;  // polls of ~1 us: a barrier gives up after about a second
 
 struct GridSync {
@@ -150,29 +182,30 @@ struct GridSync {
 
 __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
   __shared__ uint32_t ok;
+  drain();
   __syncthreads();
   if (threadIdx.x == 0) {
     bool good = true;
-    const uint32_t gen0 = __hip_atomic_load(g.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t gen0 = get(g.gen);
+    drain();  // the generation read before this workgroup can complete the barrier
     const uint32_t arrived = __hip_atomic_fetch_add(g.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (arrived == groups - 1) {
-      __hip_atomic_store(g.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(g.gen, gen0 + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      put(g.count, 0u);
+      drain();
+      put(g.gen, gen0 + 1u);
     } else {
       uint32_t n = 0;
-      while (__hip_atomic_load(g.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen0) {
-        if (__hip_atomic_load(g.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u || ++n > kSpin) {
+      while (get(g.gen) == gen0) {
+        if (get(g.abort) != 0u || ++n > kSpin) {
           good = false;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (!good) {
-      __hip_atomic_store(g.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // ordered before this workgroup's exit count
+      put(g.abort, 1u);
+      drain();  // completed before this workgroup's exit count
     }
     ok = good ? 1u : 0u;
   }
@@ -183,17 +216,15 @@ __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
 // Called by every workgroup once it has passed its last barrier or given up: the last to leave
 // returns the words to their starting state, so the next launch needs no reset launch before it
 // and never starts from a count or an abort flag left by an aborted one (the context's state
-// starts zeroed). The exit count is relaxed: a workgroup that raised the abort flag released it
-// first, and only the last workgroup acquires, so the common path adds one atomic and no L2
-// writeback.
+// starts zeroed; a workgroup that raised the abort flag drained that store before counting its
+// exit).
 __device__ void leave(const GridSync& g, uint32_t groups) {
   if (threadIdx.x == 0) {
     const uint32_t left = __hip_atomic_fetch_add(g.exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (left == groups - 1) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(g.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(g.abort, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(g.exits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      put(g.count, 0u);
+      put(g.abort, 0u);
+      put(g.exits, 0u);
     }
   }
 }
@@ -208,7 +239,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
   const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
   // This call's draw (one per sampled step, Session.decodeStep session.ts:351): taken by
   // workgroup 0 before the first barrier, read by everyone after it.
-  if (rng && dp && g == 0 && tid == 0) dp->random = egd::mulberry32_next(rng);
+  if (rng && dp && g == 0 && tid == 0) put(&dp->random, egd::mulberry32_next(rng));
   SampleParams p = dp ? *dp : hp;  // `random` is read again after the first barrier (below)
   const uint32_t base = g * kSlice, first = base + tid * kPerThread;
   const uint32_t end = min(base + kSlice, p.vocab);
@@ -273,15 +304,15 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       s = block_sum(s, scratch);
     }
     if (tid == 0) {
-      w.max_part[2 * g] = __float_as_uint(bv);
-      w.max_part[2 * g + 1] = bi;
-      w.sum_part[g] = s;
+      put(&w.max_part[2 * g], __float_as_uint(bv));
+      put(&w.max_part[2 * g + 1], bi);
+      put_f64(&w.sum_part[g], s);
     }
   }
   // the level bins are summed with atomics: cleared here, before the barrier that orders them
   // before any level adds to them
   if (g == 0)
-    for (int i = tid; i < kLevels * kBins; i += kThreads) w.bins[i] = 0;
+    for (int i = tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
   if (!grid_barrier(gs, G)) {
     if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
     return;
@@ -298,9 +329,9 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
     uint32_t bi = 0;
     double sg = 0.0;
     if (tid < G) {
-      bv = mg = __uint_as_float(w.max_part[2 * tid]);
-      bi = w.max_part[2 * tid + 1];
-      sg = w.sum_part[tid];
+      bv = mg = __uint_as_float(get(&w.max_part[2 * tid]));
+      bi = get(&w.max_part[2 * tid + 1]);
+      sg = get_f64(&w.sum_part[tid]);
     }
     block_argmax(bv, bi, sv, si);
     mx = bv;
@@ -366,7 +397,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
         }
         if (last) {
           const uint32_t slot = atomicAdd(&cand_n, 1u);
-          if (slot < kCand) w.cand[(size_t)g * kCand + slot] = make_uint2(first + r, bits);
+          if (slot < kCand) put(&w.cand[(size_t)g * kCand + slot], ((unsigned long long)bits << 32) | (first + r));
         }
         const int k = (int)((bits >> shift) & (kBins - 1));
         if (k != run_bin) {
@@ -393,9 +424,9 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       for (int i = tid; i < kBins; i += kThreads)
         if (bins[i]) __hip_atomic_fetch_add(&summed[i], bins[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (last && tid == 0) {
-        w.above_part[g] = above_g;
-        w.above_count[g] = above_n;
-        w.cand_count[g] = cand_n;
+        put(&w.above_part[g], (uint64_t)above_g);
+        put(&w.above_count[g], above_n);
+        put(&w.cand_count[g], cand_n);
       }
       if (!grid_barrier(gs, G)) {
         if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
@@ -406,9 +437,9 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
         last_done = true;
         cand_prefix = prefix;
         if (tid < G) {
-          g_above = w.above_part[tid];
-          g_above_n = w.above_count[tid];
-          g_cand_n = w.cand_count[tid];
+          g_above = get(&w.above_part[tid]);
+          g_above_n = get(&w.above_count[tid]);
+          g_cand_n = get(&w.cand_count[tid]);
         }
       }
       // cum(k) = above + mass of bins >= k; the selected bin is the highest k with cum(k) >=
@@ -420,7 +451,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       unsigned long long m[kPer], part = 0;
 #pragma unroll
       for (int j = 0; j < kPer; j++) {
-        m[j] = summed[kBins - 1 - (tid * kPer + j)];  // descending bin order
+        m[j] = get(&summed[kBins - 1 - (tid * kPer + j)]);  // descending bin order
         part += m[j];
       }
       unsigned long long cum = above + block_exclusive_scan(part, nullptr);
@@ -476,7 +507,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       gk = g_above;
       gc = g_above_n;
       for (uint32_t c = 0; c < g_cand_n; c++) {
-        const float pc = __uint_as_float(w.cand[(size_t)tid * kCand + c].y);
+        const float pc = __uint_as_float((uint32_t)(get(&w.cand[(size_t)tid * kCand + c]) >> 32));
         if (pc >= thr) {
           gk += to_fix(pc);
           gc++;
@@ -489,16 +520,16 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
     const unsigned long long kept = block_sum(mine, ks);
     const uint32_t count = block_sum(cnt, cs);
     if (tid == 0) {
-      w.kept_part[g] = kept;
-      w.count_part[g] = count;
+      put(&w.kept_part[g], (uint64_t)kept);
+      put(&w.count_part[g], count);
     }
     if (!grid_barrier(gs, G)) {
       if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
       return;
     }
     if (tid < G) {
-      gk = w.kept_part[tid];
-      gc = w.count_part[tid];
+      gk = get(&w.kept_part[tid]);
+      gc = get(&w.count_part[tid]);
     }
   }
   // Kept mass per slice in id order: the target, then the first slice whose inclusive prefix
@@ -573,7 +604,7 @@ Work workspace(eg_context* ctx, GridSync* gs) {
   off += (size_t)kMaxGroups * 4;
   w.cand_count = reinterpret_cast<uint32_t*>(part + off);
   off += (size_t)kMaxGroups * 4;
-  w.cand = reinterpret_cast<uint2*>(part + off);
+  w.cand = reinterpret_cast<unsigned long long*>(part + off);
   off += (size_t)kMaxGroups * kCand * 8;
   static_assert((size_t)kMaxGroups * (44 + kCand * 8) + (size_t)kLevels * kBins * 8 <= eg::kPartialsBytes,
                 "sampler partials exceed the workspace");
