@@ -12,7 +12,8 @@ Reported:
                    256 MB Infinity Cache), algorithmic bytes / wall time of the timed steps;
   sequential_*     the same step as 168 per-projection launches in one hipGraph (the
                    reference's dispatch order), cold;
-  lm_head          config 2: the 151936 x 896 int8 tied head with the fused greedy argmax;
+  lm_head          config 2: the 151936 x 896 int8 tied head with the fused greedy argmax (and
+                   its finalize launch), the head GEMV launch alone, and the sampled token;
   per_gemv_us      single launches of each shape, cold;
   roofline         the dominant kernel (the K=896 batched launch), its algorithmic bytes over
                    its own HIP-event-timed duration on the library's stream;
@@ -318,6 +319,7 @@ def main() -> int:
 
     hn = head_numbers(dev, ev, stream, args, rng)
     head_us, head_gbs, sampled_us = hn["us"], hn["gbs"], hn["sampled_us"]
+    head_gemv_gbs = LM_HEAD_BYTES / (hn["gemv_us"] * 1e-6) / 1e9
 
     # ---- prefill chunk (config 3) ----
     prefill = prefill_numbers(dev, ev, stream, args)
@@ -356,6 +358,10 @@ def main() -> int:
         "lm_head": {"config": "BASELINE config 2: 151936x896 int8 per-row + fused argmax", "us": round(head_us, 2),
                     "gbs": round(head_gbs, 1), "pct_of_peak": round(100 * head_gbs / HBM_PEAK_GBS, 2),
                     "bytes": LM_HEAD_BYTES,
+                    "gemv_alone": {"us": round(hn["gemv_us"], 2), "gbs": round(head_gemv_gbs, 1),
+                                   "pct_of_peak": round(100 * head_gemv_gbs / HBM_PEAK_GBS, 2),
+                                   "note": "the head GEMV launch alone (logits stored, no argmax): the decode-shape "
+                                           "int8 GEMV; `us` above adds the argmax finalize launch"},
                     "sampled_token_us": round(sampled_us, 2),
                     "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history"},
         "per_gemv_us": per_gemv,
@@ -454,10 +460,27 @@ def head_numbers(dev, ev, stream, args, rng) -> dict:
     ev.sync(ss2[-1])
     sampled_us = float(np.median([ev.ms(ss2[i], ss2[i + 1]) for i in range(args.steps)])) * 1e3
     log(f"lm_head+sample (T 0.7, top-p 0.9, penalty 1.1): {sampled_us:.1f} us")
+
+    # the head GEMV alone (the reference's lm_head_q8 binding: logits stored, no argmax)
+    def plain_head(i):
+        hu = head_k.uniform()
+        hu.write(dims)
+        head_k.encode(head_k.bind_group([h, heads[i % 3][0], heads[i % 3][1], None, logits, hu]), (1, 1, 1))
+
+    for i in range(args.warmup):
+        plain_head(i)
+    ss3 = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(ss3[0], stream)
+    for i in range(args.steps):
+        plain_head(i)
+        ev.record(ss3[i + 1], stream)
+    ev.sync(ss3[-1])
+    plain_us = float(np.median([ev.ms(ss3[i], ss3[i + 1]) for i in range(args.steps)])) * 1e3
+    log(f"lm_head GEMV alone: {plain_us:.1f} us, {LM_HEAD_BYTES / (plain_us * 1e-6) / 1e9:.0f} GB/s cold")
     for a, b in heads:
         a.release()
         b.release()
-    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us}
+    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us, "gemv_us": plain_us}
 
 
 def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
