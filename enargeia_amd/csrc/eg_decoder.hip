@@ -259,9 +259,12 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
   for (uint32_t l = 0; l < m.layers && st == EG_OK; l++) {
     const eg_layer_desc& L = d->layers[l];
     st = eg::rmsnorm_rows(ctx, d->ph[0], L.input_norm, count, H, m.rms_eps, d->pxn);
-    gemm(d->pxn, L.q, L.q_bias, nullptr, d->pq, H, H, H, 0);
-    gemm(d->pxn, L.k, L.k_bias, nullptr, d->pk, kvn, H, kvn, 0);
-    gemm(d->pxn, L.v, L.v_bias, nullptr, d->pv, kvn, H, kvn, 0);
+    // q, k and v in one launch (they share the normed rows)
+    const eg::PrefillMatrix qkv[3] = {
+        {L.q.packed, L.q.scales, L.q.zeros, L.q_bias, nullptr, d->pq, H, H, 0},
+        {L.k.packed, L.k.scales, L.k.zeros, L.k_bias, nullptr, d->pk, kvn, kvn, 0},
+        {L.v.packed, L.v.scales, L.v.zeros, L.v_bias, nullptr, d->pv, kvn, kvn, 0}};
+    if (st == EG_OK) st = eg::prefill_gemm_multi(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, qkv, 3);
     if (st != EG_OK) break;
     eg_attention_prefill_dims ad{count, begin + count, begin, m.heads, m.kv_heads, m.head_dim, m.max_context,
                                  m.rope_theta};
@@ -269,8 +272,10 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
                               d->v_cache + l * d->layer_stride, d->pqr, d->patt, &ad);
     gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
     if (st == EG_OK) st = eg::rmsnorm_rows(ctx, d->ph[1], L.post_attention_norm, count, H, m.rms_eps, d->pxn);
-    gemm(d->pxn, L.gate, nullptr, nullptr, d->pgu, I, H, 2 * I, 0);
-    gemm(d->pxn, L.up, nullptr, nullptr, d->pgu, I, H, 2 * I, I);
+    // gate and up in one launch, side by side in each row of pgu
+    const eg::PrefillMatrix gu[2] = {{L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, nullptr, d->pgu, I, 2 * I, 0},
+                                     {L.up.packed, L.up.scales, L.up.zeros, nullptr, nullptr, d->pgu, I, 2 * I, I}};
+    if (st == EG_OK) st = eg::prefill_gemm_multi(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, gu, 2);
     if (st == EG_OK) st = eg::silu_mul_rows(ctx, d->pgu, count, I, d->pa);
     gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0);  // ph0 = ph1 + down(...)
   }

@@ -35,6 +35,19 @@ constexpr int kPad = 8;     // bf16 elements of padding per LDS row
 constexpr int kLds = kBK + kPad;
 constexpr int kStages = 3;  // register stages of the chunked staging pipeline
 
+// One matrix of a multi-matrix launch: its streams, outputs and the end of its range of 64-column
+// tiles along grid.x (the matrices share x, M, K, the quant block size and the encoding).
+struct PrefillSeg {
+  const uint32_t* packed;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  const float* residual;
+  float* out;
+  uint32_t n, out_stride, out_offset, tiles_end;
+};
+constexpr uint32_t kMaxSegs = 3;
+
 struct PrefillArgs {
   const float* x;
   const uint32_t* packed;
@@ -47,7 +60,37 @@ struct PrefillArgs {
   uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset, k_per_split;
   int bits;
   uint32_t block_shift;  // log2(block_size) (the chunked staging takes power-of-two blocks)
+  uint32_t nsegs;        // > 1: several matrices in one launch (segs), no K split
+  PrefillSeg segs[kMaxSegs];
 };
+
+// The matrix of a multi-matrix launch that owns tile column `tx`: its fields replace the
+// launch's (wave-uniform: every value comes from the kernel arguments), and the tile column
+// becomes its own.
+__device__ __forceinline__ uint32_t select_segment(PrefillArgs& a, uint32_t tx) {
+  if (a.nsegs <= 1) return tx;
+  uint32_t s = 0, before = 0;
+#pragma unroll
+  for (uint32_t i = 0; i + 1 < kMaxSegs; i++)
+    if (i + 1 < a.nsegs && tx >= a.segs[i].tiles_end) {
+      s = i + 1;
+      before = a.segs[i].tiles_end;
+    }
+  PrefillSeg g = a.segs[0];
+#pragma unroll
+  for (uint32_t i = 1; i < kMaxSegs; i++)
+    if (s == i) g = a.segs[i];
+  a.packed = g.packed;
+  a.scales = g.scales;
+  a.zeros = g.zeros;
+  a.bias = g.bias;
+  a.residual = g.residual;
+  a.out = g.out;
+  a.n = g.n;
+  a.out_stride = g.out_stride;
+  a.out_offset = g.out_offset;
+  return tx - before;
+}
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) {
   uint32_t u = __float_as_uint(v);
@@ -232,7 +275,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   const uint32_t group = threadIdx.x >> 8;
   uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
   uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
-  const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+  const uint32_t m0 = blockIdx.y * kTile, n0 = select_segment(a, blockIdx.x) * kTile;
   const uint32_t tid = threadIdx.x & 255u, wave = tid >> 6, lane = tid & 63u;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
@@ -435,7 +478,7 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   PrefillArgs a{x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                 residual, out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
                 dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits,
-                (uint32_t)__builtin_ctz(bs)};
+                (uint32_t)__builtin_ctz(bs), 1u, {}};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
   const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
                        (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
@@ -461,6 +504,70 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
     hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.bias, residual,
                        out, m, n, (uint32_t)splits, dims->out_stride, dims->out_offset);
   }
+  return eg::check_launch(ctx, op);
+}
+
+int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
+                           int encoding, int bits, const PrefillMatrix* mats, uint32_t count) {
+  const char* op = "matmul_q4_prefill";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (count > 0 && !mats) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL matrix list", op);
+  auto one = [&](const PrefillMatrix& w) {
+    eg_matmul_q4_dims dm{};
+    dm.m = m;
+    dm.n = w.n;
+    dm.k = k;
+    dm.use_bias = w.bias != nullptr;
+    dm.block_size = block_size;
+    dm.blocks_per_row = block_size ? k / block_size : 0;
+    dm.out_stride = w.out_stride;
+    dm.out_offset = w.out_offset;
+    return eg::prefill_gemm(ctx, x, w.packed, w.scales, w.zeros, w.bias, w.residual, w.out, &dm, encoding, bits);
+  };
+  // One launch where the chunked staging takes every matrix and no matrix would split K;
+  // otherwise (and for anything the single path must reject with its own message) one each.
+  bool together = count >= 2 && count <= kMaxSegs && m > 0 && x && bits == 4 &&
+                  (encoding == EG_ENC_SIGNED || encoding == EG_ENC_OFFSET_ZEROS) && block_size >= 16 &&
+                  (block_size & (block_size - 1)) == 0 && k % block_size == 0 && k % 32 == 0 &&
+                  (k + kBK - 1) / kBK < 32 && (uint64_t)m * k * 4 < kOutside &&
+                  (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  uint64_t tiles_n = 0;
+  for (uint32_t i = 0; together && i < count; i++) {
+    const PrefillMatrix& w = mats[i];
+    together = w.n > 0 && w.packed && w.scales && w.out && (encoding == EG_ENC_SIGNED || w.zeros) &&
+               (m == 1 || w.out_stride >= w.n) && (uint64_t)w.n * k / 2 < kOutside &&
+               (uint64_t)w.n * (k / block_size) < (1ull << 32) && (reinterpret_cast<uintptr_t>(w.packed) & 7u) == 0;
+    tiles_n += (w.n + kTile - 1) / kTile;
+  }
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  if (!together || tiles_n > 0x7FFFFFFFull || tiles_m > 65535) {
+    for (uint32_t i = 0; i < count; i++) {
+      const int st = one(mats[i]);
+      if (st != EG_OK) return st;
+    }
+    return EG_OK;
+  }
+  PrefillArgs a{x, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, m, 0, k, block_size,
+                k / block_size, 0, 0, k, bits, (uint32_t)__builtin_ctz(block_size), count, {}};
+  uint32_t end = 0;
+  for (uint32_t i = 0; i < count; i++) {
+    const PrefillMatrix& w = mats[i];
+    end += (w.n + kTile - 1) / kTile;
+    a.segs[i] = PrefillSeg{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, w.residual,
+                           w.out, w.n, w.out_stride, w.out_offset, end};
+  }
+  const int kg = ctx->prefill_groups ? ctx->prefill_groups : (tiles_n * tiles_m >= (uint64_t)ctx->cu_count ? 1 : 4);
+  const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
+  const dim3 block(256 * kg);
+#define EG_PREFILL_MULTI(ENC)                                                                           \
+  do {                                                                                                  \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4>), grid, block, 0, ctx->stream, a);    \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2>), grid, block, 0, ctx->stream, a); \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1>), grid, block, 0, ctx->stream, a);            \
+  } while (0)
+  if (encoding == EG_ENC_SIGNED) EG_PREFILL_MULTI(EG_ENC_SIGNED);
+  else EG_PREFILL_MULTI(EG_ENC_OFFSET_ZEROS);
+#undef EG_PREFILL_MULTI
   return eg::check_launch(ctx, op);
 }
 

@@ -132,6 +132,23 @@ int prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, const 
                  const float* bias, const float* residual, float* out, const eg_matmul_q4_dims* dims, int encoding,
                  int bits);
 
+// Several matrices that share x (m rows of k values), the quant block size and the encoding in
+// ONE launch - the prompt chain's q|k|v and gate|up: for each matrix s (at most 3),
+// out_s[r * out_stride_s + col + out_offset_s] = sum_k x[r, k] W_s[col, k] + bias_s[col]
+// (+ residual_s at the same index). Layouts the chunked staging does not take, and a K deep
+// enough that a lone matrix would split it, run one prefill_gemm per matrix instead.
+struct PrefillMatrix {
+  const uint32_t* packed;
+  const float* scales;
+  const uint32_t* zeros;
+  const float* bias;
+  const float* residual;
+  float* out;
+  uint32_t n, out_stride, out_offset;
+};
+int prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
+                       int bits, const PrefillMatrix* mats, uint32_t count);
+
 // Row-wise kernels of the prefill chain (one workgroup per row):
 //   embed_rows: out[r] = the dequantized table row of ids[r] (ops.ts:222-233), r < rows;
 //   rmsnorm_rows: out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w (ops.ts:30-51);
