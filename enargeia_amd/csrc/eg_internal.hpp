@@ -34,6 +34,10 @@ struct eg_context {
   // workgroup recomputes the stage, but the decoder's launches measured faster with more,
   // shorter-lived workgroups than with two tiles per wave).
   uint32_t fused_tiles_per_wave = 1;
+  // The sampler's bounded waits: polls before a wait gives up (eg_test_sample_spin; off: about a
+  // second's worth), so tests can force the give-up path from the host.
+  bool sample_spin_override = false;
+  uint32_t sample_spin_polls = 0;
   // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
   // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
   int prefill_groups = 0;

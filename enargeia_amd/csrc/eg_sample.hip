@@ -168,7 +168,7 @@ __device__ __forceinline__ void drain() {
 
 // Central barrier over the launch's workgroups: thread 0 of each counts the workgroup once its
 // waves have drained their stores; the last to arrive resets the count and, once that store
-// has completed, advances the generation, which the others poll. Polls are bounded: past kSpin,
+// has completed, advances the generation, which the others poll. Polls are bounded: past `spin`,
 // or when another workgroup has given up, the abort flag is raised and false is returned to
 // every thread.
 constexpr uint32_t kSpin = 1u << 20;  // polls of ~1 us: a barrier gives up after about a second
@@ -178,6 +178,7 @@ struct GridSync {
   uint32_t* gen;    // advanced once per completed barrier
   uint32_t* abort;  // set by a timed-out wait
   uint32_t* exits;  // workgroups done with every barrier of the current launch
+  uint32_t spin;    // polls before a wait gives up (kSpin; the context's test hook may lower it)
 };
 
 __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
@@ -196,7 +197,7 @@ __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
     } else {
       uint32_t n = 0;
       while (get(g.gen) == gen0) {
-        if (get(g.abort) != 0u || ++n > kSpin) {
+        if (get(g.abort) != 0u || ++n > g.spin) {
           good = false;
           break;
         }
@@ -618,6 +619,7 @@ int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* ou
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
   GridSync gs;
   Work w = workspace(ctx, &gs);
+  gs.spin = ctx->sample_spin_override ? ctx->sample_spin_polls : kSpin;
   hipLaunchKernelGGL(sample_kernel, dim3(groups), dim3(kThreads), 0, ctx->stream, logits, history, out, hp, dp, w, gs,
                      rng);
   return eg::check_launch(ctx, "sample");
@@ -635,6 +637,13 @@ int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* his
   SampleParams hp{};
   hp.vocab = vocab;
   return launch(ctx, logits, history, out, hp, reinterpret_cast<SampleParams*>(params), rng);
+}
+
+extern "C" int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "test_sample_spin: ctx is NULL");
+  ctx->sample_spin_override = override != 0;
+  ctx->sample_spin_polls = polls;
+  return EG_OK;
 }
 
 extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,

@@ -211,6 +211,13 @@ EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const 
 EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
               const eg_sample_dims* dims);
 
+/* Test hook, no counterpart in the reference: with override != 0 every later sampler launch on
+ * this context (eg_sample and the decoder's sampled steps) gives a barrier wait up after `polls`
+ * polls instead of about a second, so the give-up path (out[0] = 0xFFFFFFFF, every workgroup
+ * leaving, the barrier words restored for the next launch) can be forced from the host; override
+ * 0 restores the default. Not for production use. */
+EG_API int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls);
+
 /* ---- decode step: embedding, attention, fused GEMV inputs ----------------------------------- */
 
 /* embed_gather_<dtype> (embedding_variants.ts:93-133, :56-63 for q8): for the one token id read

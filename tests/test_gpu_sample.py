@@ -193,3 +193,30 @@ def test_sampler_deterministic_and_reentrant(device, config2):
         assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
     finally:
         s.close()
+
+
+def test_barrier_give_up_is_clean_and_next_call_recovers(device, config2):
+    # The sampler's waits are bounded. Forced from the host to give up at their first poll (the
+    # test hook eg_test_sample_spin), a launch must still end - every workgroup leaves - with
+    # 0xFFFFFFFF as its token, and the next launch on the same context, with the default
+    # bound, must find the barrier words restored and sample normally.
+    from enargeia_amd import _lib
+
+    lib = _lib.load()
+    s = Sampler(device, VOCAB)
+    try:
+        params = K.SamplingParams(0.7, 0.9, 1.0)
+        expect = s(config2, [], params, 0.37)
+        _lib.check(lib.eg_test_sample_spin(device.ctx, 1, 0), device.ctx)
+        try:
+            # the first workgroups to arrive at the first barrier poll before the last arrives
+            assert s(config2, [], params, 0.37) == 0xFFFFFFFF
+            # one barrier: ends either way
+            assert s(config2, [], K.GREEDY, 0.5) in (0xFFFFFFFF, oracle.argmax(config2))
+        finally:
+            _lib.check(lib.eg_test_sample_spin(device.ctx, 0, 0), device.ctx)
+        for _ in range(3):
+            assert s(config2, [], params, 0.37) == expect
+        assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
+    finally:
+        s.close()
