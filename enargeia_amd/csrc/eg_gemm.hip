@@ -35,14 +35,15 @@ constexpr int kPad = 8;     // bf16 elements of padding per LDS row
 constexpr int kLds = kBK + kPad;
 constexpr int kStages = 3;  // register stages of the chunked staging pipeline
 
-// One matrix of a multi-matrix launch: its streams, outputs and the end of its range of 64-column
-// tiles along grid.x (the matrices share x, M, K, the quant block size and the encoding).
-struct PrefillSeg {
+// One matrix of a launch: its streams, outputs and the end of its range of 64-column tiles along
+// grid.x. A multi-matrix launch holds several that share x, M, K, the quant block size and the
+// encoding; the usual launch holds one.
+struct PrefillMat {
   const uint32_t* packed;
   const float* scales;
   const uint32_t* zeros;
   const float* bias;
-  const float* residual;
+  const float* residual;  // nullable: out = acc + bias + residual[r * out_stride + col + out_offset]
   float* out;
   uint32_t n, out_stride, out_offset, tiles_end;
 };
@@ -50,46 +51,23 @@ constexpr uint32_t kMaxSegs = 3;
 
 struct PrefillArgs {
   const float* x;
-  const uint32_t* packed;
-  const float* scales;
-  const uint32_t* zeros;
-  const float* bias;
-  const float* residual;  // nullable: out = acc + bias + residual[r * out_stride + col + out_offset]
-  float* out;
   float* partials;  // split-K: [splits][m][n] f32; NULL when grid.z == 1
-  uint32_t m, n, k, block_size, blocks_per_row, out_stride, out_offset, k_per_split;
+  uint32_t m, k, block_size, blocks_per_row, k_per_split;
   int bits;
   uint32_t block_shift;  // log2(block_size) (the chunked staging takes power-of-two blocks)
-  uint32_t nsegs;        // > 1: several matrices in one launch (segs), no K split
-  PrefillSeg segs[kMaxSegs];
+  uint32_t nmats;        // matrices in mats (> 1: no K split)
+  PrefillMat mats[kMaxSegs];
 };
 
-// The matrix of a multi-matrix launch that owns tile column `tx`: its fields replace the
-// launch's (wave-uniform: every value comes from the kernel arguments), and the tile column
-// becomes its own.
-__device__ __forceinline__ uint32_t select_segment(PrefillArgs& a, uint32_t tx) {
-  if (a.nsegs <= 1) return tx;
-  uint32_t s = 0, before = 0;
+// The matrix that owns tile column `tx` and the first tile column of its range. The matrix is
+// read in place from the kernel arguments (the arguments are never written: a written copy with
+// an indexed array member would be kept in scratch memory).
+__device__ __forceinline__ uint32_t select_matrix(const PrefillArgs& a, uint32_t tx) {
+  uint32_t s = 0;
 #pragma unroll
   for (uint32_t i = 0; i + 1 < kMaxSegs; i++)
-    if (i + 1 < a.nsegs && tx >= a.segs[i].tiles_end) {
-      s = i + 1;
-      before = a.segs[i].tiles_end;
-    }
-  PrefillSeg g = a.segs[0];
-#pragma unroll
-  for (uint32_t i = 1; i < kMaxSegs; i++)
-    if (s == i) g = a.segs[i];
-  a.packed = g.packed;
-  a.scales = g.scales;
-  a.zeros = g.zeros;
-  a.bias = g.bias;
-  a.residual = g.residual;
-  a.out = g.out;
-  a.n = g.n;
-  a.out_stride = g.out_stride;
-  a.out_offset = g.out_offset;
-  return tx - before;
+    if (i + 1 < a.nmats && tx >= a.mats[i].tiles_end) s = i + 1;
+  return s;
 }
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) {
@@ -136,7 +114,7 @@ struct StageBase {
   uint32_t sblk;    // the row's first quant block index
 };
 
-__device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, uint32_t m0, uint32_t n0) {
+__device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, const PrefillMat& w, uint32_t m0, uint32_t n0) {
   const uint32_t tid = threadIdx.x & 255u;  // the thread within its group of 4 waves
   StageBase b;
   b.xc = (tid & 15u) * 4u;
@@ -147,7 +125,7 @@ __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, uint32_t m
   }
   const uint32_t nrow = n0 + (tid >> 2);
   b.kc = 16u * (tid & 3u);
-  b.w = nrow < a.n ? (nrow * a.k + b.kc) / 2u : kOutside;
+  b.w = nrow < w.n ? (nrow * a.k + b.kc) / 2u : kOutside;
   b.sblk = nrow * a.blocks_per_row;
   return b;
 }
@@ -227,8 +205,8 @@ __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLd
 
 // Element-by-element staging for the layouts the chunked path does not take.
 template <int ENC>
-__device__ void stage_elements(const PrefillArgs& a, uint32_t m0, uint32_t n0, uint32_t k0, uint16_t (*As)[kLds],
-                               uint16_t (*Bs)[kLds]) {
+__device__ void stage_elements(const PrefillArgs& a, const PrefillMat& w, uint32_t m0, uint32_t n0, uint32_t k0,
+                               uint16_t (*As)[kLds], uint16_t (*Bs)[kLds]) {
   const uint32_t tid = threadIdx.x & 255u;
   const uint32_t per_word = 32u / (uint32_t)a.bits, mask = (1u << a.bits) - 1u;
 #pragma unroll 4
@@ -243,18 +221,18 @@ __device__ void stage_elements(const PrefillArgs& a, uint32_t m0, uint32_t n0, u
     const uint32_t r = e / kBK, c = e % kBK;
     const uint32_t nrow = n0 + r, kk = k0 + c;
     float v = 0.f;
-    if (nrow < a.n && kk < a.k) {
+    if (nrow < w.n && kk < a.k) {
       const size_t flat = (size_t)nrow * a.k + kk;
-      uint32_t code = (a.packed[flat / per_word] >> (a.bits * (flat % per_word))) & mask;
+      uint32_t code = (w.packed[flat / per_word] >> (a.bits * (flat % per_word))) & mask;
       const uint32_t blk = nrow * a.blocks_per_row + kk / a.block_size;
       int32_t z;
       if (ENC == EG_ENC_OFFSET_ZEROS) {
-        z = (int32_t)((a.zeros[blk / per_word] >> (a.bits * (blk % per_word))) & mask);
+        z = (int32_t)((w.zeros[blk / per_word] >> (a.bits * (blk % per_word))) & mask);
       } else {
         code ^= 1u << (a.bits - 1);
         z = 1 << (a.bits - 1);
       }
-      v = (float)((int32_t)code - z) * a.scales[blk];
+      v = (float)((int32_t)code - z) * w.scales[blk];
     }
     Bs[r][c] = bf16_bits(v);
   }
@@ -275,7 +253,8 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   const uint32_t group = threadIdx.x >> 8;
   uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
   uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
-  const uint32_t m0 = blockIdx.y * kTile, n0 = select_segment(a, blockIdx.x) * kTile;
+  const PrefillMat& w = a.mats[select_matrix(a, blockIdx.x)];
+  const uint32_t m0 = blockIdx.y * kTile, n0 = (blockIdx.x - (w.tiles_end - ((w.n + kTile - 1) / kTile))) * kTile;
   const uint32_t tid = threadIdx.x & 255u, wave = tid >> 6, lane = tid & 63u;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
@@ -319,10 +298,10 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     // remaining blocks are already in flight and drain in a loop that issues no loads.
     // four groups fit four waves per SIMD only within 128 VGPRs: they keep one block in flight
     constexpr int S = KG >= 4 ? 2 : kStages;
-    const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(a.packed, a.n * a.k / 2u),
-                     egd::buffer(a.scales, a.n * a.blocks_per_row * 4u),
-                     egd::buffer(a.zeros, ((a.n * a.blocks_per_row + 7u) / 8u) * 4u)};
-    const StageBase sb = stage_base(a, m0, n0);
+    const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(w.packed, w.n * a.k / 2u),
+                     egd::buffer(w.scales, w.n * a.blocks_per_row * 4u),
+                     egd::buffer(w.zeros, ((w.n * a.blocks_per_row + 7u) / 8u) * 4u)};
+    const StageBase sb = stage_base(a, w, m0, n0);
     Staged st[S];
 #pragma unroll
     for (int u = 0; u + 1 < S; u++)
@@ -352,7 +331,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   } else {
     for (uint32_t it = 0; it < iters; it++) {
       const uint32_t blk = min(block_of(it), nblk - 1);
-      stage_elements<ENC>(a, m0, n0, kbeg + blk * kBK, As, Bs);
+      stage_elements<ENC>(a, w, m0, n0, kbeg + blk * kBK, As, Bs);
       __syncthreads();
       if (block_of(it) < nblk) mfma_block();
       __syncthreads();
@@ -372,15 +351,15 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     __syncthreads();
     for (uint32_t idx = threadIdx.x; idx < kTile * kTile; idx += 256u * KG) {
       const uint32_t r = idx / kTile, c = idx % kTile, row = m0 + r, col = n0 + c;
-      if (row >= a.m || col >= a.n) continue;
+      if (row >= a.m || col >= w.n) continue;
       float v = reinterpret_cast<const float*>(lds)[idx];
 #pragma unroll
       for (int g = 1; g < KG; g++) v += reinterpret_cast<const float*>(lds + g * kStageBytes)[idx];
       if (a.partials) {
-        a.partials[((size_t)blockIdx.z * a.m + row) * a.n + col] = v;
+        a.partials[((size_t)blockIdx.z * a.m + row) * w.n + col] = v;
       } else {
-        const size_t o = (size_t)row * a.out_stride + col + a.out_offset;
-        a.out[o] = v + (a.bias ? a.bias[col] : 0.f) + (a.residual ? a.residual[o] : 0.f);
+        const size_t o = (size_t)row * w.out_stride + col + w.out_offset;
+        w.out[o] = v + (w.bias ? w.bias[col] : 0.f) + (w.residual ? w.residual[o] : 0.f);
       }
     }
     return;
@@ -392,17 +371,17 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const uint32_t col = n0 + wn + j * 16 + (lane & 15);
-      if (col >= a.n) continue;
-      const float b = (a.partials == nullptr && a.bias) ? a.bias[col] : 0.f;
+      if (col >= w.n) continue;
+      const float b = (a.partials == nullptr && w.bias) ? w.bias[col] : 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const uint32_t row = m0 + wm + i * 16 + 4 * (lane >> 4) + e;
         if (row >= a.m) continue;
         if (a.partials) {
-          a.partials[((size_t)blockIdx.z * a.m + row) * a.n + col] = acc[i][j][e];
+          a.partials[((size_t)blockIdx.z * a.m + row) * w.n + col] = acc[i][j][e];
         } else {
-          const size_t o = (size_t)row * a.out_stride + col + a.out_offset;
-          a.out[o] = acc[i][j][e] + b + (a.residual ? a.residual[o] : 0.f);
+          const size_t o = (size_t)row * w.out_stride + col + w.out_offset;
+          w.out[o] = acc[i][j][e] + b + (w.residual ? w.residual[o] : 0.f);
         }
       }
     }
@@ -475,10 +454,10 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   uint32_t k_per_split = (uint32_t)((((uint64_t)k + splits - 1) / splits + kBK - 1) / kBK * kBK);
   splits = (k + k_per_split - 1) / k_per_split;
   const bool split = splits > 1;
-  PrefillArgs a{x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
-                residual, out, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, n, k, bs,
-                dims->blocks_per_row, dims->out_stride, dims->out_offset, k_per_split, bits,
-                (uint32_t)__builtin_ctz(bs), 1u, {}};
+  PrefillArgs a{x, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, k, bs, dims->blocks_per_row,
+                k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, {}};
+  a.mats[0] = PrefillMat{packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
+                         residual, out, n, dims->out_stride, dims->out_offset, tiles_n};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
   const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
                        (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
@@ -501,7 +480,7 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   if (split) {
     const uint64_t total = (uint64_t)m * n;
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);
-    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.bias, residual,
+    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, a.partials, a.mats[0].bias, residual,
                        out, m, n, (uint32_t)splits, dims->out_stride, dims->out_offset);
   }
   return eg::check_launch(ctx, op);
@@ -547,13 +526,12 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
     }
     return EG_OK;
   }
-  PrefillArgs a{x, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, m, 0, k, block_size,
-                k / block_size, 0, 0, k, bits, (uint32_t)__builtin_ctz(block_size), count, {}};
+  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count, {}};
   uint32_t end = 0;
   for (uint32_t i = 0; i < count; i++) {
     const PrefillMatrix& w = mats[i];
     end += (w.n + kTile - 1) / kTile;
-    a.segs[i] = PrefillSeg{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, w.residual,
+    a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, w.residual,
                            w.out, w.n, w.out_stride, w.out_offset, end};
   }
   const int kg = ctx->prefill_groups ? ctx->prefill_groups : (tiles_n * tiles_m >= (uint64_t)ctx->cu_count ? 1 : 4);

@@ -62,7 +62,7 @@ int hip_fail(eg_context* ctx, hipError_t err, const char* what);
 // Workspace layout (bytes from ctx->workspace). Fixed offsets; sizes bound the op limits.
 constexpr size_t kStateOffset = 256;           // small per-op state
 constexpr size_t kPartialsOffset = 8192;       // per-workgroup partials
-constexpr size_t kWorkspaceBytes = 16u << 20;  // 16 MiB
+constexpr size_t kWorkspaceBytes = 64u << 20;  // 64 MiB
 
 inline uint8_t* state(eg_context* ctx) { return ctx->workspace + kStateOffset; }
 inline uint8_t* partials(eg_context* ctx) { return ctx->workspace + kPartialsOffset; }

@@ -277,14 +277,20 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads over the grid limit", op, d.heads);
   hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
                      v_cache, d);
-  // Keys split where the (query block, head) grid leaves most CUs idle over a long key range:
-  // splits of at least 4 key tiles, about one workgroup per CU in all, within the workspace.
+  // Keys split over a long key range, within the workspace: where the (query block, head) grid
+  // leaves most CUs idle, into splits of at least 4 key tiles, about one workgroup per CU in all;
+  // and so that no workgroup walks more than 8 tiles - the causal limit makes the last query
+  // blocks of a long chunk the longest, and with the split their keys spread over more
+  // workgroups while the early blocks' later splits are empty.
   const uint32_t blocks = (d.queries + kQ - 1) / kQ;
   const uint64_t grid = (uint64_t)blocks * d.heads;
   const uint32_t tiles = (d.keys + kK - 1) / kK;
   uint32_t splits = 1;
-  if (grid < (uint64_t)ctx->cu_count && tiles >= 8)
-    splits = (uint32_t)std::min<uint64_t>((ctx->cu_count + grid - 1) / grid, tiles / 4);
+  if (tiles >= 8) {
+    if (grid < (uint64_t)ctx->cu_count)
+      splits = (uint32_t)std::min<uint64_t>((ctx->cu_count + grid - 1) / grid, tiles / 4);
+    splits = std::max(splits, (tiles + 7) / 8);
+  }
   const uint64_t rows = (uint64_t)d.queries * d.heads;
   while (splits > 1 && (uint64_t)splits * rows * (kD + 2) * 4 > eg::kPartialsBytes) splits--;
   Splits sp{nullptr, 0, 1};

@@ -49,9 +49,11 @@ def run(device, q, k, v, kc16, vc16, begin, dims=None):
 
 # (1000, 256) and (1792, 256) split their keys over grid.z (the (query block, head) grid alone
 # would leave most CUs idle): 5 and 8 splits of 256 keys, rows whose causal limit ends before a
-# split's first key (an empty split for that row) included; (1900, 148) splits into 7.
+# split's first key (an empty split for that row) included; (1900, 148) splits into 7; a whole
+# 1024- or 2048-token prompt splits so that no workgroup walks more than 8 key tiles (2 and 4
+# splits, most of the early query blocks' later splits empty).
 @pytest.mark.parametrize("begin,n", [(0, 256), (0, 128), (300, 77), (1900, 148), (5, 1), (63, 64), (1000, 256),
-                                     (1792, 256)])
+                                     (1792, 256), (0, 1024), (0, 2048)])
 def test_prefill_attention_matches_oracle(device, begin, n):
     print(f"prefill attention begin {begin} queries {n}", flush=True)
     rng = np.random.default_rng(1000 + begin + n)
@@ -64,7 +66,11 @@ def test_prefill_attention_matches_oracle(device, begin, n):
     kc16, vc16 = kc.astype(np.float16).view(np.uint16), vc.astype(np.float16).view(np.uint16)
     got_qr, got, got_kc, got_vc = run(device, q, k, v, kc16, vc16, begin)
     want_qr, want = prefill_attention(q, k, v, kc, vc, begin, H, KV, D, THETA)
-    np.testing.assert_array_equal(got_qr, want_qr)
+    # The rotation runs in double precision on both sides; the GPU's and the host's double cos /
+    # sin may differ in their last bit, which flips the f32 rounding of a rare element by one
+    # ulp (1 of 1.8 M at 2048 positions): bit-exact otherwise.
+    np.testing.assert_array_max_ulp(got_qr, want_qr, maxulp=1)
+    assert np.count_nonzero(got_qr != want_qr) <= max(1, got_qr.size // 100000)
     np.testing.assert_array_equal(got_kc, kc.astype(np.float16).view(np.uint16))
     np.testing.assert_array_equal(got_vc, vc.astype(np.float16).view(np.uint16))
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
