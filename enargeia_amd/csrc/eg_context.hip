@@ -107,6 +107,13 @@ int eg_create(int device, eg_context** out_ctx) {
     const int v = std::atoi(tpw);
     if (v >= 1 && v <= 64) ctx->fused_tiles_per_wave = (uint32_t)v;
   }
+  if (const char* a = std::getenv("EG_ATTENTION_SPLIT")) {
+    int t = 0, f = 0;
+    if (std::sscanf(a, "%d,%d", &t, &f) == 2 && t >= 1 && t <= 64 && f >= 1 && f <= 8) {
+      ctx->attention_split_tiles = (uint32_t)t;
+      ctx->attention_split_fill = (uint32_t)f;
+    }
+  }
   if (const char* g = std::getenv("EG_PREFILL_GROUPS")) {
     const int v = std::atoi(g);
     if (v == 1 || v == 2 || v == 4) ctx->prefill_groups = v;

@@ -41,6 +41,10 @@ struct eg_context {
   // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
   // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
   int prefill_groups = 0;
+  // chunk attention's key split: at most this many 64-key tiles per workgroup, and a small grid
+  // split up to this many workgroups per CU
+  uint32_t attention_split_tiles = 8;
+  uint32_t attention_split_fill = 1;
   // Resident workgroups per CU of each kernel launched through this context (from
   // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
   // the device.

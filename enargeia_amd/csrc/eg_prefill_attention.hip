@@ -78,40 +78,98 @@ struct Splits {
   uint32_t count;    // splits (grid.z)
 };
 
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// One key tile's K and V in registers between its global loads and its LDS stores: K as two
+// 16-byte pieces of key tid / 4 (d 16 * (tid % 4) .. +16), V as 4 d values (4 * (tid % 16) .. +4)
+// of the 4 keys 4 * (tid / 16) .. +4. The caches are read through buffer resources that end at
+// the workgroup's last key: rows past it read as zeros without touching memory (a V row there
+// must be finite - its weight is 0 - and no branch is needed).
+struct KVTile {
+  egd::u32x4 k[2];
+  uint64_t v[4];
+};
+
+struct KVStream {
+  __amdgpu_buffer_rsrc_t k, v;
+  uint32_t koff, voff, pitch;  // this thread's byte offsets in tile 0; bytes between cache rows
+};
+
+__device__ __forceinline__ void load_tile(KVTile& t, const KVStream& st, uint32_t j0) {
+  const uint32_t base = j0 * st.pitch;
+  t.k[0] = egd::load_b128(st.k, st.koff + base);
+  t.k[1] = egd::load_b128(st.k, st.koff + base + 16u);
+#pragma unroll
+  for (int i = 0; i < 4; i++) t.v[i] = egd::load_b64(st.v, st.voff + base + i * st.pitch);
+}
+
+// LDS row of key r in Ks: bit 2 flipped where bit 4 is set, so the 16 rows one S^T operand read
+// touches (keys 0-3, 8-11, 16-19, 24-27 of a half tile, plus 4 for odd blocks) fall in 16
+// different groups of 4 banks.
+__device__ __forceinline__ uint32_t ks_row(uint32_t r) { return r ^ (((r >> 4) & 1u) << 2); }
+
+// K row-major, V transposed: the 4 x 4 block of V (keys 4a .. 4a+3, d c .. c+3) becomes 4 rows of
+// Vt, one 8-byte store each.
+__device__ __forceinline__ void store_tile(const KVTile& t, uint16_t (*Ks)[kRow], uint16_t (*Vt)[kRow], uint32_t tid) {
+  {
+    const uint32_t r = ks_row(tid >> 2), c = (tid & 3u) * 16u;
+    *reinterpret_cast<egd::u32x4*>(&Ks[r][c]) = t.k[0];
+    *reinterpret_cast<egd::u32x4*>(&Ks[r][c + 8]) = t.k[1];
+  }
+  const uint32_t a = tid >> 4, c = (tid & 15u) * 4u;
+  // t.v[i] = (d c, c+1 | c+2, c+3) of key 4a + i; row c + e of Vt takes element e of each key
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int sh = 32 * (e >> 1);
+    const uint32_t k0 = (uint32_t)(t.v[0] >> sh), k1 = (uint32_t)(t.v[1] >> sh);
+    const uint32_t k2 = (uint32_t)(t.v[2] >> sh), k3 = (uint32_t)(t.v[3] >> sh);
+    // element e is the low (e even) or high (e odd) half of word e / 2
+    const uint2 row = (e & 1) ? make_uint2((k0 >> 16) | (k1 & 0xFFFF0000u), (k2 >> 16) | (k3 & 0xFFFF0000u))
+                              : make_uint2((k0 & 0xFFFFu) | (k1 << 16), (k2 & 0xFFFFu) | (k3 << 16));
+    *reinterpret_cast<uint2*>(&Vt[c + e][4 * a]) = row;
+  }
+}
+
+// Flash attention in the transposed form: S^T = K Q^T and O^T += V^T P^T, so that each lane holds
+// ONE query's scores (the MFMA D layout puts a column in a lane) and P goes from the S^T
+// accumulators straight into the B operand of the second product, with no LDS round trip.
+//
+// Key order inside a tile: row m = 4g + e of S^T block n (n < 4, g = m / 4, e = m % 4) is key
+// 32 (n / 2) + 8 g + 4 (n % 2) + e, so a lane (column lr, group g = lane / 16) holds, for each half
+// h of the tile, the 8 consecutive keys 32 h + 8 g .. +8 - exactly the 8 k-slots of its P^T operand
+// in the second product, whose V^T operand then reads 8 consecutive keys of a Vt row.
 __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q_rope,
                                                         const uint16_t* __restrict__ k_cache,
                                                         const uint16_t* __restrict__ v_cache, float* __restrict__ out,
                                                         eg_attention_prefill_dims d, Splits sp) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kK][kRow];     // [key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kRow];     // [d][key]
-  __shared__ __attribute__((aligned(16))) uint16_t Ps[4][16][kRow];  // per wave: [query][key]
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kK][kRow];  // [buffer][key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD][kRow];  // [buffer][d][key]
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
   const uint32_t lr = lane & 15u, lg = lane >> 4;  // MFMA lane coordinates
   const uint32_t h = blockIdx.y, kv = h / (d.heads / d.kv_heads);
   const uint32_t q0 = blockIdx.x * kQ;
-  const uint32_t row0 = q0 + wave * 16;
+  const uint32_t query = q0 + wave * 16 + lr;  // this lane's query (its column of S^T and O^T)
 
-  // Q fragments (A operand of S = Q K^T): lane holds query row0 + lr, d 8*lg + 32*ks .. +8.
-  half8 qa[2];
+  // Q^T fragments (B operand of S^T = K Q^T): query lr, d 32 ks + 8 lg .. +8.
+  half8 qb[2];
   {
-    const uint32_t r = row0 + lr;
+    const bool in = query < d.queries;
+    const float4* src = reinterpret_cast<const float4*>(q_rope + ((size_t)(in ? query : 0) * d.heads + h) * kD + 8 * lg);
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        qa[ks][e] = r < d.queries ? (_Float16)q_rope[((size_t)r * d.heads + h) * kD + 32 * ks + 8 * lg + e]
-                                  : (_Float16)0.f;
+    for (int ks = 0; ks < 2; ks++) {
+      const float4 a = in ? src[8 * ks] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 b = in ? src[8 * ks + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+      qb[ks] = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                     (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+    }
   }
 
-  // O blocks (d 16*n .. 16*n+15) in the MFMA D layout: lane holds rows 4*lg + e, column lr.
+  // O^T blocks (d 16 nd .. +16) in the D layout: lane holds d 16 nd + 4 lg + e of its query.
   f32x4 o[4];
-  float m[4], l[4];
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    o[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m[e] = kMasked;
-    l[e] = 0.f;
-  }
+  for (int n = 0; n < 4; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kMasked;  // the query's running max (the same in the 4 lanes holding it)
+  float l = 0.f;      // this lane's share of the running sum (its 16 keys of each tile)
 
   const uint32_t last_query = min(q0 + (uint32_t)kQ, d.queries) - 1;
   uint32_t key_end = d.query_begin + last_query + 1;  // the keys any row of this group sees
@@ -120,133 +178,149 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     key_begin = blockIdx.z * sp.keys;
     key_end = min(key_end, key_begin + sp.keys);
   }
-  const size_t pitch = (size_t)d.kv_heads * kD;             // f16 elements between cache rows
-  for (uint32_t j0 = key_begin; j0 < key_end; j0 += kK) {
-    __syncthreads();  // the previous tile's K, V and P are consumed
-    {
-      const uint32_t r = tid >> 2, c = (tid & 3u) * 16u;  // 64 keys x 4 pieces of 16 elements
-      const uint32_t j = j0 + r;
-      uint4 kk[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-      uint4 vv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-      if (j < key_end) {
-        const uint4* ks = reinterpret_cast<const uint4*>(k_cache + (size_t)j * pitch + kv * kD + c);
-        const uint4* vs = reinterpret_cast<const uint4*>(v_cache + (size_t)j * pitch + kv * kD + c);
-        kk[0] = ks[0];
-        kk[1] = ks[1];
-        vv[0] = vs[0];
-        vv[1] = vs[1];
-      }
-      *reinterpret_cast<uint4*>(&Ks[r][c]) = kk[0];
-      *reinterpret_cast<uint4*>(&Ks[r][c + 8]) = kk[1];
-      const uint16_t* vh = reinterpret_cast<const uint16_t*>(vv);
-#pragma unroll
-      for (int e = 0; e < 16; e++) Vt[c + e][r] = vh[e];
-    }
-    __syncthreads();
+  const uint32_t ntiles = key_end > key_begin ? (key_end - key_begin + kK - 1) / kK : 0;
+  const uint32_t limit = d.query_begin + query;  // the last key this query sees
+  // a tile wholly at or below the wave's first query's limit (and inside the keys) needs no mask
+  const uint32_t open_end = min(d.query_begin + q0 + wave * 16 + 1, key_end);
+  // this lane's A-operand rows of S^T blocks n (even, odd): key 32 (n / 2) + 8 (lr / 4) + 4 (n % 2)
+  // + lr % 4, at its swizzled LDS row
+  const uint32_t krow = 8 * (lr >> 2) + (lr & 3u);
+  const uint32_t krows[2] = {ks_row(krow), ks_row(krow + 4)};
 
-    // S = Q K^T, 16 queries x 64 keys per wave.
+  const uint32_t pitch = d.kv_heads * kD * 2u;
+  const KVStream kst{egd::buffer(k_cache, key_end * pitch), egd::buffer(v_cache, key_end * pitch),
+                     (tid >> 2) * pitch + kv * kD * 2u + (tid & 3u) * 32u,
+                     (tid >> 4) * 4u * pitch + kv * kD * 2u + (tid & 15u) * 8u, pitch};
+  KVTile kvt;
+  if (ntiles) {
+    load_tile(kvt, kst, key_begin);
+    store_tile(kvt, Ks[0], Vt[0], tid);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < ntiles; t++) {
+    const uint32_t j0 = key_begin + t * kK, buf = t & 1u;
+    // the next tile's loads stay in flight through this tile's products
+    if (t + 1 < ntiles) load_tile(kvt, kst, j0 + kK);
+
     f32x4 s[4];
 #pragma unroll
     for (int n = 0; n < 4; n++) {
       s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t row = 32 * (n >> 1) + krows[n & 1];
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
-        const half8 kb = *reinterpret_cast<const half8*>(&Ks[16 * n + lr][32 * ks + 8 * lg]);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], kb, s[n], 0, 0, 0);
+        const half8 ka = *reinterpret_cast<const half8*>(&Ks[buf][row][32 * ks + 8 * lg]);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[ks], s[n], 0, 0, 0);
       }
     }
 
-    // Causal mask and the online softmax, per row (4 per lane; a row's 64 keys live in the 16
-    // lanes sharing lg, 4 per lane).
+    // Causal mask (tiles that cross a limit or the last key) and the online softmax: the lane's
+    // 16 scores, then the max over the 4 lanes holding the query (lanes lr, lr + 16, lr + 32,
+    // lr + 48).
+    if (j0 + kK > open_end) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t i = row0 + 4 * lg + e;
-      float mx = kMasked;
+      for (int n = 0; n < 4; n++)
 #pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const uint32_t j = j0 + 16 * n + lr;
-        const float v = (j <= d.query_begin + i && j < d.keys) ? s[n][e] : kMasked;
-        s[n][e] = v;
-        mx = fmaxf(mx, v);
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float mnew = fmaxf(m[e], mx);
-      const float alpha = expf(m[e] - mnew);
-      // a row with no visible key yet (a split wholly past its causal limit) keeps nothing
-      const bool none = mnew == kMasked;
-      float sum = 0.f;
-#pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const float p = none ? 0.f : expf(s[n][e] - mnew);
-        s[n][e] = p;
-        sum += p;
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
-      l[e] = l[e] * alpha + sum;
-      m[e] = mnew;
-#pragma unroll
-      for (int n = 0; n < 4; n++) o[n][e] *= alpha;
+        for (int e = 0; e < 4; e++) {
+          const uint32_t j = j0 + 32 * (n >> 1) + 8 * lg + 4 * (n & 1) + e;
+          if (!(j <= limit && j < key_end)) s[n][e] = kMasked;
+        }
     }
-
-    // P (f16) through LDS into the A-operand layout, then O += P V.
+    float mx = kMasked;
 #pragma unroll
     for (int n = 0; n < 4; n++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) Ps[wave][4 * lg + e][16 * n + lr] = float_to_half(s[n][e]);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P writes are in LDS
-    __builtin_amdgcn_wave_barrier();
+      for (int e = 0; e < 4; e++) mx = fmaxf(mx, s[n][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
+    // a query with no visible key yet (a split wholly past its causal limit) keeps nothing: its
+    // exponent offset is pushed past f32's range below zero
+    const float ml = mnew == kMasked ? 3.0e38f : mnew * kLog2e;
+    float sum = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const half8 pa = *reinterpret_cast<const half8*>(&Ps[wave][lr][32 * ks + 8 * lg]);
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[n][e], kLog2e, -ml));
+        s[n][e] = p;
+        sum += p;
+      }
+    l = l * alpha + sum;
+    // the accumulators are rescaled only when some query of the wave found a larger max
+    if (__builtin_amdgcn_ballot_w64(mnew > m) != 0) {
+#pragma unroll
+      for (int n = 0; n < 4; n++) o[n] *= alpha;
+    }
+    m = mnew;
+
+    // O^T += V^T P^T over the two halves of the tile.
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const half8 pb = half8{(_Float16)s[2 * hh][0],     (_Float16)s[2 * hh][1],     (_Float16)s[2 * hh][2],
+                             (_Float16)s[2 * hh][3],     (_Float16)s[2 * hh + 1][0], (_Float16)s[2 * hh + 1][1],
+                             (_Float16)s[2 * hh + 1][2], (_Float16)s[2 * hh + 1][3]};
 #pragma unroll
       for (int n = 0; n < 4; n++) {
-        const half8 vb = *reinterpret_cast<const half8*>(&Vt[16 * n + lr][32 * ks + 8 * lg]);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[n], 0, 0, 0);
+        const half8 va = *reinterpret_cast<const half8*>(&Vt[buf][16 * n + lr][32 * hh + 8 * lg]);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[n], 0, 0, 0);
       }
     }
+    // the other buffer was last read in the previous iteration, before the barrier that ended it
+    if (t + 1 < ntiles) store_tile(kvt, Ks[buf ^ 1u], Vt[buf ^ 1u], tid);
+    __syncthreads();
   }
 
+  // the query's sum over its 4 lanes
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (query >= d.queries) return;
+  if (sp.o) {
+    const size_t row = ((size_t)blockIdx.z * d.queries + query) * d.heads + h;
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const uint32_t i = row0 + 4 * lg + e;
-    if (i >= d.queries) continue;
-    if (sp.o) {
-      const size_t row = ((size_t)blockIdx.z * d.queries + i) * d.heads + h;
-#pragma unroll
-      for (int n = 0; n < 4; n++) sp.o[row * kD + 16 * n + lr] = o[n][e];
-      if (lr == 0) {
-        float* ml = sp.o + (size_t)sp.count * d.queries * d.heads * kD;
-        ml[row] = m[e];
-        ml[(size_t)sp.count * d.queries * d.heads + row] = l[e];
-      }
-      continue;
+    for (int n = 0; n < 4; n++)
+      *reinterpret_cast<float4*>(&sp.o[row * kD + 16 * n + 4 * lg]) = make_float4(o[n][0], o[n][1], o[n][2], o[n][3]);
+    if (lg == 0) {
+      float* mlp = sp.o + (size_t)sp.count * d.queries * d.heads * kD;
+      mlp[row] = m;
+      mlp[(size_t)sp.count * d.queries * d.heads + row] = l;
     }
-    const float inv = 1.0f / l[e];
-#pragma unroll
-    for (int n = 0; n < 4; n++) out[((size_t)i * d.heads + h) * kD + 16 * n + lr] = o[n][e] * inv;
+    return;
   }
+  const float inv = 1.0f / l;
+  float* dst = out + ((size_t)query * d.heads + h) * kD + 4 * lg;
+#pragma unroll
+  for (int n = 0; n < 4; n++)
+    *reinterpret_cast<float4*>(dst + 16 * n) = make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
 }
 
 // The splits merged: out = sum_z o_z e^(m_z - M) / sum_z l_z e^(m_z - M), M = max_z m_z, splits
-// in order (an empty split has m = NEG_LARGE and l = 0, weight 0).
+// in order (an empty split has m = NEG_LARGE and l = 0, weight 0, and its o is not read). One
+// thread per 4 elements of a row.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                       uint32_t rows, uint32_t splits) {
   const size_t total = (size_t)rows * kD;
   const float* m = part + (size_t)splits * total;
   const float* l = m + (size_t)splits * rows;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (size_t)gridDim.x * blockDim.x) {
-    const size_t row = idx / kD;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total / 4; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = idx / (kD / 4);
     float M = kMasked;
     for (uint32_t z = 0; z < splits; z++) M = fmaxf(M, m[(size_t)z * rows + row]);
-    float L = 0.f, acc = 0.f;
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t z = 0; z < splits; z++) {
-      const float w = l[(size_t)z * rows + row] > 0.f ? expf(m[(size_t)z * rows + row] - M) : 0.f;
-      L = fmaf(l[(size_t)z * rows + row], w, L);
-      acc = fmaf(part[(size_t)z * total + idx], w, acc);
+      const float lz = l[(size_t)z * rows + row];
+      if (!(lz > 0.f)) continue;
+      const float w = expf(m[(size_t)z * rows + row] - M);
+      L = fmaf(lz, w, L);
+      const float4 v = reinterpret_cast<const float4*>(part + (size_t)z * total)[idx];
+      acc.x = fmaf(v.x, w, acc.x);
+      acc.y = fmaf(v.y, w, acc.y);
+      acc.z = fmaf(v.z, w, acc.z);
+      acc.w = fmaf(v.w, w, acc.w);
     }
-    out[idx] = acc / L;
+    reinterpret_cast<float4*>(out)[idx] = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
   }
 }
 
@@ -273,6 +347,11 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
                     (unsigned long long)d.query_begin + d.queries, d.max_context);
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches must be 16-byte aligned", op);
+  if ((reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: q_rope and out must be 16-byte aligned", op);
+  if ((uint64_t)d.max_context * d.kv_heads * d.head_dim * 2 >= (1ull << 31))
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: a cache of %u positions x %u kv heads exceeds 2 GiB", op, d.max_context,
+                    d.kv_heads);
   if (d.heads > 65535 || (d.queries + kQ - 1) / kQ > 0x7FFFFFFFu)
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads over the grid limit", op, d.heads);
   hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
@@ -285,11 +364,12 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
   const uint32_t blocks = (d.queries + kQ - 1) / kQ;
   const uint64_t grid = (uint64_t)blocks * d.heads;
   const uint32_t tiles = (d.keys + kK - 1) / kK;
+  const uint32_t cap = ctx->attention_split_tiles;
+  const uint64_t target = (uint64_t)ctx->cu_count * ctx->attention_split_fill;
   uint32_t splits = 1;
   if (tiles >= 8) {
-    if (grid < (uint64_t)ctx->cu_count)
-      splits = (uint32_t)std::min<uint64_t>((ctx->cu_count + grid - 1) / grid, tiles / 4);
-    splits = std::max(splits, (tiles + 7) / 8);
+    if (grid < target) splits = (uint32_t)std::min<uint64_t>((target + grid - 1) / grid, tiles / 4);
+    splits = std::max(splits, (tiles + cap - 1) / cap);
   }
   const uint64_t rows = (uint64_t)d.queries * d.heads;
   while (splits > 1 && (uint64_t)splits * rows * (kD + 2) * 4 > eg::kPartialsBytes) splits--;
@@ -303,7 +383,7 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
                      v_cache, out, d, sp);
   if (sp.o) {
     const uint64_t total = rows * kD;
-    const uint32_t cblocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, (uint64_t)ctx->cu_count * 8);
+    const uint32_t cblocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256, (uint64_t)ctx->cu_count * 8);
     hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count);
   }
   return eg::check_launch(ctx, op);
