@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_buf_zero": (_i, [_vp, _vp, _sz, _sz]),
     "eg_matmul_q4_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_matmul_q4_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "eg_matmul_q4_prefill_swiglu": (_i, [_vp] * 11 + [_i, _i]),
     "eg_lm_head": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_lm_head_argmax": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_lm_head_argmax_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),

@@ -272,11 +272,11 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
                               d->v_cache + l * d->layer_stride, d->pqr, d->patt, &ad);
     gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
     if (st == EG_OK) st = eg::rmsnorm_rows(ctx, d->ph[1], L.post_attention_norm, count, H, m.rms_eps, d->pxn);
-    // gate and up in one launch, side by side in each row of pgu
-    const eg::PrefillMatrix gu[2] = {{L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, nullptr, d->pgu, I, 2 * I, 0},
-                                     {L.up.packed, L.up.scales, L.up.zeros, nullptr, nullptr, d->pgu, I, 2 * I, I}};
-    if (st == EG_OK) st = eg::prefill_gemm_multi(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, gu, 2);
-    if (st == EG_OK) st = eg::silu_mul_rows(ctx, d->pgu, count, I, d->pa);
+    // SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch form's rows)
+    const eg::PrefillMatrix gate{L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, nullptr, d->pa, I, I, 0};
+    const eg::PrefillMatrix up{L.up.packed, L.up.scales, L.up.zeros, nullptr, nullptr, d->pa, I, I, 0};
+    if (st == EG_OK)
+      st = eg::prefill_gemm_swiglu(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, gate, up, d->pa, d->pgu);
     gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0);  // ph0 = ph1 + down(...)
   }
   return st;

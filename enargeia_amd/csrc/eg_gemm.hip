@@ -238,13 +238,21 @@ __device__ void stage_elements(const PrefillArgs& a, const PrefillMat& w, uint32
   }
 }
 
+// SiLU(g) * u with SiLU(g) = g / (1 + e^-g), the prompt chain's silu_mul_rows formula.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // KG groups of 4 waves share a workgroup and a tile: group g stages and multiplies the 64-deep
 // blocks g, g + KG, ... of the workgroup's K range into its own accumulators (its own LDS
 // buffers; one barrier pair per KG blocks), and the groups' sums are added in group order at the
 // end. With one workgroup per CU (the tile grids here hold ~1 per CU) a single group leaves
 // every SIMD one wave, so each block's staging, LDS round trip, barriers and MFMAs run back to
 // back; KG groups put KG waves on each SIMD and cut the serial chain by KG.
-template <int ENC, bool CHUNKED, int KG>
+//
+// PAIR (the gate|up SwiGLU pair, chunked staging only): tile column t holds rows 32t .. 32t+31 of
+// mats[0] (gate) in its first 32 columns and the same rows of mats[1] (up) in the last 32 - waves
+// 0-1 of a group stage gate rows, waves 2-3 up rows - and the epilogue stores SiLU(gate) * up for
+// the 32 columns into mats[0].out.
+template <int ENC, bool CHUNKED, int KG, bool PAIR = false>
 __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   // staging buffers of every group; after the K loop they hold the groups' f32 sums
   constexpr uint32_t kStageBytes = 2u * kTile * kLds * 2u;  // As + Bs of one group
@@ -253,9 +261,13 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   const uint32_t group = threadIdx.x >> 8;
   uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
   uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
-  const PrefillMat& w = a.mats[select_matrix(a, blockIdx.x)];
-  const uint32_t m0 = blockIdx.y * kTile, n0 = (blockIdx.x - (w.tiles_end - ((w.n + kTile - 1) / kTile))) * kTile;
   const uint32_t tid = threadIdx.x & 255u, wave = tid >> 6, lane = tid & 63u;
+  // the matrix whose rows this thread stages (wave-uniform), and the tile's first row of it
+  const uint32_t half = PAIR ? __builtin_amdgcn_readfirstlane(wave >> 1) : 0u;
+  const PrefillMat& w = a.mats[PAIR ? half : select_matrix(a, blockIdx.x)];
+  const uint32_t m0 = blockIdx.y * kTile;
+  const uint32_t n0 = PAIR ? 32u * blockIdx.x - 32u * half
+                           : (blockIdx.x - (w.tiles_end - ((w.n + kTile - 1) / kTile))) * kTile;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
 
@@ -337,7 +349,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
       __syncthreads();
     }
   }
-  if (KG > 1) {
+  if (KG > 1 || PAIR) {
     // every group's sums into its own buffers (the last barrier above ended the staging), then
     // the groups added in order by the thread that stores the element
     float* sums = reinterpret_cast<float*>(lds + group * kStageBytes);
@@ -349,6 +361,25 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
         for (int e = 0; e < 4; e++)
           sums[(wm + i * 16 + 4 * (lane >> 4) + e) * kTile + wn + j * 16 + (lane & 15)] = acc[i][j][e];
     __syncthreads();
+    if (PAIR) {
+      const PrefillMat& g = a.mats[0];
+      const PrefillMat& u = a.mats[1];
+      for (uint32_t idx = threadIdx.x; idx < kTile * 32u; idx += 256u * KG) {
+        const uint32_t r = idx / 32u, c = idx % 32u, row = m0 + r, col = 32u * blockIdx.x + c;
+        if (row >= a.m || col >= g.n) continue;
+        float gv = reinterpret_cast<const float*>(lds)[r * kTile + c];
+        float uv = reinterpret_cast<const float*>(lds)[r * kTile + c + 32u];
+#pragma unroll
+        for (int k = 1; k < KG; k++) {
+          gv += reinterpret_cast<const float*>(lds + k * kStageBytes)[r * kTile + c];
+          uv += reinterpret_cast<const float*>(lds + k * kStageBytes)[r * kTile + c + 32u];
+        }
+        gv = gv + (g.bias ? g.bias[col] : 0.f) + 0.f;
+        uv = uv + (u.bias ? u.bias[col] : 0.f) + 0.f;
+        g.out[(size_t)row * g.out_stride + col + g.out_offset] = silu_mul(gv, uv);
+      }
+      return;
+    }
     for (uint32_t idx = threadIdx.x; idx < kTile * kTile; idx += 256u * KG) {
       const uint32_t r = idx / kTile, c = idx % kTile, row = m0 + r, col = n0 + c;
       if (row >= a.m || col >= w.n) continue;
@@ -486,6 +517,29 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   return eg::check_launch(ctx, op);
 }
 
+namespace {
+
+// Whether matrices sharing x run in ONE launch: the chunked staging takes every one of them and
+// no K split is wanted. Sets the total of their 64-column tiles.
+bool one_launch(const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding, int bits,
+                const eg::PrefillMatrix* mats, uint32_t count, uint64_t* tiles_n) {
+  bool ok = count >= 1 && count <= kMaxSegs && m > 0 && x && bits == 4 &&
+            (encoding == EG_ENC_SIGNED || encoding == EG_ENC_OFFSET_ZEROS) && block_size >= 16 &&
+            (block_size & (block_size - 1)) == 0 && k % block_size == 0 && k % 32 == 0 &&
+            (k + kBK - 1) / kBK < 32 && (uint64_t)m * k * 4 < kOutside && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  *tiles_n = 0;
+  for (uint32_t i = 0; ok && i < count; i++) {
+    const eg::PrefillMatrix& w = mats[i];
+    ok = w.n > 0 && w.packed && w.scales && w.out && (encoding == EG_ENC_SIGNED || w.zeros) &&
+         (m == 1 || w.out_stride >= w.n) && (uint64_t)w.n * k / 2 < kOutside &&
+         (uint64_t)w.n * (k / block_size) < (1ull << 32) && (reinterpret_cast<uintptr_t>(w.packed) & 7u) == 0;
+    *tiles_n += (w.n + kTile - 1) / kTile;
+  }
+  return ok && *tiles_n <= 0x7FFFFFFFull && (m + kTile - 1) / kTile <= 65535;
+}
+
+}  // namespace
+
 int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
                            int encoding, int bits, const PrefillMatrix* mats, uint32_t count) {
   const char* op = "matmul_q4_prefill";
@@ -505,21 +559,9 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
   };
   // One launch where the chunked staging takes every matrix and no matrix would split K;
   // otherwise (and for anything the single path must reject with its own message) one each.
-  bool together = count >= 2 && count <= kMaxSegs && m > 0 && x && bits == 4 &&
-                  (encoding == EG_ENC_SIGNED || encoding == EG_ENC_OFFSET_ZEROS) && block_size >= 16 &&
-                  (block_size & (block_size - 1)) == 0 && k % block_size == 0 && k % 32 == 0 &&
-                  (k + kBK - 1) / kBK < 32 && (uint64_t)m * k * 4 < kOutside &&
-                  (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   uint64_t tiles_n = 0;
-  for (uint32_t i = 0; together && i < count; i++) {
-    const PrefillMatrix& w = mats[i];
-    together = w.n > 0 && w.packed && w.scales && w.out && (encoding == EG_ENC_SIGNED || w.zeros) &&
-               (m == 1 || w.out_stride >= w.n) && (uint64_t)w.n * k / 2 < kOutside &&
-               (uint64_t)w.n * (k / block_size) < (1ull << 32) && (reinterpret_cast<uintptr_t>(w.packed) & 7u) == 0;
-    tiles_n += (w.n + kTile - 1) / kTile;
-  }
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
-  if (!together || tiles_n > 0x7FFFFFFFull || tiles_m > 65535) {
+  if (count < 2 || !one_launch(x, m, k, block_size, encoding, bits, mats, count, &tiles_n)) {
     for (uint32_t i = 0; i < count; i++) {
       const int st = one(mats[i]);
       if (st != EG_OK) return st;
@@ -547,6 +589,71 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
   else EG_PREFILL_MULTI(EG_ENC_OFFSET_ZEROS);
 #undef EG_PREFILL_MULTI
   return eg::check_launch(ctx, op);
+}
+
+int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
+                            int encoding, int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out,
+                            float* scratch) {
+  const char* op = "matmul_q4_prefill";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!out || !scratch || gate.n != up.n)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: SwiGLU pair needs matching gate and up and two outputs", op);
+  const uint32_t n = gate.n;
+  // the pair as ONE launch of paired tiles where the chunked staging takes both and K is short
+  const PrefillMatrix pair[2] = {{gate.packed, gate.scales, gate.zeros, gate.bias, nullptr, out, n, n, 0},
+                                 {up.packed, up.scales, up.zeros, up.bias, nullptr, out, n, n, 0}};
+  uint64_t tiles_n = 0;
+  if (n == 0 || m == 0 || !ctx->prefill_pair || !one_launch(x, m, k, block_size, encoding, bits, pair, 2, &tiles_n)) {
+    // otherwise gate | up side by side in the scratch rows, then SiLU(gate) * up
+    const PrefillMatrix gu[2] = {{gate.packed, gate.scales, gate.zeros, gate.bias, nullptr, scratch, n, 2 * n, 0},
+                                 {up.packed, up.scales, up.zeros, up.bias, nullptr, scratch, n, 2 * n, n}};
+    int st = eg::prefill_gemm_multi(ctx, x, m, k, block_size, encoding, bits, gu, 2);
+    if (st == EG_OK && m > 0 && n > 0) st = eg::silu_mul_rows(ctx, scratch, m, n, out);
+    return st;
+  }
+  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u, {}};
+  const uint32_t tiles_x = (n + 31) / 32;
+  for (int i = 0; i < 2; i++) {
+    const PrefillMatrix& w = pair[i];
+    a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, nullptr,
+                           w.out, n, n, 0, tiles_x};
+  }
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  const int kg = ctx->prefill_groups ? ctx->prefill_groups : ((uint64_t)tiles_x * tiles_m >= (uint64_t)ctx->cu_count ? 1 : 4);
+  const dim3 grid(tiles_x, (uint32_t)tiles_m, 1);
+  const dim3 block(256 * kg);
+#define EG_PREFILL_PAIR(ENC)                                                                              \
+  do {                                                                                                    \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, true>), grid, block, 0, ctx->stream, a);   \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, true>), grid, block, 0, ctx->stream, a); \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, true>), grid, block, 0, ctx->stream, a);           \
+  } while (0)
+  if (encoding == EG_ENC_SIGNED) EG_PREFILL_PAIR(EG_ENC_SIGNED);
+  else EG_PREFILL_PAIR(EG_ENC_OFFSET_ZEROS);
+#undef EG_PREFILL_PAIR
+  return eg::check_launch(ctx, op);
+}
+
+extern "C" int eg_matmul_q4_prefill_swiglu(eg_context* ctx, const float* x, const uint32_t* gate_packed,
+                                           const float* gate_scales, const uint32_t* gate_zeros,
+                                           const uint32_t* up_packed, const float* up_scales, const uint32_t* up_zeros,
+                                           float* out, float* scratch, const eg_matmul_q4_dims* dims, int encoding,
+                                           int bits) {
+  const char* op = "matmul_q4_prefill_swiglu";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!dims || !x || !gate_packed || !gate_scales || !up_packed || !up_scales || !out || !scratch)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if (dims->use_bias || dims->out_offset != 0 || (dims->m > 1 && dims->out_stride != dims->n))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: no bias, out_stride n and out_offset 0 are required", op);
+  if (dims->block_size == 0 || dims->k % dims->block_size != 0 || dims->blocks_per_row != dims->k / dims->block_size)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: k %u, block size %u and blocks per row %u disagree", op, dims->k,
+                    dims->block_size, dims->blocks_per_row);
+  if (dims->n % 4 != 0 || (reinterpret_cast<uintptr_t>(scratch) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: n %u must be a multiple of 4 and out, scratch 16-byte aligned", op,
+                    dims->n);
+  const eg::PrefillMatrix gate{gate_packed, gate_scales, gate_zeros, nullptr, nullptr, out, dims->n, dims->n, 0};
+  const eg::PrefillMatrix up{up_packed, up_scales, up_zeros, nullptr, nullptr, out, dims->n, dims->n, 0};
+  return eg::prefill_gemm_swiglu(ctx, x, dims->m, dims->k, dims->block_size, encoding, bits, gate, up, out, scratch);
 }
 
 extern "C" int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,

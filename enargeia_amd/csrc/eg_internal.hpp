@@ -43,6 +43,8 @@ struct eg_context {
   int prefill_groups = 0;
   // chunk attention's key split: at most this many 64-key tiles per workgroup, and a small grid
   // split up to this many workgroups per CU
+  // the SwiGLU pair as one launch of paired gate|up tiles (false: gate | up, then silu_mul_rows)
+  bool prefill_pair = true;
   uint32_t attention_split_tiles = 8;
   uint32_t attention_split_fill = 1;
   // Resident workgroups per CU of each kernel launched through this context (from
@@ -156,6 +158,11 @@ struct PrefillMatrix {
 };
 int prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
                        int bits, const PrefillMatrix* mats, uint32_t count);
+// The SwiGLU pair: out[r][j] = SiLU(x[r] . gate_j + bias) * (x[r] . up_j + bias), j < gate.n, rows
+// gate.n apart (the outputs and strides in gate and up are ignored). One launch of paired tiles
+// where the staging allows; otherwise gate | up into `scratch` ([m][2 n]) and silu_mul_rows.
+int prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
+                        int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out, float* scratch);
 
 // Row-wise kernels of the prefill chain (one workgroup per row):
 //   embed_rows: out[r] = the dequantized table row of ids[r] (ops.ts:222-233), r < rows;

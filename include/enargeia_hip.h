@@ -149,6 +149,19 @@ EG_API int eg_matmul_q4_prefill(eg_context* ctx, const float* x, const uint32_t*
                          const float* scales, const uint32_t* zeros, const float* bias,
                          float* out, const eg_matmul_q4_dims* dims, int encoding, int bits);
 
+/* The prompt MLP's gate and up projections and silu_mul in one operator (graph.ts:484-497:
+ * mlp_gate and mlp_up through matmul_q4_prefill, then SILU_MUL, silu_mul.wgsl): for m rows of x,
+ *   out[r*n + j] = silu(x[r] . gate_j) * (x[r] . up_j),  silu(g) = g / (1 + e^-g),  j < n
+ * with the prefill GEMM's arithmetic (bf16 operands, f32 accumulation). gate and up share the
+ * dims (n rows of k each; use_bias must be 0, out_stride n, out_offset 0), the encoding and
+ * the bits. One launch where the chunked staging takes both matrices and K is at most 1984;
+ * otherwise gate | up side by side into scratch ([m][2n] floats, required) and silu_mul. */
+EG_API int eg_matmul_q4_prefill_swiglu(eg_context* ctx, const float* x, const uint32_t* gate_packed,
+                                       const float* gate_scales, const uint32_t* gate_zeros,
+                                       const uint32_t* up_packed, const float* up_scales,
+                                       const uint32_t* up_zeros, float* out, float* scratch,
+                                       const eg_matmul_q4_dims* dims, int encoding, int bits);
+
 /* lm_head_<dtype> (embedding_variants.ts:135-180, q8 body :56-63): for row < row_count,
  *   out[row + out_offset] = sum_k x[k] * (code - zero) * scale[block]
  * bits = 8 (lm_head_q8, the shipped tied head) or 4 (lm_head_q4). */

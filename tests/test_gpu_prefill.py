@@ -140,3 +140,91 @@ def test_prefill_deterministic(device):
     a = run_prefill(device, x, q, None, 128)
     b = run_prefill(device, x, q, None, 128)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def run_swiglu(device, x, gate, up, m):
+    """eg_matmul_q4_prefill_swiglu through the C ABI: SiLU(x . gate) * (x . up), [m][n]."""
+    import ctypes
+    from enargeia_amd import _lib
+    n, k = gate.rows, gate.cols
+    opt = lambda a: device.upload(a) if a is not None else None
+    bufs = [device.upload(x), device.upload(gate.packed), device.upload(gate.scales), opt(gate.zeros),
+            device.upload(up.packed), device.upload(up.scales), opt(up.zeros)]
+    out, scratch = device.buffer(m * n * 4), device.buffer(m * 2 * n * 4)
+    d = K.MatmulDims.from_buffer_copy(K.matmul_q4_dims(m, n, k, False, gate.block_size, n, 0))
+    vp = lambda b: ctypes.c_void_p(b.ptr if b is not None else None)
+    try:
+        _lib.check(_lib.load().eg_matmul_q4_prefill_swiglu(device.ctx, *[vp(b) for b in bufs], vp(out), vp(scratch),
+                                                            ctypes.byref(d), gate.encoding, gate.bits), device.ctx)
+        return device.read_array(out, np.float32, m * n)
+    finally:
+        for b in bufs + [out, scratch]:
+            if b is not None:
+                b.release()
+
+
+@pytest.fixture(scope="module")
+def unpaired():
+    """A second context whose SwiGLU operator always takes the two-launch form."""
+    import os
+    os.environ["EG_PREFILL_PAIR"] = "0"
+    try:
+        dev = K.Device(0)
+    finally:
+        del os.environ["EG_PREFILL_PAIR"]
+    yield dev
+    dev.close()
+
+
+@pytest.mark.parametrize("m,n,k,sym", [(256, 4864, 896, True), (200, 1000, 896, False), (3, 100, 64, True),
+                                       (70, 4864, 4864, True)])
+def test_prefill_swiglu_pair(device, unpaired, m, n, k, sym):
+    # The prompt MLP's gate / up / silu_mul (graph.ts:484-497) as one operator: gate and up rows
+    # side by side in paired tiles, SiLU(g) * u in the epilogue. Each projection's f32 sums are
+    # the plain GEMM's to the bit (same staging, MFMA order and group split at these shapes), so
+    # the result equals the two-launch form (gate | up into the scratch rows, then
+    # silu_mul_rows) bit for bit, and SiLU·up of two eg_matmul_q4_prefill outputs computed on the
+    # host up to the exponential's and the division's last bits (numpy's float32 exp against the
+    # device's expf: 6 ulp measured at most). K = 4864 takes the two-launch form on both.
+    x = oracle.random_floats(m * k, 41)
+    if sym:
+        gate = oracle.quantize_sym(oracle.normal_floats(n * k, 42, 0.05), n, k, 4, 32)
+        up = oracle.quantize_sym(oracle.normal_floats(n * k, 43, 0.05), n, k, 4, 32)
+    else:
+        gate = oracle.quantize_q4_ref(oracle.random_floats(n * k, 42), n, k)
+        up = oracle.quantize_q4_ref(oracle.random_floats(n * k, 43), n, k)
+    got = run_swiglu(device, x, gate, up, m).reshape(m, n)
+    two = run_swiglu(unpaired, x, gate, up, m).reshape(m, n)
+    np.testing.assert_array_equal(got.view(np.uint32), two.view(np.uint32))
+    g = run_prefill(device, x, gate, None, m).reshape(m, n)
+    u = run_prefill(device, x, up, None, m).reshape(m, n)
+    want = g / (np.float32(1) + np.exp(-g)) * u
+    np.testing.assert_array_max_ulp(got, want.astype(np.float32), maxulp=16)
+    # and the fp32 reference: each projection's bar (|a - e| <= 2e-2 (|e| + rms(e))) carried
+    # through SiLU(g) * u to first order: |d| <= |SiLU'(g) u| bar_g + |SiLU(g)| bar_u
+    gf = oracle.linear_q_fast(x, gate, None, m).reshape(m, n).astype(np.float64)
+    uf = oracle.linear_q_fast(x, up, None, m).reshape(m, n).astype(np.float64)
+    sig = 1 / (1 + np.exp(-gf))
+    ref = gf * sig * uf
+    bar = lambda e: 2e-2 * (np.abs(e) + np.sqrt(np.mean(e ** 2)))
+    bound = np.abs(sig * (1 + gf * (1 - sig)) * uf) * bar(gf) + np.abs(gf * sig) * bar(uf)
+    excess = np.abs(got - ref) / bound
+    assert excess.max() <= 1.0, f"swiglu {m}x{n}x{k}: {excess.max() * 100:.1f}% of the carried bar"
+
+
+def test_prefill_swiglu_rejects_bad_dims(device):
+    import ctypes
+    from enargeia_amd import _lib
+    lib = _lib.load()
+    buf = device.buffer(4096)
+    p = ctypes.c_void_p(buf.ptr)
+    try:
+        for dims, what in ((K.matmul_q4_dims(4, 64, 64, True, 32, 64, 0), "bias"),
+                           (K.matmul_q4_dims(4, 64, 64, False, 32, 96, 0), "stride"),
+                           (K.matmul_q4_dims(4, 62, 64, False, 32, 62, 0), "n % 4")):
+            d = K.MatmulDims.from_buffer_copy(dims)
+            st = lib.eg_matmul_q4_prefill_swiglu(device.ctx, p, p, p, None, p, p, None, p, p, ctypes.byref(d),
+                                                 K.ENC_SIGNED, 4)
+            assert st != 0, what
+    finally:
+        buf.release()

@@ -133,3 +133,37 @@ def test_prefill_chain_config4(device):
     finally:
         dec.close()
         dm.release()
+
+
+@pytest.mark.parametrize("chunk", [None, 64])
+def test_prefill_swiglu_pair_matches_two_launches_bit_exactly(device, chunk):
+    """gate|up as one launch of paired tiles with SiLU·up in its epilogue (the default) gives the
+    logits, to the bit, of gate | up in one launch followed by silu_mul_rows (a second context
+    created with EG_PREFILL_PAIR=0): the same sums in the same order, the same SiLU."""
+    import os
+    from enargeia_amd import kernels as K
+    os.environ["EG_PREFILL_PAIR"] = "0"
+    try:
+        other = K.Device(0)
+    finally:
+        del os.environ["EG_PREFILL_PAIR"]
+    cfg = ModelConfig(layers=2, max_context=512)
+    m = synthetic_model(cfg)
+    prompt = [int(t) for t in oracle.random_ids(300, 77, cfg.vocab)]
+    runs = []
+    try:
+        for dev in (device, other):
+            dm = DeviceModel(dev, m)
+            dec = Decoder(dm)
+            try:
+                if chunk:
+                    dec.set_prefill_chunk(chunk)
+                tok = dec.prefill(0, prompt)
+                runs.append((tok, dec.logits().copy()))
+            finally:
+                dec.close()
+                dm.release()
+    finally:
+        other.close()
+    assert runs[0][0] == runs[1][0]
+    np.testing.assert_array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
