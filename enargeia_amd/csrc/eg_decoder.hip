@@ -258,25 +258,26 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
   };
   for (uint32_t l = 0; l < m.layers && st == EG_OK; l++) {
     const eg_layer_desc& L = d->layers[l];
-    st = eg::rmsnorm_rows(ctx, d->ph[0], L.input_norm, count, H, m.rms_eps, d->pxn);
-    // q, k and v in one launch (they share the normed rows)
+    // RMSNorm, then q, k and v in one launch (they share the normed rows; the norm folded in)
     const eg::PrefillMatrix qkv[3] = {
         {L.q.packed, L.q.scales, L.q.zeros, L.q_bias, nullptr, d->pq, H, H, 0},
         {L.k.packed, L.k.scales, L.k.zeros, L.k_bias, nullptr, d->pk, kvn, kvn, 0},
         {L.v.packed, L.v.scales, L.v.zeros, L.v_bias, nullptr, d->pv, kvn, kvn, 0}};
-    if (st == EG_OK) st = eg::prefill_gemm_multi(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, qkv, 3);
+    st = eg::prefill_gemm_multi(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, 3, L.input_norm,
+                                m.rms_eps, d->pxn);
     if (st != EG_OK) break;
     eg_attention_prefill_dims ad{count, begin + count, begin, m.heads, m.kv_heads, m.head_dim, m.max_context,
                                  m.rope_theta};
     st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, d->k_cache + l * d->layer_stride,
                               d->v_cache + l * d->layer_stride, d->pqr, d->patt, &ad);
     gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
-    if (st == EG_OK) st = eg::rmsnorm_rows(ctx, d->ph[1], L.post_attention_norm, count, H, m.rms_eps, d->pxn);
-    // SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch form's rows)
+    // RMSNorm and SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch
+    // form's rows)
     const eg::PrefillMatrix gate{L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, nullptr, d->pa, I, I, 0};
     const eg::PrefillMatrix up{L.up.packed, L.up.scales, L.up.zeros, nullptr, nullptr, d->pa, I, I, 0};
     if (st == EG_OK)
-      st = eg::prefill_gemm_swiglu(ctx, d->pxn, count, H, m.block_size, m.encoding, m.bits, gate, up, d->pa, d->pgu);
+      st = eg::prefill_gemm_swiglu(ctx, d->ph[1], count, H, m.block_size, m.encoding, m.bits, gate, up, d->pa, d->pgu,
+                                   L.post_attention_norm, m.rms_eps, d->pxn);
     gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0);  // ph0 = ph1 + down(...)
   }
   return st;

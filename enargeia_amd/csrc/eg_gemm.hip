@@ -56,6 +56,8 @@ struct PrefillArgs {
   int bits;
   uint32_t block_shift;  // log2(block_size) (the chunked staging takes power-of-two blocks)
   uint32_t nmats;        // matrices in mats (> 1: no K split)
+  const float* norm;     // NORM launches: x is RMS-normalised per row with these weights (no K split)
+  float eps;
   PrefillMat mats[kMaxSegs];
 };
 
@@ -89,6 +91,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 // tid / 4, codes 16 * (tid % 4) .. +16 of the block - with their block's scale and zero-point.
 struct Staged {
   float4 x[4];
+  float4 g;  // NORM: the norm weights of the 4 x columns
   uint2 q;
   float s;
   float z;
@@ -98,7 +101,7 @@ struct Staged {
 // memory, so a block's edge needs no branch (a branch around a load makes the compiler wait
 // for it on the spot, which would serialize the stages).
 struct Streams {
-  __amdgpu_buffer_rsrc_t x, w, s, z;
+  __amdgpu_buffer_rsrc_t x, w, s, z, g;
 };
 constexpr uint32_t kOutside = 0x80000000u;  // an offset past every stream (streams < 2 GiB here)
 
@@ -130,7 +133,7 @@ __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, const Pref
   return b;
 }
 
-template <int ENC>
+template <int ENC, bool NORM>
 __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& r, const StageBase& b, uint32_t k0,
                                            Staged& st) {
   const bool xin = k0 + b.xc < a.k;
@@ -138,6 +141,10 @@ __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& 
   for (int i = 0; i < 4; i++) {
     const egd::u32x4 v = egd::load_b128(r.x, xin && b.x[i] != kOutside ? b.x[i] + k0 * 4u : kOutside);
     st.x[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
+  if (NORM) {
+    const egd::u32x4 v = egd::load_b128(r.g, xin ? (k0 + b.xc) * 4u : kOutside);
+    st.g = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   }
   const bool in = b.w != kOutside && k0 + b.kc < a.k;
   const uint32_t blk = b.sblk + ((k0 + b.kc) >> a.block_shift);
@@ -152,15 +159,17 @@ __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& 
   }
 }
 
-template <int ENC>
+template <int ENC, bool NORM>
 __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds]) {
   const uint32_t tid = threadIdx.x & 255u;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t idx = tid + i * 256u;
     const uint32_t r = idx >> 4, c = (idx & 15u) * 4u;
-    *reinterpret_cast<uint2*>(&As[r][c]) =
-        make_uint2(pack_bf16(st.x[i].x, st.x[i].y), pack_bf16(st.x[i].z, st.x[i].w));
+    // NORM: x times its column's norm weight here, the row's 1 / rms in the epilogue
+    const float4 v = NORM ? make_float4(st.x[i].x * st.g.x, st.x[i].y * st.g.y, st.x[i].z * st.g.z, st.x[i].w * st.g.w)
+                          : st.x[i];
+    *reinterpret_cast<uint2*>(&As[r][c]) = make_uint2(pack_bf16(v.x, v.y), pack_bf16(v.z, v.w));
   }
   // (code - zero) * scale in f32, exactly the reference's dequantElement, then bf16. Each word's
   // low and high nibbles are masked in place (the high ones stay 16x, their scale is divided
@@ -252,12 +261,19 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // mats[0] (gate) in its first 32 columns and the same rows of mats[1] (up) in the last 32 - waves
 // 0-1 of a group stage gate rows, waves 2-3 up rows - and the epilogue stores SiLU(gate) * up for
 // the 32 columns into mats[0].out.
-template <int ENC, bool CHUNKED, int KG, bool PAIR = false>
+//
+// NORM (chunked staging, no K split): x is a residual row, RMS-normalised on the way in - each
+// staged x value times its column's norm weight before the bf16 rounding, each thread summing
+// the squares of the x it stages; the rows' sums meet in LDS after the K loop and the epilogue
+// scales each output row by 1 / sqrt(sum / K + eps) (rmsnorm_rows' formula, with the row's
+// scale applied after the products instead of before them).
+template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false>
 __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   // staging buffers of every group; after the K loop they hold the groups' f32 sums
   constexpr uint32_t kStageBytes = 2u * kTile * kLds * 2u;  // As + Bs of one group
   static_assert(kStageBytes >= kTile * kTile * 4u, "a group's buffers hold its 64 x 64 f32 sums");
   __shared__ __attribute__((aligned(16))) uint8_t lds[KG * kStageBytes];
+  __shared__ float row_ss[NORM ? KG : 1][kTile];  // NORM: each group's sums of squares per row
   const uint32_t group = threadIdx.x >> 8;
   uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
   uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
@@ -312,20 +328,32 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     constexpr int S = KG >= 4 ? 2 : kStages;
     const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(w.packed, w.n * a.k / 2u),
                      egd::buffer(w.scales, w.n * a.blocks_per_row * 4u),
-                     egd::buffer(w.zeros, ((w.n * a.blocks_per_row + 7u) / 8u) * 4u)};
+                     egd::buffer(w.zeros, ((w.n * a.blocks_per_row + 7u) / 8u) * 4u),
+                     egd::buffer(NORM ? a.norm : nullptr, NORM ? a.k * 4u : 0u)};
     const StageBase sb = stage_base(a, w, m0, n0);
     Staged st[S];
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};  // NORM: squares of this thread's x, rows tid / 16 + 16 i
+    auto square = [&](const Staged& v) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        ss[i] = fmaf(v.x[i].x, v.x[i].x, ss[i]);
+        ss[i] = fmaf(v.x[i].y, v.x[i].y, ss[i]);
+        ss[i] = fmaf(v.x[i].z, v.x[i].z, ss[i]);
+        ss[i] = fmaf(v.x[i].w, v.x[i].w, ss[i]);
+      }
+    };
 #pragma unroll
     for (int u = 0; u + 1 < S; u++)
-      load_block<ENC>(a, rs, sb, kbeg + min(block_of((uint32_t)u), nblk - 1) * kBK, st[u]);
+      load_block<ENC, NORM>(a, rs, sb, kbeg + min(block_of((uint32_t)u), nblk - 1) * kBK, st[u]);
     const uint32_t full = iters / S;
     for (uint32_t g = 0; g < full; g++) {
 #pragma unroll
       for (int u = 0; u < S; u++) {
         const uint32_t it = g * S + u;
-        store_block<ENC>(st[u], As, Bs);
+        store_block<ENC, NORM>(st[u], As, Bs);
+        if (NORM && block_of(it) < nblk) square(st[u]);
         __syncthreads();
-        load_block<ENC>(a, rs, sb, kbeg + min(block_of(it + S - 1), nblk - 1) * kBK, st[(u + S - 1) % S]);
+        load_block<ENC, NORM>(a, rs, sb, kbeg + min(block_of(it + S - 1), nblk - 1) * kBK, st[(u + S - 1) % S]);
         if (block_of(it) < nblk) mfma_block();
         __syncthreads();
       }
@@ -334,11 +362,23 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int u = 0; u + 1 < S; u++) {
       if ((uint32_t)u < rest) {
-        store_block<ENC>(st[u], As, Bs);
+        store_block<ENC, NORM>(st[u], As, Bs);
+        if (NORM && block_of(full * S + u) < nblk) square(st[u]);
         __syncthreads();
         if (block_of(full * S + u) < nblk) mfma_block();
         __syncthreads();
       }
+    }
+    if (NORM) {
+      // the 16 threads of a row group (lanes 16 q .. 16 q + 15 of a wave) hold the row's columns
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 64);
+      if ((tid & 15u) == 0)
+#pragma unroll
+        for (int i = 0; i < 4; i++) row_ss[NORM ? group : 0][(tid >> 4) + 16 * i] = ss[i];
+      __syncthreads();
     }
   } else {
     for (uint32_t it = 0; it < iters; it++) {
@@ -349,6 +389,13 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
       __syncthreads();
     }
   }
+  // NORM: 1 / rms of tile row r, the groups' sums of squares added in group order
+  auto inv_rms = [&](uint32_t r) {
+    float t = row_ss[0][r];
+#pragma unroll
+    for (int g = 1; g < (NORM ? KG : 1); g++) t += row_ss[NORM ? g : 0][r];
+    return 1.0f / sqrtf(t / (float)a.k + a.eps);
+  };
   if (KG > 1 || PAIR) {
     // every group's sums into its own buffers (the last barrier above ended the staging), then
     // the groups added in order by the thread that stores the element
@@ -374,6 +421,11 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
           gv += reinterpret_cast<const float*>(lds + k * kStageBytes)[r * kTile + c];
           uv += reinterpret_cast<const float*>(lds + k * kStageBytes)[r * kTile + c + 32u];
         }
+        if (NORM) {
+          const float inv = inv_rms(r);
+          gv *= inv;
+          uv *= inv;
+        }
         gv = gv + (g.bias ? g.bias[col] : 0.f) + 0.f;
         uv = uv + (u.bias ? u.bias[col] : 0.f) + 0.f;
         g.out[(size_t)row * g.out_stride + col + g.out_offset] = silu_mul(gv, uv);
@@ -386,6 +438,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
       float v = reinterpret_cast<const float*>(lds)[idx];
 #pragma unroll
       for (int g = 1; g < KG; g++) v += reinterpret_cast<const float*>(lds + g * kStageBytes)[idx];
+      if (NORM) v *= inv_rms(r);
       if (a.partials) {
         a.partials[((size_t)blockIdx.z * a.m + row) * w.n + col] = v;
       } else {
@@ -406,13 +459,13 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
       const float b = (a.partials == nullptr && w.bias) ? w.bias[col] : 0.f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const uint32_t row = m0 + wm + i * 16 + 4 * (lane >> 4) + e;
+        const uint32_t r = wm + i * 16 + 4 * (lane >> 4) + e, row = m0 + r;
         if (row >= a.m) continue;
         if (a.partials) {
           a.partials[((size_t)blockIdx.z * a.m + row) * w.n + col] = acc[i][j][e];
         } else {
           const size_t o = (size_t)row * w.out_stride + col + w.out_offset;
-          w.out[o] = acc[i][j][e] + b + (w.residual ? w.residual[o] : 0.f);
+          w.out[o] = (NORM ? acc[i][j][e] * inv_rms(r) : acc[i][j][e]) + b + (w.residual ? w.residual[o] : 0.f);
         }
       }
     }
@@ -432,6 +485,21 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
     const size_t o = (size_t)row * out_stride + col + out_offset;
     out[o] = acc + (bias ? bias[col] : 0.f) + (residual ? residual[o] : 0.f);
   }
+}
+
+// One launch of the chunked staging with kg groups of 4 waves per workgroup.
+template <bool PAIR, bool NORM>
+void launch_chunked(int encoding, int kg, dim3 grid, hipStream_t stream, const PrefillArgs& a) {
+  const dim3 block(256 * kg);
+#define EG_KG(ENC)                                                                                      \
+  do {                                                                                                  \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, PAIR, NORM>), grid, block, 0, stream, a);    \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, PAIR, NORM>), grid, block, 0, stream, a); \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, PAIR, NORM>), grid, block, 0, stream, a);            \
+  } while (0)
+  if (encoding == EG_ENC_SIGNED) EG_KG(EG_ENC_SIGNED);
+  else EG_KG(EG_ENC_OFFSET_ZEROS);
+#undef EG_KG
 }
 
 }  // namespace
@@ -486,7 +554,7 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   splits = (k + k_per_split - 1) / k_per_split;
   const bool split = splits > 1;
   PrefillArgs a{x, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, k, bs, dims->blocks_per_row,
-                k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, {}};
+                k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, nullptr, 0.f, {}};
   a.mats[0] = PrefillMat{packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                          residual, out, n, dims->out_stride, dims->out_offset, tiles_n};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
@@ -538,13 +606,61 @@ bool one_launch(const float* x, uint32_t m, uint32_t k, uint32_t block_size, int
   return ok && *tiles_n <= 0x7FFFFFFFull && (m + kTile - 1) / kTile <= 65535;
 }
 
+// Groups per workgroup for a tile grid: one where the grid holds at least a tile per CU, else four.
+int groups_for(const eg_context* ctx, uint64_t tiles) {
+  return ctx->prefill_groups ? ctx->prefill_groups : (tiles >= (uint64_t)ctx->cu_count ? 1 : 4);
+}
+
+// Whether a launch folds the rows' RMSNorm in: only with four-group workgroups (a grid under one
+// tile per CU, latency-bound), where the extra staging work (the weight multiply and the squares,
+// 32 VALU operations per thread and block) is hidden; a launch that fills the device is bound by
+// that work, and a separate rmsnorm_rows launch costs less there (measured at 2048 rows: the
+// gate|up pair 94 -> 128 us with the norm folded in, against 5.5 us for rmsnorm_rows).
+bool fold_norm(const eg_context* ctx, uint64_t tiles, const float* norm) {
+  return norm && (reinterpret_cast<uintptr_t>(norm) & 15u) == 0 && groups_for(ctx, tiles) == 4;
+}
+
+// The matrices (one_launch accepted them) as one chunked launch; norm non-NULL folds the rows'
+// RMSNorm into it.
+int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding, int bits,
+                 const eg::PrefillMatrix* mats, uint32_t count, uint64_t tiles_n, const float* norm, float eps) {
+  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count,
+                norm, eps, {}};
+  uint32_t end = 0;
+  for (uint32_t i = 0; i < count; i++) {
+    const eg::PrefillMatrix& w = mats[i];
+    end += (w.n + kTile - 1) / kTile;
+    a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, w.residual,
+                           w.out, w.n, w.out_stride, w.out_offset, end};
+  }
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  const int kg = groups_for(ctx, tiles_n * tiles_m);
+  const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
+  if (norm) launch_chunked<false, true>(encoding, kg, grid, ctx->stream, a);
+  else launch_chunked<false, false>(encoding, kg, grid, ctx->stream, a);
+  return eg::check_launch(ctx, "matmul_q4_prefill");
+}
+
 }  // namespace
 
 int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
-                           int encoding, int bits, const PrefillMatrix* mats, uint32_t count) {
+                           int encoding, int bits, const PrefillMatrix* mats, uint32_t count, const float* norm,
+                           float eps, float* normed) {
   const char* op = "matmul_q4_prefill";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (count > 0 && !mats) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL matrix list", op);
+  uint64_t tiles_n = 0;
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  if (norm) {
+    // RMSNorm folded into the one launch where that pays (fold_norm); otherwise rmsnorm_rows
+    // into `normed` and the launches below on it
+    if (one_launch(x, m, k, block_size, encoding, bits, mats, count, &tiles_n) && fold_norm(ctx, tiles_n * tiles_m, norm))
+      return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, count, tiles_n, norm, eps);
+    if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "%s: RMSNorm needs a buffer for the normed rows", op);
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    if (st != EG_OK) return st;
+    x = normed;
+  }
   auto one = [&](const PrefillMatrix& w) {
     eg_matmul_q4_dims dm{};
     dm.m = m;
@@ -559,8 +675,6 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
   };
   // One launch where the chunked staging takes every matrix and no matrix would split K;
   // otherwise (and for anything the single path must reject with its own message) one each.
-  uint64_t tiles_n = 0;
-  const uint64_t tiles_m = (m + kTile - 1) / kTile;
   if (count < 2 || !one_launch(x, m, k, block_size, encoding, bits, mats, count, &tiles_n)) {
     for (uint32_t i = 0; i < count; i++) {
       const int st = one(mats[i]);
@@ -568,32 +682,13 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
     }
     return EG_OK;
   }
-  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count, {}};
-  uint32_t end = 0;
-  for (uint32_t i = 0; i < count; i++) {
-    const PrefillMatrix& w = mats[i];
-    end += (w.n + kTile - 1) / kTile;
-    a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, w.residual,
-                           w.out, w.n, w.out_stride, w.out_offset, end};
-  }
-  const int kg = ctx->prefill_groups ? ctx->prefill_groups : (tiles_n * tiles_m >= (uint64_t)ctx->cu_count ? 1 : 4);
-  const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
-  const dim3 block(256 * kg);
-#define EG_PREFILL_MULTI(ENC)                                                                           \
-  do {                                                                                                  \
-    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4>), grid, block, 0, ctx->stream, a);    \
-    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2>), grid, block, 0, ctx->stream, a); \
-    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1>), grid, block, 0, ctx->stream, a);            \
-  } while (0)
-  if (encoding == EG_ENC_SIGNED) EG_PREFILL_MULTI(EG_ENC_SIGNED);
-  else EG_PREFILL_MULTI(EG_ENC_OFFSET_ZEROS);
-#undef EG_PREFILL_MULTI
-  return eg::check_launch(ctx, op);
+  (void)tiles_m;
+  return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, count, tiles_n, nullptr, 0.f);
 }
 
 int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
                             int encoding, int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out,
-                            float* scratch) {
+                            float* scratch, const float* norm, float eps, float* normed) {
   const char* op = "matmul_q4_prefill";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!out || !scratch || gate.n != up.n)
@@ -607,30 +702,30 @@ int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_
     // otherwise gate | up side by side in the scratch rows, then SiLU(gate) * up
     const PrefillMatrix gu[2] = {{gate.packed, gate.scales, gate.zeros, gate.bias, nullptr, scratch, n, 2 * n, 0},
                                  {up.packed, up.scales, up.zeros, up.bias, nullptr, scratch, n, 2 * n, n}};
-    int st = eg::prefill_gemm_multi(ctx, x, m, k, block_size, encoding, bits, gu, 2);
+    int st = eg::prefill_gemm_multi(ctx, x, m, k, block_size, encoding, bits, gu, 2, norm, eps, normed);
     if (st == EG_OK && m > 0 && n > 0) st = eg::silu_mul_rows(ctx, scratch, m, n, out);
     return st;
   }
-  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u, {}};
   const uint32_t tiles_x = (n + 31) / 32;
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  const int kg = groups_for(ctx, (uint64_t)tiles_x * tiles_m);
+  if (norm && !fold_norm(ctx, (uint64_t)tiles_x * tiles_m, norm)) {
+    if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "%s: RMSNorm needs a buffer for the normed rows", op);
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    if (st != EG_OK) return st;
+    x = normed;
+    norm = nullptr;
+  }
+  PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u,
+                norm, eps, {}};
   for (int i = 0; i < 2; i++) {
     const PrefillMatrix& w = pair[i];
     a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, nullptr,
                            w.out, n, n, 0, tiles_x};
   }
-  const uint64_t tiles_m = (m + kTile - 1) / kTile;
-  const int kg = ctx->prefill_groups ? ctx->prefill_groups : ((uint64_t)tiles_x * tiles_m >= (uint64_t)ctx->cu_count ? 1 : 4);
   const dim3 grid(tiles_x, (uint32_t)tiles_m, 1);
-  const dim3 block(256 * kg);
-#define EG_PREFILL_PAIR(ENC)                                                                              \
-  do {                                                                                                    \
-    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, true>), grid, block, 0, ctx->stream, a);   \
-    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, true>), grid, block, 0, ctx->stream, a); \
-    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, true>), grid, block, 0, ctx->stream, a);           \
-  } while (0)
-  if (encoding == EG_ENC_SIGNED) EG_PREFILL_PAIR(EG_ENC_SIGNED);
-  else EG_PREFILL_PAIR(EG_ENC_OFFSET_ZEROS);
-#undef EG_PREFILL_PAIR
+  if (norm) launch_chunked<true, true>(encoding, kg, grid, ctx->stream, a);
+  else launch_chunked<true, false>(encoding, kg, grid, ctx->stream, a);
   return eg::check_launch(ctx, op);
 }
 

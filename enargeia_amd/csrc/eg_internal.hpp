@@ -156,13 +156,19 @@ struct PrefillMatrix {
   float* out;
   uint32_t n, out_stride, out_offset;
 };
+// norm non-NULL: x is RMS-normalised per row first (rmsnorm_rows' x * (1 / rms) * norm, eps) - folded
+// into the one launch where it can be, else rmsnorm_rows into `normed` ([m][k]) and the launches
+// on that.
 int prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
-                       int bits, const PrefillMatrix* mats, uint32_t count);
+                       int bits, const PrefillMatrix* mats, uint32_t count, const float* norm = nullptr,
+                       float eps = 0.f, float* normed = nullptr);
 // The SwiGLU pair: out[r][j] = SiLU(x[r] . gate_j + bias) * (x[r] . up_j + bias), j < gate.n, rows
 // gate.n apart (the outputs and strides in gate and up are ignored). One launch of paired tiles
 // where the staging allows; otherwise gate | up into `scratch` ([m][2 n]) and silu_mul_rows.
+// norm, eps, normed: as prefill_gemm_multi's.
 int prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
-                        int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out, float* scratch);
+                        int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out, float* scratch,
+                        const float* norm = nullptr, float eps = 0.f, float* normed = nullptr);
 
 // Row-wise kernels of the prefill chain (one workgroup per row):
 //   embed_rows: out[r] = the dequantized table row of ids[r] (ops.ts:222-233), r < rows;
