@@ -147,13 +147,16 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   const uint32_t tid = threadIdx.x;
   const uint32_t live = min((uint32_t)CHUNK, pos + 1 - j0);
 
-  __shared__ float qs[GMAX][D];          // rotated, pre-scaled queries of this workgroup's heads
-  __shared__ float knew[D], vnew[D];     // the new key (rotated) and value
-  __shared__ double2 cs[D / 2];          // RoPE cos/sin at `pos`
-  __shared__ uint16_t ks[CHUNK][D + 2];  // K rows (f16), padded against bank conflicts
-  __shared__ uint16_t vs[CHUNK][D + 2];  // V rows (f16)
-  __shared__ float p[GMAX][CHUNK];       // scores, then exp(score - max)
+  // K rows padded to 144 bytes: 16-byte row reads by 16 lanes on 16 rows cover the 64 banks once.
+  // V rows unpadded: the P.V loop's 8-byte reads take 4 rows a wave, 2 on each half of the banks.
+  __shared__ __attribute__((aligned(16))) float qs[GMAX][D];          // rotated, pre-scaled queries
+  __shared__ float knew[D], vnew[D];                                  // the new key (rotated), value
+  __shared__ double2 cs[D / 2];                                       // RoPE cos/sin at `pos`
+  __shared__ __attribute__((aligned(16))) uint16_t ks[CHUNK][D + 8];  // K rows (f16)
+  __shared__ __attribute__((aligned(16))) uint16_t vs[CHUNK][D];      // V rows (f16)
+  __shared__ float p[GMAX][CHUNK];                                    // scores, then exp(score - max)
   __shared__ float mstat[GMAX], lstat[GMAX];
+  __shared__ __attribute__((aligned(16))) float half_sum[GMAX][D];    // P.V: the second wave's sums
 
   const float scale = 1.0f / sqrtf((float)D);
   const bool owns_new = pos < j0 + CHUNK;
@@ -195,7 +198,8 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   }
   __syncthreads();
 
-  // scores: thread -> one position, a strided subset of the group's heads
+  // scores: thread -> one position, a strided subset of the group's heads; the K row in 16-byte
+  // pieces, the query in float4s (a broadcast), products summed in element order
   {
     const uint32_t j = tid % CHUNK;
     const uint32_t g0 = tid / CHUNK, gs = kThreads / CHUNK;
@@ -203,8 +207,20 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
       float s = -INFINITY;
       if (j < live) {
         float acc = 0.f;
-#pragma unroll 16
-        for (int e = 0; e < D; e++) acc = fmaf(qs[g][e], half_to_float(ks[j][e]), acc);
+#pragma unroll
+        for (int w = 0; w < D / 8; w++) {
+          const uint4 kk = *reinterpret_cast<const uint4*>(&ks[j][8 * w]);
+          const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * w]);
+          const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * w + 4]);
+          acc = fmaf(qa.x, half_to_float((uint16_t)kk.x), acc);
+          acc = fmaf(qa.y, half_to_float((uint16_t)(kk.x >> 16)), acc);
+          acc = fmaf(qa.z, half_to_float((uint16_t)kk.y), acc);
+          acc = fmaf(qa.w, half_to_float((uint16_t)(kk.y >> 16)), acc);
+          acc = fmaf(qb.x, half_to_float((uint16_t)kk.z), acc);
+          acc = fmaf(qb.y, half_to_float((uint16_t)(kk.z >> 16)), acc);
+          acc = fmaf(qb.z, half_to_float((uint16_t)kk.w), acc);
+          acc = fmaf(qb.w, half_to_float((uint16_t)(kk.w >> 16)), acc);
+        }
         s = acc;
       }
       p[g][j] = s;
@@ -234,12 +250,53 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   }
   __syncthreads();
 
-  // o[g][e] = sum_j p[g][j] * V[j][e]
-  for (uint32_t i = tid; i < ng * D; i += blockDim.x) {
-    const uint32_t g = i / D, e = i % D;
-    float acc = 0.f;
-    for (uint32_t j = 0; j < live; j++) acc = fmaf(p[g][j], half_to_float(vs[j][e]), acc);
-    po[(size_t)i * chunks] = acc;
+  // o[g][e] = sum_j p[g][j] * V[j][e]: WPH waves per head, each over its CHUNK / WPH positions;
+  // a lane takes 4 consecutive e (lane % 16) and every 4th position (lane / 16), four independent
+  // sums; the 4 position phases are added across lanes, then the waves in order.
+  {
+    constexpr uint32_t kWPH = (kThreads / 64) / GMAX;
+    static_assert(kWPH >= 1 && kWPH <= 2 && D == 64, "P.V lane layout");
+    const uint32_t g = wave / kWPH, wh = wave % kWPH;
+    const uint32_t e4 = 4 * (lane & 15u), ph = lane >> 4;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (g < ng) {
+      const uint32_t jb = wh * (CHUNK / kWPH), je = min(live, jb + CHUNK / kWPH);
+      for (uint32_t j = jb + ph; j < je; j += 4) {
+        const float pj = p[g][j];
+        const uint2 vv = *reinterpret_cast<const uint2*>(&vs[j][e4]);
+        a0 = fmaf(pj, half_to_float((uint16_t)vv.x), a0);
+        a1 = fmaf(pj, half_to_float((uint16_t)(vv.x >> 16)), a1);
+        a2 = fmaf(pj, half_to_float((uint16_t)vv.y), a2);
+        a3 = fmaf(pj, half_to_float((uint16_t)(vv.y >> 16)), a3);
+      }
+    }
+    a0 += __shfl_xor(a0, 16, 64);
+    a1 += __shfl_xor(a1, 16, 64);
+    a2 += __shfl_xor(a2, 16, 64);
+    a3 += __shfl_xor(a3, 16, 64);
+    a0 += __shfl_xor(a0, 32, 64);
+    a1 += __shfl_xor(a1, 32, 64);
+    a2 += __shfl_xor(a2, 32, 64);
+    a3 += __shfl_xor(a3, 32, 64);
+    if (kWPH > 1) {
+      if (g < ng && wh == 1 && ph == 0)
+        *reinterpret_cast<float4*>(&half_sum[g][e4]) = make_float4(a0, a1, a2, a3);
+      __syncthreads();
+      if (g < ng && wh == 0) {
+        const float4 b = *reinterpret_cast<const float4*>(&half_sum[g][e4]);
+        a0 += b.x;
+        a1 += b.y;
+        a2 += b.z;
+        a3 += b.w;
+      }
+    }
+    if (g < ng && wh == 0 && ph == 0) {
+      float* o = po + (size_t)(g * D + e4) * chunks;
+      o[0] = a0;
+      o[chunks] = a1;
+      o[2 * chunks] = a2;
+      o[3 * chunks] = a3;
+    }
   }
   if (tid < ng) {
     pm[(size_t)tid * chunks] = mstat[tid];
