@@ -263,13 +263,26 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
         {L.q.packed, L.q.scales, L.q.zeros, L.q_bias, nullptr, d->pq, H, H, 0},
         {L.k.packed, L.k.scales, L.k.zeros, L.k_bias, nullptr, d->pk, kvn, kvn, 0},
         {L.v.packed, L.v.scales, L.v.zeros, L.v_bias, nullptr, d->pv, kvn, kvn, 0}};
-    st = eg::prefill_gemm_multi(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, 3, L.input_norm,
-                                m.rms_eps, d->pxn);
-    if (st != EG_OK) break;
     eg_attention_prefill_dims ad{count, begin + count, begin, m.heads, m.kv_heads, m.head_dim, m.max_context,
                                  m.rope_theta};
-    st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, d->k_cache + l * d->layer_stride,
-                              d->v_cache + l * d->layer_stride, d->pqr, d->patt, &ad);
+    uint16_t* kc = d->k_cache + l * d->layer_stride;
+    uint16_t* vc = d->v_cache + l * d->layer_stride;
+    // RoPE and the cache append in the q|k|v launch's epilogue where it can take them (then the
+    // attention launches alone), else rope_append's launch before the attention
+    bool fused = false;
+    st = eg::check_attention_prefill(ctx, "attention_prefill", &ad);
+    if (st == EG_OK && m.head_dim == 64) {
+      const eg::PrefillRope rope{reinterpret_cast<const double2*>(d->rope_table), d->pqr, kc, vc, begin, m.heads,
+                                 m.kv_heads};
+      st = eg::prefill_qkv_rope(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, L.input_norm,
+                                m.rms_eps, d->pxn, rope, &fused);
+    }
+    if (st == EG_OK && !fused)
+      st = eg::prefill_gemm_multi(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, 3, L.input_norm,
+                                  m.rms_eps, d->pxn);
+    if (st != EG_OK) break;
+    if (fused) st = eg::attention_prefill_run(ctx, d->pqr, kc, vc, d->patt, ad);
+    else st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, kc, vc, d->pqr, d->patt, &ad);
     gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
     // RMSNorm and SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch
     // form's rows)

@@ -58,6 +58,14 @@ struct PrefillArgs {
   uint32_t nmats;        // matrices in mats (> 1: no K split)
   const float* norm;     // NORM launches: x is RMS-normalised per row with these weights (no K split)
   float eps;
+  // ROPE launches (q | k | v, 64-column tiles = heads): q rows rotated and scaled by 1/8 into
+  // q_rope [row][q heads][64], k rows rotated and v rows as they are into the f16 caches at
+  // positions rope_pos0 + row ([pos][kv_heads][64]); rope = the cos/sin table [pos][32]
+  const double2* rope;
+  float* q_rope;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  uint32_t rope_pos0, q_heads, kv_heads;
   PrefillMat mats[kMaxSegs];
 };
 
@@ -267,8 +275,17 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // the squares of the x it stages; the rows' sums meet in LDS after the K loop and the epilogue
 // scales each output row by 1 / sqrt(sum / K + eps) (rmsnorm_rows' formula, with the row's
 // scale applied after the products instead of before them).
-template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false>
+//
+// ROPE (chunked staging; mats = q, k, v with head_dim 64, so a tile is one head): the epilogue
+// takes each row's (e, e + 32) pairs from the LDS sums, adds the biases, rotates them in double
+// precision with the table's cos/sin of the row's position - rope_append's arithmetic - and
+// stores q * RoPE / 8 in f32 and k, v in f16 into the caches.
+template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false, bool ROPE = false>
 __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
+  // No contraction of separate operations into fused multiply-adds (the explicit fmaf calls stay):
+  // every epilogue then rounds the row's norm scale and the bias addition on their own, so the
+  // launches that fold different work into their epilogues give the same values.
+#pragma clang fp contract(off)
   // staging buffers of every group; after the K loop they hold the groups' f32 sums
   constexpr uint32_t kStageBytes = 2u * kTile * kLds * 2u;  // As + Bs of one group
   static_assert(kStageBytes >= kTile * kTile * 4u, "a group's buffers hold its 64 x 64 f32 sums");
@@ -396,7 +413,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     for (int g = 1; g < (NORM ? KG : 1); g++) t += row_ss[NORM ? g : 0][r];
     return 1.0f / sqrtf(t / (float)a.k + a.eps);
   };
-  if (KG > 1 || PAIR) {
+  if (KG > 1 || PAIR || ROPE) {
     // every group's sums into its own buffers (the last barrier above ended the staging), then
     // the groups added in order by the thread that stores the element
     float* sums = reinterpret_cast<float*>(lds + group * kStageBytes);
@@ -408,6 +425,41 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
         for (int e = 0; e < 4; e++)
           sums[(wm + i * 16 + 4 * (lane >> 4) + e) * kTile + wn + j * 16 + (lane & 15)] = acc[i][j][e];
     __syncthreads();
+    if (ROPE) {
+      const uint32_t s = select_matrix(a, blockIdx.x), hd = n0 / kTile;
+      auto sum = [&](uint32_t r, uint32_t c) {
+        float v = reinterpret_cast<const float*>(lds)[r * kTile + c];
+#pragma unroll
+        for (int k = 1; k < KG; k++) v += reinterpret_cast<const float*>(lds + k * kStageBytes)[r * kTile + c];
+        if (NORM) v *= inv_rms(r);
+        return v + (w.bias ? w.bias[n0 + c] : 0.f) + 0.f;
+      };
+      if (s == 2) {  // v: the rows as they are, f16
+        for (uint32_t idx = threadIdx.x; idx < kTile * kTile; idx += 256u * KG) {
+          const uint32_t r = idx / kTile, c = idx % kTile, row = m0 + r;
+          if (row >= a.m) continue;
+          a.v_cache[((size_t)(a.rope_pos0 + row) * a.kv_heads + hd) * kTile + c] = egd::float_to_half(sum(r, c));
+        }
+        return;
+      }
+      for (uint32_t idx = threadIdx.x; idx < kTile * 32u; idx += 256u * KG) {
+        const uint32_t r = idx / 32u, e = idx % 32u, row = m0 + r;
+        if (row >= a.m) continue;
+        const double2 cs = a.rope[(size_t)(a.rope_pos0 + row) * 32u + e];
+        const float2 rr = egd::rotate(sum(r, e), sum(r, e + 32u), cs);
+        const float r0 = rr.x, r1 = rr.y;
+        if (s == 0) {
+          float* dst = a.q_rope + ((size_t)row * a.q_heads + hd) * kTile;
+          dst[e] = r0 * 0.125f;
+          dst[e + 32u] = r1 * 0.125f;
+        } else {
+          uint16_t* dst = a.k_cache + ((size_t)(a.rope_pos0 + row) * a.kv_heads + hd) * kTile;
+          dst[e] = egd::float_to_half(r0);
+          dst[e + 32u] = egd::float_to_half(r1);
+        }
+      }
+      return;
+    }
     if (PAIR) {
       const PrefillMat& g = a.mats[0];
       const PrefillMat& u = a.mats[1];
@@ -488,14 +540,14 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
 }
 
 // One launch of the chunked staging with kg groups of 4 waves per workgroup.
-template <bool PAIR, bool NORM>
+template <bool PAIR, bool NORM, bool ROPE = false>
 void launch_chunked(int encoding, int kg, dim3 grid, hipStream_t stream, const PrefillArgs& a) {
   const dim3 block(256 * kg);
-#define EG_KG(ENC)                                                                                      \
-  do {                                                                                                  \
-    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, PAIR, NORM>), grid, block, 0, stream, a);    \
-    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, PAIR, NORM>), grid, block, 0, stream, a); \
-    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, PAIR, NORM>), grid, block, 0, stream, a);            \
+#define EG_KG(ENC)                                                                                            \
+  do {                                                                                                        \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, PAIR, NORM, ROPE>), grid, block, 0, stream, a);    \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, PAIR, NORM, ROPE>), grid, block, 0, stream, a); \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, PAIR, NORM, ROPE>), grid, block, 0, stream, a);            \
   } while (0)
   if (encoding == EG_ENC_SIGNED) EG_KG(EG_ENC_SIGNED);
   else EG_KG(EG_ENC_OFFSET_ZEROS);
@@ -554,7 +606,8 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   splits = (k + k_per_split - 1) / k_per_split;
   const bool split = splits > 1;
   PrefillArgs a{x, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, k, bs, dims->blocks_per_row,
-                k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, nullptr, 0.f, {}};
+                k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr,
+                0u, 0u, 0u, {}};
   a.mats[0] = PrefillMat{packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                          residual, out, n, dims->out_stride, dims->out_offset, tiles_n};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
@@ -623,9 +676,19 @@ bool fold_norm(const eg_context* ctx, uint64_t tiles, const float* norm) {
 // The matrices (one_launch accepted them) as one chunked launch; norm non-NULL folds the rows'
 // RMSNorm into it.
 int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding, int bits,
-                 const eg::PrefillMatrix* mats, uint32_t count, uint64_t tiles_n, const float* norm, float eps) {
+                 const eg::PrefillMatrix* mats, uint32_t count, uint64_t tiles_n, const float* norm, float eps,
+                 const eg::PrefillRope* rope = nullptr) {
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count,
-                norm, eps, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, {}};
+  if (rope) {
+    a.rope = rope->table;
+    a.q_rope = rope->q_rope;
+    a.k_cache = rope->k_cache;
+    a.v_cache = rope->v_cache;
+    a.rope_pos0 = rope->pos0;
+    a.q_heads = rope->q_heads;
+    a.kv_heads = rope->kv_heads;
+  }
   uint32_t end = 0;
   for (uint32_t i = 0; i < count; i++) {
     const eg::PrefillMatrix& w = mats[i];
@@ -636,8 +699,14 @@ int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
   const int kg = groups_for(ctx, tiles_n * tiles_m);
   const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
-  if (norm) launch_chunked<false, true>(encoding, kg, grid, ctx->stream, a);
-  else launch_chunked<false, false>(encoding, kg, grid, ctx->stream, a);
+  if (rope) {
+    if (norm) launch_chunked<false, true, true>(encoding, kg, grid, ctx->stream, a);
+    else launch_chunked<false, false, true>(encoding, kg, grid, ctx->stream, a);
+  } else if (norm) {
+    launch_chunked<false, true>(encoding, kg, grid, ctx->stream, a);
+  } else {
+    launch_chunked<false, false>(encoding, kg, grid, ctx->stream, a);
+  }
   return eg::check_launch(ctx, "matmul_q4_prefill");
 }
 
@@ -686,6 +755,28 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
   return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, count, tiles_n, nullptr, 0.f);
 }
 
+int eg::prefill_qkv_rope(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
+                         int bits, const PrefillMatrix* mats, const float* norm, float eps, float* normed,
+                         const PrefillRope& rope, bool* done) {
+  *done = false;
+  if (!ctx || !mats || !ctx->prefill_rope || m == 0) return EG_OK;
+  uint64_t tiles_n = 0;
+  if (!rope.table || !rope.q_rope || !rope.k_cache || !rope.v_cache || mats[0].n != rope.q_heads * kTile ||
+      mats[1].n != rope.kv_heads * kTile || mats[2].n != rope.kv_heads * kTile ||
+      !one_launch(x, m, k, block_size, encoding, bits, mats, 3, &tiles_n))
+    return EG_OK;
+  const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  if (norm && !fold_norm(ctx, tiles_n * tiles_m, norm)) {
+    if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "matmul_q4_prefill: RMSNorm needs a buffer for the normed rows");
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    if (st != EG_OK) return st;
+    x = normed;
+    norm = nullptr;
+  }
+  *done = true;
+  return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, 3, tiles_n, norm, eps, &rope);
+}
+
 int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
                             int encoding, int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out,
                             float* scratch, const float* norm, float eps, float* normed) {
@@ -717,7 +808,7 @@ int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_
     norm = nullptr;
   }
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u,
-                norm, eps, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, {}};
   for (int i = 0; i < 2; i++) {
     const PrefillMatrix& w = pair[i];
     a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, nullptr,

@@ -45,6 +45,8 @@ struct eg_context {
   // split up to this many workgroups per CU
   // the SwiGLU pair as one launch of paired gate|up tiles (false: gate | up, then silu_mul_rows)
   bool prefill_pair = true;
+  // the prompt chain's RoPE and cache append in the q|k|v launch (false: rope_append's launch)
+  bool prefill_rope = true;
   uint32_t attention_split_tiles = 8;
   uint32_t attention_split_fill = 1;
   // Resident workgroups per CU of each kernel launched through this context (from
@@ -162,6 +164,27 @@ struct PrefillMatrix {
 int prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
                        int bits, const PrefillMatrix* mats, uint32_t count, const float* norm = nullptr,
                        float eps = 0.f, float* normed = nullptr);
+// q | k | v of a prompt chunk with rope_append's work in the launch's epilogue (head_dim 64): q
+// rows rotated and scaled by 1/8 into q_rope, k rows rotated and v rows appended to the f16
+// caches at positions pos0 + row, cos/sin read from a table of launch_rope_table rows.
+struct PrefillRope {
+  const double2* table;  // [position][32] (cos, sin), covering pos0 .. pos0 + m - 1
+  float* q_rope;         // [m][q_heads][64]
+  uint16_t* k_cache;     // [position][kv_heads][64]
+  uint16_t* v_cache;
+  uint32_t pos0, q_heads, kv_heads;
+};
+// mats = q, k, v (q_heads * 64, kv_heads * 64, kv_heads * 64 rows). Runs the one fused launch
+// (norm, eps, normed as prefill_gemm_multi's) and sets *done, or - when the launch cannot take
+// these shapes or the context disables it - launches nothing and leaves *done false.
+int prefill_qkv_rope(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
+                     int bits, const PrefillMatrix* mats, const float* norm, float eps, float* normed,
+                     const PrefillRope& rope, bool* done);
+// Chunk attention over caches that already hold the chunk's rows, q_rope already written (the
+// launches of eg_attention_prefill after its rope_append); dims as that entry point checks them.
+int attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16_t* k_cache, const uint16_t* v_cache,
+                          float* out, const eg_attention_prefill_dims& d);
+int check_attention_prefill(eg_context* ctx, const char* op, const eg_attention_prefill_dims* dims);
 // The SwiGLU pair: out[r][j] = SiLU(x[r] . gate_j + bias) * (x[r] . up_j + bias), j < gate.n, rows
 // gate.n apart (the outputs and strides in gate and up are ignored). One launch of paired tiles
 // where the staging allows; otherwise gate | up into `scratch` ([m][2 n]) and silu_mul_rows.
@@ -454,11 +477,19 @@ __device__ __forceinline__ void rope_table(double2* cs, uint32_t i, uint32_t pos
   const double angle = (double)position / pow((double)theta, (2.0 * i) / D);
   cs[i] = make_double2(cos(angle), sin(angle));
 }
+// (a, b) rotated by (cos, sin) in double, each product rounded on its own - no fused multiply-add,
+// as a host evaluates a * cos - b * sin and b * cos + a * sin - then rounded to f32. Every RoPE
+// here goes through it, so a row rotated in any kernel is the same to the bit.
+__device__ __forceinline__ float2 rotate(double a, double b, double2 cs) {
+#pragma clang fp contract(off)
+  return make_float2((float)(a * cs.x - b * cs.y), (float)(b * cs.x + a * cs.y));
+}
+
 template <int D>
 __device__ __forceinline__ void rope_apply(float* v, uint32_t i, const double2* cs) {
-  const double a = v[i], b = v[i + D / 2];
-  v[i] = (float)(a * cs[i].x - b * cs[i].y);
-  v[i + D / 2] = (float)(b * cs[i].x + a * cs[i].y);
+  const float2 r = rotate(v[i], v[i + D / 2], cs[i]);
+  v[i] = r.x;
+  v[i + D / 2] = r.y;
 }
 
 }  // namespace egd

@@ -54,9 +54,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const float* __restric
     const uint32_t pp = is_q ? p : p - qn;
     const uint32_t head = pp / (kD / 2), e = pp % (kD / 2);
     const float* src = is_q ? q + ((size_t)i * d.heads + head) * kD : k + ((size_t)i * d.kv_heads + head) * kD;
-    const double a = src[e], b = src[e + kD / 2];
-    const float ra = (float)(a * cs[e].x - b * cs[e].y);
-    const float rb = (float)(b * cs[e].x + a * cs[e].y);
+    const float2 rr = egd::rotate(src[e], src[e + kD / 2], cs[e]);
+    const float ra = rr.x, rb = rr.y;
     if (is_q) {
       float* dst = q_rope + ((size_t)i * d.heads + head) * kD;
       dst[e] = ra * scale;
@@ -326,13 +325,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 }  // namespace
 
-extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float* k, const float* v, uint16_t* k_cache,
-                                    uint16_t* v_cache, float* q_rope, float* out,
-                                    const eg_attention_prefill_dims* dims) {
-  const char* op = "attention_prefill";
-  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
-  if (!dims || !q || !k || !v || !k_cache || !v_cache || !q_rope || !out)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+// The dims checks of eg_attention_prefill (pointers aside).
+int eg::check_attention_prefill(eg_context* ctx, const char* op, const eg_attention_prefill_dims* dims) {
   const eg_attention_prefill_dims& d = *dims;
   if (d.head_dim != (uint32_t)kD)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: head_dim %u is not supported (64)", op, d.head_dim);
@@ -345,17 +339,22 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
   if ((uint64_t)d.query_begin + d.queries > d.max_context)
     return eg::fail(ctx, EG_ERR_RANGE, "%s: positions up to %llu exceed the cache's %u", op,
                     (unsigned long long)d.query_begin + d.queries, d.max_context);
-  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches must be 16-byte aligned", op);
-  if ((reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) & 15u)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: q_rope and out must be 16-byte aligned", op);
   if ((uint64_t)d.max_context * d.kv_heads * d.head_dim * 2 >= (1ull << 31))
     return eg::fail(ctx, EG_ERR_RANGE, "%s: a cache of %u positions x %u kv heads exceeds 2 GiB", op, d.max_context,
                     d.kv_heads);
   if (d.heads > 65535 || (d.queries + kQ - 1) / kQ > 0x7FFFFFFFu)
     return eg::fail(ctx, EG_ERR_RANGE, "%s: %u heads over the grid limit", op, d.heads);
-  hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
-                     v_cache, d);
+  return EG_OK;
+}
+
+int eg::attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16_t* k_cache, const uint16_t* v_cache,
+                              float* out, const eg_attention_prefill_dims& d) {
+  const char* op = "attention_prefill";
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches must be 16-byte aligned", op);
+  if ((reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: q_rope and out must be 16-byte aligned", op);
+  if (d.queries == 0) return EG_OK;
   // Keys split over a long key range, within the workspace: where the (query block, head) grid
   // leaves most CUs idle, into splits of at least 4 key tiles, about one workgroup per CU in all;
   // and so that no workgroup walks more than 8 tiles - the causal limit makes the last query
@@ -387,4 +386,23 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
     hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count);
   }
   return eg::check_launch(ctx, op);
+}
+
+extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float* k, const float* v, uint16_t* k_cache,
+                                    uint16_t* v_cache, float* q_rope, float* out,
+                                    const eg_attention_prefill_dims* dims) {
+  const char* op = "attention_prefill";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!dims || !q || !k || !v || !k_cache || !v_cache || !q_rope || !out)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  int st = eg::check_attention_prefill(ctx, op, dims);
+  if (st != EG_OK || dims->queries == 0) return st;
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches must be 16-byte aligned", op);
+  if ((reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: q_rope and out must be 16-byte aligned", op);
+  const eg_attention_prefill_dims& d = *dims;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
+                     v_cache, d);
+  return eg::attention_prefill_run(ctx, q_rope, k_cache, v_cache, out, d);
 }

@@ -135,21 +135,25 @@ def test_prefill_chain_config4(device):
         dm.release()
 
 
+@pytest.mark.parametrize("switch", ["EG_PREFILL_PAIR", "EG_PREFILL_ROPE"])
 @pytest.mark.parametrize("chunk", [None, 64])
-def test_prefill_swiglu_pair_matches_two_launches_bit_exactly(device, chunk):
-    """gate|up as one launch of paired tiles with SiLU·up in its epilogue (the default) gives the
-    logits, to the bit, of gate | up in one launch followed by silu_mul_rows (a second context
-    created with EG_PREFILL_PAIR=0): the same sums in the same order, the same SiLU."""
+def test_prefill_fused_launches_match_unfused_bit_exactly(device, switch, chunk):
+    """The chain's fused launches against their unfused forms, in a second context created with
+    the switch off, to the bit (logits and both caches): EG_PREFILL_PAIR - gate|up as one launch of
+    paired tiles with SiLU·up in its epilogue against gate | up then silu_mul_rows;
+    EG_PREFILL_ROPE - RoPE and the cache append in the q|k|v launch's epilogue against
+    rope_append's launch. The same sums in the same order, the same rotation and roundings."""
     import os
     from enargeia_amd import kernels as K
-    os.environ["EG_PREFILL_PAIR"] = "0"
+    os.environ[switch] = "0"
     try:
         other = K.Device(0)
     finally:
-        del os.environ["EG_PREFILL_PAIR"]
+        del os.environ[switch]
     cfg = ModelConfig(layers=2, max_context=512)
     m = synthetic_model(cfg)
     prompt = [int(t) for t in oracle.random_ids(300, 77, cfg.vocab)]
+    n = cfg.layers * cfg.max_context * cfg.kv_heads * cfg.head_dim
     runs = []
     try:
         for dev in (device, other):
@@ -159,7 +163,9 @@ def test_prefill_swiglu_pair_matches_two_launches_bit_exactly(device, chunk):
                 if chunk:
                     dec.set_prefill_chunk(chunk)
                 tok = dec.prefill(0, prompt)
-                runs.append((tok, dec.logits().copy()))
+                kc = dev.read_array(dec.buffers.k_cache, np.uint16, n)
+                vc = dev.read_array(dec.buffers.v_cache, np.uint16, n)
+                runs.append((tok, dec.logits().copy(), kc, vc))
             finally:
                 dec.close()
                 dm.release()
@@ -167,3 +173,5 @@ def test_prefill_swiglu_pair_matches_two_launches_bit_exactly(device, chunk):
         other.close()
     assert runs[0][0] == runs[1][0]
     np.testing.assert_array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    np.testing.assert_array_equal(runs[0][2], runs[1][2])
+    np.testing.assert_array_equal(runs[0][3], runs[1][3])
