@@ -477,6 +477,27 @@ __device__ __forceinline__ void rope_table(double2* cs, uint32_t i, uint32_t pos
   const double angle = (double)position / pow((double)theta, (2.0 * i) / D);
   cs[i] = make_double2(cos(angle), sin(angle));
 }
+// Data one workgroup hands another inside a launch: agent-scope atomic stores and loads (the sc1
+// bit on gfx950), which write through and read past the XCD-private caching of ordinary
+// accesses - the instructions the memory model's agent-scope atomics use. A writer drains its
+// stores before it counts itself (drain, then a relaxed atomic on a counter); a reader that has
+// seen the count reads with get. No L2 write-back or invalidate is involved.
+template <typename T>
+__device__ __forceinline__ void put(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T get(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// This wave's memory operations issued so far complete before any issued after (the compiler
+// keeps them on their side of it: a signal fence on each side of the wait).
+__device__ __forceinline__ void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0 (loads and stores), expcnt 7, lgkmcnt 15
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // (a, b) rotated by (cos, sin) in double, each product rounded on its own - no fused multiply-add,
 // as a host evaluates a * cos - b * sin and b * cos + a * sin - then rounded to f32. Every RoPE
 // here goes through it, so a row rotated in any kernel is the same to the bit.

@@ -137,33 +137,20 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
 // ---- cross-workgroup data and the grid barrier -----------------------------------------------
 
 // Everything one workgroup hands another inside the launch moves through device-coherent
-// accesses: agent-scope atomic stores and loads (the sc1 bit on gfx950), which write through and
-// read past the XCD-private caching of ordinary accesses - the same instructions the agent-scope
-// atomics of the memory model use. The only thing a barrier then has to order is that every such
-// store of a workgroup has completed before the workgroup is counted: each wave drains its
-// stores (vmcnt 0) before the workgroup's s_barrier, and thread 0 counts it after. No L2
-// write-back or invalidate is needed (the release/acquire fences that do them cost ~2.5 us per
-// barrier here), and no ordinary load ever reads data another workgroup wrote in this launch.
-template <typename T>
-__device__ __forceinline__ void put(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T get(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// accesses (egd::put / egd::get: agent-scope atomic stores and loads), and the only thing a
+// barrier then has to order is that every such store of a workgroup has completed before the
+// workgroup is counted: each wave drains its stores (egd::drain) before the workgroup's
+// s_barrier, and thread 0 counts it after. No L2 write-back or invalidate is needed (the
+// release/acquire fences that do them cost ~2.5 us per barrier here), and no ordinary load ever
+// reads data another workgroup wrote in this launch.
+using egd::drain;
+using egd::get;
+using egd::put;
 __device__ __forceinline__ void put_f64(double* p, double v) {
   put(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v));
 }
 __device__ __forceinline__ double get_f64(const double* p) {
   return __builtin_bit_cast(double, get(reinterpret_cast<const unsigned long long*>(p)));
-}
-// This wave's memory operations issued so far complete before any issued after (the compiler
-// keeps them on their side of it: a signal fence on each side of the wait).
-__device__ __forceinline__ void drain() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0 (loads and stores), expcnt 7, lgkmcnt 15
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Central barrier over the launch's workgroups: thread 0 of each counts the workgroup once its
