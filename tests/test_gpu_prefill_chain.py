@@ -163,8 +163,10 @@ def test_prefill_fused_launches_match_unfused_bit_exactly(device, switch, chunk)
                 if chunk:
                     dec.set_prefill_chunk(chunk)
                 tok = dec.prefill(0, prompt)
-                kc = dev.read_array(dec.buffers.k_cache, np.uint16, n)
-                vc = dev.read_array(dec.buffers.v_cache, np.uint16, n)
+                # the prompt's rows of both caches (the rows past them are never written)
+                shape = (cfg.layers, cfg.max_context, cfg.kv_heads * cfg.head_dim)
+                kc = dev.read_array(dec.buffers.k_cache, np.uint16, n).reshape(shape)[:, :len(prompt)]
+                vc = dev.read_array(dec.buffers.v_cache, np.uint16, n).reshape(shape)[:, :len(prompt)]
                 runs.append((tok, dec.logits().copy(), kc, vc))
             finally:
                 dec.close()
