@@ -137,6 +137,24 @@ struct Prefetch {
   }
 };
 
+// Wave-wide max or sum: four DPP steps reduce each row of 16 lanes (quad pairs, quads, half-row
+// mirror, row mirror: every lane of a row then holds the row's value), and the four rows' values
+// are read as scalars and combined in row order - no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp<0x141>(v));  // row_half_mirror
+  v = op(v, dpp<0x140>(v));  // row_mirror
+  auto row = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+  return op(op(row(0), row(16)), op(row(32), row(48)));
+}
+
 // The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
 // statistics and the partial o, written to po/pm/pl, from what `pre` loaded.
 template <int D, int CHUNK, int GMAX>
@@ -233,16 +251,14 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   for (uint32_t g = wave; g < ng; g += kThreads / 64) {
     float m = -INFINITY;
     for (uint32_t j = lane; j < CHUNK; j += 64) m = fmaxf(m, p[g][j]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = wave_reduce<true>(m);
     float l = 0.f;
     for (uint32_t j = lane; j < CHUNK; j += 64) {
       const float e = j < live ? expf(p[g][j] - m) : 0.f;
       p[g][j] = e;
       l += e;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    l = wave_reduce<false>(l);
     if (lane == 0) {
       mstat[g] = m;
       lstat[g] = l;

@@ -84,7 +84,12 @@ class Checker:
             self.e2e_compared += 1
 
 
-@pytest.mark.parametrize("temperature,min_sampler,min_e2e", [(T, 0.4, 0.0), (0.1, 0.8, 0.6)])
+# The minimum counts keep the test from passing vacuously: every step whose decisions clear the
+# margins must give the same token, and at least this share of the steps must clear them. At
+# T 0.7 the random-init logits are nearly flat, so the share clearing the sampler's margins
+# depends on the trajectory (16 of 41 steps with one kernel revision, at least 17 with another
+# whose logits differ by rounding): 80 steps and a floor of a quarter hold it clear of chance.
+@pytest.mark.parametrize("temperature,min_sampler,min_e2e", [(T, 0.25, 0.0), (0.1, 0.8, 0.6)])
 @pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
 def test_sampled_decode_matches_oracle(device, small_model, graph, temperature, min_sampler, min_e2e):
     dm = DeviceModel(device, small_model)
@@ -108,7 +113,7 @@ def test_sampled_decode_matches_oracle(device, small_model, graph, temperature, 
         history = list(prompt)
         c.check(token, want, history, "first token")
         history.append(token)
-        steps = 40
+        steps = 80
         for s in range(steps):
             pos = len(prompt) + s
             new = dec.step()
