@@ -243,7 +243,7 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
   int st = eg::embed_rows(ctx, ids, count, m.embedding.packed, m.embedding.scales, m.embedding.zeros, H,
                           m.embed_block_size, m.embed_encoding, m.embed_bits, d->ph[0]);
   auto gemm = [&](const float* x, const eg_quant_matrix& w, const float* bias, const float* residual, float* out,
-                  uint32_t n, uint32_t k, uint32_t out_stride, uint32_t out_offset) {
+                  uint32_t n, uint32_t k, uint32_t out_stride, uint32_t out_offset, bool x_bf16) {
     if (st != EG_OK) return;
     eg_matmul_q4_dims dm{};
     dm.m = count;
@@ -254,7 +254,7 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
     dm.blocks_per_row = k / m.block_size;
     dm.out_stride = out_stride;
     dm.out_offset = out_offset;
-    st = eg::prefill_gemm(ctx, x, w.packed, w.scales, w.zeros, bias, residual, out, &dm, m.encoding, m.bits);
+    st = eg::prefill_gemm(ctx, x, w.packed, w.scales, w.zeros, bias, residual, out, &dm, m.encoding, m.bits, x_bf16);
   };
   for (uint32_t l = 0; l < m.layers && st == EG_OK; l++) {
     const eg_layer_desc& L = d->layers[l];
@@ -281,17 +281,21 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
       st = eg::prefill_gemm_multi(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, 3, L.input_norm,
                                   m.rms_eps, d->pxn);
     if (st != EG_OK) break;
-    if (fused) st = eg::attention_prefill_run(ctx, d->pqr, kc, vc, d->patt, ad);
+    // the o and down projections take their x as bf16 rows where they stage them (the attention
+    // and the SwiGLU pair store them rounded exactly as the staging would)
+    const bool xb_o = fused && ctx->prefill_xb16 && eg::prefill_chunked(count, H, H, m.block_size, m.bits, d->patt, L.o.packed);
+    const bool xb_down = ctx->prefill_xb16 && eg::prefill_chunked(count, H, I, m.block_size, m.bits, d->pa, L.down.packed);
+    if (fused) st = eg::attention_prefill_run(ctx, d->pqr, kc, vc, d->patt, ad, xb_o);
     else st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, kc, vc, d->pqr, d->patt, &ad);
-    gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0);  // ph1 = ph0 + o(attn)
+    gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0, xb_o);  // ph1 = ph0 + o(attn)
     // RMSNorm and SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch
     // form's rows)
     const eg::PrefillMatrix gate{L.gate.packed, L.gate.scales, L.gate.zeros, nullptr, nullptr, d->pa, I, I, 0};
     const eg::PrefillMatrix up{L.up.packed, L.up.scales, L.up.zeros, nullptr, nullptr, d->pa, I, I, 0};
     if (st == EG_OK)
       st = eg::prefill_gemm_swiglu(ctx, d->ph[1], count, H, m.block_size, m.encoding, m.bits, gate, up, d->pa, d->pgu,
-                                   L.post_attention_norm, m.rms_eps, d->pxn);
-    gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0);  // ph0 = ph1 + down(...)
+                                   L.post_attention_norm, m.rms_eps, d->pxn, xb_down);
+    gemm(d->pa, L.down, nullptr, d->ph[1], d->ph[0], H, I, H, 0, xb_down);  // ph0 = ph1 + down(...)
   }
   return st;
 }

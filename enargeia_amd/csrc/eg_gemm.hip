@@ -66,6 +66,8 @@ struct PrefillArgs {
   uint16_t* k_cache;
   uint16_t* v_cache;
   uint32_t rope_pos0, q_heads, kv_heads;
+  uint32_t out_bf16;  // PAIR launches: SiLU(g) * u stored as bf16 (the next GEMM's x, bit-for-bit
+                      // what its staging would round it to)
   PrefillMat mats[kMaxSegs];
 };
 
@@ -87,12 +89,7 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
   return (uint16_t)(u >> 16);
 }
 
-// Two floats to a packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
+using egd::pack_bf16;
 
 // One 64 x 64 block of x and of W held in registers between its global loads and its LDS
 // stores (chunked layout): x as 4 float4 per thread; W as 16 codes (8 bytes) per thread - row
@@ -125,6 +122,7 @@ struct StageBase {
   uint32_t sblk;    // the row's first quant block index
 };
 
+template <bool XB16>
 __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, const PrefillMat& w, uint32_t m0, uint32_t n0) {
   const uint32_t tid = threadIdx.x & 255u;  // the thread within its group of 4 waves
   StageBase b;
@@ -132,7 +130,7 @@ __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, const Pref
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t row = m0 + (tid >> 4) + 16u * i;
-    b.x[i] = row < a.m ? (row * a.k + b.xc) * 4u : kOutside;
+    b.x[i] = row < a.m ? (row * a.k + b.xc) * (XB16 ? 2u : 4u) : kOutside;
   }
   const uint32_t nrow = n0 + (tid >> 2);
   b.kc = 16u * (tid & 3u);
@@ -141,14 +139,19 @@ __device__ __forceinline__ StageBase stage_base(const PrefillArgs& a, const Pref
   return b;
 }
 
-template <int ENC, bool NORM>
+template <int ENC, bool NORM, bool XB16>
 __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& r, const StageBase& b, uint32_t k0,
                                            Staged& st) {
   const bool xin = k0 + b.xc < a.k;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const egd::u32x4 v = egd::load_b128(r.x, xin && b.x[i] != kOutside ? b.x[i] + k0 * 4u : kOutside);
-    st.x[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    if (XB16) {  // 4 bf16 values, kept as their bits in x and y
+      const uint64_t v = egd::load_b64(r.x, xin && b.x[i] != kOutside ? b.x[i] + k0 * 2u : kOutside);
+      st.x[i] = make_float4(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)), 0.f, 0.f);
+    } else {
+      const egd::u32x4 v = egd::load_b128(r.x, xin && b.x[i] != kOutside ? b.x[i] + k0 * 4u : kOutside);
+      st.x[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    }
   }
   if (NORM) {
     const egd::u32x4 v = egd::load_b128(r.g, xin ? (k0 + b.xc) * 4u : kOutside);
@@ -167,13 +170,17 @@ __device__ __forceinline__ void load_block(const PrefillArgs& a, const Streams& 
   }
 }
 
-template <int ENC, bool NORM>
+template <int ENC, bool NORM, bool XB16>
 __device__ __forceinline__ void store_block(const Staged& st, uint16_t (*As)[kLds], uint16_t (*Bs)[kLds]) {
   const uint32_t tid = threadIdx.x & 255u;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t idx = tid + i * 256u;
     const uint32_t r = idx >> 4, c = (idx & 15u) * 4u;
+    if (XB16) {
+      *reinterpret_cast<uint2*>(&As[r][c]) = make_uint2(__float_as_uint(st.x[i].x), __float_as_uint(st.x[i].y));
+      continue;
+    }
     // NORM: x times its column's norm weight here, the row's 1 / rms in the epilogue
     const float4 v = NORM ? make_float4(st.x[i].x * st.g.x, st.x[i].y * st.g.y, st.x[i].z * st.g.z, st.x[i].w * st.g.w)
                           : st.x[i];
@@ -255,6 +262,9 @@ __device__ void stage_elements(const PrefillArgs& a, const PrefillMat& w, uint32
   }
 }
 
+// v rounded to bf16 as pack_bf16 rounds it (round to nearest even).
+__device__ __forceinline__ uint16_t bf16_of(float v) { return (uint16_t)(pack_bf16(v, 0.f) & 0xFFFFu); }
+
 // SiLU(g) * u with SiLU(g) = g / (1 + e^-g), the prompt chain's silu_mul_rows formula.
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
@@ -280,7 +290,10 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // takes each row's (e, e + 32) pairs from the LDS sums, adds the biases, rotates them in double
 // precision with the table's cos/sin of the row's position - rope_append's arithmetic - and
 // stores q * RoPE / 8 in f32 and k, v in f16 into the caches.
-template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false, bool ROPE = false>
+//
+// XB16 (chunked staging, no NORM): x holds bf16 values (a producer stored them rounded as the
+// staging would), staged as they are.
+template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false, bool ROPE = false, bool XB16 = false>
 __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   // No contraction of separate operations into fused multiply-adds (the explicit fmaf calls stay):
   // every epilogue then rounds the row's norm scale and the bias addition on their own, so the
@@ -343,11 +356,11 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     // remaining blocks are already in flight and drain in a loop that issues no loads.
     // four groups fit four waves per SIMD only within 128 VGPRs: they keep one block in flight
     constexpr int S = KG >= 4 ? 2 : kStages;
-    const Streams rs{egd::buffer(a.x, a.m * a.k * 4u), egd::buffer(w.packed, w.n * a.k / 2u),
+    const Streams rs{egd::buffer(a.x, a.m * a.k * (XB16 ? 2u : 4u)), egd::buffer(w.packed, w.n * a.k / 2u),
                      egd::buffer(w.scales, w.n * a.blocks_per_row * 4u),
                      egd::buffer(w.zeros, ((w.n * a.blocks_per_row + 7u) / 8u) * 4u),
                      egd::buffer(NORM ? a.norm : nullptr, NORM ? a.k * 4u : 0u)};
-    const StageBase sb = stage_base(a, w, m0, n0);
+    const StageBase sb = stage_base<XB16>(a, w, m0, n0);
     Staged st[S];
     float ss[4] = {0.f, 0.f, 0.f, 0.f};  // NORM: squares of this thread's x, rows tid / 16 + 16 i
     auto square = [&](const Staged& v) {
@@ -361,16 +374,16 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
     };
 #pragma unroll
     for (int u = 0; u + 1 < S; u++)
-      load_block<ENC, NORM>(a, rs, sb, kbeg + min(block_of((uint32_t)u), nblk - 1) * kBK, st[u]);
+      load_block<ENC, NORM, XB16>(a, rs, sb, kbeg + min(block_of((uint32_t)u), nblk - 1) * kBK, st[u]);
     const uint32_t full = iters / S;
     for (uint32_t g = 0; g < full; g++) {
 #pragma unroll
       for (int u = 0; u < S; u++) {
         const uint32_t it = g * S + u;
-        store_block<ENC, NORM>(st[u], As, Bs);
+        store_block<ENC, NORM, XB16>(st[u], As, Bs);
         if (NORM && block_of(it) < nblk) square(st[u]);
         __syncthreads();
-        load_block<ENC, NORM>(a, rs, sb, kbeg + min(block_of(it + S - 1), nblk - 1) * kBK, st[(u + S - 1) % S]);
+        load_block<ENC, NORM, XB16>(a, rs, sb, kbeg + min(block_of(it + S - 1), nblk - 1) * kBK, st[(u + S - 1) % S]);
         if (block_of(it) < nblk) mfma_block();
         __syncthreads();
       }
@@ -379,7 +392,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int u = 0; u + 1 < S; u++) {
       if ((uint32_t)u < rest) {
-        store_block<ENC, NORM>(st[u], As, Bs);
+        store_block<ENC, NORM, XB16>(st[u], As, Bs);
         if (NORM && block_of(full * S + u) < nblk) square(st[u]);
         __syncthreads();
         if (block_of(full * S + u) < nblk) mfma_block();
@@ -480,7 +493,9 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
         }
         gv = gv + (g.bias ? g.bias[col] : 0.f) + 0.f;
         uv = uv + (u.bias ? u.bias[col] : 0.f) + 0.f;
-        g.out[(size_t)row * g.out_stride + col + g.out_offset] = silu_mul(gv, uv);
+        const size_t o = (size_t)row * g.out_stride + col + g.out_offset;
+        if (a.out_bf16) reinterpret_cast<uint16_t*>(g.out)[o] = bf16_of(silu_mul(gv, uv));
+        else g.out[o] = silu_mul(gv, uv);
       }
       return;
     }
@@ -540,14 +555,14 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
 }
 
 // One launch of the chunked staging with kg groups of 4 waves per workgroup.
-template <bool PAIR, bool NORM, bool ROPE = false>
+template <bool PAIR, bool NORM, bool ROPE = false, bool XB16 = false>
 void launch_chunked(int encoding, int kg, dim3 grid, hipStream_t stream, const PrefillArgs& a) {
   const dim3 block(256 * kg);
-#define EG_KG(ENC)                                                                                            \
-  do {                                                                                                        \
-    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, PAIR, NORM, ROPE>), grid, block, 0, stream, a);    \
-    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, PAIR, NORM, ROPE>), grid, block, 0, stream, a); \
-    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, PAIR, NORM, ROPE>), grid, block, 0, stream, a);            \
+#define EG_KG(ENC)                                                                                                  \
+  do {                                                                                                              \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, true, 4, PAIR, NORM, ROPE, XB16>), grid, block, 0, stream, a);    \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, true, 2, PAIR, NORM, ROPE, XB16>), grid, block, 0, stream, a); \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, true, 1, PAIR, NORM, ROPE, XB16>), grid, block, 0, stream, a);            \
   } while (0)
   if (encoding == EG_ENC_SIGNED) EG_KG(EG_ENC_SIGNED);
   else EG_KG(EG_ENC_OFFSET_ZEROS);
@@ -556,9 +571,16 @@ void launch_chunked(int encoding, int kg, dim3 grid, hipStream_t stream, const P
 
 }  // namespace
 
+bool eg::prefill_chunked(uint32_t m, uint32_t n, uint32_t k, uint32_t bs, int bits, const void* x,
+                         const uint32_t* packed) {
+  return bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
+         (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
+         (reinterpret_cast<uintptr_t>(packed) & 7u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
 int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
                      const uint32_t* zeros, const float* bias, const float* residual, float* out,
-                     const eg_matmul_q4_dims* dims, int encoding, int bits) {
+                     const eg_matmul_q4_dims* dims, int encoding, int bits, bool x_bf16) {
   const char* op = "matmul_q4_prefill";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!dims || !x || !packed || !scales || !out) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
@@ -607,13 +629,13 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   const bool split = splits > 1;
   PrefillArgs a{x, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, k, bs, dims->blocks_per_row,
                 k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr,
-                0u, 0u, 0u, {}};
+                0u, 0u, 0u, 0u, {}};
   a.mats[0] = PrefillMat{packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                          residual, out, n, dims->out_stride, dims->out_offset, tiles_n};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
-  const bool chunked = bits == 4 && k % 32 == 0 && bs % 16 == 0 && (bs & (bs - 1)) == 0 && k % 4 == 0 &&
-                       (uint64_t)m * k * 4 < kOutside && (uint64_t)n * k / 2 < kOutside &&
-                       (reinterpret_cast<uintptr_t>(packed) & 7u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  const bool chunked = eg::prefill_chunked(m, n, k, bs, bits, x, packed);
+  if (x_bf16 && !chunked)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: bf16 rows of x need the chunked staging", op);
   const dim3 block(256 * kg);
 #define EG_PREFILL_LAUNCH(ENC, CH)                                                                        \
   do {                                                                                                    \
@@ -621,7 +643,9 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
     else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 2>), grid, block, 0, ctx->stream, a);   \
     else hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1>), grid, block, 0, ctx->stream, a);                \
   } while (0)
-  if (encoding == EG_ENC_SIGNED) {
+  if (x_bf16) {
+    launch_chunked<false, false, false, true>(encoding, kg, grid, ctx->stream, a);
+  } else if (encoding == EG_ENC_SIGNED) {
     if (chunked) EG_PREFILL_LAUNCH(EG_ENC_SIGNED, true);
     else EG_PREFILL_LAUNCH(EG_ENC_SIGNED, false);
   } else {
@@ -677,9 +701,9 @@ bool fold_norm(const eg_context* ctx, uint64_t tiles, const float* norm) {
 // RMSNorm into it.
 int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding, int bits,
                  const eg::PrefillMatrix* mats, uint32_t count, uint64_t tiles_n, const float* norm, float eps,
-                 const eg::PrefillRope* rope = nullptr) {
+                 const eg::PrefillRope* rope = nullptr, bool x_bf16 = false) {
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count,
-                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, 0u, {}};
   if (rope) {
     a.rope = rope->table;
     a.q_rope = rope->q_rope;
@@ -701,9 +725,12 @@ int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32
   const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
   if (rope) {
     if (norm) launch_chunked<false, true, true>(encoding, kg, grid, ctx->stream, a);
+    else if (x_bf16) launch_chunked<false, false, true, true>(encoding, kg, grid, ctx->stream, a);
     else launch_chunked<false, false, true>(encoding, kg, grid, ctx->stream, a);
   } else if (norm) {
     launch_chunked<false, true>(encoding, kg, grid, ctx->stream, a);
+  } else if (x_bf16) {
+    launch_chunked<false, false, false, true>(encoding, kg, grid, ctx->stream, a);
   } else {
     launch_chunked<false, false>(encoding, kg, grid, ctx->stream, a);
   }
@@ -722,12 +749,16 @@ int eg::prefill_gemm_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
   if (norm) {
     // RMSNorm folded into the one launch where that pays (fold_norm); otherwise rmsnorm_rows
-    // into `normed` and the launches below on it
-    if (one_launch(x, m, k, block_size, encoding, bits, mats, count, &tiles_n) && fold_norm(ctx, tiles_n * tiles_m, norm))
+    // into `normed` (as bf16 rows when the one launch stages them) and the launches below on it
+    const bool one = one_launch(x, m, k, block_size, encoding, bits, mats, count, &tiles_n);
+    if (one && fold_norm(ctx, tiles_n * tiles_m, norm))
       return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, count, tiles_n, norm, eps);
     if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "%s: RMSNorm needs a buffer for the normed rows", op);
-    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    const bool xb = one && ctx->prefill_xb16;
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed, xb);
     if (st != EG_OK) return st;
+    if (xb) return launch_multi(ctx, normed, m, k, block_size, encoding, bits, mats, count, tiles_n, nullptr, 0.f,
+                                nullptr, true);
     x = normed;
   }
   auto one = [&](const PrefillMatrix& w) {
@@ -766,20 +797,22 @@ int eg::prefill_qkv_rope(eg_context* ctx, const float* x, uint32_t m, uint32_t k
       !one_launch(x, m, k, block_size, encoding, bits, mats, 3, &tiles_n))
     return EG_OK;
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
+  bool xb = false;
   if (norm && !fold_norm(ctx, tiles_n * tiles_m, norm)) {
     if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "matmul_q4_prefill: RMSNorm needs a buffer for the normed rows");
-    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    xb = ctx->prefill_xb16;
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed, xb);
     if (st != EG_OK) return st;
     x = normed;
     norm = nullptr;
   }
   *done = true;
-  return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, 3, tiles_n, norm, eps, &rope);
+  return launch_multi(ctx, x, m, k, block_size, encoding, bits, mats, 3, tiles_n, norm, eps, &rope, xb);
 }
 
 int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size,
                             int encoding, int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out,
-                            float* scratch, const float* norm, float eps, float* normed) {
+                            float* scratch, const float* norm, float eps, float* normed, bool out_bf16) {
   const char* op = "matmul_q4_prefill";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!out || !scratch || gate.n != up.n)
@@ -794,21 +827,23 @@ int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_
     const PrefillMatrix gu[2] = {{gate.packed, gate.scales, gate.zeros, gate.bias, nullptr, scratch, n, 2 * n, 0},
                                  {up.packed, up.scales, up.zeros, up.bias, nullptr, scratch, n, 2 * n, n}};
     int st = eg::prefill_gemm_multi(ctx, x, m, k, block_size, encoding, bits, gu, 2, norm, eps, normed);
-    if (st == EG_OK && m > 0 && n > 0) st = eg::silu_mul_rows(ctx, scratch, m, n, out);
+    if (st == EG_OK && m > 0 && n > 0) st = eg::silu_mul_rows(ctx, scratch, m, n, out, out_bf16);
     return st;
   }
   const uint32_t tiles_x = (n + 31) / 32;
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
   const int kg = groups_for(ctx, (uint64_t)tiles_x * tiles_m);
+  bool xb = false;
   if (norm && !fold_norm(ctx, (uint64_t)tiles_x * tiles_m, norm)) {
     if (!normed) return eg::fail(ctx, EG_ERR_INVALID, "%s: RMSNorm needs a buffer for the normed rows", op);
-    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed);
+    xb = ctx->prefill_xb16;
+    const int st = eg::rmsnorm_rows(ctx, x, norm, m, k, eps, normed, xb);
     if (st != EG_OK) return st;
     x = normed;
     norm = nullptr;
   }
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u,
-                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, out_bf16 ? 1u : 0u, {}};
   for (int i = 0; i < 2; i++) {
     const PrefillMatrix& w = pair[i];
     a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, nullptr,
@@ -816,6 +851,7 @@ int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_
   }
   const dim3 grid(tiles_x, (uint32_t)tiles_m, 1);
   if (norm) launch_chunked<true, true>(encoding, kg, grid, ctx->stream, a);
+  else if (xb) launch_chunked<true, false, false, true>(encoding, kg, grid, ctx->stream, a);
   else launch_chunked<true, false>(encoding, kg, grid, ctx->stream, a);
   return eg::check_launch(ctx, op);
 }

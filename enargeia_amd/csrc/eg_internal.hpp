@@ -47,6 +47,8 @@ struct eg_context {
   bool prefill_pair = true;
   // the prompt chain's RoPE and cache append in the q|k|v launch (false: rope_append's launch)
   bool prefill_rope = true;
+  // the prompt chain's GEMM inputs produced as bf16 rows where the GEMM stages them (false: f32)
+  bool prefill_xb16 = true;
   uint32_t attention_split_tiles = 8;
   uint32_t attention_split_fill = 1;
   // Resident workgroups per CU of each kernel launched through this context (from
@@ -139,10 +141,10 @@ int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float
 
 // eg_matmul_q4_prefill with a residual added in the epilogue: out[r * out_stride + col +
 // out_offset] = sum_k x[r, k] W[col, k] + bias[col] + residual[same index] (residual nullable;
-// it may not alias out).
+// it may not alias out). x_bf16: x holds bf16 rows (the chunked staging only).
 int prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales, const uint32_t* zeros,
                  const float* bias, const float* residual, float* out, const eg_matmul_q4_dims* dims, int encoding,
-                 int bits);
+                 int bits, bool x_bf16 = false);
 
 // Several matrices that share x (m rows of k values), the quant block size and the encoding in
 // ONE launch - the prompt chain's q|k|v and gate|up: for each matrix s (at most 3),
@@ -182,8 +184,13 @@ int prefill_qkv_rope(eg_context* ctx, const float* x, uint32_t m, uint32_t k, ui
                      const PrefillRope& rope, bool* done);
 // Chunk attention over caches that already hold the chunk's rows, q_rope already written (the
 // launches of eg_attention_prefill after its rope_append); dims as that entry point checks them.
+// out_bf16: the output rows stored as bf16 (egd::pack_bf16), the o projection's x.
 int attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16_t* k_cache, const uint16_t* v_cache,
-                          float* out, const eg_attention_prefill_dims& d);
+                          float* out, const eg_attention_prefill_dims& d, bool out_bf16 = false);
+// Whether a prefill GEMM over (k, block size, bits, x, packed) takes the chunked staging (the
+// launches that can stage bf16 rows of x).
+bool prefill_chunked(uint32_t m, uint32_t n, uint32_t k, uint32_t block_size, int bits, const void* x,
+                     const uint32_t* packed);
 int check_attention_prefill(eg_context* ctx, const char* op, const eg_attention_prefill_dims* dims);
 // The SwiGLU pair: out[r][j] = SiLU(x[r] . gate_j + bias) * (x[r] . up_j + bias), j < gate.n, rows
 // gate.n apart (the outputs and strides in gate and up are ignored). One launch of paired tiles
@@ -191,7 +198,7 @@ int check_attention_prefill(eg_context* ctx, const char* op, const eg_attention_
 // norm, eps, normed: as prefill_gemm_multi's.
 int prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32_t block_size, int encoding,
                         int bits, const PrefillMatrix& gate, const PrefillMatrix& up, float* out, float* scratch,
-                        const float* norm = nullptr, float eps = 0.f, float* normed = nullptr);
+                        const float* norm = nullptr, float eps = 0.f, float* normed = nullptr, bool out_bf16 = false);
 
 // Row-wise kernels of the prefill chain (one workgroup per row):
 //   embed_rows: out[r] = the dequantized table row of ids[r] (ops.ts:222-233), r < rows;
@@ -200,8 +207,10 @@ int prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_t k,
 //   2n, ops.ts:207-216).
 int embed_rows(eg_context* ctx, const uint32_t* ids, uint32_t rows, const uint32_t* packed, const float* scales,
                const uint32_t* zeros, uint32_t hidden, uint32_t block_size, int encoding, int bits, float* out);
-int rmsnorm_rows(eg_context* ctx, const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* out);
-int silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out);
+// out_bf16: the rows stored as bf16 (egd::pack_bf16), for a GEMM that stages them as they are.
+int rmsnorm_rows(eg_context* ctx, const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* out,
+                 bool out_bf16 = false);
+int silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out, bool out_bf16 = false);
 
 // Resolves the calling thread's current device's copy of the no-alloc scratch array
 // (hipGetSymbolAddress, once per device) into ctx->noalloc_scratch.
@@ -477,6 +486,15 @@ __device__ __forceinline__ void rope_table(double2* cs, uint32_t i, uint32_t pos
   const double angle = (double)position / pow((double)theta, (2.0 * i) / D);
   cs[i] = make_double2(cos(angle), sin(angle));
 }
+// Two floats to a packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32 on gfx950). Every
+// bf16 rounding of the prompt chain's x goes through it, whether a GEMM's staging or the kernel
+// that produced x does it, so both give the same bits.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Data one workgroup hands another inside a launch: agent-scope atomic stores and loads (the sc1
 // bit on gfx950), which write through and read past the XCD-private caching of ordinary
 // accesses - the instructions the memory model's agent-scope atomics use. A writer drains its

@@ -46,12 +46,19 @@ __device__ __forceinline__ float block_total(float v) {
 }
 
 // n is a multiple of 4 (checked on the host).
+// Four results stored as f32, or as bf16 (egd::pack_bf16) for a GEMM that stages them as they are.
+template <bool B16>
+__device__ __forceinline__ void store4(float* out, size_t i, float4 v) {
+  if (B16) reinterpret_cast<uint2*>(out)[i] = make_uint2(egd::pack_bf16(v.x, v.y), egd::pack_bf16(v.z, v.w));
+  else reinterpret_cast<float4*>(out)[i] = v;
+}
+
+template <bool B16>
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float* x, const float* w, uint32_t n, float eps,
                                                                 float* out) {
   const uint32_t r = blockIdx.x;
   const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)r * n);
   const float4* w4 = reinterpret_cast<const float4*>(w);
-  float4* o4 = reinterpret_cast<float4*>(out + (size_t)r * n);
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < n / 4; i += kThreads) {
     const float4 v = x4[i];
@@ -63,19 +70,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float* x, 
   const float inv = 1.0f / sqrtf(block_total(ss) / (float)n + eps);
   for (uint32_t i = threadIdx.x; i < n / 4; i += kThreads) {
     const float4 v = x4[i], g = w4[i];
-    o4[i] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+    store4<B16>(out, (size_t)r * (n / 4) + i, make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w));
   }
 }
 
+template <bool B16>
 __global__ __launch_bounds__(kThreads) void silu_mul_rows_kernel(const float* x, uint32_t n, float* out) {
   const uint32_t r = blockIdx.x;
   const float4* g4 = reinterpret_cast<const float4*>(x + (size_t)r * 2 * n);
   const float4* u4 = g4 + n / 4;
-  float4* o4 = reinterpret_cast<float4*>(out + (size_t)r * n);
   for (uint32_t i = threadIdx.x; i < n / 4; i += kThreads) {
     const float4 g = g4[i], u = u4[i];
-    o4[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
-                        g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+    store4<B16>(out, (size_t)r * (n / 4) + i,
+                make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                            g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w));
   }
 }
 
@@ -94,18 +102,20 @@ int eg::embed_rows(eg_context* ctx, const uint32_t* ids, uint32_t rows, const ui
 }
 
 int eg::rmsnorm_rows(eg_context* ctx, const float* x, const float* w, uint32_t rows, uint32_t n, float eps,
-                     float* out) {
+                     float* out, bool out_bf16) {
   if (rows == 0) return EG_OK;
   if (rows > 65535 || n % 4 != 0 || !aligned16(x) || !aligned16(w) || !aligned16(out))
     return eg::fail(ctx, EG_ERR_INVALID, "rmsnorm_rows: %u rows of %u (a multiple of 4, 16-byte aligned)", rows, n);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
+  if (out_bf16) hipLaunchKernelGGL(rmsnorm_rows_kernel<true>, dim3(rows), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
+  else hipLaunchKernelGGL(rmsnorm_rows_kernel<false>, dim3(rows), dim3(kThreads), 0, ctx->stream, x, w, n, eps, out);
   return eg::check_launch(ctx, "rmsnorm_rows");
 }
 
-int eg::silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out) {
+int eg::silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out, bool out_bf16) {
   if (rows == 0) return EG_OK;
   if (rows > 65535 || n % 4 != 0 || !aligned16(x) || !aligned16(out))
     return eg::fail(ctx, EG_ERR_INVALID, "silu_mul_rows: %u rows of %u (a multiple of 4, 16-byte aligned)", rows, n);
-  hipLaunchKernelGGL(silu_mul_rows_kernel, dim3(rows), dim3(kThreads), 0, ctx->stream, x, n, out);
+  if (out_bf16) hipLaunchKernelGGL(silu_mul_rows_kernel<true>, dim3(rows), dim3(kThreads), 0, ctx->stream, x, n, out);
+  else hipLaunchKernelGGL(silu_mul_rows_kernel<false>, dim3(rows), dim3(kThreads), 0, ctx->stream, x, n, out);
   return eg::check_launch(ctx, "silu_mul_rows");
 }

@@ -140,7 +140,7 @@ __device__ __forceinline__ void store_tile(const KVTile& t, uint16_t (*Ks)[kRow]
 __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q_rope,
                                                         const uint16_t* __restrict__ k_cache,
                                                         const uint16_t* __restrict__ v_cache, float* __restrict__ out,
-                                                        eg_attention_prefill_dims d, Splits sp) {
+                                                        eg_attention_prefill_dims d, Splits sp, uint32_t out_bf16) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kK][kRow];  // [buffer][key][d]
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD][kRow];  // [buffer][d][key]
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
@@ -288,17 +288,21 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     return;
   }
   const float inv = 1.0f / l;
-  float* dst = out + ((size_t)query * d.heads + h) * kD + 4 * lg;
+  const size_t at = ((size_t)query * d.heads + h) * kD + 4 * lg;
 #pragma unroll
-  for (int n = 0; n < 4; n++)
-    *reinterpret_cast<float4*>(dst + 16 * n) = make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
+  for (int n = 0; n < 4; n++) {
+    const float4 v = make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
+    if (out_bf16) *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + at + 16 * n) =
+        make_uint2(egd::pack_bf16(v.x, v.y), egd::pack_bf16(v.z, v.w));
+    else *reinterpret_cast<float4*>(out + at + 16 * n) = v;
+  }
 }
 
 // The splits merged: out = sum_z o_z e^(m_z - M) / sum_z l_z e^(m_z - M), M = max_z m_z, splits
 // in order (an empty split has m = NEG_LARGE and l = 0, weight 0, and its o is not read). One
 // thread per 4 elements of a row.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                      uint32_t rows, uint32_t splits) {
+                                                      uint32_t rows, uint32_t splits, uint32_t out_bf16) {
   const size_t total = (size_t)rows * kD;
   const float* m = part + (size_t)splits * total;
   const float* l = m + (size_t)splits * rows;
@@ -319,7 +323,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       acc.z = fmaf(v.z, w, acc.z);
       acc.w = fmaf(v.w, w, acc.w);
     }
-    reinterpret_cast<float4*>(out)[idx] = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+    const float4 v = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+    if (out_bf16) reinterpret_cast<uint2*>(out)[idx] = make_uint2(egd::pack_bf16(v.x, v.y), egd::pack_bf16(v.z, v.w));
+    else reinterpret_cast<float4*>(out)[idx] = v;
   }
 }
 
@@ -348,7 +354,7 @@ int eg::check_attention_prefill(eg_context* ctx, const char* op, const eg_attent
 }
 
 int eg::attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16_t* k_cache, const uint16_t* v_cache,
-                              float* out, const eg_attention_prefill_dims& d) {
+                              float* out, const eg_attention_prefill_dims& d, bool out_bf16) {
   const char* op = "attention_prefill";
   if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches must be 16-byte aligned", op);
@@ -379,11 +385,12 @@ int eg::attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16
     sp.o = reinterpret_cast<float*>(eg::partials(ctx));
   }
   hipLaunchKernelGGL(attention_kernel, dim3(blocks, d.heads, sp.count), dim3(256), 0, ctx->stream, q_rope, k_cache,
-                     v_cache, out, d, sp);
+                     v_cache, out, d, sp, out_bf16 ? 1u : 0u);
   if (sp.o) {
     const uint64_t total = rows * kD;
     const uint32_t cblocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256, (uint64_t)ctx->cu_count * 8);
-    hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count);
+    hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count,
+                       out_bf16 ? 1u : 0u);
   }
   return eg::check_launch(ctx, op);
 }

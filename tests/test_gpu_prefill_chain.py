@@ -135,14 +135,16 @@ def test_prefill_chain_config4(device):
         dm.release()
 
 
-@pytest.mark.parametrize("switch", ["EG_PREFILL_PAIR", "EG_PREFILL_ROPE"])
+@pytest.mark.parametrize("switch", ["EG_PREFILL_PAIR", "EG_PREFILL_ROPE", "EG_PREFILL_XB16"])
 @pytest.mark.parametrize("chunk", [None, 64])
 def test_prefill_fused_launches_match_unfused_bit_exactly(device, switch, chunk):
     """The chain's fused launches against their unfused forms, in a second context created with
     the switch off, to the bit (logits and both caches): EG_PREFILL_PAIR - gate|up as one launch of
     paired tiles with SiLU·up in its epilogue against gate | up then silu_mul_rows;
     EG_PREFILL_ROPE - RoPE and the cache append in the q|k|v launch's epilogue against
-    rope_append's launch. The same sums in the same order, the same rotation and roundings."""
+    rope_append's launch; EG_PREFILL_XB16 - GEMM inputs stored as bf16 rows by the kernels that
+    produce them against f32 rows rounded to bf16 in the GEMMs' staging. The same sums in the same
+    order, the same rotation and roundings."""
     import os
     from enargeia_amd import kernels as K
     os.environ[switch] = "0"
