@@ -146,7 +146,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
   const uint32_t lr = lane & 15u, lg = lane >> 4;  // MFMA lane coordinates
   const uint32_t h = blockIdx.y, kv = h / (d.heads / d.kv_heads);
-  const uint32_t q0 = blockIdx.x * kQ;
+  // the last query blocks (the longest causal walks) first, so they do not start last
+  const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * kQ;
   const uint32_t query = q0 + wave * 16 + lr;  // this lane's query (its column of S^T and O^T)
 
   // Q^T fragments (B operand of S^T = K Q^T): query lr, d 32 ks + 8 lg .. +8.
