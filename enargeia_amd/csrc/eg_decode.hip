@@ -137,24 +137,6 @@ struct Prefetch {
   }
 };
 
-// Wave-wide max or sum: four DPP steps reduce each row of 16 lanes (quad pairs, quads, half-row
-// mirror, row mirror: every lane of a row then holds the row's value), and the four rows' values
-// are read as scalars and combined in row order - no LDS round trip.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
-template <bool MAX>
-__device__ __forceinline__ float wave_reduce(float v) {
-  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
-  v = op(v, dpp<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = op(v, dpp<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = op(v, dpp<0x141>(v));  // row_half_mirror
-  v = op(v, dpp<0x140>(v));  // row_mirror
-  auto row = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
-  return op(op(row(0), row(16)), op(row(32), row(48)));
-}
-
 // The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
 // statistics and the partial o, written to po/pm/pl, from what `pre` loaded.
 template <int D, int CHUNK, int GMAX>
@@ -246,19 +228,20 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   }
   __syncthreads();
 
-  // softmax statistics: one wave per head, lanes over the chunk, fixed-order reductions
+  // softmax statistics: one wave per head, lanes over the chunk, fixed-order reductions (DPP
+  // within rows, a swizzle and readlanes across them)
   const uint32_t wave = tid >> 6, lane = tid & 63u;
   for (uint32_t g = wave; g < ng; g += kThreads / 64) {
     float m = -INFINITY;
     for (uint32_t j = lane; j < CHUNK; j += 64) m = fmaxf(m, p[g][j]);
-    m = wave_reduce<true>(m);
+    m = egd::team_allmax<64>(m);
     float l = 0.f;
     for (uint32_t j = lane; j < CHUNK; j += 64) {
       const float e = j < live ? expf(p[g][j] - m) : 0.f;
       p[g][j] = e;
       l += e;
     }
-    l = wave_reduce<false>(l);
+    l = egd::team_allsum<64>(l);
     if (lane == 0) {
       mstat[g] = m;
       lstat[g] = l;
