@@ -110,6 +110,7 @@ int eg_create(int device, eg_context** out_ctx) {
   if (const char* pp = std::getenv("EG_PREFILL_PAIR")) ctx->prefill_pair = std::atoi(pp) != 0;
   if (const char* pr = std::getenv("EG_PREFILL_ROPE")) ctx->prefill_rope = std::atoi(pr) != 0;
   if (const char* xb = std::getenv("EG_PREFILL_XB16")) ctx->prefill_xb16 = std::atoi(xb) != 0;
+  if (const char* xc = std::getenv("EG_PREFILL_XCD")) ctx->prefill_xcd = std::atoi(xc) != 0;
   if (const char* a = std::getenv("EG_ATTENTION_SPLIT")) {
     int t = 0, f = 0;
     if (std::sscanf(a, "%d,%d", &t, &f) == 2 && t >= 1 && t <= 64 && f >= 1 && f <= 8) {

@@ -68,6 +68,8 @@ struct PrefillArgs {
   uint32_t rope_pos0, q_heads, kv_heads;
   uint32_t out_bf16;  // PAIR launches: SiLU(g) * u stored as bf16 (the next GEMM's x, bit-for-bit
                       // what its staging would round it to)
+  uint32_t xcd_rows;  // grid.y a multiple of 8, grid.z 1: tiles mapped so that each XCD runs whole
+                      // row tiles (below)
   PrefillMat mats[kMaxSegs];
 };
 
@@ -308,12 +310,21 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
   uint16_t(*As)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes);
   uint16_t(*Bs)[kLds] = reinterpret_cast<uint16_t(*)[kLds]>(lds + group * kStageBytes + kTile * kLds * 2u);
   const uint32_t tid = threadIdx.x & 255u, wave = tid >> 6, lane = tid & 63u;
+  // The tile (tx, ty). Workgroups are dispatched to the 8 XCDs in turn (workgroup L of the grid
+  // on XCD L % 8), each with its own L2. With xcd_rows the workgroups of one XCD take whole row
+  // tiles (row tiles k, k + 8, ... on XCD k, every column tile of each), so a row tile's x is
+  // fetched into one L2 instead of up to eight; otherwise the grid's own order.
+  uint32_t tx = blockIdx.x, ty = blockIdx.y;
+  if (a.xcd_rows) {
+    const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y, k = L % 8u, j = L / 8u;
+    ty = k + 8u * (j / gridDim.x);
+    tx = j % gridDim.x;
+  }
   // the matrix whose rows this thread stages (wave-uniform), and the tile's first row of it
   const uint32_t half = PAIR ? __builtin_amdgcn_readfirstlane(wave >> 1) : 0u;
-  const PrefillMat& w = a.mats[PAIR ? half : select_matrix(a, blockIdx.x)];
-  const uint32_t m0 = blockIdx.y * kTile;
-  const uint32_t n0 = PAIR ? 32u * blockIdx.x - 32u * half
-                           : (blockIdx.x - (w.tiles_end - ((w.n + kTile - 1) / kTile))) * kTile;
+  const PrefillMat& w = a.mats[PAIR ? half : select_matrix(a, tx)];
+  const uint32_t m0 = ty * kTile;
+  const uint32_t n0 = PAIR ? 32u * tx - 32u * half : (tx - (w.tiles_end - ((w.n + kTile - 1) / kTile))) * kTile;
   const uint32_t wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const uint32_t kbeg = blockIdx.z * a.k_per_split, kend = min(a.k, kbeg + a.k_per_split);
 
@@ -439,7 +450,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
           sums[(wm + i * 16 + 4 * (lane >> 4) + e) * kTile + wn + j * 16 + (lane & 15)] = acc[i][j][e];
     __syncthreads();
     if (ROPE) {
-      const uint32_t s = select_matrix(a, blockIdx.x), hd = n0 / kTile;
+      const uint32_t s = select_matrix(a, tx), hd = n0 / kTile;
       auto sum = [&](uint32_t r, uint32_t c) {
         float v = reinterpret_cast<const float*>(lds)[r * kTile + c];
 #pragma unroll
@@ -477,7 +488,7 @@ __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
       const PrefillMat& g = a.mats[0];
       const PrefillMat& u = a.mats[1];
       for (uint32_t idx = threadIdx.x; idx < kTile * 32u; idx += 256u * KG) {
-        const uint32_t r = idx / 32u, c = idx % 32u, row = m0 + r, col = 32u * blockIdx.x + c;
+        const uint32_t r = idx / 32u, c = idx % 32u, row = m0 + r, col = 32u * tx + c;
         if (row >= a.m || col >= g.n) continue;
         float gv = reinterpret_cast<const float*>(lds)[r * kTile + c];
         float uv = reinterpret_cast<const float*>(lds)[r * kTile + c + 32u];
@@ -552,6 +563,14 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
     const size_t o = (size_t)row * out_stride + col + out_offset;
     out[o] = acc + (bias ? bias[col] : 0.f) + (residual ? residual[o] : 0.f);
   }
+}
+
+// Whether a launch maps whole row tiles to each XCD: its grid has no K split and a multiple of 8
+// row tiles, and its column tiles are not a multiple of 8 (with a multiple of 8 the grid's own
+// order already keeps each column tile on one XCD, which suits the wide launches whose weight
+// tiles outweigh their x tiles).
+uint32_t xcd_rows_for(const eg_context* ctx, dim3 grid) {
+  return ctx->prefill_xcd && grid.z == 1 && grid.y % 8 == 0 && grid.x % 8 != 0 ? 1u : 0u;
 }
 
 // One launch of the chunked staging with kg groups of 4 waves per workgroup.
@@ -629,10 +648,11 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   const bool split = splits > 1;
   PrefillArgs a{x, split ? reinterpret_cast<float*>(eg::partials(ctx)) : nullptr, m, k, bs, dims->blocks_per_row,
                 k_per_split, bits, (uint32_t)__builtin_ctz(bs), 1u, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr,
-                0u, 0u, 0u, 0u, {}};
+                0u, 0u, 0u, 0u, 0u, {}};
   a.mats[0] = PrefillMat{packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, dims->use_bias ? bias : nullptr,
                          residual, out, n, dims->out_stride, dims->out_offset, tiles_n};
   const dim3 grid(tiles_n, tiles_m, (uint32_t)splits);
+  a.xcd_rows = xcd_rows_for(ctx, grid);
   const bool chunked = eg::prefill_chunked(m, n, k, bs, bits, x, packed);
   if (x_bf16 && !chunked)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: bf16 rows of x need the chunked staging", op);
@@ -703,7 +723,7 @@ int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32
                  const eg::PrefillMatrix* mats, uint32_t count, uint64_t tiles_n, const float* norm, float eps,
                  const eg::PrefillRope* rope = nullptr, bool x_bf16 = false) {
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), count,
-                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, 0u, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, 0u, 0u, {}};
   if (rope) {
     a.rope = rope->table;
     a.q_rope = rope->q_rope;
@@ -723,6 +743,7 @@ int launch_multi(eg_context* ctx, const float* x, uint32_t m, uint32_t k, uint32
   const uint64_t tiles_m = (m + kTile - 1) / kTile;
   const int kg = groups_for(ctx, tiles_n * tiles_m);
   const dim3 grid((uint32_t)tiles_n, (uint32_t)tiles_m, 1);
+  a.xcd_rows = xcd_rows_for(ctx, grid);
   if (rope) {
     if (norm) launch_chunked<false, true, true>(encoding, kg, grid, ctx->stream, a);
     else if (x_bf16) launch_chunked<false, false, true, true>(encoding, kg, grid, ctx->stream, a);
@@ -843,13 +864,14 @@ int eg::prefill_gemm_swiglu(eg_context* ctx, const float* x, uint32_t m, uint32_
     norm = nullptr;
   }
   PrefillArgs a{x, nullptr, m, k, block_size, k / block_size, k, bits, (uint32_t)__builtin_ctz(block_size), 2u,
-                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, out_bf16 ? 1u : 0u, {}};
+                norm, eps, nullptr, nullptr, nullptr, nullptr, 0u, 0u, 0u, out_bf16 ? 1u : 0u, 0u, {}};
   for (int i = 0; i < 2; i++) {
     const PrefillMatrix& w = pair[i];
     a.mats[i] = PrefillMat{w.packed, w.scales, encoding == EG_ENC_SIGNED ? nullptr : w.zeros, w.bias, nullptr,
                            w.out, n, n, 0, tiles_x};
   }
   const dim3 grid(tiles_x, (uint32_t)tiles_m, 1);
+  a.xcd_rows = xcd_rows_for(ctx, grid);
   if (norm) launch_chunked<true, true>(encoding, kg, grid, ctx->stream, a);
   else if (xb) launch_chunked<true, false, false, true>(encoding, kg, grid, ctx->stream, a);
   else launch_chunked<true, false>(encoding, kg, grid, ctx->stream, a);

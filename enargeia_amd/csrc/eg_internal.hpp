@@ -49,6 +49,9 @@ struct eg_context {
   bool prefill_rope = true;
   // the prompt chain's GEMM inputs produced as bf16 rows where the GEMM stages them (false: f32)
   bool prefill_xb16 = true;
+  // prefill GEMM tiles mapped so each XCD runs whole row tiles where that applies (false: the
+  // grid's own order)
+  bool prefill_xcd = true;
   uint32_t attention_split_tiles = 8;
   uint32_t attention_split_fill = 1;
   // Resident workgroups per CU of each kernel launched through this context (from

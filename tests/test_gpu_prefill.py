@@ -212,6 +212,18 @@ def test_prefill_swiglu_pair(device, unpaired, m, n, k, sym):
     assert excess.max() <= 1.0, f"swiglu {m}x{n}x{k}: {excess.max() * 100:.1f}% of the carried bar"
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 896, 896), (1024, 896, 4864), (1024, 1152, 896)])
+def test_prefill_row_tiles_per_xcd(device, m, n, k):
+    # A multiple of 8 row tiles and a column-tile count that is not: the launch maps whole row
+    # tiles to each XCD (workgroup L of the grid runs tile (L / 8 % columns, L % 8 + 8 * (L / 8 /
+    # columns))), every tile exactly once - against the bf16 model like any other shape. The
+    # K = 4864 case splits K and keeps the grid's own order.
+    x, q = config3(m, n, k, 0x5EED ^ (m + n + k))
+    got = run_prefill(device, x, q, None, m)
+    model = oracle.linear_q_bf16_fast(x, q, None, m)
+    assert_close(got, model, *model_tol(model), label=f"xcd rows {m}x{n}x{k}")
+
+
 def test_prefill_swiglu_rejects_bad_dims(device):
     import ctypes
     from enargeia_amd import _lib

@@ -179,3 +179,39 @@ def test_prefill_fused_launches_match_unfused_bit_exactly(device, switch, chunk)
     np.testing.assert_array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
     np.testing.assert_array_equal(runs[0][2], runs[1][2])
     np.testing.assert_array_equal(runs[0][3], runs[1][3])
+
+
+def test_prefill_row_tiles_per_xcd_bit_exact(device):
+    """A 512-token prompt (8 row tiles: the o, down and q|k|v launches map whole row tiles to
+    each XCD) against the grid's own order (EG_PREFILL_XCD=0), logits and caches to the bit."""
+    import os
+    from enargeia_amd import kernels as K
+    os.environ["EG_PREFILL_XCD"] = "0"
+    try:
+        other = K.Device(0)
+    finally:
+        del os.environ["EG_PREFILL_XCD"]
+    cfg = ModelConfig(layers=2, max_context=1024)
+    m = synthetic_model(cfg)
+    prompt = [int(t) for t in oracle.random_ids(512, 78, cfg.vocab)]
+    n = cfg.layers * cfg.max_context * cfg.kv_heads * cfg.head_dim
+    shape = (cfg.layers, cfg.max_context, cfg.kv_heads * cfg.head_dim)
+    runs = []
+    try:
+        for dev in (device, other):
+            dm = DeviceModel(dev, m)
+            dec = Decoder(dm)
+            try:
+                tok = dec.prefill(0, prompt)
+                kc = dev.read_array(dec.buffers.k_cache, np.uint16, n).reshape(shape)[:, :len(prompt)]
+                vc = dev.read_array(dec.buffers.v_cache, np.uint16, n).reshape(shape)[:, :len(prompt)]
+                runs.append((tok, dec.logits().copy(), kc, vc))
+            finally:
+                dec.close()
+                dm.release()
+    finally:
+        other.close()
+    assert runs[0][0] == runs[1][0]
+    np.testing.assert_array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    np.testing.assert_array_equal(runs[0][2], runs[1][2])
+    np.testing.assert_array_equal(runs[0][3], runs[1][3])
