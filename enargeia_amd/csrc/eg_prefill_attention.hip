@@ -300,31 +300,69 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 }
 
 // The splits merged: out = sum_z o_z e^(m_z - M) / sum_z l_z e^(m_z - M), M = max_z m_z, splits
-// in order (an empty split has m = NEG_LARGE and l = 0, weight 0, and its o is not read). One
-// thread per 4 elements of a row.
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                      uint32_t rows, uint32_t splits, uint32_t out_bf16) {
-  const size_t total = (size_t)rows * kD;
-  const float* m = part + (size_t)splits * total;
-  const float* l = m + (size_t)splits * rows;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total / 4; idx += (size_t)gridDim.x * blockDim.x) {
-    const size_t row = idx / (kD / 4);
-    float M = kMasked;
-    for (uint32_t z = 0; z < splits; z++) M = fmaxf(M, m[(size_t)z * rows + row]);
-    float L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t z = 0; z < splits; z++) {
-      const float lz = l[(size_t)z * rows + row];
-      if (!(lz > 0.f)) continue;
+// in order (an empty split has m = NEG_LARGE and l = 0, weight 0). One thread per 4 elements of a
+// row. A row's splits past its causal limit are empty (z > zmax: the split's first key is past the
+// row's last) and are not read. Up to kFastSplits splits, the statistics and values of the
+// others are loaded at once (no chain of dependent round trips); more splits take the loop. Both
+// add in split order: the same result.
+constexpr uint32_t kFastSplits = 8;
+
+__device__ __forceinline__ float4 merged(const float* __restrict__ part, const float* m, const float* l, size_t total,
+                                         uint32_t rows, size_t row, size_t idx, uint32_t splits, uint32_t zmax) {
+  float M = kMasked, L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (splits <= kFastSplits) {
+    float mz[kFastSplits], lz[kFastSplits];
+    float4 vz[kFastSplits];
+#pragma unroll
+    for (uint32_t z = 0; z < kFastSplits; z++) {
+      if (z <= zmax) {
+        mz[z] = m[(size_t)z * rows + row];
+        lz[z] = l[(size_t)z * rows + row];
+        vz[z] = reinterpret_cast<const float4*>(part + (size_t)z * total)[idx];
+      }
+    }
+#pragma unroll
+    for (uint32_t z = 0; z < kFastSplits; z++)
+      if (z <= zmax) M = fmaxf(M, mz[z]);
+#pragma unroll
+    for (uint32_t z = 0; z < kFastSplits; z++) {
+      if (z <= zmax && lz[z] > 0.f) {
+        const float w = expf(mz[z] - M);
+        L = fmaf(lz[z], w, L);
+        acc.x = fmaf(vz[z].x, w, acc.x);
+        acc.y = fmaf(vz[z].y, w, acc.y);
+        acc.z = fmaf(vz[z].z, w, acc.z);
+        acc.w = fmaf(vz[z].w, w, acc.w);
+      }
+    }
+  } else {
+    for (uint32_t z = 0; z <= zmax; z++) M = fmaxf(M, m[(size_t)z * rows + row]);
+    for (uint32_t z = 0; z <= zmax; z++) {
+      const float lzz = l[(size_t)z * rows + row];
+      if (!(lzz > 0.f)) continue;
       const float w = expf(m[(size_t)z * rows + row] - M);
-      L = fmaf(lz, w, L);
+      L = fmaf(lzz, w, L);
       const float4 v = reinterpret_cast<const float4*>(part + (size_t)z * total)[idx];
       acc.x = fmaf(v.x, w, acc.x);
       acc.y = fmaf(v.y, w, acc.y);
       acc.z = fmaf(v.z, w, acc.z);
       acc.w = fmaf(v.w, w, acc.w);
     }
-    const float4 v = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+  }
+  return make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                      uint32_t rows, uint32_t splits, uint32_t out_bf16, uint32_t heads,
+                                                      uint32_t query_begin, uint32_t split_keys) {
+  const size_t total = (size_t)rows * kD;
+  const float* m = part + (size_t)splits * total;
+  const float* l = m + (size_t)splits * rows;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total / 4; idx += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = idx / (kD / 4);
+    const uint32_t zmax = min(splits - 1, (query_begin + (uint32_t)(row / heads)) / split_keys);
+    const float4 v = merged(part, m, l, total, rows, row, idx, splits, zmax);
     if (out_bf16) reinterpret_cast<uint2*>(out)[idx] = make_uint2(egd::pack_bf16(v.x, v.y), egd::pack_bf16(v.z, v.w));
     else reinterpret_cast<float4*>(out)[idx] = v;
   }
@@ -391,7 +429,7 @@ int eg::attention_prefill_run(eg_context* ctx, const float* q_rope, const uint16
     const uint64_t total = rows * kD;
     const uint32_t cblocks = (uint32_t)std::min<uint64_t>((total / 4 + 255) / 256, (uint64_t)ctx->cu_count * 8);
     hipLaunchKernelGGL(combine_kernel, dim3(cblocks), dim3(256), 0, ctx->stream, sp.o, out, (uint32_t)rows, sp.count,
-                       out_bf16 ? 1u : 0u);
+                       out_bf16 ? 1u : 0u, d.heads, d.query_begin, sp.keys);
   }
   return eg::check_launch(ctx, op);
 }
