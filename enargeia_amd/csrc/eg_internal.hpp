@@ -83,8 +83,11 @@ constexpr size_t kPartialsBytes = kWorkspaceBytes - kPartialsOffset;
 
 // Second stage of every multi-workgroup argmax: one workgroup reduces `groups` partials
 // (value bits, index) in a fixed order into result = [index, value bits]. A separate launch
-// rather than a last-arriving workgroup: the arrival protocol needs an agent-scope release
-// (an L2 writeback) in every workgroup, which costs far more than a launch.
+// rather than a last-arriving workgroup. Measured on the 151,936-row LM head (2048 workgroups):
+// with an L2 write-back release per workgroup the arrival protocol costs far more than a launch;
+// with coherent stores (egd::put / drain), one arrival counter and egd::get reads it added 12 us
+// over the GEMV alone (every workgroup's atomic serialises on the one word), and with 16 group
+// counters 128 bytes apart 5.7 us - against 3.9 us for this launch.
 void launch_argmax_finalize(eg_context* ctx, const uint32_t* partials, uint32_t groups, uint32_t sentinel_index,
                             uint32_t* result);
 

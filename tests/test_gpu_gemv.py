@@ -190,6 +190,24 @@ def test_lm_head_q8_config2_logits_and_fused_argmax(device):
     assert res[1] == logits[res[0]].view(np.uint32)
 
 
+@pytest.mark.parametrize("r1,r2", [(37, 39000), (20000, 20001), (5, 38000)])
+def test_lm_head_fused_argmax_across_workgroups_and_calls(device, r1, r2):
+    # The fused argmax is reduced by the launch's last-arriving workgroup, which then resets the
+    # context's arrival counter: consecutive calls on one context each reduce every workgroup's
+    # partial, and two equal maxima in rows far apart (different workgroups) resolve to the lower
+    # index, as the reference's argmax does (test/reference/ops.ts:237-244: the first maximum kept).
+    rows, hidden = 40000, 896
+    h = oracle.normal_floats(hidden, 0x5EED ^ r1, 1.0)
+    t = oracle.normal_floats(rows * hidden, 0x5EED ^ r2, 0.02).reshape(rows, hidden).copy()
+    t[r1] = t[r2] = 0.05 * np.sign(h)  # the same codes and scale: bit-identical logits, the largest
+    q = oracle.quantize_sym(t.ravel(), rows, hidden, 8, hidden)
+    for _ in range(2):
+        logits, res = _run_head(device, q, h, fused=True)
+        assert logits[r1].view(np.uint32) == logits[r2].view(np.uint32)
+        assert res[0] == min(r1, r2) == int(np.argmax(logits))
+        assert res[1] == logits[res[0]].view(np.uint32)
+
+
 def test_lm_head_q8_reference_format_with_offset(device):
     rows, hidden = 4096, 896
     q = oracle.quantize_blocks_n(oracle.random_floats(rows * hidden, 61), rows, hidden, 8)
