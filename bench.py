@@ -330,12 +330,14 @@ def main() -> int:
     # ---- roofline: the dominant kernel = the K=896 batched launch ----
     t896_ms = dominant_ms
     achieved = BATCH896_BYTES / (t896_ms * 1e-3) / 1e9
+    traffic, traffic_commit = measured_traffic()
     roofline = {"bound": "hbm", "kernel": "gemv_kernel<4,SIGNED,...,BATCHED> (K=896 projections, 24 layers)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": "not measured in this run: the committed rocprofv3 --pmc summary "
-                                  "profiles/gemv_batched_k896_config1_traffic.md (FETCH_SIZE + WRITE_SIZE per "
-                                  "dispatch, each scaled by a calibration kernel of known size)",
+                                  "profiles/gemv_batched_config1_traffic.md (FETCH_SIZE + WRITE_SIZE per "
+                                  "dispatch, each scaled by a calibration kernel of known size), measured on the "
+                                  f"kernels of commit {traffic_commit}",
                 "bytes_per_launch": BATCH896_BYTES, "avg_launch_us": round(t896_ms * 1e3, 2)}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(mats)
@@ -685,27 +687,31 @@ def prefill_numbers(dev, ev, stream, args) -> dict:
 
 
 CALIBRATION_BYTES = 256 << 20
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_batched_k896_config1_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_batched_config1_traffic.md")
 
 
 def measured_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its calibration kernel)."""
+    """(HBM bytes per launch of the dominant kernel, the commit whose kernels were measured), from
+    the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its
+    calibration kernel); (None, None) without it."""
+    traffic, commit = None, None
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip().replace(",", ""))
+                    traffic = int(line.split(":", 1)[1].strip().replace(",", ""))
+                elif line.startswith("traffic_measured_at:"):
+                    commit = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return traffic, commit
 
 
 def traffic_probe() -> int:
     """Dispatches, in order: argmax over CALIBRATION_BYTES of floats (reads exactly that),
     a zero fill of CALIBRATION_BYTES (writes exactly that), then the K=896 batched projection
-    launch three times over three cold replicas. Per-dispatch FETCH_SIZE / WRITE_SIZE of the
-    calibration kernels give the counters' scale; see profiles/."""
+    launch three times over three cold replicas, then the K=4864 one likewise. Per-dispatch
+    FETCH_SIZE / WRITE_SIZE of the calibration kernels give the counters' scale; see profiles/."""
     from enargeia_amd import kernels as K
     from enargeia_amd import quant
 
@@ -721,23 +727,27 @@ def traffic_probe() -> int:
     dev.sync()
     dev.zero(big, CALIBRATION_BYTES)
     dev.sync()
-    rows = [r for _, r, k in PROJECTIONS if k == HIDDEN]
-    mats = [quant.quantize_sym(quant.normal(r * HIDDEN, 300 + i, 0.02), r, HIDDEN, 4, GROUP) for i, r in enumerate(rows)]
-    out = dev.buffer(LAYERS * sum(rows) * 4)
-    x = dev.upload(np.random.default_rng(7).standard_normal(HIDDEN, dtype=np.float32))
-    plans = []
-    for _ in range(3):
-        segs, off = [], 0
-        for _layer in range(LAYERS):
-            for q in mats:
-                segs.append((dev.upload(q.packed), dev.upload(q.scales), None, None, out, q.rows, off))
-                off += q.rows
-        plans.append(K.GemvPlan(dev, HIDDEN, GROUP, segs))
-    for p in plans:
-        p.launch(x)
-    dev.sync()
+    rng = np.random.default_rng(7)
+    for k in (HIDDEN, INTER):
+        rows = [r for _, r, kk in PROJECTIONS if kk == k]
+        mats = [quant.quantize_sym(quant.normal(r * k, 300 + 10 * (k == INTER) + i, 0.02), r, k, 4, GROUP)
+                for i, r in enumerate(rows)]
+        out = dev.buffer(LAYERS * sum(rows) * 4)
+        x = dev.upload(rng.standard_normal(k, dtype=np.float32))
+        plans = []
+        for _ in range(3):
+            segs, off = [], 0
+            for _layer in range(LAYERS):
+                for q in mats:
+                    segs.append((dev.upload(q.packed), dev.upload(q.scales), None, None, out, q.rows, off))
+                    off += q.rows
+            plans.append(K.GemvPlan(dev, k, GROUP, segs))
+        for p in plans:
+            p.launch(x)
+        dev.sync()
     print(json.dumps({"traffic_probe": True, "calibration_bytes": CALIBRATION_BYTES,
-                      "batch896_bytes": BATCH896_BYTES}), flush=True)
+                      "batch896_bytes": BATCH896_BYTES, "batch4864_bytes": STEP_BYTES - BATCH896_BYTES}),
+          flush=True)
     dev.close()
     return 0
 
