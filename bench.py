@@ -142,6 +142,9 @@ def main() -> int:
     ap.add_argument("--skip-decode", action="store_true",
                     help="leave out the config-4 decode measurement (rocprofv3 kernel tracing does not survive the "
                          "decoder's captured graph; --decode-profile covers the decode step eagerly)")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="only the config-4 decode step captured in a hipGraph, with per-wave wall-clock stamps "
+                         "(eg_test_launch_stamps): the per-launch timeline of the step as it is timed")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel and two calibration kernels of known size "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -174,6 +177,11 @@ def main() -> int:
     if args.head_profile:
         dev = K.Device(0)
         print(json.dumps(head_numbers(dev, HipEvents(), dev.stream, args, np.random.default_rng(7))), flush=True)
+        dev.close()
+        return 0
+    if args.decode_timeline:
+        dev = K.Device(0)
+        print(json.dumps(decode_timeline(dev, args)), flush=True)
         dev.close()
         return 0
     if args.decode_profile:
@@ -580,6 +588,96 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     return result
 
 
+STAMP_WAVES = 8192  # per launch slot (eg_test_launch_stamps)
+
+
+def decode_timeline(dev, args) -> dict:
+    """The config-4 decode step as bench.py times it - captured in a hipGraph, at positions
+    1920..2047, one 4-byte readback per token - with every launch writing per-wave wall-clock
+    stamps (eg_test_launch_stamps: each wave's entry and exit, s_memrealtime). Per launch of the
+    step: its duration (first wave in to last wave out) and the gap to the next launch, medians
+    over the timed steps; also the gap between steps (the readback and the next replay's
+    submission). Greedy steps, then the same positions sampled (T 0.7 / top-p 0.9 / penalty 1.1)."""
+    from enargeia_amd import _lib
+    from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, cache_fill, config4_workload, synthetic_model
+
+    lib = _lib.load()
+    hip = ctypes.CDLL("libamdhip64.so")
+    rate_khz = ctypes.c_int()
+    assert hip.hipDeviceGetAttribute(ctypes.byref(rate_khz), 10017, 0) == 0  # hipDeviceAttributeWallClockRate
+    tick_us = 1e3 / rate_khz.value
+    cfg = QWEN25_05B
+    w = config4_workload(cfg)
+    dm = DeviceModel(dev, synthetic_model(cfg))
+    dec = Decoder(dm)
+    kf, vf = cache_fill(cfg, w.fill_seed)
+    dev.write(dec.buffers.k_cache, kf.view(np.uint16))
+    dev.write(dec.buffers.v_cache, vf.view(np.uint16))
+    dev.sync()
+    del kf, vf
+    start = w.prime + len(w.prompt)
+    layer_names = ["q|k|v GEMV (RMSNorm stage)", "attention", "o GEMV (combine stage)", "gate|up SwiGLU pair",
+                   "down GEMV"]
+    result = {"config": "BASELINE config 4 decode step at positions 1920..2047, captured, a readback per token",
+              "wall_clock_mhz": rate_khz.value / 1e3}
+    cap = 5 * cfg.layers + 3
+    buf = dev.buffer(cap * STAMP_WAVES * 16)
+    for mode in ("greedy", "sampled"):
+        if mode == "sampled":
+            dec.set_sampling(0.7, 0.9, 1.1)
+            dec.seed(0x5EED)
+        dev.zero(buf, cap * STAMP_WAVES * 16)
+        _lib.check(lib.eg_test_launch_stamps(dev.ctx, ctypes.c_void_p(buf.ptr), cap, None), dev.ctx)
+        dec.capture()
+        rec = ctypes.c_uint32()
+        _lib.check(lib.eg_test_launch_stamps(dev.ctx, None, 0, ctypes.byref(rec)), dev.ctx)
+        n = rec.value
+        names = [f"L{l} {layer_names[j]}" for l in range(cfg.layers) for j in range(5)]
+        names += ["LM head (final-norm stage)"] + (["sampler"] if mode == "sampled" else []) + ["step tail"]
+        assert n == len(names), f"{n} launches took a slot, {len(names)} expected"
+        for i, t in enumerate(w.prompt):
+            dec.reset(w.prime + i, t)
+            first = dec.step(read_token=True)
+        if mode == "sampled":
+            dec.set_history(list(w.prompt) + [first])
+        dec.reset(start, first)
+        for _ in range(8):
+            dec.step(read_token=True)
+        durs, gaps, steps_us, between = [], [], [], []
+        prev_end = None
+        for _ in range(min(args.steps, 120)):
+            dec.step(read_token=True)
+            raw = np.frombuffer(dev.read(buf, n * STAMP_WAVES * 16), np.uint64).reshape(n, STAMP_WAVES, 2)
+            t0s = np.array([r[r[:, 0] > 0, 0].min() for r in raw], np.float64)
+            t1s = np.array([r[r[:, 1] > 0, 1].max() for r in raw], np.float64)
+            durs.append((t1s - t0s) * tick_us)
+            gaps.append((t0s[1:] - t1s[:-1]) * tick_us)
+            steps_us.append((t1s[-1] - t0s[0]) * tick_us)
+            if prev_end is not None:
+                between.append((t0s[0] - prev_end) * tick_us)
+            prev_end = t1s[-1]
+        d = np.median(np.array(durs), axis=0)
+        g = np.median(np.array(gaps), axis=0)
+        per_kind = {}
+        for j, kind in enumerate(layer_names):
+            per_kind[kind] = {"us": round(float(np.median(d[j:5 * cfg.layers:5])), 2),
+                              "gap_after_us": round(float(np.median(g[j:5 * cfg.layers:5])), 2)}
+        for i in range(5 * cfg.layers, n):
+            per_kind[names[i]] = {"us": round(float(d[i]), 2),
+                                  "gap_after_us": round(float(g[i]), 2) if i < n - 1 else None}
+        result[mode] = {
+            "launches": n, "per_launch": per_kind,
+            "kernel_us_per_step": round(float(d.sum()), 1), "gaps_us_per_step": round(float(g.sum()), 1),
+            "first_in_to_last_out_us": round(float(np.median(steps_us)), 1),
+            "between_steps_us": round(float(np.median(between)), 1) if between else None,
+            "token_us": round(float(np.median(steps_us)) + (float(np.median(between)) if between else 0.0), 1)}
+        log(f"decode timeline ({mode}): {result[mode]}")
+    dec.close()
+    dm.release()
+    buf.release()
+    return result
+
+
 def prompt_throughput(dev, dec, cfg) -> dict:
     """The prompt path (eg_decoder_prefill: chunks of 256 rows through the bf16-MFMA projections
     and the chunk attention, then the first token from the last row): the reference's prefill
@@ -779,7 +877,31 @@ def cpu_baseline(mats):
             "sample": f"the full config-1 step ({STEP_BYTES} B, 168 GEMVs): 1 run on 1 thread, 4 runs on "
                       f"{cores} threads; oracle restatement of the reference's linearQ4 loop",
             "single_core_gbs": round(STEP_BYTES / one / 1e9, 4),
-            "step_ms_single_core": round(one * 1e3, 1), "step_ms_all_cores": round(many * 1e3, 1)}
+            "step_ms_single_core": round(one * 1e3, 1), "step_ms_all_cores": round(many * 1e3, 1),
+            "javascript": js_baseline()}
+
+
+def js_baseline():
+    """The reference's CPU loop in its own language: oracle/linear_q4_time.js (linearQ4 and
+    dequantElement, quant.ts:77-111, restated in plain JavaScript) under the host's Node, one core,
+    over one layer of config 1 (7 GEMVs, 9.41 MB) 20 times; None where no Node is installed."""
+    import shutil
+    import subprocess
+
+    node = shutil.which("node") or shutil.which("nodejs")
+    if not node:
+        return None
+    res = subprocess.run([node, os.path.join(ROOT, "oracle", "linear_q4_time.js"), "20"], capture_output=True,
+                         text=True, timeout=120)
+    if res.returncode != 0:
+        log(f"js baseline failed: {res.stderr.strip()[-300:]}")
+        return None
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    log(f"cpu baseline (JavaScript, Node {r['node']}, 1 core): {r['gbs']:.4f} GB/s")
+    return {"value": round(r["gbs"], 4), "unit": "GB/s", "cores": 1, "node": r["node"],
+            "sample": "one config-1 layer (q, k, v, o, gate, up, down: 9,410,048 B), 20 runs, "
+                      "oracle/linear_q4_time.js",
+            "step_ms": round(r["seconds"] * LAYERS * 1e3, 1)}
 
 
 if __name__ == "__main__":

@@ -93,14 +93,15 @@ int eg_create(int device, eg_context** out_ctx) {
   }
   ctx->stream = ctx->own_stream;
   if (const char* shape = std::getenv("EG_GEMV_SHAPE")) {
-    int t = 0, c = 0, u = 0, d = 2;
-    const int got = std::sscanf(shape, "%d,%d,%d,%d", &t, &c, &u, &d);
+    int t = 0, c = 0, u = 0, d = 2, xl = 0;
+    const int got = std::sscanf(shape, "%d,%d,%d,%d,%d", &t, &c, &u, &d, &xl);
     if (got >= 3 && (t == 8 || t == 16 || t == 32 || t == 64) && c >= 1 && c <= 4 && (u == 1 || u == 2 || u == 4) &&
-        d >= 2 && d <= 8) {
+        d >= 2 && d <= 8 && (xl == 0 || xl == 1)) {
       ctx->gemv_override[0] = t;
       ctx->gemv_override[1] = c;
       ctx->gemv_override[2] = u;
       ctx->gemv_override[3] = d;
+      ctx->gemv_override[4] = xl;
     }
   }
   if (const char* tpw = std::getenv("EG_FUSED_TILES_PER_WAVE")) {
@@ -118,6 +119,7 @@ int eg_create(int device, eg_context** out_ctx) {
       ctx->attention_split_fill = (uint32_t)f;
     }
   }
+  if (const char* g = std::getenv("EG_PREFILL_STAGES")) ctx->prefill_stages = std::atoi(g);
   if (const char* g = std::getenv("EG_PREFILL_GROUPS")) {
     const int v = std::atoi(g);
     if (v == 1 || v == 2 || v == 4) ctx->prefill_groups = v;
@@ -177,7 +179,7 @@ int eg_sync(eg_context* ctx) {
   if (ctx->capturing) return fail(ctx, EG_ERR_STATE, "eg_sync: a graph capture is in progress");
   hipError_t err = hipStreamSynchronize(ctx->stream);
   if (err != hipSuccess) return hip_fail(ctx, err, "eg_sync");
-  return EG_OK;
+  return eg::report_sample_failures(ctx, "eg_sync");
 }
 
 int eg_buf_alloc(eg_context* ctx, size_t bytes, void** out_ptr) {
@@ -216,7 +218,7 @@ int eg_buf_read(eg_context* ctx, const void* src, size_t offset, void* host_dst,
                                   hipMemcpyDeviceToHost, ctx->stream);
   if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
   if (err != hipSuccess) return hip_fail(ctx, err, "eg_buf_read");
-  return EG_OK;
+  return eg::report_sample_failures(ctx, "eg_buf_read");
 }
 
 int eg_buf_zero(eg_context* ctx, void* dst, size_t offset, size_t bytes) {
@@ -227,6 +229,16 @@ int eg_buf_zero(eg_context* ctx, void* dst, size_t offset, size_t bytes) {
   if (blocks > 4096) blocks = 4096;
   zero_fill_kernel<<<(unsigned)blocks, 256, 0, ctx->stream>>>(static_cast<uint8_t*>(dst) + offset, bytes);
   return eg::check_launch(ctx, "eg_buf_zero");
+}
+
+int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t launches, uint32_t* recorded) {
+  if (!ctx) return fail(nullptr, EG_ERR_INVALID, "test_launch_stamps: ctx is NULL");
+  if (ctx->capturing) return fail(ctx, EG_ERR_STATE, "test_launch_stamps: a graph capture is in progress");
+  if (recorded) *recorded = ctx->stamp_next;
+  ctx->stamps = buffer;
+  ctx->stamp_capacity = buffer ? launches : 0u;
+  ctx->stamp_next = 0;
+  return EG_OK;
 }
 
 int eg_graph_begin(eg_context* ctx) {

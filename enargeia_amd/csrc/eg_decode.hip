@@ -312,7 +312,9 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32
                                                                     const float* k, const float* v,
                                                                     uint16_t* k_cache, uint16_t* v_cache,
                                                                     float* partials, uint32_t* counter, float* out,
-                                                                    eg_attention_dims d, const double2* rope) {
+                                                                    eg_attention_dims d, const double2* rope,
+                                                                    uint64_t* stamp_slot) {
+  const egd::WaveStamp stamp(stamp_slot);
   const uint32_t kv = blockIdx.y / HSPLIT, hs = blockIdx.y % HSPLIT;
   const uint32_t c = blockIdx.x;
   const uint32_t chunks = gridDim.x;
@@ -425,11 +427,11 @@ int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, 
   if (dims->chunk == 64) {
     const dim3 grid(dims->max_context / 64, dims->kv_heads * 2);
     hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims, cs);
+                       v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
   } else {
     const dim3 grid(dims->max_context / 128, dims->kv_heads * 4);
     hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims, cs);
+                       v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
   }
   return eg::check_launch(ctx, op);
 }
@@ -439,12 +441,13 @@ int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, 
 // (a greedy step reduces the LM head's argmax partials - the same (value, index) order as the
 // argmax finalize: larger value, then lower index; a prompt-fill step takes the next prompt id;
 // a sampled step's sampler has already written it), the position advanced, the token appended
-// to the sampler's history (Session pushes every produced token, session.ts:437-445) and, for a
-// greedy step, the draw state advanced (Session draws once per decodeStep whatever the
-// temperature, session.ts:351); then the next step's input - the new token's embedding row,
-// dequantized - and the RoPE cos/sin of the next position, which every attention launch of that
-// step reads instead of computing. Without `advance` (a reset) the token and position already in
-// device memory are used as they are.
+// to the sampler's history (Session pushes every produced token, session.ts:437-445) and the
+// draw state advanced (Session draws once per decodeStep whatever the temperature,
+// session.ts:351; a sampled step's sampler took the draw without advancing the state); then the
+// next step's input - the new token's embedding row, dequantized - and the RoPE cos/sin of the
+// next position, which every attention launch of that step reads instead of computing. Without
+// `advance` (a reset) the token and position already in device memory are used as they are. A
+// sampled step whose sampler gave up is counted in t.status and changes nothing else.
 //
 // The launch is a chain of two memory round trips, each issued all at once: (1) every partial
 // (up to kTailPartials per thread), the position and the small state; (2) once the token is known,
@@ -455,7 +458,9 @@ constexpr uint32_t kTailPartials = 8;  // per thread: 2048 partials, the LM head
 __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uint32_t* token, uint32_t* position,
                                                              const uint32_t* packed, const float* scales,
                                                              const uint32_t* zeros, eg_embedding_dims d, int encoding,
-                                                             int bits, float* emb, double2* rope, float theta) {
+                                                             int bits, float* emb, double2* rope, float theta,
+                                                             uint64_t* stamp_slot) {
+  const egd::WaveStamp stamp(stamp_slot);
   constexpr int D = 64;
   const uint32_t tid = threadIdx.x;
   __shared__ uint32_t next_token, next_pos;
@@ -504,7 +509,13 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
     }
   }
   if (tid == 0) {
-    if (t.advance) {
+    // a sampled step whose sampler gave up has no token (0xFFFFFFFF): counted, and nothing moves
+    const bool failed = t.advance && !t.partials && !t.token_src && tok0 - d.row_begin >= d.row_count;
+    if (failed) {
+      if (t.status) *t.status += 1u;
+      next_token = tok0;  // outside the table: the embedding row below is left as it is
+      next_pos = pos0;
+    } else if (t.advance) {
       const uint32_t id = t.partials ? greedy_id : t.token_src ? src : tok0;
       if (t.token_src) token[0] = id;
       next_pos = pos0 + 1;
@@ -516,7 +527,9 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
       if (t.rng) (void)egd::mulberry32_next(t.rng);
       next_token = id;
     } else {
-      next_token = tok0;
+      // a reset; with token_src its id becomes the input
+      next_token = t.token_src ? src : tok0;
+      if (t.token_src) token[0] = next_token;
       next_pos = pos0;
     }
   }
@@ -603,7 +616,7 @@ int eg::launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, ui
     return eg::fail(ctx, EG_ERR_RANGE, "step_tail: %u argmax partials, at most %u", t.groups, kTailPartials * kThreads);
   hipLaunchKernelGGL(step_tail_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, t, token, position, packed, scales,
                      encoding == EG_ENC_SIGNED ? nullptr : zeros, *ed, encoding, bits, emb,
-                     reinterpret_cast<double2*>(rope), theta);
+                     reinterpret_cast<double2*>(rope), theta, eg::stamp_slot(ctx));
   return eg::check_launch(ctx, "step_tail");
 }
 

@@ -19,6 +19,7 @@
 // parameters, its history and the mulberry32 draw state) lives in device memory, so one captured
 // hipGraph replays every step with no host work per launch.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <type_traits>
 #include <vector>
@@ -40,7 +41,9 @@ struct eg_decoder {
   float* emb = nullptr;              // [hidden]: the current token's embedding, layer 0's input
   double* rope = nullptr;            // [head_dim / 2] (cos, sin) at the current position
   double* rope_table = nullptr;      // [max_context][head_dim / 2] (cos, sin), computed once
-  uint32_t* token = nullptr;         // [2]: next input id, its logit bits
+  // [4]: next input id, its logit bits (greedy), sampled steps whose sampler gave up (counted by
+  // the step tail until the host reads and clears it), unused
+  uint32_t* token = nullptr;
   uint32_t* position = nullptr;      // [1]
   // the sample step's state (DecodeGraph.history / setPosition's uniform, graph_decode.ts:150,
   // 398-406; Session's random source, session.ts:75-83)
@@ -78,7 +81,7 @@ struct eg_decoder {
   eg_graph* graph = nullptr;
   std::vector<void*> allocations;
   uint32_t host_position = 0;  // mirrors position[0]: steps are refused once the cache is full
-  uint32_t* host_token = nullptr;  // pinned: the per-token readback lands here (no staging copy)
+  uint32_t* host_token = nullptr;  // pinned [3]: the per-token readback lands here (no staging copy)
 };
 
 namespace {
@@ -217,8 +220,12 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
                                      m.embed_bits, &groups);
   }
   if (st != EG_OK) return st;
-  if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, rng)) != EG_OK)
+  // the sampler takes the draw, the tail advances the state once the step has its token; a
+  // sampler that gives up leaves 0xFFFFFFFF, which the tail counts in token[2], changing nothing
+  if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, rng, nullptr)) != EG_OK)
     return st;
+  t.rng = rng;
+  t.status = d->token + 2;
   return tail(d, t);
 }
 
@@ -310,13 +317,28 @@ int write_ids(eg_decoder* d, uint32_t* dst, const uint32_t* host, uint32_t count
   return err == hipSuccess ? EG_OK : eg::hip_fail(d->ctx, err, "decoder: upload");
 }
 
-// One 4-byte readback of the token the last step produced, into pinned memory (a direct copy,
-// no staging through a bounce buffer as a pageable destination would need).
-int read_token(eg_decoder* d, uint32_t* token_out) {
-  hipError_t err = hipMemcpyAsync(d->host_token, d->token, sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);
+// The one readback per step: the token the last step produced and the count of sampled steps
+// whose sampler gave up (token[0..2], one copy into pinned memory: no staging through a bounce
+// buffer as a pageable destination would need). A nonzero count is an error: it is cleared, the
+// host's position mirror steps back by it (those steps moved nothing on the device) and the
+// caller's next step redoes the step.
+int read_token(eg_decoder* d, uint32_t* token_out, const char* op) {
+  hipError_t err = hipMemcpyAsync(d->host_token, d->token, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, d->ctx->stream);
   if (err == hipSuccess) err = hipStreamSynchronize(d->ctx->stream);
-  if (err != hipSuccess) return eg::hip_fail(d->ctx, err, "decoder_step");
-  *token_out = *d->host_token;
+  if (err != hipSuccess) return eg::hip_fail(d->ctx, err, op);
+  const uint32_t failed = d->host_token[2];
+  if (failed != 0) {
+    d->host_position -= std::min(failed, d->host_position);
+    const uint32_t zero = 0;
+    int st = write_ids(d, d->token + 2, &zero, 1);
+    if (st != EG_OK) return st;
+    return eg::fail(d->ctx, EG_ERR_DEVICE,
+                    "%s: the sampler gave up on %u step(s) (a grid barrier timed out: not every workgroup was "
+                    "resident at once); the position, history and draw state are as before those steps, and the "
+                    "next step redoes the step",
+                    op, failed);
+  }
+  *token_out = d->host_token[0];
   return EG_OK;
 }
 
@@ -411,7 +433,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take((size_t)2 * m.intermediate * 4, &d->gu);
   take((size_t)m.kv_heads * chunks * (m.heads / std::max(1u, m.kv_heads)) * (m.head_dim + 2) * 4 + 4, &d->partials);
   take((size_t)m.vocab * 4, &d->logits);
-  take(8, &d->token);
+  take(16, &d->token);
   take(4, &d->position);
   take((size_t)m.max_context * 4, &d->history);
   d->chunk_capacity = d->chunk = std::min<uint32_t>(kMaxChunk, m.max_context);
@@ -481,7 +503,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
   }
   if (st == EG_OK) {
-    hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), sizeof(uint32_t), hipHostMallocDefault);
+    hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), 4 * sizeof(uint32_t), hipHostMallocDefault);
     if (err != hipSuccess) d->host_token = nullptr;
     if (err == hipSuccess) {
       err = hipHostMalloc(reinterpret_cast<void**>(&d->host_staging), (size_t)m.max_context * 4, hipHostMallocDefault);
@@ -541,7 +563,7 @@ int eg_decoder_reset(eg_decoder* d, uint32_t position, uint32_t token) {
                     d->desc.max_context);
   if (token >= d->desc.vocab)
     return eg::fail(d->ctx, EG_ERR_INVALID, "decoder_reset: token %u outside the vocabulary", token);
-  const uint32_t tok[2] = {token, 0};
+  const uint32_t tok[3] = {token, 0, 0};  // clears the count of failed steps
   int st = eg_buf_write(d->ctx, d->token, 0, tok, sizeof(tok));
   if (st == EG_OK) st = eg_buf_write(d->ctx, d->position, 0, &position, 4);
   if (st == EG_OK) st = tail(d, eg::StepTail{});  // this token's embedding, this position's RoPE table
@@ -560,7 +582,7 @@ int eg_decoder_step(eg_decoder* d, uint32_t* token_out) {
     return eg::fail(d->ctx, EG_ERR_RANGE, "decoder_step: context of %u positions exhausted", d->desc.max_context);
   int st = d->graph ? eg_graph_launch(d->ctx, d->graph) : run_step(d, sampled_mode(d->sampling));
   if (st == EG_OK) d->host_position++;
-  if (st == EG_OK && token_out) st = read_token(d, token_out);
+  if (st == EG_OK && token_out) st = read_token(d, token_out, "decoder_step");
   return st;
 }
 
@@ -574,8 +596,11 @@ int eg_decoder_set_sampling(eg_decoder* d, const eg_sampling_params* params) {
   if (!d || !params) return eg::fail(d ? d->ctx : nullptr, EG_ERR_INVALID, "%s: NULL argument", op);
   if (d->ctx->capturing) return eg::fail(d->ctx, EG_ERR_STATE, "%s: a graph capture is in progress", op);
   const eg_sampling_params& p = *params;
-  if (!(p.temperature == p.temperature) || !(p.top_p > 0.f && p.top_p <= 1.f) || !(p.repetition_penalty > 0.f))
-    return eg::fail(d->ctx, EG_ERR_INVALID, "%s: temperature %g, topP %g (0, 1], repetitionPenalty %g (> 0)", op,
+  // DecodeGraph.setSampling (graph_decode.ts:387) takes any values and the sampler handles every
+  // finite one as the reference's kernel does (topP <= 0 keeps the argmax fallback, topP >= 1
+  // keeps every id); only values no f32 uniform can carry meaningfully are refused
+  if (!std::isfinite(p.temperature) || !std::isfinite(p.top_p) || !std::isfinite(p.repetition_penalty))
+    return eg::fail(d->ctx, EG_ERR_INVALID, "%s: temperature %g, topP %g and repetitionPenalty %g must be finite", op,
                     (double)p.temperature, (double)p.top_p, (double)p.repetition_penalty);
   const float vals[3] = {p.temperature, p.top_p, p.repetition_penalty};
   uint32_t words[3];
@@ -660,11 +685,20 @@ int eg_decoder_prefill(eg_decoder* d, uint32_t position, const uint32_t* host_id
   // the last position's token: the head on the last row, then the tail advances the position
   // past the prompt (sampleFromPrefill, session.ts:472-495: the decode graph's sample step)
   const uint32_t last = position + count - 1;
+  const bool sampled = sampled_mode(d->sampling);
   if (st == EG_OK) st = write_ids(d, d->position, &last, 1);
-  if (st == EG_OK) st = run_head(d, sampled_mode(d->sampling), d->ph[0] + (size_t)(last_rows - 1) * d->desc.hidden);
+  if (st == EG_OK && sampled) {
+    // The last prompt id and position as the decode step's input (its embedding row and RoPE
+    // row): should the sampler give up, nothing advances and the next eg_decoder_step redoes
+    // that position as a decode step and samples.
+    eg::StepTail input;
+    input.token_src = d->history + (count - 1);
+    st = tail(d, input);
+  }
+  if (st == EG_OK) st = run_head(d, sampled, d->ph[0] + (size_t)(last_rows - 1) * d->desc.hidden);
   if (st != EG_OK) return st;
   d->host_position = position + count;
-  return token_out ? read_token(d, token_out) : EG_OK;
+  return token_out ? read_token(d, token_out, op) : EG_OK;
 }
 
 }  // extern "C"

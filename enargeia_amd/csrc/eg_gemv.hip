@@ -91,33 +91,50 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
   X(64, 1, 4, 3) X(64, 2, 1, 2) X(64, 2, 2, 2) X(64, 3, 1, 2) X(64, 3, 1, 3) X(64, 3, 1, 4) X(64, 3, 2, 2) \
   X(64, 4, 1, 2)
 
+// Shapes instantiated with their last chunk slot's x in LDS (XL = 1; int4 rows of 3-4 slots).
+#define EG_XL_SHAPES(X) X(64, 3, 1, 2) X(64, 3, 1, 3) X(64, 3, 1, 4) X(64, 4, 1, 2)
+
 template <int BITS, int ENC, int MODE>
-KernelFn pick(int team, int cpl, int u, int nb) {
+KernelFn pick(int team, int cpl, int u, int nb, int xl) {
+  if (xl == 0) {
 #define EG_CASE(T, P, UU, D) \
   if (team == T && cpl == P && u == UU && nb == D) return gemv_kernel<BITS, ENC, T, P, UU, D, MODE, EG_INPUT_VECTOR>;
-  EG_SHAPES(EG_CASE)
+    EG_SHAPES(EG_CASE)
 #undef EG_CASE
+  } else if constexpr (BITS == 4) {
+    if (xl == 1) {
+#define EG_XL_CASE(T, P, UU, D)                            \
+  if (team == T && cpl == P && u == UU && nb == D) \
+    return gemv_kernel<BITS, ENC, T, P, UU, D, MODE, EG_INPUT_VECTOR, 1>;
+      EG_XL_SHAPES(EG_XL_CASE)
+#undef EG_XL_CASE
+    }
+  }
   return nullptr;
 }
 
 template <int BITS, int ENC>
-KernelFn pick_mode(int mode, int team, int cpl, int u, int nb) {
-  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb);
-  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb);
-  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb);
-  return pick<BITS, ENC, kPlain>(team, cpl, u, nb);
+KernelFn pick_mode(int mode, int team, int cpl, int u, int nb, int xl) {
+  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb, xl);
+  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb, xl);
+  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb, xl);
+  return pick<BITS, ENC, kPlain>(team, cpl, u, nb, xl);
 }
 
-KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u, int nb, int in_kind = EG_INPUT_VECTOR) {
+// The kernel of a (format, mode, shape); xl (x slots read from LDS) applies to x given as a
+// vector only - a fused input stage takes the register form.
+KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u, int nb, int in_kind = EG_INPUT_VECTOR,
+                     int xl = 0) {
   if (in_kind != EG_INPUT_VECTOR) return pick_fused(bits, enc, mode, in_kind, team, cpl, u, nb);
-  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
-  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
-  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
-  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb, xl);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u, nb, xl);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb, xl);
+  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u, nb, xl);
 }
 
 struct Shape {
   int team = 0, cpl = 0, u = 0, nb = 2;
+  int xl = 0;  // chunk slots whose x is read from LDS per tile
   uint32_t tiles = 0;
 };
 
@@ -166,6 +183,7 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
     sh.cpl = ctx->gemv_override[1];
     sh.u = ctx->gemv_override[2];
     sh.nb = ctx->gemv_override[3];
+    sh.xl = ctx->gemv_override[4];
     if ((uint32_t)(sh.team * sh.cpl) < chunks) return Shape{};
   }
   const uint32_t rpw = 64u / sh.team;
@@ -304,7 +322,7 @@ int launch(eg_context* ctx, const QuantView& v) {
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   const int in_kind = v.input ? v.input->kind : EG_INPUT_VECTOR;
   KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u,
-                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind)
+                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind, shape.xl)
                            : nullptr;
   if (fused && !fn)
     return eg::fail(ctx, EG_ERR_INVALID,
@@ -333,6 +351,7 @@ int launch(eg_context* ctx, const QuantView& v) {
     const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
     if ((st = partials_fit(grid)) != EG_OK) return st;
+    a.stamp = eg::stamp_slot(ctx);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   } else {
     uint64_t blocks = (v.n + kWaves - 1) / kWaves;
@@ -480,7 +499,7 @@ struct eg_gemv_plan {
   uint32_t count = 0;
   uint32_t swiglu_rows = 0;  // a SwiGLU pair (eg_gemv_swiglu_plan_create): the rows of each matrix
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
-  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
+  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2, xl = 0;
 };
 
 extern "C" {
@@ -564,7 +583,9 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->cpl = shape.cpl;
   plan->u = shape.u;
   plan->nb = shape.nb;
-  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb);
+  plan->xl = shape.xl;
+  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb, EG_INPUT_VECTOR,
+                            shape.xl);
   plan->smem = k * 4u;
   plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
   delete[] host;
@@ -635,13 +656,14 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
     return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: a SwiGLU pair takes the RMSNORM input stage");
   a.n = plan->swiglu_rows;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, pair ? kSwiGLU : kBatched, plan->team, plan->cpl, plan->u,
-                            a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb, a.in_kind);
+                            a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb, a.in_kind, plan->xl);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
                             ? grid_for(ctx, fn, plan->total_passes, plan->smem + extra, ctx->fused_tiles_per_wave)
                             : plan->grid;
   const uint32_t smem = plan->smem + extra;
+  a.stamp = eg::stamp_slot(ctx);
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }

@@ -87,6 +87,7 @@ struct GemvArgs {
   const float* x2;         // norm weight / up
   float eps;
   uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
+  uint64_t* stamp;         // launch stamps (egd::WaveStamp), nullable
 };
 
 template <int BITS>
@@ -131,6 +132,38 @@ struct Codes<4> {
     }
     return a0 + a1;
   }
+  // The same sum with x read from LDS (chunk-transposed: piece e of the chunk at xp[e * stride],
+  // unscaled) instead of registers: the high nibbles are shifted down (one more op per word) in
+  // place of x's pre-division by 16, so every product and sum is the one dot() forms - the
+  // products 16c * (x / 16) and c * x are the same exact value inside each fused multiply-add.
+  template <int ENC>
+  static __device__ __forceinline__ float dot_lds(const uint4& q, const egd::u32x4* xp, uint32_t stride) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const egd::u32x4 p0 = xp[(size_t)(2 * i) * stride], p1 = xp[(size_t)(2 * i + 1) * stride];
+      const float xv[8] = {__uint_as_float(p0.x), __uint_as_float(p0.y), __uint_as_float(p0.z), __uint_as_float(p0.w),
+                           __uint_as_float(p1.x), __uint_as_float(p1.y), __uint_as_float(p1.z), __uint_as_float(p1.w)};
+      uint32_t lo, hi;
+      if (ENC == EG_ENC_SIGNED) {
+        lo = (d[i] & 0x0F0F0F0Fu) ^ 0x08080808u;
+        hi = ((d[i] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+      } else {
+        lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
+        hi = egd::and_opaque(d[i] >> 4, 0x0F0F0F0Fu);
+      }
+      a0 = fmaf(egd::ub0(lo), xv[0], a0);
+      a1 = fmaf(egd::ub0(hi), xv[1], a1);
+      a0 = fmaf(egd::ub1(lo), xv[2], a0);
+      a1 = fmaf(egd::ub1(hi), xv[3], a1);
+      a0 = fmaf(egd::ub2(lo), xv[4], a0);
+      a1 = fmaf(egd::ub2(hi), xv[5], a1);
+      a0 = fmaf(egd::ub3(lo), xv[6], a0);
+      a1 = fmaf(egd::ub3(hi), xv[7], a1);
+    }
+    return a0 + a1;
+  }
 };
 
 template <>
@@ -138,6 +171,20 @@ struct Codes<8> {
   static constexpr int kPerChunk = 16;
   static constexpr int kZeroPerWord = 4;
   static __device__ __forceinline__ float x_scale(int) { return 1.0f; }
+  // dot() with x read from LDS (piece e of the chunk at xp[e * stride])
+  template <int ENC>
+  static __device__ __forceinline__ float dot_lds(const uint4& q, const egd::u32x4* xp, uint32_t stride) {
+    float x[16];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const egd::u32x4 p = xp[(size_t)e * stride];
+      x[4 * e] = __uint_as_float(p.x);
+      x[4 * e + 1] = __uint_as_float(p.y);
+      x[4 * e + 2] = __uint_as_float(p.z);
+      x[4 * e + 3] = __uint_as_float(p.w);
+    }
+    return dot<ENC>(q, x);
+  }
   template <int ENC>
   static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[16]) {
     uint32_t d[4] = {q.x, q.y, q.z, q.w};
@@ -395,8 +442,20 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
 //     its last tile (an L2 hit) instead of branching around the spare buffers;
 //   * stores are unconditional - the team total is in every lane of the team, every lane
 //     stores it, and a clamped or repeated row stores the value that row already has.
-template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+//
+// XL > 0 (int4 full-wave teams): the last XL chunk slots keep x in LDS, read per tile, instead of
+// registers. A slot's x costs 32 VGPRs a lane; long rows (K = 4864: three slots) hold fewer waves
+// per SIMD for it, and in their last slot most lanes compute on padding. Reading that slot's x
+// from the workgroup's LDS copy each tile (8 conflict-free 16-byte reads per lane; a lane whose
+// slot lies past the row reads chunk 0 and its product is dropped) frees its registers for a
+// fourth wave per SIMD.
+template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN, int XL = 0>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 : 1, 8))) void gemv_kernel(
+    GemvArgs a) {
+  const egd::WaveStamp stamp(a.stamp);
+  static_assert(XL >= 0 && XL < CPL && (XL == 0 || (BITS == 4 && TEAM == 64 && IN == EG_INPUT_VECTOR)),
+                "x slots from LDS: int4 full-wave teams with x given as a vector");
+  constexpr int CR = CPL - XL;  // chunk slots whose x is held in registers
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
@@ -576,26 +635,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
   // This lane's activations: chunk slot j covers x[cj*EPC, cj*EPC + EPC), zero past the row
   // (filled from LDS once the input stage has written x there).
-  float xr[CPL][EPC];
+  float xr[CR][EPC];
   float sx[CPL];
+  bool xvalid[CPL];  // the slot covers a chunk of the row (XL slots: the others' products are dropped)
   auto load_x = [&]() {
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
       const bool valid = t + j * TEAM < a.chunks;
+      xvalid[j] = valid;
       sx[j] = 0.f;
       const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + cj[j];  // piece e at e * chunks
+      float xv[EPC];
 #pragma unroll
       for (int e = 0; e < EPC / 4; e++) {
         const egd::u32x4 v = xs[(size_t)e * a.chunks];
-        xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
-        xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
-        xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
-        xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
+        xv[4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
+        xv[4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
+        xv[4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
+        xv[4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
       }
 #pragma unroll
-      for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
+      for (int e = 0; e < EPC; e++) sx[j] += xv[e];
+      if (j < CR) {
 #pragma unroll
-      for (int e = 0; e < EPC; e++) xr[j][e] *= C::x_scale(e);
+        for (int e = 0; e < EPC; e++) xr[j < CR ? j : 0][e] = xv[e] * C::x_scale(e);
+      }
     }
   };
 
@@ -620,7 +684,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         } else {
           z = (float)(1 << (BITS - 1));
         }
-        acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j]) - z * sx[j], acc);
+        if (j < CR) {
+          acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j < CR ? j : 0]) - z * sx[j], acc);
+        } else {
+          // x from LDS; a slot past the row reads chunk 0's codes and x, whose product is dropped
+          const float dsum = C::template dot_lds<ENC>(q, reinterpret_cast<const egd::u32x4*>(smem) + cj[j], a.chunks);
+          acc = fmaf(xvalid[j] ? L.s[u][j] : 0.f, dsum - z * sx[j], acc);
+        }
       }
       const float v = egd::team_allsum<TEAM>(acc);
       if (kPair) {

@@ -26,21 +26,28 @@ struct eg_context {
   // This device's copy of the fixed scratch array of eg_lm_head_argmax_noalloc (resolved by
   // eg::noalloc_scratch_init at creation; shared by every context on the device).
   void* noalloc_scratch = nullptr;
-  // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth) from
-  // EG_GEMV_SHAPE="t,c,u[,d]", read once at creation; zeros mean the built-in choice. For
-  // tuning sweeps.
-  int gemv_override[4] = {0, 0, 0, 0};
+  // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth, chunk slots with
+  // x in LDS) from EG_GEMV_SHAPE="t,c,u[,d[,xl]]", read once at creation; zeros mean the
+  // built-in choice. For tuning sweeps.
+  int gemv_override[5] = {0, 0, 0, 0, 0};
   // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 1: every
   // workgroup recomputes the stage, but the decoder's launches measured faster with more,
   // shorter-lived workgroups than with two tiles per wave).
   uint32_t fused_tiles_per_wave = 1;
-  // The sampler's bounded waits: polls before a wait gives up (eg_test_sample_spin; off: about a
-  // second's worth), so tests can force the give-up path from the host.
-  bool sample_spin_override = false;
-  uint32_t sample_spin_polls = 0;
+  // eg_sample has run on this context: synchronising calls then check the count of its launches
+  // that gave up (eg::report_sample_failures).
+  bool sample_used = false;
+  // Launch stamps (eg_test_launch_stamps): the device buffer the next decode-step launches write
+  // their per-wave wall-clock stamps to, its slots, and the next free slot.
+  uint64_t* stamps = nullptr;
+  uint32_t stamp_capacity = 0;
+  uint32_t stamp_next = 0;
   // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
   // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
   int prefill_groups = 0;
+  // Register stages of the prefill GEMM's staging pipeline, for tuning sweeps of the plain
+  // launch (EG_PREFILL_STAGES; 0 = the group count's default)
+  int prefill_stages = 0;
   // chunk attention's key split: at most this many 64-key tiles per workgroup, and a small grid
   // split up to this many workgroups per CU
   // the SwiGLU pair as one launch of paired gate|up tiles (false: gate | up, then silu_mul_rows)
@@ -104,12 +111,16 @@ struct StepTail {
   bool advance = false;                 // false: a reset (token[0] and position[0] as written)
   const uint32_t* partials = nullptr;   // greedy step: the LM head's argmax partials, `groups` of them
   uint32_t groups = 0;
-  const uint32_t* token_src = nullptr;  // prompt-fill step: the next input id is *token_src
+  const uint32_t* token_src = nullptr;  // prompt-fill step or reset: the next input id is *token_src
   // (neither: a sampled step, whose sampler already wrote token[0])
   uint32_t* history = nullptr;          // the new token is appended (not by fill steps) ...
   uint32_t* history_length = nullptr;   // ... at history[*history_length]++, up to the capacity
   uint32_t history_capacity = 0;
-  uint32_t* rng = nullptr;              // mulberry32 state: advanced once (a greedy step's draw)
+  uint32_t* rng = nullptr;              // mulberry32 state: advanced once (the step's draw)
+  // A sampled step whose sampler gave up (token[0] outside the vocabulary) has no token: the tail
+  // then counts it in *status (nullable) and leaves the position, the history, the draw state
+  // and the next step's input (embedding row, RoPE row) as they were, so the next step redoes it.
+  uint32_t* status = nullptr;
   // the RoPE cos/sin of positions [0, rope_positions) (launch_rope_table); the next position's
   // row is copied from here (computed in the launch where it is NULL or the position is past it)
   const double2* rope_table = nullptr;
@@ -131,13 +142,21 @@ int launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32
                      const float* scales, const uint32_t* zeros, const eg_embedding_dims* ed, int encoding, int bits,
                      float* emb, double* rope, uint32_t head_dim, float theta);
 
-// eg_sample's launches with every parameter read from DEVICE memory `params` (the 32-byte
-// sample dims: vocab, history_length, temperature, top_p, repetition_penalty, random), all
-// passes launched whatever the values, so a captured graph replays with new values. With `rng`
-// the launch first draws params->random from the mulberry32 state there (advancing it).
-// `vocab` sizes the grid and must equal params->vocab.
+// eg_sample's launch with every parameter read from DEVICE memory `params` (the 32-byte
+// sample dims: vocab, history_length, temperature, top_p, repetition_penalty, random), so a
+// captured graph replays with new values. With `rng` the launch first takes params->random as
+// the mulberry32 draw from the state there, WITHOUT advancing it (the caller advances it once
+// the step has its token). `vocab` sizes the grid and must equal params->vocab. A launch whose
+// bounded waits give up leaves out[0] = 0xFFFFFFFF and adds 1 to *status (status nullable: a
+// caller that counts from out[0] itself).
 int launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
-                         eg_sample_dims* params, uint32_t* rng);
+                         eg_sample_dims* params, uint32_t* rng, uint32_t* status);
+
+// Reports, once, the standalone sampler launches that gave up since the last report: when the
+// context has run eg_sample, reads (after the stream has drained) and clears the count the
+// sampler keeps in the context's state, and fails with EG_ERR_DEVICE when it is not zero.
+// eg_sync and eg_buf_read call it; `op` names the caller in the message.
+int report_sample_failures(eg_context* ctx, const char* op);
 
 // eg_attention_decode with the RoPE cos/sin of the current position read from `rope` ([head_dim
 // / 2] pairs of doubles, as egd::rope_table computes them) instead of computed in the launch.
@@ -229,6 +248,14 @@ int occupancy_of(eg_context* ctx, const void* kernel, uint32_t smem_bytes = 0);
 // Validates a launch once the kernel is enqueued (hipGetLastError catches bad configurations
 // immediately; faults surface at the next synchronisation).
 int check_launch(eg_context* ctx, const char* op);
+
+// Launch stamps: each launch that takes a slot writes (entry, exit) wall-clock stamps of up to
+// kStampWaves waves there (egd::WaveStamp); NULL when the context records none.
+constexpr uint32_t kStampWaves = 8192;
+inline uint64_t* stamp_slot(eg_context* ctx) {
+  if (!ctx->stamps || ctx->stamp_next >= ctx->stamp_capacity) return nullptr;
+  return ctx->stamps + 2ull * kStampWaves * ctx->stamp_next++;
+}
 
 }  // namespace eg
 
@@ -450,6 +477,26 @@ __device__ __forceinline__ float attention_combine_at(const float* partials, uin
   return acc;
 }
 
+// A launch's per-wave wall-clock stamps (eg::stamp_slot): lane 0 of each wave stores the wave's
+// entry time (s_memrealtime, 100 MHz) at construction and its exit time when the kernel's scope
+// ends, wave w of the launch at base[2 w], base[2 w + 1]. Nothing without a slot.
+struct WaveStamp {
+  uint64_t* p = nullptr;
+  __device__ __forceinline__ explicit WaveStamp(uint64_t* base) {
+    if (base != nullptr && (threadIdx.x & 63u) == 0) {
+      const uint32_t block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+      const uint32_t w = block * (blockDim.x / 64u) + threadIdx.x / 64u;
+      if (w < eg::kStampWaves) {
+        p = base + 2u * w;
+        p[0] = wall_clock64();
+      }
+    }
+  }
+  __device__ __forceinline__ ~WaveStamp() {
+    if (p != nullptr) p[1] = wall_clock64();
+  }
+};
+
 // (value, index) ordering used by every argmax here: larger value wins, ties go to the lower
 // index (argmax.wgsl:53-57, sample.wgsl:181-186).
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
@@ -469,15 +516,20 @@ __device__ __forceinline__ void team_argmax(float& v, uint32_t& i) {
   }
 }
 
-// mulberry32 (session.ts:75-83): advances the state and returns the next draw as the f32 the
-// reference's uniform carries (u / 2^32 rounded to f32; rounding u to 24 bits then scaling by
-// the power of two 2^-32 rounds identically).
-__device__ __forceinline__ float mulberry32_next(uint32_t* state) {
-  const uint32_t s = *state + 0x6D2B79F5u;
-  *state = s;
+// mulberry32 (session.ts:75-83): the next draw from `state` as the f32 the reference's uniform
+// carries (u / 2^32 rounded to f32; rounding u to 24 bits then scaling by the power of two 2^-32
+// rounds identically), without advancing the state ...
+__device__ __forceinline__ float mulberry32_peek(uint32_t state) {
+  const uint32_t s = state + 0x6D2B79F5u;
   uint32_t t = (s ^ (s >> 15)) * (1u | s);
   t = (t + (t ^ (t >> 7)) * (61u | t)) ^ t;
   return (float)(t ^ (t >> 14)) * 0x1p-32f;
+}
+// ... and advancing it.
+__device__ __forceinline__ float mulberry32_next(uint32_t* state) {
+  const float r = mulberry32_peek(*state);
+  *state += 0x6D2B79F5u;
+  return r;
 }
 
 // binary16 <-> f32 (round to nearest even), the KV cache's element type.

@@ -41,7 +41,11 @@
 // from the reference's f32 tree sums only by rounding, which can change a decision only when
 // a mass is within ~1e-7 of topP or the target within ~1e-7 of a cumulative boundary.
 // A barrier that times out (a workgroup that never became resident) raises an abort flag that
-// every wait also reads; every workgroup then leaves and the result is 0xFFFFFFFF.
+// every wait also reads; every workgroup then leaves, and the last to leave sets the result to
+// 0xFFFFFFFF (also stored before the first barrier, the result of every path that never reaches
+// the final store) and adds 1 to the launch's status word, which the host reads as an error.
+#include <algorithm>
+
 #include "eg_internal.hpp"
 
 namespace {
@@ -165,7 +169,10 @@ struct GridSync {
   uint32_t* gen;    // advanced once per completed barrier
   uint32_t* abort;  // set by a timed-out wait
   uint32_t* exits;  // workgroups done with every barrier of the current launch
-  uint32_t spin;    // polls before a wait gives up (kSpin; the context's test hook may lower it)
+  uint32_t* status; // +1 per launch that gave up (nullable: the caller counts from out[0])
+  // polls before a wait gives up: kSpin while this word is 0, else its value - 1 (the context's
+  // test hook sets it; read at every barrier, so a captured graph follows it too)
+  const uint32_t* spin;
 };
 
 __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
@@ -182,9 +189,11 @@ __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
       drain();
       put(g.gen, gen0 + 1u);
     } else {
+      const uint32_t w = get(g.spin);
+      const uint32_t spin = w ? w - 1u : kSpin;
       uint32_t n = 0;
       while (get(g.gen) == gen0) {
-        if (get(g.abort) != 0u || ++n > g.spin) {
+        if (get(g.abort) != 0u || ++n > spin) {
           good = false;
           break;
         }
@@ -201,15 +210,23 @@ __device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
   return ok != 0u;
 }
 
-// Called by every workgroup once it has passed its last barrier or given up: the last to leave
-// returns the words to their starting state, so the next launch needs no reset launch before it
-// and never starts from a count or an abort flag left by an aborted one (the context's state
-// starts zeroed; a workgroup that raised the abort flag drained that store before counting its
-// exit).
-__device__ void leave(const GridSync& g, uint32_t groups) {
+// Called by every workgroup once it has passed its last barrier or given up. The last to leave
+// settles an aborted launch - out[0] = 0xFFFFFFFF, after every workgroup's own store to it (a
+// workgroup can time out at the last barrier after a late arrival has released the others, one
+// of which may still store a token), and +1 in the status word - then returns the words to their
+// starting state, so the next launch needs no reset launch before it and never starts from a
+// count or an abort flag left by an aborted one (the context's state starts zeroed). Thread 0
+// makes every store to out[0]; it drains them, as a workgroup that raised the abort flag drained
+// that store, before counting its exit.
+__device__ void leave(const GridSync& g, uint32_t groups, uint32_t* out) {
   if (threadIdx.x == 0) {
+    drain();
     const uint32_t left = __hip_atomic_fetch_add(g.exits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (left == groups - 1) {
+      if (get(g.abort) != 0u) {
+        put(out, 0xFFFFFFFFu);
+        if (g.status) __hip_atomic_fetch_add(g.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       put(g.count, 0u);
       put(g.abort, 0u);
       put(g.exits, 0u);
@@ -225,9 +242,16 @@ __device__ void leave(const GridSync& g, uint32_t groups) {
 __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* history, uint32_t* out, SampleParams hp,
                                               SampleParams* dp, const Work& w, const GridSync& gs, uint32_t* rng) {
   const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
-  // This call's draw (one per sampled step, Session.decodeStep session.ts:351): taken by
-  // workgroup 0 before the first barrier, read by everyone after it.
-  if (rng && dp && g == 0 && tid == 0) put(&dp->random, egd::mulberry32_next(rng));
+  if (g == 0 && tid == 0) {
+    // The give-up result, replaced by the token once one is found. Both are stored coherently
+    // (out[0] is written by two workgroups, possibly on different XCDs), and this one completes
+    // before the first barrier counts workgroup 0, so it always precedes the token.
+    put(out, 0xFFFFFFFFu);
+    // This call's draw (one per sampled step, Session.decodeStep session.ts:351) from the
+    // mulberry32 state, which the caller advances once the step has its token: taken by
+    // workgroup 0 before the first barrier, read by everyone after it.
+    if (rng && dp) put(&dp->random, egd::mulberry32_peek(*rng));
+  }
   SampleParams p = dp ? *dp : hp;  // `random` is read again after the first barrier (below)
   const uint32_t base = g * kSlice, first = base + tid * kPerThread;
   const uint32_t end = min(base + kSlice, p.vocab);
@@ -301,10 +325,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
   // before any level adds to them
   if (g == 0)
     for (int i = tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
-  if (!grid_barrier(gs, G)) {
-    if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
-    return;
-  }
+  if (!grid_barrier(gs, G)) return;  // out[0] keeps the give-up result
   if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
   float mx;
   uint32_t amax;
@@ -325,7 +346,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
     mx = bv;
     amax = bi;
     if (greedy) {
-      if (g == 0 && tid == 0) out[0] = amax;
+      if (g == 0 && tid == 0) put(out, amax);
       return;
     }
     // the normaliser: every slice's sum rescaled from its own max to the global one
@@ -416,10 +437,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
         put(&w.above_count[g], above_n);
         put(&w.cand_count[g], cand_n);
       }
-      if (!grid_barrier(gs, G)) {
-        if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
-        return;
-      }
+      if (!grid_barrier(gs, G)) return;
       if (last) {
         // every group's figures for the kept masses below (loaded here, beside the bins)
         last_done = true;
@@ -511,10 +529,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       put(&w.kept_part[g], (uint64_t)kept);
       put(&w.count_part[g], count);
     }
-    if (!grid_barrier(gs, G)) {
-      if (g == 0 && tid == 0) out[0] = 0xFFFFFFFFu;
-      return;
-    }
+    if (!grid_barrier(gs, G)) return;
     if (tid < G) {
       gk = get(&w.kept_part[tid]);
       gc = get(&w.count_part[tid]);
@@ -541,7 +556,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
   if (tid == pick_group) group_prefix = gbefore;
   __syncthreads();
   if (pick_group == 0xFFFFFFFFu) {
-    if (g == 0 && tid == 0) out[0] = amax;
+    if (g == 0 && tid == 0) put(out, amax);
     return;
   }
   if (g != pick_group) return;
@@ -557,15 +572,21 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
     }
   }
   __syncthreads();
-  if (tid == 0) out[0] = pick != 0xFFFFFFFFu ? pick : amax;
+  if (tid == 0) put(out, pick != 0xFFFFFFFFu ? pick : amax);
 }
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const uint32_t* history, uint32_t* out,
                                                           SampleParams hp, SampleParams* dp, Work w, GridSync gs,
-                                                          uint32_t* rng) {
+                                                          uint32_t* rng, uint64_t* stamp_slot) {
+  const egd::WaveStamp stamp(stamp_slot);
   sample_phases(logits, history, out, hp, dp, w, gs, rng);
-  leave(gs, gridDim.x);
+  leave(gs, gridDim.x, out);
 }
+
+// The count of eg_sample launches that gave up, and the test hook's poll limit, in the context's
+// state (zeroed at creation).
+uint32_t* standalone_status(eg_context* ctx) { return reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048 + 512); }
+uint32_t* spin_word(eg_context* ctx) { return reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048 + 640); }
 
 Work workspace(eg_context* ctx, GridSync* gs) {
   Work w;
@@ -599,23 +620,30 @@ Work workspace(eg_context* ctx, GridSync* gs) {
   return w;
 }
 
-// One launch (all its workgroups must be resident at once: G <= kMaxGroups = 256 workgroups of
-// 256 threads and ~12 KB of LDS each fit the device).
+// One launch. All its workgroups must be resident at once (G <= kMaxGroups = 256 workgroups of
+// 256 threads and ~12 KB of LDS each fit an MI355X); a device that cannot hold them (fewer CUs,
+// a partition) is refused here rather than left to the bounded waits.
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
-           SampleParams* dp, uint32_t* rng = nullptr) {
+           SampleParams* dp, uint32_t* rng, uint32_t* status) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
+  const int per_cu = eg::occupancy_of(ctx, reinterpret_cast<const void*>(sample_kernel));
+  if (per_cu > 0 && (uint64_t)per_cu * (uint64_t)ctx->cu_count < groups)
+    return eg::fail(ctx, EG_ERR_RANGE,
+                    "sample: vocab %u needs %u workgroups resident at once; this device holds %d per CU x %d CUs",
+                    hp.vocab, groups, per_cu, ctx->cu_count);
   GridSync gs;
   Work w = workspace(ctx, &gs);
-  gs.spin = ctx->sample_spin_override ? ctx->sample_spin_polls : kSpin;
+  gs.status = status;
+  gs.spin = spin_word(ctx);
   hipLaunchKernelGGL(sample_kernel, dim3(groups), dim3(kThreads), 0, ctx->stream, logits, history, out, hp, dp, w, gs,
-                     rng);
+                     rng, eg::stamp_slot(ctx));
   return eg::check_launch(ctx, "sample");
 }
 
 }  // namespace
 
 int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
-                             eg_sample_dims* params, uint32_t* rng) {
+                             eg_sample_dims* params, uint32_t* rng, uint32_t* status) {
   static_assert(sizeof(eg_sample_dims) == sizeof(SampleParams), "the device block is the 32-byte sample dims");
   if (!logits || !out || !params) return eg::fail(ctx, EG_ERR_INVALID, "sample: NULL argument");
   if (vocab == 0 || (vocab + kSlice - 1) / kSlice > kMaxGroups)
@@ -623,14 +651,36 @@ int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* his
                     kMaxGroups * kSlice);
   SampleParams hp{};
   hp.vocab = vocab;
-  return launch(ctx, logits, history, out, hp, reinterpret_cast<SampleParams*>(params), rng);
+  return launch(ctx, logits, history, out, hp, reinterpret_cast<SampleParams*>(params), rng, status);
+}
+
+int eg::report_sample_failures(eg_context* ctx, const char* op) {
+  if (!ctx->sample_used) return EG_OK;
+  uint32_t* word = standalone_status(ctx);
+  uint32_t failed = 0;
+  hipError_t err = hipMemcpyAsync(&failed, word, 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+  if (err == hipSuccess && failed != 0) {
+    const uint32_t zero = 0;
+    err = hipMemcpyAsync(word, &zero, 4, hipMemcpyHostToDevice, ctx->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);  // `zero` is a stack local
+  }
+  if (err != hipSuccess) return eg::hip_fail(ctx, err, op);
+  if (failed != 0)
+    return eg::fail(ctx, EG_ERR_DEVICE,
+                    "%s: %u sample launch(es) gave up (a grid barrier timed out: not every workgroup was resident "
+                    "at once); their out[0] is 0xFFFFFFFF",
+                    op, failed);
+  return EG_OK;
 }
 
 extern "C" int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls) {
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "test_sample_spin: ctx is NULL");
-  ctx->sample_spin_override = override != 0;
-  ctx->sample_spin_polls = polls;
-  return EG_OK;
+  if (ctx->capturing) return eg::fail(ctx, EG_ERR_STATE, "test_sample_spin: a graph capture is in progress");
+  const uint32_t word = override ? std::min(polls, 0xFFFFFFFEu) + 1u : 0u;
+  hipError_t err = hipMemcpyAsync(spin_word(ctx), &word, 4, hipMemcpyHostToDevice, ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);  // `word` is a stack local
+  return err == hipSuccess ? EG_OK : eg::hip_fail(ctx, err, "test_sample_spin");
 }
 
 extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
@@ -645,5 +695,7 @@ extern "C" int eg_sample(eg_context* ctx, float* logits, const uint32_t* history
                     kMaxGroups * kSlice);
   SampleParams hp;
   std::memcpy(&hp, dims, sizeof(hp));
-  return launch(ctx, logits, history, out, hp, nullptr);
+  const int st = launch(ctx, logits, history, out, hp, nullptr, nullptr, standalone_status(ctx));
+  if (st == EG_OK) ctx->sample_used = true;
+  return st;
 }

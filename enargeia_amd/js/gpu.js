@@ -261,9 +261,11 @@ class BufferPool {
   }
 }
 
-/** readBuffer (readback.ts:18): all `source.size` bytes, after all submitted work. */
+/** readBuffer (readback.ts:18): all `source.size` bytes, after all submitted work. A buffer with
+ * its own `read(size)` (a decoder's result word, read with its status) is read through it. */
 async function readBuffer(ctx, pool, source) {
   const buffer = source.buffer || source;
+  if (buffer.read) return buffer.read(source.size);
   return native.bufRead(ctx.device.ctx, buffer.ptr, 0, source.size);
 }
 

@@ -115,7 +115,10 @@ EG_API int eg_abi_version(void);
  * Passing NULL to eg_set_stream restores the context's own stream. */
 EG_API int eg_get_stream(eg_context* ctx, void** out_stream);
 EG_API int eg_set_stream(eg_context* ctx, void* stream);
-/* Blocks until all work on the context's stream finished (queue.onSubmittedWorkDone). */
+/* Blocks until all work on the context's stream finished (queue.onSubmittedWorkDone). Errors
+ * raised on the device since the last blocking call surface here, as WebGPU's error scopes
+ * surface them asynchronously (helpers/gpu.ts:41-50): an eg_sample launch that gave up is
+ * EG_ERR_DEVICE ("... sample launch(es) gave up ..."), reported once. */
 EG_API int eg_sync(eg_context* ctx);
 
 /* ---- buffers (src/gpu/pool.ts:55 acquire/release; queue.writeBuffer; readback.ts:18) ----- */
@@ -124,7 +127,8 @@ EG_API int eg_buf_free(eg_context* ctx, void* ptr);
 /* Stream-ordered host->device copy (GPUQueue.writeBuffer). The host memory must stay valid
  * until the copy completed (eg_sync), as pageable copies may be deferred. */
 EG_API int eg_buf_write(eg_context* ctx, void* dst, size_t offset, const void* host_src, size_t bytes);
-/* Synchronous device->host copy after all prior work (readBuffer, readback.ts:18-38). */
+/* Synchronous device->host copy after all prior work (readBuffer, readback.ts:18-38). Reports
+ * device-side errors as eg_sync does (the data is copied either way). */
 EG_API int eg_buf_read(eg_context* ctx, const void* src, size_t offset, void* host_dst, size_t bytes);
 /* Stream-ordered zero fill by a kernel (pool.clear), safe inside graph capture. */
 EG_API int eg_buf_zero(eg_context* ctx, void* dst, size_t offset, size_t bytes);
@@ -218,18 +222,32 @@ EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const 
  * occurrence of each id in history[0..history_length), then greedy argmax (temperature <= 0)
  * or temperature / top-p (threshold bisection, 32 steps) / draw at `random` in ascending id
  * order, with the argmax fallback. out[0] = the token id. One launch whose workgroups (one per
- * 2048 ids, vocab <= 524,288) must all be resident at once; should one never start (the device shared with other
- * work), the launch's bounded waits give up and out[0] = 0xFFFFFFFF. Calls that overlap on one
- * context race (they share its workspace). */
+ * 2048 ids, vocab <= 524,288) must all be resident at once: a device that cannot hold them is
+ * EG_ERR_RANGE here; should one still never start (the device shared with other work), the
+ * launch's bounded waits give up, out[0] = 0xFFFFFFFF and the next eg_sync or eg_buf_read on the
+ * context fails with EG_ERR_DEVICE. Calls that overlap on one context race (they share its
+ * workspace). */
 EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
               const eg_sample_dims* dims);
 
 /* Test hook, no counterpart in the reference: with override != 0 every later sampler launch on
- * this context (eg_sample and the decoder's sampled steps) gives a barrier wait up after `polls`
- * polls instead of about a second, so the give-up path (out[0] = 0xFFFFFFFF, every workgroup
- * leaving, the barrier words restored for the next launch) can be forced from the host; override
- * 0 restores the default. Not for production use. */
+ * this context (eg_sample and the decoder's sampled steps, replays of captured graphs included:
+ * the limit lives in device memory) gives a barrier wait up after `polls` polls instead of about
+ * a second, so the give-up path (out[0] = 0xFFFFFFFF and an error at the
+ * next blocking call, every workgroup leaving, the barrier words restored for the next launch)
+ * can be forced from the host; override 0 restores the default. Not for production use. */
 EG_API int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls);
+
+/* Profiling hook, no counterpart in the reference (its decode loop is profiled by timestamp
+ * queries, graph_decode.ts:416-433): with `buffer` non-NULL (device memory of at least
+ * launches * 131072 bytes, zeroed by the caller), each of the next `launches` launches of a
+ * decode-step kernel on this context - GEMVs and GEMV plans (the LM head included), the decode
+ * attention, the sampler, the step tail; eager, or captured into a graph whose every replay then
+ * writes the same slots - stores per-wave wall-clock stamps (s_memrealtime, 100 MHz): wave w of
+ * launch i at buffer[2 * (8192 * i + w)] (entry) and [... + 1] (exit), for w < 8192. *recorded
+ * (nullable) receives the number of launches that took a slot since the previous call; NULL
+ * turns the stamps off. Not for production use. */
+EG_API int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t launches, uint32_t* recorded);
 
 /* ---- decode step: embedding, attention, fused GEMV inputs ----------------------------------- */
 
@@ -344,8 +362,10 @@ typedef struct eg_decoder eg_decoder;
 
 /* Device buffers a decoder owns, for callers that fill or inspect them (the KV caches are
  * [layers][max_context][kv_heads][head_dim] f16; logits f32[vocab] (penalized in place by a
- * sampled step, as the reference's sample kernel does); token u32 = the next input id, written
- * by each step; position u32; history u32[max_context] = the sampler's history (DecodeGraph's
+ * sampled step, as the reference's sample kernel does); token u32[3] = the next input id
+ * (written by each step), its logit bits (greedy steps) and the status word: the count of
+ * sampled steps whose sampler gave up, which changed nothing else (cleared by the readback that
+ * reports it and by eg_decoder_reset); position u32; history u32[max_context] = the sampler's history (DecodeGraph's
  * `history` buffer); sample_params = the sample step's 32-byte uniform, live on the device:
  * history_length is advanced by every step and `random` holds the last step's draw; rng = the
  * mulberry32 state). */
@@ -361,7 +381,8 @@ typedef struct eg_decoder_buffers {
 } eg_decoder_buffers;
 
 /* SamplingParams (sample.ts:24-31): temperature <= 0 is greedy (GREEDY = {0, 1, 1}, sample.ts:33),
- * top_p in (0, 1], repetition_penalty > 0 (1 disables it). */
+ * top_p >= 1 keeps every id, top_p <= 0 leaves the argmax fallback, repetition_penalty 1 disables
+ * the penalty. Any finite values, as the reference's setSampling takes them. */
 typedef struct eg_sampling_params {
   float temperature, top_p, repetition_penalty;
 } eg_sampling_params;
@@ -384,8 +405,12 @@ EG_API int eg_decoder_reset(eg_decoder* decoder, uint32_t position, uint32_t tok
  * the draw; sample.wgsl:143-332) with one mulberry32 draw taken on the device. Either way the
  * token is appended to the history, the draw state advances once (Session draws once per step
  * whatever the parameters) and the position advances, all on the device. token_out (host,
- * nullable) receives the new token: the one 4-byte readback per step. Replays the captured
- * graph if there is one. */
+ * nullable) receives the new token: the one readback per step (12 bytes: the token with the
+ * status word). Replays the captured graph if there is one. A sampled step whose sampler gave up
+ * (its grid barrier timed out) moves nothing - position, history, draw state and the next
+ * step's input stay as they were, so the next step redoes it - and is reported as EG_ERR_DEVICE
+ * by the readback that sees it (the one of this step or, device-chained without token_out, the
+ * next one that reads). */
 EG_API int eg_decoder_step(eg_decoder* decoder, uint32_t* token_out);
 /* Captures one step as a hipGraph; later eg_decoder_step calls replay it (no host work per
  * launch; every per-token value already lives in device memory). A change of sampling
@@ -411,7 +436,9 @@ EG_API int eg_decoder_set_history(eg_decoder* decoder, const uint32_t* host_ids,
  * 472-495): the history becomes the prompt, positions [position, position + count) receive the
  * prompt's cache rows, and the last one's logits are sampled (one draw) into the next token,
  * which is appended to the history. A prompt past the context is EG_ERR_RANGE
- * ("prompt of N exceeds the remaining context of M"). token_out as for eg_decoder_step. */
+ * ("prompt of N exceeds the remaining context of M"). token_out as for eg_decoder_step; should
+ * the sampler give up, the decoder is left at the prompt's last position with that id as its
+ * input, and the next eg_decoder_step recomputes that position and samples. */
 EG_API int eg_decoder_prefill(eg_decoder* decoder, uint32_t position, const uint32_t* host_ids, uint32_t count,
                               uint32_t* token_out);
 /* Rows per prompt chunk (Session's prefillChunk, session.ts:146): a longer prompt runs as several

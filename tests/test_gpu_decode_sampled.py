@@ -237,3 +237,97 @@ def test_session_generate_and_prompt_range(device, small_model):
     finally:
         dec.close()
         dm.release()
+
+
+def _spin(device, on):
+    lib = _lib.load()
+    _lib.check(lib.eg_test_sample_spin(device.ctx, 1 if on else 0, 0), device.ctx)
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
+def test_sampler_give_up_is_an_error_and_the_next_step_redoes_it(device, small_model, graph):
+    """A sampled step whose sampler gives up (forced from the host: every bounded wait gives up at
+    its first poll, and every kernel still exits) is EG_ERR_DEVICE at its readback and moves
+    nothing: the position, the history, the draw state and the next step's input stay as they
+    were, so the next step redoes it and produces exactly the token a decoder that never failed
+    produces. Device-chained (no readback), the failure is reported by the next readback and the
+    state is again that of a decoder that never failed."""
+    dm = DeviceModel(device, small_model)
+    dec, ref = Decoder(dm), Decoder(dm)
+    try:
+        prompt = prompt_ids(10, SMALL.vocab, 41)
+        for d in (dec, ref):
+            d.set_sampling(T, TOP_P, PENALTY)
+            d.seed(0x5EED)
+            if graph:
+                d.capture()
+        assert dec.prefill(0, prompt) == ref.prefill(0, prompt)
+        want = [ref.step() for _ in range(4)]
+        got = [dec.step()]
+        # a step that gives up, with its readback
+        pos, hist, rng = dec.position(), dec.history().tolist(), dec.rng_state()
+        _spin(device, True)
+        try:
+            with pytest.raises(_lib.EgError, match="the sampler gave up on 1 step"):
+                dec.step()
+        finally:
+            _spin(device, False)
+        assert (dec.position(), dec.history().tolist(), dec.rng_state()) == (pos, hist, rng)
+        got.append(dec.step())
+        # device-chained: the failure surfaces at the next readback, whose step succeeded
+        _spin(device, True)
+        try:
+            dec.step(read_token=False)
+        finally:
+            _spin(device, False)
+        assert (dec.position(), dec.rng_state()) == (pos + 1, ref_rng_after(0x5EED, 3))  # prefill + 2 steps
+        with pytest.raises(_lib.EgError, match="the sampler gave up on 1 step"):
+            dec.step()
+        got.append(int(dec.history()[-1]))
+        got.append(dec.step())
+        assert got == want
+        np.testing.assert_array_equal(dec.history(), ref.history())
+        np.testing.assert_array_equal(dec.logits(), ref.logits())
+        assert dec.position() == ref.position() == len(prompt) + 4
+        assert dec.rng_state() == ref.rng_state()
+    finally:
+        dec.close()
+        ref.close()
+        dm.release()
+
+
+def ref_rng_after(seed, draws):
+    return (seed + draws * 0x6D2B79F5) % 2 ** 32
+
+
+def test_prefill_give_up_leaves_the_last_prompt_position(device, small_model):
+    """A prompt whose sampled first token gives up is an error; the decoder is left at the
+    prompt's last position with the prompt as its history and no draw taken, and the next step
+    recomputes that position as a decode step and samples it with the first draw."""
+    dm = DeviceModel(device, small_model)
+    dec = Decoder(dm)
+    try:
+        prompt = prompt_ids(9, SMALL.vocab, 43)
+        dec.set_sampling(0.1, TOP_P, PENALTY)
+        dec.seed(0x5EED)
+        _spin(device, True)
+        try:
+            with pytest.raises(_lib.EgError, match="the sampler gave up on 1 step"):
+                dec.prefill(0, prompt)
+        finally:
+            _spin(device, False)
+        assert dec.position() == len(prompt) - 1
+        assert dec.history().tolist() == prompt
+        assert dec.rng_state() == 0x5EED
+        tok = dec.step()
+        assert dec.position() == len(prompt)
+        assert dec.history().tolist() == prompt + [tok]
+        assert dec.rng_state() == ref_rng_after(0x5EED, 1)
+        # the token is the sampler's on the logits of that recomputed position, with the first draw
+        r = np.float32(oracle.Mulberry32Stream(0x5EED)())
+        ref_tok, info, _ = oracle.sample(dec.logits(), np.zeros(0, np.uint32), 0.1, TOP_P, 1.0, r)
+        if info.bisect_margin > SAMPLER_EPS and info.draw_margin > SAMPLER_EPS:
+            assert tok == ref_tok
+    finally:
+        dec.close()
+        dm.release()

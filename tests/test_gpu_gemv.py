@@ -192,8 +192,8 @@ def test_lm_head_q8_config2_logits_and_fused_argmax(device):
 
 @pytest.mark.parametrize("r1,r2", [(37, 39000), (20000, 20001), (5, 38000)])
 def test_lm_head_fused_argmax_across_workgroups_and_calls(device, r1, r2):
-    # The fused argmax is reduced by the launch's last-arriving workgroup, which then resets the
-    # context's arrival counter: consecutive calls on one context each reduce every workgroup's
+    # The fused argmax leaves one (value, index) partial per workgroup, which a finalize launch
+    # reduces in a fixed order: consecutive calls on one context each reduce every workgroup's
     # partial, and two equal maxima in rows far apart (different workgroups) resolve to the lower
     # index, as the reference's argmax does (test/reference/ops.ts:237-244: the first maximum kept).
     rows, hidden = 40000, 896

@@ -195,11 +195,12 @@ def test_sampler_deterministic_and_reentrant(device, config2):
         s.close()
 
 
-def test_barrier_give_up_is_clean_and_next_call_recovers(device, config2):
+def test_barrier_give_up_is_an_error_and_next_call_recovers(device, config2):
     # The sampler's waits are bounded. Forced from the host to give up at their first poll (the
     # test hook eg_test_sample_spin), a launch must still end - every workgroup leaves - with
-    # 0xFFFFFFFF as its token, and the next launch on the same context, with the default
-    # bound, must find the barrier words restored and sample normally.
+    # 0xFFFFFFFF as its token and an EG_ERR_DEVICE at the next blocking call (eg_buf_read or
+    # eg_sync, reported once), and the next launch on the same context, with the default bound,
+    # must find the barrier words restored and sample normally.
     from enargeia_amd import _lib
 
     lib = _lib.load()
@@ -210,13 +211,56 @@ def test_barrier_give_up_is_clean_and_next_call_recovers(device, config2):
         _lib.check(lib.eg_test_sample_spin(device.ctx, 1, 0), device.ctx)
         try:
             # the first workgroups to arrive at the first barrier poll before the last arrives
-            assert s(config2, [], params, 0.37) == 0xFFFFFFFF
-            # one barrier: ends either way
-            assert s(config2, [], K.GREEDY, 0.5) in (0xFFFFFFFF, oracle.argmax(config2))
+            with pytest.raises(_lib.EgError, match="sample launch\\(es\\) gave up"):
+                s(config2, [], params, 0.37)
+            assert int(device.read_array(s.out, np.uint32, 1)[0]) == 0xFFFFFFFF  # reported once
+            # the same through eg_sync
+            s.kern.encode(s.kern.bind_group([s.logits, s.history, s.out, _uniform(s, params, 0.37)]),
+                          K.SAMPLE_WORKGROUPS)
+            with pytest.raises(_lib.EgError, match="eg_sync: 1 sample launch"):
+                device.sync()
+            device.sync()
+            # one barrier: ends either way, and either way consistently
+            try:
+                assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
+            except _lib.EgError:
+                assert int(device.read_array(s.out, np.uint32, 1)[0]) == 0xFFFFFFFF
         finally:
             _lib.check(lib.eg_test_sample_spin(device.ctx, 0, 0), device.ctx)
         for _ in range(3):
             assert s(config2, [], params, 0.37) == expect
         assert s(config2, [], K.GREEDY, 0.5) == oracle.argmax(config2)
+        device.sync()
     finally:
         s.close()
+
+
+def _uniform(s, params, random):
+    u = s.kern.uniform()
+    u.write(K.sample_dims(s.vocab, 0, params, random))
+    return u
+
+
+@pytest.mark.parametrize("top_p", [0.0, -0.5, 1.5])
+def test_top_p_outside_the_unit_interval(device, top_p):
+    # The reference's setSampling takes any topP (graph_decode.ts:387) and its kernel handles
+    # them: topP <= 0 moves every bisection step up, so nothing is kept and the draw falls back
+    # to the argmax (sample.wgsl:324-331); topP >= 1 keeps every id (threshold 0).
+    logits = oracle.normal_floats(VOCAB, 31, 3.0)
+    rng = oracle.Mulberry32Stream(31)
+    draws = [rng() for _ in range(8)]
+    params = K.SamplingParams(0.7, top_p, 1.0)
+    if top_p <= 0:
+        # every bisection step sees mass >= 0 >= topP, whatever the rounding: no decision near a
+        # boundary, and the oracle's own token is the argmax for every draw
+        s = Sampler(device, VOCAB)
+        try:
+            for r in draws:
+                ref = oracle.sample(logits, np.zeros(0, np.uint32), 0.7, top_p, 1.0, r)[0]
+                assert ref == int(np.argmax(logits))
+                assert s(logits, [], params, r) == ref
+        finally:
+            s.close()
+    else:
+        c, e = _compare(device, logits, np.zeros(0, np.uint32), params, draws, f"top-p {top_p}")
+        assert e >= 6
