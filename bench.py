@@ -576,8 +576,9 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
         result["sampled_tok_s"] = round(DECODE_STEPS / wall, 1)
         result["sampled_ms_per_token"] = round(wall / DECODE_STEPS * 1e3, 4)
         result["sampled_config"] = "T 0.7 / top-p 0.9 / penalty 1.1, history = prompt + tokens, graph"
+        result["sampled_vs_oracle"] = verify_sampled(dec, w)
         log(f"decode (graph, sampled): {result['sampled_tok_s']} tok/s with a readback per token; "
-            f"{len(set(sampled))} distinct tokens")
+            f"{len(set(sampled))} distinct tokens; vs oracle {result['sampled_vs_oracle']}")
         dec.set_sampling(0.0, 1.0, 1.0)
     result["prompt"] = prompt_throughput(dev, dec, cfg)
     step_bytes = (STEP_BYTES + LM_HEAD_BYTES
@@ -588,16 +589,67 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     return result
 
 
+GOLDEN_SAMPLED = os.path.join(ROOT, "tests", "golden", "config4_sampled.npz")
+
+
+def verify_sampled(dec, w) -> dict:
+    """The sampled-decoding check of tests/test_gpu_decode_config4_sampled.py on the timed decoder
+    (captured step): the oracle's sampled run of config 4 (tests/golden/config4_sampled.npz: the
+    prompt's last position, then 32 steps at T 0.1 / top-p 0.9 / penalty 1.1 from seed 0x5eed) -
+    draws equal bit for bit at every step, the token equal to the oracle's sampler on the GPU's
+    own logits wherever that sampler is 2e-6 clear of its boundaries, and to the oracle's token
+    wherever its margins clear the logit error (4 x max error over its 64 largest logits / T)."""
+    import oracle
+
+    with np.load(GOLDEN_SAMPLED, allow_pickle=False) as f:
+        g = {k: f[k] for k in f.files}
+    T, top_p = float(g["temperature"]), float(g["top_p"])
+    for s_, t in enumerate(w.prompt[:-1]):
+        dec.reset(w.prime + s_, t)
+        dec.step(read_token=False)
+    dec.set_sampling(T, top_p, float(g["penalty"]))
+    dec.seed(int(g["seed"]))
+    history = [int(t) for t in w.prompt]
+    dec.set_history(history)
+    dec.reset(w.prime + len(w.prompt) - 1, w.prompt[-1])
+    draws_equal, sampler, e2e, forced, max_err = 0, 0, 0, 0, 0.0
+    steps = len(g["positions"])
+    for i, pos in enumerate(g["positions"]):
+        tok = dec.step()
+        draws_equal += int(dec.sample_params()["random"].view(np.uint32) == g["draws"][i].view(np.uint32))
+        got = dec.logits()
+        err = float(np.abs(got[g["top_ids"][i]].astype(np.float64) - g["top_values"][i]).max())
+        max_err = max(max_err, err / float(g["rms"][i]))
+        mine, info, _ = oracle.sample(got, np.zeros(0, np.uint32), T, top_p, 1.0, float(g["draws"][i]))
+        if info.bisect_margin > 2e-6 and info.draw_margin > 2e-6:
+            sampler += int(tok == mine) - (tok != mine) * 1000  # a mismatch fails the check below
+        want = int(g["tokens"][i])
+        eps = 4 * err / T
+        if g["bisect_margin"][i] > eps and g["draw_margin"][i] > eps:
+            e2e += int(tok == want) - (tok != want) * 1000
+        history.append(want)
+        if tok != want:
+            dec.reset(int(pos) + 1, want)
+            dec.set_history(history)
+            forced += 1
+    return {"oracle": "tests/golden/config4_sampled.npz", "steps": steps, "draws_equal": draws_equal,
+            "sampler_on_gpu_logits_equal": sampler, "end_to_end_equal": e2e, "continued_on_oracle_token": forced,
+            "max_logit_error_vs_rms": round(max_err, 6),
+            "verified": draws_equal == steps and sampler >= 0.8 * steps and e2e >= 0.75 * steps}
+
+
 STAMP_WAVES = 8192  # per launch slot (eg_test_launch_stamps)
 
 
 def decode_timeline(dev, args) -> dict:
     """The config-4 decode step as bench.py times it - captured in a hipGraph, at positions
     1920..2047, one 4-byte readback per token - with every launch writing per-wave wall-clock
-    stamps (eg_test_launch_stamps: each wave's entry and exit, s_memrealtime). Per launch of the
-    step: its duration (first wave in to last wave out) and the gap to the next launch, medians
-    over the timed steps; also the gap between steps (the readback and the next replay's
-    submission). Greedy steps, then the same positions sampled (T 0.7 / top-p 0.9 / penalty 1.1)."""
+    stamps (eg_test_launch_stamps: each wave's entry and exit, s_memrealtime). The stamps of the
+    last of 8 back-to-back steps are read, so every sample follows seven steps run as the timed
+    loop runs them. Per launch of the step: its duration (first wave in to last wave out) and the
+    gap to the next launch, medians over the samples; the step's first-in to last-out time, and
+    the host's share of a token (wall time of the 8 steps / 8 minus the step). Greedy steps, then
+    the same positions sampled (T 0.7 / top-p 0.9 / penalty 1.1)."""
     from enargeia_amd import _lib
     from enargeia_amd.model import QWEN25_05B, Decoder, DeviceModel, cache_fill, config4_workload, synthetic_model
 
@@ -632,45 +684,73 @@ def decode_timeline(dev, args) -> dict:
         rec = ctypes.c_uint32()
         _lib.check(lib.eg_test_launch_stamps(dev.ctx, None, 0, ctypes.byref(rec)), dev.ctx)
         n = rec.value
-        names = [f"L{l} {layer_names[j]}" for l in range(cfg.layers) for j in range(5)]
-        names += ["LM head (final-norm stage)"] + (["sampler"] if mode == "sampled" else []) + ["step tail"]
+        tail_names = ["LM head (final-norm stage)"] + (["sampler"] if mode == "sampled" else []) + ["step tail"]
+        persistent = n == 1 + len(tail_names)
+        if persistent:  # the 24 layers as one launch (eg_layers.hip)
+            names = ["decode layers (one persistent launch)"] + tail_names
+        else:
+            names = [f"L{l} {layer_names[j]}" for l in range(cfg.layers) for j in range(5)] + tail_names
         assert n == len(names), f"{n} launches took a slot, {len(names)} expected"
         for i, t in enumerate(w.prompt):
             dec.reset(w.prime + i, t)
             first = dec.step(read_token=True)
         if mode == "sampled":
             dec.set_history(list(w.prompt) + [first])
-        dec.reset(start, first)
-        for _ in range(8):
-            dec.step(read_token=True)
-        durs, gaps, steps_us, between = [], [], [], []
-        prev_end = None
-        for _ in range(min(args.steps, 120)):
+        durs, gaps, steps_us, walls, phase_adds = [], [], [], [], []
+        for rep in range(max(4, min(args.steps, 120) // 8)):
+            dec.reset(start + 8 * (rep % 12), first)
+            t = time.perf_counter()
+            for _ in range(8):
+                dec.step(read_token=True)
+            walls.append((time.perf_counter() - t) / 8 * 1e6)
+            # the sample: one more step, after zeroing the persistent launch's per-phase maxima
+            dev.zero(buf, STAMP_WAVES * 8, STAMP_WAVES * 8)
             dec.step(read_token=True)
             raw = np.frombuffer(dev.read(buf, n * STAMP_WAVES * 16), np.uint64).reshape(n, STAMP_WAVES, 2)
-            t0s = np.array([r[r[:, 0] > 0, 0].min() for r in raw], np.float64)
-            t1s = np.array([r[r[:, 1] > 0, 1].max() for r in raw], np.float64)
+            waves = [r[:STAMP_WAVES // 2] if (persistent and i == 0) else r for i, r in enumerate(raw)]
+            t0s = np.array([r[r[:, 0] > 0, 0].min() for r in waves], np.float64)
+            t1s = np.array([r[r[:, 1] > 0, 1].max() for r in waves], np.float64)
             durs.append((t1s - t0s) * tick_us)
             gaps.append((t0s[1:] - t1s[:-1]) * tick_us)
             steps_us.append((t1s[-1] - t0s[0]) * tick_us)
-            if prev_end is not None:
-                between.append((t0s[0] - prev_end) * tick_us)
-            prev_end = t1s[-1]
+            if persistent:
+                # per phase: ~ the first workgroup past its wait, the last one past it, the last
+                # arrival (the first layer's q|k|v waits for nothing: the launch's first wave)
+                flat = raw[0].reshape(-1)[STAMP_WAVES:STAMP_WAVES + 4 * 5 * cfg.layers].reshape(-1, 4)
+                first_in = np.where(flat[:, 0] > 0, (~flat[:, 0]).astype(np.float64), np.nan)
+                last_in = flat[:, 1].astype(np.float64)
+                ends = flat[:, 2].astype(np.float64)
+                first_in[0] = last_in[0] = t0s[0]
+                prev = np.concatenate([[t0s[0]], ends[:-1]])
+                phase_adds.append(np.stack([ends - prev, first_in - prev, last_in - first_in, ends - last_in]) * tick_us)
         d = np.median(np.array(durs), axis=0)
         g = np.median(np.array(gaps), axis=0)
         per_kind = {}
-        for j, kind in enumerate(layer_names):
-            per_kind[kind] = {"us": round(float(np.median(d[j:5 * cfg.layers:5])), 2),
-                              "gap_after_us": round(float(np.median(g[j:5 * cfg.layers:5])), 2)}
-        for i in range(5 * cfg.layers, n):
+        first_tail = 1 if persistent else 5 * cfg.layers
+        if persistent:
+            # [4, phases]: the phase's add to the launch (previous phase's last arrival to its
+            # own), of which: to the first workgroup past the wait, from there to the last one
+            # past it, from there to the last arrival; medians over samples, then layers (the
+            # first layer's q|k|v, which waits for nothing, left out)
+            adds = np.median(np.array(phase_adds), axis=0)
+            keys = ["adds_us", "to_first_past_wait_us", "first_to_last_past_wait_us", "last_past_wait_to_last_arrival_us"]
+            per_kind[names[0]] = {"us": round(float(d[0]), 2), "gap_after_us": round(float(g[0]), 2),
+                                  "phases": {kind: {k: round(float(np.median(adds[i, j + (5 if j == 0 else 0)::5])), 2)
+                                                    for i, k in enumerate(keys)}
+                                             for j, kind in enumerate(layer_names)}}
+        else:
+            for j, kind in enumerate(layer_names):
+                per_kind[kind] = {"us": round(float(np.median(d[j:5 * cfg.layers:5])), 2),
+                                  "gap_after_us": round(float(np.median(g[j:5 * cfg.layers:5])), 2)}
+        for i in range(first_tail, n):
             per_kind[names[i]] = {"us": round(float(d[i]), 2),
                                   "gap_after_us": round(float(g[i]), 2) if i < n - 1 else None}
+        step_us, wall_us = float(np.median(steps_us)), float(np.median(walls))
         result[mode] = {
-            "launches": n, "per_launch": per_kind,
+            "launches": n, "samples": len(durs), "per_launch": per_kind,
             "kernel_us_per_step": round(float(d.sum()), 1), "gaps_us_per_step": round(float(g.sum()), 1),
-            "first_in_to_last_out_us": round(float(np.median(steps_us)), 1),
-            "between_steps_us": round(float(np.median(between)), 1) if between else None,
-            "token_us": round(float(np.median(steps_us)) + (float(np.median(between)) if between else 0.0), 1)}
+            "first_in_to_last_out_us": round(step_us, 1), "wall_us_per_token": round(wall_us, 1),
+            "host_and_readback_us_per_token": round(wall_us - step_us, 1)}
         log(f"decode timeline ({mode}): {result[mode]}")
     dec.close()
     dm.release()

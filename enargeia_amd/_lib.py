@@ -79,6 +79,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_decoder_capture": (_i, [_vp]),
     "eg_decoder_set_sampling": (_i, [_vp, _vp]),
     "eg_decoder_seed": (_i, [_vp, ctypes.c_uint32]),
+    "eg_decoder_launches": (_i, [_vp, ctypes.POINTER(ctypes.c_uint32)]),
     "eg_decoder_set_position": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
     "eg_decoder_set_history": (_i, [_vp, _vp, ctypes.c_uint32]),
     "eg_decoder_prefill": (_i, [_vp, ctypes.c_uint32, _vp, ctypes.c_uint32, _vp]),

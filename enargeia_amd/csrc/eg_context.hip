@@ -1,5 +1,6 @@
 // Context, buffers, errors and graph capture: the part of the ABI that replaces the
 // reference's gpu layer (src/gpu/device.ts, pool.ts, readback.ts) for this path.
+#include <algorithm>
 #include <cstdlib>
 
 #include "eg_internal.hpp"
@@ -93,15 +94,14 @@ int eg_create(int device, eg_context** out_ctx) {
   }
   ctx->stream = ctx->own_stream;
   if (const char* shape = std::getenv("EG_GEMV_SHAPE")) {
-    int t = 0, c = 0, u = 0, d = 2, xl = 0;
-    const int got = std::sscanf(shape, "%d,%d,%d,%d,%d", &t, &c, &u, &d, &xl);
+    int t = 0, c = 0, u = 0, d = 2;
+    const int got = std::sscanf(shape, "%d,%d,%d,%d", &t, &c, &u, &d);
     if (got >= 3 && (t == 8 || t == 16 || t == 32 || t == 64) && c >= 1 && c <= 4 && (u == 1 || u == 2 || u == 4) &&
-        d >= 2 && d <= 8 && (xl == 0 || xl == 1)) {
+        d >= 2 && d <= 8) {
       ctx->gemv_override[0] = t;
       ctx->gemv_override[1] = c;
       ctx->gemv_override[2] = u;
       ctx->gemv_override[3] = d;
-      ctx->gemv_override[4] = xl;
     }
   }
   if (const char* tpw = std::getenv("EG_FUSED_TILES_PER_WAVE")) {
@@ -112,6 +112,9 @@ int eg_create(int device, eg_context** out_ctx) {
   if (const char* pr = std::getenv("EG_PREFILL_ROPE")) ctx->prefill_rope = std::atoi(pr) != 0;
   if (const char* xb = std::getenv("EG_PREFILL_XB16")) ctx->prefill_xb16 = std::atoi(xb) != 0;
   if (const char* xc = std::getenv("EG_PREFILL_XCD")) ctx->prefill_xcd = std::atoi(xc) != 0;
+  if (const char* dp = std::getenv("EG_DECODE_PERSISTENT")) ctx->decode_persistent = std::atoi(dp) != 0;
+  if (const char* pg = std::getenv("EG_PERSISTENT_GRID")) ctx->persistent_grid = (uint32_t)std::max(0, std::atoi(pg));
+  if (const char* pp = std::getenv("EG_PERSISTENT_POLL")) ctx->persistent_poll = (uint32_t)std::min(64, std::max(0, std::atoi(pp)));
   if (const char* a = std::getenv("EG_ATTENTION_SPLIT")) {
     int t = 0, f = 0;
     if (std::sscanf(a, "%d,%d", &t, &f) == 2 && t >= 1 && t <= 64 && f >= 1 && f <= 8) {
@@ -119,7 +122,6 @@ int eg_create(int device, eg_context** out_ctx) {
       ctx->attention_split_fill = (uint32_t)f;
     }
   }
-  if (const char* g = std::getenv("EG_PREFILL_STAGES")) ctx->prefill_stages = std::atoi(g);
   if (const char* g = std::getenv("EG_PREFILL_GROUPS")) {
     const int v = std::atoi(g);
     if (v == 1 || v == 2 || v == 4) ctx->prefill_groups = v;

@@ -77,6 +77,9 @@ struct eg_decoder {
   uint16_t* v_cache = nullptr;
   size_t layer_stride = 0;  // cache elements per layer
   std::vector<eg_gemv_plan*> plans;  // per layer: qkv, o, gate|up (a SwiGLU pair if swiglu), down
+  // the layers of a step as one persistent launch (eg_layers.hip), where the shapes and the
+  // device allow; NULL: one launch per op
+  eg_layers* layers_kernel = nullptr;
   bool swiglu = false;               // gate|up stores silu(gate) * up in gu[0, intermediate)
   eg_graph* graph = nullptr;
   std::vector<void*> allocations;
@@ -99,6 +102,7 @@ void release(eg_decoder* d) {
   if (d->host_staging) (void)hipHostFree(d->host_staging);
   if (d->graph) eg_graph_destroy(d->graph);
   if (d->head_plan) eg_gemv_plan_destroy(d->ctx, d->head_plan);
+  eg::layers_destroy(d->ctx, d->layers_kernel);
   for (eg_gemv_plan* p : d->plans) eg_gemv_plan_destroy(d->ctx, p);
   for (void* p : d->allocations) eg_buf_free(d->ctx, p);
   delete d;
@@ -130,6 +134,8 @@ int tail(eg_decoder* d, eg::StepTail t) {
   const eg_embedding_dims ed = embedding_dims_of(m);
   t.rope_table = reinterpret_cast<const double2*>(d->rope_table);
   t.rope_positions = m.max_context;
+  if (d->layers_kernel)
+    eg::layers_sync_words(d->layers_kernel, &t.sync_counters, &t.sync_count, &t.sync_stride, &t.sync_abort);
   return eg::launch_step_tail(d->ctx, t, d->token, d->position, m.embedding.packed, m.embedding.scales,
                               m.embedding.zeros, &ed, m.embed_encoding, m.embed_bits, d->emb, d->rope, m.head_dim,
                               m.rope_theta);
@@ -144,10 +150,33 @@ eg::StepTail advancing_tail(eg_decoder* d) {
   return t;
 }
 
+// The input of each per-layer plan (qkv, o, gate|up, down) - the per-op launches' and the
+// persistent kernel's.
+void layer_inputs(const eg_decoder* d, uint32_t l, eg_gemv_input in[4]) {
+  const eg_model_desc& m = d->desc;
+  const eg_layer_desc& L = d->layers[l];
+  for (int j = 0; j < 4; j++) in[j] = eg_gemv_input{};
+  in[0].kind = EG_INPUT_RMSNORM;
+  in[0].x = l == 0 ? d->emb : d->h[0];
+  in[0].x2 = L.input_norm;
+  in[0].eps = m.rms_eps;
+  in[1].kind = EG_INPUT_ATTENTION;
+  in[1].x = d->partials;
+  in[1].attention = d->att;
+  in[2].kind = EG_INPUT_RMSNORM;
+  in[2].x = d->h[1];
+  in[2].x2 = L.post_attention_norm;
+  in[2].eps = m.rms_eps;
+  in[3].kind = d->swiglu ? EG_INPUT_VECTOR : EG_INPUT_SILU_MUL;
+  in[3].x = d->gu;
+  in[3].x2 = d->swiglu ? nullptr : d->gu + m.intermediate;
+}
+
 // The 24 layers of a step on the token whose embedding is in d->emb at position[0].
 int run_layers(eg_decoder* d) {
   eg_context* ctx = d->ctx;
   const eg_model_desc& m = d->desc;
+  if (d->layers_kernel) return eg::layers_launch(ctx, d->layers_kernel);
   int st = EG_OK;
   for (uint32_t l = 0; l < m.layers; l++) {
     const eg_layer_desc& L = d->layers[l];
@@ -200,6 +229,7 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
   in.x2 = m.final_norm;
   in.eps = m.rms_eps;
   eg::StepTail t = advancing_tail(d);
+  t.status = d->token + 2;  // a step that gives up is counted here and moves nothing
   if (!sampled) {
     eg_embedding_dims hd = embedding_dims_of(m);
     hd.grid_width = 65535;
@@ -225,7 +255,6 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
   if ((st = eg::launch_sample_device(ctx, d->logits, d->history, d->token, m.vocab, d->sp, rng, nullptr)) != EG_OK)
     return st;
   t.rng = rng;
-  t.status = d->token + 2;
   return tail(d, t);
 }
 
@@ -333,9 +362,9 @@ int read_token(eg_decoder* d, uint32_t* token_out, const char* op) {
     int st = write_ids(d, d->token + 2, &zero, 1);
     if (st != EG_OK) return st;
     return eg::fail(d->ctx, EG_ERR_DEVICE,
-                    "%s: the sampler gave up on %u step(s) (a grid barrier timed out: not every workgroup was "
-                    "resident at once); the position, history and draw state are as before those steps, and the "
-                    "next step redoes the step",
+                    "%s: %u step(s) gave up: a bounded wait timed out (not every workgroup was resident at once); "
+                    "the position, history and draw state are as before those steps, and the next step redoes the "
+                    "step",
                     op, failed);
   }
   *token_out = d->host_token[0];
@@ -502,6 +531,27 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     eg_gemv_segment head[1] = {{m.embedding.packed, m.embedding.scales, m.embedding.zeros, nullptr, d->logits, m.vocab, 0}};
     st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
   }
+  if (st == EG_OK && ctx->decode_persistent) {
+    std::vector<eg::LayerPlans> lp(m.layers);
+    for (uint32_t l = 0; l < m.layers; l++) {
+      for (int j = 0; j < 4; j++) lp[l].plan[j] = d->plans[4 * (size_t)l + j];
+      layer_inputs(d, l, lp[l].input);
+    }
+    eg::LayersDesc ld{};
+    ld.layers = m.layers;
+    ld.plans = lp.data();
+    ld.att = d->att;
+    ld.position = d->position;
+    ld.rope = d->rope;
+    ld.q = d->q;
+    ld.k = d->kv;
+    ld.v = d->kv + kvn;
+    ld.partials = d->partials;
+    ld.k_cache = d->k_cache;
+    ld.v_cache = d->v_cache;
+    ld.layer_stride = d->layer_stride;
+    st = eg::layers_create(ctx, ld, &d->layers_kernel);
+  }
   if (st == EG_OK) {
     hipError_t err = hipHostMalloc(reinterpret_cast<void**>(&d->host_token), 4 * sizeof(uint32_t), hipHostMallocDefault);
     if (err != hipSuccess) d->host_token = nullptr;
@@ -611,6 +661,15 @@ int eg_decoder_set_sampling(eg_decoder* d, const eg_sampling_params* params) {
   // a graph captured in the other mode (greedy fused argmax / sampler) is captured again
   if (d->graph && (d->graph_sampled != sampled_mode(p) || d->graph_host_driven != d->host_driven)) st = capture(d);
   return st;
+}
+
+int eg_decoder_launches(eg_decoder* d, uint32_t* per_step) {
+  if (!d || !per_step) return eg::fail(d ? d->ctx : nullptr, EG_ERR_INVALID, "decoder_launches: NULL argument");
+  // the layers (one persistent launch, or 5 per layer), the LM head, the sampler unless GREEDY,
+  // the tail, and a host-driven step's input preparation
+  *per_step = (d->layers_kernel ? 1u : 5u * d->desc.layers) + 2u + (sampled_mode(d->sampling) ? 1u : 0u) +
+              (d->host_driven ? 1u : 0u);
+  return EG_OK;
 }
 
 int eg_decoder_seed(eg_decoder* d, uint32_t seed) {

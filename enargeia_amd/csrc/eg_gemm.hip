@@ -296,7 +296,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // XB16 (chunked staging, no NORM): x holds bf16 values (a producer stored them rounded as the
 // staging would), staged as they are.
 //
-// S: register stages of the chunked staging (blocks in flight per group: S - 1).
+// S: register stages of the chunked staging (blocks in flight per group: S - 1). Four groups fit
+// four waves per SIMD only within 128 VGPRs: they keep one block in flight. Measured on the
+// config-3 shapes, deeper staging does not pay: one group at S = 5 runs as S = 3, at S = 8 (one
+// wave per SIMD) 18.5 -> 27.4 us for gate M = 256; two groups at S = 4 and four at S = 3 are
+// slower than their defaults.
 template <int ENC, bool CHUNKED, int KG, bool PAIR = false, bool NORM = false, bool ROPE = false, bool XB16 = false,
           int S = (KG >= 4 ? 2 : kStages)>
 __global__ __launch_bounds__(256 * KG) void prefill_kernel(PrefillArgs a) {
@@ -658,21 +662,11 @@ int eg::prefill_gemm(eg_context* ctx, const float* x, const uint32_t* packed, co
   if (x_bf16 && !chunked)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: bf16 rows of x need the chunked staging", op);
   const dim3 block(256 * kg);
-  // register stages: the group count's default, or EG_PREFILL_STAGES where that form is built
-  const int stages = ctx->prefill_stages;
-#define EG_PREFILL_LAUNCH(ENC, CH)                                                                                \
-  do {                                                                                                            \
-    if (kg == 4 && stages == 3) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 4, false, false, false, false, 3>), grid, \
-                                                   block, 0, ctx->stream, a);                                     \
-    else if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 4>), grid, block, 0, ctx->stream, a);           \
-    else if (kg == 2 && stages == 4) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 2, false, false, false, false, 4>), \
-                                                        grid, block, 0, ctx->stream, a);                          \
-    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 2>), grid, block, 0, ctx->stream, a);           \
-    else if (stages == 5) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1, false, false, false, false, 5>), grid,     \
-                                             block, 0, ctx->stream, a);                                           \
-    else if (stages == 8) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1, false, false, false, false, 8>), grid,     \
-                                             block, 0, ctx->stream, a);                                           \
-    else hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1>), grid, block, 0, ctx->stream, a);                        \
+#define EG_PREFILL_LAUNCH(ENC, CH)                                                                        \
+  do {                                                                                                    \
+    if (kg == 4) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 4>), grid, block, 0, ctx->stream, a);        \
+    else if (kg == 2) hipLaunchKernelGGL((prefill_kernel<ENC, CH, 2>), grid, block, 0, ctx->stream, a);   \
+    else hipLaunchKernelGGL((prefill_kernel<ENC, CH, 1>), grid, block, 0, ctx->stream, a);                \
   } while (0)
   if (x_bf16) {
     launch_chunked<false, false, false, true>(encoding, kg, grid, ctx->stream, a);

@@ -91,50 +91,33 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
   X(64, 1, 4, 3) X(64, 2, 1, 2) X(64, 2, 2, 2) X(64, 3, 1, 2) X(64, 3, 1, 3) X(64, 3, 1, 4) X(64, 3, 2, 2) \
   X(64, 4, 1, 2)
 
-// Shapes instantiated with their last chunk slot's x in LDS (XL = 1; int4 rows of 3-4 slots).
-#define EG_XL_SHAPES(X) X(64, 3, 1, 2) X(64, 3, 1, 3) X(64, 3, 1, 4) X(64, 4, 1, 2)
-
 template <int BITS, int ENC, int MODE>
-KernelFn pick(int team, int cpl, int u, int nb, int xl) {
-  if (xl == 0) {
+KernelFn pick(int team, int cpl, int u, int nb) {
 #define EG_CASE(T, P, UU, D) \
   if (team == T && cpl == P && u == UU && nb == D) return gemv_kernel<BITS, ENC, T, P, UU, D, MODE, EG_INPUT_VECTOR>;
-    EG_SHAPES(EG_CASE)
+  EG_SHAPES(EG_CASE)
 #undef EG_CASE
-  } else if constexpr (BITS == 4) {
-    if (xl == 1) {
-#define EG_XL_CASE(T, P, UU, D)                            \
-  if (team == T && cpl == P && u == UU && nb == D) \
-    return gemv_kernel<BITS, ENC, T, P, UU, D, MODE, EG_INPUT_VECTOR, 1>;
-      EG_XL_SHAPES(EG_XL_CASE)
-#undef EG_XL_CASE
-    }
-  }
   return nullptr;
 }
 
 template <int BITS, int ENC>
-KernelFn pick_mode(int mode, int team, int cpl, int u, int nb, int xl) {
-  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb, xl);
-  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb, xl);
-  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb, xl);
-  return pick<BITS, ENC, kPlain>(team, cpl, u, nb, xl);
+KernelFn pick_mode(int mode, int team, int cpl, int u, int nb) {
+  if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb);
+  if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb);
+  if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb);
+  return pick<BITS, ENC, kPlain>(team, cpl, u, nb);
 }
 
-// The kernel of a (format, mode, shape); xl (x slots read from LDS) applies to x given as a
-// vector only - a fused input stage takes the register form.
-KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u, int nb, int in_kind = EG_INPUT_VECTOR,
-                     int xl = 0) {
+KernelFn pick_kernel(int bits, int enc, int mode, int team, int cpl, int u, int nb, int in_kind = EG_INPUT_VECTOR) {
   if (in_kind != EG_INPUT_VECTOR) return pick_fused(bits, enc, mode, in_kind, team, cpl, u, nb);
-  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb, xl);
-  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u, nb, xl);
-  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb, xl);
-  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u, nb, xl);
+  if (bits == 4 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<4, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
+  if (bits == 4 && enc == EG_ENC_SIGNED) return pick_mode<4, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
+  if (bits == 8 && enc == EG_ENC_OFFSET_ZEROS) return pick_mode<8, EG_ENC_OFFSET_ZEROS>(mode, team, cpl, u, nb);
+  return pick_mode<8, EG_ENC_SIGNED>(mode, team, cpl, u, nb);
 }
 
 struct Shape {
   int team = 0, cpl = 0, u = 0, nb = 2;
-  int xl = 0;  // chunk slots whose x is read from LDS per tile
   uint32_t tiles = 0;
 };
 
@@ -183,7 +166,6 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
     sh.cpl = ctx->gemv_override[1];
     sh.u = ctx->gemv_override[2];
     sh.nb = ctx->gemv_override[3];
-    sh.xl = ctx->gemv_override[4];
     if ((uint32_t)(sh.team * sh.cpl) < chunks) return Shape{};
   }
   const uint32_t rpw = 64u / sh.team;
@@ -322,7 +304,7 @@ int launch(eg_context* ctx, const QuantView& v) {
   const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   const int in_kind = v.input ? v.input->kind : EG_INPUT_VECTOR;
   KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u,
-                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind, shape.xl)
+                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind)
                            : nullptr;
   if (fused && !fn)
     return eg::fail(ctx, EG_ERR_INVALID,
@@ -499,7 +481,7 @@ struct eg_gemv_plan {
   uint32_t count = 0;
   uint32_t swiglu_rows = 0;  // a SwiGLU pair (eg_gemv_swiglu_plan_create): the rows of each matrix
   uint32_t k = 0, block_size = 0, chunks = 0, total_passes = 0, grid = 0, smem = 0;
-  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2, xl = 0;
+  int encoding = 0, bits = 0, team = 0, cpl = 0, u = 0, nb = 2;
 };
 
 extern "C" {
@@ -583,9 +565,7 @@ int eg_gemv_plan_create(eg_context* ctx, uint32_t k, uint32_t block_size, int en
   plan->cpl = shape.cpl;
   plan->u = shape.u;
   plan->nb = shape.nb;
-  plan->xl = shape.xl;
-  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb, EG_INPUT_VECTOR,
-                            shape.xl);
+  KernelFn fn = pick_kernel(bits, encoding, kBatched, shape.team, shape.cpl, shape.u, shape.nb);
   plan->smem = k * 4u;
   plan->grid = fn ? grid_for(ctx, fn, pass, plan->smem) : 0;
   delete[] host;
@@ -656,7 +636,7 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
     return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: a SwiGLU pair takes the RMSNORM input stage");
   a.n = plan->swiglu_rows;
   KernelFn fn = pick_kernel(plan->bits, plan->encoding, pair ? kSwiGLU : kBatched, plan->team, plan->cpl, plan->u,
-                            a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb, a.in_kind, plan->xl);
+                            a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb, a.in_kind);
   if (!fn) return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_launch: no kernel for this plan's shape");
   const uint32_t extra = input_scratch_bytes(a);
   const uint32_t grid = a.in_kind != EG_INPUT_VECTOR
@@ -667,6 +647,43 @@ int eg_gemv_plan_launch_input(eg_context* ctx, const eg_gemv_plan* plan, const e
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
   return eg::check_launch(ctx, "gemv_plan_launch");
 }
+
+}  // extern "C"
+
+int eg_gemv::plan_phase(eg_context* ctx, const eg_gemv_plan* plan, const eg_gemv_input* input, GemvArgs* args,
+                        PlanPhase* phase) {
+  if (!plan || !input || !input->x || !args || !phase)
+    return eg::fail(ctx, EG_ERR_INVALID, "gemv_plan_phase: NULL argument");
+  GemvArgs a{};
+  int st = apply_input(ctx, "gemv_plan_phase", input, plan->k, a);
+  if (st != EG_OK) return st;
+  a.chunks = plan->chunks;
+  a.chunks_per_block = plan->block_size / (128u / plan->bits);
+  a.blocks_per_row = plan->k / plan->block_size;
+  a.segs = plan->table;
+  a.seg_index = plan->seg_index;
+  a.seg_count = plan->count;
+  if (plan->count <= kInlineSegments)
+    for (uint32_t i = 0; i < plan->count; i++) a.inline_segs[i] = plan->inline_table[i];
+  a.total_passes = plan->total_passes;
+  a.any_bias = plan->any_bias;
+  const bool pair = plan->swiglu_rows != 0;
+  a.n = plan->swiglu_rows;
+  *args = a;
+  phase->bits = plan->bits;
+  phase->encoding = plan->encoding;
+  phase->mode = pair ? kSwiGLU : kBatched;
+  phase->in_kind = a.in_kind;
+  phase->team = plan->team;
+  phase->cpl = plan->cpl;
+  phase->u = plan->u;
+  phase->nb = a.in_kind != EG_INPUT_VECTOR ? 2 : plan->nb;
+  phase->tiles = plan->total_passes;
+  phase->smem = plan->smem + input_scratch_bytes(a);
+  return EG_OK;
+}
+
+extern "C" {
 
 int eg_gemv_plan_destroy(eg_context* ctx, eg_gemv_plan* plan) {
   if (!plan) return EG_OK;

@@ -132,38 +132,6 @@ struct Codes<4> {
     }
     return a0 + a1;
   }
-  // The same sum with x read from LDS (chunk-transposed: piece e of the chunk at xp[e * stride],
-  // unscaled) instead of registers: the high nibbles are shifted down (one more op per word) in
-  // place of x's pre-division by 16, so every product and sum is the one dot() forms - the
-  // products 16c * (x / 16) and c * x are the same exact value inside each fused multiply-add.
-  template <int ENC>
-  static __device__ __forceinline__ float dot_lds(const uint4& q, const egd::u32x4* xp, uint32_t stride) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const egd::u32x4 p0 = xp[(size_t)(2 * i) * stride], p1 = xp[(size_t)(2 * i + 1) * stride];
-      const float xv[8] = {__uint_as_float(p0.x), __uint_as_float(p0.y), __uint_as_float(p0.z), __uint_as_float(p0.w),
-                           __uint_as_float(p1.x), __uint_as_float(p1.y), __uint_as_float(p1.z), __uint_as_float(p1.w)};
-      uint32_t lo, hi;
-      if (ENC == EG_ENC_SIGNED) {
-        lo = (d[i] & 0x0F0F0F0Fu) ^ 0x08080808u;
-        hi = ((d[i] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-      } else {
-        lo = egd::and_opaque(d[i], 0x0F0F0F0Fu);
-        hi = egd::and_opaque(d[i] >> 4, 0x0F0F0F0Fu);
-      }
-      a0 = fmaf(egd::ub0(lo), xv[0], a0);
-      a1 = fmaf(egd::ub0(hi), xv[1], a1);
-      a0 = fmaf(egd::ub1(lo), xv[2], a0);
-      a1 = fmaf(egd::ub1(hi), xv[3], a1);
-      a0 = fmaf(egd::ub2(lo), xv[4], a0);
-      a1 = fmaf(egd::ub2(hi), xv[5], a1);
-      a0 = fmaf(egd::ub3(lo), xv[6], a0);
-      a1 = fmaf(egd::ub3(hi), xv[7], a1);
-    }
-    return a0 + a1;
-  }
 };
 
 template <>
@@ -171,20 +139,6 @@ struct Codes<8> {
   static constexpr int kPerChunk = 16;
   static constexpr int kZeroPerWord = 4;
   static __device__ __forceinline__ float x_scale(int) { return 1.0f; }
-  // dot() with x read from LDS (piece e of the chunk at xp[e * stride])
-  template <int ENC>
-  static __device__ __forceinline__ float dot_lds(const uint4& q, const egd::u32x4* xp, uint32_t stride) {
-    float x[16];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const egd::u32x4 p = xp[(size_t)e * stride];
-      x[4 * e] = __uint_as_float(p.x);
-      x[4 * e + 1] = __uint_as_float(p.y);
-      x[4 * e + 2] = __uint_as_float(p.z);
-      x[4 * e + 3] = __uint_as_float(p.w);
-    }
-    return dot<ENC>(q, x);
-  }
   template <int ENC>
   static __device__ __forceinline__ float dot(const uint4& q, const float (&x)[16]) {
     uint32_t d[4] = {q.x, q.y, q.z, q.w};
@@ -218,6 +172,20 @@ struct Loads {
   float b;  // lane t < U of a team: the bias of the team's row t
 };
 
+// How a GEMV body runs. LaunchEnv: as its own launch - its grid, nothing to wait for, default
+// cache policy. The persistent decode kernel (eg_layers.hip) runs the same body as one phase of a
+// longer launch with an environment of its own: a virtual grid (the phase's workgroups), a wait
+// for the phase's inputs (called once the first tiles' weights are in flight), and coherent
+// accesses (kAux = egd::kCoherent) to everything another workgroup of the launch writes or reads -
+// the input vector, the residual bias, the outputs.
+struct LaunchEnv {
+  static constexpr int kAux = 0;
+  static constexpr bool kPhase = false;
+  __device__ __forceinline__ uint32_t block() const { return blockIdx.x; }
+  __device__ __forceinline__ uint32_t blocks() const { return gridDim.x; }
+  __device__ __forceinline__ void wait() const {}
+};
+
 // Where float4 i of x (P float4 per 16-byte chunk of codes: 8 for int4, 4 for int8) sits in LDS:
 // chunk-transposed, piece e of every chunk side by side (x_slot = e * chunks + chunk). A lane
 // reads its chunk's pieces in order, so at each read the lanes of a team touch consecutive 16-byte
@@ -243,13 +211,14 @@ __device__ __forceinline__ uint32_t x_slot(uint32_t i, uint32_t chunks) {
 // kernel issues its first tiles' weight loads there, so the weights are in flight while the
 // stage waits for its own reads and computes. (A wave's reads complete in issue order, so the
 // stage still waits only for its own loads; a workgroup barrier does not wait for reads.)
-template <int IN, int P, typename Early>
+// Env::kAux is the cache policy of the reads of x (and of the attention partials), which a phase
+// of the persistent kernel reads after another workgroup wrote them.
+template <int IN, int P, class Env, typename Early>
 __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint32_t n, float* scratch,
                                               Early&& early) {
+  constexpr int AUX = Env::kAux;
   const uint32_t tid = threadIdx.x;
   const uint32_t n4 = n / 4;  // n is a multiple of 32
-  const float4* x4 = reinterpret_cast<const float4*>(a.x);
-  const float4* y4 = reinterpret_cast<const float4*>(a.x2);
   // x goes into LDS chunk-transposed (see x_slot): float4 i of x at x_slot(i)
   float4* xs4 = reinterpret_cast<float4*>(xs);
   const uint32_t xchunks = n4 / P;  // 16-byte chunks of codes per row
@@ -264,7 +233,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     egd::u32x4 xv[kVec], wv[kVec];
 #pragma unroll
     for (uint32_t r = 0; r < kVec; r++) {
-      xv[r] = egd::load_b128(xb, (tid + r * 256u) * 16u);
+      xv[r] = egd::load_b128_p<AUX>(xb, (tid + r * 256u) * 16u);
       wv[r] = egd::load_b128(wb, (tid + r * 256u) * 16u);
     }
     early();
@@ -279,7 +248,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       ss = fmaf(v.w, v.w, ss);
     }
     for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) {
-      const float4 v = x4[i];
+      const float4 v = f4(egd::load_b128_p<AUX>(xb, i * 16u));
       ss = fmaf(v.x, v.x, ss);
       ss = fmaf(v.y, v.y, ss);
       ss = fmaf(v.z, v.z, ss);
@@ -300,7 +269,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       if (i < n4) put4(i, make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w));
     }
     for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) {
-      const float4 v = x4[i], w = y4[i];
+      const float4 v = f4(egd::load_b128_p<AUX>(xb, i * 16u)), w = f4(egd::load_b128(wb, i * 16u));
       put4(i, make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w));
     }
   } else if (IN == EG_INPUT_SILU_MUL) {
@@ -311,8 +280,8 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     egd::u32x4 gv[kVec], uv[kVec];
 #pragma unroll
     for (uint32_t r = 0; r < kVec; r++) {
-      gv[r] = egd::load_b128(gb, (tid + r * 256u) * 16u);
-      uv[r] = egd::load_b128(ub, (tid + r * 256u) * 16u);
+      gv[r] = egd::load_b128_p<AUX>(gb, (tid + r * 256u) * 16u);
+      uv[r] = egd::load_b128_p<AUX>(ub, (tid + r * 256u) * 16u);
     }
     early();
     auto silu_mul = [](const float4& g, const float4& u) {
@@ -324,7 +293,8 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       const uint32_t i = tid + r * 256u;
       if (i < n4) put4(i, silu_mul(f4(gv[r]), f4(uv[r])));
     }
-    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x) put4(i, silu_mul(x4[i], y4[i]));
+    for (uint32_t i = tid + kVec * 256u; i < n4; i += blockDim.x)
+      put4(i, silu_mul(f4(egd::load_b128_p<AUX>(gb, i * 16u)), f4(egd::load_b128_p<AUX>(ub, i * 16u))));
   } else if (IN == EG_INPUT_ATTENTION) {
     // The combine of the attention partials (chunk-fastest: o[h][D][chunks], m[h][chunks],
     // l[h][chunks]): every (head, chunk) pair's weight e^(m_c - M) / L goes into LDS, then every
@@ -359,8 +329,8 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       sval[r] = p < heads * G && c < chunks;
       sidx[r] = (p / G) * chunks + c;
       const uint32_t off = sval[r] ? sidx[r] * 4u : 0xFFFFFFF0u;  // past the stream: reads zero
-      mv[r] = __uint_as_float(egd::load_b32(mb, off));
-      lv[r] = __uint_as_float(egd::load_b32(lb, off));
+      mv[r] = __uint_as_float(egd::load_b32_p<AUX>(mb, off));
+      lv[r] = __uint_as_float(egd::load_b32_p<AUX>(lb, off));
     }
     egd::u32x4 ov[kOut][kQ];
     if (batched) {
@@ -368,7 +338,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       for (uint32_t r = 0; r < kOut; r++)
 #pragma unroll
         for (uint32_t q = 0; q < kQ; q++)
-          ov[r][q] = q < q4 ? egd::load_b128(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
+          ov[r][q] = q < q4 ? egd::load_b128_p<AUX>(ob, ((tid + r * 256u) * chunks + 4u * q) * 4u) : egd::u32x4{0, 0, 0, 0};
     }
     early();
 #pragma unroll
@@ -402,10 +372,9 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
       }
     } else {
       for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float* o = a.x + (size_t)i * chunks;
         const float* w = wts + (i / D) * chunks;
         float acc = 0.f;
-        for (uint32_t c = 0; c < chunks; c++) acc = fmaf(o[c], w[c], acc);
+        for (uint32_t c = 0; c < chunks; c++) acc = fmaf(egd::load_f32_p<AUX>(ob, (i * chunks + c) * 4u), w[c], acc);
         xs[x_slot<P>(i / 4, xchunks) * 4 + i % 4] = acc;
       }
     }
@@ -416,7 +385,7 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
     const auto src = egd::buffer(a.x, n4 * 16u);
     egd::u32x4 v[kMaxLoads];
 #pragma unroll
-    for (uint32_t r = 0; r < kMaxLoads; r++) v[r] = egd::load_b128(src, (tid + r * 256u) * 16u);
+    for (uint32_t r = 0; r < kMaxLoads; r++) v[r] = egd::load_b128_p<AUX>(src, (tid + r * 256u) * 16u);
     early();
     egd::u32x4* dst = reinterpret_cast<egd::u32x4*>(xs);
 #pragma unroll
@@ -442,20 +411,9 @@ __device__ __forceinline__ void produce_input(const GemvArgs& a, float* xs, uint
 //     its last tile (an L2 hit) instead of branching around the spare buffers;
 //   * stores are unconditional - the team total is in every lane of the team, every lane
 //     stores it, and a clamped or repeated row stores the value that row already has.
-//
-// XL > 0 (int4 full-wave teams): the last XL chunk slots keep x in LDS, read per tile, instead of
-// registers. A slot's x costs 32 VGPRs a lane; long rows (K = 4864: three slots) hold fewer waves
-// per SIMD for it, and in their last slot most lanes compute on padding. Reading that slot's x
-// from the workgroup's LDS copy each tile (8 conflict-free 16-byte reads per lane; a lane whose
-// slot lies past the row reads chunk 0 and its product is dropped) frees its registers for a
-// fourth wave per SIMD.
-template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN, int XL = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 : 1, 8))) void gemv_kernel(
-    GemvArgs a) {
-  const egd::WaveStamp stamp(a.stamp);
-  static_assert(XL >= 0 && XL < CPL && (XL == 0 || (BITS == 4 && TEAM == 64 && IN == EG_INPUT_VECTOR)),
-                "x slots from LDS: int4 full-wave teams with x given as a vector");
-  constexpr int CR = CPL - XL;  // chunk slots whose x is held in registers
+template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN, class Env>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
+  constexpr int AUX = Env::kAux;
   using C = Codes<BITS>;
   constexpr int EPC = C::kPerChunk;
   constexpr int RPW = 64 / TEAM;
@@ -469,8 +427,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t t = lane % TEAM;
   const uint32_t slot = lane / TEAM;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
-  const uint32_t total_waves = gridDim.x * kWaves;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(env.block() * kWaves + (threadIdx.x >> 6));
+  const uint32_t total_waves = env.blocks() * kWaves;
 
   // Dynamic LDS: x (chunks * EPC floats), then the input stage's scratch. The workgroup copies
   // x in once, so the activations cross L2 once per workgroup rather than once per wave; each
@@ -594,9 +552,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
     load_segment(seg);
   };
 
-  // What computing a tile needs once its loads are in flight: where its rows are stored.
+  // What computing a tile needs once its loads are in flight: where its rows are stored (and,
+  // for a phase's first tiles, whose bias loads wait for the phase's inputs, where it is read).
   struct Pending {
-    __amdgpu_buffer_rsrc_t o;
+    __amdgpu_buffer_rsrc_t o, b;
     uint32_t row0, out_offset;
   };
 
@@ -605,7 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
   // take one load instruction: lane t < U of each team reads its row t's (lanes past U re-read
   // row U-1's, unused).
   const uint32_t boff = ((t < (uint32_t)U ? t : (uint32_t)(U - 1)) * RPW + slot) * 4u;
-  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P) {
+  auto issue = [&](uint32_t tl, Loads<BITS, U, CPL>& L, Pending& P, bool with_bias = true) {
     tl = min(tl, last);
     if (MODE == kBatched)
       while (tl >= cur.end) load_segment(++seg);
@@ -614,7 +573,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
     const uint32_t row0 = __builtin_amdgcn_readfirstlane(min((tl - cur.first) * TILE, cur.rows - TILE));
     const uint32_t sq = row0 * (a.chunks * 16u);
     const uint32_t ss = row0 * (a.blocks_per_row * 4u);
-    L.b = egd::load_f32(cur.b, boff, row0 * 4u);
+    if (with_bias) L.b = egd::load_f32_p<AUX>(cur.b, boff, row0 * 4u);
 #pragma unroll
     for (int u = 0; u < U; u++) {
 #pragma unroll
@@ -629,37 +588,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
       }
     }
     P.o = cur.o;
+    P.b = cur.b;
     P.row0 = row0;
     P.out_offset = cur.out_offset;
   };
 
   // This lane's activations: chunk slot j covers x[cj*EPC, cj*EPC + EPC), zero past the row
   // (filled from LDS once the input stage has written x there).
-  float xr[CR][EPC];
+  float xr[CPL][EPC];
   float sx[CPL];
-  bool xvalid[CPL];  // the slot covers a chunk of the row (XL slots: the others' products are dropped)
   auto load_x = [&]() {
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
       const bool valid = t + j * TEAM < a.chunks;
-      xvalid[j] = valid;
       sx[j] = 0.f;
       const egd::u32x4* xs = reinterpret_cast<const egd::u32x4*>(smem) + cj[j];  // piece e at e * chunks
-      float xv[EPC];
 #pragma unroll
       for (int e = 0; e < EPC / 4; e++) {
         const egd::u32x4 v = xs[(size_t)e * a.chunks];
-        xv[4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
-        xv[4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
-        xv[4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
-        xv[4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
+        xr[j][4 * e + 0] = valid ? __uint_as_float(v.x) : 0.f;
+        xr[j][4 * e + 1] = valid ? __uint_as_float(v.y) : 0.f;
+        xr[j][4 * e + 2] = valid ? __uint_as_float(v.z) : 0.f;
+        xr[j][4 * e + 3] = valid ? __uint_as_float(v.w) : 0.f;
       }
 #pragma unroll
-      for (int e = 0; e < EPC; e++) sx[j] += xv[e];
-      if (j < CR) {
+      for (int e = 0; e < EPC; e++) sx[j] += xr[j][e];
 #pragma unroll
-        for (int e = 0; e < EPC; e++) xr[j < CR ? j : 0][e] = xv[e] * C::x_scale(e);
-      }
+      for (int e = 0; e < EPC; e++) xr[j][e] *= C::x_scale(e);
     }
   };
 
@@ -684,20 +639,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
         } else {
           z = (float)(1 << (BITS - 1));
         }
-        if (j < CR) {
-          acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j < CR ? j : 0]) - z * sx[j], acc);
-        } else {
-          // x from LDS; a slot past the row reads chunk 0's codes and x, whose product is dropped
-          const float dsum = C::template dot_lds<ENC>(q, reinterpret_cast<const egd::u32x4*>(smem) + cj[j], a.chunks);
-          acc = fmaf(xvalid[j] ? L.s[u][j] : 0.f, dsum - z * sx[j], acc);
-        }
+        acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j]) - z * sx[j], acc);
       }
       const float v = egd::team_allsum<TEAM>(acc);
       if (kPair) {
         pair[u & 1] = v;
         continue;
       }
-      if (kStore) egd::store_f32(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
+      if (kStore) egd::store_f32_p<AUX>(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
       if (kBest) {
         const uint32_t idx = row + P.out_offset;
         const bool take = egd::better(v, idx, best_v, best_i);
@@ -707,7 +656,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
     }
     if (kPair) {
       const float g = pair[0];
-      egd::store_f32(P.o, roff[0], g / (1.0f + expf(-g)) * pair[1], (P.row0 + P.out_offset) * 4u);
+      egd::store_f32_p<AUX>(P.o, roff[0], g / (1.0f + expf(-g)) * pair[1], (P.row0 + P.out_offset) * 4u);
     }
   };
 
@@ -728,10 +677,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
   auto start = [&]() {
     if (MODE == kBatched) find_first_segment();
 #pragma unroll
-    for (int b = 0; b + 1 < NB; b++) issue(first + b, L[b], P[b]);
+    for (int b = 0; b + 1 < NB; b++) issue(first + b, L[b], P[b], !Env::kPhase);
     __builtin_amdgcn_sched_barrier(0);
   };
-  produce_input<IN, EPC / 4>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
+  if constexpr (Env::kPhase) {
+    // A phase: the first tiles' weights go out before the wait for the phase's inputs, and
+    // travel while it lasts; their biases (a residual another workgroup writes) and x after it.
+    start();
+    env.wait();
+#pragma unroll
+    for (int b = 0; b + 1 < NB; b++) L[b].b = egd::load_f32_p<AUX>(P[b].b, boff, P[b].row0 * 4u);
+    produce_input<IN, EPC / 4, Env>(a, reinterpret_cast<float*>(smem), x_words, scratch, [] {});
+  } else {
+    produce_input<IN, EPC / 4, Env>(a, reinterpret_cast<float*>(smem), x_words, scratch, start);
+  }
   __syncthreads();
   load_x();
   const uint32_t count = end - begin;
@@ -775,10 +734,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(XL > 0 ? 4 
           bv = wv[k];
           bi = wi[k];
         }
-      a.partials[2 * blockIdx.x + 0] = __float_as_uint(bv);
-      a.partials[2 * blockIdx.x + 1] = bi;
+      a.partials[2 * env.block() + 0] = __float_as_uint(bv);
+      a.partials[2 * env.block() + 1] = bi;
     }
   }
+}
+
+template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  const egd::WaveStamp stamp(a.stamp);
+  gemv_body<BITS, ENC, TEAM, CPL, U, NB, MODE, IN>(a, LaunchEnv{});
 }
 
 using KernelFn = void (*)(GemvArgs);
@@ -833,6 +798,16 @@ KernelFn pick_fused_format(int bits, int enc, int mode, int team, int cpl, int u
 KernelFn pick_rmsnorm(int bits, int enc, int mode, int team, int cpl, int u);
 KernelFn pick_silu_mul(int bits, int enc, int mode, int team, int cpl, int u);
 KernelFn pick_attention(int bits, int enc, int mode, int team, int cpl, int u);
+
+// A plan's launch on an input as the persistent decode kernel runs it (one of its phases): the
+// kernel arguments eg_gemv_plan_launch_input would pass, the plan's shape and mode, its tiles,
+// and the dynamic LDS the body needs. Defined in eg_gemv.hip.
+struct PlanPhase {
+  int bits, encoding, mode, in_kind, team, cpl, u, nb;
+  uint32_t tiles, smem;
+};
+int plan_phase(eg_context* ctx, const eg_gemv_plan* plan, const eg_gemv_input* input, GemvArgs* args,
+               PlanPhase* phase);
 
 // The kernel for a fused input stage (in_kind RMSNORM, SILU_MUL or ATTENTION) of one
 // (format, mode, shape), or nullptr where none is instantiated.

@@ -26,10 +26,10 @@ struct eg_context {
   // This device's copy of the fixed scratch array of eg_lm_head_argmax_noalloc (resolved by
   // eg::noalloc_scratch_init at creation; shared by every context on the device).
   void* noalloc_scratch = nullptr;
-  // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth, chunk slots with
-  // x in LDS) from EG_GEMV_SHAPE="t,c,u[,d[,xl]]", read once at creation; zeros mean the
-  // built-in choice. For tuning sweeps.
-  int gemv_override[5] = {0, 0, 0, 0, 0};
+  // GEMV shape override (team, chunks per lane, rows per lane, pipeline depth) from
+  // EG_GEMV_SHAPE="t,c,u[,d]", read once at creation; zeros mean the built-in choice. For
+  // tuning sweeps.
+  int gemv_override[4] = {0, 0, 0, 0};
   // Tiles per wave for GEMVs with a fused input stage (EG_FUSED_TILES_PER_WAVE, default 1: every
   // workgroup recomputes the stage, but the decoder's launches measured faster with more,
   // shorter-lived workgroups than with two tiles per wave).
@@ -45,9 +45,6 @@ struct eg_context {
   // Groups of 4 waves per prefill GEMM workgroup, each on its own K blocks: 0 = chosen per
   // launch from the tile grid; EG_PREFILL_GROUPS=1, 2 or 4 forces one (for tuning sweeps).
   int prefill_groups = 0;
-  // Register stages of the prefill GEMM's staging pipeline, for tuning sweeps of the plain
-  // launch (EG_PREFILL_STAGES; 0 = the group count's default)
-  int prefill_stages = 0;
   // chunk attention's key split: at most this many 64-key tiles per workgroup, and a small grid
   // split up to this many workgroups per CU
   // the SwiGLU pair as one launch of paired gate|up tiles (false: gate | up, then silu_mul_rows)
@@ -61,6 +58,11 @@ struct eg_context {
   bool prefill_xcd = true;
   uint32_t attention_split_tiles = 8;
   uint32_t attention_split_fill = 1;
+  // the decode step's layers as one persistent launch where the shapes allow (EG_DECODE_PERSISTENT=1;
+  // off by default: one launch per op measured ~7% faster on MI355X)
+  bool decode_persistent = false;
+  uint32_t persistent_grid = 0;  // EG_PERSISTENT_GRID: workgroups of that launch (0: the default)
+  uint32_t persistent_poll = 1;  // EG_PERSISTENT_POLL: 64-clock sleeps between polls of a wait
   // Resident workgroups per CU of each kernel launched through this context (from
   // hipOccupancyMaxActiveBlocksPerMultiprocessor), so grids can be sized to one full wave of
   // the device.
@@ -73,6 +75,8 @@ struct eg_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 };
+
+struct eg_layers;  // the persistent decode layers of a decoder (eg_layers.hip)
 
 namespace eg {
 
@@ -121,6 +125,12 @@ struct StepTail {
   // then counts it in *status (nullable) and leaves the position, the history, the draw state
   // and the next step's input (embedding row, RoPE row) as they were, so the next step redoes it.
   uint32_t* status = nullptr;
+  // The persistent layers' abort flag (nullable): raised, the step's layers ran without waiting
+  // and the step failed as above. Either way the tail zeroes the flag and the arrival counters
+  // (sync_count words, sync_stride apart) for the next launch.
+  uint32_t* sync_abort = nullptr;
+  uint32_t* sync_counters = nullptr;
+  uint32_t sync_count = 0, sync_stride = 0;
   // the RoPE cos/sin of positions [0, rope_positions) (launch_rope_table); the next position's
   // row is copied from here (computed in the launch where it is NULL or the position is past it)
   const double2* rope_table = nullptr;
@@ -151,6 +161,12 @@ int launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32
 // caller that counts from out[0] itself).
 int launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
                          eg_sample_dims* params, uint32_t* rng, uint32_t* status);
+
+// The test hook's limit on the bounded waits of in-launch synchronisation (the sampler's grid
+// barriers, the persistent decode layers' phase waits): 0 = their default (about a second), else
+// limit + 1 polls. A word of the context's state, set by eg_test_sample_spin; kernels read it at
+// every wait, so captured graphs follow it too.
+inline uint32_t* wait_limit_word(eg_context* ctx) { return reinterpret_cast<uint32_t*>(state(ctx) + 2048 + 640); }
 
 // Reports, once, the standalone sampler launches that gave up since the last report: when the
 // context has run eg_sample, reads (after the stream has drained) and clears the count the
@@ -236,6 +252,33 @@ int embed_rows(eg_context* ctx, const uint32_t* ids, uint32_t rows, const uint32
 int rmsnorm_rows(eg_context* ctx, const float* x, const float* w, uint32_t rows, uint32_t n, float eps, float* out,
                  bool out_bf16 = false);
 int silu_mul_rows(eg_context* ctx, const float* x, uint32_t rows, uint32_t n, float* out, bool out_bf16 = false);
+
+// The decode step's layers as one persistent launch (eg_layers.hip). Per layer, the four GEMV
+// plans the per-op launches use (q|k|v, o, the gate|up pair, down) with their inputs; the
+// attention's buffers and dims. layers_create leaves *out NULL, with EG_OK, where the shapes or
+// the device's occupancy do not fit the persistent kernel (the per-op launches then run).
+struct LayerPlans {
+  const eg_gemv_plan* plan[4];
+  eg_gemv_input input[4];
+};
+struct LayersDesc {
+  uint32_t layers;
+  const LayerPlans* plans;
+  eg_attention_dims att;
+  const uint32_t* position;
+  const double* rope;
+  const float *q, *k, *v;
+  float* partials;
+  uint16_t *k_cache, *v_cache;
+  size_t layer_stride;  // cache elements per layer
+};
+int layers_create(eg_context* ctx, const LayersDesc& desc, eg_layers** out);
+int layers_launch(eg_context* ctx, eg_layers* layers);
+// The arrival counters (`count` words, `stride` words apart) and the abort flag, which the step
+// tail reads and zeroes after every launch.
+void layers_sync_words(const eg_layers* layers, uint32_t** counters, uint32_t* count, uint32_t* stride,
+                       uint32_t** abort);
+void layers_destroy(eg_context* ctx, eg_layers* layers);
 
 // Resolves the calling thread's current device's copy of the no-alloc scratch array
 // (hipGetSymbolAddress, once per device) into ctx->noalloc_scratch.
@@ -331,6 +374,27 @@ __device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 __device__ __forceinline__ void store_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset, float v, uint32_t soffset = 0) {
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, soffset, 0);
+}
+
+// The same accesses with an explicit cache policy: AUX = 0 is the default policy; AUX = kCoherent
+// (sc1) is the agent-scope coherent form egd::put / egd::get use, for data another workgroup of
+// the same launch writes or reads.
+constexpr int kCoherent = 16;
+template <int AUX>
+__device__ __forceinline__ u32x4 load_b128_p(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, AUX);
+}
+template <int AUX>
+__device__ __forceinline__ uint32_t load_b32_p(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, AUX);
+}
+template <int AUX>
+__device__ __forceinline__ float load_f32_p(__amdgpu_buffer_rsrc_t r, uint32_t offset, uint32_t soffset = 0) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, AUX));
+}
+template <int AUX>
+__device__ __forceinline__ void store_f32_p(__amdgpu_buffer_rsrc_t r, uint32_t offset, float v, uint32_t soffset = 0) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, soffset, AUX);
 }
 
 // Opaque AND: keeps the compiler from folding a nibble mask into per-element bitfield

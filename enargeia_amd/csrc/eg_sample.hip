@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const u
 // The count of eg_sample launches that gave up, and the test hook's poll limit, in the context's
 // state (zeroed at creation).
 uint32_t* standalone_status(eg_context* ctx) { return reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048 + 512); }
-uint32_t* spin_word(eg_context* ctx) { return reinterpret_cast<uint32_t*>(eg::state(ctx) + 2048 + 640); }
+uint32_t* spin_word(eg_context* ctx) { return eg::wait_limit_word(ctx); }
 
 Work workspace(eg_context* ctx, GridSync* gs) {
   Work w;

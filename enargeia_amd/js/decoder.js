@@ -72,23 +72,22 @@ class DecodeGraph {
     const b = native.decoderBuffers(this.handle);
     this.tokenId = borrowed(device, b.token, 4, 'decode/token_id');
     this.result = borrowed(device, b.token, 4, 'decode/result');
-    // The result is read with the decoder's status word (token[2]: sampled steps whose sampler
-    // gave up, which moved nothing), in the same copy; a failure is an Error, as the reference's
+    // The result is read with the decoder's status word (token[2]: steps that gave up, which moved
+    // nothing), in the same copy; a failure is an Error, as the reference's
     // kernel layer fails loudly (kernel.ts:97-107), and the word is cleared.
     this.result.buffer.read = (size) => {
       const bytes = native.bufRead(device.ctx, b.token, 0, 12);
       const words = new Uint32Array(bytes);
       if (words[2] !== 0) {
         native.bufWrite(device.ctx, b.token, 8, new Uint32Array([0]));
-        throw new Error(`decode: the sampler gave up on ${words[2]} step(s) (a grid barrier timed out: not every ` +
-                        'workgroup was resident at once); the position, history and draw state are as before');
+        throw new Error(`decode: ${words[2]} step(s) gave up: a bounded wait timed out (not every workgroup was ` +
+                        'resident at once); the position, history and draw state are as before');
       }
       return bytes.slice(0, size);
     };
     this.history = borrowed(device, b.history, desc.maxContext * 4, 'decode/history');
     this.logits = borrowed(device, b.logits, desc.vocab * 4, 'decode/logits');
     this.params = { temperature: 0, topP: 1, repetitionPenalty: 1 };
-    this.hostDriven = false;
   }
 
   /** graph_decode.ts:387 */
@@ -100,7 +99,6 @@ class DecodeGraph {
   /** graph_decode.ts:398-406: the per-token values of the next step (the one host write). */
   setPosition(position, historyLength, random) {
     native.decoderSetPosition(this.handle, position, historyLength, random);
-    this.hostDriven = true;
   }
 
   /** graph_decode.ts:442-448: one decode step, run at submit. */
@@ -117,21 +115,18 @@ class DecodeGraph {
   /** The prompt and its first token (ForwardGraph + sampleFromPrefill in one call); the draw is
    * the decoder's own mulberry32 stream, restarted by seed(). */
   prefill(position, prompt) {
-    this.hostDriven = false;  // eg_decoder_prefill returns the decoder to device-chained steps
     return native.decoderPrefill(this.handle, position, new Uint32Array(prompt));
   }
 
   seed(seed) {
     native.decoderSeed(this.handle, seed);
-    this.hostDriven = false;
   }
 
-  /** launches per step: 5 per layer, the LM head and the tail, the sampler's one launch when the
-   * parameters are not GREEDY, and the input preparation a host-driven step (setPosition) runs
-   * first */
+  /** launches per step (eg_decoder_launches): the layers (one persistent launch, or 5 per layer),
+   * the LM head and the tail, the sampler's one launch when the parameters are not GREEDY, and the
+   * input preparation a host-driven step (setPosition) runs first */
   get dispatchCount() {
-    const sampled = this.params.temperature > 0 || this.params.repetitionPenalty !== 1;
-    return 5 * this.config.layers + 2 + (sampled ? 1 : 0) + (this.hostDriven ? 1 : 0);
+    return native.decoderLaunches(this.handle);
   }
 
   destroy() {

@@ -665,6 +665,18 @@ napi_value DecoderSeed(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// decoderLaunches(dec) -> launches of the next step (eg_decoder_launches)
+napi_value DecoderLaunches(napi_env env, napi_callback_info info) {
+  Args a(env, info, "decoderLaunches", 1);
+  auto* h = live_decoder(env, a, "decoderLaunches");
+  if (!h || !a.ok) return nullptr;
+  uint32_t n = 0;
+  if (throw_status(env, h->ctx, eg_decoder_launches(h->dec, &n))) return nullptr;
+  napi_value v;
+  napi_create_uint32(env, n, &v);
+  return v;
+}
+
 // decoderSetPosition(dec, position, historyLength, random) (DecodeGraph.setPosition)
 napi_value DecoderSetPosition(napi_env env, napi_callback_info info) {
   Args a(env, info, "decoderSetPosition", 4);
@@ -987,6 +999,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"decoderBuffers", nullptr, DecoderBuffers, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderSetSampling", nullptr, DecoderSetSampling, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderSeed", nullptr, DecoderSeed, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decoderLaunches", nullptr, DecoderLaunches, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderSetPosition", nullptr, DecoderSetPosition, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderSetHistory", nullptr, DecoderSetHistory, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decoderPrefill", nullptr, DecoderPrefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

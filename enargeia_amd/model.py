@@ -282,6 +282,12 @@ class Decoder:
     def logits(self) -> np.ndarray:
         return self.device.read_array(self.buffers.logits, np.float32, self.model.cfg.vocab)
 
+    def launches(self) -> int:
+        """Launches one step of the current mode enqueues (eg_decoder_launches)."""
+        n = ctypes.c_uint32()
+        check(_lib.load().eg_decoder_launches(self.handle, ctypes.byref(n)), self.device.ctx)
+        return n.value
+
     def position(self) -> int:
         return int(self.device.read_array(self.buffers.position, np.uint32, 1)[0])
 

@@ -233,7 +233,8 @@ EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, ui
 /* Test hook, no counterpart in the reference: with override != 0 every later sampler launch on
  * this context (eg_sample and the decoder's sampled steps, replays of captured graphs included:
  * the limit lives in device memory) gives a barrier wait up after `polls` polls instead of about
- * a second, so the give-up path (out[0] = 0xFFFFFFFF and an error at the
+ * a second, and so does every phase wait of the decoder's persistent layers (with polls 0 such a
+ * wait gives up without polling: the step fails and moves nothing), so the give-up path (out[0] = 0xFFFFFFFF and an error at the
  * next blocking call, every workgroup leaving, the barrier words restored for the next launch)
  * can be forced from the host; override 0 restores the default. Not for production use. */
 EG_API int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls);
@@ -419,6 +420,11 @@ EG_API int eg_decoder_capture(eg_decoder* decoder);
 /* The sampling parameters of the following steps (DecodeGraph.setSampling, graph_decode.ts:387;
  * a new decoder is GREEDY). */
 EG_API int eg_decoder_set_sampling(eg_decoder* decoder, const eg_sampling_params* params);
+/* Launches one step of the current mode enqueues (DecodeGraph.dispatchCount's counterpart): the
+ * 24 layers as one persistent launch where the shapes and the device allow it (else 5 per layer),
+ * the LM head, the sampler unless the parameters are GREEDY, the tail, and the input preparation
+ * of a host-driven step. */
+EG_API int eg_decoder_launches(eg_decoder* decoder, uint32_t* per_step);
 /* Restarts the draw source: mulberry32(seed) (session.ts:75-83; a new decoder has the session's
  * default seed 0x5eed, :125), and returns the decoder to device-chained steps. */
 EG_API int eg_decoder_seed(eg_decoder* decoder, uint32_t seed);
