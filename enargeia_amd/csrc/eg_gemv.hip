@@ -82,8 +82,8 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
 
 // Instantiated (TEAM, CPL, U, NB) shapes: one chunk slot per lane for rows of up to 64 chunks
 // (TEAM the next power of two), a full-wave team with 2-4 slots for longer rows. The library
-// picks NB = 2 (measured fastest on MI355X: a deeper pipeline costs resident waves and
-// duplicate tail tiles); NB 3-4 variants of the main shapes stay selectable through
+// picks NB = 2 (a deeper pipeline costs resident waves and duplicate tail tiles) except for
+// the long walks of choose_shape; the other NB 3-4 variants stay selectable through
 // EG_GEMV_SHAPE for tuning.
 #define EG_SHAPES(X)                                                                                      \
   X(8, 1, 1, 2) X(8, 1, 2, 2) X(8, 1, 4, 2) X(16, 1, 1, 2) X(16, 1, 2, 2) X(16, 1, 4, 2) X(32, 1, 1, 2)    \
@@ -178,10 +178,13 @@ Shape choose_shape(uint32_t n, uint32_t chunks, const eg_context* ctx, uint32_t 
   if (rpw * sh.u > n) return Shape{};
   const uint32_t tile_rows = rpw * sh.u;
   sh.tiles = (n + tile_rows - 1) / tile_rows;
-  // Three-slot rows (K = 4864 int4: 152 chunks) over many tiles per wave stream best with three
-  // load buffers (measured, interleaved: the 24-matrix K = 4864 launch 14.1-14.3 against
-  // 14.8-15.0 us with two); launches with a fused input stage always take two.
-  if (!(ctx && ctx->gemv_override[0]) && sh.cpl == 3 && sh.u == 1 && sh.tiles > 16u * (ctx ? (uint32_t)ctx->cu_count : 256u))
+  // Over many tiles per wave, three-slot rows (K = 4864 int4: 152 chunks) and two-row 32-lane
+  // tiles (K = 896 int4) stream best with three load buffers (measured, interleaved: the
+  // 24-matrix K = 4864 launch 13.9 us against 15.1 with two and 14.2 with four; the K = 896 one
+  // 26.8 against 27.5 with two); launches with a fused input stage always take two.
+  const bool long_walk = sh.tiles > 16u * (ctx ? (uint32_t)ctx->cu_count : 256u);
+  if (!(ctx && ctx->gemv_override[0]) && long_walk &&
+      ((sh.cpl == 3 && sh.u == 1) || (sh.team == 32 && sh.cpl == 1 && sh.u == 2)))
     sh.nb = 3;
   return sh;
 }
