@@ -180,6 +180,8 @@ def main() -> int:
         dev.close()
         return 0
     if args.decode_timeline:
+        from enargeia_amd import _lib
+        _lib.use_profiling_build()  # the stamps live in the profiling build only
         dev = K.Device(0)
         print(json.dumps(decode_timeline(dev, args)), flush=True)
         dev.close()

@@ -11,6 +11,8 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libenargeia_hip.so")
+# the profiling build (per-wave launch stamps compiled in: eg_test_launch_stamps records)
+PROF_LIB_PATH = os.path.join(HERE, "libenargeia_hip_prof.so")
 
 EG_OK = 0
 EG_ERR_INVALID = -1
@@ -108,6 +110,15 @@ class EgRangeError(EgError, IndexError):
 
 
 _lib: ctypes.CDLL | None = None
+
+
+def use_profiling_build() -> None:
+    """Load the profiling build (launch stamps compiled in) instead of the product library; only
+    before the library is first loaded in this process."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != PROF_LIB_PATH:
+        raise RuntimeError("use_profiling_build: the product library is already loaded in this process")
+    LIB_PATH = PROF_LIB_PATH
 
 
 def load() -> ctypes.CDLL:

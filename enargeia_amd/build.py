@@ -20,6 +20,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_PATH = os.path.join(HERE, "libenargeia_hip.so")
+# The profiling build: the same sources with EG_LAUNCH_STAMPS, whose kernels can record per-wave
+# wall-clock stamps (eg_test_launch_stamps; bench.py --decode-timeline loads it). The product
+# library carries no stamp code: compiled in, even unused, it slows every kernel.
+PROF_LIB_PATH = os.path.join(HERE, "libenargeia_hip_prof.so")
 NAPI_SRC = os.path.join(HERE, "js", "eg_napi.cc")
 NAPI_PATH = os.path.join(HERE, "js", "eg_napi.node")
 NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
@@ -47,9 +51,12 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    extra = FILE_FLAGS.get(os.path.basename(src), [])
+def _compile(job: tuple[str, bool]) -> str:
+    src, prof = job
+    obj_dir = os.path.join(BUILD_DIR, "prof" if prof else "prod")
+    os.makedirs(obj_dir, exist_ok=True)
+    obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
+    extra = FILE_FLAGS.get(os.path.basename(src), []) + (["-DEG_LAUNCH_STAMPS"] if prof else [])
     cmd = [HIPCC, *HIP_FLAGS, *extra, "-I", os.path.join(ROOT, "include"), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -58,19 +65,22 @@ def _compile(src: str) -> str:
 
 
 def build(verbose: bool = True) -> str:
+    """Both libraries: the product (LIB_PATH) and the profiling build (PROF_LIB_PATH)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sources()
-    workers = min(len(srcs), max(1, (os.cpu_count() or 4) // 2), 8)
+    jobs = [(src, prof) for prof in (False, True) for src in srcs]
+    workers = min(len(jobs), max(1, (os.cpu_count() or 4) // 2), 8)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+        objs = list(pool.map(_compile, jobs))
+    for path, group in ((LIB_PATH, objs[:len(srcs)]), (PROF_LIB_PATH, objs[len(srcs):])):
+        tmp = path + ".tmp"
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *group]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stderr}")
+        os.replace(tmp, path)
+        if verbose:
+            print(f"built {path} from {len(srcs)} sources", file=sys.stderr)
     build_napi(verbose)
     return LIB_PATH
 

@@ -236,6 +236,10 @@ int eg_buf_zero(eg_context* ctx, void* dst, size_t offset, size_t bytes) {
 int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t launches, uint32_t* recorded) {
   if (!ctx) return fail(nullptr, EG_ERR_INVALID, "test_launch_stamps: ctx is NULL");
   if (ctx->capturing) return fail(ctx, EG_ERR_STATE, "test_launch_stamps: a graph capture is in progress");
+  if (!egd::kLaunchStamps && buffer)
+    return fail(ctx, EG_ERR_STATE,
+                "test_launch_stamps: this library is built without launch stamps; the profiling build "
+                "(libenargeia_hip_prof.so, EG_LAUNCH_STAMPS) records them");
   if (recorded) *recorded = ctx->stamp_next;
   ctx->stamps = buffer;
   ctx->stamp_capacity = buffer ? launches : 0u;

@@ -114,7 +114,7 @@ __device__ void wait_for(const Persist& p, uint32_t phase) {
       }
       for (uint32_t i = 0; i < p.poll_sleep; i++) __builtin_amdgcn_s_sleep(1);
     }
-    if (p.phases) {
+    if (egd::kLaunchStamps && p.phases) {
       const uint64_t now = wall_clock64();
       uint64_t* at = p.phases + 4 * (phase + 1);
       __hip_atomic_fetch_max(at, ~now, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -130,7 +130,7 @@ __device__ __forceinline__ void publish(const Persist& p, uint32_t phase) {
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(counter_of(p, phase, blockIdx.x % kGroups), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (p.phases)
+    if (egd::kLaunchStamps && p.phases)
       __hip_atomic_fetch_max(p.phases + 4 * phase + 2, (uint64_t)wall_clock64(), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -312,7 +312,7 @@ int eg::layers_launch(eg_context* ctx, eg_layers* L) {
   Persist p = L->args;
   p.stamp = eg::stamp_slot(ctx);
   // the per-phase stamps after the waves' own (kMaxGrid workgroups of 4 waves take 4096 words)
-  p.phases = p.stamp ? p.stamp + eg::kStampWaves : nullptr;
+  p.phases = egd::kLaunchStamps && p.stamp ? p.stamp + eg::kStampWaves : nullptr;
   hipLaunchKernelGGL(L->kernel, dim3(L->grid), dim3(256), L->smem, ctx->stream, L->table, p);
   return eg::check_launch(ctx, "decode_layers");
 }

@@ -247,7 +247,9 @@ EG_API int eg_test_sample_spin(eg_context* ctx, int override, uint32_t polls);
  * writes the same slots - stores per-wave wall-clock stamps (s_memrealtime, 100 MHz): wave w of
  * launch i at buffer[2 * (8192 * i + w)] (entry) and [... + 1] (exit), for w < 8192. *recorded
  * (nullable) receives the number of launches that took a slot since the previous call; NULL
- * turns the stamps off. Not for production use. */
+ * turns the stamps off. Only the profiling build of the library (libenargeia_hip_prof.so,
+ * compiled with EG_LAUNCH_STAMPS) records stamps; the production build returns EG_ERR_STATE for
+ * a non-NULL buffer, its kernels carrying no stamp code. Not for production use. */
 EG_API int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t launches, uint32_t* recorded);
 
 /* ---- decode step: embedding, attention, fused GEMV inputs ----------------------------------- */

@@ -42,6 +42,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.eg_abi_version() == 1
 
 
+def test_profiling_build_exports_the_same_symbols():
+    # libenargeia_hip_prof.so: the same sources with the launch stamps compiled in
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.PROF_LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if " T " in ln and ln.split()[-1].startswith("eg_")})
+    assert exported == declared_symbols()
+    assert b"gfx950" in open(_lib.PROF_LIB_PATH, "rb").read()
+
+
 def test_library_is_gfx950_code():
     # The device code object inside the library targets gfx950.
     data = open(_lib.LIB_PATH, "rb").read()

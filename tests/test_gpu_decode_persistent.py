@@ -35,19 +35,9 @@ def persistent_device():
 
 
 def launches_per_step(device, dec):
-    """Launches one captured step takes (eg_test_launch_stamps counts the launches that take a slot)."""
-    lib = _lib.load()
-    buf = device.buffer(256 * 8192 * 16)
-    try:
-        device.zero(buf, 256 * 8192 * 16)
-        _lib.check(lib.eg_test_launch_stamps(device.ctx, K._vp(buf.ptr), 256, None), device.ctx)
-        dec.capture()
-        import ctypes
-        rec = ctypes.c_uint32()
-        _lib.check(lib.eg_test_launch_stamps(device.ctx, None, 0, ctypes.byref(rec)), device.ctx)
-        return rec.value
-    finally:
-        buf.release()
+    """Launches one captured step takes (eg_decoder_launches), after capturing it."""
+    dec.capture()
+    return dec.launches()
 
 
 def run(device, model, cfg, prompt, steps, sampling, graph, fill=None, start=0):
@@ -142,3 +132,16 @@ def test_persistent_wait_give_up_fails_the_step_and_the_next_redoes_it(persisten
         dec.close()
         ref.close()
         dm.release()
+
+
+def test_production_build_records_no_launch_stamps(device):
+    """The product library carries no stamp code (it slows every kernel even switched off): its
+    eg_test_launch_stamps refuses a buffer with EG_ERR_STATE, naming the profiling build."""
+    lib = _lib.load()
+    buf = device.buffer(8192 * 16)
+    try:
+        with pytest.raises(_lib.EgError, match="profiling build"):
+            _lib.check(lib.eg_test_launch_stamps(device.ctx, K._vp(buf.ptr), 1, None), device.ctx)
+        _lib.check(lib.eg_test_launch_stamps(device.ctx, None, 0, None), device.ctx)  # off: accepted
+    finally:
+        buf.release()
