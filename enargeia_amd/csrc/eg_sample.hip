@@ -14,7 +14,8 @@
 // MI355X design. The reference makes ~36 passes over the vocabulary inside one workgroup. Here
 // the vocabulary is split over G workgroups (2048 ids each, G = 75 at 151,936 ids) that are all
 // resident at once, and the whole sample is ONE launch whose phases are separated by grid
-// barriers (a central counter with a generation word; every wait bounded; what workgroups hand
+// barriers (an arrival counter that only grows during the launch and a generation word; every
+// wait bounded; what workgroups hand
 // each other moves through device-coherent accesses, so a barrier only drains stores and needs
 // no cache write-back or invalidate): each workgroup loads its slice's logits once and keeps
 // them - and later their probabilities - in registers through every phase:
@@ -158,15 +159,19 @@ __device__ __forceinline__ double get_f64(const double* p) {
 }
 
 // Central barrier over the launch's workgroups: thread 0 of each counts the workgroup once its
-// waves have drained their stores; the last to arrive resets the count and, once that store
-// has completed, advances the generation, which the others poll. Polls are bounded: past `spin`,
-// or when another workgroup has given up, the abort flag is raised and false is returned to
-// every thread.
+// waves have drained their stores. The count only grows during a launch (the last workgroup to
+// leave zeroes it), so the launch's barrier b is complete at (b + 1) x groups arrivals; the
+// arrival that completes it finds that in its own atomic's result and advances the generation
+// word - which only grows, launch after launch - to gen0 + b + 1, gen0 being the value every
+// workgroup read at the launch's start; the others poll the generation (a line of its own: polls
+// of the counter itself slow the arrivals, measured). On the way through, a workgroup makes one
+// atomic round trip, and the last arrival one store. Polls are bounded: past `spin`, or when
+// another workgroup has given up, the abort flag is raised and false is returned to every thread.
 constexpr uint32_t kSpin = 1u << 20;  // polls of ~1 us: a barrier gives up after about a second
 
 struct GridSync {
-  uint32_t* count;  // arrivals at the current barrier (0 between barriers)
-  uint32_t* gen;    // advanced once per completed barrier
+  uint32_t* count;  // arrivals since the launch began (zero between launches)
+  uint32_t* gen;    // advanced once per completed barrier, never reset
   uint32_t* abort;  // set by a timed-out wait
   uint32_t* exits;  // workgroups done with every barrier of the current launch
   uint32_t* status; // +1 per launch that gave up (nullable: the caller counts from out[0])
@@ -175,25 +180,28 @@ struct GridSync {
   const uint32_t* spin;
 };
 
-__device__ bool grid_barrier(const GridSync& g, uint32_t groups) {
+// `passed` counts the barriers this workgroup has passed in the launch (the same at every thread);
+// `gen0` is the generation thread 0 read at the launch's start (the barrier's drain completes that
+// read before the first arrival).
+__device__ bool grid_barrier(const GridSync& g, uint32_t groups, uint32_t& passed, uint32_t gen0) {
   __shared__ uint32_t ok;
   drain();
   __syncthreads();
+  passed++;
   if (threadIdx.x == 0) {
     bool good = true;
-    const uint32_t gen0 = get(g.gen);
-    drain();  // the generation read before this workgroup can complete the barrier
-    const uint32_t arrived = __hip_atomic_fetch_add(g.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (arrived == groups - 1) {
-      put(g.count, 0u);
-      drain();
-      put(g.gen, gen0 + 1u);
+    const uint32_t target = passed * groups, release = gen0 + passed;
+    const uint32_t w = get(g.spin);  // in flight beside the arrival
+    const uint32_t arrived = __hip_atomic_fetch_add(g.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (arrived == target) {
+      put(g.gen, release);
     } else {
-      const uint32_t w = get(g.spin);
       const uint32_t spin = w ? w - 1u : kSpin;
       uint32_t n = 0;
-      while (get(g.gen) == gen0) {
-        if (get(g.abort) != 0u || ++n > spin) {
+      for (;;) {
+        const uint32_t c = get(g.gen), stop = get(g.abort);  // one round trip for both
+        if ((int32_t)(c - release) >= 0) break;
+        if (stop != 0u || ++n > spin) {
           good = false;
           break;
         }
@@ -242,6 +250,8 @@ __device__ void leave(const GridSync& g, uint32_t groups, uint32_t* out) {
 __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* history, uint32_t* out, SampleParams hp,
                                               SampleParams* dp, const Work& w, const GridSync& gs, uint32_t* rng) {
   const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
+  uint32_t passed = 0;  // grid barriers passed
+  const uint32_t gen0 = tid == 0 ? get(gs.gen) : 0u;  // the generation before this launch's barriers
   if (g == 0 && tid == 0) {
     // The give-up result, replaced by the token once one is found. Both are stored coherently
     // (out[0] is written by two workgroups, possibly on different XCDs), and this one completes
@@ -269,14 +279,26 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       for (int e = 0; e < 4; e++) v[r + e] = first + r + e < p.vocab ? logits[first + r + e] : 0.f;
     }
   }
-  if (p.repetition_penalty != 1.0f) {
+  const bool penalize = p.repetition_penalty != 1.0f;
+  // the first kHistory x 256 history ids, read beside the logits (one round trip for both)
+  constexpr uint32_t kHistory = 4;
+  uint32_t hv[kHistory];
+#pragma unroll
+  for (uint32_t r = 0; r < kHistory; r++) {
+    const uint32_t h = tid + r * kThreads;
+    hv[r] = penalize && h < p.history_length ? history[h] : 0xFFFFFFFFu;
+  }
+  if (penalize) {
     // The penalty applies once per distinct history id (the reference applies it at an id's
     // first occurrence only): mark the ids this slice owns, then penalize each marked element
     // once, in registers and in place in memory.
     __shared__ uint8_t hit[kSlice];
     for (uint32_t i = tid; i < kSlice; i += kThreads) hit[i] = 0;
     __syncthreads();
-    for (uint32_t h = tid; h < p.history_length; h += kThreads) {
+#pragma unroll
+    for (uint32_t r = 0; r < kHistory; r++)
+      if (hv[r] >= base && hv[r] < end) hit[hv[r] - base] = 1;
+    for (uint32_t h = tid + kHistory * kThreads; h < p.history_length; h += kThreads) {
       const uint32_t id = history[h];
       if (id >= base && id < end) hit[id - base] = 1;
     }
@@ -325,7 +347,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
   // before any level adds to them
   if (g == 0)
     for (int i = tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
-  if (!grid_barrier(gs, G)) return;  // out[0] keeps the give-up result
+  if (!grid_barrier(gs, G, passed, gen0)) return;  // out[0] keeps the give-up result
   if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
   float mx;
   uint32_t amax;
@@ -437,7 +459,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
         put(&w.above_count[g], above_n);
         put(&w.cand_count[g], cand_n);
       }
-      if (!grid_barrier(gs, G)) return;
+      if (!grid_barrier(gs, G, passed, gen0)) return;
       if (last) {
         // every group's figures for the kept masses below (loaded here, beside the bins)
         last_done = true;
@@ -529,7 +551,7 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       put(&w.kept_part[g], (uint64_t)kept);
       put(&w.count_part[g], count);
     }
-    if (!grid_barrier(gs, G)) return;
+    if (!grid_barrier(gs, G, passed, gen0)) return;
     if (tid < G) {
       gk = get(&w.kept_part[tid]);
       gc = get(&w.count_part[tid]);
