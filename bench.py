@@ -375,7 +375,11 @@ def main() -> int:
                                    "note": "the head GEMV launch alone (logits stored, no argmax): the decode-shape "
                                            "int8 GEMV; `us` above adds the argmax finalize launch"},
                     "sampled_token_us": round(sampled_us, 2),
-                    "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history"},
+                    "sampled_token_fused_us": round(hn["sampled_fused_us"], 2),
+                    "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history: "
+                                      "sampled_token_us through the reference's two ops (lm_head_q8, sample), "
+                                      "sampled_token_fused_us through eg_lm_head_sample (the head hands the "
+                                      "sampler its per-workgroup max and normaliser partials)"},
         "per_gemv_us": per_gemv,
         "prefill": prefill,
         "decode_tok_s_2048": decode["tok_s"] if decode else None,
@@ -473,6 +477,24 @@ def head_numbers(dev, ev, stream, args, rng) -> dict:
     sampled_us = float(np.median([ev.ms(ss2[i], ss2[i + 1]) for i in range(args.steps)])) * 1e3
     log(f"lm_head+sample (T 0.7, top-p 0.9, penalty 1.1): {sampled_us:.1f} us")
 
+    # the same sampled token through eg_lm_head_sample: the head applies the penalty and hands the
+    # sampler its per-workgroup (max, index, normaliser) partials (the decoder's sampled steps)
+    def fused_token(i):
+        K.lm_head_sample(dev, h, heads[i % 3][0], heads[i % 3][1], None, logits, hist, tok, dims,
+                         K.sample_dims(VOCAB, 512, K.SamplingParams(0.7, 0.9, 1.1), (i * 0.618) % 1.0), 8,
+                         K.ENC_SIGNED)
+
+    for i in range(args.warmup):
+        fused_token(i)
+    ss4 = [ev.create() for _ in range(args.steps + 1)]
+    ev.record(ss4[0], stream)
+    for i in range(args.steps):
+        fused_token(i)
+        ev.record(ss4[i + 1], stream)
+    ev.sync(ss4[-1])
+    fused_us = float(np.median([ev.ms(ss4[i], ss4[i + 1]) for i in range(args.steps)])) * 1e3
+    log(f"lm_head_sample, one call (same parameters): {fused_us:.1f} us")
+
     # the head GEMV alone (the reference's lm_head_q8 binding: logits stored, no argmax)
     def plain_head(i):
         hu = head_k.uniform()
@@ -492,7 +514,7 @@ def head_numbers(dev, ev, stream, args, rng) -> dict:
     for a, b in heads:
         a.release()
         b.release()
-    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us, "gemv_us": plain_us}
+    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us, "sampled_fused_us": fused_us, "gemv_us": plain_us}
 
 
 def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:

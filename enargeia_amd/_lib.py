@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "eg_gemv_plan_destroy": (_i, [_vp, _vp]),
     "eg_argmax": (_i, [_vp, _vp, _vp, _vp]),
     "eg_sample": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "eg_lm_head_sample": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
     "eg_test_sample_spin": (_i, [_vp, ctypes.c_int, ctypes.c_uint32]),
     "eg_test_launch_stamps": (_i, [_vp, _vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
     "eg_embed_gather": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),

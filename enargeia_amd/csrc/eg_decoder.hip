@@ -13,9 +13,10 @@
 // the position and prepares the next step: the new token's embedding row (layer 0's input) and
 // the RoPE cos/sin of the next position (read by every attention launch instead of computed
 // there). Greedy steps (GREEDY, sample.ts:33) take the LM head's fused argmax partials, which the
-// tail reduces; other sampling parameters store the logits and run the sampler (penalty,
-// temperature, top-p, draw; sample.wgsl) between the head and the tail, the decoder's sample
-// step (graph_decode.ts:382-385). Every per-token value (token id, position, the sampler's
+// tail reduces; other sampling parameters run the sampler (penalty, temperature, top-p, draw;
+// sample.wgsl) between the head and the tail, the decoder's sample step
+// (graph_decode.ts:382-385) - an int8 head stores the penalized logits and hands the sampler
+// per-workgroup (max, index, normaliser) partials, so the sampler starts at its radix levels. Every per-token value (token id, position, the sampler's
 // parameters, its history and the mulberry32 draw state) lives in device memory, so one captured
 // hipGraph replays every step with no host work per launch.
 #include <algorithm>
@@ -51,7 +52,7 @@ struct eg_decoder {
   eg_sample_dims* sp = nullptr;      // {vocab, history_length, temperature, top_p, penalty, random}
   uint32_t* rng = nullptr;           // [1]: mulberry32 state, one draw per step
   eg_sampling_params sampling{0.f, 1.f, 1.f};  // host copy of sp's parameters
-  eg_gemv_plan* head_plan = nullptr; // the LM head storing logits for the sampler (vocab % 8 == 0)
+  eg_gemv_plan* head_plan = nullptr; // an int4 LM head storing logits for the sampler (vocab % 8 == 0)
   // Host-driven steps (DecodeGraph.setPosition, graph_decode.ts:398-406): the host writes the
   // position, the history length and the draw before each step, and each step starts from the
   // token in `token` (its embedding and RoPE table prepared first), as the reference's Session
@@ -237,6 +238,18 @@ int run_head(eg_decoder* d, bool sampled, const float* hidden) {
                                           m.embed_bits, &t.groups)) != EG_OK)
       return st;
     t.partials = reinterpret_cast<const uint32_t*>(eg::partials(ctx));
+    t.rng = rng;
+    return tail(d, t);
+  }
+  if (m.embed_bits == 8) {
+    // the int8 head applies the penalty and leaves the sampler its per-workgroup (max, index,
+    // normaliser) partials; the sampler takes the draw, the tail advances the state once the
+    // step has its token; a sampler that gives up leaves 0xFFFFFFFF, which the tail counts in
+    // token[2], changing nothing
+    eg_embedding_dims hd = embedding_dims_of(m);
+    if ((st = eg::lm_head_sample_device(ctx, &in, e.packed, e.scales, e.zeros, d->logits, &hd, m.embed_encoding,
+                                        m.embed_bits, d->history, d->token, d->sp, rng, nullptr)) != EG_OK)
+      return st;
     t.rng = rng;
     return tail(d, t);
   }
@@ -524,10 +537,10 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     if (st != EG_OK) break;
     d->plans.push_back(plan);
   }
-  // the LM head storing logits for the sampler: a one-matrix plan with the final norm as its
+  // an int4 LM head storing logits for the sampler: a one-matrix plan with the final norm as its
   // input stage (plans need rows in multiples of 8; other vocabularies use the fused-argmax head
-  // and ignore its partials)
-  if (st == EG_OK && m.vocab % 8 == 0) {
+  // and ignore its partials; an int8 head leaves the sampler its partials instead)
+  if (st == EG_OK && m.vocab % 8 == 0 && m.embed_bits != 8) {
     eg_gemv_segment head[1] = {{m.embedding.packed, m.embedding.scales, m.embedding.zeros, nullptr, d->logits, m.vocab, 0}};
     st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
   }

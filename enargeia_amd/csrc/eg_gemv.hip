@@ -100,8 +100,22 @@ KernelFn pick(int team, int cpl, int u, int nb) {
   return nullptr;
 }
 
+// kSampleStats (int8 heads): the shapes at pipeline depth 2
+template <int ENC>
+KernelFn pick_stats(int team, int cpl, int u, int nb) {
+#define EG_CASE(T, P, UU, D)                                 \
+  if constexpr (D == 2)                                      \
+    if (team == T && cpl == P && u == UU && nb == D)         \
+      return gemv_kernel<8, ENC, T, P, UU, D, kSampleStats, EG_INPUT_VECTOR>;
+  EG_SHAPES(EG_CASE)
+#undef EG_CASE
+  return nullptr;
+}
+
 template <int BITS, int ENC>
 KernelFn pick_mode(int mode, int team, int cpl, int u, int nb) {
+  if constexpr (BITS == 8)
+    if (mode == kSampleStats) return pick_stats<ENC>(team, cpl, u, nb);
   if (mode == kArgmax) return pick<BITS, ENC, kArgmax>(team, cpl, u, nb);
   if (mode == kArgmaxOnly) return pick<BITS, ENC, kArgmaxOnly>(team, cpl, u, nb);
   if (mode == kBatched) return pick<BITS, ENC, kBatched>(team, cpl, u, nb);
@@ -204,6 +218,13 @@ struct QuantView {
   uint32_t* groups_out = nullptr;  // fused argmax: skip the finalize, report the partials' count here
   uint32_t* partials = nullptr;    // fused argmax: where the partials go (NULL: the context workspace)
   size_t partials_bytes = 0;       // its size
+  // the sampling statistics (kSampleStats, with `result` and `groups_out`): the parameters from
+  // device memory (sample_dev) or as given (sample_host), and the history the penalty reads
+  const eg_sample_dims* sample_dev = nullptr;
+  const eg_sample_dims* sample_host = nullptr;
+  const uint32_t* history = nullptr;
+  uint32_t* clear = nullptr;  // zeroed by workgroup 0 (clear_words words)
+  uint32_t clear_words = 0;
 };
 
 // LDS the input stage needs beyond x and the segment table.
@@ -282,10 +303,11 @@ int launch(eg_context* ctx, const QuantView& v) {
   int st = validate(ctx, v);
   if (st != EG_OK) return st;
   if (v.n == 0) {
-    if (v.result) return eg::fail(ctx, EG_ERR_INVALID, "%s: argmax over zero rows", v.op);
+    if (v.result || v.sample_dev || v.sample_host) return eg::fail(ctx, EG_ERR_INVALID, "%s: argmax over zero rows", v.op);
     return EG_OK;
   }
-  const bool argmax = v.result != nullptr;
+  const bool stats = v.sample_dev || v.sample_host;
+  const bool argmax = v.result != nullptr || stats;
   const uint32_t epc = 128u / v.bits;
   const bool fused = v.input && v.input->kind != EG_INPUT_VECTOR;
   const bool aligned = (reinterpret_cast<uintptr_t>(v.packed) & 15u) == 0 &&
@@ -296,23 +318,28 @@ int launch(eg_context* ctx, const QuantView& v) {
     shape = choose_shape(v.n, chunks, ctx);
   uint32_t* partials = v.partials ? v.partials : reinterpret_cast<uint32_t*>(eg::partials(ctx));
   const size_t partials_cap = v.partials ? v.partials_bytes : eg::kPartialsBytes;
-  // one (value bits, index) partial per workgroup, checked before anything is launched
+  // one (value bits, index) partial per workgroup - (value, index, float64 sum) for the sampling
+  // statistics - checked before anything is launched
   auto partials_fit = [&](uint64_t groups) {
-    return !argmax || groups * 8 <= partials_cap ? EG_OK
+    return !argmax || groups * (stats ? 16 : 8) <= partials_cap ? EG_OK
                                                  : eg::fail(ctx, EG_ERR_RANGE,
                                                             "%s: %llu workgroups' partials exceed the %zu-byte buffer",
                                                             v.op, (unsigned long long)groups, partials_cap);
   };
   uint32_t grid = 0;
-  const int mode = argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
+  const int mode = stats ? kSampleStats : argmax ? (v.out ? kArgmax : kArgmaxOnly) : kPlain;
   const int in_kind = v.input ? v.input->kind : EG_INPUT_VECTOR;
   KernelFn fn = shape.team ? pick_kernel(v.bits, v.encoding, mode, shape.team, shape.cpl, shape.u,
-                                         in_kind != EG_INPUT_VECTOR ? 2 : shape.nb, in_kind)
+                                         in_kind != EG_INPUT_VECTOR || stats ? 2 : shape.nb, in_kind)
                            : nullptr;
   if (fused && !fn)
     return eg::fail(ctx, EG_ERR_INVALID,
                     "%s: no kernel for this shape with a fused input stage (k and the block must be multiples of %u)",
                     v.op, epc);
+  if (stats && (!fn || !v.out || !v.groups_out))
+    return eg::fail(ctx, EG_ERR_INVALID,
+                    "%s: the sampling statistics need an int8 head whose k and block are multiples of %u", v.op,
+                    epc);
   if (fn) {
     GemvArgs a{};
     a.x = v.x;
@@ -335,6 +362,22 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.any_bias = v.bias != nullptr;
     const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
+    if (stats) {
+      // every workgroup's rows, and the up to TILE - 1 rows a shifted last tile recomputes below
+      // them, within the kernel's per-workgroup record (kStatsRows)
+      const uint32_t tile_rows = (64u / shape.team) * shape.u;
+      const uint32_t tiles_per_group = (kStatsRows - tile_rows) / tile_rows;
+      grid = std::max<uint32_t>(grid, (shape.tiles + tiles_per_group - 1) / tiles_per_group);
+      a.sample_dev = v.sample_dev;
+      if (v.sample_host) {
+        a.temperature = v.sample_host->temperature;
+        a.repetition_penalty = v.sample_host->repetition_penalty;
+        a.history_length = v.sample_host->history_length;
+      }
+      a.history = v.history;
+      a.clear = v.clear;
+      a.clear_words = v.clear ? v.clear_words : 0u;
+    }
     if ((st = partials_fit(grid)) != EG_OK) return st;
     a.stamp = eg::stamp_slot(ctx);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, ctx->stream, a);
@@ -468,6 +511,25 @@ int eg::lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, con
   QuantView v{"lm_head_argmax", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
               dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
               bits, partials, input, groups};
+  return launch(ctx, v);
+}
+
+int eg::lm_head_sample_partials(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed,
+                                const float* scales, const uint32_t* zeros, float* out, const eg_embedding_dims* dims,
+                                int encoding, int bits, const eg_sample_dims* sample_dev,
+                                const eg_sample_dims* sample_host, const uint32_t* history, uint32_t* partials,
+                                size_t partials_bytes, uint32_t* clear, uint32_t clear_words, uint32_t* groups) {
+  if (!dims || !input || !groups || !out || (!sample_dev && !sample_host))
+    return eg::fail(ctx, EG_ERR_INVALID, "lm_head_sample: NULL argument");
+  if (bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_sample: an int8 head (bits 8), not %d", bits);
+  QuantView v{"lm_head_sample", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
+              dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
+              bits, nullptr, input, groups, partials, partials ? partials_bytes : 0};
+  v.sample_dev = sample_dev;
+  v.sample_host = sample_host;
+  v.history = history;
+  v.clear = clear;
+  v.clear_words = clear_words;
   return launch(ctx, v);
 }
 

@@ -88,6 +88,15 @@ struct GemvArgs {
   float eps;
   uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
   uint64_t* stamp;         // launch stamps (egd::WaveStamp), nullable
+  // kSampleStats: the sampling parameters - from device memory (sample_dev, the 32-byte sample
+  // dims, so a captured graph replays with new values) or, when that is NULL, these - and the
+  // history the penalty reads
+  const eg_sample_dims* sample_dev;
+  float temperature, repetition_penalty;
+  uint32_t history_length;
+  const uint32_t* history;
+  uint32_t* clear;  // kSampleStats: workgroup 0 zeroes clear[0, clear_words) (nullable)
+  uint32_t clear_words;
 };
 
 template <int BITS>
@@ -183,8 +192,16 @@ struct Codes<8> {
 // matrices that share x and K. kSwiGLU: two matrices of equal shape (gate, up; the argument
 // table's first two entries) whose row r is computed by the same team, which stores
 // silu(gate_r) * up_r (ops.ts:207-216) - so the SiLU is evaluated once per row, in the
-// producer, instead of by every workgroup of the down projection's input stage.
-enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3, kSwiGLU = 4 };
+// producer, instead of by every workgroup of the down projection's input stage. kSampleStats:
+// the LM head ahead of the sampler (sample.wgsl:143-236 up to its normaliser) - each row's logit
+// penalized (once per distinct history id: v > 0 ? v / penalty : v * penalty) and stored, and a
+// per-workgroup partial (max of l/T, its lowest index, sum of exp(l/T - that max) in float64;
+// l itself and no sum at temperature <= 0) in place of the sampler's per-slice pass.
+enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3, kSwiGLU = 4, kSampleStats = 5 };
+
+// kSampleStats: rows of a workgroup's record (one per thread of the epilogue; the host sizes the
+// grid so that every workgroup's rows fit).
+constexpr uint32_t kStatsRows = 256;
 
 template <int BITS, int U, int CPL>
 struct Loads {
@@ -444,8 +461,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   constexpr bool kPair = MODE == kSwiGLU;
   static_assert(!kPair || U == 2, "a SwiGLU tile pairs one gate row with one up row");
   constexpr int TILE = kPair ? RPW : RPW * U;
-  constexpr bool kStore = MODE != kArgmaxOnly;
+  constexpr bool kStats = MODE == kSampleStats;
+  constexpr bool kStore = MODE != kArgmaxOnly && !kStats;
   constexpr bool kBest = MODE == kArgmax || MODE == kArgmaxOnly;
+  static_assert(!kStats || (!Env::kPhase && MODE != kBatched), "the sampling statistics are a launch of their own");
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t t = lane % TEAM;
   const uint32_t slot = lane / TEAM;
@@ -643,6 +662,48 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   float best_v = -1.0e30f;
   uint32_t best_i = a.out_offset;
 
+  // kSampleStats: the tile loop only records each row's logit in stats_x, for the workgroup's
+  // nominal rows [stats_lo, stats_hi) - its tiles' rows before a last partial tile's shift back;
+  // the rows that tile recomputes below stats_lo belong to the workgroup before and are left to
+  // it - and the epilogue does the rest, one row per thread: the penalty (`hit`: the history ids
+  // among the rows), the store, l/T and the partial.
+  // The parameters (device memory or the arguments) and the first kStatsHistory x 256 history
+  // ids are read before the input stage, so their round trips overlap its own and the first
+  // tiles' weights.
+  static_assert(!kStats || kStatsRows == kWaves * 64, "the epilogue takes one row per thread");
+  constexpr uint32_t kStatsHistory = 4;
+  __shared__ float stats_x[kStats ? kStatsRows : 1];
+  __shared__ uint32_t hit[kStats ? kStatsRows / 32 : 1];
+  uint32_t stats_lo = 0, stats_hi = 0, hist_len = 0;
+  float temp = 0.0f, pen = 1.0f;
+  uint32_t hv[kStats ? kStatsHistory : 1];
+  if constexpr (kStats) {
+    // (wave-uniform values pinned to scalar registers, as begin and end below)
+    stats_lo = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(((uint64_t)a.total_passes * (env.block() * kWaves)) / total_waves) * TILE);
+    stats_hi = __builtin_amdgcn_readfirstlane(
+        min((uint32_t)(((uint64_t)a.total_passes * ((env.block() + 1) * kWaves)) / total_waves) * TILE, a.n));
+    temp = a.temperature;
+    pen = a.repetition_penalty;
+    hist_len = a.history_length;
+    if (a.sample_dev) {
+      temp = a.sample_dev->temperature;
+      pen = a.sample_dev->repetition_penalty;
+      hist_len = a.sample_dev->history_length;
+    }
+    temp = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, temp)));
+    pen = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, pen)));
+    hist_len = __builtin_amdgcn_readfirstlane(hist_len);
+#pragma unroll
+    for (uint32_t r = 0; r < kStatsHistory; r++) {
+      const uint32_t h = threadIdx.x + r * blockDim.x;
+      hv[r] = pen != 1.0f && a.history && h < hist_len ? a.history[h] : 0xFFFFFFFFu;
+    }
+    for (uint32_t i = threadIdx.x; i < kStatsRows / 32; i += blockDim.x) hit[i] = 0u;
+    if (a.clear && env.block() == 0)
+      for (uint32_t i = threadIdx.x; i < a.clear_words; i += blockDim.x) a.clear[i] = 0u;
+  }
+
   auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
     float pair[2];  // kSwiGLU: the gate and up totals of the team's row
 #pragma unroll
@@ -663,10 +724,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
         }
         acc = fmaf(L.s[u][j], C::template dot<ENC>(q, xr[j]) - z * sx[j], acc);
       }
-      const float v = egd::team_allsum<TEAM>(acc);
+      float v = egd::team_allsum<TEAM>(acc);
       if (kPair) {
         pair[u & 1] = v;
         continue;
+      }
+      if constexpr (kStats) {
+        const uint32_t rel = row - stats_lo;  // a shifted tile's rows below stats_lo wrap: left out
+        if (rel < kStatsRows && t == 0) stats_x[rel] = v;
       }
       if (kStore) egd::store_f32_p<AUX>(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
       if (kBest) {
@@ -715,6 +780,20 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   }
   __syncthreads();
   load_x();
+  if constexpr (kStats) {
+    // the history ids among the workgroup's rows (the penalty's set: each id once); the epilogue's
+    // barrier orders these marks before their reads
+#pragma unroll
+    for (uint32_t r = 0; r < kStatsHistory; r++) {
+      const uint32_t rel = hv[r] - stats_lo;
+      if (rel < stats_hi - stats_lo) atomicOr(&hit[rel >> 5], 1u << (rel & 31u));
+    }
+    if (pen != 1.0f && a.history)
+      for (uint32_t h = threadIdx.x + kStatsHistory * blockDim.x; h < hist_len; h += blockDim.x) {
+        const uint32_t rel = a.history[h] - stats_lo;
+        if (rel < stats_hi - stats_lo) atomicOr(&hit[rel >> 5], 1u << (rel & 31u));
+      }
+  }
   const uint32_t count = end - begin;
   const uint32_t groups = count / NB;
   uint32_t tile = begin;
@@ -739,6 +818,51 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   // they complete before the wave ends.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
 
+  if constexpr (kStats) {
+    // The epilogue, thread i on row stats_lo + i.
+    __syncthreads();  // the record and the marks complete
+    const uint32_t i = threadIdx.x, row = stats_lo + i;
+    const bool valid = row < stats_hi;
+    float v = valid ? stats_x[i] : 0.0f;
+    if (valid && ((hit[i >> 5] >> (i & 31u)) & 1u)) v = v > 0.0f ? v / pen : v * pen;
+    if (valid) a.out[a.out_offset + row] = v;
+    const float x = temp > 0.0f ? v / temp : v;  // what the argmax ranks: l/T, or l when greedy
+    float bv = valid ? x : -1.0e30f;
+    uint32_t bi = valid ? a.out_offset + row : a.out_offset;
+    __shared__ float wv[kWaves];
+    __shared__ uint32_t wi[kWaves];
+    egd::team_argmax<64>(bv, bi);
+    if (lane == 0) {
+      wv[threadIdx.x >> 6] = bv;
+      wi[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    bv = wv[0];
+    bi = wi[0];
+    for (int k = 1; k < kWaves; k++)
+      if (egd::better(wv[k], wi[k], bv, bi)) {
+        bv = wv[k];
+        bi = wi[k];
+      }
+    // sum of exp(l/T - the workgroup's max) over its rows in float64 (the sampler's per-slice
+    // statement, sample.wgsl:230-236, over this workgroup's rows)
+    __shared__ double ws[kWaves];
+    double e = valid && temp > 0.0f ? (double)expf(x - bv) : 0.0;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) e += __shfl_xor(e, m, 64);
+    if (lane == 0) ws[threadIdx.x >> 6] = e;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double sum = 0.0;
+      for (int k = 0; k < kWaves; k++) sum += ws[k];
+      const uint64_t sb = __builtin_bit_cast(uint64_t, sum);
+      a.partials[4 * env.block() + 0] = __float_as_uint(bv);
+      a.partials[4 * env.block() + 1] = bi;
+      a.partials[4 * env.block() + 2] = (uint32_t)sb;
+      a.partials[4 * env.block() + 3] = (uint32_t)(sb >> 32);
+    }
+  }
+
   if (kBest) {
     __shared__ float wv[kWaves];
     __shared__ uint32_t wi[kWaves];
@@ -762,6 +886,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   }
 }
 
+// (kSampleStats kernels take 90-105 VGPRs, four waves per SIMD against the plain head's six;
+// held to six waves they spill around the tile loop, and the config-2 head took 39 us instead of
+// ~27. Measured on MI355X.)
 template <int BITS, int ENC, int TEAM, int CPL, int U, int NB, int MODE, int IN>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const egd::WaveStamp stamp(a.stamp);
@@ -805,6 +932,8 @@ KernelFn pick_fused_mode(int mode, int team, int cpl, int u) {
   if (mode == kArgmaxOnly) return pick_fused_shape<IN, BITS, ENC, kArgmaxOnly>(team, cpl, u);
   if constexpr (IN == EG_INPUT_RMSNORM && BITS == 4)  // the int4 gate|up pair after the post-attention norm
     if (mode == kSwiGLU) return pick_fused_shape<IN, BITS, ENC, kSwiGLU>(team, cpl, u);
+  if constexpr (IN == EG_INPUT_RMSNORM && BITS == 8)  // the int8 LM head after the final norm, ahead of the sampler
+    if (mode == kSampleStats) return pick_fused_shape<IN, BITS, ENC, kSampleStats>(team, cpl, u);
   return nullptr;
 }
 

@@ -110,6 +110,19 @@ int lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, const u
                             const float* scales, const uint32_t* zeros, float* out, const eg_embedding_dims* dims,
                             int encoding, int bits, uint32_t* groups);
 
+// The int8 LM head ahead of the sampler (kSampleStats): each logit penalized and stored in `out`,
+// and per workgroup (max of l/T, its lowest index, float64 sum of exp(l/T - that max)) - 16 bytes,
+// (value bits, index, sum) - left in `partials` (NULL: the workspace), their count in *groups.
+// The parameters come from device memory (sample_dev, so a captured graph follows them) or, when
+// that is NULL, from sample_host; the penalty reads `history` (the first history_length ids).
+// Workgroup 0 also zeroes clear[0, clear_words) (the sampler's level-0 bins, which the launch after
+// this one sums into with no barrier first; NULL: nothing).
+int lm_head_sample_partials(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed, const float* scales,
+                            const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding, int bits,
+                            const eg_sample_dims* sample_dev, const eg_sample_dims* sample_host,
+                            const uint32_t* history, uint32_t* partials, size_t partials_bytes, uint32_t* clear,
+                            uint32_t clear_words, uint32_t* groups);
+
 // What a decode step's tail does before it prepares the next step (see launch_step_tail).
 struct StepTail {
   bool advance = false;                 // false: a reset (token[0] and position[0] as written)
@@ -161,6 +174,17 @@ int launch_step_tail(eg_context* ctx, const StepTail& t, uint32_t* token, uint32
 // caller that counts from out[0] itself).
 int launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
                          eg_sample_dims* params, uint32_t* rng, uint32_t* status);
+
+// The int8 LM head and the sampler as one sampled token, the parameters in DEVICE memory as for
+// launch_sample_device (vocab = dims->row_count, out_offset 0): the head applies the penalty to
+// the logits it stores in `logits` and leaves per-workgroup partials (max of l/T, its index, the
+// float64 sum of exp(l/T - that max)), from which the sampler takes the global max, its index and
+// the normaliser instead of its own penalty pass, slice maxima and first grid barrier. Same token
+// semantics, give-up behaviour and status counting as launch_sample_device.
+int lm_head_sample_device(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed, const float* scales,
+                          const uint32_t* zeros, float* logits, const eg_embedding_dims* dims, int encoding, int bits,
+                          const uint32_t* history, uint32_t* out, eg_sample_dims* params, uint32_t* rng,
+                          uint32_t* status);
 
 // The test hook's limit on the bounded waits of in-launch synchronisation (the sampler's grid
 // barriers, the persistent decode layers' phase waits): 0 = their default (about a second), else

@@ -69,6 +69,9 @@ struct SampleParams {
 static_assert(sizeof(SampleParams) == 32, "sample dims are 32 bytes");
 
 constexpr uint32_t kCand = 32;  // candidates of the last radix level kept per group
+constexpr uint32_t kMaxHeadGroups = 2048;                 // LM-head partials a launch reduces
+constexpr uint32_t kHeadPer = kMaxHeadGroups / kThreads;  // per thread
+constexpr size_t kHeadPartialsOffset = 1u << 20;          // in the workspace, past the sampler's own data
 
 struct Work {
   uint32_t* max_part;     // 2 u32 per group
@@ -247,8 +250,11 @@ __device__ void leave(const GridSync& g, uint32_t groups, uint32_t* out) {
 // Thread t of workgroup g owns ids g * kSlice + t * kPerThread + [0, kPerThread): thread order is
 // id order, which the final scan relies on.
 // Every return is taken by a whole workgroup at once.
+// `head` (nullable): the LM head's per-workgroup partials (eg::lm_head_sample_partials), head_groups
+// of them, which replace the penalty and the slices' first pass.
 __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* history, uint32_t* out, SampleParams hp,
-                                              SampleParams* dp, const Work& w, const GridSync& gs, uint32_t* rng) {
+                                              SampleParams* dp, const Work& w, const GridSync& gs, uint32_t* rng,
+                                              const uint4* head, uint32_t head_groups) {
   const uint32_t G = gridDim.x, g = blockIdx.x, tid = threadIdx.x;
   uint32_t passed = 0;  // grid barriers passed
   const uint32_t gen0 = tid == 0 ? get(gs.gen) : 0u;  // the generation before this launch's barriers
@@ -279,91 +285,36 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       for (int e = 0; e < 4; e++) v[r + e] = first + r + e < p.vocab ? logits[first + r + e] : 0.f;
     }
   }
-  const bool penalize = p.repetition_penalty != 1.0f;
-  // the first kHistory x 256 history ids, read beside the logits (one round trip for both)
-  constexpr uint32_t kHistory = 4;
-  uint32_t hv[kHistory];
-#pragma unroll
-  for (uint32_t r = 0; r < kHistory; r++) {
-    const uint32_t h = tid + r * kThreads;
-    hv[r] = penalize && h < p.history_length ? history[h] : 0xFFFFFFFFu;
-  }
-  if (penalize) {
-    // The penalty applies once per distinct history id (the reference applies it at an id's
-    // first occurrence only): mark the ids this slice owns, then penalize each marked element
-    // once, in registers and in place in memory.
-    __shared__ uint8_t hit[kSlice];
-    for (uint32_t i = tid; i < kSlice; i += kThreads) hit[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (uint32_t r = 0; r < kHistory; r++)
-      if (hv[r] >= base && hv[r] < end) hit[hv[r] - base] = 1;
-    for (uint32_t h = tid + kHistory * kThreads; h < p.history_length; h += kThreads) {
-      const uint32_t id = history[h];
-      if (id >= base && id < end) hit[id - base] = 1;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kPerThread; r++) {
-      const uint32_t i = first + r;
-      if (i < end && hit[i - base]) {
-        v[r] = v[r] > 0.0f ? v[r] / p.repetition_penalty : v[r] * p.repetition_penalty;
-        logits[i] = v[r];
-      }
-    }
-  }
   const bool greedy = p.temperature <= 0.0f;
-  {
-    // the slice's (max, argmax) of l/T (of l when greedy) and its sum of exp(l/T - that max)
-    __shared__ float sv[kWaves];
-    __shared__ uint32_t si[kWaves];
-    __shared__ double scratch[kWaves];
-    float bv = -1.0e30f;
-    uint32_t bi = greedy ? 0u : base;
-#pragma unroll
-    for (int r = 0; r < kPerThread; r++) {
-      const uint32_t i = first + r;
-      const float x = greedy ? v[r] : v[r] / p.temperature;
-      if (i < end && egd::better(x, i, bv, bi)) {
-        bv = x;
-        bi = i;
-      }
-    }
-    block_argmax(bv, bi, sv, si);
-    double s = 0.0;
-    if (!greedy) {
-#pragma unroll
-      for (int r = 0; r < kPerThread; r++)
-        if (first + r < end) s += (double)expf(v[r] / p.temperature - bv);
-      s = block_sum(s, scratch);
-    }
-    if (tid == 0) {
-      put(&w.max_part[2 * g], __float_as_uint(bv));
-      put(&w.max_part[2 * g + 1], bi);
-      put_f64(&w.sum_part[g], s);
-    }
-  }
-  // the level bins are summed with atomics: cleared here, before the barrier that orders them
-  // before any level adds to them
-  if (g == 0)
-    for (int i = tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
-  if (!grid_barrier(gs, G, passed, gen0)) return;  // out[0] keeps the give-up result
-  if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
   float mx;
   uint32_t amax;
   float total;
-  {
+  if (head) {
+    // The LM head applied the penalty and left per-workgroup partials (max of l/T - of l when
+    // greedy - its lowest index, float64 sum of exp(l/T - that max)): the global max, its index
+    // and the normaliser come from them, with no pass over the slice and no barrier first.
+    // Level 0's bins were zeroed by the head launch; the other levels' are cleared here, before
+    // workgroup 0's first arrival, which orders them before any of their adds.
+    if (g == 0)
+      for (int i = kBins + tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
+    if (rng && dp) p.random = egd::mulberry32_peek(*rng);  // the draw workgroup 0 records
     __shared__ float sv[kWaves];
     __shared__ uint32_t si[kWaves];
     __shared__ double scratch[kWaves];
-    float bv = -1.0e30f, mg = -1.0e30f;
-    uint32_t bi = 0;
-    double sg = 0.0;
-    if (tid < G) {
-      bv = mg = __uint_as_float(get(&w.max_part[2 * tid]));
-      bi = get(&w.max_part[2 * tid + 1]);
-      sg = get_f64(&w.sum_part[tid]);
+    uint4 hq[kHeadPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kHeadPer; r++) {
+      const uint32_t i = tid + r * kThreads;
+      hq[r] = i < head_groups ? head[i] : make_uint4(0u, 0u, 0u, 0u);
     }
+    float bv = -1.0e30f;
+    uint32_t bi = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kHeadPer; r++)
+      if (tid + r * kThreads < head_groups && egd::better(__uint_as_float(hq[r].x), hq[r].y, bv, bi)) {
+        bv = __uint_as_float(hq[r].x);
+        bi = hq[r].y;
+      }
     block_argmax(bv, bi, sv, si);
     mx = bv;
     amax = bi;
@@ -371,8 +322,105 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
       if (g == 0 && tid == 0) put(out, amax);
       return;
     }
-    // the normaliser: every slice's sum rescaled from its own max to the global one
-    total = (float)block_sum(tid < G ? sg * exp((double)mg - (double)mx) : 0.0, scratch);
+    double s = 0.0;
+#pragma unroll
+    for (uint32_t r = 0; r < kHeadPer; r++)
+      if (tid + r * kThreads < head_groups)
+        s += __builtin_bit_cast(double, (uint64_t)hq[r].z | ((uint64_t)hq[r].w << 32)) *
+             exp((double)__uint_as_float(hq[r].x) - (double)mx);
+    total = (float)block_sum(s, scratch);
+  } else {
+    const bool penalize = p.repetition_penalty != 1.0f;
+    // the first kHistory x 256 history ids, read beside the logits (one round trip for both)
+    constexpr uint32_t kHistory = 4;
+    uint32_t hv[kHistory];
+#pragma unroll
+    for (uint32_t r = 0; r < kHistory; r++) {
+      const uint32_t h = tid + r * kThreads;
+      hv[r] = penalize && h < p.history_length ? history[h] : 0xFFFFFFFFu;
+    }
+    if (penalize) {
+      // The penalty applies once per distinct history id (the reference applies it at an id's
+      // first occurrence only): mark the ids this slice owns, then penalize each marked element
+      // once, in registers and in place in memory.
+      __shared__ uint8_t hit[kSlice];
+      for (uint32_t i = tid; i < kSlice; i += kThreads) hit[i] = 0;
+      __syncthreads();
+#pragma unroll
+      for (uint32_t r = 0; r < kHistory; r++)
+        if (hv[r] >= base && hv[r] < end) hit[hv[r] - base] = 1;
+      for (uint32_t h = tid + kHistory * kThreads; h < p.history_length; h += kThreads) {
+        const uint32_t id = history[h];
+        if (id >= base && id < end) hit[id - base] = 1;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < kPerThread; r++) {
+        const uint32_t i = first + r;
+        if (i < end && hit[i - base]) {
+          v[r] = v[r] > 0.0f ? v[r] / p.repetition_penalty : v[r] * p.repetition_penalty;
+          logits[i] = v[r];
+        }
+      }
+    }
+    {
+      // the slice's (max, argmax) of l/T (of l when greedy) and its sum of exp(l/T - that max)
+      __shared__ float sv[kWaves];
+      __shared__ uint32_t si[kWaves];
+      __shared__ double scratch[kWaves];
+      float bv = -1.0e30f;
+      uint32_t bi = greedy ? 0u : base;
+#pragma unroll
+      for (int r = 0; r < kPerThread; r++) {
+        const uint32_t i = first + r;
+        const float x = greedy ? v[r] : v[r] / p.temperature;
+        if (i < end && egd::better(x, i, bv, bi)) {
+          bv = x;
+          bi = i;
+        }
+      }
+      block_argmax(bv, bi, sv, si);
+      double s = 0.0;
+      if (!greedy) {
+#pragma unroll
+        for (int r = 0; r < kPerThread; r++)
+          if (first + r < end) s += (double)expf(v[r] / p.temperature - bv);
+        s = block_sum(s, scratch);
+      }
+      if (tid == 0) {
+        put(&w.max_part[2 * g], __float_as_uint(bv));
+        put(&w.max_part[2 * g + 1], bi);
+        put_f64(&w.sum_part[g], s);
+      }
+    }
+    // the level bins are summed with atomics: cleared here, before the barrier that orders them
+    // before any level adds to them
+    if (g == 0)
+      for (int i = tid; i < kLevels * kBins; i += kThreads) put(&w.bins[i], 0ull);
+    if (!grid_barrier(gs, G, passed, gen0)) return;  // out[0] keeps the give-up result
+    if (dp) p.random = __hip_atomic_load(&dp->random, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // this call's draw
+    {
+      __shared__ float sv[kWaves];
+      __shared__ uint32_t si[kWaves];
+      __shared__ double scratch[kWaves];
+      float bv = -1.0e30f, mg = -1.0e30f;
+      uint32_t bi = 0;
+      double sg = 0.0;
+      if (tid < G) {
+        bv = mg = __uint_as_float(get(&w.max_part[2 * tid]));
+        bi = get(&w.max_part[2 * tid + 1]);
+        sg = get_f64(&w.sum_part[tid]);
+      }
+      block_argmax(bv, bi, sv, si);
+      mx = bv;
+      amax = bi;
+      if (greedy) {
+        if (g == 0 && tid == 0) put(out, amax);
+        return;
+      }
+      // the normaliser: every slice's sum rescaled from its own max to the global one
+      total = (float)block_sum(tid < G ? sg * exp((double)mg - (double)mx) : 0.0, scratch);
+    }
   }
   // p = exp(l/T - max) / total in registers; ids past the vocabulary get -1 (never kept)
 #pragma unroll
@@ -599,9 +647,10 @@ __device__ __forceinline__ void sample_phases(float* logits, const uint32_t* his
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(float* logits, const uint32_t* history, uint32_t* out,
                                                           SampleParams hp, SampleParams* dp, Work w, GridSync gs,
-                                                          uint32_t* rng, uint64_t* stamp_slot) {
+                                                          uint32_t* rng, const uint4* head, uint32_t head_groups,
+                                                          uint64_t* stamp_slot) {
   const egd::WaveStamp stamp(stamp_slot);
-  sample_phases(logits, history, out, hp, dp, w, gs, rng);
+  sample_phases(logits, history, out, hp, dp, w, gs, rng, head, head_groups);
   leave(gs, gridDim.x, out);
 }
 
@@ -646,7 +695,7 @@ Work workspace(eg_context* ctx, GridSync* gs) {
 // 256 threads and ~12 KB of LDS each fit an MI355X); a device that cannot hold them (fewer CUs,
 // a partition) is refused here rather than left to the bounded waits.
 int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, const SampleParams& hp,
-           SampleParams* dp, uint32_t* rng, uint32_t* status) {
+           SampleParams* dp, uint32_t* rng, uint32_t* status, const uint4* head = nullptr, uint32_t head_groups = 0) {
   const uint32_t groups = (hp.vocab + kSlice - 1) / kSlice;
   const int per_cu = eg::occupancy_of(ctx, reinterpret_cast<const void*>(sample_kernel));
   if (per_cu > 0 && (uint64_t)per_cu * (uint64_t)ctx->cu_count < groups)
@@ -658,11 +707,50 @@ int launch(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* ou
   gs.status = status;
   gs.spin = spin_word(ctx);
   hipLaunchKernelGGL(sample_kernel, dim3(groups), dim3(kThreads), 0, ctx->stream, logits, history, out, hp, dp, w, gs,
-                     rng, eg::stamp_slot(ctx));
+                     rng, head, head_groups, eg::stamp_slot(ctx));
   return eg::check_launch(ctx, "sample");
 }
 
+// The int8 LM head ahead of the sampler (eg::lm_head_sample_partials: penalty, logits, per-
+// workgroup partials), then the sampler on its partials. The partials go past the sampler's own
+// data in the workspace, and the head launch zeroes the sampler's level-0 bins, which the
+// sampler then sums into with no barrier first.
+int head_then_sample(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed, const float* scales,
+                     const uint32_t* zeros, float* logits, const eg_embedding_dims* dims, int encoding, int bits,
+                     const uint32_t* history, uint32_t* out, const SampleParams& hp, SampleParams* dp, uint32_t* rng,
+                     uint32_t* status) {
+  static_assert((size_t)kMaxGroups * (44 + kCand * 8) + (size_t)kLevels * kBins * 8 <= kHeadPartialsOffset &&
+                    kHeadPartialsOffset + (size_t)kMaxHeadGroups * 16 <= eg::kPartialsBytes,
+                "the LM head's partials sit past the sampler's data, inside the workspace");
+  GridSync gs;
+  Work w = workspace(ctx, &gs);
+  uint32_t* parts = reinterpret_cast<uint32_t*>(eg::partials(ctx) + kHeadPartialsOffset);
+  uint32_t groups = 0;
+  int st = eg::lm_head_sample_partials(ctx, input, packed, scales, zeros, logits, dims, encoding, bits,
+                                       reinterpret_cast<const eg_sample_dims*>(dp),
+                                       dp ? nullptr : reinterpret_cast<const eg_sample_dims*>(&hp), history, parts,
+                                       (size_t)kMaxHeadGroups * 16, reinterpret_cast<uint32_t*>(w.bins), kBins * 2,
+                                       &groups);
+  if (st != EG_OK) return st;
+  return launch(ctx, logits, history, out, hp, dp, rng, status, reinterpret_cast<const uint4*>(parts), groups);
+}
+
 }  // namespace
+
+int eg::lm_head_sample_device(eg_context* ctx, const eg_gemv_input* input, const uint32_t* packed, const float* scales,
+                              const uint32_t* zeros, float* logits, const eg_embedding_dims* dims, int encoding,
+                              int bits, const uint32_t* history, uint32_t* out, eg_sample_dims* params, uint32_t* rng,
+                              uint32_t* status) {
+  if (!logits || !out || !params || !dims) return eg::fail(ctx, EG_ERR_INVALID, "lm_head_sample: NULL argument");
+  const uint32_t vocab = dims->row_count;
+  if (vocab == 0 || (vocab + kSlice - 1) / kSlice > kMaxGroups || dims->out_offset != 0)
+    return eg::fail(ctx, EG_ERR_RANGE, "lm_head_sample: vocab %u (offset %u) outside the sampler's range (1..%u)",
+                    vocab, dims->out_offset, kMaxGroups * kSlice);
+  SampleParams hp{};
+  hp.vocab = vocab;
+  return head_then_sample(ctx, input, packed, scales, zeros, logits, dims, encoding, bits, history, out, hp,
+                          reinterpret_cast<SampleParams*>(params), rng, status);
+}
 
 int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out, uint32_t vocab,
                              eg_sample_dims* params, uint32_t* rng, uint32_t* status) {
@@ -674,6 +762,31 @@ int eg::launch_sample_device(eg_context* ctx, float* logits, const uint32_t* his
   SampleParams hp{};
   hp.vocab = vocab;
   return launch(ctx, logits, history, out, hp, reinterpret_cast<SampleParams*>(params), rng, status);
+}
+
+extern "C" int eg_lm_head_sample(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                                 const uint32_t* zeros, float* out, const uint32_t* history, uint32_t* token,
+                                 const eg_embedding_dims* dims, int encoding, int bits, const eg_sample_dims* sample) {
+  const char* op = "lm_head_sample";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!x || !out || !token || !dims || !sample) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if (sample->history_length > 0 && !history)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: historyLength %u with no history buffer", op, sample->history_length);
+  if (sample->vocab != dims->row_count || dims->out_offset != 0)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: sample vocab %u must equal the head's rows %u at offset 0", op,
+                    sample->vocab, dims->row_count);
+  if (sample->vocab == 0 || (sample->vocab + kSlice - 1) / kSlice > kMaxGroups)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: vocab %u outside the sampler's range (1..%u)", op, sample->vocab,
+                    kMaxGroups * kSlice);
+  SampleParams hp;
+  std::memcpy(&hp, sample, sizeof(hp));
+  eg_gemv_input in{};
+  in.kind = EG_INPUT_VECTOR;
+  in.x = x;
+  const int st = head_then_sample(ctx, &in, packed, scales, zeros, out, dims, encoding, bits, history, token, hp,
+                                  nullptr, nullptr, standalone_status(ctx));
+  if (st == EG_OK) ctx->sample_used = true;
+  return st;
 }
 
 int eg::report_sample_failures(eg_context* ctx, const char* op) {

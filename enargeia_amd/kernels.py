@@ -425,11 +425,24 @@ def lm_head_argmax(device: Device, x, packed, scales, zeros, out, result, dims: 
                                         encoding, bits), device.ctx)
 
 
+def lm_head_sample(device: Device, x, packed, scales, zeros, logits, history, token, dims: bytes,
+                   sample: bytes, bits: int = 8, encoding: int = ENC_OFFSET_ZEROS) -> None:
+    """The int8 LM head and the sampler as one sampled token (no reference op; the reference runs
+    lm_head_q8 then sample, graph_decode.ts:363-385; see include/enargeia_hip.h). `dims` are the
+    head's embedding dims, `sample` the sample dims (sample_dims); token[0] gets the id and
+    `logits` the penalized logits, as eg_sample leaves them."""
+    d = EmbeddingDims.from_buffer_copy(dims)
+    sd = SampleDims.from_buffer_copy(sample)
+    check(_lib.load().eg_lm_head_sample(device.ctx, _vp(_ptr(x)), _vp(_ptr(packed)), _vp(_ptr(scales)),
+                                        _vp(_ptr(zeros)), _vp(_ptr(logits)), _vp(_ptr(history)), _vp(_ptr(token)),
+                                        ctypes.byref(d), encoding, bits, ctypes.byref(sd)), device.ctx)
+
+
 __all__ = [
     "ARGMAX", "ARGMAX_WORKGROUPS", "Binding", "Buffer", "ComputeKernel", "Device", "ENC_OFFSET_ZEROS",
     "ENC_SIGNED", "EgError", "EgRangeError", "GREEDY", "GemvPlan", "GemvSegment", "Graph", "KernelSpec", "MATMUL_Q4_DECODE",
     "MATMUL_Q4_PREFILL", "MAX_WORKGROUPS_PER_DIMENSION", "SAMPLE", "SAMPLE_WORKGROUPS", "SamplingParams",
     "argmax_dims", "coverage", "decode_grid_width", "embedding_dims", "embedding_head_spec",
-    "embedding_head_workgroups", "lm_head_argmax", "matmul_q4_decode_workgroups", "matmul_q4_dims",
+    "embedding_head_workgroups", "lm_head_argmax", "lm_head_sample", "matmul_q4_decode_workgroups", "matmul_q4_dims",
     "matmul_q4_prefill_workgroups", "sample_dims", "with_format",
 ]

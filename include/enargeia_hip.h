@@ -230,6 +230,19 @@ EG_API int eg_argmax(eg_context* ctx, const float* logits, uint32_t* out, const 
 EG_API int eg_sample(eg_context* ctx, float* logits, const uint32_t* history, uint32_t* out,
               const eg_sample_dims* dims);
 
+/* The int8 LM head and the sampler as one sampled token: no counterpart op in the reference,
+ * which runs lm_head_q8 then sample (graph_decode.ts:363-385). Arguments as eg_lm_head (bits 8;
+ * out = the logits, dims->out_offset 0) and eg_sample (history, token = its out, sample->vocab =
+ * dims->row_count). The head applies the repetition penalty to each logit it computes and stores
+ * it as eg_sample leaves it, and hands the sampler per-workgroup partials (max of l/T, its lowest
+ * index, the float64 sum of exp(l/T - that max)) in place of the sampler's own penalty pass,
+ * slice maxima, normaliser and first grid barrier; the draw, its semantics, limits and give-up
+ * behaviour are eg_sample's. The normaliser's float64 sum is grouped by the head's workgroups
+ * rather than the sampler's slices, so it can differ from eg_sample's in the last bits. */
+EG_API int eg_lm_head_sample(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
+                             const uint32_t* zeros, float* out, const uint32_t* history, uint32_t* token,
+                             const eg_embedding_dims* dims, int encoding, int bits, const eg_sample_dims* sample);
+
 /* Test hook, no counterpart in the reference: with override != 0 every later sampler launch on
  * this context (eg_sample and the decoder's sampled steps, replays of captured graphs included:
  * the limit lives in device memory) gives a barrier wait up after `polls` polls instead of about
