@@ -360,7 +360,7 @@ int launch(eg_context* ctx, const QuantView& v) {
     a.seg_count = 0;
     a.total_passes = shape.tiles;
     a.any_bias = v.bias != nullptr;
-    const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a);
+    const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a) + (stats ? kStatsLdsBytes : 0u);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
     if (stats) {
       // every workgroup's rows, and the up to TILE - 1 rows a shifted last tile recomputes below

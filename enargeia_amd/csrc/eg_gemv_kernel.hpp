@@ -200,8 +200,12 @@ struct Codes<8> {
 enum Mode { kPlain = 0, kArgmax = 1, kBatched = 2, kArgmaxOnly = 3, kSwiGLU = 4, kSampleStats = 5 };
 
 // kSampleStats: rows of a workgroup's record (one per thread of the epilogue; the host sizes the
-// grid so that every workgroup's rows fit).
+// grid so that every workgroup's rows fit), and the dynamic LDS the mode adds after x: the record,
+// the history bitmap, and the epilogue's (value, index) and float64 slots per wave. (In dynamic
+// LDS rather than __shared__ arrays: any static LDS makes the compiler plan these kernels for
+// fewer waves, and the int8 head took 99 VGPRs instead of 75.)
 constexpr uint32_t kStatsRows = 256;
+constexpr uint32_t kStatsLdsBytes = kStatsRows * 4 + kStatsRows / 32 * 4 + 4 * 8 + 4 * 8;
 
 template <int BITS, int U, int CPL>
 struct Loads {
@@ -671,9 +675,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
   // ids are read before the input stage, so their round trips overlap its own and the first
   // tiles' weights.
   static_assert(!kStats || kStatsRows == kWaves * 64, "the epilogue takes one row per thread");
+  static_assert(kStatsLdsBytes == kStatsRows * 4 + kStatsRows / 32 * 4 + kWaves * 8 + kWaves * 8, "stats LDS");
   constexpr uint32_t kStatsHistory = 4;
-  __shared__ float stats_x[kStats ? kStatsRows : 1];
-  __shared__ uint32_t hit[kStats ? kStatsRows / 32 : 1];
+  float* const stats_x = scratch;  // the mode takes no input stage with scratch of its own
+  uint32_t* const hit = reinterpret_cast<uint32_t*>(stats_x + kStatsRows);
   uint32_t stats_lo = 0, stats_hi = 0, hist_len = 0;
   float temp = 0.0f, pen = 1.0f;
   uint32_t hv[kStats ? kStatsHistory : 1];
@@ -706,6 +711,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
 
   auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
     float pair[2];  // kSwiGLU: the gate and up totals of the team's row
+    float rec[U];   // kSampleStats: the tile's row values (lane t < U of each team records row t)
 #pragma unroll
     for (int u = 0; u < U; u++) {
       // The bias starts lane u's partial (linearQ4 starts its sum from the bias too; zero
@@ -729,10 +735,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
         pair[u & 1] = v;
         continue;
       }
-      if constexpr (kStats) {
-        const uint32_t rel = row - stats_lo;  // a shifted tile's rows below stats_lo wrap: left out
-        if (rel < kStatsRows && t == 0) stats_x[rel] = v;
-      }
+      if constexpr (kStats) rec[u] = v;
       if (kStore) egd::store_f32_p<AUX>(P.o, roff[u], v, (P.row0 + P.out_offset) * 4u);
       if (kBest) {
         const uint32_t idx = row + P.out_offset;
@@ -740,6 +743,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
         best_v = take ? v : best_v;
         best_i = take ? idx : best_i;
       }
+    }
+    if constexpr (kStats) {
+      // one LDS write per tile: lane t < U of each team records its team's row t (a shifted
+      // tile's rows below stats_lo wrap and are left out)
+      float mine = rec[0];
+#pragma unroll
+      for (int u = 1; u < U; u++) mine = t == (uint32_t)u ? rec[u] : mine;
+      const uint32_t rel = P.row0 + (t < (uint32_t)U ? t : 0u) * RPW + slot - stats_lo;
+      if (t < (uint32_t)U && rel < kStatsRows) stats_x[rel] = mine;
     }
     if (kPair) {
       const float g = pair[0];
@@ -829,8 +841,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
     const float x = temp > 0.0f ? v / temp : v;  // what the argmax ranks: l/T, or l when greedy
     float bv = valid ? x : -1.0e30f;
     uint32_t bi = valid ? a.out_offset + row : a.out_offset;
-    __shared__ float wv[kWaves];
-    __shared__ uint32_t wi[kWaves];
+    float* const wv = reinterpret_cast<float*>(hit + kStatsRows / 32);
+    uint32_t* const wi = reinterpret_cast<uint32_t*>(wv + kWaves);
+    double* const ws = reinterpret_cast<double*>(wi + kWaves);  // 8-byte aligned: 1,088 bytes in
     egd::team_argmax<64>(bv, bi);
     if (lane == 0) {
       wv[threadIdx.x >> 6] = bv;
@@ -846,7 +859,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
       }
     // sum of exp(l/T - the workgroup's max) over its rows in float64 (the sampler's per-slice
     // statement, sample.wgsl:230-236, over this workgroup's rows)
-    __shared__ double ws[kWaves];
     double e = valid && temp > 0.0f ? (double)expf(x - bv) : 0.0;
 #pragma unroll
     for (int m = 32; m > 0; m >>= 1) e += __shfl_xor(e, m, 64);
