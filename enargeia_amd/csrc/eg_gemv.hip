@@ -363,20 +363,20 @@ int launch(eg_context* ctx, const QuantView& v) {
     const uint32_t smem = chunks * epc * 4u + input_scratch_bytes(a) + (stats ? kStatsLdsBytes : 0u);
     grid = grid_for(ctx, fn, shape.tiles, smem, a.in_kind != EG_INPUT_VECTOR ? ctx->fused_tiles_per_wave : 1);
     if (stats) {
-      // every workgroup's rows, and the up to TILE - 1 rows a shifted last tile recomputes below
-      // them, within the kernel's per-workgroup record (kStatsRows)
+      // every workgroup's nominal rows within the kernel's per-workgroup record (kStatsRows; a
+      // tile to spare)
       const uint32_t tile_rows = (64u / shape.team) * shape.u;
       const uint32_t tiles_per_group = (kStatsRows - tile_rows) / tile_rows;
       grid = std::max<uint32_t>(grid, (shape.tiles + tiles_per_group - 1) / tiles_per_group);
-      a.sample_dev = v.sample_dev;
+      a.stats.sample_dev = v.sample_dev;
       if (v.sample_host) {
-        a.temperature = v.sample_host->temperature;
-        a.repetition_penalty = v.sample_host->repetition_penalty;
-        a.history_length = v.sample_host->history_length;
+        a.stats.temperature = v.sample_host->temperature;
+        a.stats.repetition_penalty = v.sample_host->repetition_penalty;
+        a.stats.history_length = v.sample_host->history_length;
       }
-      a.history = v.history;
-      a.clear = v.clear;
-      a.clear_words = v.clear ? v.clear_words : 0u;
+      a.stats.history = v.history;
+      a.stats.clear = v.clear;
+      a.stats.clear_words = v.clear ? v.clear_words : 0u;
     }
     if ((st = partials_fit(grid)) != EG_OK) return st;
     a.stamp = eg::stamp_slot(ctx);

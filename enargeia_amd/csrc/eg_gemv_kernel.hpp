@@ -63,6 +63,17 @@ static_assert(sizeof(DevSegment) == 64, "DevSegment is read as 16 dwords");
 // 2 matrices); larger tables stay in global memory and are read with scalar loads.
 constexpr uint32_t kInlineSegments = 4;
 
+// kSampleStats: the sampling parameters - from device memory (sample_dev, the 32-byte sample
+// dims, so a captured graph replays with new values) or, when that is NULL, the values here - the
+// history the penalty reads, and words workgroup 0 zeroes (clear[0, clear_words), nullable).
+struct SampleStatsArgs {
+  const eg_sample_dims* sample_dev;
+  const uint32_t* history;
+  uint32_t* clear;
+  float temperature, repetition_penalty;
+  uint32_t history_length, clear_words;
+};
+
 struct GemvArgs {
   const float* x;
   const uint4* w;          // code stream viewed as 16-byte chunks, row-major
@@ -78,7 +89,13 @@ struct GemvArgs {
   uint32_t* partials;      // argmax: (value bits, index) per workgroup
   const DevSegment* segs;  // batched launches only
   uint32_t seg_count;
-  DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
+  union {
+    DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
+    // kSampleStats launches, never batched, keep their arguments in the table's place: every
+    // launch's arguments stay the size they were (a larger argument block measured ~1% slower
+    // over the decode step's 120 launches)
+    SampleStatsArgs stats;
+  };
   const uint32_t* seg_index;  // seg_count > kInlineSegments: the segment of each pass, 16 bits per pass
   uint32_t total_passes;   // tiles over all rows (all segments)
   // input stage (eg_input_kind): how each workgroup produces x in LDS
@@ -88,15 +105,6 @@ struct GemvArgs {
   float eps;
   uint32_t att_heads, att_kv_heads, att_head_dim, att_chunks;
   uint64_t* stamp;         // launch stamps (egd::WaveStamp), nullable
-  // kSampleStats: the sampling parameters - from device memory (sample_dev, the 32-byte sample
-  // dims, so a captured graph replays with new values) or, when that is NULL, these - and the
-  // history the penalty reads
-  const eg_sample_dims* sample_dev;
-  float temperature, repetition_penalty;
-  uint32_t history_length;
-  const uint32_t* history;
-  uint32_t* clear;  // kSampleStats: workgroup 0 zeroes clear[0, clear_words) (nullable)
-  uint32_t clear_words;
 };
 
 template <int BITS>
@@ -688,13 +696,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
         (uint32_t)(((uint64_t)a.total_passes * (env.block() * kWaves)) / total_waves) * TILE);
     stats_hi = __builtin_amdgcn_readfirstlane(
         min((uint32_t)(((uint64_t)a.total_passes * ((env.block() + 1) * kWaves)) / total_waves) * TILE, a.n));
-    temp = a.temperature;
-    pen = a.repetition_penalty;
-    hist_len = a.history_length;
-    if (a.sample_dev) {
-      temp = a.sample_dev->temperature;
-      pen = a.sample_dev->repetition_penalty;
-      hist_len = a.sample_dev->history_length;
+    temp = a.stats.temperature;
+    pen = a.stats.repetition_penalty;
+    hist_len = a.stats.history_length;
+    if (a.stats.sample_dev) {
+      temp = a.stats.sample_dev->temperature;
+      pen = a.stats.sample_dev->repetition_penalty;
+      hist_len = a.stats.sample_dev->history_length;
     }
     temp = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, temp)));
     pen = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, pen)));
@@ -702,11 +710,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
 #pragma unroll
     for (uint32_t r = 0; r < kStatsHistory; r++) {
       const uint32_t h = threadIdx.x + r * blockDim.x;
-      hv[r] = pen != 1.0f && a.history && h < hist_len ? a.history[h] : 0xFFFFFFFFu;
+      hv[r] = pen != 1.0f && a.stats.history && h < hist_len ? a.stats.history[h] : 0xFFFFFFFFu;
     }
     for (uint32_t i = threadIdx.x; i < kStatsRows / 32; i += blockDim.x) hit[i] = 0u;
-    if (a.clear && env.block() == 0)
-      for (uint32_t i = threadIdx.x; i < a.clear_words; i += blockDim.x) a.clear[i] = 0u;
+    if (a.stats.clear && env.block() == 0)
+      for (uint32_t i = threadIdx.x; i < a.stats.clear_words; i += blockDim.x) a.stats.clear[i] = 0u;
   }
 
   auto compute = [&](const Loads<BITS, U, CPL>& L, const Pending& P) {
@@ -800,9 +808,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const Env& env) {
       const uint32_t rel = hv[r] - stats_lo;
       if (rel < stats_hi - stats_lo) atomicOr(&hit[rel >> 5], 1u << (rel & 31u));
     }
-    if (pen != 1.0f && a.history)
+    if (pen != 1.0f && a.stats.history)
       for (uint32_t h = threadIdx.x + kStatsHistory * blockDim.x; h < hist_len; h += blockDim.x) {
-        const uint32_t rel = a.history[h] - stats_lo;
+        const uint32_t rel = a.stats.history[h] - stats_lo;
         if (rel < stats_hi - stats_lo) atomicOr(&hit[rel >> 5], 1u << (rel & 31u));
       }
   }
