@@ -60,8 +60,10 @@ struct DevSegment {
 static_assert(sizeof(DevSegment) == 64, "DevSegment is read as 16 dwords");
 // Plans of up to this many matrices carry their table in the kernel arguments, so a wave knows
 // its first segment with no memory round trip (the decoder's q|k|v and gate|up plans are 3 and
-// 2 matrices); larger tables stay in global memory and are read with scalar loads.
-constexpr uint32_t kInlineSegments = 4;
+// 2 matrices); larger tables stay in global memory and are read with scalar loads. Three, not
+// more: the argument block's size shows in the decode step (its 97 GEMV launches a token ran
+// 0.3% faster at three entries than at four, and ~1% slower with 48 bytes more; MI355X).
+constexpr uint32_t kInlineSegments = 3;
 
 // kSampleStats: the sampling parameters - from device memory (sample_dev, the 32-byte sample
 // dims, so a captured graph replays with new values) or, when that is NULL, the values here - the
@@ -91,9 +93,8 @@ struct GemvArgs {
   uint32_t seg_count;
   union {
     DevSegment inline_segs[kInlineSegments];  // the table itself when seg_count <= kInlineSegments
-    // kSampleStats launches, never batched, keep their arguments in the table's place: every
-    // launch's arguments stay the size they were (a larger argument block measured ~1% slower
-    // over the decode step's 120 launches)
+    // kSampleStats launches, never batched, keep their arguments in the table's place, so no
+    // launch's argument block grows for them
     SampleStatsArgs stats;
   };
   const uint32_t* seg_index;  // seg_count > kInlineSegments: the segment of each pass, 16 bits per pass
