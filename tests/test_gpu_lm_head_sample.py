@@ -113,3 +113,31 @@ def test_ragged_vocab_with_history_in_the_last_tiles(device, vocab):
             _agree(head, hist, params, [rng() for _ in range(4)], f"vocab {vocab} {params}")
     finally:
         head.close()
+
+
+def test_rejects_bad_arguments(device):
+    # Checked on the host before anything is launched: an int4 head, a sample vocabulary that is
+    # not the head's rows, an output offset, a history length with no history.
+    import ctypes
+    from enargeia_amd import _lib
+    lib = _lib.load()
+    buf = device.buffer(1 << 20)
+    vp = ctypes.c_void_p(buf.ptr)
+    dims = K.EmbeddingDims.from_buffer_copy(K.embedding_dims(1, 896, 0, 1024, 896, 1024, 0))
+    shifted = K.EmbeddingDims.from_buffer_copy(K.embedding_dims(1, 896, 0, 1024, 896, 1024, 8))
+    params = K.SamplingParams(0.7, 0.9, 1.1)
+
+    def call(d, sample, bits=8, history=vp):
+        sd = K.SampleDims.from_buffer_copy(sample)
+        return lib.eg_lm_head_sample(device.ctx, vp, vp, vp, None, vp, history, vp, ctypes.byref(d), K.ENC_SIGNED,
+                                     bits, ctypes.byref(sd))
+
+    try:
+        assert call(dims, K.sample_dims(1024, 0, params, 0.5), bits=4) == _lib.EG_ERR_INVALID
+        assert call(dims, K.sample_dims(1000, 0, params, 0.5)) == _lib.EG_ERR_INVALID
+        assert b"must equal the head's rows" in lib.eg_last_error(device.ctx)
+        assert call(shifted, K.sample_dims(1024, 0, params, 0.5)) == _lib.EG_ERR_INVALID
+        assert call(dims, K.sample_dims(1024, 5, params, 0.5), history=None) == _lib.EG_ERR_INVALID
+        assert b"no history buffer" in lib.eg_last_error(device.ctx)
+    finally:
+        buf.release()
