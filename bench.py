@@ -604,6 +604,8 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
         log(f"decode (graph, sampled): {result['sampled_tok_s']} tok/s with a readback per token; "
             f"{len(set(sampled))} distinct tokens; vs oracle {result['sampled_vs_oracle']}")
         dec.set_sampling(0.0, 1.0, 1.0)
+    if "graph" in modes:
+        result["f32_cache"] = f32_cache_decode(dev, dm, cfg, w, first, [first] + tokens)
     result["prompt"] = prompt_throughput(dev, dec, cfg)
     step_bytes = (STEP_BYTES + LM_HEAD_BYTES
                   + 2 * cfg.layers * (start + DECODE_STEPS // 2) * cfg.kv_heads * cfg.head_dim * 2)
@@ -611,6 +613,45 @@ def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:
     dec.close()
     dm.release()
     return result
+
+
+def f32_cache_decode(dev, dm, cfg, w, first, f16_tokens) -> dict:
+    """The same greedy steps on a decoder with the reference's f32 KV cache variant (SessionOptions
+    cacheDType 'f32'): the primed rows [0, 1888) hold the f16 run's values as f32, the prompt and
+    the 128 timed steps append unrounded rows; captured, one readback per token. The f32 cache's
+    numerics are held to the oracle by tests/test_gpu_decode.py; here its tokens are counted
+    against the f16 run's (they may part where the top two logits are closer than the f16
+    rounding of the new rows moves them)."""
+    from enargeia_amd.model import Decoder, cache_fill
+
+    dec = Decoder(dm, cache="f32")
+    try:
+        kf, vf = cache_fill(cfg, w.fill_seed)
+        dev.write(dec.buffers.k_cache, kf.astype(np.float32))
+        dev.write(dec.buffers.v_cache, vf.astype(np.float32))
+        dev.sync()
+        del kf, vf
+        dec.capture()
+        for i, t in enumerate(w.prompt):
+            dec.reset(w.prime + i, t)
+            dec.step(read_token=True)
+        start = w.prime + len(w.prompt)
+        for _ in range(8):
+            dec.step(read_token=False)
+        dec.reset(start, first)
+        t = time.perf_counter()
+        tokens = [dec.step(read_token=True) for _ in range(DECODE_STEPS)]
+        wall = time.perf_counter() - t
+        same = sum(int(a == b) for a, b in zip([first] + tokens, f16_tokens))
+        res = {"tok_s": round(DECODE_STEPS / wall, 1), "ms_per_token": round(wall / DECODE_STEPS * 1e3, 4),
+               "tokens_equal_to_f16_run": f"{same}/{len(f16_tokens)}",
+               "config": "config 4 greedy steps with an f32 KV cache (eg_decoder_create_cache), graph, "
+                         "a readback per token"}
+        log(f"decode (graph, f32 KV cache): {res['tok_s']} tok/s with a readback per token; "
+            f"tokens equal to the f16 run {res['tokens_equal_to_f16_run']}")
+        return res
+    finally:
+        dec.close()
 
 
 GOLDEN_SAMPLED = os.path.join(ROOT, "tests", "golden", "config4_sampled.npz")

@@ -61,13 +61,16 @@ SIGNATURES: dict[str, tuple] = {
     "eg_test_launch_stamps": (_i, [_vp, _vp, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
     "eg_embed_gather": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_attention_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "eg_attention_decode_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "eg_attention_combine": (_i, [_vp, _vp, _vp, _vp]),
     "eg_gemv_plan_launch_input": (_i, [_vp, _vp, _vp]),
     "eg_gemv_swiglu_plan_create": (_i, [_vp, ctypes.c_uint32, ctypes.c_uint32, _i, _i, _vp, ctypes.POINTER(_vp)]),
     "eg_lm_head_argmax_input": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eg_decode_advance": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_uint32]),
     "eg_decoder_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "eg_decoder_create_cache": (_i, [_vp, _vp, _i, ctypes.POINTER(_vp)]),
     "eg_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "eg_attention_prefill_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "eg_container_open": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "eg_container_close": (_i, [_vp]),
     "eg_container_header_get": (_i, [_vp, _vp]),

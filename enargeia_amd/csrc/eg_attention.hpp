@@ -1,13 +1,16 @@
-// Fused decode attention (RoPE, the f16 cache append, split-K flash-decoding partials), shared by
-// its own launch (eg_decode.hip) and the persistent decode kernel (eg_layers.hip). Not part of
-// the ABI.
+// Fused decode attention (RoPE, the cache append, split-K flash-decoding partials), shared by its
+// own launch (eg_decode.hip) and the persistent decode kernel (eg_layers.hip). Not part of the
+// ABI. The cache element type CT is uint16_t (f16 bits, the reference's f16 cache variant) or
+// float (its f32 variant); every cached value is f32 once read.
 //
 // Reference pieces: rope.wgsl + the f16 cache pack (cache_variants.ts:147-305,
-// graph_decode.ts:276-320), attn_scores / softmax / attn_apply decode (graph_decode.ts:322-345;
-// CPU semantics ops.ts:87-205).
+// graph_decode.ts:276-320; the f32 cache's v projection writes the slot itself, :281-283),
+// attn_scores / softmax / attn_apply decode (graph_decode.ts:322-345, per dtype
+// cache_variants.ts:21-40; CPU semantics ops.ts:87-205).
 #pragma once
 
 #include <cmath>
+#include <type_traits>
 
 #include "eg_internal.hpp"
 
@@ -21,6 +24,13 @@ using egd::rope_apply;
 using egd::rope_table;
 
 constexpr uint32_t kMaxCombine = 1024;  // heads x chunks the one-workgroup combine holds in LDS
+
+// A value as the cache holds it: f16 bits (round to nearest even) or the f32 itself.
+template <class CT>
+__device__ __forceinline__ CT to_cache(float x) {
+  if constexpr (std::is_same<CT, float>::value) return x;
+  else return float_to_half(x);
+}
 
 // The whole attention output from the chunk-fastest partials, by one workgroup: per (head,
 // chunk) statistics into LDS, each chunk's weight e^(m_c - M) / L, then every output's weighted
@@ -73,9 +83,10 @@ __device__ void combine_all(const float* partials, float* out, uint32_t heads, u
 // a chunk always lies inside the cache - so these loads need not wait for it; rows past the
 // live history are loaded too and never read), then one query element per thread and the new
 // key and value. All of it is in flight at once; the position arrives by a scalar load beside.
-template <int D, int CHUNK, int GMAX>
+template <int D, int CHUNK, int GMAX, class CT = uint16_t>
 struct Prefetch {
-  static constexpr uint32_t kVecs = D / 8;                      // 16-byte vectors per row
+  static constexpr uint32_t kPer = 16 / sizeof(CT);             // cache elements per 16 bytes
+  static constexpr uint32_t kVecs = D / kPer;                   // 16-byte vectors per row
   static constexpr uint32_t kLoads = CHUNK * kVecs / kThreads;  // per thread
   static_assert(CHUNK * kVecs % kThreads == 0, "a chunk's rows split evenly over the threads");
   static_assert(GMAX * D <= kThreads && D <= kThreads, "one query element per thread");
@@ -84,13 +95,13 @@ struct Prefetch {
   double2 cs = make_double2(0.0, 0.0);  // the RoPE table's entry tid, when one is given
   // The cached rows (and the RoPE row): written before the launch, so a phase of the persistent
   // kernel issues them before waiting for its inputs.
-  __device__ __forceinline__ void load_cache(const uint16_t* k_cache, const uint16_t* v_cache, uint32_t j0,
-                                             uint32_t kv, uint32_t kv_heads, const double2* rope) {
+  __device__ __forceinline__ void load_cache(const CT* k_cache, const CT* v_cache, uint32_t j0, uint32_t kv,
+                                             uint32_t kv_heads, const double2* rope) {
     const uint32_t tid = threadIdx.x;
 #pragma unroll
     for (uint32_t r = 0; r < kLoads; r++) {
       const uint32_t i = tid + r * kThreads, row = i / kVecs, w = i % kVecs;
-      const size_t at = ((size_t)(j0 + row) * kv_heads + kv) * D + w * 8;
+      const size_t at = ((size_t)(j0 + row) * kv_heads + kv) * D + w * kPer;
       k[r] = *reinterpret_cast<const uint4*>(k_cache + at);
       v[r] = *reinterpret_cast<const uint4*>(v_cache + at);
     }
@@ -119,21 +130,24 @@ __device__ __forceinline__ void store_p(float* p, float v) {
 
 // The work of one (kv head share, chunk) workgroup: RoPE, the cache append, scores, softmax
 // statistics and the partial o, written to po/pm/pl, from what `pre` loaded.
-template <int D, int CHUNK, int GMAX, int AUX = 0>
+template <int D, int CHUNK, int GMAX, int AUX = 0, class CT = uint16_t>
 __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, uint32_t hs, uint32_t ng,
-                                       uint32_t chunks, const Prefetch<D, CHUNK, GMAX>& pre, bool rope, uint16_t* k_cache,
-                                       uint16_t* v_cache, float* po, float* pm, float* pl,
+                                       uint32_t chunks, const Prefetch<D, CHUNK, GMAX, CT>& pre, bool rope,
+                                       CT* k_cache, CT* v_cache, float* po, float* pm, float* pl,
                                        const eg_attention_dims& d) {
+  using Pre = Prefetch<D, CHUNK, GMAX, CT>;
+  constexpr bool kF32 = std::is_same<CT, float>::value;
   const uint32_t tid = threadIdx.x;
   const uint32_t live = min((uint32_t)CHUNK, pos + 1 - j0);
 
-  // K rows padded to 144 bytes: 16-byte row reads by 16 lanes on 16 rows cover the 64 banks once.
-  // V rows unpadded: the P.V loop's 8-byte reads take 4 rows a wave, 2 on each half of the banks.
+  // K rows padded by 16 bytes (144 bytes f16, 272 f32): 16-byte row reads by 16 lanes on 16 rows
+  // cover the 64 banks once. V rows unpadded: the f16 P.V loop's 8-byte reads take 4 rows a
+  // wave, 2 on each half of the banks (the f32 loop's 16-byte reads, 4 rows on 4 quarters).
   __shared__ __attribute__((aligned(16))) float qs[GMAX][D];          // rotated, pre-scaled queries
   __shared__ float knew[D], vnew[D];                                  // the new key (rotated), value
   __shared__ double2 cs[D / 2];                                       // RoPE cos/sin at `pos`
-  __shared__ __attribute__((aligned(16))) uint16_t ks[CHUNK][D + 8];  // K rows (f16)
-  __shared__ __attribute__((aligned(16))) uint16_t vs[CHUNK][D];      // V rows (f16)
+  __shared__ __attribute__((aligned(16))) CT ks[CHUNK][D + Pre::kPer];  // K rows
+  __shared__ __attribute__((aligned(16))) CT vs[CHUNK][D];              // V rows
   __shared__ float p[GMAX][CHUNK];                                    // scores, then exp(score - max)
   __shared__ float mstat[GMAX], lstat[GMAX];
   __shared__ __attribute__((aligned(16))) float half_sum[GMAX][D];    // P.V: the second wave's sums
@@ -143,10 +157,10 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   // The cached rows into LDS (every row of the chunk; the row at `pos`, stale in the cache, is
   // replaced by the new one after the next barriers).
 #pragma unroll
-  for (uint32_t r = 0; r < Prefetch<D, CHUNK, GMAX>::kLoads; r++) {
-    const uint32_t i = tid + r * kThreads, row = i / (D / 8), w = i % (D / 8);
-    uint32_t* kd = reinterpret_cast<uint32_t*>(&ks[row][w * 8]);
-    uint32_t* vd = reinterpret_cast<uint32_t*>(&vs[row][w * 8]);
+  for (uint32_t r = 0; r < Pre::kLoads; r++) {
+    const uint32_t i = tid + r * kThreads, row = i / Pre::kVecs, w = i % Pre::kVecs;
+    uint32_t* kd = reinterpret_cast<uint32_t*>(&ks[row][w * Pre::kPer]);
+    uint32_t* vd = reinterpret_cast<uint32_t*>(&vs[row][w * Pre::kPer]);
     kd[0] = pre.k[r].x; kd[1] = pre.k[r].y; kd[2] = pre.k[r].z; kd[3] = pre.k[r].w;
     vd[0] = pre.v[r].x; vd[1] = pre.v[r].y; vd[2] = pre.v[r].z; vd[3] = pre.v[r].w;
   }
@@ -167,7 +181,7 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
   // The row at `pos` is the new one: appended to the cache (by the first head share only) and
   // staged from registers.
   if (owns_new && tid < D) {
-    const uint16_t kh = float_to_half(knew[tid]), vh = float_to_half(vnew[tid]);
+    const CT kh = to_cache<CT>(knew[tid]), vh = to_cache<CT>(vnew[tid]);
     if (hs == 0) {
       const size_t at = ((size_t)pos * d.kv_heads + kv) * D + tid;
       k_cache[at] = kh;
@@ -187,19 +201,31 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
       float s = -INFINITY;
       if (j < live) {
         float acc = 0.f;
+        if constexpr (kF32) {
 #pragma unroll
-        for (int w = 0; w < D / 8; w++) {
-          const uint4 kk = *reinterpret_cast<const uint4*>(&ks[j][8 * w]);
-          const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * w]);
-          const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * w + 4]);
-          acc = fmaf(qa.x, half_to_float((uint16_t)kk.x), acc);
-          acc = fmaf(qa.y, half_to_float((uint16_t)(kk.x >> 16)), acc);
-          acc = fmaf(qa.z, half_to_float((uint16_t)kk.y), acc);
-          acc = fmaf(qa.w, half_to_float((uint16_t)(kk.y >> 16)), acc);
-          acc = fmaf(qb.x, half_to_float((uint16_t)kk.z), acc);
-          acc = fmaf(qb.y, half_to_float((uint16_t)(kk.z >> 16)), acc);
-          acc = fmaf(qb.z, half_to_float((uint16_t)kk.w), acc);
-          acc = fmaf(qb.w, half_to_float((uint16_t)(kk.w >> 16)), acc);
+          for (int w = 0; w < D / 4; w++) {
+            const float4 kk = *reinterpret_cast<const float4*>(&ks[j][4 * w]);
+            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][4 * w]);
+            acc = fmaf(qa.x, kk.x, acc);
+            acc = fmaf(qa.y, kk.y, acc);
+            acc = fmaf(qa.z, kk.z, acc);
+            acc = fmaf(qa.w, kk.w, acc);
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < D / 8; w++) {
+            const uint4 kk = *reinterpret_cast<const uint4*>(&ks[j][8 * w]);
+            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][8 * w]);
+            const float4 qb = *reinterpret_cast<const float4*>(&qs[g][8 * w + 4]);
+            acc = fmaf(qa.x, half_to_float((uint16_t)kk.x), acc);
+            acc = fmaf(qa.y, half_to_float((uint16_t)(kk.x >> 16)), acc);
+            acc = fmaf(qa.z, half_to_float((uint16_t)kk.y), acc);
+            acc = fmaf(qa.w, half_to_float((uint16_t)(kk.y >> 16)), acc);
+            acc = fmaf(qb.x, half_to_float((uint16_t)kk.z), acc);
+            acc = fmaf(qb.y, half_to_float((uint16_t)(kk.z >> 16)), acc);
+            acc = fmaf(qb.z, half_to_float((uint16_t)kk.w), acc);
+            acc = fmaf(qb.w, half_to_float((uint16_t)(kk.w >> 16)), acc);
+          }
         }
         s = acc;
       }
@@ -242,11 +268,19 @@ __device__ __forceinline__ void attend(uint32_t pos, uint32_t j0, uint32_t kv, u
       const uint32_t jb = wh * (CHUNK / kWPH), je = min(live, jb + CHUNK / kWPH);
       for (uint32_t j = jb + ph; j < je; j += 4) {
         const float pj = p[g][j];
-        const uint2 vv = *reinterpret_cast<const uint2*>(&vs[j][e4]);
-        a0 = fmaf(pj, half_to_float((uint16_t)vv.x), a0);
-        a1 = fmaf(pj, half_to_float((uint16_t)(vv.x >> 16)), a1);
-        a2 = fmaf(pj, half_to_float((uint16_t)vv.y), a2);
-        a3 = fmaf(pj, half_to_float((uint16_t)(vv.y >> 16)), a3);
+        if constexpr (kF32) {
+          const float4 vv = *reinterpret_cast<const float4*>(&vs[j][e4]);
+          a0 = fmaf(pj, vv.x, a0);
+          a1 = fmaf(pj, vv.y, a1);
+          a2 = fmaf(pj, vv.z, a2);
+          a3 = fmaf(pj, vv.w, a3);
+        } else {
+          const uint2 vv = *reinterpret_cast<const uint2*>(&vs[j][e4]);
+          a0 = fmaf(pj, half_to_float((uint16_t)vv.x), a0);
+          a1 = fmaf(pj, half_to_float((uint16_t)(vv.x >> 16)), a1);
+          a2 = fmaf(pj, half_to_float((uint16_t)vv.y), a2);
+          a3 = fmaf(pj, half_to_float((uint16_t)(vv.y >> 16)), a3);
+        }
       }
     }
     a0 += __shfl_xor(a0, 16, 64);
@@ -300,9 +334,9 @@ struct AttnLaunchEnv {
 // [j0, j0 + CHUNK) (bx). Splitting the group's heads over HSPLIT workgroups doubles the
 // parallelism of a launch that otherwise has only chunks x kv_heads workgroups; the K/V rows they
 // share come from L2.
-template <int D, int CHUNK, int GMAX, int HSPLIT, class Env>
+template <int D, int CHUNK, int GMAX, int HSPLIT, class Env, class CT = uint16_t>
 __device__ __forceinline__ void attention_body(const uint32_t* position, const float* q, const float* k,
-                                               const float* v, uint16_t* k_cache, uint16_t* v_cache,
+                                               const float* v, CT* k_cache, CT* v_cache,
                                                float* partials, uint32_t* counter, float* out,
                                                const eg_attention_dims& d, const double2* rope, const Env& env) {
   constexpr int AUX = Env::kAux;
@@ -315,7 +349,7 @@ __device__ __forceinline__ void attention_body(const uint32_t* position, const f
   const uint32_t j0 = c * CHUNK;
   const uint32_t tid = threadIdx.x;
   const uint32_t h0 = kv * group + gb;
-  Prefetch<D, CHUNK, GMAX> pre;
+  Prefetch<D, CHUNK, GMAX, CT> pre;
   pre.load_cache(k_cache, v_cache, j0, kv, d.kv_heads, rope);
   env.wait();
   pre.template load_inputs<AUX>(q, h0, ng, kv, k, v);
@@ -336,7 +370,8 @@ __device__ __forceinline__ void attention_body(const uint32_t* position, const f
     }
   }
   if (ng > 0 && !empty)
-    attend<D, CHUNK, GMAX, AUX>(pos, j0, kv, hs, ng, chunks, pre, rope != nullptr, k_cache, v_cache, po, pm, pl, d);
+    attend<D, CHUNK, GMAX, AUX, CT>(pos, j0, kv, hs, ng, chunks, pre, rope != nullptr, k_cache, v_cache, po, pm, pl,
+                                    d);
 
   // The combine, once, by the last workgroup to arrive: the fence releases this workgroup's
   // partials device-wide before it counts itself; the last one's fence acquires everyone's.
@@ -356,16 +391,16 @@ __device__ __forceinline__ void attention_body(const uint32_t* position, const f
   }
 }
 
-template <int D, int CHUNK, int GMAX, int HSPLIT>
+template <int D, int CHUNK, int GMAX, int HSPLIT, class CT>
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(const uint32_t* position, const float* q,
-                                                                    const float* k, const float* v,
-                                                                    uint16_t* k_cache, uint16_t* v_cache,
+                                                                    const float* k, const float* v, CT* k_cache,
+                                                                    CT* v_cache,
                                                                     float* partials, uint32_t* counter, float* out,
                                                                     eg_attention_dims d, const double2* rope,
                                                                     uint64_t* stamp_slot) {
   const egd::WaveStamp stamp(stamp_slot);
-  attention_body<D, CHUNK, GMAX, HSPLIT>(position, q, k, v, k_cache, v_cache, partials, counter, out, d, rope,
-                                         AttnLaunchEnv{});
+  attention_body<D, CHUNK, GMAX, HSPLIT, AttnLaunchEnv, CT>(position, q, k, v, k_cache, v_cache, partials, counter,
+                                                           out, d, rope, AttnLaunchEnv{});
 }
 
 }  // namespace eg_attn

@@ -108,9 +108,11 @@ int check_attention(eg_context* ctx, const char* op, const eg_attention_dims* d)
   return EG_OK;
 }
 
+// CT: the cache element, uint16_t (f16 bits) or float
+template <class CT>
 int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, const float* q, const float* k,
-                     const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials, uint32_t* counter,
-                     float* out, const eg_attention_dims* dims, const double* rope) {
+                     const float* v, CT* k_cache, CT* v_cache, float* partials, uint32_t* counter, float* out,
+                     const eg_attention_dims* dims, const double* rope) {
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!position || !q || !k || !v || !k_cache || !v_cache || !partials)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
@@ -124,12 +126,12 @@ int launch_attention(eg_context* ctx, const char* op, const uint32_t* position, 
   // chunk 64: two workgroups share a kv group's query heads; chunk 128: four do
   if (dims->chunk == 64) {
     const dim3 grid(dims->max_context / 64, dims->kv_heads * 2);
-    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
+    hipLaunchKernelGGL((attention_decode_kernel<64, 64, 4, 2, CT>), grid, dim3(kThreads), 0, ctx->stream, position, q,
+                       k, v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
   } else {
     const dim3 grid(dims->max_context / 128, dims->kv_heads * 4);
-    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4>), grid, dim3(kThreads), 0, ctx->stream, position, q, k,
-                       v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
+    hipLaunchKernelGGL((attention_decode_kernel<64, 128, 2, 4, CT>), grid, dim3(kThreads), 0, ctx->stream, position,
+                       q, k, v, k_cache, v_cache, partials, counter, out, *dims, cs, eg::stamp_slot(ctx));
   }
   return eg::check_launch(ctx, op);
 }
@@ -304,6 +306,14 @@ int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const f
                           dims, rope);
 }
 
+int eg::attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                              const float* v, float* k_cache, float* v_cache, float* partials,
+                              const eg_attention_dims* dims, const double* rope) {
+  if (!rope) return eg::fail(ctx, EG_ERR_INVALID, "attention_decode_f32: rope table is NULL");
+  return launch_attention(ctx, "attention_decode_f32", position, q, k, v, k_cache, v_cache, partials, nullptr,
+                          nullptr, dims, rope);
+}
+
 int eg::launch_rope_table(eg_context* ctx, double* table, uint32_t positions, uint32_t head_dim, float theta) {
   if (head_dim != 64) return eg::fail(ctx, EG_ERR_INVALID, "rope_table: head_dim %u (64 is supported)", head_dim);
   if (positions == 0) return EG_OK;
@@ -354,6 +364,13 @@ int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* 
                         const eg_attention_dims* dims) {
   return launch_attention(ctx, "attention_decode", position, q, k, v, k_cache, v_cache, partials, counter, out, dims,
                           nullptr);
+}
+
+int eg_attention_decode_f32(eg_context* ctx, const uint32_t* position, const float* q, const float* k, const float* v,
+                            float* k_cache, float* v_cache, float* partials, uint32_t* counter, float* out,
+                            const eg_attention_dims* dims) {
+  return launch_attention(ctx, "attention_decode_f32", position, q, k, v, k_cache, v_cache, partials, counter, out,
+                          dims, nullptr);
 }
 
 int eg_attention_combine(eg_context* ctx, const float* partials, float* out, const eg_attention_dims* dims) {

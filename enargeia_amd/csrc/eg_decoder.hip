@@ -74,8 +74,11 @@ struct eg_decoder {
   float* patt = nullptr;             // [chunk][hidden] attention output
   float* pgu = nullptr;              // [chunk][2 * intermediate] gate | up
   float* pa = nullptr;               // [chunk][intermediate] silu(gate) * up
-  uint16_t* k_cache = nullptr;
-  uint16_t* v_cache = nullptr;
+  // [layers][max_context][kv_heads][head_dim] of f16 bits, or of f32 (cache_f32: the
+  // reference's f32 cache variant, SessionOptions.cacheDType)
+  void* k_cache = nullptr;
+  void* v_cache = nullptr;
+  bool cache_f32 = false;
   size_t layer_stride = 0;  // cache elements per layer
   std::vector<eg_gemv_plan*> plans;  // per layer: qkv, o, gate|up (a SwiGLU pair if swiglu), down
   // the layers of a step as one persistent launch (eg_layers.hip), where the shapes and the
@@ -89,6 +92,12 @@ struct eg_decoder {
 };
 
 namespace {
+
+// Layer l's rows of a cache (CT: uint16_t for f16 bits, float for an f32 cache).
+template <class CT>
+CT* layer_cache(const eg_decoder* d, void* base, uint32_t l) {
+  return static_cast<CT*>(base) + (size_t)l * d->layer_stride;
+}
 
 constexpr uint32_t kMaxChunk = 2048;
 
@@ -192,9 +201,12 @@ int run_layers(eg_decoder* d) {
     // The combine runs in the o projection's input stage: measured faster here than the
     // attention launch's last-workgroup combine, whose device-scope fences cost more than the
     // per-workgroup recomputation.
-    if ((st = eg::attention_decode_rope(ctx, d->position, d->q, d->kv, d->kv + kvn, d->k_cache + l * d->layer_stride,
-                                        d->v_cache + l * d->layer_stride, d->partials, &d->att, d->rope)) != EG_OK)
-      return st;
+    st = d->cache_f32 ? eg::attention_decode_rope(ctx, d->position, d->q, d->kv, d->kv + kvn, layer_cache<float>(d, d->k_cache, l),
+                                                  layer_cache<float>(d, d->v_cache, l), d->partials, &d->att, d->rope)
+                      : eg::attention_decode_rope(ctx, d->position, d->q, d->kv, d->kv + kvn,
+                                                  layer_cache<uint16_t>(d, d->k_cache, l),
+                                                  layer_cache<uint16_t>(d, d->v_cache, l), d->partials, &d->att, d->rope);
+    if (st != EG_OK) return st;
     in = eg_gemv_input{};
     in.kind = EG_INPUT_ATTENTION;
     in.x = d->partials;
@@ -314,13 +326,14 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
         {L.v.packed, L.v.scales, L.v.zeros, L.v_bias, nullptr, d->pv, kvn, kvn, 0}};
     eg_attention_prefill_dims ad{count, begin + count, begin, m.heads, m.kv_heads, m.head_dim, m.max_context,
                                  m.rope_theta};
-    uint16_t* kc = d->k_cache + l * d->layer_stride;
-    uint16_t* vc = d->v_cache + l * d->layer_stride;
+    uint16_t* kc = layer_cache<uint16_t>(d, d->k_cache, l);
+    uint16_t* vc = layer_cache<uint16_t>(d, d->v_cache, l);
     // RoPE and the cache append in the q|k|v launch's epilogue where it can take them (then the
-    // attention launches alone), else rope_append's launch before the attention
+    // attention launches alone), else rope_append's launch before the attention; an f32 cache
+    // takes the separate launches (the epilogue stores f16 rows)
     bool fused = false;
     st = eg::check_attention_prefill(ctx, "attention_prefill", &ad);
-    if (st == EG_OK && m.head_dim == 64) {
+    if (st == EG_OK && m.head_dim == 64 && !d->cache_f32) {
       const eg::PrefillRope rope{reinterpret_cast<const double2*>(d->rope_table), d->pqr, kc, vc, begin, m.heads,
                                  m.kv_heads};
       st = eg::prefill_qkv_rope(ctx, d->ph[0], count, H, m.block_size, m.encoding, m.bits, qkv, L.input_norm,
@@ -335,6 +348,9 @@ int run_prefill_chunk(eg_decoder* d, const uint32_t* ids, uint32_t begin, uint32
     const bool xb_o = fused && ctx->prefill_xb16 && eg::prefill_chunked(count, H, H, m.block_size, m.bits, d->patt, L.o.packed);
     const bool xb_down = ctx->prefill_xb16 && eg::prefill_chunked(count, H, I, m.block_size, m.bits, d->pa, L.down.packed);
     if (fused) st = eg::attention_prefill_run(ctx, d->pqr, kc, vc, d->patt, ad, xb_o);
+    else if (d->cache_f32)
+      st = eg_attention_prefill_f32(ctx, d->pq, d->pk, d->pv, layer_cache<float>(d, d->k_cache, l),
+                                    layer_cache<float>(d, d->v_cache, l), d->pqr, d->patt, &ad);
     else st = eg_attention_prefill(ctx, d->pq, d->pk, d->pv, kc, vc, d->pqr, d->patt, &ad);
     gemm(d->patt, L.o, nullptr, d->ph[0], d->ph[1], H, H, H, 0, xb_o);  // ph1 = ph0 + o(attn)
     // RMSNorm and SiLU(gate) * up in one launch of paired gate|up tiles (pgu: the two-launch
@@ -421,11 +437,17 @@ int capture(eg_decoder* d) {
 extern "C" {
 
 int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** out_decoder) {
+  return eg_decoder_create_cache(ctx, desc, EG_CACHE_F16, out_decoder);
+}
+
+int eg_decoder_create_cache(eg_context* ctx, const eg_model_desc* desc, int cache_dtype, eg_decoder** out_decoder) {
   const char* op = "decoder_create";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
   if (!desc || !out_decoder || !desc->layer || !desc->final_norm)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
   *out_decoder = nullptr;
+  if (cache_dtype != EG_CACHE_F16 && cache_dtype != EG_CACHE_F32)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: cache dtype %d (EG_CACHE_F16 or EG_CACHE_F32)", op, cache_dtype);
   const eg_model_desc& m = *desc;
   if (m.layers == 0 || m.hidden == 0 || m.heads == 0 || m.kv_heads == 0 || m.head_dim == 0 || m.intermediate == 0 ||
       m.vocab == 0)
@@ -448,6 +470,7 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   d->desc = m;
   d->layers.assign(m.layer, m.layer + m.layers);
   d->desc.layer = d->layers.data();
+  d->cache_f32 = cache_dtype == EG_CACHE_F32;
   d->att.heads = m.heads;
   d->att.kv_heads = m.kv_heads;
   d->att.head_dim = m.head_dim;
@@ -492,8 +515,9 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
   take(rows * m.intermediate * 4, &d->pa);
   take(sizeof(eg_sample_dims), &d->sp);
   take(4, &d->rng);
-  take(d->layer_stride * m.layers * 2, &d->k_cache);
-  take(d->layer_stride * m.layers * 2, &d->v_cache);
+  const size_t cache_bytes = d->layer_stride * m.layers * (d->cache_f32 ? 4 : 2);
+  if (st == EG_OK) st = alloc(d, cache_bytes, &d->k_cache);
+  if (st == EG_OK) st = alloc(d, cache_bytes, &d->v_cache);
   if (st == EG_OK) st = eg::launch_rope_table(ctx, d->rope_table, m.max_context, m.head_dim, m.rope_theta);
   if (st != EG_OK) {
     release(d);
@@ -544,7 +568,8 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     eg_gemv_segment head[1] = {{m.embedding.packed, m.embedding.scales, m.embedding.zeros, nullptr, d->logits, m.vocab, 0}};
     st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
   }
-  if (st == EG_OK && ctx->decode_persistent) {
+  // (the persistent kernel's attention phase reads an f16 cache)
+  if (st == EG_OK && ctx->decode_persistent && !d->cache_f32) {
     std::vector<eg::LayerPlans> lp(m.layers);
     for (uint32_t l = 0; l < m.layers; l++) {
       for (int j = 0; j < 4; j++) lp[l].plan[j] = d->plans[4 * (size_t)l + j];
@@ -560,8 +585,8 @@ int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** o
     ld.k = d->kv;
     ld.v = d->kv + kvn;
     ld.partials = d->partials;
-    ld.k_cache = d->k_cache;
-    ld.v_cache = d->v_cache;
+    ld.k_cache = static_cast<uint16_t*>(d->k_cache);
+    ld.v_cache = static_cast<uint16_t*>(d->v_cache);
     ld.layer_stride = d->layer_stride;
     st = eg::layers_create(ctx, ld, &d->layers_kernel);
   }

@@ -203,6 +203,9 @@ int report_sample_failures(eg_context* ctx, const char* op);
 int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
                           const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
                           const eg_attention_dims* dims, const double* rope);
+int attention_decode_rope(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                          const float* v, float* k_cache, float* v_cache, float* partials,
+                          const eg_attention_dims* dims, const double* rope);
 
 // eg_matmul_q4_prefill with a residual added in the epilogue: out[r * out_stride + col +
 // out_offset] = sum_k x[r, k] W[col, k] + bias[col] + residual[same index] (residual nullable;

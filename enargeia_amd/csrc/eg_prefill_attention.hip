@@ -19,7 +19,12 @@
 //      long prompt: 4 x 14 workgroups walking up to 32 tiles at 2048 keys), the keys are split
 //      over grid.z: each split writes its rows' unnormalised o and (max, sum) to the context's
 //      workspace and 3. a combine launch merges the splits in split order.
+//
+// The f32 cache variant (eg_attention_prefill_f32; cache_variants.ts:21-40 generates the same
+// kernels per cache dtype) appends exact f32 rows and runs the attention as f32 FMAs: the
+// matrix cores here take f16 or bf16 operands, which would round the f32 keys and values.
 #include <algorithm>
+#include <type_traits>
 
 #include "eg_internal.hpp"
 
@@ -36,10 +41,17 @@ constexpr float kMasked = -1.0e30f;  // NEG_LARGE, cache_variants.ts
 
 using egd::float_to_half;
 
+// A value as the cache holds it: f16 bits or the f32 itself.
+template <class CT>
+__device__ __forceinline__ CT to_cache(float x) {
+  if constexpr (std::is_same<CT, float>::value) return x;
+  else return float_to_half(x);
+}
+
+template <class CT>
 __global__ __launch_bounds__(256) void rope_append_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v, float* __restrict__ q_rope,
-                                                          uint16_t* __restrict__ k_cache,
-                                                          uint16_t* __restrict__ v_cache,
+                                                          CT* __restrict__ k_cache, CT* __restrict__ v_cache,
                                                           eg_attention_prefill_dims d) {
   const uint32_t i = blockIdx.x;  // query row of the chunk
   const uint32_t pos = d.query_begin + i;
@@ -61,13 +73,112 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const float* __restric
       dst[e] = ra * scale;
       dst[e + kD / 2] = rb * scale;
     } else {
-      uint16_t* dst = k_cache + ((size_t)pos * d.kv_heads + head) * kD;
-      dst[e] = float_to_half(ra);
-      dst[e + kD / 2] = float_to_half(rb);
+      CT* dst = k_cache + ((size_t)pos * d.kv_heads + head) * kD;
+      dst[e] = to_cache<CT>(ra);
+      dst[e + kD / 2] = to_cache<CT>(rb);
     }
   }
   for (uint32_t p = tid; p < d.kv_heads * kD; p += blockDim.x)
-    v_cache[(size_t)pos * d.kv_heads * kD + p] = float_to_half(v[(size_t)i * d.kv_heads * kD + p]);
+    v_cache[(size_t)pos * d.kv_heads * kD + p] = to_cache<CT>(v[(size_t)i * d.kv_heads * kD + p]);
+}
+
+// The attention over an f32 cache. One workgroup per (query row i, kv head): the group's query
+// heads (at most kF32Group) walk the keys [0, query_begin + i] in tiles of 256, one key per
+// thread - its scores, products summed in element order - with the online softmax in f32 (the
+// tile's max and sum of exp per head by fixed-order wave and cross-wave reductions), then each
+// thread's outputs (head g, element e; two per thread) take the tile's weighted V rows in key
+// order. Keys past the query's limit weigh 0, as the reference's NEG_LARGE mask makes them.
+constexpr uint32_t kF32Tile = 256;
+constexpr uint32_t kF32Group = 8;
+
+__global__ __launch_bounds__(256) void attention_f32_kernel(const float* __restrict__ q_rope,
+                                                            const float* __restrict__ k_cache,
+                                                            const float* __restrict__ v_cache, float* __restrict__ out,
+                                                            eg_attention_prefill_dims d) {
+  __shared__ __attribute__((aligned(16))) float qs[kF32Group][kD];
+  __shared__ float pw[kF32Group][kF32Tile];  // the tile's weights e^(s - M)
+  __shared__ float red[4][kF32Group];        // per-wave maxima, then sums
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t i = blockIdx.x, kv = blockIdx.y;
+  const uint32_t G = d.heads / d.kv_heads, h0 = kv * G;
+  const uint32_t limit = d.query_begin + i;  // the last key this query sees
+  for (uint32_t t = tid; t < G * kD; t += blockDim.x) qs[t / kD][t % kD] = q_rope[((size_t)i * d.heads + h0) * kD + t];
+  __syncthreads();
+  float M[kF32Group], L[kF32Group];  // running max and sum per head (the same in every thread)
+#pragma unroll
+  for (uint32_t g = 0; g < kF32Group; g++) {
+    M[g] = -INFINITY;
+    L[g] = 0.f;
+  }
+  // this thread's outputs: (g, e) = (tid / 64, tid % 64) and (4 + tid / 64, tid % 64)
+  const uint32_t e = lane, ga = wave, gb = wave + 4;
+  float acc_a = 0.f, acc_b = 0.f;
+  const size_t row_pitch = (size_t)d.kv_heads * kD;
+  for (uint32_t t0 = 0; t0 <= limit; t0 += kF32Tile) {
+    const uint32_t key = t0 + tid;
+    const bool valid = key <= limit;
+    float s[kF32Group];
+    {
+      float4 kr[kD / 4];
+      const float4* src = reinterpret_cast<const float4*>(k_cache + (valid ? key : 0) * row_pitch + kv * kD);
+#pragma unroll
+      for (int w = 0; w < kD / 4; w++) kr[w] = src[w];
+#pragma unroll
+      for (uint32_t g = 0; g < kF32Group; g++) {
+        float a = 0.f;
+        if (g < G) {
+#pragma unroll
+          for (int w = 0; w < kD / 4; w++) {
+            const float4 qv = *reinterpret_cast<const float4*>(&qs[g][4 * w]);
+            a = fmaf(qv.x, kr[w].x, a);
+            a = fmaf(qv.y, kr[w].y, a);
+            a = fmaf(qv.z, kr[w].z, a);
+            a = fmaf(qv.w, kr[w].w, a);
+          }
+        }
+        s[g] = valid ? a : -INFINITY;
+      }
+    }
+    // the tile's max per head, then the new running max and the rescale of what came before
+    float scale[kF32Group];
+#pragma unroll
+    for (uint32_t g = 0; g < kF32Group; g++) {
+      const float m = egd::team_allmax<64>(s[g]);
+      if (lane == 0) red[wave][g] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t g = 0; g < kF32Group; g++) {
+      const float mt = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
+      const float mn = fmaxf(M[g], mt);
+      scale[g] = g < G ? expf(M[g] - mn) : 0.f;  // e^-inf = 0 on the first tile
+      M[g] = mn;
+    }
+    __syncthreads();  // red is reused below
+#pragma unroll
+    for (uint32_t g = 0; g < kF32Group; g++) {
+      const float p = valid && g < G ? expf(s[g] - M[g]) : 0.f;
+      pw[g][tid] = p;
+      const float sum = egd::team_allsum<64>(p);
+      if (lane == 0) red[wave][g] = sum;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t g = 0; g < kF32Group; g++) L[g] = fmaf(L[g], scale[g], ((red[0][g] + red[1][g]) + red[2][g]) + red[3][g]);
+    const uint32_t n = min(kF32Tile, limit + 1 - t0);
+    const float* vrow = v_cache + (size_t)t0 * row_pitch + kv * kD + e;
+    float sa = 0.f, sb = 0.f;
+    for (uint32_t j = 0; j < n; j++) {
+      const float vv = vrow[(size_t)j * row_pitch];
+      sa = fmaf(pw[ga][j], vv, sa);
+      sb = fmaf(pw[gb][j], vv, sb);
+    }
+    acc_a = fmaf(acc_a, scale[ga], sa);
+    acc_b = fmaf(acc_b, scale[gb], sb);
+    __syncthreads();  // pw and red are rewritten by the next tile
+  }
+  if (ga < G) out[((size_t)i * d.heads + h0 + ga) * kD + e] = acc_a / L[ga];
+  if (gb < G) out[((size_t)i * d.heads + h0 + gb) * kD + e] = acc_b / L[gb];
 }
 
 // Split partials: o [split][query][head][kD] (unnormalised), then m and l [split][query][head].
@@ -448,7 +559,31 @@ extern "C" int eg_attention_prefill(eg_context* ctx, const float* q, const float
   if ((reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) & 15u)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: q_rope and out must be 16-byte aligned", op);
   const eg_attention_prefill_dims& d = *dims;
-  hipLaunchKernelGGL(rope_append_kernel, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
-                     v_cache, d);
+  hipLaunchKernelGGL(rope_append_kernel<uint16_t>, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope,
+                     k_cache, v_cache, d);
   return eg::attention_prefill_run(ctx, q_rope, k_cache, v_cache, out, d);
+}
+
+extern "C" int eg_attention_prefill_f32(eg_context* ctx, const float* q, const float* k, const float* v, float* k_cache,
+                                        float* v_cache, float* q_rope, float* out,
+                                        const eg_attention_prefill_dims* dims) {
+  const char* op = "attention_prefill_f32";
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
+  if (!dims || !q || !k || !v || !k_cache || !v_cache || !q_rope || !out)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  int st = eg::check_attention_prefill(ctx, op, dims);
+  if (st != EG_OK || dims->queries == 0) return st;
+  const eg_attention_prefill_dims& d = *dims;
+  if (d.heads / d.kv_heads > kF32Group)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: %u query heads per kv head (at most %u)", op, d.heads / d.kv_heads,
+                    kF32Group);
+  if (d.kv_heads > 65535) return eg::fail(ctx, EG_ERR_RANGE, "%s: %u kv heads exceed the grid", op, d.kv_heads);
+  if ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
+       reinterpret_cast<uintptr_t>(q_rope)) & 15u)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: the caches and q_rope must be 16-byte aligned", op);
+  hipLaunchKernelGGL(rope_append_kernel<float>, dim3(d.queries), dim3(256), 0, ctx->stream, q, k, v, q_rope, k_cache,
+                     v_cache, d);
+  hipLaunchKernelGGL(attention_f32_kernel, dim3(d.queries, d.kv_heads), dim3(256), 0, ctx->stream, q_rope, k_cache,
+                     v_cache, out, d);
+  return eg::check_launch(ctx, op);
 }

@@ -10,7 +10,8 @@ class Decoder {
   /** device: a HipDevice; desc: {layers, hidden, heads, kvHeads, headDim, intermediate, vocab,
    * maxContext, rmsEps, ropeTheta, encoding, bits, blockSize, embedding: {packed, scales, zeros},
    * embedEncoding, embedBits, embedBlockSize, finalNorm, layer: [{q, k, v, o, gate, up, down,
-   * qBias, kBias, vBias, inputNorm, postAttentionNorm}]} */
+   * qBias, kBias, vBias, inputNorm, postAttentionNorm}], cacheDType?: 'f16' | 'f32'} (the KV
+   * cache's element type, SessionOptions.cacheDType; 'f16' when absent) */
   constructor(device, desc) {
     this.device = device;
     this.vocab = desc.vocab;

@@ -563,8 +563,23 @@ napi_value DecoderCreate(napi_env env, napi_callback_info info) {
     l.post_attention_norm = static_cast<const float*>(pn);
   }
   m.layer = layers.data();
+  // optional cacheDType: 'f16' (the default) or 'f32' (SessionOptions.cacheDType, session.ts:44)
+  int cache = EG_CACHE_F16;
+  bool has_cache = false;
+  if (napi_has_named_property(env, d, "cacheDType", &has_cache) == napi_ok && has_cache) {
+    napi_value cv;
+    char name[8] = {0};
+    size_t len = 0;
+    napi_get_named_property(env, d, "cacheDType", &cv);
+    if (napi_get_value_string_utf8(env, cv, name, sizeof(name), &len) != napi_ok ||
+        (std::string(name) != "f16" && std::string(name) != "f32")) {
+      napi_throw_type_error(env, "EG_ERR_INVALID", "decoderCreate: cacheDType must be 'f16' or 'f32'");
+      return nullptr;
+    }
+    cache = std::string(name) == "f32" ? EG_CACHE_F32 : EG_CACHE_F16;
+  }
   eg_decoder* dec = nullptr;
-  if (throw_status(env, ctx, eg_decoder_create(ctx, &m, &dec))) return nullptr;
+  if (throw_status(env, ctx, eg_decoder_create_cache(ctx, &m, cache, &dec))) return nullptr;
   return make_handle(env, new DecoderHandle{dec, ctx}, finalize_decoder);
 }
 

@@ -216,16 +216,22 @@ class DeviceModel:
         self.buffers = []
 
 
+CACHE_DTYPES = {"f16": 0, "f32": 1}  # EG_CACHE_F16, EG_CACHE_F32 (SessionOptions.cacheDType)
+
+
 class Decoder:
     """eg_decoder: decode steps with the token, the position, the sampler's parameters, its
-    history and the draw state on the device (greedy until set_sampling says otherwise)."""
+    history and the draw state on the device (greedy until set_sampling says otherwise).
+    cache: the KV cache dtype, "f16" (the default) or "f32"."""
 
-    def __init__(self, model: DeviceModel):
+    def __init__(self, model: DeviceModel, cache: str = "f16"):
         self.model = model
         self.device = model.device
+        self.cache = cache
         lib = _lib.load()
         h = ctypes.c_void_p()
-        check(lib.eg_decoder_create(self.device.ctx, ctypes.byref(model.desc), ctypes.byref(h)), self.device.ctx)
+        check(lib.eg_decoder_create_cache(self.device.ctx, ctypes.byref(model.desc), CACHE_DTYPES[cache],
+                                          ctypes.byref(h)), self.device.ctx)
         self.handle = h
         bufs = DecoderBuffers()
         check(lib.eg_decoder_buffers_get(h, ctypes.byref(bufs)), self.device.ctx)

@@ -304,6 +304,13 @@ typedef struct eg_attention_dims {
 EG_API int eg_attention_decode(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
                                const float* v, uint16_t* k_cache, uint16_t* v_cache, float* partials,
                                uint32_t* counter, float* out, const eg_attention_dims* dims);
+/* eg_attention_decode over caches of f32 rows (the reference's f32 cache variant: the same four
+ * attention kernels generated per cache dtype, cache_variants.ts:21-40, SessionOptions.cacheDType
+ * session.ts:44, 134): the new rows are appended exactly, every cached value is read as it is.
+ * Same arguments, partials and combine. */
+EG_API int eg_attention_decode_f32(eg_context* ctx, const uint32_t* position, const float* q, const float* k,
+                                   const float* v, float* k_cache, float* v_cache, float* partials,
+                                   uint32_t* counter, float* out, const eg_attention_dims* dims);
 /* The attention output from the partials: out[h * head_dim + d] = sum_c o_c[d] e^(m_c - M) /
  * sum_c l_c e^(m_c - M), M = max_c m_c (the reference's attn_out, [heads * head_dim]). The
  * decoder does this inside the o projection's input stage instead (EG_INPUT_ATTENTION). */
@@ -377,7 +384,8 @@ typedef struct eg_model_desc {
 typedef struct eg_decoder eg_decoder;
 
 /* Device buffers a decoder owns, for callers that fill or inspect them (the KV caches are
- * [layers][max_context][kv_heads][head_dim] f16; logits f32[vocab] (penalized in place by a
+ * [layers][max_context][kv_heads][head_dim] of f16, or of f32 for a decoder created with
+ * EG_CACHE_F32; logits f32[vocab] (penalized in place by a
  * sampled step, as the reference's sample kernel does); token u32[3] = the next input id
  * (written by each step), its logit bits (greedy steps) and the status word: the count of
  * sampled steps whose sampler gave up, which changed nothing else (cleared by the readback that
@@ -386,7 +394,7 @@ typedef struct eg_decoder eg_decoder;
  * history_length is advanced by every step and `random` holds the last step's draw; rng = the
  * mulberry32 state). */
 typedef struct eg_decoder_buffers {
-  uint16_t *k_cache, *v_cache;
+  void *k_cache, *v_cache;
   float* logits;
   float* hidden;
   uint32_t* token;
@@ -411,6 +419,16 @@ typedef struct eg_sampling_params {
  * per layer + 2, against the reference's ~19 dispatches per layer. Allocates the caches and
  * scratch. The weights stay owned by the caller and must outlive the decoder. */
 EG_API int eg_decoder_create(eg_context* ctx, const eg_model_desc* desc, eg_decoder** out_decoder);
+/* KV cache element types (SessionOptions.cacheDType, session.ts:44, 134; cacheElementBytes,
+ * cache_variants.ts:21-26). */
+#define EG_CACHE_F16 0
+#define EG_CACHE_F32 1
+/* eg_decoder_create with the cache dtype chosen (eg_decoder_create is EG_CACHE_F16): an f32 cache
+ * doubles the cache's memory and read traffic and keeps every cached key and value exact. Its
+ * steps run the attention once per layer as its own launch (the persistent layers option reads
+ * an f16 cache) and its prompt chunks append the cache rows in their own launch. */
+EG_API int eg_decoder_create_cache(eg_context* ctx, const eg_model_desc* desc, int cache_dtype,
+                                   eg_decoder** out_decoder);
 EG_API int eg_decoder_destroy(eg_decoder* decoder);
 EG_API int eg_decoder_buffers_get(eg_decoder* decoder, eg_decoder_buffers* out);
 /* Position and next input token (rows [0, position) of the caches are the history). */
@@ -486,6 +504,12 @@ typedef struct eg_attention_prefill_dims {
 EG_API int eg_attention_prefill(eg_context* ctx, const float* q, const float* k, const float* v, uint16_t* k_cache,
                                 uint16_t* v_cache, float* q_rope, float* out,
                                 const eg_attention_prefill_dims* dims);
+/* eg_attention_prefill over caches of f32 rows (cache_variants.ts:21-40 and 81-145 for the f32
+ * dtype): the rotated k and v rows are appended exactly and the attention runs on f32 FMAs
+ * with f32 operands throughout; at most 8 query heads per kv head. */
+EG_API int eg_attention_prefill_f32(eg_context* ctx, const float* q, const float* k, const float* v, float* k_cache,
+                                    float* v_cache, float* q_rope, float* out,
+                                    const eg_attention_prefill_dims* dims);
 
 /* ---- the .enargeia container (enargeia.ts:1-50, 112-240; WeightStore.loadQuantized,
  * weights.ts:299-471) ------------------------------------------------------------------------

@@ -58,18 +58,20 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, heads: int, kv_heads:
 
 
 def prefill_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
-                      begin: int, heads: int, kv_heads: int, head_dim: int, theta: float):
+                      begin: int, heads: int, kv_heads: int, head_dim: int, theta: float, cache: str = "f16"):
     """The reference's chunked prefill for one layer (graph.ts:411-459): RoPE on the chunk's q
     and k rows at positions begin + i (ops.ts:87-114), k and v written into the caches (f16
-    rows, the f16 cache variant), then per query row i the causal attention over cache rows
+    rows for the f16 cache variant, the f32 rows themselves for `cache="f32"`,
+    cache_variants.ts:21-40), then per query row i the causal attention over cache rows
     [0, begin + i] (attn_scores, softmax, attn_apply; cache_variants.ts:81-145), in float64.
-    q [n][heads*D], k / v [n][kv_heads*D]; the caches [context][kv_heads][D] (f32 arrays holding
-    f16 values) are updated in place. Returns (q_rope scaled by 1/sqrt(D), out [n][heads*D])."""
+    q [n][heads*D], k / v [n][kv_heads*D]; the caches [context][kv_heads][D] (f32 arrays) are
+    updated in place. Returns (q_rope scaled by 1/sqrt(D), out [n][heads*D])."""
     n = q.shape[0]
+    keep = f16_array if cache == "f16" else (lambda a: np.asarray(a, np.float32))
     qr = np.stack([rope(q[i], 1, heads, head_dim, theta, begin + i) for i in range(n)])
     kr = np.stack([rope(k[i], 1, kv_heads, head_dim, theta, begin + i) for i in range(n)])
-    k_cache[begin:begin + n] = f16_array(kr).reshape(n, kv_heads, head_dim)
-    v_cache[begin:begin + n] = f16_array(v).reshape(n, kv_heads, head_dim)
+    k_cache[begin:begin + n] = keep(kr).reshape(n, kv_heads, head_dim)
+    v_cache[begin:begin + n] = keep(v).reshape(n, kv_heads, head_dim)
     out = np.stack([attention(qr[i], k_cache[:begin + i + 1], v_cache[:begin + i + 1], heads, kv_heads, head_dim)
                     for i in range(n)])
     return (qr * np.float32(1.0 / np.sqrt(head_dim))).astype(np.float32), out

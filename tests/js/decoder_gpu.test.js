@@ -58,6 +58,18 @@ describe('decoder', () => {
     dec.destroy();
   });
 
+  it('runs greedy steps over an f32 KV cache', async () => {
+    const { device: dev } = await device();
+    const dec = new eg.Decoder(dev, Object.assign({}, desc, { cacheDType: 'f32' }));
+    dec.reset(0, model.manifest.first_token);
+    const tokens = [];
+    for (let s = 0; s < steps; s++) tokens.push(dec.step());
+    results.f32 = tokens;
+    dec.destroy();
+    expectThrows(() => new eg.Decoder(dev, Object.assign({}, desc, { cacheDType: 'bf16' })),
+      (e) => expect(e.code === 'EG_ERR_INVALID', e.code), 'cacheDType');
+  });
+
   it('refuses a full context, a bad token and a foreign handle', async () => {
     const { device: dev } = await device();
     const dec = new eg.Decoder(dev, desc);

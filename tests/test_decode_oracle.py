@@ -188,3 +188,35 @@ def test_prefill_attention_zero_queries_average_the_visible_rows():
         mean = visible[:begin + i + 1].astype(np.float64).mean(axis=0)
         for h in range(H):
             np.testing.assert_allclose(out[i].reshape(H, D)[h], mean[h // (H // KV)], rtol=1e-6, atol=1e-7)
+
+
+def test_prefill_attention_f32_cache_keeps_the_rows_exact():
+    """cache="f32" (the reference's f32 cache variant): the appended rows are RoPE(k) and v
+    themselves, not f16-rounded, so the first query of an empty cache returns its own value row
+    exactly and zero queries return the plain mean of the exact rows (values chosen so that f16
+    rounding would move them: an f32 cache that rounds fails both)."""
+    from oracle.decode import prefill_attention
+    H, KV, D, n, begin = 4, 2, 16, 5, 3
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((n, H * D), dtype=np.float32)
+    k = rng.standard_normal((n, KV * D), dtype=np.float32)
+    v = rng.standard_normal((n, KV * D), dtype=np.float32)
+    assert np.any(f16_array(v) != v)
+    kc = np.zeros((16, KV, D), np.float32)
+    vc = np.zeros((16, KV, D), np.float32)
+    _, out = prefill_attention(q, k, v, kc, vc, 0, H, KV, D, 1e4, cache="f32")
+    np.testing.assert_array_equal(vc[:n], v.reshape(n, KV, D))
+    for i in range(n):
+        np.testing.assert_array_equal(kc[i], oracle.rope(k[i], 1, KV, D, 1e4, i).reshape(KV, D))
+    for h in range(H):
+        np.testing.assert_allclose(out[0].reshape(H, D)[h], v.reshape(n, KV, D)[0, h // (H // KV)], rtol=1e-7, atol=0)
+    q0 = np.zeros_like(q)
+    kc = rng.standard_normal((16, KV, D), dtype=np.float32)
+    vc = rng.standard_normal((16, KV, D), dtype=np.float32)
+    visible = vc.copy()
+    visible[begin:begin + n] = v.reshape(n, KV, D)
+    _, out = prefill_attention(q0, k, v, kc, vc, begin, H, KV, D, 1e4, cache="f32")
+    for i in range(n):
+        mean = visible[:begin + i + 1].astype(np.float64).mean(axis=0)
+        for h in range(H):
+            np.testing.assert_allclose(out[i].reshape(H, D)[h], mean[h // (H // KV)], rtol=1e-6, atol=1e-7)

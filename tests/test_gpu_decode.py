@@ -37,27 +37,30 @@ def lib():
 # ---- fused attention ---------------------------------------------------------------------------
 
 
-def run_attention(device, cfg, pos, seed=0, chunk=128):
-    """q/k/v and a cache whose rows [0, pos) are random f16; returns (out, k_cache, v_cache, inputs)."""
+def run_attention(device, cfg, pos, seed=0, chunk=128, cache="f16"):
+    """q/k/v and a cache whose rows [0, pos) are random (f16, or f32 for cache="f32", through
+    eg_attention_decode_f32); returns (out, k_cache, v_cache, inputs)."""
     rng = np.random.default_rng(seed)
     H, KV, D, T = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.max_context
     q = rng.standard_normal(H * D).astype(np.float32)
     k = rng.standard_normal(KV * D).astype(np.float32)
     v = rng.standard_normal(KV * D).astype(np.float32)
-    kc = np.zeros((T, KV, D), np.float16)
-    vc = np.zeros((T, KV, D), np.float16)
-    kc[:pos] = rng.standard_normal((pos, KV, D)).astype(np.float16)
-    vc[:pos] = rng.standard_normal((pos, KV, D)).astype(np.float16)
+    ct = np.float16 if cache == "f16" else np.float32
+    kc = np.zeros((T, KV, D), ct)
+    vc = np.zeros((T, KV, D), ct)
+    kc[:pos] = rng.standard_normal((pos, KV, D)).astype(ct)
+    vc[:pos] = rng.standard_normal((pos, KV, D)).astype(ct)
+    raw = (lambda a: a.view(np.uint16)) if cache == "f16" else (lambda a: a)
     dims = attention_dims(cfg, chunk)
-    bufs = dict(q=device.upload(q), k=device.upload(k), v=device.upload(v), kc=device.upload(kc.view(np.uint16)),
-                vc=device.upload(vc.view(np.uint16)), pos=device.upload(np.array([pos], np.uint32)),
+    bufs = dict(q=device.upload(q), k=device.upload(k), v=device.upload(v), kc=device.upload(raw(kc)),
+                vc=device.upload(raw(vc)), pos=device.upload(np.array([pos], np.uint32)),
                 part=device.buffer(KV * (T // chunk) * (H // KV) * (D + 2) * 4), out=device.buffer(H * D * 4),
                 fused=device.buffer(H * D * 4), counter=device.upload(np.zeros(1, np.uint32)))
     vp = ctypes.c_void_p
-    _lib.check(lib().eg_attention_decode(device.ctx, vp(bufs["pos"].ptr), vp(bufs["q"].ptr), vp(bufs["k"].ptr),
-                                         vp(bufs["v"].ptr), vp(bufs["kc"].ptr), vp(bufs["vc"].ptr),
-                                         vp(bufs["part"].ptr), vp(bufs["counter"].ptr), vp(bufs["fused"].ptr),
-                                         ctypes.byref(dims)), device.ctx)
+    fn = lib().eg_attention_decode if cache == "f16" else lib().eg_attention_decode_f32
+    _lib.check(fn(device.ctx, vp(bufs["pos"].ptr), vp(bufs["q"].ptr), vp(bufs["k"].ptr), vp(bufs["v"].ptr),
+                  vp(bufs["kc"].ptr), vp(bufs["vc"].ptr), vp(bufs["part"].ptr), vp(bufs["counter"].ptr),
+                  vp(bufs["fused"].ptr), ctypes.byref(dims)), device.ctx)
     _lib.check(lib().eg_attention_combine(device.ctx, vp(bufs["part"].ptr), vp(bufs["out"].ptr), ctypes.byref(dims)),
                device.ctx)
     out = device.read_array(bufs["out"], np.float32, H * D)
@@ -65,8 +68,12 @@ def run_attention(device, cfg, pos, seed=0, chunk=128):
     # counter at 0 for the next launch
     np.testing.assert_array_equal(device.read_array(bufs["fused"], np.float32, H * D), out)
     assert device.read_array(bufs["counter"], np.uint32, 1)[0] == 0
-    kc_after = device.read_array(bufs["kc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
-    vc_after = device.read_array(bufs["vc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
+    if cache == "f16":
+        kc_after = device.read_array(bufs["kc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
+        vc_after = device.read_array(bufs["vc"], np.uint16, T * KV * D).view(np.float16).reshape(T, KV, D)
+    else:
+        kc_after = device.read_array(bufs["kc"], np.float32, T * KV * D).reshape(T, KV, D)
+        vc_after = device.read_array(bufs["vc"], np.float32, T * KV * D).reshape(T, KV, D)
     for b in bufs.values():
         b.release()
     return out, kc_after, vc_after, (q, k, v, kc, vc)
@@ -92,6 +99,28 @@ def test_attention_decode_matches_oracle(device, pos, chunk):
     V_all = np.concatenate([vc0[:pos].astype(np.float32), vr[None]], axis=0)
     want = attention(qr, K_all, V_all, H, KV, D)
     assert_close(out, want, ATT_TOL[0] * rms(want), ATT_TOL[1], label=f"attention pos={pos} chunk={chunk}")
+
+
+@pytest.mark.parametrize("chunk", [64, 128])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 128, 129, 1000, 2047])
+def test_attention_decode_f32_cache_matches_oracle(device, pos, chunk):
+    """The f32 cache variant: the appended value row is v itself and the key row RoPE(k) (one f32
+    ulp for the double-precision angle), not their f16 roundings; the output over the exact f32
+    rows at the same bar."""
+    cfg = ModelConfig()
+    out, kc, vc, (q, k, v, kc0, vc0) = run_attention(device, cfg, pos, seed=pos + 7, chunk=chunk, cache="f32")
+    H, KV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+    qr = oracle_rope(q, 1, H, D, cfg.rope_theta, pos)
+    kr = oracle_rope(k, 1, KV, D, cfg.rope_theta, pos).reshape(KV, D)
+    np.testing.assert_array_equal(vc[pos], v.reshape(KV, D))
+    np.testing.assert_array_max_ulp(kc[pos], kr, maxulp=1)
+    assert np.any(f16_array(v) != v)  # an f16 rounding of the row would have shown
+    np.testing.assert_array_equal(kc[:pos], kc0[:pos])
+    np.testing.assert_array_equal(vc[pos + 1:], vc0[pos + 1:])
+    K_all = np.concatenate([kc0[:pos], kr[None]], axis=0)
+    V_all = np.concatenate([vc0[:pos], v.reshape(KV, D)[None]], axis=0)
+    want = attention(qr, K_all, V_all, H, KV, D)
+    assert_close(out, want, ATT_TOL[0] * rms(want), ATT_TOL[1], label=f"f32 attention pos={pos} chunk={chunk}")
 
 
 def test_attention_rejects_unsupported_shapes(device):
@@ -266,6 +295,85 @@ def test_decoder_long_context_crosses_chunks(device, max_context, prime):
         assert dec.position() == prime + 16
     finally:
         dec.close()
+        dm.release()
+
+
+def test_decoder_f32_cache_matches_oracle(device, small_model):
+    """A decoder created with an f32 KV cache (eg_decoder_create_cache, SessionOptions.cacheDType
+    'f32') against the oracle's f32 cache: the prompt stepped position by position, then greedy
+    steps, at the decoder bar; the cache holds the steps' rows unrounded (not f16 values) and
+    equal to the oracle's within f32 sums' error."""
+    m = small_model
+    dm = DeviceModel(device, m)
+    dec = Decoder(dm, cache="f32")
+    ora = OracleDecoder(m, max_context=SMALL.max_context, cache="f32")
+    prompt = prompt_ids(24, SMALL.vocab, 0x51)
+    try:
+        for pos, tok in enumerate(prompt):
+            dec.reset(pos, tok)
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got_token, f"f32 cache prompt pos {pos}")
+        tok = got_token
+        for pos in range(len(prompt), len(prompt) + 12):
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got_token, f"f32 cache greedy pos {pos}")
+            tok = got_token
+        n = len(prompt) + 12
+        L, T, KV, D = SMALL.layers, SMALL.max_context, SMALL.kv_heads, SMALL.head_dim
+        for name, ref in (("k", ora.k), ("v", ora.v)):
+            buf = dec.buffers.k_cache if name == "k" else dec.buffers.v_cache
+            c = device.read_array(buf, np.float32, L * T * KV * D).reshape(L, T, KV, D)
+            assert np.count_nonzero(c[:, :n] != f16_array(c[:, :n])) > c[:, :n].size // 2, f"{name}: f16 values"
+            np.testing.assert_allclose(c[:, :n], ref[:, :n], rtol=1e-3, atol=1e-4 * np.abs(ref[:, :n]).max())
+    finally:
+        dec.close()
+        dm.release()
+
+
+def test_decoder_f32_cache_long_context_and_graph(device):
+    """An f32 cache primed with random f32 rows [0, 1016) of a 2048 context (16 chunks of the
+    split attention), stepping across a chunk boundary against the oracle over the same rows; the
+    same steps replayed from a captured graph give the same tokens and logits bit for bit."""
+    cfg = ModelConfig(layers=2, max_context=2048)
+    m = synthetic_model(cfg)
+    dm = DeviceModel(device, m)
+    eager, graph = Decoder(dm, cache="f32"), Decoder(dm, cache="f32")
+    ora = OracleDecoder(m, max_context=cfg.max_context, cache="f32")
+    rng = np.random.default_rng(99)
+    shape = (cfg.layers, cfg.max_context, cfg.kv_heads, cfg.head_dim)
+    kf = rng.standard_normal(shape, dtype=np.float32)
+    vf = rng.standard_normal(shape, dtype=np.float32)
+    ora.k[:], ora.v[:] = kf, vf
+    prime = 1016
+    try:
+        for d in (eager, graph):
+            device.write(d.buffers.k_cache, kf)
+            device.write(d.buffers.v_cache, vf)
+        device.sync()
+        tok = prompt_ids(1, cfg.vocab, 77)[0]
+        eager.reset(prime, tok)
+        graph.reset(prime, tok)
+        graph.capture()
+        for pos in range(prime, prime + 16):
+            a, b = eager.step(), graph.step()
+            assert a == b, f"pos {pos}: eager {a} graph {b}"
+            np.testing.assert_array_equal(eager.logits(), graph.logits())
+            check_step(eager.logits(), ora.step(tok, pos), a, f"f32 cache context 2048 pos {pos}")
+            tok = a
+    finally:
+        eager.close()
+        graph.close()
+        dm.release()
+
+
+def test_decoder_rejects_unknown_cache_dtype(device, small_model):
+    dm = DeviceModel(device, small_model)
+    h = ctypes.c_void_p()
+    try:
+        st = lib().eg_decoder_create_cache(device.ctx, ctypes.byref(dm.desc), 2, ctypes.byref(h))
+        assert st == _lib.EG_ERR_INVALID and b"cache dtype 2" in lib().eg_last_error(device.ctx)
+        assert not h.value
+    finally:
         dm.release()
 
 

@@ -27,21 +27,24 @@ class PrefillDims(ctypes.Structure):
                                                "max_context")] + [("theta", ctypes.c_float)]
 
 
-def run(device, q, k, v, kc16, vc16, begin, dims=None):
+def run(device, q, k, v, kc16, vc16, begin, dims=None, heads=H, kv_heads=KV):
+    """eg_attention_prefill over f16 caches (uint16 arrays), or eg_attention_prefill_f32 where the
+    caches given are float32 arrays."""
     n = q.shape[0]
+    f32 = kc16.dtype == np.float32
     bq, bk, bv = device.upload(q), device.upload(k), device.upload(v)
     bkc, bvc = device.upload(kc16), device.upload(vc16)
     bqr, bo = device.buffer(q.nbytes), device.buffer(q.nbytes)
-    d = dims or PrefillDims(n, begin + n, begin, H, KV, D, CTX, THETA)
+    d = dims or PrefillDims(n, begin + n, begin, heads, kv_heads, D, CTX, THETA)
     vp = ctypes.c_void_p
+    fn = _lib.load().eg_attention_prefill_f32 if f32 else _lib.load().eg_attention_prefill
     try:
-        _lib.check(_lib.load().eg_attention_prefill(device.ctx, vp(bq.ptr), vp(bk.ptr), vp(bv.ptr), vp(bkc.ptr),
-                                                    vp(bvc.ptr), vp(bqr.ptr), vp(bo.ptr), ctypes.byref(d)),
-                   device.ctx)
+        _lib.check(fn(device.ctx, vp(bq.ptr), vp(bk.ptr), vp(bv.ptr), vp(bkc.ptr), vp(bvc.ptr), vp(bqr.ptr),
+                      vp(bo.ptr), ctypes.byref(d)), device.ctx)
         return (device.read_array(bqr, np.float32, q.size).reshape(q.shape),
                 device.read_array(bo, np.float32, q.size).reshape(q.shape),
-                device.read_array(bkc, np.uint16, kc16.size).reshape(kc16.shape),
-                device.read_array(bvc, np.uint16, vc16.size).reshape(vc16.shape))
+                device.read_array(bkc, kc16.dtype, kc16.size).reshape(kc16.shape),
+                device.read_array(bvc, vc16.dtype, vc16.size).reshape(vc16.shape))
     finally:
         for b in (bq, bk, bv, bkc, bvc, bqr, bo):
             b.release()
@@ -75,6 +78,39 @@ def test_prefill_attention_matches_oracle(device, begin, n):
     np.testing.assert_array_equal(got_vc, vc.astype(np.float16).view(np.uint16))
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     assert_close(got.ravel(), want.ravel(), 1e-2 * rms, 1e-2, label=f"prefill attention begin {begin} n {n}")
+
+
+# the f32 cache variant: tiles of 256 keys; a chunk inside the first tile, one crossing several
+# tiles after cached rows, one ending at the context's end; 7 and 8 query heads per kv head
+@pytest.mark.parametrize("begin,n,heads,kv_heads", [(0, 64, H, KV), (300, 77, H, KV), (1900, 148, H, KV),
+                                                     (5, 1, H, KV), (0, 300, 16, 2), (511, 130, 8, 4)])
+def test_prefill_attention_f32_cache_matches_oracle(device, begin, n, heads, kv_heads):
+    """eg_attention_prefill_f32: q_rope as the f16 variant's; the appended rows RoPE(k) (one ulp
+    for the double-precision angle) and v exactly, f32; the output over the exact rows within
+    the decode attention's f32 bar (1e-5 x rms + 2e-5 relative: f32 FMAs and one exp per score
+    against float64)."""
+    print(f"prefill attention f32 begin {begin} queries {n} heads {heads}/{kv_heads}", flush=True)
+    rng = np.random.default_rng(2000 + begin + n)
+    q = rng.standard_normal((n, heads * D), dtype=np.float32)
+    k = rng.standard_normal((n, kv_heads * D), dtype=np.float32)
+    v = rng.standard_normal((n, kv_heads * D), dtype=np.float32)
+    kc = rng.standard_normal((CTX, kv_heads, D), dtype=np.float32)
+    vc = rng.standard_normal((CTX, kv_heads, D), dtype=np.float32)
+    got_qr, got, got_kc, got_vc = run(device, q, k, v, kc.copy(), vc.copy(), begin, heads=heads, kv_heads=kv_heads)
+    want_qr, want = prefill_attention(q, k, v, kc, vc, begin, heads, kv_heads, D, THETA, cache="f32")
+    np.testing.assert_array_max_ulp(got_qr, want_qr, maxulp=1)
+    np.testing.assert_array_max_ulp(got_kc, kc, maxulp=1)
+    np.testing.assert_array_equal(got_vc, vc)
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(got.ravel(), want.ravel(), 1e-5 * rms, 2e-5, label=f"f32 prefill attention begin {begin} n {n}")
+
+
+def test_prefill_attention_f32_rejects_wide_groups(device):
+    q = np.zeros((2, 18 * D), np.float32)
+    k = np.zeros((2, 2 * D), np.float32)
+    c = np.zeros((CTX, 2, D), np.float32)
+    with pytest.raises(_lib.EgError, match="9 query heads per kv head"):
+        run(device, q, k, k, c, c, 0, heads=18, kv_heads=2)
 
 
 def test_prefill_attention_rejects_bad_dims(device):

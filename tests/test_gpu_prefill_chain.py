@@ -130,6 +130,64 @@ def test_prefill_chain_matches_oracle(device, n, begin, chunk):
         dm.release()
 
 
+@pytest.mark.parametrize("n,begin,chunk", [(300, 0, 256), (129, 100, None)])
+def test_prefill_chain_f32_cache(device, n, begin, chunk):
+    """A decoder with an f32 KV cache: the prompt's rows are appended unrounded by the separate
+    RoPE/append launch and attended in f32 (eg_attention_prefill_f32); against the f32-cache
+    oracle stepped one position at a time, at the reference-arithmetic bars above (the
+    projections still run on bf16 operands); cached rows before the prompt (f32, not
+    f16-representable) untouched; decoding continues over the chain's rows."""
+    cfg = ModelConfig(layers=2, max_context=512)
+    m = synthetic_model(cfg)
+    dm = DeviceModel(device, m)
+    dec = Decoder(dm, cache="f32")
+    if chunk:
+        dec.set_prefill_chunk(chunk)
+    ora = OracleDecoder(m, max_context=cfg.max_context, cache="f32")
+    L, T, KV, D = cfg.layers, cfg.max_context, cfg.kv_heads, cfg.head_dim
+    try:
+        rng = np.random.default_rng(n + 5)
+        if begin:
+            shape = (L, T, KV, D)
+            kf = rng.standard_normal(shape, dtype=np.float32)
+            vf = rng.standard_normal(shape, dtype=np.float32)
+            ora.k[:], ora.v[:] = kf, vf
+            device.write(dec.buffers.k_cache, kf)
+            device.write(dec.buffers.v_cache, vf)
+            device.sync()
+        prompt = [int(t) for t in oracle.random_ids(n, 3000 + n, cfg.vocab)]
+        tok = dec.prefill(begin, prompt)
+        got = dec.logits()
+        for i, t in enumerate(prompt):
+            want = ora.step(t, begin + i)
+        err = np.abs(got.astype(np.float64) - want)
+        scale = rms(want)
+        print(f"f32 cache chain: max {err.max() / scale:.3e} x rms, rms {rms(err) / scale:.3e} x rms")
+        assert err.max() <= 0.1 * scale, f"logits max error {err.max() / scale:.3e} x rms"
+        assert rms(err) <= 2e-2 * scale, f"logits rms error {rms(err) / scale:.3e} x rms"
+        gap, best = gap_of(want)
+        if gap > 0.2 * scale:
+            assert tok == best, f"first token {tok} vs oracle {best} (gap {gap / scale:.3f} x rms)"
+        for name, ref in (("k", ora.k), ("v", ora.v)):
+            buf = dec.buffers.k_cache if name == "k" else dec.buffers.v_cache
+            c = device.read_array(buf, np.float32, L * T * KV * D).reshape(L, T, KV, D)
+            rows = slice(begin, begin + n)
+            rel = np.abs(c[:, rows] - ref[:, rows]).max() / np.abs(ref[:, rows]).max()
+            assert rel <= 2e-2, f"{name} cache rows off by {rel:.3e}"
+            assert np.count_nonzero(c[:, rows] != c[:, rows].astype(np.float16)) > c[:, rows].size // 2
+            np.testing.assert_array_equal(c[:, :begin], ref[:, :begin])
+        for s in range(4):
+            pos = begin + n + s
+            got_tok = dec.step()
+            want = ora.step(tok, pos)
+            e = np.abs(dec.logits().astype(np.float64) - want).max() / rms(want)
+            assert e <= 5e-2, f"decode at {pos} after the prompt: {e:.3e} x rms"
+            tok = got_tok
+    finally:
+        dec.close()
+        dm.release()
+
+
 def test_prefill_chain_config4(device):
     """The config-4 run at full size: the 32-token prompt through the chain at positions
     1888..1919 over the primed cache, its first token and logits against the oracle's run

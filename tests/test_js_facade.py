@@ -86,7 +86,7 @@ def _write_model(host, directory):
 @pytest.mark.gpu
 def test_node_decoder_matches_python_decoder(tmp_path, device):
     """The same model driven from Node (N-API decoder binding) and from Python (ctypes) gives the
-    same greedy tokens, eagerly and as a replayed graph."""
+    same greedy tokens, eagerly and as a replayed graph, and over an f32 KV cache."""
     import json
 
     from enargeia_amd.model import Decoder, DeviceModel, ModelConfig, synthetic_model
@@ -103,14 +103,19 @@ def test_node_decoder_matches_python_decoder(tmp_path, device):
     node_tokens = json.loads(next(line for line in res.stdout.splitlines() if line.startswith('{"eager"')))
     dm = DeviceModel(device, host)
     dec = Decoder(dm)
+    dec32 = Decoder(dm, cache="f32")
     try:
         dec.reset(0, manifest["first_token"])
         py_tokens = [dec.step() for _ in range(steps)]
+        dec32.reset(0, manifest["first_token"])
+        py_tokens32 = [dec32.step() for _ in range(steps)]
     finally:
         dec.close()
+        dec32.close()
         dm.release()
     assert node_tokens["eager"] == py_tokens
     assert node_tokens["graph"] == py_tokens
+    assert node_tokens["f32"] == py_tokens32
 
 
 @needs_node
