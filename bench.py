@@ -376,6 +376,8 @@ def main() -> int:
                                            "int8 GEMV; `us` above adds the argmax finalize launch"},
                     "sampled_token_us": round(sampled_us, 2),
                     "sampled_token_fused_us": round(hn["sampled_fused_us"], 2),
+                    "dense_tables": dict(hn["dense"], config="the same head over an f16 / f32 table "
+                                                             "(lm_head_f16 / lm_head_f32), GEMV alone"),
                     "sampled_config": "LM head + sampler, T 0.7 / top-p 0.9 / penalty 1.1, 512-id history: "
                                       "sampled_token_us through the reference's two ops (lm_head_q8, sample), "
                                       "sampled_token_fused_us through eg_lm_head_sample (the head hands the "
@@ -514,7 +516,36 @@ def head_numbers(dev, ev, stream, args, rng) -> dict:
     for a, b in heads:
         a.release()
         b.release()
-    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us, "sampled_fused_us": fused_us, "gemv_us": plain_us}
+
+    # the same head shape over an f16 and an f32 table (the reference's 'f16' / 'f32' embedding
+    # dtypes): the head GEMV alone, one table (272 / 545 MB, past the 256 MB Infinity Cache)
+    dense = {}
+    for dtype, bits in (("f16", 16), ("f32", 32)):
+        t = quant.dense_table(quant.normal(VOCAB * HIDDEN, 0x5EED ^ 0x1000, 0.02), VOCAB, HIDDEN, bits)
+        bt = dev.upload(t.packed)
+        nbytes = t.packed.nbytes + HIDDEN * 4 + VOCAB * 4
+        del t
+        dk = K.ComputeKernel(dev, K.embedding_head_spec(dtype))
+
+        def dense_head(i):
+            hu = dk.uniform()
+            hu.write(dims)
+            dk.encode(dk.bind_group([h, bt, None, None, logits, hu]), (1, 1, 1))
+
+        for i in range(args.warmup):
+            dense_head(i)
+        es = [ev.create() for _ in range(args.steps + 1)]
+        ev.record(es[0], stream)
+        for i in range(args.steps):
+            dense_head(i)
+            ev.record(es[i + 1], stream)
+        ev.sync(es[-1])
+        us = float(np.median([ev.ms(es[i], es[i + 1]) for i in range(args.steps)])) * 1e3
+        dense[dtype] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes}
+        log(f"lm_head_{dtype} GEMV: {us:.1f} us, {dense[dtype]['gbs']:.0f} GB/s")
+        bt.release()
+    return {"us": head_us, "gbs": head_gbs, "sampled_us": sampled_us, "sampled_fused_us": fused_us, "gemv_us": plain_us,
+            "dense": dense}
 
 
 def decode_throughput(dev, ev, stream, args, modes=("eager", "graph")) -> dict:

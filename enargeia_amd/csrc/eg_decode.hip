@@ -37,20 +37,9 @@ __global__ __launch_bounds__(kThreads) void embed_gather_kernel(const uint32_t* 
   const uint32_t id = token[0];
   if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
   const uint32_t row = id - d.row_begin;
-  const uint32_t per_word = 32u / (uint32_t)bits;
-  const uint32_t mask = (1u << bits) - 1u;
   for (uint32_t i = threadIdx.x; i < d.hidden; i += blockDim.x) {
-    const uint64_t e = (uint64_t)row * d.hidden + i;
-    uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
-    const uint32_t blk = row * d.blocks_per_row + i / d.block_size;
-    float zero;
-    if (encoding == EG_ENC_OFFSET_ZEROS) {
-      zero = (float)((zeros[blk / per_word] >> (bits * (blk % per_word))) & mask);
-    } else {
-      code ^= 1u << (bits - 1);  // two's complement -> offset binary
-      zero = (float)(1u << (bits - 1));
-    }
-    out[d.out_offset + i] = ((float)code - zero) * scales[blk];
+    const uint64_t blk = bits >= 16 ? 0 : (uint64_t)row * d.blocks_per_row + i / d.block_size;
+    out[d.out_offset + i] = egd::table_value(packed, scales, zeros, (uint64_t)row * d.hidden + i, blk, encoding, bits);
   }
 }
 
@@ -252,6 +241,11 @@ __global__ __launch_bounds__(kThreads) void step_tail_kernel(eg::StepTail t, uin
   }
   if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
   const uint32_t row = id - d.row_begin;
+  if (bits >= 16) {  // an f16 or f32 table
+    for (uint32_t i = tid; i < d.hidden; i += blockDim.x)
+      emb[d.out_offset + i] = egd::table_value(packed, scales, zeros, (uint64_t)row * d.hidden + i, 0, encoding, bits);
+    return;
+  }
   const uint32_t per_word = 32u / (uint32_t)bits;
   const uint32_t mask = (1u << bits) - 1u;
   if (d.block_size % per_word == 0 && (uint64_t)d.hidden * bits % 32 == 0) {
@@ -344,18 +338,23 @@ int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* pack
                     const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding, int bits) {
   const char* op = "embed_gather";
   if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", op);
-  if (!token || !packed || !scales || !out || !dims) return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
-  if (bits != 4 && bits != 8) return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8", op);
-  if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", op, encoding);
-  if (encoding == EG_ENC_OFFSET_ZEROS && !zeros) return eg::fail(ctx, EG_ERR_INVALID, "%s: zeros is NULL", op);
+  const bool dense = bits == 16 || bits == 32;  // an f16 / f32 table: no scales, zeros or blocks
+  if (!token || !packed || !out || !dims || (!dense && !scales))
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
+  if (bits != 4 && bits != 8 && !dense)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4, 8, 16 (f16 table) or 32 (f32 table), got %d", op, bits);
   if (dims->seq != 1) return eg::fail(ctx, EG_ERR_INVALID, "%s: seq %u (decode gathers one token)", op, dims->seq);
-  if (dims->block_size == 0 || dims->hidden % dims->block_size != 0 ||
-      dims->blocks_per_row != dims->hidden / dims->block_size)
-    return eg::fail(ctx, EG_ERR_INVALID, "%s: hidden %u / block %u / blocksPerRow %u disagree", op, dims->hidden,
-                    dims->block_size, dims->blocks_per_row);
+  if (!dense) {
+    if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", op, encoding);
+    if (encoding == EG_ENC_OFFSET_ZEROS && !zeros) return eg::fail(ctx, EG_ERR_INVALID, "%s: zeros is NULL", op);
+    if (dims->block_size == 0 || dims->hidden % dims->block_size != 0 ||
+        dims->blocks_per_row != dims->hidden / dims->block_size)
+      return eg::fail(ctx, EG_ERR_INVALID, "%s: hidden %u / block %u / blocksPerRow %u disagree", op, dims->hidden,
+                      dims->block_size, dims->blocks_per_row);
+  }
   hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, token, packed, scales,
-                     encoding == EG_ENC_SIGNED ? nullptr : zeros, out, *dims, encoding, bits);
+                     dense || encoding == EG_ENC_SIGNED ? nullptr : zeros, out, *dims, encoding, bits);
   return eg::check_launch(ctx, op);
 }
 

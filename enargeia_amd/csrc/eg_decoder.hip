@@ -132,8 +132,9 @@ eg_embedding_dims embedding_dims_of(const eg_model_desc& m) {
   ed.hidden = m.hidden;
   ed.row_begin = 0;
   ed.row_count = m.vocab;
-  ed.block_size = m.embed_block_size;
-  ed.blocks_per_row = m.hidden / m.embed_block_size;
+  // an f16 / f32 table has no blocks: the fields describe one block per row
+  ed.block_size = m.embed_bits >= 16 ? m.hidden : m.embed_block_size;
+  ed.blocks_per_row = m.hidden / ed.block_size;
   ed.grid_width = 1;
   return ed;
 }
@@ -456,7 +457,14 @@ int eg_decoder_create_cache(eg_context* ctx, const eg_model_desc* desc, int cach
     return eg::fail(ctx, EG_ERR_INVALID, "%s: max_context %u is not a positive multiple of 128", op, m.max_context);
   if (m.heads * m.head_dim != m.hidden)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: heads %u x head_dim %u != hidden %u", op, m.heads, m.head_dim, m.hidden);
-  if (!matrix_ok(m.embedding, m.embed_encoding) || m.embed_block_size == 0 || m.hidden % m.embed_block_size != 0)
+  // the tied table: codes of 4 or 8 bits with their scales (and zero-points), or an f16 (bits
+  // 16) / f32 (bits 32) table as it is (embedding_variants.ts:26-74)
+  const bool dense_table = m.embed_bits == 16 || m.embed_bits == 32;
+  if (m.embed_bits != 4 && m.embed_bits != 8 && !dense_table)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: embedding bits %d (4, 8, 16 or 32)", op, m.embed_bits);
+  if (dense_table ? !m.embedding.packed
+                  : !matrix_ok(m.embedding, m.embed_encoding) || m.embed_block_size == 0 ||
+                        m.hidden % m.embed_block_size != 0)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: bad embedding table", op);
   for (uint32_t l = 0; l < m.layers; l++) {
     const eg_layer_desc& L = m.layer[l];
@@ -564,7 +572,7 @@ int eg_decoder_create_cache(eg_context* ctx, const eg_model_desc* desc, int cach
   // an int4 LM head storing logits for the sampler: a one-matrix plan with the final norm as its
   // input stage (plans need rows in multiples of 8; other vocabularies use the fused-argmax head
   // and ignore its partials; an int8 head leaves the sampler its partials instead)
-  if (st == EG_OK && m.vocab % 8 == 0 && m.embed_bits != 8) {
+  if (st == EG_OK && m.vocab % 8 == 0 && m.embed_bits == 4) {
     eg_gemv_segment head[1] = {{m.embedding.packed, m.embedding.scales, m.embedding.zeros, nullptr, d->logits, m.vocab, 0}};
     st = eg_gemv_plan_create(ctx, m.hidden, m.embed_block_size, m.embed_encoding, m.embed_bits, head, 1, &d->head_plan);
   }

@@ -80,6 +80,145 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
   }
 }
 
+// The LM head over an f16 (BITS 16) or f32 (BITS 32) tied table (the 'f16' / 'f32' dtypes of
+// embedding_variants.ts:46-74, 135-180): out[n] = sum_k x[k] table[n][k]. With no codes to
+// unpack the launch streams the table: one wave per row, two rows per step (their loads issued
+// together), grid-stride over the rows; x in LDS, RMS-normalised there when the final norm is
+// fused (NORM, the quantized input stage's arithmetic and order, so the same bits); the row as
+// 16-byte vectors (VEC; 8 halves or 4 floats, element 2j of an f16 pair in the low half), each
+// lane's products summed in element order, then the wave's DPP sum. VEC false reads element by
+// element (a row that is not a whole number of vectors, or an unaligned table). ARGMAX leaves
+// one (value bits, index) partial per workgroup, as gemv_generic_kernel does.
+constexpr uint32_t kDenseMaxK = 16384;  // x in LDS: 64 KiB
+
+template <int BITS>
+__device__ __forceinline__ float dense_dot(const uint4 w, const float* xv, float acc) {
+  if constexpr (BITS == 32) {
+    const float4 a = *reinterpret_cast<const float4*>(xv);
+    acc = fmaf(__uint_as_float(w.x), a.x, acc);
+    acc = fmaf(__uint_as_float(w.y), a.y, acc);
+    acc = fmaf(__uint_as_float(w.z), a.z, acc);
+    return fmaf(__uint_as_float(w.w), a.w, acc);
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(xv), b = *reinterpret_cast<const float4*>(xv + 4);
+    acc = fmaf(egd::half_to_float((uint16_t)w.x), a.x, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)(w.x >> 16)), a.y, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)w.y), a.z, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)(w.y >> 16)), a.w, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)w.z), b.x, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)(w.z >> 16)), b.y, acc);
+    acc = fmaf(egd::half_to_float((uint16_t)w.w), b.z, acc);
+    return fmaf(egd::half_to_float((uint16_t)(w.w >> 16)), b.w, acc);
+  }
+}
+
+template <int BITS, bool ARGMAX, bool NORM, bool VEC>
+__global__ __launch_bounds__(256) void dense_head_kernel(const float* __restrict__ x, const float* __restrict__ norm_w,
+                                                         float eps, const uint32_t* __restrict__ table, float* out,
+                                                         uint32_t n, uint32_t k, uint32_t out_offset,
+                                                         uint32_t* partials) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  if (NORM) {  // k is a multiple of 4, x and the weight 16-byte aligned (checked on the host)
+    __shared__ float red[kWaves];
+    const uint32_t n4 = k / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+    float ss = 0.f;
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+      const float4 v = x4[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) total += red[w];
+    const float inv = 1.0f / sqrtf(total / (float)k + eps);
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+      const float4 v = x4[i], g = w4[i];
+      reinterpret_cast<float4*>(xs)[i] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+    }
+  } else {
+    for (uint32_t i = tid; i < k; i += blockDim.x) xs[i] = x[i];
+  }
+  __syncthreads();
+  constexpr uint32_t kEpv = 128u / BITS;  // elements per 16-byte vector
+  constexpr int kBatch = 2;               // vectors per lane and row issued before any is used
+  const uint32_t wave = blockIdx.x * kWaves + (tid >> 6), waves = gridDim.x * kWaves;
+  float best_v = -1.0e30f;
+  uint32_t best_i = out_offset;
+  for (uint32_t r0 = wave; r0 < n; r0 += 2 * waves) {
+    const uint32_t rows[2] = {r0, r0 + waves};
+    float acc[2] = {0.f, 0.f};
+    if (VEC) {
+      const uint32_t vecs = k / kEpv;
+      for (uint32_t v0 = lane; v0 < vecs; v0 += 64u * kBatch) {
+        uint4 w[2][kBatch];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+          for (int b = 0; b < kBatch; b++) {
+            const uint32_t v = v0 + 64u * b;
+            w[r][b] = rows[r] < n && v < vecs ? reinterpret_cast<const uint4*>(table)[(size_t)rows[r] * vecs + v]
+                                              : make_uint4(0u, 0u, 0u, 0u);
+          }
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+          for (int b = 0; b < kBatch; b++) {
+            const uint32_t v = v0 + 64u * b;
+            if (v < vecs) acc[r] = dense_dot<BITS>(w[r][b], xs + v * kEpv, acc[r]);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        if (rows[r] < n)
+          for (uint32_t i = lane; i < k; i += 64)
+            acc[r] = fmaf(egd::table_value(table, nullptr, nullptr, (uint64_t)rows[r] * k + i, 0, 0, BITS), xs[i],
+                          acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const float v = egd::team_sum<64>(acc[r]);
+      if (lane == 63 && rows[r] < n) {
+        if (out) out[rows[r] + out_offset] = v;
+        if (ARGMAX && egd::better(v, rows[r] + out_offset, best_v, best_i)) {
+          best_v = v;
+          best_i = rows[r] + out_offset;
+        }
+      }
+    }
+  }
+  if (ARGMAX) {
+    __shared__ float wv[kWaves];
+    __shared__ uint32_t wi[kWaves];
+    egd::team_argmax<64>(best_v, best_i);
+    if (lane == 0) {
+      wv[tid >> 6] = best_v;
+      wi[tid >> 6] = best_i;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float bv = wv[0];
+      uint32_t bi = wi[0];
+      for (int q = 1; q < kWaves; q++)
+        if (egd::better(wv[q], wi[q], bv, bi)) {
+          bv = wv[q];
+          bi = wi[q];
+        }
+      partials[2 * blockIdx.x] = __float_as_uint(bv);
+      partials[2 * blockIdx.x + 1] = bi;
+    }
+  }
+}
+
 // Instantiated (TEAM, CPL, U, NB) shapes: one chunk slot per lane for rows of up to 64 chunks
 // (TEAM the next power of two), a full-wave team with 2-4 slots for longer rows. The library
 // picks NB = 2 (a deeper pipeline costs resident waves and duplicate tail tiles) except for
@@ -225,6 +364,7 @@ struct QuantView {
   const uint32_t* history = nullptr;
   uint32_t* clear = nullptr;  // zeroed by workgroup 0 (clear_words words)
   uint32_t clear_words = 0;
+  bool table = false;  // an LM head: f16 (bits 16) and f32 (bits 32) tables are taken too
 };
 
 // LDS the input stage needs beyond x and the segment table.
@@ -299,7 +439,56 @@ int validate(eg_context* ctx, const QuantView& v) {
   return EG_OK;
 }
 
+// An LM head over an f16 or f32 table (dense_head_kernel).
+int launch_dense(eg_context* ctx, const QuantView& v) {
+  if (!ctx) return eg::fail(nullptr, EG_ERR_INVALID, "%s: ctx is NULL", v.op);
+  if (!v.x || !v.packed) return eg::fail(ctx, EG_ERR_INVALID, "%s: x and the table are required", v.op);
+  if (!v.out && !v.result) return eg::fail(ctx, EG_ERR_INVALID, "%s: out is NULL", v.op);
+  if (v.sample_dev || v.sample_host)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: the sampling statistics need an int8 head", v.op);
+  const bool norm = v.input && v.input->kind == EG_INPUT_RMSNORM;
+  if (v.input && v.input->kind != EG_INPUT_VECTOR && !norm)
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: an f16 / f32 head takes x as given or after an RMSNorm", v.op);
+  if (v.k > kDenseMaxK)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: hidden %u over the %u an f16 / f32 head holds", v.op, v.k, kDenseMaxK);
+  const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (norm && (!v.input->x2 || v.k % 4 != 0 || !aligned(v.x) || !aligned(v.input->x2)))
+    return eg::fail(ctx, EG_ERR_INVALID,
+                    "%s: the fused RMSNorm needs its weight, hidden a multiple of 4 and 16-byte aligned vectors", v.op);
+  if (((uint64_t)v.out_offset + v.n) * 4 >= (1ull << 32))
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: rows up to %llu exceed the output range", v.op,
+                    (unsigned long long)v.out_offset + v.n);
+  if (v.n == 0) return v.result ? eg::fail(ctx, EG_ERR_INVALID, "%s: argmax over zero rows", v.op) : EG_OK;
+  const bool argmax = v.result != nullptr;
+  const bool vec = aligned(v.packed) && ((uint64_t)v.k * v.bits) % 128 == 0;
+  uint64_t blocks = ((uint64_t)v.n + 2 * kWaves - 1) / (2 * kWaves);
+  blocks = std::min<uint64_t>(blocks, (uint64_t)ctx->cu_count * 8);
+  uint32_t* partials = v.partials ? v.partials : reinterpret_cast<uint32_t*>(eg::partials(ctx));
+  const size_t partials_cap = v.partials ? v.partials_bytes : eg::kPartialsBytes;
+  if (argmax && blocks * 8 > partials_cap)
+    return eg::fail(ctx, EG_ERR_RANGE, "%s: %llu workgroups' partials exceed the %zu-byte buffer", v.op,
+                    (unsigned long long)blocks, partials_cap);
+  using Fn = void (*)(const float*, const float*, float, const uint32_t*, float*, uint32_t, uint32_t, uint32_t,
+                      uint32_t*);
+#define EG_DENSE(B, A, N) (vec ? (Fn)dense_head_kernel<B, A, N, true> : (Fn)dense_head_kernel<B, A, N, false>)
+#define EG_DENSE_B(B) (argmax ? (norm ? EG_DENSE(B, true, true) : EG_DENSE(B, true, false)) \
+                              : (norm ? EG_DENSE(B, false, true) : EG_DENSE(B, false, false)))
+  const Fn fn = v.bits == 16 ? EG_DENSE_B(16) : EG_DENSE_B(32);
+#undef EG_DENSE_B
+#undef EG_DENSE
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), std::max<uint32_t>(v.k, 4) * 4u, ctx->stream, v.x,
+                     norm ? v.input->x2 : nullptr, norm ? v.input->eps : 0.f, v.packed, v.out, v.n, v.k,
+                     v.out_offset, partials);
+  if (argmax && v.groups_out) *v.groups_out = (uint32_t)blocks;
+  else if (argmax) eg::launch_argmax_finalize(ctx, partials, (uint32_t)blocks, v.out_offset, v.result);
+  return eg::check_launch(ctx, v.op);
+}
+
 int launch(eg_context* ctx, const QuantView& v) {
+  if (v.bits == 16 || v.bits == 32) {
+    if (v.table) return launch_dense(ctx, v);
+    return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4 or 8, got %d", v.op, v.bits);
+  }
   int st = validate(ctx, v);
   if (st != EG_OK) return st;
   if (v.n == 0) {
@@ -455,6 +644,7 @@ int eg_lm_head(eg_context* ctx, const float* x, const uint32_t* packed, const fl
   QuantView v{bits == 4 ? "lm_head_q4" : "lm_head_q8", x, packed, scales,
               encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out, dims->row_count, dims->hidden,
               dims->block_size, dims->blocks_per_row, dims->out_offset, encoding, bits, nullptr};
+  v.table = true;
   return launch(ctx, v);
 }
 
@@ -466,6 +656,7 @@ int eg_lm_head_argmax(eg_context* ctx, const float* x, const uint32_t* packed, c
   QuantView v{"lm_head_argmax", x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
               dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
               bits, result};
+  v.table = true;
   if (ctx) {
     const uint64_t max_groups = eg::kPartialsBytes / 8;
     if ((uint64_t)ctx->cu_count * 8 > max_groups)
@@ -486,6 +677,7 @@ int eg_lm_head_argmax_noalloc(eg_context* ctx, const float* x, const uint32_t* p
               dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding, bits, result};
   v.partials = static_cast<uint32_t*>(ctx->noalloc_scratch);
   v.partials_bytes = kNoAllocScratchBytes;
+  v.table = true;
   return launch(ctx, v);
 }
 
@@ -498,6 +690,7 @@ int eg_lm_head_argmax_input(eg_context* ctx, const eg_gemv_input* input, const u
   QuantView v{"lm_head_argmax", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
               dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
               bits, result, input};
+  v.table = true;
   return launch(ctx, v);
 }
 
@@ -511,6 +704,7 @@ int eg::lm_head_argmax_partials(eg_context* ctx, const eg_gemv_input* input, con
   QuantView v{"lm_head_argmax", input->x, packed, scales, encoding == EG_ENC_SIGNED ? nullptr : zeros, nullptr, out,
               dims->row_count, dims->hidden, dims->block_size, dims->blocks_per_row, dims->out_offset, encoding,
               bits, partials, input, groups};
+  v.table = true;
   return launch(ctx, v);
 }
 

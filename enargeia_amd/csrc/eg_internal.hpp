@@ -639,6 +639,27 @@ __device__ __forceinline__ float mulberry32_next(uint32_t* state) {
 __device__ __forceinline__ float half_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t float_to_half(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// Element e (= row * hidden + column) of a tied table as f32, per storage format
+// (embedding_variants.ts:46-74 weightAt): bits 4 / 8 are codes with the scale of quant block
+// `blk` (minus its zero-point for EG_ENC_OFFSET_ZEROS, two's complement for EG_ENC_SIGNED);
+// bits 16 an f16 table (two halves per word, element 2j in the low half, as unpack2x16float
+// reads it); bits 32 an f32 table. scales and zeros are not read for 16 and 32.
+__device__ __forceinline__ float table_value(const uint32_t* packed, const float* scales, const uint32_t* zeros,
+                                            uint64_t e, uint64_t blk, int encoding, int bits) {
+  if (bits == 32) return __uint_as_float(packed[e]);
+  if (bits == 16) return half_to_float((uint16_t)(packed[e >> 1] >> (16u * (uint32_t)(e & 1u))));
+  const uint32_t per_word = 32u / (uint32_t)bits, mask = (1u << bits) - 1u;
+  uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
+  float zero;
+  if (encoding == EG_ENC_OFFSET_ZEROS) {
+    zero = (float)((zeros[blk / per_word] >> (bits * (uint32_t)(blk % per_word))) & mask);
+  } else {
+    code ^= 1u << (bits - 1);  // two's complement -> offset binary
+    zero = (float)(1u << (bits - 1));
+  }
+  return ((float)code - zero) * scales[blk];
+}
+
 // RoPE (ops.ts:87-114): pairs (i, i + D/2) rotated by angle = position * theta^(-2i/D). The
 // angle, its cosine and sine are computed once per frequency, in double precision like the CPU
 // reference, and the rotation itself is evaluated in double too.

@@ -15,21 +15,10 @@ __global__ __launch_bounds__(kThreads) void embed_rows_kernel(const uint32_t* id
                                                               int bits, float* out) {
   const uint32_t r = blockIdx.x;
   const uint32_t id = ids[r];
-  const uint32_t per_word = 32u / (uint32_t)bits;
-  const uint32_t mask = (1u << bits) - 1u;
-  const uint32_t bpr = hidden / block_size;
+  const uint32_t bpr = bits >= 16 ? 0 : hidden / block_size;
   for (uint32_t i = threadIdx.x; i < hidden; i += kThreads) {
-    const uint64_t e = (uint64_t)id * hidden + i;
-    uint32_t code = (packed[e / per_word] >> (bits * (uint32_t)(e % per_word))) & mask;
-    const uint64_t blk = (uint64_t)id * bpr + i / block_size;
-    float zero;
-    if (encoding == EG_ENC_OFFSET_ZEROS) {
-      zero = (float)((zeros[blk / per_word] >> (bits * (uint32_t)(blk % per_word))) & mask);
-    } else {
-      code ^= 1u << (bits - 1);
-      zero = (float)(1u << (bits - 1));
-    }
-    out[(size_t)r * hidden + i] = ((float)code - zero) * scales[blk];
+    const uint64_t blk = bits >= 16 ? 0 : (uint64_t)id * bpr + i / block_size;
+    out[(size_t)r * hidden + i] = egd::table_value(packed, scales, zeros, (uint64_t)id * hidden + i, blk, encoding, bits);
   }
 }
 
@@ -94,7 +83,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int eg::embed_rows(eg_context* ctx, const uint32_t* ids, uint32_t rows, const uint32_t* packed, const float* scales,
                    const uint32_t* zeros, uint32_t hidden, uint32_t block_size, int encoding, int bits, float* out) {
   if (rows == 0) return EG_OK;
-  if (rows > 65535 || block_size == 0 || hidden % block_size != 0)
+  if (rows > 65535 || (bits < 16 && (block_size == 0 || hidden % block_size != 0)))
     return eg::fail(ctx, EG_ERR_INVALID, "embed_rows: %u rows of %u in blocks of %u", rows, hidden, block_size);
   hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(kThreads), 0, ctx->stream, ids, packed, scales,
                      encoding == EG_ENC_SIGNED ? nullptr : zeros, hidden, block_size, encoding, bits, out);

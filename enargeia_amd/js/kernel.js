@@ -32,6 +32,8 @@ const DISPATCH = {
   matmul_q4_prefill: (ctx, p, u, s) => native.matmulQ4Prefill(ctx, p[0], p[1], p[2], p[3], p[4], p[5], u, s.encoding, s.bits),
   lm_head_q4: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
   lm_head_q8: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  lm_head_f16: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  lm_head_f32: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
   argmax: (ctx, p, u) => native.argmax(ctx, p[0], p[1], u),
   sample: (ctx, p, u) => native.sample(ctx, p[0], p[1], p[2], u),
 };

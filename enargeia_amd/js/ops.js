@@ -39,10 +39,10 @@ function withFormat(spec, bits, encoding) {
   return Object.freeze(Object.assign({}, spec, { bits, encoding }));
 }
 
-/** embeddingHeadSpec (embedding_variants.ts:195-203) for the quantized dtypes. */
+/** embeddingHeadSpec (embedding_variants.ts:195-203): q4 and q8 codes, or an f16 / f32 table. */
 function embeddingHeadSpec(dtype, encoding) {
-  const bits = { q4: 4, q8: 8 }[dtype];
-  if (!bits) throw new Error(`lm_head_${dtype}: only q4 and q8 heads run on this path`);
+  const bits = { q4: 4, q8: 8, f16: 16, f32: 32 }[dtype];
+  if (!bits) throw new Error(`lm_head_${dtype}: the dtypes are q4, q8, f16 and f32`);
   return Object.freeze({
     name: `lm_head_${dtype}`, bindings: EMBED_BINDINGS, workgroupSize: [64, 1, 1], uniformBytes: 48,
     bits, encoding: encoding === undefined ? ENCODING.OFFSET_ZEROS : encoding,

@@ -236,10 +236,11 @@ _EMBED_BINDINGS = ("read", "read", "read", "read", "read_write", "uniform")
 
 
 def embedding_head_spec(dtype: str, encoding: int = ENC_OFFSET_ZEROS) -> KernelSpec:
-    """embeddingHeadSpec (embedding_variants.ts:195-203) for the quantized dtypes."""
-    bits = {"q4": 4, "q8": 8}.get(dtype)
+    """embeddingHeadSpec (embedding_variants.ts:195-203): q4 and q8 codes, or an f16 / f32 table
+    (bits 16 / 32; scales and zeros unused)."""
+    bits = {"q4": 4, "q8": 8, "f16": 16, "f32": 32}.get(dtype)
     if bits is None:
-        raise EgError(_lib.EG_ERR_INVALID, f"lm_head_{dtype}: only q4 and q8 heads run on this path")
+        raise EgError(_lib.EG_ERR_INVALID, f"lm_head_{dtype}: the dtypes are q4, q8, f16 and f32")
     return KernelSpec(f"lm_head_{dtype}", _EMBED_BINDINGS, (64, 1, 1), 48, bits, encoding)
 
 
@@ -380,6 +381,8 @@ _DISPATCH = {
     "matmul_q4_prefill": lambda k, p, r: _matmul(k, p, r, "eg_matmul_q4_prefill"),
     "lm_head_q4": _lm_head,
     "lm_head_q8": _lm_head,
+    "lm_head_f16": _lm_head,
+    "lm_head_f32": _lm_head,
     "argmax": _argmax,
     "sample": _sample,
 }

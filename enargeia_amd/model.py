@@ -18,7 +18,7 @@ import numpy as np
 from . import _lib
 from ._lib import ENC_SIGNED, check
 from .kernels import Device
-from .quant import QuantTensor, normal, quantize_asym, quantize_sym
+from .quant import QuantTensor, dense_table, normal, quantize_asym, quantize_sym
 
 
 @dataclass(frozen=True)
@@ -70,11 +70,13 @@ def seed_for(layer: int, slot: int, base: int = 0x5EED) -> int:
     return base ^ (layer * 16 + slot)
 
 
-def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED, fmt: str = "sym") -> HostModel:
+def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED, fmt: str = "sym",
+                    embed_dtype: str = "q8") -> HostModel:
     """Random-init weights of the model's shape. fmt "sym": the BASELINE formats (int4 with an
     f32 scale per cfg.group weights, int8 per-row table, norms 1). fmt "reference": the
     reference quantizer's formats (asymmetric int4 / int8 in blocks of cfg.group with zero-points,
-    quantize.py:74-103, --embed-dtype q8) and norm weights drawn around 1."""
+    quantize.py:74-103, --embed-dtype q8) and norm weights drawn around 1. embed_dtype "f16" or
+    "f32" stores the tied table as it is (--embed-dtype f16 / f32) instead of int8."""
     layers = []
     ref = fmt == "reference"
     for layer in range(cfg.layers):
@@ -93,8 +95,11 @@ def synthetic_model(cfg: ModelConfig = QWEN25_05B, base: int = 0x5EED, fmt: str 
             n2 = n1.copy()
         layers.append(HostLayer(mats, biases, n1, n2))
     table = normal(cfg.vocab * cfg.hidden, base ^ 0x1000, 0.02)
-    embedding = quantize_asym(table, cfg.vocab, cfg.hidden, 8, cfg.group) if ref else \
-        quantize_sym(table, cfg.vocab, cfg.hidden, 8, cfg.hidden)
+    if embed_dtype in ("f16", "f32"):
+        embedding = dense_table(table, cfg.vocab, cfg.hidden, 16 if embed_dtype == "f16" else 32)
+    else:
+        embedding = quantize_asym(table, cfg.vocab, cfg.hidden, 8, cfg.group) if ref else \
+            quantize_sym(table, cfg.vocab, cfg.hidden, 8, cfg.hidden)
     final = (1.0 + normal(cfg.hidden, base ^ 0x2000, 0.1)).astype(np.float32) if ref else np.ones(cfg.hidden, np.float32)
     return HostModel(cfg, layers, embedding, final)
 
@@ -194,7 +199,8 @@ class DeviceModel:
             return b.ptr
 
         def mat(q: QuantTensor) -> QuantMatrix:
-            return QuantMatrix(up(q.packed), up(q.scales), None if q.zeros is None else up(q.zeros))
+            scales = up(q.scales) if q.scales.size else None  # an f16 / f32 table has none
+            return QuantMatrix(up(q.packed), scales, None if q.zeros is None else up(q.zeros))
 
         self.layer_descs = (LayerDesc * self.cfg.layers)()
         for i, L in enumerate(host.layers):
@@ -207,7 +213,8 @@ class DeviceModel:
         c = self.cfg
         self.desc = ModelDesc(c.layers, c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate, c.vocab,
                               c.max_context, c.rms_eps, c.rope_theta, ENC_SIGNED, c.bits, c.group,
-                              mat(host.embedding), ENC_SIGNED, 8, c.hidden, up(host.final_norm),
+                              mat(host.embedding), host.embedding.encoding, host.embedding.bits,
+                              host.embedding.block_size, up(host.final_norm),
                               ctypes.cast(self.layer_descs, ctypes.POINTER(LayerDesc)))
 
     def release(self) -> None:

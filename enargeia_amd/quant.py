@@ -47,6 +47,21 @@ def _pack(codes: np.ndarray, bits: int) -> np.ndarray:
     return np.bitwise_or.reduce(c << shifts, axis=1).astype(np.uint32)
 
 
+def dense_table(values: np.ndarray, rows: int, cols: int, bits: int = 16) -> QuantTensor:
+    """A table stored as it is, the reference's 'f16' and 'f32' embedding dtypes
+    (embedding_variants.ts:26-74): bits 16 packs two halves per u32 (element 2j in the low half,
+    as unpack2x16float reads them), bits 32 plain floats. No scales or zero-points (an empty
+    scale stream); block_size is the row."""
+    if bits not in (16, 32):
+        raise ValueError(f"a dense table is f16 (16) or f32 (32) bits, not {bits}")
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    if bits == 16 and v.size % 2:
+        raise ValueError("an f16 table needs an even element count (two halves per word)")
+    raw = v.astype(np.float16).view(np.uint16).astype(np.uint32) if bits == 16 else v.view(np.uint32)
+    packed = (raw[0::2] | (raw[1::2] << np.uint32(16))).astype(np.uint32) if bits == 16 else raw.copy()
+    return QuantTensor(rows, cols, cols, bits, ENC_SIGNED, packed, np.zeros(0, np.float32), None)
+
+
 def quantize_sym(values: np.ndarray, rows: int, cols: int, bits: int = 4, block_size: int = 32) -> QuantTensor:
     if bits not in (4, 8) or cols % block_size:
         raise ValueError(f"reduction axis {cols} is not a multiple of {block_size}")

@@ -10,7 +10,7 @@
  *   reference op (KernelSpec.name)       binding order (kernel.ts / op .ts)          entry point
  *   matmul_q4_decode                     x, packed, scales, zeros, bias, out, dims  eg_matmul_q4_decode
  *   matmul_q4_prefill                    x, packed, scales, zeros, bias, out, dims  eg_matmul_q4_prefill
- *   lm_head_q8 / lm_head_q4              x, packed, scales, zeros, out, dims        eg_lm_head
+ *   lm_head_q8 / _q4 / _f16 / _f32        x, packed, scales, zeros, out, dims        eg_lm_head
  *   argmax                               logits, out, dims                          eg_argmax
  *   sample                               logits(rw), history, out(rw), dims         eg_sample
  *
@@ -168,7 +168,10 @@ EG_API int eg_matmul_q4_prefill_swiglu(eg_context* ctx, const float* x, const ui
 
 /* lm_head_<dtype> (embedding_variants.ts:135-180, q8 body :56-63): for row < row_count,
  *   out[row + out_offset] = sum_k x[k] * (code - zero) * scale[block]
- * bits = 8 (lm_head_q8, the shipped tied head) or 4 (lm_head_q4). */
+ * bits = 8 (lm_head_q8, the shipped tied head) or 4 (lm_head_q4); bits = 16 (lm_head_f16: packed
+ * holds the table as halves, two per word, element 2j in the low half, :66-70) or 32
+ * (lm_head_f32: plain floats, :71-73) reads the table itself - scales, zeros, the encoding and
+ * the block fields are not used. The argmax forms below take the same four. */
 EG_API int eg_lm_head(eg_context* ctx, const float* x, const uint32_t* packed, const float* scales,
                const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding,
                int bits);
@@ -271,7 +274,8 @@ EG_API int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t lau
  * from DEVICE memory token[0] (the previous step's argmax/sample result, so a captured step
  * needs no host round trip): if row_begin <= id < row_begin + row_count,
  *   out[out_offset + i] = (code[id - row_begin, i] - zero) * scale[block]   for i < hidden
- * else out is left untouched (another part of a split table owns the id). seq must be 1. */
+ * else out is left untouched (another part of a split table owns the id). seq must be 1.
+ * bits 4 / 8 as eg_lm_head; 16 / 32 gather an f16 / f32 table's row as it is (scales unused). */
 EG_API int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* packed, const float* scales,
                            const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding,
                            int bits);
@@ -375,7 +379,7 @@ typedef struct eg_model_desc {
   int encoding, bits;          /* projections */
   uint32_t block_size;
   eg_quant_matrix embedding;   /* the tied table: gathered, and the LM head */
-  int embed_encoding, embed_bits;
+  int embed_encoding, embed_bits; /* 4 / 8 codes, or 16 / 32: an f16 / f32 table (no scales) */
   uint32_t embed_block_size;
   const float* final_norm;
   const eg_layer_desc* layer;  /* `layers` entries */

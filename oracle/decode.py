@@ -77,11 +77,37 @@ def prefill_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, k_cache: np.n
     return (qr * np.float32(1.0 / np.sqrt(head_dim))).astype(np.float32), out
 
 
+def dense_values(q, begin: int = 0, end: int | None = None) -> np.ndarray:
+    """Rows [begin, end) of an f16 (bits 16) or f32 (bits 32) table as f32 [rows][cols]
+    (embedding_variants.ts:66-73: unpack2x16float takes element 2j from a word's low half)."""
+    end = q.rows if end is None else end
+    per = 32 // q.bits
+    w = np.asarray(q.packed[begin * q.cols // per:end * q.cols // per], np.uint32)
+    if q.bits == 32:
+        return w.view(np.float32).reshape(end - begin, q.cols).copy()
+    halves = np.stack([w & np.uint32(0xFFFF), w >> np.uint32(16)], axis=1).reshape(-1).astype(np.uint16)
+    return halves.view(np.float16).astype(np.float32).reshape(end - begin, q.cols)
+
+
+def dense_head(x: np.ndarray, q, rows_per_block: int = 8192) -> np.ndarray:
+    """lm_head_f16 / lm_head_f32 (embedding_variants.ts:135-180): out[n] = sum_k table[n][k] x[k],
+    summed in float64, f32 results (the table taken a block of rows at a time)."""
+    x64 = np.asarray(x, np.float64)
+    out = np.empty(q.rows, np.float32)
+    for r0 in range(0, q.rows, rows_per_block):
+        r1 = min(q.rows, r0 + rows_per_block)
+        out[r0:r1] = (dense_values(q, r0, r1).astype(np.float64) @ x64).astype(np.float32)
+    return out
+
+
 def dequant_row(q, row: int) -> np.ndarray:
     """One row of a quantized table as f32 (embed, ops.ts:222-233, with the gather's dequant,
     embedding_variants.ts:56-63 / embed_gather_q4.wgsl): value = (code - zero) * scale per block
     for the offset encoding, code * scale with two's-complement codes for the signed one. Nibble
-    n of a word is element 8w + n (byte b of a word is element 4w + b for int8)."""
+    n of a word is element 8w + n (byte b of a word is element 4w + b for int8). An f16 / f32
+    table's row as it is (dense_values)."""
+    if q.bits in (16, 32):
+        return dense_values(q, row, row + 1)[0]
     per = 32 // q.bits
     mask = (1 << q.bits) - 1
     words = np.asarray(q.packed[row * q.cols // per:(row + 1) * q.cols // per], np.uint32)
@@ -146,4 +172,6 @@ class OracleDecoder:
             a = silu_mul(self.linear(xn, L.mats["gate"]), self.linear(xn, L.mats["up"]))
             h = (h + self.linear(a, L.mats["down"])).astype(np.float32)
         xf = rmsnorm(h, self.m.final_norm, 1, c.hidden, c.rms_eps)
+        if self.m.embedding.bits in (16, 32):  # an f16 / f32 tied table
+            return dense_head(xf, self.m.embedding)
         return self.linear(xf, self.m.embedding)

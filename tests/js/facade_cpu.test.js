@@ -104,7 +104,8 @@ describe('ComputeKernel', () => {
   it('refuses ops that are not on this path', () => {
     expectThrows(() => new eg.ComputeKernel(FAKE_DEVICE, null, { name: 'rmsnorm', bindings: [] }),
       (e) => expect(/not an op of this library/.test(e.message), e.message), 'constructor');
-    expectThrows(() => eg.embeddingHeadSpec('f16'), (e) => expect(/only q4 and q8/.test(e.message), e.message), 'f16');
+    expectThrows(() => eg.embeddingHeadSpec('bf16'), (e) => expect(/the dtypes are q4, q8, f16 and f32/.test(e.message), e.message), 'bf16');
+    expect(['q4', 'q8', 'f16', 'f32'].map((d) => eg.embeddingHeadSpec(d).bits).join() === '4,8,16,32', 'dtypes');
   });
 
   it('carries the format on the spec', () => {

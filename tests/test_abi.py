@@ -105,5 +105,7 @@ def test_encode_rejects_grid_over_limit_as_range_error():
 def test_unknown_op_is_refused():
     with pytest.raises(K.EgError, match="not an op of this library"):
         K.ComputeKernel(_NoDevice(), K.KernelSpec("rmsnorm", ("read", "read_write", "uniform"), (256, 1, 1), 16))
-    with pytest.raises(K.EgError, match="only q4 and q8"):
-        K.embedding_head_spec("f16")
+    with pytest.raises(K.EgError, match="the dtypes are q4, q8, f16 and f32"):
+        K.embedding_head_spec("bf16")
+    # the reference's four embedding dtypes (embedding_variants.ts:26): codes, or the table itself
+    assert [K.embedding_head_spec(d).bits for d in ("q4", "q8", "f16", "f32")] == [4, 8, 16, 32]

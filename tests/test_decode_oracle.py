@@ -220,3 +220,44 @@ def test_prefill_attention_f32_cache_keeps_the_rows_exact():
         mean = visible[:begin + i + 1].astype(np.float64).mean(axis=0)
         for h in range(H):
             np.testing.assert_allclose(out[i].reshape(H, D)[h], mean[h // (H // KV)], rtol=1e-6, atol=1e-7)
+
+
+def test_dense_table_packing_known_halves():
+    """The f16 table's words (embedding_variants.ts:66-70, unpack2x16float): element 2j in the
+    low half. IEEE binary16 bits: 1.0 = 0x3C00, 2.0 = 0x4000, -0.5 = 0xB800, 65504 = 0x7BFF; an
+    f32 table keeps each float's own bits."""
+    from enargeia_amd.quant import dense_table
+    from oracle.decode import dense_values
+    v = np.array([1.0, 2.0, -0.5, 65504.0], np.float32)
+    t16 = dense_table(v, 1, 4, 16)
+    assert t16.packed.tolist() == [0x40003C00, 0x7BFFB800]
+    np.testing.assert_array_equal(dense_values(t16)[0], v)
+    t32 = dense_table(v, 2, 2, 32)
+    assert t32.packed.tolist() == [0x3F800000, 0x40000000, 0xBF000000, 0x477FE000]
+    np.testing.assert_array_equal(dense_values(t32), v.reshape(2, 2))
+
+
+def test_dense_head_closed_forms_and_the_int8_head():
+    """lm_head_f16 / lm_head_f32 in the oracle: one-hot rows select x's elements; a table of
+    small integers (exact in f16) gives the int8 head's logits over the same integers (scale 1:
+    every row's absmax is 127) from the C restatement of linearQ4's loop (quant.ts:95-111);
+    dequant_row of a dense table is its row (the gather)."""
+    from enargeia_amd.quant import dense_table
+    from oracle.decode import dense_head, dense_values, dequant_row
+    rng = np.random.default_rng(3)
+    k = 64
+    x = rng.standard_normal(k).astype(np.float32)
+    onehot = np.zeros((8, k), np.float32)
+    picks = [(5 * r + 3) % k for r in range(8)]
+    onehot[np.arange(8), picks] = 1.0
+    for bits in (16, 32):
+        np.testing.assert_array_equal(dense_head(x, dense_table(onehot, 8, k, bits)), x[picks])
+    ints = rng.integers(-127, 128, size=(16, k)).astype(np.float32)
+    ints[:, 0] = 127.0
+    q8 = oracle.quantize_sym(ints.reshape(-1), 16, k, 8, k)
+    want = oracle.linear_q(x, q8, None, 1)
+    got = dense_head(x, dense_table(ints, 16, k, 16))
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+    t = dense_table(rng.standard_normal((4, k)).astype(np.float32), 4, k, 16)
+    for r in range(4):
+        np.testing.assert_array_equal(dequant_row(t, r), dense_values(t)[r])

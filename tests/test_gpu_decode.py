@@ -377,6 +377,57 @@ def test_decoder_rejects_unknown_cache_dtype(device, small_model):
         dm.release()
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_decoder_dense_table_matches_oracle(device, dtype):
+    """A tied table stored as it is (--embed-dtype f16 / f32; embedding_variants.ts:26-74): the
+    prompt's rows gathered by the prompt chain, each step's next row by the step tail, the head
+    with the final norm and the greedy argmax over the table. The prompt through
+    eg_decoder_prefill against the oracle stepped position by position (the chain's bf16
+    projections: the reference-arithmetic bars of tests/test_gpu_prefill_chain.py), then greedy
+    steps at the decoder bar; a captured graph replays the same tokens and logits; sampled steps
+    (the head's logits, then the sampler) give ids in range."""
+    cfg = ModelConfig(layers=2, max_context=256, vocab=32768)
+    m = synthetic_model(cfg, embed_dtype=dtype)
+    dm = DeviceModel(device, m)
+    dec, graph = Decoder(dm), Decoder(dm)
+    ora = OracleDecoder(m, max_context=cfg.max_context)
+    prompt = prompt_ids(20, cfg.vocab, 0xD7)
+    try:
+        tok = dec.prefill(0, prompt)
+        for pos, t in enumerate(prompt):
+            want = ora.step(t, pos)
+        err = np.abs(dec.logits().astype(np.float64) - want).max() / rms(want)
+        assert err <= 0.1, f"{dtype} table: prompt logits {err:.3e} x rms from the oracle"
+        order = np.argsort(want)
+        if want[order[-1]] - want[order[-2]] > 0.2 * rms(want):
+            assert tok == int(order[-1])
+        # the prompt again through the decode step, position by position (both sides rewrite
+        # their cache rows at decode precision), then greedy steps, at the decoder bar
+        for pos, t in enumerate(prompt):
+            dec.reset(pos, t)
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(t, pos), got_token, f"{dtype} table prompt pos {pos}")
+        tok = got_token
+        for pos in range(len(prompt), len(prompt) + 8):
+            got_token = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got_token, f"{dtype} table greedy pos {pos}")
+            tok = got_token
+        dec.reset(0, prompt[0])
+        graph.reset(0, prompt[0])
+        graph.capture()
+        for s_ in range(6):
+            a, b = dec.step(), graph.step()
+            assert a == b, f"{dtype} table step {s_}: eager {a} graph {b}"
+            np.testing.assert_array_equal(dec.logits(), graph.logits())
+        dec.set_sampling(0.7, 0.9, 1.1)
+        for _ in range(4):
+            assert 0 <= dec.step() < cfg.vocab
+    finally:
+        dec.close()
+        graph.close()
+        dm.release()
+
+
 def test_decoder_graph_replay_equals_eager(device, small_model):
     dm = DeviceModel(device, small_model)
     eager, graph = Decoder(dm), Decoder(dm)
