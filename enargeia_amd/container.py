@@ -97,7 +97,12 @@ PROJECTION_NAMES = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self
 def qwen2_tensors(host) -> dict:
     """A HostModel (enargeia_amd.model) as checkpoint-named tensors, in the sorted-name order
     tools/quantize.py writes them."""
-    out = {"model.embed_tokens.weight": host.embedding, "model.norm.weight": host.final_norm}
+    e = host.embedding
+    # an f16 / f32 table (bits 16 / 32) is written as the F16 / F32 tensor it is: the packed
+    # words hold its elements in order (element 2j in the low half of an f16 pair)
+    table = e if e.bits not in (16, 32) else \
+        e.packed.view(np.float16 if e.bits == 16 else np.float32).reshape(e.rows, e.cols)
+    out = {"model.embed_tokens.weight": table, "model.norm.weight": host.final_norm}
     for i, L in enumerate(host.layers):
         p = f"model.layers.{i}."
         for short, long in PROJECTION_NAMES.items():

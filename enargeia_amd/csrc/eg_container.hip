@@ -635,8 +635,10 @@ int eg_container_model_desc(eg_context* ctx, const eg_container* c, const void* 
   if (st != EG_OK) return st;
   if (find("lm_head.weight"))
     return fail(ctx, EG_ERR_FORMAT, "%s: lm_head.weight is present; this decoder runs tied embeddings only", op);
-  if (emb->dtype != EG_DTYPE_Q4 && emb->dtype != EG_DTYPE_Q8)
-    return fail(ctx, EG_ERR_FORMAT, "model.embed_tokens.weight: %s tables are not supported; quantize it as Q8 or Q4",
+  // the tied table: Q4 / Q8, or F16 / F32 as it is (--embed-dtype f16 / f32; embedding_variants.ts:26-74)
+  const bool dense_table = emb->dtype == EG_DTYPE_F16 || emb->dtype == EG_DTYPE_F32;
+  if (dense_table && emb->shape.size() != 2)
+    return fail(ctx, EG_ERR_FORMAT, "model.embed_tokens.weight: an %s table must be 2-D",
                 emb->dtype == EG_DTYPE_F16 ? "F16" : "F32");
   uint32_t n_layers = 0;
   while (find("model.layers." + std::to_string(n_layers) + ".self_attn.q_proj.weight")) n_layers++;
@@ -673,10 +675,17 @@ int eg_container_model_desc(eg_context* ctx, const eg_container* c, const void* 
   desc->encoding = EG_ENC_OFFSET_ZEROS;  // the container's quantizer is asymmetric (quantize.py:74-103)
   desc->bits = q0->bits;
   desc->block_size = q0->block_size;
-  if ((st = quant(emb, vocab, hidden, &desc->embedding)) != EG_OK) return st;
-  desc->embed_encoding = EG_ENC_OFFSET_ZEROS;
+  if (dense_table) {
+    desc->embedding = eg_quant_matrix{};
+    desc->embedding.packed = reinterpret_cast<const uint32_t*>(base + emb->data[0]);
+    desc->embed_encoding = EG_ENC_SIGNED;  // not read for an f16 / f32 table
+    desc->embed_block_size = (uint32_t)hidden;
+  } else {
+    if ((st = quant(emb, vocab, hidden, &desc->embedding)) != EG_OK) return st;
+    desc->embed_encoding = EG_ENC_OFFSET_ZEROS;
+    desc->embed_block_size = emb->block_size;
+  }
   desc->embed_bits = emb->bits;
-  desc->embed_block_size = emb->block_size;
   const Tensor* norm;
   if ((st = require("model.norm.weight", &norm)) != EG_OK) return st;
   if ((st = vec(norm, hidden, &desc->final_norm)) != EG_OK) return st;

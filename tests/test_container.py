@@ -202,6 +202,22 @@ def test_model_desc_points_into_the_blob(ref_checkpoint):
     assert got.heads == 4 and got.group == 64
 
 
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_model_desc_takes_f16_and_f32_tables(tmp_path, ref_checkpoint, dtype):
+    """An F16 / F32 tied table (--embed-dtype f16 / f32): the description points at its data
+    range with 16 / 32 embedding bits and no scales or zero-points."""
+    cfg, host, tensors, header, path = ref_checkpoint
+    t = dict(tensors, **{"model.embed_tokens.weight": np.zeros((512, 128), dtype)})
+    p = tmp_path / "dense.enargeia"
+    h = write_enargeia(str(p), t)
+    with Container(str(p)) as c:
+        desc, layers, got = c.describe(FAKE_BLOB, head_dim=32, max_context=256, rms_eps=1e-5, rope_theta=1e4)
+    assert (desc.vocab, desc.hidden, desc.embed_bits, desc.embed_block_size) == \
+        (512, 128, 16 if dtype == np.float16 else 32, 128)
+    assert desc.embedding.packed == FAKE_BLOB + h["tensors"]["model.embed_tokens.weight"]["offsets"]["data"][0]
+    assert not desc.embedding.scales and not desc.embedding.zeros
+
+
 def _describe_error(tmp_path, tensors, **kw) -> str:
     path = tmp_path / "bad.enargeia"
     write_enargeia(str(path), tensors)
@@ -221,9 +237,8 @@ def test_model_desc_errors(tmp_path, ref_checkpoint):
     assert _describe_error(tmp_path, t) == "model.layers.1.mlp.up_proj.weight is missing"
     t = dict(tensors, **{"lm_head.weight": tensors["model.embed_tokens.weight"]})
     assert "tied embeddings only" in _describe_error(tmp_path, t)
-    t = dict(tensors, **{"model.embed_tokens.weight": np.zeros((512, 128), np.float16)})
-    assert _describe_error(tmp_path, t) == \
-        "model.embed_tokens.weight: F16 tables are not supported; quantize it as Q8 or Q4"
+    t = dict(tensors, **{"model.embed_tokens.weight": np.zeros(512 * 128, np.float16)})
+    assert _describe_error(tmp_path, t) == "model.embed_tokens.weight: an F16 table must be 2-D"
     from enargeia_amd.quant import normal, quantize_asym
     t = dict(tensors, **{"model.layers.2.mlp.gate_proj.weight": quantize_asym(normal(256 * 128, 5, 0.02), 256, 128, 4, 32)})
     assert "4-bit blocks of 32, the model's first projection has 4-bit blocks of 64" in _describe_error(tmp_path, t)

@@ -66,3 +66,32 @@ def test_loaded_checkpoint_decodes_like_the_oracle(device, checkpoint):
         dec.close()
         model.release()
     assert checked == 36
+
+
+def test_f16_table_checkpoint_decodes_like_the_oracle(device, tmp_path):
+    """The same checkpoint with its tied table written as F16 (--embed-dtype f16): loaded through
+    eg_container_model_desc (16 embedding bits, the table's data range) and decoded against the
+    oracle over the same halves, at the decoder bar."""
+    host = synthetic_model(CFG, base=0xE4A, fmt="reference", embed_dtype="f16")
+    path = tmp_path / "qwen2-tiny-f16.enargeia"
+    write_enargeia(str(path), qwen2_tensors(host))
+    with Container(str(path)) as c:
+        model = c.load(device, head_dim=CFG.head_dim, max_context=CFG.max_context, rms_eps=CFG.rms_eps,
+                       rope_theta=CFG.rope_theta)
+    assert model.desc.embed_bits == 16
+    dec = Decoder(model)
+    ora = OracleDecoder(host, max_context=CFG.max_context)
+    try:
+        prompt = prompt_ids(12, CFG.vocab, seed=0xF16)
+        for pos, tok in enumerate(prompt):
+            dec.reset(pos, tok)
+            got = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got, f"f16 table prompt pos {pos}")
+        tok = got
+        for pos in range(len(prompt), len(prompt) + 8):
+            got = dec.step()
+            check_step(dec.logits(), ora.step(tok, pos), got, f"f16 table greedy pos {pos}")
+            tok = got
+    finally:
+        dec.close()
+        model.release()
