@@ -34,12 +34,14 @@ __global__ __launch_bounds__(kThreads) void embed_gather_kernel(const uint32_t* 
                                                                 const float* scales, const uint32_t* zeros,
                                                                 float* out, eg_embedding_dims d, int encoding,
                                                                 int bits) {
-  const uint32_t id = token[0];
+  const uint32_t s = blockIdx.x;  // one id of the `seq` per workgroup
+  const uint32_t id = token[s];
   if (id < d.row_begin || id - d.row_begin >= d.row_count) return;
   const uint32_t row = id - d.row_begin;
+  float* dst = out + d.out_offset + (size_t)s * d.hidden;
   for (uint32_t i = threadIdx.x; i < d.hidden; i += blockDim.x) {
     const uint64_t blk = bits >= 16 ? 0 : (uint64_t)row * d.blocks_per_row + i / d.block_size;
-    out[d.out_offset + i] = egd::table_value(packed, scales, zeros, (uint64_t)row * d.hidden + i, blk, encoding, bits);
+    dst[i] = egd::table_value(packed, scales, zeros, (uint64_t)row * d.hidden + i, blk, encoding, bits);
   }
 }
 
@@ -343,7 +345,7 @@ int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* pack
     return eg::fail(ctx, EG_ERR_INVALID, "%s: NULL argument", op);
   if (bits != 4 && bits != 8 && !dense)
     return eg::fail(ctx, EG_ERR_INVALID, "%s: bits must be 4, 8, 16 (f16 table) or 32 (f32 table), got %d", op, bits);
-  if (dims->seq != 1) return eg::fail(ctx, EG_ERR_INVALID, "%s: seq %u (decode gathers one token)", op, dims->seq);
+  if (dims->seq > 0x7FFFFFFFu) return eg::fail(ctx, EG_ERR_RANGE, "%s: seq %u over the grid", op, dims->seq);
   if (!dense) {
     if (encoding != EG_ENC_OFFSET_ZEROS && encoding != EG_ENC_SIGNED)
       return eg::fail(ctx, EG_ERR_INVALID, "%s: unknown encoding %d", op, encoding);
@@ -353,7 +355,8 @@ int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* pack
       return eg::fail(ctx, EG_ERR_INVALID, "%s: hidden %u / block %u / blocksPerRow %u disagree", op, dims->hidden,
                       dims->block_size, dims->blocks_per_row);
   }
-  hipLaunchKernelGGL(embed_gather_kernel, dim3(1), dim3(kThreads), 0, ctx->stream, token, packed, scales,
+  if (dims->seq == 0) return EG_OK;
+  hipLaunchKernelGGL(embed_gather_kernel, dim3(dims->seq), dim3(kThreads), 0, ctx->stream, token, packed, scales,
                      dense || encoding == EG_ENC_SIGNED ? nullptr : zeros, out, *dims, encoding, bits);
   return eg::check_launch(ctx, op);
 }

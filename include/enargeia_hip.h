@@ -270,11 +270,12 @@ EG_API int eg_test_launch_stamps(eg_context* ctx, uint64_t* buffer, uint32_t lau
 
 /* ---- decode step: embedding, attention, fused GEMV inputs ----------------------------------- */
 
-/* embed_gather_<dtype> (embedding_variants.ts:93-133, :56-63 for q8): for the one token id read
- * from DEVICE memory token[0] (the previous step's argmax/sample result, so a captured step
- * needs no host round trip): if row_begin <= id < row_begin + row_count,
- *   out[out_offset + i] = (code[id - row_begin, i] - zero) * scale[block]   for i < hidden
- * else out is left untouched (another part of a split table owns the id). seq must be 1.
+/* embed_gather_<dtype> (embedding_variants.ts:93-133, :56-63 for q8): for each of the seq token
+ * ids read from DEVICE memory token[s] (a decode step's one id is the previous step's
+ * argmax/sample result, so a captured step needs no host round trip): if row_begin <= id <
+ * row_begin + row_count,
+ *   out[out_offset + s * hidden + i] = (code[id - row_begin, i] - zero) * scale[block]   for i < hidden
+ * else that row of out is left untouched (another part of a split table owns the id).
  * bits 4 / 8 as eg_lm_head; 16 / 32 gather an f16 / f32 table's row as it is (scales unused). */
 EG_API int eg_embed_gather(eg_context* ctx, const uint32_t* token, const uint32_t* packed, const float* scales,
                            const uint32_t* zeros, float* out, const eg_embedding_dims* dims, int encoding,

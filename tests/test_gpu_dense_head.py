@@ -174,3 +174,32 @@ def test_dense_head_argument_errors(device):
                                      32) == _lib.EG_ERR_INVALID
     finally:
         buf.release()
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_gather_many_ids(device, bits):
+    """The reference's gather over dims.seq ids (embedding_variants.ts:113-123: one row per id,
+    out[s * hidden + i]), ids of another part of a split table leaving their rows untouched."""
+    from enargeia_amd.quant import quantize_sym
+    from oracle.decode import dequant_row
+    rng = np.random.default_rng(31 + bits)
+    n, k = 500, 128
+    vals = rng.standard_normal(n * k, dtype=np.float32)
+    t = dense_table(vals, n, k, 16) if bits == 16 else quantize_sym(vals, n, k, 8, 32)
+    ids = np.array([3, 499, 250, 1000, 0, 250], np.uint32)  # 1000: another part's id
+    seq = ids.size
+    bt = device.upload(t.packed)
+    bs = device.upload(t.scales) if bits == 8 else None
+    bo, bid = device.upload(np.full(seq * k, -7.0, np.float32)), device.upload(ids)
+    d = K.EmbeddingDims.from_buffer_copy(K.embedding_dims(seq, k, 0, n, k if bits == 16 else 32, 0, 0))
+    try:
+        _lib.check(_lib.load().eg_embed_gather(device.ctx, _vp(bid.ptr), _vp(bt.ptr), _vp(bs.ptr) if bs else None,
+                                               None, _vp(bo.ptr), ctypes.byref(d), K.ENC_SIGNED, bits), device.ctx)
+        got = device.read_array(bo, np.float32, seq * k).reshape(seq, k)
+    finally:
+        for b in (bt, bs, bo, bid):
+            if b is not None:
+                b.release()
+    for s_, i in enumerate(ids):
+        want = np.full(k, -7.0, np.float32) if i >= n else dequant_row(t, int(i))
+        np.testing.assert_array_equal(got[s_], want, err_msg=f"row {s_} (id {i})")
