@@ -384,6 +384,24 @@ napi_value LmHead(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
+// embedGather(ctx, ids, packed, scales, zeros, out, dims, encoding, bits)
+napi_value EmbedGather(napi_env env, napi_callback_info info) {
+  Args a(env, info, "embedGather", 9);
+  auto* ctx = a.handle<eg_context>(0, "context");
+  auto* ids = static_cast<const uint32_t*>(a.ptr(1));
+  auto* packed = static_cast<const uint32_t*>(a.ptr(2));
+  auto* scales = static_cast<const float*>(a.ptr(3));
+  auto* zeros = static_cast<const uint32_t*>(a.ptr(4));
+  auto* out = static_cast<float*>(a.ptr(5));
+  eg_embedding_dims dims;
+  a.uniform(6, &dims);
+  int encoding = a.i32(7), bits = a.i32(8);
+  if (!a.ok) return nullptr;
+  if (throw_status(env, ctx, eg_embed_gather(ctx, ids, packed, scales, zeros, out, &dims, encoding, bits)))
+    return nullptr;
+  return undefined(env);
+}
+
 // lmHeadArgmax(ctx, x, packed, scales, zeros, out|null, result, dims, encoding, bits)
 napi_value LmHeadArgmax(napi_env env, napi_callback_info info) {
   Args a(env, info, "lmHeadArgmax", 10);
@@ -1004,6 +1022,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"matmulQ4Decode", nullptr, Matmul<eg_matmul_q4_decode>, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"matmulQ4Prefill", nullptr, Matmul<eg_matmul_q4_prefill>, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"lmHead", nullptr, LmHead, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"embedGather", nullptr, EmbedGather, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"lmHeadArgmax", nullptr, LmHeadArgmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

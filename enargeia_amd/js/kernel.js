@@ -34,6 +34,10 @@ const DISPATCH = {
   lm_head_q8: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
   lm_head_f16: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
   lm_head_f32: (ctx, p, u, s) => native.lmHead(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  embed_gather_q4: (ctx, p, u, s) => native.embedGather(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  embed_gather_q8: (ctx, p, u, s) => native.embedGather(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  embed_gather_f16: (ctx, p, u, s) => native.embedGather(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
+  embed_gather_f32: (ctx, p, u, s) => native.embedGather(ctx, p[0], p[1], p[2], p[3], p[4], u, s.encoding, s.bits),
   argmax: (ctx, p, u) => native.argmax(ctx, p[0], p[1], u),
   sample: (ctx, p, u) => native.sample(ctx, p[0], p[1], p[2], u),
 };

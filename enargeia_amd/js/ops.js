@@ -39,6 +39,11 @@ function withFormat(spec, bits, encoding) {
   return Object.freeze(Object.assign({}, spec, { bits, encoding }));
 }
 
+/** embeddingGatherSpec (embedding_variants.ts:186-193): the rows of `seq` ids (binding 0 holds them). */
+function embeddingGatherSpec(dtype, encoding) {
+  return Object.freeze(Object.assign({}, embeddingHeadSpec(dtype, encoding), { name: `embed_gather_${dtype}` }));
+}
+
 /** embeddingHeadSpec (embedding_variants.ts:195-203): q4 and q8 codes, or an f16 / f32 table. */
 function embeddingHeadSpec(dtype, encoding) {
   const bits = { q4: 4, q8: 8, f16: 16, f32: 32 }[dtype];
@@ -104,6 +109,7 @@ module.exports = {
   GREEDY,
   withFormat,
   embeddingHeadSpec,
+  embeddingGatherSpec,
   decodeGridWidth,
   matmulQ4Dims,
   matmulQ4PrefillWorkgroups,

@@ -348,6 +348,20 @@ def _vp(p: int) -> ctypes.c_void_p:
     return ctypes.c_void_p(p or None)
 
 
+def embedding_gather_spec(dtype: str, encoding: int = ENC_OFFSET_ZEROS) -> KernelSpec:
+    """embeddingGatherSpec (embedding_variants.ts:186-193): binding 0 holds the `seq` ids."""
+    h = embedding_head_spec(dtype, encoding)
+    return KernelSpec(f"embed_gather_{dtype}", h.bindings, h.workgroup_size, h.uniform_bytes, h.bits, h.encoding)
+
+
+def _gather(k: ComputeKernel, p: list, raw: bytes) -> None:
+    d = EmbeddingDims.from_buffer_copy(raw)
+    ctx = k.device.ctx
+    ids, packed, scales, zeros, out = p
+    check(_lib.load().eg_embed_gather(ctx, _vp(ids), _vp(packed), _vp(scales), _vp(zeros), _vp(out), ctypes.byref(d),
+                                      k.spec.encoding, k.spec.bits), ctx)
+
+
 def _matmul(k: ComputeKernel, p: list, raw: bytes, fn: str) -> None:
     d = MatmulDims.from_buffer_copy(raw)
     ctx = k.device.ctx
@@ -383,6 +397,10 @@ _DISPATCH = {
     "lm_head_q8": _lm_head,
     "lm_head_f16": _lm_head,
     "lm_head_f32": _lm_head,
+    "embed_gather_q4": _gather,
+    "embed_gather_q8": _gather,
+    "embed_gather_f16": _gather,
+    "embed_gather_f32": _gather,
     "argmax": _argmax,
     "sample": _sample,
 }
@@ -446,6 +464,6 @@ __all__ = [
     "ENC_SIGNED", "EgError", "EgRangeError", "GREEDY", "GemvPlan", "GemvSegment", "Graph", "KernelSpec", "MATMUL_Q4_DECODE",
     "MATMUL_Q4_PREFILL", "MAX_WORKGROUPS_PER_DIMENSION", "SAMPLE", "SAMPLE_WORKGROUPS", "SamplingParams",
     "argmax_dims", "coverage", "decode_grid_width", "embedding_dims", "embedding_head_spec",
-    "embedding_head_workgroups", "lm_head_argmax", "lm_head_sample", "matmul_q4_decode_workgroups", "matmul_q4_dims",
+    "embedding_gather_spec", "embedding_head_workgroups", "lm_head_argmax", "lm_head_sample", "matmul_q4_decode_workgroups", "matmul_q4_dims",
     "matmul_q4_prefill_workgroups", "sample_dims", "with_format",
 ]

@@ -106,6 +106,8 @@ describe('ComputeKernel', () => {
       (e) => expect(/not an op of this library/.test(e.message), e.message), 'constructor');
     expectThrows(() => eg.embeddingHeadSpec('bf16'), (e) => expect(/the dtypes are q4, q8, f16 and f32/.test(e.message), e.message), 'bf16');
     expect(['q4', 'q8', 'f16', 'f32'].map((d) => eg.embeddingHeadSpec(d).bits).join() === '4,8,16,32', 'dtypes');
+    expect(eg.embeddingGatherSpec('f16').name === 'embed_gather_f16' && eg.embeddingGatherSpec('f16').bits === 16,
+      'gather spec');
   });
 
   it('carries the format on the spec', () => {

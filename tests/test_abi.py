@@ -109,3 +109,4 @@ def test_unknown_op_is_refused():
         K.embedding_head_spec("bf16")
     # the reference's four embedding dtypes (embedding_variants.ts:26): codes, or the table itself
     assert [K.embedding_head_spec(d).bits for d in ("q4", "q8", "f16", "f32")] == [4, 8, 16, 32]
+    assert K.embedding_gather_spec("f32").name == "embed_gather_f32" and K.embedding_gather_spec("f32").bits == 32

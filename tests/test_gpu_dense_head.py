@@ -203,3 +203,30 @@ def test_gather_many_ids(device, bits):
     for s_, i in enumerate(ids):
         want = np.full(k, -7.0, np.float32) if i >= n else dequant_row(t, int(i))
         np.testing.assert_array_equal(got[s_], want, err_msg=f"row {s_} (id {i})")
+
+
+@pytest.mark.parametrize("dtype", ["q8", "f16"])
+def test_gather_through_the_kernel_interface(device, dtype):
+    """embeddingGatherSpec(dtype) through ComputeKernel (kernel.ts:20-112), as a reference caller
+    binds it: [ids, packed, scales, zeros, out, dims] and embeddingGatherWorkgroups' grid."""
+    from enargeia_amd.quant import quantize_sym
+    from oracle.decode import dequant_row
+    rng = np.random.default_rng(41)
+    n, k = 256, 64
+    vals = rng.standard_normal(n * k, dtype=np.float32)
+    t = dense_table(vals, n, k, 16) if dtype == "f16" else quantize_sym(vals, n, k, 8, k)
+    ids = np.array([7, 255, 0, 128], np.uint32)
+    kern = K.ComputeKernel(device, K.embedding_gather_spec(dtype, K.ENC_SIGNED))
+    bufs = [device.upload(ids), device.upload(t.packed), device.upload(t.scales) if t.scales.size else None, None,
+            device.buffer(ids.size * k * 4)]
+    try:
+        u = kern.uniform()
+        u.write(K.embedding_dims(ids.size, k, 0, n, t.block_size, 0, 0))
+        kern.encode(kern.bind_group(bufs + [u]), (1, ids.size, 1))
+        got = device.read_array(bufs[4], np.float32, ids.size * k).reshape(ids.size, k)
+    finally:
+        for b in bufs:
+            if b is not None:
+                b.release()
+    for s_, i in enumerate(ids):
+        np.testing.assert_array_equal(got[s_], dequant_row(t, int(i)))
