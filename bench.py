@@ -954,6 +954,21 @@ def prefill_numbers(dev, ev, stream, args) -> dict:
         pairs = H * sum(begin + i + 1 for i in range(M))
         tf = 4.0 * D * pairs / (us * 1e-6) / 1e12
         res[f"attention_m{M}_begin{begin}"] = {"us": round(us, 2), "tflops": round(tf, 3)}
+    # the same chunk over an f32 cache (eg_attention_prefill_f32: exact rows, f32 FMAs)
+    caches32 = [dev.upload(rng.standard_normal(CTX * KVH * D, dtype=np.float32)) for _ in range(2)]
+    keep += caches32
+    for begin in (0, CTX - M):
+        d = Dims(M, begin + M, begin, H, KVH, D, CTX, 1.0e6)
+
+        def call32():
+            _lib.check(_lib.load().eg_attention_prefill_f32(dev.ctx, vp(q.ptr), vp(kvb[0].ptr), vp(kvb[1].ptr),
+                                                            vp(caches32[0].ptr), vp(caches32[1].ptr), vp(qr.ptr),
+                                                            vp(out.ptr), ctypes.byref(d)), dev.ctx)
+
+        us = timed_each(call32, args.steps)
+        pairs = H * sum(begin + i + 1 for i in range(M))
+        tf = 4.0 * D * pairs / (us * 1e-6) / 1e12
+        res[f"attention_f32_cache_m{M}_begin{begin}"] = {"us": round(us, 2), "tflops": round(tf, 3)}
     log(f"prefill attention: { {k: v for k, v in res.items() if k.startswith('attention')} }")
     for b in keep:
         b.release()
